@@ -1,0 +1,182 @@
+"""Decode benchmark of the MI355X HIP backend (one GPU).
+
+Workload (the metric's configuration): a random-init
+Llama-style 1.1B model (22 layers, hidden 2048, FFN 5632 SwiGLU, 32/4 heads,
+head_dim 64, vocab 32000) with Q8_0 weights and a Q8_0 KV cache.  The cache is
+filled to 2048 tokens of seeded random ids (untimed: 2048-W prompt tokens
+through the decode step, then W warm-up decode steps), then exactly `steps`
+greedy decode steps are timed with HIP events on the library's stream
+(context 2048 -> 2048+steps).  value = steps / time (tok/s).
+
+roofline: the dominant kernel of the step, the fused RMSNorm + gate/up
+dequant-GEMV with the SwiGLU epilogue (52% of a step's bytes), timed live
+with HIP events over launches that rotate through 12 distinct weight pairs
+(295 MB, more than the 256 MB Infinity Cache), so the bytes come from HBM.
+
+cpu_baseline: the oracle's restatement of the reference decode step
+(oracle/vlrf_oracle.c: f32 decoded weights, AVX2 streaming GEMV, full-cache
+dequant, per-head flash attention) on the host's cores at context 2048.
+
+    python bench.py [--gpus 1] [--steps 128] [--warmup 8] [--dtype q8_0|q4_0]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0   # MI355X published HBM3E bandwidth
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def gemv_roofline(ctx, V, F, cfg, dtype, launches=96):
+    """Live HIP-event timing of the gate/up SwiGLU dequant-GEMV at the step's shape."""
+    D, Fd = cfg["d_model"], cfg["d_ff"]
+    pairs = []
+    for i in range(12):
+        g = F.quantize(F.normal(99, f"bench.g{i}", Fd * D, 0.02), dtype)
+        u = F.quantize(F.normal(99, f"bench.u{i}", Fd * D, 0.02), dtype)
+        pairs.append((V.QuantWeight(ctx, g, dtype, Fd, D), V.QuantWeight(ctx, u, dtype, Fd, D)))
+    x = ctx.to_device(F.normal(99, "bench.x", D))
+    nw = ctx.to_device(np.ones(D, np.float32))
+    h = ctx.alloc(Fd * 4)
+    for i in range(24):                       # warm-up
+        wg, wu = pairs[i % 12]
+        ctx.qlinear_swiglu(wg, wu, x, h, 1, nw, 1e-5)
+    ctx.sync()
+    ctx.timer_start()
+    for i in range(launches):
+        wg, wu = pairs[i % 12]
+        ctx.qlinear_swiglu(wg, wu, x, h, 1, nw, 1e-5)
+    ms = ctx.timer_stop()
+    per_launch_s = ms / 1e3 / launches
+    wbytes = 2 * pairs[0][0].device_bytes
+    algo = wbytes + D * 4 * 2 + Fd * 4          # weights + x + norm weight + h
+    achieved = algo / per_launch_s / 1e9
+    return {"kernel": "qlinear_kernel<Q8_0,1,swiglu> (gate/up 2x5632x2048)",
+            "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "bytes_per_launch": int(algo), "us_per_launch": round(per_launch_s * 1e6, 3)}
+
+
+def cpu_baseline(cfg, f32w, ctx_len, budget_s=12.0, max_steps=8):
+    """Oracle decode steps at context ctx_len on the host cores."""
+    import oracle
+    try:
+        ncpu = len(os.sched_getaffinity(0))
+    except AttributeError:
+        ncpu = os.cpu_count() or 1
+    threads = max(1, min(16, ncpu))
+    om = oracle.Model(cfg, f32w, n_threads=threads)
+    om.reset()
+    om.fill_kv(ctx_len - 1, seed=7)
+    tok = 1
+    t0 = time.perf_counter()
+    tok = om.forward([tok])                   # warm-up step
+    warm = time.perf_counter() - t0
+    n = max(1, min(max_steps, int(budget_s / max(warm, 1e-3))))
+    t0 = time.perf_counter()
+    for _ in range(n):
+        tok = om.forward([tok])
+    dt = time.perf_counter() - t0
+    del om
+    return {"value": round(n / dt, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"{n} decode steps of the 1.1B f32-decoded model at context {ctx_len}-"
+                      f"{ctx_len + n} (oracle restatement, {threads} threads, KV cache filled "
+                      f"with seeded codes instead of a CPU prefill)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=128)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--ctx", type=int, default=2048)
+    ap.add_argument("--dtype", default="q8_0", choices=["q8_0", "q4_0"])
+    ap.add_argument("--seed", type=int, default=1234)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-roofline", action="store_true")
+    a = ap.parse_args()
+
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(see DESIGN.md, 'How the path would shard').", file=sys.stderr)
+        sys.exit(2)
+
+    import vlrf_amd as V
+    from vlrf_amd import formats as F
+
+    dtype = V.DT_Q8_0 if a.dtype == "q8_0" else V.DT_Q4_0
+    cfg = F.llama_1b(max_seq_len=a.ctx + a.steps, weight_dtype=dtype)
+    ctx = V.Context(0)
+    log("[bench]", ctx.device_info())
+
+    t0 = time.time()
+    model = V.Model(ctx, cfg)
+    f32w = F.load_model(model, a.seed, want_f32=not a.no_cpu_baseline)
+    log(f"[bench] weights generated and uploaded in {time.time() - t0:.1f}s")
+
+    prompt = F.tokens(a.seed, "bench.prompt", a.ctx - a.warmup, cfg["vocab_size"])
+    model.reset()
+    t0 = time.time()
+    nxt = model.prefill(prompt)
+    ctx.sync()
+    log(f"[bench] {prompt.size} prompt tokens through the decode step in {time.time() - t0:.2f}s")
+    if a.warmup:
+        warm = model.generate_ids(nxt, a.warmup)
+        nxt = int(warm[-1])
+    assert model.used == a.ctx, model.used
+
+    ctx.sync()
+    wall0 = time.perf_counter()
+    ctx.timer_start()
+    model.generate_async(nxt, a.steps)
+    ms = ctx.timer_stop()
+    wall = time.perf_counter() - wall0
+    ids = model.read_generated(a.steps)
+    log(f"[bench] {a.steps} steps: {ms:.3f} ms (events), {wall * 1e3:.3f} ms (wall); "
+        f"first ids {ids[:8].tolist()}")
+
+    tok_s = a.steps / (ms / 1e3)
+    step_bytes = [sum(model.step_bytes(a.ctx + i)) for i in range(a.steps)]
+    step_gbs = sum(step_bytes) / (ms / 1e3) / 1e9
+
+    out = {
+        "metric": "decode tok/s at 1.1B-shape ctx 2048",
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms / a.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": f"f32 compute, {a.dtype} weights, q8_0 KV",
+        "data": "synthetic: seeded N(0,0.02) weights, random token ids",
+        "config": {"workload": "llama-1.1B-shape greedy decode, ctx 2048->%d, batch 1"
+                   % (a.ctx + a.steps), "weights": a.dtype, "kv_cache": "q8_0 per token row",
+                   "layers": 22, "hidden": 2048, "ffn": 5632, "heads": "32/4", "vocab": 32000},
+        "step_roofline": {"bytes_per_step": int(np.mean(step_bytes)), "achieved": round(step_gbs, 1),
+                          "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                          "frac": round(step_gbs / HBM_PEAK_GBS, 4)},
+    }
+    del model
+    if not a.no_roofline:
+        out["roofline"] = gemv_roofline(ctx, V, F, cfg, dtype)
+    if not a.no_cpu_baseline:
+        log("[bench] cpu baseline ...")
+        out["cpu_baseline"] = cpu_baseline(cfg, f32w, a.ctx)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,229 @@
+/*
+ * vlrf_hip.h - C ABI of the MI355X (gfx950) HIP decode backend for VLRF.
+ *
+ * Plain C: opaque handles, device pointers, sizes and int status codes.  No
+ * exception crosses this boundary; every entry point returns VLRF_HIP_OK (0)
+ * or a negative status, and vlrf_hip_last_error() gives the message of the
+ * calling thread's last failure.  On a nonzero status a caller keeps the
+ * reference's behaviour of running the CPU op instead
+ * (reference include/backend/backend.hpp:128-176: "falls back to CPU").
+ *
+ * Device work is queued on the context's own HIP stream and is asynchronous
+ * unless stated otherwise; vlrf_hip_sync() waits for it.  A context, and
+ * every handle made from it, is used by one host thread at a time (the
+ * reference serialises per model: src/api/vlrf_api.cpp:84,370).
+ *
+ * Each declaration names the reference interface it replaces or serves.
+ */
+#ifndef VLRF_HIP_H
+#define VLRF_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes --------------------------------------------------------- */
+#define VLRF_HIP_OK            0
+#define VLRF_HIP_ERR_ARG      -1   /* bad argument / unsupported shape          */
+#define VLRF_HIP_ERR_RUNTIME  -2   /* HIP runtime error (message has the detail) */
+#define VLRF_HIP_ERR_NOMEM    -3   /* device allocation failed                  */
+#define VLRF_HIP_ERR_OVERFLOW -4   /* KV cache capacity exceeded                */
+#define VLRF_HIP_ERR_NODEV    -5   /* no usable gfx950 device                    */
+
+/* ---- data types: GGML type ids, as the reference's GGUF reader uses them
+ * (tools/converter/convert_gguf.py GGMLType) -------------------------------- */
+#define VLRF_DT_F32   0
+#define VLRF_DT_Q4_0  2
+#define VLRF_DT_Q8_0  8
+
+/* KV cache dtypes: reference include/model/kv_cache.hpp:36-40 (KVCacheDType). */
+#define VLRF_KV_F32   0
+#define VLRF_KV_Q8_0  2
+
+typedef struct vlrf_hip_ctx*    vlrf_hip_ctx_t;
+typedef struct vlrf_hip_weight* vlrf_hip_weight_t;
+typedef struct vlrf_hip_kv*     vlrf_hip_kv_t;
+typedef struct vlrf_hip_model*  vlrf_hip_model_t;
+
+/* ============================================================================
+ * Context, device memory, streams
+ * Replaces: IBackend::{type,device_info,is_available,synchronize,to_device,
+ * to_host} (reference include/backend/ibackend.hpp:48-58) and
+ * BackendRegistry::try_opencl/try_sycl (backend.hpp:556-570).
+ * ========================================================================== */
+const char* vlrf_hip_last_error(void);
+int   vlrf_hip_device_count(void);
+/* Fails with VLRF_HIP_ERR_NODEV when `device` is not a gfx950 GPU. */
+int   vlrf_hip_init(int device, vlrf_hip_ctx_t* out);
+void  vlrf_hip_shutdown(vlrf_hip_ctx_t ctx);
+int   vlrf_hip_device_info(vlrf_hip_ctx_t ctx, char* buf, size_t len);
+int   vlrf_hip_sync(vlrf_hip_ctx_t ctx);
+void* vlrf_hip_stream(vlrf_hip_ctx_t ctx);            /* the context's hipStream_t */
+int   vlrf_hip_malloc(vlrf_hip_ctx_t ctx, size_t bytes, void** dptr);
+int   vlrf_hip_free(vlrf_hip_ctx_t ctx, void* dptr);
+/* Copies are ordered on the context stream and return when complete. */
+int   vlrf_hip_h2d(vlrf_hip_ctx_t ctx, void* dst, const void* src, size_t bytes);
+int   vlrf_hip_d2h(vlrf_hip_ctx_t ctx, void* dst, const void* src, size_t bytes);
+int   vlrf_hip_memset(vlrf_hip_ctx_t ctx, void* dst, int value, size_t bytes);
+/* Event timing on the context stream: records start/stop around queued work. */
+int   vlrf_hip_timer_start(vlrf_hip_ctx_t ctx);
+int   vlrf_hip_timer_stop(vlrf_hip_ctx_t ctx, float* ms);  /* waits for the stop event */
+
+/* ============================================================================
+ * Attention
+ * ========================================================================== */
+/* Fused scaled-dot-product attention over f32 K/V, batched per head:
+ * Q [n_h,T,d_h], K/V [n_h,ctx_len,d_h], O [n_h,T,d_h]; d_h <= 128.
+ * Causal rule: key j is masked for query i when j > i + (ctx_len - T).
+ * Replaces: IBackend::sdp_attention (ibackend.hpp:79-82) and the CPU
+ * AttentionBlock::flash_attn_head per head (attention.hpp:207-309, 431-442). */
+int vlrf_hip_attn_f32(vlrf_hip_ctx_t ctx, const float* Q, const float* K, const float* V,
+                      float* O, int n_h, int T, int ctx_len, int d_h, float scale, int causal);
+
+/* ============================================================================
+ * KV cache (Q8_0 per token row, reference kv_cache.hpp:14-17,132-293).
+ * Device layout: per layer, K and V int8 [n_kv_heads][max_seq][d_head]
+ * (head-major, so one head's history is one contiguous stream) and one f32
+ * scale per token row for K and for V.
+ * ========================================================================== */
+/* Replaces: KVCache::KVCache (kv_cache.hpp:152-177), per layer. */
+int vlrf_hip_kv_create(vlrf_hip_ctx_t ctx, int n_layers, int max_seq, int n_kv_heads,
+                       int d_head, int dtype, vlrf_hip_kv_t* out);
+void vlrf_hip_kv_destroy(vlrf_hip_kv_t kv);
+/* Replaces: KVCache::reset (kv_cache.hpp:179-196): zero data, used = 0. */
+int vlrf_hip_kv_reset(vlrf_hip_kv_t kv);
+/* Tokens stored so far in `layer` (KVCache::used). */
+int vlrf_hip_kv_used(vlrf_hip_kv_t kv, int layer);
+/* Replaces: KVCache::append (kv_cache.hpp:215-251): quantizes T rows of
+ * device f32 k/v [T, n_kv_heads*d_head] bit-exactly as quantize_row_q8_0
+ * (kv_cache.hpp:102-117) at positions [used, used+T), then used += T.
+ * VLRF_HIP_ERR_OVERFLOW when used+T > max_seq (the reference throws). */
+int vlrf_hip_kv_append(vlrf_hip_kv_t kv, int layer, const float* k, const float* v, int T);
+/* Copies rows [row0,row0+n) of `layer` to host in the reference's token-major
+ * layout: k_q/v_q int8 [n, n_kv_heads*d_head], k_s/v_s f32 [n]. Synchronous. */
+int vlrf_hip_kv_read(vlrf_hip_kv_t kv, int layer, int row0, int n, int8_t* k_q, int8_t* v_q,
+                     float* k_s, float* v_s);
+/* Replaces: KVCache::dequant_into (kv_cache.hpp:259-286): device f32
+ * K_out/V_out [ctx_len, n_kv_heads*d_head], token-major like the reference. */
+int vlrf_hip_kv_dequant(vlrf_hip_kv_t kv, int layer, int ctx_len, float* K_out, float* V_out);
+/* Decode attention of one token over the quantized cache, GQA-aware split-K:
+ * q [n_heads*d_head] (already rotated), out [n_heads*d_head]; query head h
+ * reads kv head h/(n_heads/n_kv_heads); non-causal over [0, ctx_len).
+ * Replaces the decode branch of AttentionBlock::forward: dequant_into +
+ * reshape/expand_kv_heads + sdp_heads (attention.hpp:127-176). */
+int vlrf_hip_attn_decode(vlrf_hip_kv_t kv, int layer, const float* q, float* out,
+                         int n_heads, int ctx_len, float scale);
+
+/* ============================================================================
+ * Quantized linear: y[M,N] = x[M,K] . W[N,K]^T with W in a GGUF block format.
+ * Replaces: compute::linear -> IBackend::gemm(x, W, y, 1, 0, false, true)
+ * (compute.hpp:58-68, ibackend.hpp:61-63) for weights that the converter
+ * would otherwise dequantize offline (convert_gguf.py:233-263).
+ * ========================================================================== */
+/* Host blocks in the GGUF row layout: row n holds K/32 blocks of
+ * Q8_0 [f16 d][32 x int8] (34 B) or Q4_0 [f16 d][16 B: byte j = elements 2j
+ * (low nibble) and 2j+1 (high nibble)] (18 B); F32 is plain [N][K].
+ * Weights stay resident on the device until vlrf_hip_weight_free. K % 32 == 0
+ * for block types. Synchronous. */
+int vlrf_hip_weight_upload(vlrf_hip_ctx_t ctx, const void* host, int dtype, int N, int K,
+                           vlrf_hip_weight_t* out);
+void vlrf_hip_weight_free(vlrf_hip_weight_t w);
+size_t vlrf_hip_weight_bytes(vlrf_hip_weight_t w);   /* device bytes of the packed weight */
+/* x, y device f32, 1 <= M <= 16.  norm_w (nullable, device f32 [K]): x rows
+ * are first RMS-normalised with weight norm_w and `eps` (ops.hpp:478-499).
+ * residual (nullable, device f32 [M,N], may alias y): added after the product
+ * (the residual adds of transformer_block.hpp:149-159). */
+int vlrf_hip_qlinear(vlrf_hip_ctx_t ctx, vlrf_hip_weight_t w, const float* x, float* y, int M,
+                     const float* norm_w, float eps, const float* residual);
+
+/* FFN gate/up half of FeedForward::forward with the SwiGLU epilogue:
+ * h[M,F] = silu(rmsnorm(x).Wg^T) * (rmsnorm(x).Wu^T), silu(g) = g/(1+exp(-g)).
+ * Replaces: linear(x, fc1), linear(x, gate), silu_inplace, multiply_inplace
+ * (feedforward.hpp:54-62, ops.hpp:409-441).  norm_w nullable as above;
+ * wg and wu have the same shape and dtype. */
+int vlrf_hip_qlinear_swiglu(vlrf_hip_ctx_t ctx, vlrf_hip_weight_t wg, vlrf_hip_weight_t wu,
+                            const float* x, float* h, int M, const float* norm_w, float eps);
+
+/* ============================================================================
+ * Edge ops
+ * ========================================================================== */
+/* Replaces: ops::rms_norm (ops.hpp:478-499). x/out device [rows, D]. */
+int vlrf_hip_rmsnorm(vlrf_hip_ctx_t ctx, const float* x, const float* w, float* out,
+                     int rows, int D, float eps);
+/* Replaces: RopeCache::apply (rope.hpp:75-99) with tables built on the host
+ * exactly as RopeCache::init (rope.hpp:49-71): x device [T, n_heads*d_head]
+ * rotated in place (half-split pairs) for positions pos_offset+t < max_seq. */
+int vlrf_hip_rope(vlrf_hip_ctx_t ctx, float* x, int T, int n_heads, int d_head,
+                  int pos_offset, int max_seq, float theta);
+
+/* ============================================================================
+ * Host-side format helpers (no device needed)
+ * ========================================================================== */
+/* This build's block encoders (the reference ships decoders only):
+ * Q8_0: d = amax/127 stored as f16, q = round-half-away(x / f32(d16)) in [-127,127];
+ * Q4_0: d = (signed max-magnitude element)/-8 stored as f16,
+ *       nibble = min(15, (int)(x / f32(d16) + 8.5)).
+ * n % 32 == 0. dst holds n/32 blocks. */
+int vlrf_quantize_q8_0(const float* src, void* dst, int64_t n);
+int vlrf_quantize_q4_0(const float* src, void* dst, int64_t n);
+/* Block decode, convert_gguf.py:233-263 semantics. */
+int vlrf_dequantize(const void* src, int dtype, float* dst, int64_t n);
+/* Synthetic seeded data: counter-based (splitmix64 + Box-Muller in double),
+ * identical on any host.  out[i] = std * N(0,1) sample i of stream `stream`. */
+int vlrf_synth_normal(uint64_t seed, uint64_t stream, float std_dev, float* out, int64_t n);
+/* Uniform token ids in [0, vocab). */
+int vlrf_synth_tokens(uint64_t seed, uint64_t stream, int vocab, int32_t* out, int64_t n);
+
+/* ============================================================================
+ * Decoder model (Llama-style: RMSNorm, RoPE half-split, SwiGLU, GQA, Q8_0 KV).
+ * Replaces the decode hot loop of TransformerModel::forward/generate
+ * (transformer.hpp:335-424, 439-547) with a device-resident step: only token
+ * ids cross PCIe.
+ * ========================================================================== */
+typedef struct vlrf_hip_model_config {
+    int32_t vocab_size, d_model, d_ff, n_heads, n_kv_heads, n_layers, max_seq_len;
+    float   norm_eps, rope_theta;
+    int32_t weight_dtype;   /* VLRF_DT_Q8_0 / VLRF_DT_Q4_0 / VLRF_DT_F32 for the projections */
+} vlrf_hip_model_config;
+
+int  vlrf_hip_model_create(vlrf_hip_ctx_t ctx, const vlrf_hip_model_config* cfg,
+                           vlrf_hip_model_t* out);
+void vlrf_hip_model_destroy(vlrf_hip_model_t m);
+/* Sets one tensor by its reference WeightMap name (transformer.hpp:566-629 plus
+ * "layers.{l}.ffn.gate.weight"): embed.weight / lm_head.weight /
+ * ln_final.weight, layers.{l}.{ln1,ln2}.weight,
+ * layers.{l}.attn.{q,k,v,o}_proj.weight, layers.{l}.ffn.{gate,fc1,fc2}.weight.
+ * Norm weights and the embedding are f32 (dtype VLRF_DT_F32); projection and
+ * LM-head weights are in `dtype` host blocks.  Synchronous. */
+int  vlrf_hip_model_set_weight(vlrf_hip_model_t m, const char* name, const void* host,
+                               int dtype, int rows, int cols);
+/* TransformerModel::reset_kv_cache (transformer.hpp:311-315). */
+int  vlrf_hip_model_reset(vlrf_hip_model_t m);
+int  vlrf_hip_model_used(vlrf_hip_model_t m);
+/* One decode step of token `token` (= forward({token}, true) + argmax,
+ * transformer.hpp:472-482): returns the greedy next id in *next and, when
+ * logits is non-NULL, copies the logits [vocab] to host. Synchronous. */
+int  vlrf_hip_model_step(vlrf_hip_model_t m, int32_t token, int32_t* next, float* logits);
+/* Feeds `n` tokens one step at a time (the prompt), without reading logits
+ * back; *next receives the greedy id after the last one. */
+int  vlrf_hip_model_prefill(vlrf_hip_model_t m, const int32_t* ids, int n, int32_t* next);
+/* Greedy generation of n_steps tokens starting from `first` entirely on the
+ * device (token feedback on the GPU, replayed HIP graph); out_ids (host,
+ * n_steps) receives the generated ids.  Synchronous. */
+int  vlrf_hip_model_generate(vlrf_hip_model_t m, int32_t first, int n_steps, int32_t* out_ids);
+/* Queues n_steps greedy steps without waiting (for timing); the ids stay on
+ * the device and are fetched by vlrf_hip_model_read_generated. */
+int  vlrf_hip_model_generate_async(vlrf_hip_model_t m, int32_t first, int n_steps);
+int  vlrf_hip_model_read_generated(vlrf_hip_model_t m, int32_t* out_ids, int n);
+/* Device bytes read per decode step at context length ctx_len, by stream:
+ * [0] projection + LM-head weights, [1] KV cache, [2] everything else
+ * (norm weights, embedding row, activations).  For roofline accounting. */
+int  vlrf_hip_model_step_bytes(vlrf_hip_model_t m, int ctx_len, double out[3]);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* VLRF_HIP_H */

@@ -1,0 +1,108 @@
+"""GPU parity: f32 flash attention (IBackend::sdp_attention) and the Q8_0-KV
+GQA decode attention, against the oracle's restatement of
+AttentionBlock::flash_attn_head (attention.hpp:207-309).
+
+Inputs are seeded N(0,1) from vlrf_amd.formats.normal (the reference test's
+mt19937 stream is not reproducible outside libstdc++; shapes, masks and
+tolerances follow tests/test_flash_attention.cpp:77-121)."""
+import numpy as np
+import pytest
+
+from conftest import rel_err
+from vlrf_amd import formats as F
+
+pytestmark = pytest.mark.gpu
+
+# (T, ctx, d_h, causal, seed): tests/test_flash_attention.cpp:96-121
+REF_SHAPES = [(64, 64, 32, False, 1), (128, 128, 32, True, 2), (37, 37, 8, True, 5),
+              (130, 130, 64, True, 6), (1, 1, 16, False, 3), (1, 200, 16, False, 4),
+              (1, 1, 4, True, 8), (200, 500, 64, True, 7), (300, 300, 128, False, 9)]
+
+
+def _qkv(seed, n_h, T, ctx_len, d):
+    Q = F.normal(seed, "Q", n_h * T * d).reshape(n_h, T, d)
+    K = F.normal(seed, "K", n_h * ctx_len * d).reshape(n_h, ctx_len, d)
+    V = F.normal(seed, "V", n_h * ctx_len * d).reshape(n_h, ctx_len, d)
+    return Q, K, V
+
+
+def _run_gpu(ctx, Q, K, V, scale, causal):
+    n_h, T, d = Q.shape
+    ctx_len = K.shape[1]
+    dq, dk, dv = ctx.to_device(Q), ctx.to_device(K), ctx.to_device(V)
+    do = ctx.alloc(Q.nbytes)
+    ctx.sdp_attention(dq, dk, dv, do, n_h, T, ctx_len, d, scale, causal)
+    return do.download(Q.shape)
+
+
+@pytest.mark.parametrize("T,ctx_len,d,causal,seed", REF_SHAPES)
+def test_sdp_attention_reference_shapes(ctx, orc, T, ctx_len, d, causal, seed):
+    print(f"[case] sdp T={T} ctx={ctx_len} d={d} causal={causal}", flush=True)
+    n_h = 2
+    Q, K, V = _qkv(seed, n_h, T, ctx_len, d)
+    scale = np.float32(1.0) / np.sqrt(np.float32(d))
+    out = _run_gpu(ctx, Q, K, V, scale, causal)
+    ref = orc.sdp_attention(Q, K, V, scale, causal)
+    assert np.max(np.abs(out - ref)) <= 1e-4          # the reference test's own bound
+    assert rel_err(out, ref) <= 1e-3
+
+
+def test_config1_decode_f32(ctx, orc):
+    """1 query, 8 heads, d 64, KV 512, non-causal, scale 1/8."""
+    Q, K, V = _qkv(11, 8, 1, 512, 64)
+    out = _run_gpu(ctx, Q, K, V, np.float32(0.125), False)
+    ref = orc.sdp_attention(Q, K, V, np.float32(0.125), False)
+    assert np.max(np.abs(out - ref)) <= 1e-4
+    assert rel_err(out, ref) <= 1e-3
+
+
+@pytest.mark.parametrize("ctx_len", [1, 255, 256, 257, 1000])
+def test_decode_f32_split_boundaries(ctx, orc, ctx_len):
+    """Split-K chunk boundaries (256 tokens) and a single-token context."""
+    Q, K, V = _qkv(ctx_len, 4, 1, ctx_len, 128)
+    s = np.float32(1.0) / np.sqrt(np.float32(128))
+    out = _run_gpu(ctx, Q, K, V, s, False)
+    ref = orc.sdp_attention(Q, K, V, s, False)
+    assert rel_err(out, ref) <= 1e-3
+
+
+def _gqa_reference(orc, q, kq, vq, ks, vs, n_heads, n_kv, d, ctx_len, scale):
+    """Reference decode attention: dequant_into (kv_cache.hpp:259-286), GQA head
+    h -> kv head h/(n_heads/n_kv) (attention.hpp:328-342), non-causal
+    flash_attn_head per head."""
+    row = n_kv * d
+    Kd = kq[:ctx_len].astype(np.float32) * ks[:ctx_len, None]
+    Vd = vq[:ctx_len].astype(np.float32) * vs[:ctx_len, None]
+    out = np.zeros(n_heads * d, np.float32)
+    rep = n_heads // n_kv
+    for h in range(n_heads):
+        g = h // rep
+        out[h * d:(h + 1) * d] = orc.flash_attn_head(q[h * d:(h + 1) * d][None, :],
+                                                     Kd[:, g * d:(g + 1) * d],
+                                                     Vd[:, g * d:(g + 1) * d], scale, False)[0]
+    assert Kd.shape[1] == row
+    return out
+
+
+@pytest.mark.parametrize("n_heads,n_kv,d,ctx_len", [(32, 4, 64, 4096), (32, 4, 64, 2048),
+                                                    (8, 8, 64, 300), (16, 2, 128, 777),
+                                                    (8, 1, 64, 1)])
+def test_q8_decode_attention(ctx, orc, n_heads, n_kv, d, ctx_len):
+    """BASELINE config 2 (32q/4kv, d 64, ctx 4096) and other GQA groupings."""
+    import vlrf_amd as V_
+    print(f"[case] q8 decode heads={n_heads}/{n_kv} d={d} ctx={ctx_len}", flush=True)
+    row = n_kv * d
+    kv = V_.KVCache(ctx, 1, ctx_len + 3, n_kv, d)
+    K = F.normal(5, "Kc", ctx_len * row)
+    Vv = F.normal(5, "Vc", ctx_len * row)
+    kv.append(0, ctx.to_device(K), ctx.to_device(Vv), ctx_len)
+    kq, vq, ks, vs = kv.read(0, 0, ctx_len)
+    q = F.normal(5, "q", n_heads * d)
+    dq = ctx.to_device(q)
+    dout = ctx.alloc(q.nbytes)
+    scale = np.float32(1.0) / np.sqrt(np.float32(d))
+    kv.attention_decode(0, dq, dout, n_heads, ctx_len, scale)
+    out = dout.download(q.shape)
+    ref = _gqa_reference(orc, q, kq, vq, ks, vs, n_heads, n_kv, d, ctx_len, scale)
+    assert rel_err(out, ref) <= 1e-3
+    assert np.max(np.abs(out - ref)) <= 1e-4

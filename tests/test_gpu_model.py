@@ -1,0 +1,94 @@
+"""GPU parity of the whole decode step (TransformerModel::forward/generate,
+transformer.hpp:335-547) on a small Llama-style model with the same structure
+as the 1.1B benchmark model (RMSNorm, RoPE, GQA, SwiGLU, Q8_0 KV cache).
+
+The oracle runs the reference algorithm on the decoded f32 weights and does a
+real prefill (M = prompt length GEMMs, causal attention), as
+TransformerModel::generate does; the GPU feeds the prompt one token at a time
+through the decode step.  Both then decode greedily starting from the last
+prompt id (the reference feeds it twice, transformer.hpp:448-482)."""
+import numpy as np
+import pytest
+
+import vlrf_amd as V
+from conftest import rel_err
+from vlrf_amd import formats as F
+
+pytestmark = pytest.mark.gpu
+
+
+def _models(ctx, orc, cfg, seed):
+    m = V.Model(ctx, cfg)
+    w = F.load_model(m, seed, want_f32=True, norm_std=0.1)
+    om = orc.Model(cfg, w, n_threads=4)
+    return m, om, w
+
+
+@pytest.mark.parametrize("dtype", [V.DT_Q8_0, V.DT_Q4_0])
+def test_tiny_greedy_stream(ctx, orc, dtype):
+    cfg = F.tiny(dtype, n_layers=3, max_seq_len=128)
+    m, om, _ = _models(ctx, orc, cfg, 21)
+    prompt = F.tokens(21, "prompt", 40, cfg["vocab_size"])
+    gpu = m.generate(prompt, 64)
+    om.reset()
+    om.forward(prompt)
+    last, ref = int(prompt[-1]), []
+    for _ in range(64):
+        last = om.forward([last])
+        ref.append(last)
+    assert list(gpu) == ref
+    assert m.used == om.used == 40 + 64
+
+
+def test_tiny_logits_teacher_forced(ctx, orc):
+    """Per-step logits against the oracle on the same token feed."""
+    cfg = F.tiny(V.DT_Q8_0, n_layers=2, max_seq_len=96)
+    m, om, _ = _models(ctx, orc, cfg, 22)
+    ids = F.tokens(22, "feed", 70, cfg["vocab_size"])
+    m.reset()
+    om.reset()
+    worst = 0.0
+    for t in ids:
+        g_next, g_logits = m.step(int(t), want_logits=True)
+        o_next, o_logits = om.forward([int(t)], want_logits=True)
+        worst = max(worst, rel_err(g_logits, o_logits))
+        assert g_next == int(np.argmax(g_logits))
+    assert worst <= 1e-3, worst
+    # KV caches: same codes up to rare +/-1 flips where a K/V value sits on a
+    # rounding boundary (f32 GEMV order differs from the AVX2 reference order).
+    kv_gpu = V.KVCache  # noqa: F841  (the model's cache is internal; compare via logits)
+
+
+def test_generate_matches_step_loop(ctx, orc):
+    """Device token feedback (replayed graph) == host-driven step loop."""
+    cfg = F.tiny(V.DT_Q8_0, n_layers=2, max_seq_len=80)
+    m, _, _ = _models(ctx, orc, cfg, 23)
+    prompt = F.tokens(23, "p", 10, cfg["vocab_size"])
+    a = m.generate(prompt, 50)
+    m.reset()
+    m.prefill(prompt)
+    last, b = int(prompt[-1]), []
+    for _ in range(50):
+        last = m.step(last)
+        b.append(last)
+    assert list(a) == b
+
+
+def test_model_capacity_and_errors(ctx, orc):
+    cfg = F.tiny(V.DT_Q8_0, n_layers=1, max_seq_len=8)
+    m, _, _ = _models(ctx, orc, cfg, 24)
+    m.reset()
+    m.prefill(np.arange(6, dtype=np.int32))
+    with pytest.raises(V.HipError) as e:
+        m.generate_ids(1, 3)             # 6 + 3 > 8
+    assert e.value.rc == -4
+    with pytest.raises(V.HipError):
+        m.step(cfg["vocab_size"])        # token id out of range
+    m.generate_ids(1, 2)
+    assert m.used == 8
+
+
+def test_unset_weights_rejected(ctx):
+    m = V.Model(ctx, F.tiny(V.DT_Q8_0, n_layers=1))
+    with pytest.raises(V.HipError):
+        m.step(0)

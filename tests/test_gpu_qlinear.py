@@ -1,0 +1,89 @@
+"""GPU parity: dequant-fused quantized linear (compute::linear on weights
+decoded from GGUF Q8_0/Q4_0 blocks, convert_gguf.py:233-263), BASELINE
+config 3 shapes, plus the fused RMSNorm prologue, residual epilogue and the
+SwiGLU gate/up variant.  Oracle: ops::gemm restated (oracle/vlrf_oracle.c)
+on the decoded f32 weights.  Tolerance: 1e-3 relative (fp32 path)."""
+import numpy as np
+import pytest
+
+import vlrf_amd as V
+from conftest import rel_err
+from vlrf_amd import formats as F
+
+pytestmark = pytest.mark.gpu
+
+
+def _weight(ctx, seed, name, N, K, dtype):
+    w = F.normal(seed, name, N * K, 0.02)
+    blocks = F.quantize(w, dtype)
+    dec = F.dequantize(blocks, dtype, N * K).reshape(N, K) if dtype != V.DT_F32 else w.reshape(N, K)
+    return V.QuantWeight(ctx, blocks, dtype, N, K), dec
+
+
+@pytest.mark.parametrize("dtype", [V.DT_Q8_0, V.DT_Q4_0])
+@pytest.mark.parametrize("N,K", [(5632, 2048), (2048, 5632)])
+@pytest.mark.parametrize("M", [1, 4, 16])
+def test_config3_qlinear(ctx, orc, dtype, N, K, M):
+    print(f"[case] qlinear dtype={dtype} N={N} K={K} M={M}", flush=True)
+    w, dec = _weight(ctx, 7, f"W{N}x{K}", N, K, dtype)
+    x = F.normal(7, f"x{M}", M * K).reshape(M, K)
+    dx, dy = ctx.to_device(x), ctx.alloc(M * N * 4)
+    ctx.qlinear(w, dx, dy, M)
+    y = dy.download((M, N))
+    ref = orc.linear(x, dec)
+    assert rel_err(y, ref) <= 1e-3
+    np.testing.assert_allclose(y, ref, rtol=1e-3, atol=1e-5 * np.abs(ref).max())
+
+
+@pytest.mark.parametrize("M", [1, 3, 9])
+@pytest.mark.parametrize("N,K", [(37, 64), (300, 96), (8, 1056)])
+def test_qlinear_ragged_shapes(ctx, orc, M, N, K):
+    """Row counts not divisible by the 8-row workgroup tile; K not a multiple of
+    the 1024 staging tile; M between the 1/4/16 instantiations."""
+    for dtype in (V.DT_Q8_0, V.DT_Q4_0, V.DT_F32):
+        w, dec = _weight(ctx, 8, f"R{N}x{K}", N, K, dtype)
+        x = F.normal(8, f"xr{M}", M * K).reshape(M, K)
+        dx, dy = ctx.to_device(x), ctx.alloc(M * N * 4)
+        ctx.qlinear(w, dx, dy, M)
+        assert rel_err(dy.download((M, N)), orc.linear(x, dec)) <= 1e-3
+
+
+def test_qlinear_fused_norm_and_residual(ctx, orc):
+    """y = residual + W . rms_norm(x; g) (ops.hpp:478-499 then the residual add)."""
+    N, K, M = 2560, 2048, 1
+    w, dec = _weight(ctx, 9, "Wqkv", N, K, V.DT_Q8_0)
+    x = F.normal(9, "xn", M * K).reshape(M, K) * 0.05
+    g = 1.0 + F.normal(9, "g", K, 0.1)
+    res = F.normal(9, "res", M * N).reshape(M, N)
+    dx, dg, dr = ctx.to_device(x), ctx.to_device(g), ctx.to_device(res)
+    dy = ctx.alloc(M * N * 4)
+    ctx.qlinear(w, dx, dy, M, norm_w=dg, eps=1e-5)
+    ref = orc.linear(orc.rms_norm(x, g, 1e-5), dec)
+    assert rel_err(dy.download((M, N)), ref) <= 1e-3
+    ctx.qlinear(w, dx, dr, M, norm_w=dg, eps=1e-5, residual=dr)      # in place on the residual
+    assert rel_err(dr.download((M, N)), ref + res) <= 1e-3
+
+
+@pytest.mark.parametrize("dtype", [V.DT_Q8_0, V.DT_Q4_0])
+@pytest.mark.parametrize("M", [1, 4])
+def test_swiglu_gate_up(ctx, orc, dtype, M):
+    """h = silu(x.Wg^T) * (x.Wu^T) (feedforward.hpp:54-62) with the fused norm."""
+    Fd, K = 5632, 2048
+    wg, gdec = _weight(ctx, 10, "Wg", Fd, K, dtype)
+    wu, udec = _weight(ctx, 10, "Wu", Fd, K, dtype)
+    x = F.normal(10, "xs", M * K).reshape(M, K)
+    g = np.ones(K, np.float32)
+    dx, dg, dh = ctx.to_device(x), ctx.to_device(g), ctx.alloc(M * Fd * 4)
+    ctx.qlinear_swiglu(wg, wu, dx, dh, M, norm_w=dg, eps=1e-5)
+    xn = orc.rms_norm(x, g, 1e-5)
+    ref = orc.silu_mul(orc.linear(xn, udec), orc.linear(xn, gdec))
+    assert rel_err(dh.download((M, Fd)), ref) <= 1e-3
+
+
+def test_qlinear_rejects_bad_shapes(ctx):
+    w, _ = _weight(ctx, 11, "Wbad", 64, 64, V.DT_Q8_0)
+    x = ctx.alloc(64 * 4 * 17)
+    with pytest.raises(V.HipError):
+        ctx.qlinear(w, x, ctx.alloc(64 * 4 * 17), 17)      # M above 16
+    with pytest.raises(V.HipError):
+        ctx.qlinear(w, x, x, 1)                             # x aliasing y

@@ -1,0 +1,147 @@
+// internal.hpp - shared declarations of the gfx950 decode backend.
+//
+// Device code here targets CDNA4 wave64 only.  Host-side launchers check every
+// operand shape against what their kernel and grid assume before launching.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "../../include/vlrf_hip.h"
+
+namespace vlrf_hip {
+
+// ---- error handling ---------------------------------------------------------
+void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+
+#define VH_CHECK(expr)                                                            \
+    do {                                                                          \
+        hipError_t e_ = (expr);                                                   \
+        if (e_ != hipSuccess) {                                                   \
+            ::vlrf_hip::set_error("%s failed: %s (%s:%d)", #expr,                \
+                                  hipGetErrorString(e_), __FILE__, __LINE__);     \
+            return VLRF_HIP_ERR_RUNTIME;                                          \
+        }                                                                         \
+    } while (0)
+
+#define VH_ARG(cond, ...)                                                         \
+    do {                                                                          \
+        if (!(cond)) {                                                            \
+            ::vlrf_hip::set_error(__VA_ARGS__);                                   \
+            return VLRF_HIP_ERR_ARG;                                              \
+        }                                                                         \
+    } while (0)
+
+// Checks the launch that was just queued.
+#define VH_LAUNCHED()                                                             \
+    do {                                                                          \
+        hipError_t e_ = hipGetLastError();                                        \
+        if (e_ != hipSuccess) {                                                   \
+            ::vlrf_hip::set_error("kernel launch failed: %s (%s:%d)",            \
+                                  hipGetErrorString(e_), __FILE__, __LINE__);     \
+            return VLRF_HIP_ERR_RUNTIME;                                          \
+        }                                                                         \
+    } while (0)
+
+// ---- device-resident quantized weight ---------------------------------------
+// Q8_0: q = int8 [N][K] (the block's 32 codes, rows contiguous),
+//       d = f16 [N][K/32] (block scales).
+// Q4_0: q = uint8 [N][K/2], byte j of a row's block b holds elements
+//       32b+2j (low nibble) and 32b+2j+1 (high nibble), as the GGUF block;
+//       d = f16 [N][K/32].
+// F32:  f = float [N][K].
+struct DevWeight {
+    int dtype = VLRF_DT_F32;
+    int N = 0, K = 0;
+    uint8_t* q = nullptr;
+    __half* d = nullptr;
+    float* f = nullptr;
+};
+
+size_t weight_device_bytes(int dtype, int N, int K);
+// Splits host GGUF blocks of rows [row0,row0+nrows) into the device arrays.
+int weight_upload_rows(hipStream_t s, DevWeight& w, const void* host, int row0, int nrows);
+int weight_alloc(DevWeight& w, int dtype, int N, int K);
+void weight_release(DevWeight& w);
+
+// ---- KV cache ------------------------------------------------------------------
+struct KVLayer {
+    int8_t* k = nullptr;   // [n_kv][max_seq][d_head]
+    int8_t* v = nullptr;
+    float* ks = nullptr;   // [max_seq]
+    float* vs = nullptr;
+};
+
+// ---- launchers (all queue on `s`) -----------------------------------------------
+// y[M,N] = (norm_w ? rmsnorm(x) : x) . W^T (+ residual)
+int launch_qlinear(hipStream_t s, const DevWeight& w, const float* x, float* y, int M,
+                   const float* norm_w, float eps, const float* residual);
+// h[M,N] = silu(rmsnorm(x).Wg^T) * (rmsnorm(x).Wu^T)
+int launch_qlinear_swiglu(hipStream_t s, const DevWeight& wg, const DevWeight& wu,
+                          const float* x, float* h, int M, const float* norm_w, float eps);
+
+int launch_rmsnorm(hipStream_t s, const float* x, const float* w, float* out, int rows, int D,
+                   float eps);
+int launch_rope(hipStream_t s, float* x, int T, int n_heads, int d_head, int pos_offset,
+                int max_seq, const float* cos_t, const float* sin_t);
+
+// Quantize T rows into the cache at positions pos(+t); pos comes from *pos_dev
+// when non-null.  Optionally applies RoPE to q (n_q_heads) and k first (decode
+// fusion: q rotated in place, k rotated before quantization).
+int launch_kv_append(hipStream_t s, const KVLayer& L, int n_kv, int d_head, int max_seq,
+                     const float* k, const float* v, int T, int pos, const int* pos_dev);
+int launch_rope_append(hipStream_t s, const KVLayer& L, float* q, const float* k,
+                       const float* v, int n_heads, int n_kv, int d_head, int max_seq,
+                       const int* pos_dev, const float* cos_t, const float* sin_t);
+int launch_kv_dequant(hipStream_t s, const KVLayer& L, int n_kv, int d_head, int max_seq,
+                      int ctx_len, float* K_out, float* V_out);
+
+// Split-K decode attention. KV either Q8 cache (kq/vq + scales, head stride
+// max_seq*d) or f32 [n_kv][ctx][d] (kf/vf).  ctx from *ctx_dev (+1 when
+// ctx_plus_one) when non-null.  part must hold n_heads*n_splits*(d+2) floats.
+int attn_decode_splits(int max_ctx);
+int launch_attn_decode(hipStream_t s, const float* q, const int8_t* kq, const int8_t* vq,
+                       const float* ks, const float* vs, const float* kf, const float* vf,
+                       long head_stride, int n_heads, int n_kv, int d_head, int ctx_len,
+                       const int* ctx_dev, int n_splits, float scale, float* part, float* out);
+int launch_attn_f32_tiled(hipStream_t s, const float* Q, const float* K, const float* V,
+                          float* O, int n_h, int T, int ctx_len, int d_h, float scale,
+                          int causal);
+
+int launch_embed(hipStream_t s, const float* table, const int* tok_dev, float* x, int D);
+// argmax over logits[n] (first maximum) -> state[0] (token), appends to
+// gen_ids[state[2]++], state[1] (position) += 1.
+int launch_argmax_step(hipStream_t s, const float* logits, int n, int* state, int* gen_ids,
+                       int gen_cap);
+
+// ---- wave64 reductions (DPP within rows of 16, then cross-row shuffles) -------
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+    v += dpp_f<0xB1>(v);    // quad_perm [1,0,3,2]
+    v += dpp_f<0x4E>(v);    // quad_perm [2,3,0,1]
+    v += dpp_f<0x141>(v);   // row_half_mirror
+    v += dpp_f<0x140>(v);   // row_mirror
+    v += __shfl_xor(v, 16);
+    v += __shfl_xor(v, 32);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    v = fmaxf(v, dpp_f<0x141>(v));
+    v = fmaxf(v, dpp_f<0x140>(v));
+    v = fmaxf(v, __shfl_xor(v, 16));
+    v = fmaxf(v, __shfl_xor(v, 32));
+    return v;
+}
+
+}  // namespace vlrf_hip

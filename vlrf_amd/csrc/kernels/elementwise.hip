@@ -1,0 +1,273 @@
+// elementwise.hip - edge ops of the decode step: RMSNorm, RoPE, the Q8_0 KV
+// append (quantize) and dequant, embedding gather and greedy argmax.
+#include "../internal.hpp"
+
+#include <cmath>
+
+namespace vlrf_hip {
+namespace {
+
+// Block-wide reductions for 256-thread blocks.
+__device__ __forceinline__ float block_max256(float v, float* red) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    v = wave_max(v);
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    v = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+    return v;
+}
+
+__device__ __forceinline__ float block_sum256(float v, float* red) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    v = wave_sum(v);
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    v = (red[0] + red[1]) + (red[2] + red[3]);
+    __syncthreads();
+    return v;
+}
+
+// One RoPE pair, rope.hpp:90-96.  Contraction off: the reference's scalar
+// build rounds each product separately, so this matches it bit for bit given
+// the same cos/sin tables.
+__device__ __forceinline__ void rope_pair(float* v, int i, int half, float c, float s) {
+#pragma clang fp contract(off)
+    const float x0 = v[i], x1 = v[i + half];
+    const float a = x0 * c;
+    const float b = x1 * s;
+    const float e = x1 * c;
+    const float f = x0 * s;
+    v[i] = a - b;
+    v[i + half] = e + f;
+}
+
+// quantize_row_q8_0 (kv_cache.hpp:102-117) of one row of n_kv*D floats into
+// the head-major cache at token position p.  Bit-exact: max is
+// order-independent, amax/127 and 1/scale are correctly rounded (HIP default,
+// also forced by the build), roundf rounds half away from zero as lround.
+__device__ void quantize_row_to_cache(const float* __restrict__ src, int8_t* __restrict__ dst,
+                                      float* __restrict__ sc, int p, int n_kv, int D,
+                                      int max_seq, float* red) {
+    const int row = n_kv * D;
+    float amax = 0.f;
+    for (int i = threadIdx.x; i < row; i += 256) amax = fmaxf(amax, fabsf(src[i]));
+    amax = block_max256(amax, red);
+    float inv = 0.f;
+    if (amax != 0.f) {
+        const float scale = amax / 127.f;
+        inv = 1.f / scale;
+        if (threadIdx.x == 0) sc[p] = scale;
+    } else if (threadIdx.x == 0) {
+        sc[p] = 0.f;
+    }
+    for (int i = threadIdx.x; i < row; i += 256) {
+        int q = 0;
+        if (amax != 0.f) {
+            q = (int)roundf(src[i] * inv);
+            q = min(127, max(-127, q));
+        }
+        const int h = i / D, d = i - h * D;
+        dst[((size_t)h * max_seq + p) * D + d] = (int8_t)q;
+    }
+}
+
+__global__ __launch_bounds__(256) void kv_append_kernel(int8_t* kq, int8_t* vq, float* ks, float* vs,
+                                                        const float* __restrict__ k,
+                                                        const float* __restrict__ v, int n_kv, int D,
+                                                        int max_seq, int pos, const int* pos_dev) {
+    __shared__ float red[4];
+    const int t = blockIdx.x;
+    const int p = (pos_dev ? *pos_dev : pos) + t;
+    if (p < 0 || p >= max_seq) return;   // host checks capacity; never write past the cache
+    const size_t row = (size_t)n_kv * D;
+    quantize_row_to_cache(k + t * row, kq, ks, p, n_kv, D, max_seq, red);
+    quantize_row_to_cache(v + t * row, vq, vs, p, n_kv, D, max_seq, red);
+}
+
+// Decode fusion: rotate q (n_heads) in place and k (n_kv) at position *pos_dev,
+// then quantize k and v into the cache (attention.hpp:109-128 order).
+__global__ __launch_bounds__(256) void rope_append_kernel(int8_t* kq, int8_t* vq, float* ks,
+                                                          float* vs, float* q, const float* __restrict__ k,
+                                                          const float* __restrict__ v, int n_heads,
+                                                          int n_kv, int D, int max_seq,
+                                                          const int* __restrict__ pos_dev,
+                                                          const float* __restrict__ cos_t,
+                                                          const float* __restrict__ sin_t) {
+    __shared__ float red[4];
+    __shared__ float kr[1024];
+    const int p = *pos_dev;
+    if (p < 0 || p >= max_seq) return;   // host checks capacity; never write past the cache
+    const int half = D / 2;
+    const int row = n_kv * D;
+    const float* c = cos_t + (size_t)p * half;
+    const float* s = sin_t + (size_t)p * half;
+    for (int i = threadIdx.x; i < row; i += 256) kr[i] = k[i];
+    __syncthreads();
+    for (int i = threadIdx.x; i < n_heads * half; i += 256) {
+        const int h = i / half, j = i - h * half;
+        rope_pair(q + (size_t)h * D, j, half, c[j], s[j]);
+    }
+    for (int i = threadIdx.x; i < n_kv * half; i += 256) {
+        const int h = i / half, j = i - h * half;
+        rope_pair(kr + h * D, j, half, c[j], s[j]);
+    }
+    __syncthreads();
+    quantize_row_to_cache(kr, kq, ks, p, n_kv, D, max_seq, red);
+    quantize_row_to_cache(v, vq, vs, p, n_kv, D, max_seq, red);
+}
+
+__global__ __launch_bounds__(256) void kv_dequant_kernel(const int8_t* __restrict__ kq,
+                                                         const int8_t* __restrict__ vq,
+                                                         const float* __restrict__ ks,
+                                                         const float* __restrict__ vs, int n_kv, int D,
+                                                         int max_seq, float* K_out, float* V_out) {
+    const int t = blockIdx.x;
+    const int row = n_kv * D;
+    for (int i = threadIdx.x; i < row; i += 256) {
+        const int h = i / D, d = i - h * D;
+        const size_t src = ((size_t)h * max_seq + t) * D + d;
+        K_out[(size_t)t * row + i] = (float)kq[src] * ks[t];
+        V_out[(size_t)t * row + i] = (float)vq[src] * vs[t];
+    }
+}
+
+// ops::rms_norm (ops.hpp:478-499) per row: y = x * (1/sqrt(sum(x^2)/D + eps)) * w.
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ x,
+                                                      const float* __restrict__ w, float* out, int D,
+                                                      float eps) {
+    __shared__ float red[4];
+    const float* xr = x + (size_t)blockIdx.x * D;
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < D; i += 256) ss += xr[i] * xr[i];
+    ss = block_sum256(ss, red);
+    const float inv = 1.f / sqrtf(ss / (float)D + eps);
+    float* o = out + (size_t)blockIdx.x * D;
+    for (int i = threadIdx.x; i < D; i += 256) o[i] = xr[i] * inv * w[i];
+}
+
+__global__ __launch_bounds__(256) void rope_kernel(float* x, int n_heads, int D, int pos_offset,
+                                                   int max_seq, const float* __restrict__ cos_t,
+                                                   const float* __restrict__ sin_t) {
+    const int t = blockIdx.x, pos = pos_offset + t;
+    if (pos >= max_seq) return;
+    const int half = D / 2;
+    float* row = x + (size_t)t * n_heads * D;
+    const float* c = cos_t + (size_t)pos * half;
+    const float* s = sin_t + (size_t)pos * half;
+    for (int i = threadIdx.x; i < n_heads * half; i += 256) {
+        const int h = i / half, j = i - h * half;
+        rope_pair(row + (size_t)h * D, j, half, c[j], s[j]);
+    }
+}
+
+__global__ __launch_bounds__(256) void embed_kernel(const float* __restrict__ table,
+                                                    const int* __restrict__ tok, float* x, int D) {
+    const float* r = table + (size_t)(*tok) * D;
+    for (int i = threadIdx.x; i < D; i += 256) x[i] = r[i];
+}
+
+// sampler::argmax (transformer.hpp:43-47): first index of the maximum.
+__global__ __launch_bounds__(1024) void argmax_step_kernel(const float* __restrict__ logits, int n,
+                                                           int* state, int* gen_ids, int gen_cap) {
+    __shared__ float bv[1024];
+    __shared__ int bi[1024];
+    const int tid = threadIdx.x;
+    float best = -INFINITY;
+    int idx = -1;
+    for (int i = tid; i < n; i += 1024) {
+        const float v = logits[i];
+        if (idx < 0 || best < v) { best = v; idx = i; }
+    }
+    bv[tid] = best;
+    bi[tid] = idx;
+    __syncthreads();
+    for (int off = 512; off > 0; off >>= 1) {
+        if (tid < off) {
+            const float ov = bv[tid + off];
+            const int oi = bi[tid + off];
+            const int mi = bi[tid];
+            if (oi >= 0 && (mi < 0 || bv[tid] < ov || (bv[tid] == ov && oi < mi))) {
+                bv[tid] = ov;
+                bi[tid] = oi;
+            }
+        }
+        __syncthreads();
+    }
+    if (tid == 0) {
+        const int tok = bi[0] < 0 ? 0 : bi[0];
+        state[0] = tok;
+        const int g = state[2];
+        if (g < gen_cap) gen_ids[g] = tok;
+        state[2] = g + 1;
+        state[1] = state[1] + 1;
+    }
+}
+
+}  // namespace
+
+int launch_kv_append(hipStream_t s, const KVLayer& L, int n_kv, int d_head, int max_seq,
+                     const float* k, const float* v, int T, int pos, const int* pos_dev) {
+    VH_ARG(T >= 1 && n_kv >= 1 && d_head >= 1, "kv_append: empty shape");
+    if (!pos_dev) VH_ARG(pos >= 0 && pos + T <= max_seq, "kv_append: rows [%d,%d) beyond max_seq %d",
+                         pos, pos + T, max_seq);
+    hipLaunchKernelGGL(kv_append_kernel, dim3(T), dim3(256), 0, s, L.k, L.v, L.ks, L.vs, k, v, n_kv,
+                       d_head, max_seq, pos, pos_dev);
+    VH_LAUNCHED();
+    return VLRF_HIP_OK;
+}
+
+int launch_rope_append(hipStream_t s, const KVLayer& L, float* q, const float* k, const float* v,
+                       int n_heads, int n_kv, int d_head, int max_seq, const int* pos_dev,
+                       const float* cos_t, const float* sin_t) {
+    VH_ARG(n_kv * d_head <= 1024, "rope_append: kv row %d exceeds 1024", n_kv * d_head);
+    VH_ARG(d_head % 2 == 0, "rope_append: odd d_head");
+    hipLaunchKernelGGL(rope_append_kernel, dim3(1), dim3(256), 0, s, L.k, L.v, L.ks, L.vs, q, k, v,
+                       n_heads, n_kv, d_head, max_seq, pos_dev, cos_t, sin_t);
+    VH_LAUNCHED();
+    return VLRF_HIP_OK;
+}
+
+int launch_kv_dequant(hipStream_t s, const KVLayer& L, int n_kv, int d_head, int max_seq,
+                      int ctx_len, float* K_out, float* V_out) {
+    VH_ARG(ctx_len >= 0 && ctx_len <= max_seq, "kv_dequant: ctx_len %d outside [0,%d]", ctx_len, max_seq);
+    if (ctx_len == 0) return VLRF_HIP_OK;
+    hipLaunchKernelGGL(kv_dequant_kernel, dim3(ctx_len), dim3(256), 0, s, L.k, L.v, L.ks, L.vs, n_kv,
+                       d_head, max_seq, K_out, V_out);
+    VH_LAUNCHED();
+    return VLRF_HIP_OK;
+}
+
+int launch_rmsnorm(hipStream_t s, const float* x, const float* w, float* out, int rows, int D,
+                   float eps) {
+    VH_ARG(rows >= 1 && D >= 1, "rmsnorm: empty shape");
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, s, x, w, out, D, eps);
+    VH_LAUNCHED();
+    return VLRF_HIP_OK;
+}
+
+int launch_rope(hipStream_t s, float* x, int T, int n_heads, int d_head, int pos_offset, int max_seq,
+                const float* cos_t, const float* sin_t) {
+    VH_ARG(T >= 1 && n_heads >= 1 && d_head >= 2 && d_head % 2 == 0, "rope: bad shape");
+    VH_ARG(pos_offset >= 0, "rope: negative position");
+    hipLaunchKernelGGL(rope_kernel, dim3(T), dim3(256), 0, s, x, n_heads, d_head, pos_offset, max_seq,
+                       cos_t, sin_t);
+    VH_LAUNCHED();
+    return VLRF_HIP_OK;
+}
+
+int launch_embed(hipStream_t s, const float* table, const int* tok_dev, float* x, int D) {
+    hipLaunchKernelGGL(embed_kernel, dim3(1), dim3(256), 0, s, table, tok_dev, x, D);
+    VH_LAUNCHED();
+    return VLRF_HIP_OK;
+}
+
+int launch_argmax_step(hipStream_t s, const float* logits, int n, int* state, int* gen_ids,
+                       int gen_cap) {
+    VH_ARG(n >= 1, "argmax: empty logits");
+    hipLaunchKernelGGL(argmax_step_kernel, dim3(1), dim3(1024), 0, s, logits, n, state, gen_ids, gen_cap);
+    VH_LAUNCHED();
+    return VLRF_HIP_OK;
+}
+
+}  // namespace vlrf_hip

@@ -1,0 +1,216 @@
+// qlinear.hip - dequant-fused quantized linear y[M,N] = x[M,K] . W[N,K]^T.
+//
+// Reference contract: compute::linear -> ops::gemm(x, W, y, 1, 0, false, true)
+// (include/model/compute.hpp:58-68, ops.hpp:170-310) on weights decoded from
+// GGUF Q8_0/Q4_0 blocks (tools/converter/convert_gguf.py:233-263).
+//
+// Design (gfx950, wave64): a wave owns RPW output rows and walks K in tiles
+// of 1024 that the whole workgroup stages in LDS (optionally RMS-normalised on
+// the way in).  Within a tile, lane l reads EPL consecutive weights per
+// sub-chunk at offset 64*EPL*j + EPL*l, so each weight load instruction of a
+// wave covers one contiguous 256/512 B run of the row (coalesced), and the
+// matching activation reads from LDS are contiguous across lanes
+// (conflict-free).  Weights are dequantized in registers: codes -> f32, a
+// per-lane partial dot over the lane's EPL elements, then one FMA with the
+// block scale.  The K reduction across lanes is a DPP/shuffle wave sum.
+#include "../internal.hpp"
+
+namespace vlrf_hip {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = 4;
+constexpr int kTile = 1024;
+constexpr int kRPW = 2;
+
+template <int WT> struct WT_;
+template <> struct WT_<VLRF_DT_Q8_0> { static constexpr int EPL = 4; };
+template <> struct WT_<VLRF_DT_Q4_0> { static constexpr int EPL = 8; };
+template <> struct WT_<VLRF_DT_F32>  { static constexpr int EPL = 4; };
+
+// Partial dot of the lane's EPL weights of row n starting at column c with the
+// staged activations xr (EPL floats per activation row, stride kTile).
+template <int WT, int MT>
+__device__ __forceinline__ void lane_dot(const uint8_t* __restrict__ q, const __half* __restrict__ d,
+                                         const float* __restrict__ f, int n, int K, int c,
+                                         const float* __restrict__ xr, int M, float (&acc)[MT]) {
+    constexpr int EPL = WT_<WT>::EPL;
+    float w[EPL];
+    float scale = 1.f;
+    if constexpr (WT == VLRF_DT_Q8_0) {
+        const uint32_t u = *reinterpret_cast<const uint32_t*>(q + (size_t)n * K + c);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w[i] = (float)(int8_t)(u >> (8 * i));
+        scale = __half2float(d[(size_t)n * (K / 32) + c / 32]);
+    } else if constexpr (WT == VLRF_DT_Q4_0) {
+        const uint32_t u = *reinterpret_cast<const uint32_t*>(q + (size_t)n * (K / 2) + c / 2);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) w[i] = (float)((int)((u >> (4 * i)) & 0xFu) - 8);
+        scale = __half2float(d[(size_t)n * (K / 32) + c / 32]);
+    } else {
+        const float4 v = *reinterpret_cast<const float4*>(f + (size_t)n * K + c);
+        w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+    }
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        if (m < M) {
+            const float* xm = xr + m * kTile;
+            float p = 0.f;
+#pragma unroll
+            for (int i = 0; i < EPL; i += 4) {
+                const float4 xv = *reinterpret_cast<const float4*>(xm + i);
+                p += w[i] * xv.x + w[i + 1] * xv.y + w[i + 2] * xv.z + w[i + 3] * xv.w;
+            }
+            if constexpr (WT == VLRF_DT_F32) acc[m] += p;
+            else acc[m] += scale * p;
+        }
+    }
+}
+
+template <int WT, int MT, bool SWIGLU>
+__global__ __launch_bounds__(kThreads) void qlinear_kernel(
+    const uint8_t* __restrict__ qa, const __half* __restrict__ da, const float* __restrict__ fa,
+    const uint8_t* __restrict__ qb, const __half* __restrict__ db, const float* __restrict__ fb,
+    int N, int K, int M, const float* __restrict__ x, const float* __restrict__ norm_w, float eps,
+    const float* residual, float* y) {
+    constexpr int EPL = WT_<WT>::EPL;
+    constexpr int SUB = kTile / (64 * EPL);
+    __shared__ __align__(16) float xs[MT * kTile];
+    __shared__ float inv_rms[MT];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int row0 = (blockIdx.x * kWaves + wave) * kRPW;
+
+    if (norm_w) {
+        // ops::rms_norm (ops.hpp:488-498): inv = 1 / sqrt(sum(x^2)/D + eps).
+        for (int m = wave; m < M; m += kWaves) {
+            float ss = 0.f;
+            for (int k = lane; k < K; k += 64) {
+                const float v = x[(size_t)m * K + k];
+                ss += v * v;
+            }
+            ss = wave_sum(ss);
+            if (lane == 0) inv_rms[m] = 1.f / sqrtf(ss / (float)K + eps);
+        }
+        __syncthreads();
+    }
+
+    float acc[kRPW][MT], accb[kRPW][MT];
+#pragma unroll
+    for (int r = 0; r < kRPW; ++r)
+#pragma unroll
+        for (int m = 0; m < MT; ++m) { acc[r][m] = 0.f; accb[r][m] = 0.f; }
+
+    for (int k0 = 0; k0 < K; k0 += kTile) {
+        const int kt = min(kTile, K - k0);
+        for (int i = tid; i < MT * kTile; i += kThreads) {
+            const int m = i / kTile, kk = i - m * kTile;
+            float v = 0.f;
+            if (m < M && kk < kt) {
+                v = x[(size_t)m * K + k0 + kk];
+                if (norm_w) v = v * inv_rms[m] * norm_w[k0 + kk];
+            }
+            xs[i] = v;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < SUB; ++j) {
+            const int e = j * 64 * EPL + lane * EPL;
+            if (e < kt) {
+#pragma unroll
+                for (int r = 0; r < kRPW; ++r) {
+                    const int n = row0 + r;
+                    if (n < N) {
+                        lane_dot<WT, MT>(qa, da, fa, n, K, k0 + e, xs + e, M, acc[r]);
+                        if constexpr (SWIGLU) lane_dot<WT, MT>(qb, db, fb, n, K, k0 + e, xs + e, M, accb[r]);
+                    }
+                }
+            }
+        }
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int r = 0; r < kRPW; ++r) {
+        const int n = row0 + r;
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            if (m < M) {
+                const float s = wave_sum(acc[r][m]);
+                float out = s;
+                if constexpr (SWIGLU) {
+                    // silu_inplace(g) then multiply_inplace(h, g) (ops.hpp:409-441)
+                    const float u = wave_sum(accb[r][m]);
+                    const float g = s / (1.f + expf(-s));
+                    out = u * g;
+                }
+                if (lane == 0 && n < N) {
+                    if (residual) out = out + residual[(size_t)m * N + n];
+                    y[(size_t)m * N + n] = out;
+                }
+            }
+        }
+    }
+}
+
+template <int WT, bool SWIGLU>
+int dispatch_m(hipStream_t s, const DevWeight& a, const DevWeight* b, const float* x, float* y,
+               int M, const float* norm_w, float eps, const float* residual) {
+    const int rows_per_block = kWaves * kRPW;
+    dim3 grid((a.N + rows_per_block - 1) / rows_per_block), block(kThreads);
+    const uint8_t* qb = b ? b->q : nullptr;
+    const __half* db = b ? b->d : nullptr;
+    const float* fb = b ? b->f : nullptr;
+#define VH_QL(MT)                                                                           \
+    hipLaunchKernelGGL((qlinear_kernel<WT, MT, SWIGLU>), grid, block, 0, s, a.q, a.d, a.f,  \
+                       qb, db, fb, a.N, a.K, M, x, norm_w, eps, residual, y)
+    if (M == 1) VH_QL(1);
+    else if (M <= 4) VH_QL(4);
+    else VH_QL(16);
+#undef VH_QL
+    VH_LAUNCHED();
+    return VLRF_HIP_OK;
+}
+
+int check_weight(const DevWeight& w) {
+    VH_ARG(w.N > 0 && w.K > 0, "qlinear: empty weight");
+    VH_ARG(w.dtype == VLRF_DT_F32 || w.dtype == VLRF_DT_Q8_0 || w.dtype == VLRF_DT_Q4_0,
+           "qlinear: unsupported weight dtype %d", w.dtype);
+    VH_ARG(w.K % 32 == 0, "qlinear: K=%d must be a multiple of 32", w.K);
+    if (w.dtype == VLRF_DT_F32) VH_ARG(w.f != nullptr, "qlinear: f32 weight not allocated");
+    else VH_ARG(w.q != nullptr && w.d != nullptr, "qlinear: quantized weight not allocated");
+    return VLRF_HIP_OK;
+}
+
+}  // namespace
+
+int launch_qlinear(hipStream_t s, const DevWeight& w, const float* x, float* y, int M,
+                   const float* norm_w, float eps, const float* residual) {
+    int rc = check_weight(w);
+    if (rc) return rc;
+    VH_ARG(M >= 1 && M <= 16, "qlinear: M=%d outside [1,16]", M);
+    VH_ARG(x && y, "qlinear: null activation pointer");
+    switch (w.dtype) {
+        case VLRF_DT_Q8_0: return dispatch_m<VLRF_DT_Q8_0, false>(s, w, nullptr, x, y, M, norm_w, eps, residual);
+        case VLRF_DT_Q4_0: return dispatch_m<VLRF_DT_Q4_0, false>(s, w, nullptr, x, y, M, norm_w, eps, residual);
+        default:           return dispatch_m<VLRF_DT_F32, false>(s, w, nullptr, x, y, M, norm_w, eps, residual);
+    }
+}
+
+int launch_qlinear_swiglu(hipStream_t s, const DevWeight& wg, const DevWeight& wu,
+                          const float* x, float* h, int M, const float* norm_w, float eps) {
+    int rc = check_weight(wg);
+    if (rc) return rc;
+    rc = check_weight(wu);
+    if (rc) return rc;
+    VH_ARG(wg.N == wu.N && wg.K == wu.K && wg.dtype == wu.dtype,
+           "swiglu: gate/up shapes or dtypes differ");
+    VH_ARG(M >= 1 && M <= 16, "swiglu: M=%d outside [1,16]", M);
+    switch (wg.dtype) {
+        case VLRF_DT_Q8_0: return dispatch_m<VLRF_DT_Q8_0, true>(s, wg, &wu, x, h, M, norm_w, eps, nullptr);
+        case VLRF_DT_Q4_0: return dispatch_m<VLRF_DT_Q4_0, true>(s, wg, &wu, x, h, M, norm_w, eps, nullptr);
+        default:           return dispatch_m<VLRF_DT_F32, true>(s, wg, &wu, x, h, M, norm_w, eps, nullptr);
+    }
+}
+
+}  // namespace vlrf_hip

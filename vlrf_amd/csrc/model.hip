@@ -1,0 +1,435 @@
+// model.hip - device-resident decode step of a Llama-style decoder.
+//
+// Reference: TransformerModel::forward (transformer.hpp:335-424) for one token
+// with the KV cache, TransformerBlock::forward_v2 pre-norm order
+// (transformer_block.hpp:141-159), AttentionBlock::forward (attention.hpp:89-186),
+// FeedForward::forward SwiGLU (feedforward.hpp:50-77), greedy argmax
+// (transformer.hpp:43-47).
+//
+// Per layer the step queues five kernels:
+//   qlinear(Wqkv, rmsnorm(x; ln1))        Q,K,V in one pass over the fused rows
+//   rope_append                           RoPE on q,k; Q8_0 quantize k,v at pos
+//   attn_decode (+ combine)               split-K over the quantized cache
+//   qlinear(Wo, att) + x                  residual in the epilogue
+//   swiglu(Wg, Wu, rmsnorm(x; ln2))       silu(g) * u in the epilogue
+//   qlinear(Wd, h) + x
+// then rmsnorm + LM head and argmax, which writes the next token id and
+// advances the device-side position.  The token and position live in device
+// memory, so the whole step is captured once as a HIP graph and replayed with
+// no host round trip between steps.
+#include "internal.hpp"
+#include "runtime.hpp"
+
+#include <cmath>
+#include <cstring>
+#include <new>
+#include <string>
+#include <vector>
+
+using namespace vlrf_hip;
+
+namespace {
+
+enum : int { kLn1 = 0, kLn2, kQ, kK, kV, kO, kGate, kUp, kDown, kPerLayer };
+
+struct Layer {
+    float* ln1 = nullptr;
+    float* ln2 = nullptr;
+    DevWeight wqkv, wo, wg, wu, wd;
+    KVLayer kv;
+    unsigned set = 0;
+};
+
+}  // namespace
+
+struct vlrf_hip_model {
+    Ctx* ctx = nullptr;
+    vlrf_hip_model_config cfg{};
+    int D = 0, F = 0, H = 0, G = 0, dh = 0, dkv = 0, L = 0, V = 0, S = 0;
+    float* embed = nullptr;
+    float* ln_final = nullptr;
+    DevWeight lm_head;
+    bool embed_set = false, ln_final_set = false, lm_head_set = false;
+    std::vector<Layer> layers;
+    const float* cos_t = nullptr;
+    const float* sin_t = nullptr;
+    float *x = nullptr, *qkv = nullptr, *att = nullptr, *h = nullptr, *logits = nullptr, *part = nullptr;
+    int* state = nullptr;      // [0] token, [1] position, [2] generated count
+    int* gen_ids = nullptr;    // [S]
+    int* prompt = nullptr;     // [S] staged prompt ids
+    int* pinned = nullptr;     // host pinned [4]
+    int n_splits = 0;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    int pos = 0;               // host mirror of state[1]
+
+    bool ready() const {
+        if (!embed_set || !ln_final_set || !lm_head_set) return false;
+        for (auto& l : layers)
+            if (l.set != (1u << kPerLayer) - 1) return false;
+        return true;
+    }
+};
+
+namespace {
+
+int enqueue_step(vlrf_hip_model* m, hipStream_t s) {
+    int rc = launch_embed(s, m->embed, m->state, m->x, m->D);
+    const float eps = m->cfg.norm_eps;
+    const float scale = 1.f / std::sqrt((float)m->dh);   // attention.hpp:373-374
+    for (int l = 0; l < m->L && !rc; ++l) {
+        Layer& Ly = m->layers[l];
+        float* q = m->qkv;
+        float* k = m->qkv + m->D;
+        float* v = m->qkv + m->D + m->dkv;
+        if (!rc) rc = launch_qlinear(s, Ly.wqkv, m->x, m->qkv, 1, Ly.ln1, eps, nullptr);
+        if (!rc) rc = launch_rope_append(s, Ly.kv, q, k, v, m->H, m->G, m->dh, m->S, m->state + 1,
+                                         m->cos_t, m->sin_t);
+        if (!rc) rc = launch_attn_decode(s, q, Ly.kv.k, Ly.kv.v, Ly.kv.ks, Ly.kv.vs, nullptr, nullptr,
+                                         (long)m->S * m->dh, m->H, m->G, m->dh, 1, m->state + 1,
+                                         m->n_splits, scale, m->part, m->att);
+        if (!rc) rc = launch_qlinear(s, Ly.wo, m->att, m->x, 1, nullptr, 0.f, m->x);
+        if (!rc) rc = launch_qlinear_swiglu(s, Ly.wg, Ly.wu, m->x, m->h, 1, Ly.ln2, eps);
+        if (!rc) rc = launch_qlinear(s, Ly.wd, m->h, m->x, 1, nullptr, 0.f, m->x);
+    }
+    if (!rc) rc = launch_qlinear(s, m->lm_head, m->x, m->logits, 1, m->ln_final, eps, nullptr);
+    if (!rc) rc = launch_argmax_step(s, m->logits, m->V, m->state, m->gen_ids, m->S);
+    return rc;
+}
+
+int ensure_graph(vlrf_hip_model* m) {
+    if (m->exec) return VLRF_HIP_OK;
+    hipStream_t s = m->ctx->stream;
+    VH_CHECK(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    int rc = enqueue_step(m, s);
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(s, &g);
+    if (rc) {
+        if (g) (void)hipGraphDestroy(g);
+        return rc;
+    }
+    if (e != hipSuccess) {
+        set_error("graph capture failed: %s", hipGetErrorString(e));
+        return VLRF_HIP_ERR_RUNTIME;
+    }
+    m->graph = g;
+    VH_CHECK(hipGraphInstantiate(&m->exec, g, nullptr, nullptr, 0));
+    return VLRF_HIP_OK;
+}
+
+int check_ready(vlrf_hip_model* m) {
+    VH_ARG(m != nullptr, "model: null handle");
+    VH_CHECK(hipSetDevice(m->ctx->device));
+    VH_ARG(m->ready(), "model: not every weight has been set");
+    return ensure_graph(m);
+}
+
+int parse_layer(const std::string& name, int* layer, std::string* rest) {
+    if (name.compare(0, 7, "layers.") != 0) return -1;
+    size_t dot = name.find('.', 7);
+    if (dot == std::string::npos) return -1;
+    *layer = std::atoi(name.substr(7, dot - 7).c_str());
+    *rest = name.substr(dot + 1);
+    return 0;
+}
+
+int upload_f32(hipStream_t s, float* dst, const void* host, size_t n) {
+    VH_CHECK(hipMemcpyAsync(dst, host, n * sizeof(float), hipMemcpyHostToDevice, s));
+    VH_CHECK(hipStreamSynchronize(s));
+    return VLRF_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int vlrf_hip_model_create(vlrf_hip_ctx_t ctx, const vlrf_hip_model_config* cfg, vlrf_hip_model_t* out) {
+    VH_ARG(ctx && cfg && out, "model_create: null argument");
+    *out = nullptr;
+    VH_CHECK(hipSetDevice(ctx->device));
+    const auto& c = *cfg;
+    // ModelConfig::check (config.hpp:127-140) plus what the kernels assume.
+    VH_ARG(c.d_model > 0 && c.n_heads > 0 && c.d_model % c.n_heads == 0, "model: d_model %% n_heads != 0");
+    VH_ARG(c.n_kv_heads > 0 && c.n_heads % c.n_kv_heads == 0, "model: n_heads %% n_kv_heads != 0");
+    VH_ARG(c.n_layers > 0 && c.max_seq_len > 0 && c.vocab_size > 0 && c.d_ff > 0, "model: bad sizes");
+    const int dh = c.d_model / c.n_heads;
+    VH_ARG(dh == 64 || dh == 128, "model: d_head %d not in {64,128}", dh);
+    const int rep = c.n_heads / c.n_kv_heads;
+    VH_ARG(rep == 1 || rep == 2 || rep == 4 || rep == 8, "model: GQA group %d not in {1,2,4,8}", rep);
+    VH_ARG(c.n_kv_heads * dh <= 1024, "model: kv row %d exceeds 1024", c.n_kv_heads * dh);
+    VH_ARG(c.d_model % 32 == 0 && c.d_ff % 32 == 0, "model: d_model and d_ff must be multiples of 32");
+    VH_ARG(c.weight_dtype == VLRF_DT_Q8_0 || c.weight_dtype == VLRF_DT_Q4_0 || c.weight_dtype == VLRF_DT_F32,
+           "model: unsupported weight dtype %d", c.weight_dtype);
+
+    auto* m = new (std::nothrow) vlrf_hip_model();
+    if (!m) return VLRF_HIP_ERR_NOMEM;
+    m->ctx = ctx;
+    m->cfg = c;
+    m->D = c.d_model; m->F = c.d_ff; m->H = c.n_heads; m->G = c.n_kv_heads; m->dh = dh;
+    m->dkv = c.n_kv_heads * dh; m->L = c.n_layers; m->V = c.vocab_size; m->S = c.max_seq_len;
+    m->n_splits = attn_decode_splits(m->S);
+    m->layers.resize(m->L);
+
+    int rc = VLRF_HIP_OK;
+    auto dalloc = [&](void** p, size_t bytes) {
+        if (rc) return;
+        if (hipMalloc(p, bytes) != hipSuccess) {
+            set_error("model_create: hipMalloc(%zu) failed", bytes);
+            rc = VLRF_HIP_ERR_NOMEM;
+        }
+    };
+    dalloc((void**)&m->embed, (size_t)m->V * m->D * 4);
+    dalloc((void**)&m->ln_final, (size_t)m->D * 4);
+    dalloc((void**)&m->x, (size_t)m->D * 4);
+    dalloc((void**)&m->qkv, (size_t)(m->D + 2 * m->dkv) * 4);
+    dalloc((void**)&m->att, (size_t)m->D * 4);
+    dalloc((void**)&m->h, (size_t)m->F * 4);
+    dalloc((void**)&m->logits, (size_t)m->V * 4);
+    dalloc((void**)&m->part, (size_t)m->H * m->n_splits * (dh + 2) * 4);
+    dalloc((void**)&m->state, 4 * sizeof(int));
+    dalloc((void**)&m->gen_ids, (size_t)m->S * sizeof(int));
+    dalloc((void**)&m->prompt, (size_t)m->S * sizeof(int));
+    const size_t kvdata = (size_t)m->G * m->S * dh;
+    for (auto& Ly : m->layers) {
+        dalloc((void**)&Ly.ln1, (size_t)m->D * 4);
+        dalloc((void**)&Ly.ln2, (size_t)m->D * 4);
+        dalloc((void**)&Ly.kv.k, kvdata);
+        dalloc((void**)&Ly.kv.v, kvdata);
+        dalloc((void**)&Ly.kv.ks, (size_t)m->S * 4);
+        dalloc((void**)&Ly.kv.vs, (size_t)m->S * 4);
+        if (!rc) rc = weight_alloc(Ly.wqkv, c.weight_dtype, m->D + 2 * m->dkv, m->D);
+        if (!rc) rc = weight_alloc(Ly.wo, c.weight_dtype, m->D, m->D);
+        if (!rc) rc = weight_alloc(Ly.wg, c.weight_dtype, m->F, m->D);
+        if (!rc) rc = weight_alloc(Ly.wu, c.weight_dtype, m->F, m->D);
+        if (!rc) rc = weight_alloc(Ly.wd, c.weight_dtype, m->D, m->F);
+    }
+    if (!rc && hipHostMalloc((void**)&m->pinned, 4 * sizeof(int), hipHostMallocDefault) != hipSuccess) {
+        set_error("model_create: hipHostMalloc failed");
+        rc = VLRF_HIP_ERR_NOMEM;
+    }
+    if (!rc) rc = ctx->rope_tables(m->S, dh, c.rope_theta, &m->cos_t, &m->sin_t);
+    if (!rc) rc = vlrf_hip_model_reset(m);
+    if (rc) {
+        vlrf_hip_model_destroy(m);
+        return rc;
+    }
+    *out = m;
+    return VLRF_HIP_OK;
+}
+
+void vlrf_hip_model_destroy(vlrf_hip_model_t m) {
+    if (!m) return;
+    (void)hipSetDevice(m->ctx->device);
+    (void)hipStreamSynchronize(m->ctx->stream);
+    if (m->exec) (void)hipGraphExecDestroy(m->exec);
+    if (m->graph) (void)hipGraphDestroy(m->graph);
+    for (auto& Ly : m->layers) {
+        for (void* p : {(void*)Ly.ln1, (void*)Ly.ln2, (void*)Ly.kv.k, (void*)Ly.kv.v, (void*)Ly.kv.ks,
+                        (void*)Ly.kv.vs})
+            if (p) (void)hipFree(p);
+        weight_release(Ly.wqkv);
+        weight_release(Ly.wo);
+        weight_release(Ly.wg);
+        weight_release(Ly.wu);
+        weight_release(Ly.wd);
+    }
+    weight_release(m->lm_head);
+    for (void* p : {(void*)m->embed, (void*)m->ln_final, (void*)m->x, (void*)m->qkv, (void*)m->att,
+                    (void*)m->h, (void*)m->logits, (void*)m->part, (void*)m->state,
+                    (void*)m->gen_ids, (void*)m->prompt})
+        if (p) (void)hipFree(p);
+    if (m->pinned) (void)hipHostFree(m->pinned);
+    delete m;
+}
+
+int vlrf_hip_model_set_weight(vlrf_hip_model_t m, const char* name, const void* host, int dtype,
+                              int rows, int cols) {
+    VH_ARG(m && name && host, "set_weight: null argument");
+    VH_CHECK(hipSetDevice(m->ctx->device));
+    hipStream_t s = m->ctx->stream;
+    const std::string n(name);
+    auto need = [&](int dt, int r, int c) -> int {
+        VH_ARG(dtype == dt && rows == r && cols == c,
+               "set_weight %s: expected dtype %d [%d,%d], got dtype %d [%d,%d]", name, dt, r, c, dtype,
+               rows, cols);
+        return VLRF_HIP_OK;
+    };
+    int rc;
+    if (n == "embed.weight") {
+        if ((rc = need(VLRF_DT_F32, m->V, m->D))) return rc;
+        if ((rc = upload_f32(s, m->embed, host, (size_t)m->V * m->D))) return rc;
+        m->embed_set = true;
+        return VLRF_HIP_OK;
+    }
+    if (n == "ln_final.weight") {
+        if ((rc = need(VLRF_DT_F32, 1, m->D))) return rc;
+        if ((rc = upload_f32(s, m->ln_final, host, m->D))) return rc;
+        m->ln_final_set = true;
+        return VLRF_HIP_OK;
+    }
+    if (n == "lm_head.weight") {
+        VH_ARG(rows == m->V && cols == m->D, "set_weight lm_head: shape [%d,%d] != [%d,%d]", rows, cols,
+               m->V, m->D);
+        if (m->lm_head.dtype != dtype || !(m->lm_head.q || m->lm_head.f)) {
+            VH_CHECK(hipStreamSynchronize(s));
+            // The captured step graph holds the old pointers: drop it.
+            if (m->exec) (void)hipGraphExecDestroy(m->exec);
+            if (m->graph) (void)hipGraphDestroy(m->graph);
+            m->exec = nullptr;
+            m->graph = nullptr;
+            weight_release(m->lm_head);
+            if ((rc = weight_alloc(m->lm_head, dtype, m->V, m->D))) return rc;
+        }
+        if ((rc = weight_upload_rows(s, m->lm_head, host, 0, m->V))) return rc;
+        m->lm_head_set = true;
+        return VLRF_HIP_OK;
+    }
+    int l = -1;
+    std::string rest;
+    VH_ARG(parse_layer(n, &l, &rest) == 0 && l >= 0 && l < m->L, "set_weight: unknown tensor %s", name);
+    Layer& Ly = m->layers[l];
+    const int wdt = m->cfg.weight_dtype;
+    if (rest == "ln1.weight" || rest == "ln2.weight") {
+        if ((rc = need(VLRF_DT_F32, 1, m->D))) return rc;
+        const bool one = rest == "ln1.weight";
+        if ((rc = upload_f32(s, one ? Ly.ln1 : Ly.ln2, host, m->D))) return rc;
+        Ly.set |= 1u << (one ? kLn1 : kLn2);
+        return VLRF_HIP_OK;
+    }
+    struct Slot { const char* key; DevWeight* w; int row0, rows, cols, bit; };
+    const Slot slots[] = {
+        {"attn.q_proj.weight", &Ly.wqkv, 0, m->D, m->D, kQ},
+        {"attn.k_proj.weight", &Ly.wqkv, m->D, m->dkv, m->D, kK},
+        {"attn.v_proj.weight", &Ly.wqkv, m->D + m->dkv, m->dkv, m->D, kV},
+        {"attn.o_proj.weight", &Ly.wo, 0, m->D, m->D, kO},
+        {"ffn.gate.weight", &Ly.wg, 0, m->F, m->D, kGate},
+        {"ffn.fc1.weight", &Ly.wu, 0, m->F, m->D, kUp},
+        {"ffn.fc2.weight", &Ly.wd, 0, m->D, m->F, kDown},
+    };
+    for (const auto& sl : slots) {
+        if (rest != sl.key) continue;
+        if ((rc = need(wdt, sl.rows, sl.cols))) return rc;
+        if ((rc = weight_upload_rows(s, *sl.w, host, sl.row0, sl.rows))) return rc;
+        Ly.set |= 1u << sl.bit;
+        return VLRF_HIP_OK;
+    }
+    set_error("set_weight: unknown tensor %s", name);
+    return VLRF_HIP_ERR_ARG;
+}
+
+int vlrf_hip_model_reset(vlrf_hip_model_t m) {
+    VH_ARG(m != nullptr, "model_reset: null handle");
+    VH_CHECK(hipSetDevice(m->ctx->device));
+    hipStream_t s = m->ctx->stream;
+    const size_t kvdata = (size_t)m->G * m->S * m->dh;
+    for (auto& Ly : m->layers) {
+        VH_CHECK(hipMemsetAsync(Ly.kv.k, 0, kvdata, s));
+        VH_CHECK(hipMemsetAsync(Ly.kv.v, 0, kvdata, s));
+        VH_CHECK(hipMemsetAsync(Ly.kv.ks, 0, (size_t)m->S * 4, s));
+        VH_CHECK(hipMemsetAsync(Ly.kv.vs, 0, (size_t)m->S * 4, s));
+    }
+    VH_CHECK(hipMemsetAsync(m->state, 0, 4 * sizeof(int), s));
+    VH_CHECK(hipStreamSynchronize(s));
+    m->pos = 0;
+    return VLRF_HIP_OK;
+}
+
+int vlrf_hip_model_used(vlrf_hip_model_t m) { return m ? m->pos : -1; }
+
+int vlrf_hip_model_step(vlrf_hip_model_t m, int32_t token, int32_t* next, float* logits) {
+    int rc = check_ready(m);
+    if (rc) return rc;
+    VH_ARG(token >= 0 && token < m->V, "model_step: token %d outside [0,%d)", token, m->V);
+    if (m->pos + 1 > m->S) {
+        set_error("KVCache::append: exceeds max_seq_len (%d + 1 > %d)", m->pos, m->S);
+        return VLRF_HIP_ERR_OVERFLOW;
+    }
+    hipStream_t s = m->ctx->stream;
+    m->pinned[0] = token;
+    VH_CHECK(hipMemcpyAsync(m->state, m->pinned, sizeof(int), hipMemcpyHostToDevice, s));
+    VH_CHECK(hipGraphLaunch(m->exec, s));
+    VH_CHECK(hipMemcpyAsync(m->pinned, m->state, sizeof(int), hipMemcpyDeviceToHost, s));
+    if (logits) VH_CHECK(hipMemcpyAsync(logits, m->logits, (size_t)m->V * 4, hipMemcpyDeviceToHost, s));
+    VH_CHECK(hipStreamSynchronize(s));
+    m->pos += 1;
+    if (next) *next = m->pinned[0];
+    return VLRF_HIP_OK;
+}
+
+int vlrf_hip_model_prefill(vlrf_hip_model_t m, const int32_t* ids, int n, int32_t* next) {
+    int rc = check_ready(m);
+    if (rc) return rc;
+    VH_ARG(ids != nullptr && n >= 1, "model_prefill: empty prompt");
+    for (int i = 0; i < n; ++i)
+        VH_ARG(ids[i] >= 0 && ids[i] < m->V, "model_prefill: token %d outside [0,%d)", ids[i], m->V);
+    if (m->pos + n > m->S) {
+        set_error("KVCache::append: exceeds max_seq_len (%d + %d > %d)", m->pos, n, m->S);
+        return VLRF_HIP_ERR_OVERFLOW;
+    }
+    hipStream_t s = m->ctx->stream;
+    VH_CHECK(hipMemcpyAsync(m->prompt, ids, (size_t)n * sizeof(int), hipMemcpyHostToDevice, s));
+    VH_CHECK(hipStreamSynchronize(s));
+    for (int i = 0; i < n; ++i) {
+        VH_CHECK(hipMemcpyAsync(m->state, m->prompt + i, sizeof(int), hipMemcpyDeviceToDevice, s));
+        VH_CHECK(hipGraphLaunch(m->exec, s));
+    }
+    VH_CHECK(hipMemcpyAsync(m->pinned, m->state, sizeof(int), hipMemcpyDeviceToHost, s));
+    VH_CHECK(hipStreamSynchronize(s));
+    m->pos += n;
+    if (next) *next = m->pinned[0];
+    return VLRF_HIP_OK;
+}
+
+int vlrf_hip_model_generate_async(vlrf_hip_model_t m, int32_t first, int n_steps) {
+    int rc = check_ready(m);
+    if (rc) return rc;
+    VH_ARG(first >= 0 && first < m->V, "model_generate: token %d outside [0,%d)", first, m->V);
+    VH_ARG(n_steps >= 1, "model_generate: n_steps %d < 1", n_steps);
+    if (m->pos + n_steps > m->S) {
+        set_error("KVCache::append: exceeds max_seq_len (%d + %d > %d)", m->pos, n_steps, m->S);
+        return VLRF_HIP_ERR_OVERFLOW;
+    }
+    hipStream_t s = m->ctx->stream;
+    VH_CHECK(hipStreamSynchronize(s));   // the pinned staging word is free again
+    m->pinned[0] = first;
+    m->pinned[1] = m->pos;
+    m->pinned[2] = 0;
+    VH_CHECK(hipMemcpyAsync(m->state, m->pinned, 3 * sizeof(int), hipMemcpyHostToDevice, s));
+    for (int i = 0; i < n_steps; ++i) VH_CHECK(hipGraphLaunch(m->exec, s));
+    m->pos += n_steps;
+    return VLRF_HIP_OK;
+}
+
+int vlrf_hip_model_read_generated(vlrf_hip_model_t m, int32_t* out_ids, int n) {
+    VH_ARG(m && out_ids && n >= 0 && n <= m->S, "read_generated: bad arguments");
+    VH_CHECK(hipSetDevice(m->ctx->device));
+    hipStream_t s = m->ctx->stream;
+    VH_CHECK(hipMemcpyAsync(out_ids, m->gen_ids, (size_t)n * sizeof(int), hipMemcpyDeviceToHost, s));
+    VH_CHECK(hipStreamSynchronize(s));
+    return VLRF_HIP_OK;
+}
+
+int vlrf_hip_model_generate(vlrf_hip_model_t m, int32_t first, int n_steps, int32_t* out_ids) {
+    int rc = vlrf_hip_model_generate_async(m, first, n_steps);
+    if (rc) return rc;
+    return vlrf_hip_model_read_generated(m, out_ids, n_steps);
+}
+
+int vlrf_hip_model_step_bytes(vlrf_hip_model_t m, int ctx_len, double out[3]) {
+    VH_ARG(m && out && ctx_len >= 1, "step_bytes: bad arguments");
+    double w = 0.0;
+    for (auto& Ly : m->layers)
+        for (const DevWeight* dw : {&Ly.wqkv, &Ly.wo, &Ly.wg, &Ly.wu, &Ly.wd})
+            w += (double)weight_device_bytes(dw->dtype, dw->N, dw->K);
+    w += (double)weight_device_bytes(m->lm_head.dtype, m->V, m->D);
+    // K and V codes of the context plus one f32 scale per row, per layer.
+    const double kv = (double)m->L * (2.0 * ctx_len * m->dkv + 2.0 * ctx_len * 4.0);
+    // Norm weights (2 per layer + final) and the embedding row.
+    const double other = (2.0 * m->L + 1.0) * m->D * 4.0 + m->D * 4.0;
+    out[0] = w;
+    out[1] = kv;
+    out[2] = other;
+    return VLRF_HIP_OK;
+}
+
+}  // extern "C"
