@@ -80,6 +80,11 @@ struct KVLayer {
 // y[M,N] = (norm_w ? rmsnorm(x) : x) . W^T (+ residual)
 int launch_qlinear(hipStream_t s, const DevWeight& w, const float* x, float* y, int M,
                    const float* norm_w, float eps, const float* residual);
+// y = rmsnorm(table[*row]) . W^T (M = 1, Q8_0/Q4_0): the embedding gather fused
+// into the first projection; the raw row is also copied to x_copy.
+int launch_qlinear_gather(hipStream_t s, const DevWeight& w, const float* table, const int* row,
+                          float* x_copy, float* y, const float* norm_w, float eps);
+bool qlinear_gather_supported(const DevWeight& w);
 // h[M,N] = silu(rmsnorm(x).Wg^T) * (rmsnorm(x).Wu^T)
 int launch_qlinear_swiglu(hipStream_t s, const DevWeight& wg, const DevWeight& wu,
                           const float* x, float* h, int M, const float* norm_w, float eps);
@@ -100,6 +105,20 @@ int launch_rope_append(hipStream_t s, const KVLayer& L, float* q, const float* k
 int launch_kv_dequant(hipStream_t s, const KVLayer& L, int n_kv, int d_head, int max_seq,
                       int ctx_len, float* K_out, float* V_out);
 
+// Decode fusion of the attention kernel (model step): RoPE of q and of the
+// token's k at the device position, and the Q8_0 append of its K/V row.
+struct DecodeFuse {
+    const float* k_new = nullptr;   // [n_kv*d_head] unrotated k of the token
+    const float* v_new = nullptr;
+    const float* cos_t = nullptr;   // [max_seq][d_head/2]
+    const float* sin_t = nullptr;
+    int8_t* kq_w = nullptr;         // the layer's cache (same as kq/vq)
+    int8_t* vq_w = nullptr;
+    float* ks_w = nullptr;
+    float* vs_w = nullptr;
+    int n_kv = 0, max_seq = 0;
+};
+
 // Split-K decode attention. KV either Q8 cache (kq/vq + scales, head stride
 // max_seq*d) or f32 [n_kv][ctx][d] (kf/vf).  ctx from *ctx_dev (+1 when
 // ctx_plus_one) when non-null.  part must hold n_heads*n_splits*(d+2) floats.
@@ -107,7 +126,8 @@ int attn_decode_splits(int max_ctx);
 int launch_attn_decode(hipStream_t s, const float* q, const int8_t* kq, const int8_t* vq,
                        const float* ks, const float* vs, const float* kf, const float* vf,
                        long head_stride, int n_heads, int n_kv, int d_head, int ctx_len,
-                       const int* ctx_dev, int n_splits, float scale, float* part, float* out);
+                       const int* ctx_dev, int n_splits, float scale, float* part, float* out,
+                       const DecodeFuse* fuse = nullptr);
 int launch_attn_f32_tiled(hipStream_t s, const float* Q, const float* K, const float* V,
                           float* O, int n_h, int T, int ctx_len, int d_h, float scale,
                           int causal);

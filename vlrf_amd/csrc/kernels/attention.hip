@@ -23,30 +23,58 @@
 namespace vlrf_hip {
 namespace {
 
-constexpr int kChunk = 256;
+constexpr int kChunk = 64;        // tokens per split-K workgroup
+constexpr int kMaxSplits = 512;   // contexts up to 32768 tokens
 constexpr float kNegInf = -INFINITY;
 
-template <int D, int REP, bool Q8>
+__device__ __forceinline__ float block_max256(float v, float* red) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    v = wave_max(v);
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    v = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+    return v;
+}
+
+// RoPE of one pair (rope.hpp:90-96), each product rounded separately.
+__device__ __forceinline__ void rope2(float x0, float x1, float c, float s, float* y0, float* y1) {
+#pragma clang fp contract(off)
+    const float a = x0 * c, b = x1 * s, e = x1 * c, f = x0 * s;
+    *y0 = a - b;
+    *y1 = e + f;
+}
+
+template <int D, int REP, bool Q8, bool FUSED>
 __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
-    const float* __restrict__ q, const int8_t* __restrict__ kq, const int8_t* __restrict__ vq,
-    const float* __restrict__ ks, const float* __restrict__ vs, const float* __restrict__ kf,
-    const float* __restrict__ vf, long head_stride, int ctx_len, const int* __restrict__ ctx_dev,
-    int n_splits, float scale, float* __restrict__ part) {
+    const float* __restrict__ q, const int8_t* kq, const int8_t* vq, const float* ks, const float* vs,
+    const float* __restrict__ kf, const float* __restrict__ vf, long head_stride, int ctx_len,
+    const int* __restrict__ ctx_dev, int n_splits, float scale, float* __restrict__ part, DecodeFuse fz) {
+    constexpr int DQ = D / 4;                  // dims per wave in the score phase
+    constexpr int DL = D / 64;                 // 4-dim groups per lane in the P.V phase
     __shared__ __align__(16) float qs[REP][D];
-    __shared__ float sp[REP][kChunk];
+    __shared__ float sp4[4][REP][kChunk];      // score partials per dim quarter
     __shared__ float red[4][REP][D];
     __shared__ float mstat[REP], lstat[REP];
+    __shared__ float rmax[4];
+    __shared__ float krow[FUSED ? 1024 : 1], vrow[FUSED ? 1024 : 1];
+    __shared__ __align__(16) float newk[FUSED ? D : 1], newv[FUSED ? D : 1];
 
     const int split = blockIdx.x, g = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    constexpr int HALF = D / 2;
+    int pos = -1, ctx;
+    if constexpr (FUSED) {
+        pos = *ctx_dev;          // tokens before this one
+        ctx = pos + 1;
+    } else {
+        ctx = ctx_dev ? (*ctx_dev + ctx_len) : ctx_len;
+    }
     // Rows past the cache capacity are never read, even if the device-side
     // position were corrupt (the host checks capacity before queuing).
-    const int ctx = min(ctx_dev ? (*ctx_dev + ctx_len) : ctx_len, (int)(head_stride / D));
+    ctx = min(ctx, (int)(head_stride / D));
     const int c0 = split * kChunk;
     const size_t hb = (size_t)g * head_stride;
-
-    for (int i = tid; i < REP * D; i += 256) qs[i / D][i % D] = q[(size_t)(g * REP) * D + i];
-    __syncthreads();
 
     float* pout = part + (size_t)(g * REP) * n_splits * (D + 2) + (size_t)split * (D + 2);
     if (c0 >= ctx) {   // chunk past the context: empty partial
@@ -56,98 +84,197 @@ __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
         }
         return;
     }
+    const int nt = min(kChunk, ctx - c0);       // valid tokens of the chunk
+    const bool has_new = FUSED && pos >= c0 && pos < c0 + kChunk;
 
-    // ---- phase 1: scores --------------------------------------------------
-    const int j = c0 + tid;
-    float dot[REP];
+    // ---- loads first: this thread's K slice (token lane, dims of this wave) and
+    // its V words (tokens wave*16 + t4 + 4i, dims 4dg..) -------------------------
+    const int t4 = lane >> 4, dg = lane & 15;
+    float kv[DQ];
+    float vv[4][DL][4];
+    float ksc = 0.f, vsc[4];
+    {
+        const int jt = c0 + lane;
+        const bool ok = lane < nt && !(has_new && jt == pos);
 #pragma unroll
-    for (int h = 0; h < REP; ++h) dot[h] = 0.f;
-    if (j < ctx) {
-        float kscale = Q8 ? ks[j] : 1.f;
-#pragma unroll
-        for (int d0 = 0; d0 < D; d0 += 16) {
-            float kv[16];
+        for (int i = 0; i < DQ; i += 16) {
             if constexpr (Q8) {
-                const uint4 u = *reinterpret_cast<const uint4*>(kq + hb + (size_t)j * D + d0);
+                uint4 u = make_uint4(0, 0, 0, 0);
+                if (ok) u = *reinterpret_cast<const uint4*>(kq + hb + (size_t)jt * D + wave * DQ + i);
                 const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
-                for (int i = 0; i < 16; ++i)
-                    kv[i] = (float)(int8_t)(w[i >> 2] >> (8 * (i & 3))) * kscale;  // dequantize_row_q8_0
+                for (int k = 0; k < 16; ++k) kv[i + k] = (float)(int8_t)(w[k >> 2] >> (8 * (k & 3)));
             } else {
 #pragma unroll
-                for (int i = 0; i < 16; i += 4) {
-                    const float4 v = *reinterpret_cast<const float4*>(kf + hb + (size_t)j * D + d0 + i);
-                    kv[i] = v.x; kv[i + 1] = v.y; kv[i + 2] = v.z; kv[i + 3] = v.w;
+                for (int k = 0; k < 16; k += 4) {
+                    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+                    if (ok) v = *reinterpret_cast<const float4*>(kf + hb + (size_t)jt * D + wave * DQ + i + k);
+                    kv[i + k] = v.x; kv[i + k + 1] = v.y; kv[i + k + 2] = v.z; kv[i + k + 3] = v.w;
                 }
             }
+        }
+        if (Q8 && ok) ksc = ks[jt];
 #pragma unroll
-            for (int h = 0; h < REP; ++h) {
+        for (int it = 0; it < 4; ++it) {
+            const int t = wave * 16 + t4 + 4 * it;
+            const int jj = c0 + t;
+            const bool okv = t < nt && !(has_new && jj == pos);
+            vsc[it] = (Q8 && okv) ? vs[jj] : 0.f;
 #pragma unroll
-                for (int i = 0; i < 16; i += 4) {
-                    const float4 qv = *reinterpret_cast<const float4*>(&qs[h][d0 + i]);
-                    dot[h] += qv.x * kv[i] + qv.y * kv[i + 1] + qv.z * kv[i + 2] + qv.w * kv[i + 3];
+            for (int dl = 0; dl < DL; ++dl) {
+                if constexpr (Q8) {
+                    uint32_t u = 0;
+                    if (okv) u = *reinterpret_cast<const uint32_t*>(vq + hb + (size_t)jj * D + dl * 64 + dg * 4);
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) vv[it][dl][k] = (float)(int8_t)(u >> (8 * k));
+                } else {
+                    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+                    if (okv) v = *reinterpret_cast<const float4*>(vf + hb + (size_t)jj * D + dl * 64 + dg * 4);
+                    vv[it][dl][0] = v.x; vv[it][dl][1] = v.y; vv[it][dl][2] = v.z; vv[it][dl][3] = v.w;
                 }
             }
         }
     }
-#pragma unroll
-    for (int h = 0; h < REP; ++h) sp[h][tid] = (j < ctx) ? dot[h] * scale : kNegInf;
+
+    // ---- queries of the GQA group (RoPE at the device position when fused) -------
+    if (FUSED && pos < fz.max_seq) {   // rope.hpp:84: positions >= max_seq stay unrotated
+        const float* cs = fz.cos_t + (size_t)pos * HALF;
+        const float* sn = fz.sin_t + (size_t)pos * HALF;
+        for (int i = tid; i < REP * HALF; i += 256) {
+            const int h = i / HALF, j = i - h * HALF;
+            const float* qh = q + (size_t)(g * REP + h) * D;
+            rope2(qh[j], qh[j + HALF], cs[j], sn[j], &qs[h][j], &qs[h][j + HALF]);
+        }
+    } else {
+        for (int i = tid; i < REP * D; i += 256) qs[i / D][i % D] = q[(size_t)(g * REP) * D + i];
+    }
+
+    // ---- decode fusion: the current token's K/V row --------------------------------
+    // attention.hpp:109-128: RoPE on k, then KVCache::append quantizes the whole
+    // row (quantize_row_q8_0, kv_cache.hpp:102-117) before attention reads it.
+    // Every chunk holding `pos` quantizes the row itself and uses the dequantized
+    // values for that token; the workgroup of KV head g stores head g's codes,
+    // KV head 0 stores the row scales.
+    if constexpr (FUSED) {
+        if (has_new) {
+            const int row = fz.n_kv * D;
+            for (int i = tid; i < row; i += 256) { krow[i] = fz.k_new[i]; vrow[i] = fz.v_new[i]; }
+            __syncthreads();
+            if (pos < fz.max_seq) {
+                const float* cs = fz.cos_t + (size_t)pos * HALF;
+                const float* sn = fz.sin_t + (size_t)pos * HALF;
+                for (int i = tid; i < fz.n_kv * HALF; i += 256) {
+                    const int h = i / HALF, j = i - h * HALF;
+                    float* kh = krow + h * D;
+                    const float x0 = kh[j], x1 = kh[j + HALF];
+                    rope2(x0, x1, cs[j], sn[j], &kh[j], &kh[j + HALF]);
+                }
+            }
+            __syncthreads();
+            float ak = 0.f, av = 0.f;
+            for (int i = tid; i < row; i += 256) { ak = fmaxf(ak, fabsf(krow[i])); av = fmaxf(av, fabsf(vrow[i])); }
+            ak = block_max256(ak, rmax);
+            av = block_max256(av, rmax);
+            const float sk = ak != 0.f ? ak / 127.f : 0.f, sv = av != 0.f ? av / 127.f : 0.f;
+            const float ik = ak != 0.f ? 1.f / sk : 0.f, iv = av != 0.f ? 1.f / sv : 0.f;
+            for (int i = tid; i < D; i += 256) {
+                const int a = ak != 0.f ? min(127, max(-127, (int)roundf(krow[g * D + i] * ik))) : 0;
+                const int b = av != 0.f ? min(127, max(-127, (int)roundf(vrow[g * D + i] * iv))) : 0;
+                newk[i] = (float)a * sk;
+                newv[i] = (float)b * sv;
+                fz.kq_w[hb + (size_t)pos * D + i] = (int8_t)a;
+                fz.vq_w[hb + (size_t)pos * D + i] = (int8_t)b;
+            }
+            if (g == 0 && tid == 0) { fz.ks_w[pos] = sk; fz.vs_w[pos] = sv; }
+        }
+    }
     __syncthreads();
 
-    // ---- phase 2: chunk max and sum per head ---------------------------------
-    for (int h = wave; h < REP; h += 4) {
-        float v[4], mx = kNegInf;
+    // ---- phase 1: partial scores over this wave's quarter of d_head --------------
+    {
+        float kd[DQ];
+        if (FUSED && has_new && c0 + lane == pos) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) { v[i] = sp[h][lane + 64 * i]; mx = fmaxf(mx, v[i]); }
-        mx = wave_max(mx);   // finite: token c0 < ctx is in this chunk
-        float sum = 0.f;
+            for (int i = 0; i < DQ; ++i) kd[i] = newk[wave * DQ + i];
+        } else {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float p = expf(v[i] - mx);
-            sp[h][lane + 64 * i] = p;
-            sum += p;
+            for (int i = 0; i < DQ; ++i) kd[i] = Q8 ? kv[i] * ksc : kv[i];   // dequantize_row_q8_0
         }
-        sum = wave_sum(sum);
+#pragma unroll
+        for (int h = 0; h < REP; ++h) {
+            float dsum = 0.f;
+#pragma unroll
+            for (int i = 0; i < DQ; i += 4) {
+                const float4 qv = *reinterpret_cast<const float4*>(&qs[h][wave * DQ + i]);
+                dsum += qv.x * kd[i] + qv.y * kd[i + 1] + qv.z * kd[i + 2] + qv.w * kd[i + 3];
+            }
+            sp4[wave][h][lane] = dsum;
+        }
+    }
+    __syncthreads();
+
+    // ---- phase 2: per-head chunk max and sum (DPP/shuffle wave reductions) --------
+    for (int h = wave; h < REP; h += 4) {
+        float sc = kNegInf;
+        if (lane < nt) sc = ((sp4[0][h][lane] + sp4[1][h][lane]) + (sp4[2][h][lane] + sp4[3][h][lane])) * scale;
+        const float mx = wave_max(sc);   // finite: token c0 < ctx is in this chunk
+        const float p = expf(sc - mx);
+        sp4[0][h][lane] = p;
+        const float sum = wave_sum(p);
         if (lane == 0) { mstat[h] = mx; lstat[h] = sum; }
     }
     __syncthreads();
 
-    // ---- phase 3: P.V ----------------------------------------------------------
-    constexpr int DL = D / 64;
-    float acc[REP][DL];
+    // ---- phase 3: P.V (lane = 4 dims x token offset t4, wave = 16 tokens) ----------
+    float acc[REP][DL][4];
 #pragma unroll
     for (int h = 0; h < REP; ++h)
 #pragma unroll
-        for (int i = 0; i < DL; ++i) acc[h][i] = 0.f;
-    const int t0 = wave * 64, t1 = min(t0 + 64, ctx - c0);
-#pragma unroll 4
-    for (int t = t0; t < t1; ++t) {
-        const int jj = c0 + t;
-        float vv[DL];
-        if constexpr (Q8) {
-            const float sc = vs[jj];
+        for (int dl = 0; dl < DL; ++dl)
 #pragma unroll
-            for (int i = 0; i < DL; ++i) vv[i] = (float)vq[hb + (size_t)jj * D + lane + 64 * i] * sc;
-        } else {
+            for (int k = 0; k < 4; ++k) acc[h][dl][k] = 0.f;
 #pragma unroll
-            for (int i = 0; i < DL; ++i) vv[i] = vf[hb + (size_t)jj * D + lane + 64 * i];
-        }
+    for (int it = 0; it < 4; ++it) {
+        const int t = wave * 16 + t4 + 4 * it;
+        if (t < nt) {
+            float vd[DL][4];
+            if (FUSED && has_new && c0 + t == pos) {
 #pragma unroll
-        for (int h = 0; h < REP; ++h) {
-            const float p = sp[h][t];
+                for (int dl = 0; dl < DL; ++dl)
 #pragma unroll
-            for (int i = 0; i < DL; ++i) acc[h][i] += p * vv[i];
+                    for (int k = 0; k < 4; ++k) vd[dl][k] = newv[dl * 64 + dg * 4 + k];
+            } else {
+#pragma unroll
+                for (int dl = 0; dl < DL; ++dl)
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) vd[dl][k] = Q8 ? vv[it][dl][k] * vsc[it] : vv[it][dl][k];
+            }
+#pragma unroll
+            for (int h = 0; h < REP; ++h) {
+                const float p = sp4[0][h][t];
+#pragma unroll
+                for (int dl = 0; dl < DL; ++dl)
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) acc[h][dl][k] += p * vd[dl][k];
+            }
         }
     }
 #pragma unroll
     for (int h = 0; h < REP; ++h)
 #pragma unroll
-        for (int i = 0; i < DL; ++i) red[wave][h][lane + 64 * i] = acc[h][i];
+        for (int dl = 0; dl < DL; ++dl)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                float a = acc[h][dl][k];
+                a += __shfl_xor(a, 16);
+                a += __shfl_xor(a, 32);
+                if (t4 == 0) red[wave][h][dl * 64 + dg * 4 + k] = a;
+            }
     __syncthreads();
     for (int i = tid; i < REP * D; i += 256) {
         const int h = i / D, dd = i % D;
         pout[(size_t)h * n_splits * (D + 2) + dd] =
-            red[0][h][dd] + red[1][h][dd] + red[2][h][dd] + red[3][h][dd];
+            (red[0][h][dd] + red[1][h][dd]) + (red[2][h][dd] + red[3][h][dd]);
     }
     if (tid < REP) {
         pout[(size_t)tid * n_splits * (D + 2) + D] = mstat[tid];
@@ -155,20 +282,29 @@ __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
     }
 }
 
+// Log-sum-exp merge of the per-chunk partials of one query head.  The chunk
+// maxima and sums are staged in LDS; the accumulators are read with the loop
+// unrolled so that their loads are in flight together.
 template <int D>
 __global__ __launch_bounds__(D) void attn_combine_kernel(const float* __restrict__ part, int n_splits,
                                                          float* __restrict__ out) {
+    __shared__ float pm[kMaxSplits], pl[kMaxSplits];
     const int h = blockIdx.x, d = threadIdx.x;
     const float* p = part + (size_t)h * n_splits * (D + 2);
+    for (int s = d; s < n_splits; s += D) {
+        pm[s] = p[(size_t)s * (D + 2) + D];
+        pl[s] = p[(size_t)s * (D + 2) + D + 1];
+    }
+    __syncthreads();
     float M = kNegInf;
-    for (int s = 0; s < n_splits; ++s) M = fmaxf(M, p[(size_t)s * (D + 2) + D]);
+    for (int s = 0; s < n_splits; ++s) M = fmaxf(M, pm[s]);
     float L = 0.f, o = 0.f;
     if (M != kNegInf) {
+#pragma unroll 8
         for (int s = 0; s < n_splits; ++s) {
-            const float ms = p[(size_t)s * (D + 2) + D];
-            if (ms == kNegInf) continue;
-            const float w = expf(ms - M);
-            L += w * p[(size_t)s * (D + 2) + D + 1];
+            const float ms = pm[s];
+            const float w = ms == kNegInf ? 0.f : expf(ms - M);
+            L += w * pl[s];
             o += w * p[(size_t)s * (D + 2) + d];
         }
     }
@@ -263,33 +399,45 @@ int attn_decode_splits(int max_ctx) { return (max_ctx + kChunk - 1) / kChunk; }
 int launch_attn_decode(hipStream_t s, const float* q, const int8_t* kq, const int8_t* vq,
                        const float* ks, const float* vs, const float* kf, const float* vf,
                        long head_stride, int n_heads, int n_kv, int d_head, int ctx_len,
-                       const int* ctx_dev, int n_splits, float scale, float* part, float* out) {
+                       const int* ctx_dev, int n_splits, float scale, float* part, float* out,
+                       const DecodeFuse* fuse) {
     VH_ARG(n_kv > 0 && n_heads % n_kv == 0, "attn_decode: n_heads %d not a multiple of n_kv %d",
            n_heads, n_kv);
     const int rep = n_heads / n_kv;
     VH_ARG(d_head == 64 || d_head == 128, "attn_decode: d_head %d not in {64,128}", d_head);
     VH_ARG(rep == 1 || rep == 2 || rep == 4 || rep == 8, "attn_decode: GQA group %d not in {1,2,4,8}", rep);
-    VH_ARG(n_splits >= 1, "attn_decode: no splits");
+    VH_ARG(n_splits >= 1 && n_splits <= kMaxSplits, "attn_decode: %d splits outside [1,%d]", n_splits,
+           kMaxSplits);
     if (!ctx_dev)
         VH_ARG(ctx_len >= 1 && ctx_len <= n_splits * kChunk, "attn_decode: ctx_len %d outside [1,%d]",
                ctx_len, n_splits * kChunk);
     const bool q8 = kq != nullptr;
     VH_ARG(q8 ? (vq && ks && vs) : (kf && vf), "attn_decode: missing K/V operands");
+    DecodeFuse fz{};
+    if (fuse) {
+        VH_ARG(q8 && ctx_dev, "attn_decode: fusion needs the Q8 cache and a device position");
+        VH_ARG(fuse->n_kv == n_kv && n_kv * d_head <= 1024, "attn_decode: bad fusion row");
+        fz = *fuse;
+    }
     dim3 grid(n_splits, n_kv), block(256);
-#define VH_AD(D, R, Q)                                                                          \
-    hipLaunchKernelGGL((attn_decode_partial_kernel<D, R, Q>), grid, block, 0, s, q, kq, vq, ks,  \
-                       vs, kf, vf, head_stride, ctx_len, ctx_dev, n_splits, scale, part)
-#define VH_AD_R(D, Q)                       \
-    switch (rep) {                          \
-        case 1: VH_AD(D, 1, Q); break;      \
-        case 2: VH_AD(D, 2, Q); break;      \
-        case 4: VH_AD(D, 4, Q); break;      \
-        default: VH_AD(D, 8, Q); break;     \
+#define VH_AD(D, R, Q, FU)                                                                          \
+    hipLaunchKernelGGL((attn_decode_partial_kernel<D, R, Q, FU>), grid, block, 0, s, q, kq, vq, ks,  \
+                       vs, kf, vf, head_stride, ctx_len, ctx_dev, n_splits, scale, part, fz)
+#define VH_AD_R(D, Q, FU)                       \
+    switch (rep) {                              \
+        case 1: VH_AD(D, 1, Q, FU); break;      \
+        case 2: VH_AD(D, 2, Q, FU); break;      \
+        case 4: VH_AD(D, 4, Q, FU); break;      \
+        default: VH_AD(D, 8, Q, FU); break;     \
     }
     if (d_head == 64) {
-        if (q8) { VH_AD_R(64, true) } else { VH_AD_R(64, false) }
+        if (fuse) { VH_AD_R(64, true, true) }
+        else if (q8) { VH_AD_R(64, true, false) }
+        else { VH_AD_R(64, false, false) }
     } else {
-        if (q8) { VH_AD_R(128, true) } else { VH_AD_R(128, false) }
+        if (fuse) { VH_AD_R(128, true, true) }
+        else if (q8) { VH_AD_R(128, true, false) }
+        else { VH_AD_R(128, false, false) }
     }
 #undef VH_AD_R
 #undef VH_AD

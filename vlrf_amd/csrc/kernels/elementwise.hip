@@ -167,17 +167,37 @@ __global__ __launch_bounds__(256) void embed_kernel(const float* __restrict__ ta
     for (int i = threadIdx.x; i < D; i += 256) x[i] = r[i];
 }
 
-// sampler::argmax (transformer.hpp:43-47): first index of the maximum.
+// sampler::argmax (transformer.hpp:43-47): first index of the maximum.  Each
+// thread issues all of its float4 loads before comparing (one memory round
+// trip); ties keep the lower index at every level.
+constexpr int kArgmaxPer = 16;   // float4 per thread: n <= 1024*4*16 = 65536
 __global__ __launch_bounds__(1024) void argmax_step_kernel(const float* __restrict__ logits, int n,
                                                            int* state, int* gen_ids, int gen_cap) {
     __shared__ float bv[1024];
     __shared__ int bi[1024];
     const int tid = threadIdx.x;
+    const int n4 = n / 4;
+    float4 v[kArgmaxPer];
+#pragma unroll
+    for (int k = 0; k < kArgmaxPer; ++k) {
+        const int f = tid + k * 1024;
+        v[k] = f < n4 ? reinterpret_cast<const float4*>(logits)[f] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
     float best = -INFINITY;
     int idx = -1;
-    for (int i = tid; i < n; i += 1024) {
-        const float v = logits[i];
-        if (idx < 0 || best < v) { best = v; idx = i; }
+#pragma unroll
+    for (int k = 0; k < kArgmaxPer; ++k) {
+        const int f = tid + k * 1024;
+        if (f < n4) {
+            const float e[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (idx < 0 || best < e[j]) { best = e[j]; idx = 4 * f + j; }
+        }
+    }
+    for (int i = 4 * n4 + tid; i < n; i += 1024) {   // tail when n % 4 != 0
+        const float e = logits[i];
+        if (idx < 0 || best < e || (best == e && i < idx)) { best = e; idx = i; }
     }
     bv[tid] = best;
     bi[tid] = idx;
@@ -264,7 +284,7 @@ int launch_embed(hipStream_t s, const float* table, const int* tok_dev, float* x
 
 int launch_argmax_step(hipStream_t s, const float* logits, int n, int* state, int* gen_ids,
                        int gen_cap) {
-    VH_ARG(n >= 1, "argmax: empty logits");
+    VH_ARG(n >= 1 && n <= 1024 * 4 * kArgmaxPer, "argmax: %d logits outside [1,%d]", n, 1024 * 4 * kArgmaxPer);
     hipLaunchKernelGGL(argmax_step_kernel, dim3(1), dim3(1024), 0, s, logits, n, state, gen_ids, gen_cap);
     VH_LAUNCHED();
     return VLRF_HIP_OK;

@@ -172,6 +172,255 @@ int dispatch_m(hipStream_t s, const DevWeight& a, const DevWeight* b, const floa
     return VLRF_HIP_OK;
 }
 
+// ---- M = 1 decode GEMV ---------------------------------------------------------
+// The workgroup stages the (RMS-normalised) activation vector in LDS once, in
+// a lane-interleaved layout: the i-th float4 of lane l for chunk c sits at
+// [(c*EPL/4 + i)*64 + l], so every ds_read_b128 of a wave touches 64
+// consecutive float4 (no bank conflicts).  A wave owns RPW rows (SwiGLU: RPW
+// gate/up row pairs) at a time; lane l covers EPL consecutive columns of each
+// chunk of 64*EPL columns, so one 16-byte load per lane per chunk streams a
+// contiguous 1 KiB run of a row (Q8_0: 16 codes, Q4_0: 32 nibbles).  Waves
+// walk their rows with a two-deep register pipeline: the next rows' weights
+// are in flight while the current ones are reduced, and the first rows' loads
+// are issued before the activations are staged.  Codes are decoded with
+// v_cvt_f32_ubyte*: Q8_0 codes are biased by 128 (xor 0x80), Q4_0 nibbles are
+// used as stored, and the bias is removed once per chunk with the lane's sum
+// of x (sum (q+b)x - b*sum x = sum qx).
+template <int WT>
+struct Gemv;
+template <>
+struct Gemv<VLRF_DT_Q8_0> { static constexpr int EPL = 16; static constexpr float BIAS = 128.f; };
+template <>
+struct Gemv<VLRF_DT_Q4_0> { static constexpr int EPL = 32; static constexpr float BIAS = 8.f; };
+
+constexpr int kGemvMaxK = 6144;          // staged activations: 24 KiB of LDS
+constexpr int kGemvMaxGroups = 512;      // workgroups of the row loop (2 per CU)
+constexpr int kGemvWaves = 8;            // waves per workgroup (one staged copy of x)
+
+__device__ __forceinline__ float ub(uint32_t v, int k) { return (float)((v >> (8 * k)) & 0xFFu); }
+
+template <int NM, int RPW, int NC>
+struct GemvRegs {
+    uint4 w[NM][RPW][NC];
+    float s[NM][RPW][NC];
+};
+
+template <int WT, int NM, int RPW, int NC>
+__device__ __forceinline__ void gemv_load(GemvRegs<NM, RPW, NC>& R, const uint8_t* __restrict__ qa,
+                                          const __half* __restrict__ da, const uint8_t* __restrict__ qb,
+                                          const __half* __restrict__ db, int row0, int N, int K,
+                                          int lane) {
+    constexpr int EPL = Gemv<WT>::EPL;
+    constexpr int CW = 64 * EPL;
+    const size_t qrow = WT == VLRF_DT_Q8_0 ? (size_t)K : (size_t)K / 2;
+    const int kb = K / 32;
+#pragma unroll
+    for (int m = 0; m < NM; ++m) {
+        const uint8_t* q = m ? qb : qa;
+        const __half* d = m ? db : da;
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) {
+            const int row = row0 + r;
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                const int e0 = c * CW + lane * EPL;
+                if (row < N && e0 < K) {
+                    R.w[m][r][c] = *reinterpret_cast<const uint4*>(q + (size_t)row * qrow + (size_t)c * 1024 + lane * 16);
+                    R.s[m][r][c] = __half2float(d[(size_t)row * kb + e0 / 32]);
+                } else {
+                    R.w[m][r][c] = make_uint4(0, 0, 0, 0);
+                    R.s[m][r][c] = 0.f;
+                }
+            }
+        }
+    }
+}
+
+template <int WT, int NM, int RPW, int NC, bool SWIGLU>
+__device__ __forceinline__ void gemv_compute(const GemvRegs<NM, RPW, NC>& R, const float4* xs4,
+                                             const float (&xsum)[NC], int row0, int N, int lane,
+                                             const float* residual, float* y) {
+    constexpr int EPL = Gemv<WT>::EPL;
+    float acc[NM][RPW];
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) acc[m][r] = 0.f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        float xv[EPL];
+#pragma unroll
+        for (int i = 0; i < EPL / 4; ++i) {
+            const float4 v = xs4[(c * (EPL / 4) + i) * 64 + lane];
+            xv[4 * i] = v.x; xv[4 * i + 1] = v.y; xv[4 * i + 2] = v.z; xv[4 * i + 3] = v.w;
+        }
+#pragma unroll
+        for (int m = 0; m < NM; ++m)
+#pragma unroll
+            for (int r = 0; r < RPW; ++r) {
+                const uint32_t u[4] = {R.w[m][r][c].x, R.w[m][r][c].y, R.w[m][r][c].z, R.w[m][r][c].w};
+                float p = 0.f;
+                if constexpr (WT == VLRF_DT_Q8_0) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const uint32_t b = u[j] ^ 0x80808080u;
+#pragma unroll
+                        for (int k = 0; k < 4; ++k) p += ub(b, k) * xv[4 * j + k];
+                    }
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const uint32_t lo = u[j] & 0x0F0F0F0Fu, hi = (u[j] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+                        for (int k = 0; k < 4; ++k) {
+                            // byte 4j+k holds elements 2(4j+k) (low) and 2(4j+k)+1 (high)
+                            p += ub(lo, k) * xv[8 * j + 2 * k];
+                            p += ub(hi, k) * xv[8 * j + 2 * k + 1];
+                        }
+                    }
+                }
+                acc[m][r] = fmaf(R.s[m][r][c], p - xsum[c], acc[m][r]);
+            }
+    }
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+        const int row = row0 + r;
+        float out = wave_sum(acc[0][r]);
+        if constexpr (SWIGLU) {
+            const float u = wave_sum(acc[1][r]);
+            out = u * (out / (1.f + expf(-out)));   // silu(g) * u, ops.hpp:409-441
+        }
+        if (lane == 0 && row < N) {
+            if (residual) out = out + residual[row];
+            y[row] = out;
+        }
+    }
+}
+
+template <int WT, int NC, int RPW, bool SWIGLU>
+__global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(
+    const uint8_t* __restrict__ qa, const __half* __restrict__ da, const uint8_t* __restrict__ qb,
+    const __half* __restrict__ db, int N, int K, const float* __restrict__ x,
+    const int* __restrict__ x_row, float* x_copy, const float* __restrict__ norm_w, float eps,
+    const float* residual, float* y) {
+    constexpr int EPL = Gemv<WT>::EPL;
+    constexpr int CW = 64 * EPL;
+    constexpr int NM = SWIGLU ? 2 : 1;
+    constexpr int NT = 64 * kGemvWaves;
+    constexpr int XF4 = NC * CW / 4;                  // staged float4 slots
+    constexpr int PER = (XF4 + NT - 1) / NT;          // float4 per thread
+    __shared__ float4 xs4[XF4];
+    __shared__ float red[kGemvWaves];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nwaves = gridDim.x * kGemvWaves;
+    int row0 = (blockIdx.x * kGemvWaves + wave) * RPW;
+    const int rstep = nwaves * RPW;
+
+    // The first two row groups of this wave are requested before anything else.
+    GemvRegs<NM, RPW, NC> A, B;
+    if (row0 < N) gemv_load<WT, NM, RPW, NC>(A, qa, da, qb, db, row0, N, K, lane);
+    if (row0 + rstep < N) gemv_load<WT, NM, RPW, NC>(B, qa, da, qb, db, row0 + rstep, N, K, lane);
+
+    // x_row: x is row *x_row of a table (the embedding gather of the first
+    // layer, ops.hpp:615-626); workgroup 0 copies the raw row to x_copy.
+    const float* xr = x_row ? x + (size_t)(*x_row) * K : x;
+
+    // Stage x (optionally RMS-normalised, ops.hpp:488-498) in the lane-interleaved layout.
+    float4 v[PER];
+    float ss = 0.f;
+#pragma unroll
+    for (int p = 0; p < PER; ++p) {
+        const int f = tid + p * NT;            // float4 index in x
+        v[p] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (f < XF4 && 4 * f < K) v[p] = reinterpret_cast<const float4*>(xr)[f];
+        ss += v[p].x * v[p].x + v[p].y * v[p].y + v[p].z * v[p].z + v[p].w * v[p].w;
+        if (x_copy && blockIdx.x == 0 && f < XF4 && 4 * f < K) reinterpret_cast<float4*>(x_copy)[f] = v[p];
+    }
+    float inv = 1.f;
+    if (norm_w) {
+        ss = wave_sum(ss);
+        if (lane == 0) red[wave] = ss;
+        __syncthreads();
+        ss = 0.f;
+#pragma unroll
+        for (int w = 0; w < kGemvWaves; ++w) ss += red[w];
+        inv = 1.f / sqrtf(ss / (float)K + eps);
+    }
+#pragma unroll
+    for (int p = 0; p < PER; ++p) {
+        const int f = tid + p * NT;
+        if (f < XF4) {
+            float4 o = v[p];
+            if (norm_w && 4 * f < K) {
+                const float4 g = reinterpret_cast<const float4*>(norm_w)[f];
+                o.x = o.x * inv * g.x; o.y = o.y * inv * g.y;
+                o.z = o.z * inv * g.z; o.w = o.w * inv * g.w;
+            }
+            const int e = 4 * f, c = e / CW, r = e - c * CW, l = r / EPL, i = (r - l * EPL) / 4;
+            xs4[(c * (EPL / 4) + i) * 64 + l] = o;
+        }
+    }
+    __syncthreads();
+    float xsum[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        float sacc = 0.f;
+#pragma unroll
+        for (int i = 0; i < EPL / 4; ++i) {
+            const float4 o = xs4[(c * (EPL / 4) + i) * 64 + lane];
+            sacc += (o.x + o.y) + (o.z + o.w);
+        }
+        xsum[c] = sacc * Gemv<WT>::BIAS;
+    }
+
+    for (; row0 < N; row0 += 2 * rstep) {
+        const int r1 = row0 + rstep;
+        gemv_compute<WT, NM, RPW, NC, SWIGLU>(A, xs4, xsum, row0, N, lane, residual, y);
+        const int r2 = r1 + rstep;
+        if (r2 < N) gemv_load<WT, NM, RPW, NC>(A, qa, da, qb, db, r2, N, K, lane);
+        if (r1 >= N) break;
+        gemv_compute<WT, NM, RPW, NC, SWIGLU>(B, xs4, xsum, r1, N, lane, residual, y);
+        const int r3 = r2 + rstep;
+        if (r3 < N) gemv_load<WT, NM, RPW, NC>(B, qa, da, qb, db, r3, N, K, lane);
+    }
+}
+
+template <int WT, bool SWIGLU>
+int launch_gemv(hipStream_t s, const DevWeight& a, const DevWeight* b, const float* x, float* y,
+                const float* norm_w, float eps, const float* residual, const int* x_row = nullptr,
+                float* x_copy = nullptr) {
+    constexpr int CW = 64 * Gemv<WT>::EPL;
+    const int nc = (a.K + CW - 1) / CW;
+    const uint8_t* qb = b ? b->q : nullptr;
+    const __half* db = b ? b->d : nullptr;
+#define VH_GEMV(NC, RPW)                                                                               \
+    do {                                                                                              \
+        const int groups = (a.N + kGemvWaves * (RPW)-1) / (kGemvWaves * (RPW));                        \
+        dim3 grid(groups < kGemvMaxGroups ? groups : kGemvMaxGroups);                                  \
+        hipLaunchKernelGGL((gemv_kernel<WT, NC, RPW, SWIGLU>), grid, dim3(64 * kGemvWaves), 0, s, a.q, \
+                           a.d, qb, db,                                                                \
+                           a.N, a.K, x, x_row, x_copy, norm_w, eps, residual, y);                      \
+    } while (0)
+    if (nc <= 1) {
+        VH_GEMV(1, 1);
+    } else if (nc <= 2) {
+        VH_GEMV(2, 1);
+    } else if (nc <= 3) {
+        VH_GEMV(3, 1);
+    } else {
+        VH_GEMV(6, 1);
+    }
+#undef VH_GEMV
+    VH_LAUNCHED();
+    return VLRF_HIP_OK;
+}
+
+// The LDS-staged GEMV covers K up to kGemvMaxK columns.
+bool gemv_fits(const DevWeight& w) {
+    return (w.dtype == VLRF_DT_Q8_0 || w.dtype == VLRF_DT_Q4_0) && w.K <= kGemvMaxK;
+}
+
 int check_weight(const DevWeight& w) {
     VH_ARG(w.N > 0 && w.K > 0, "qlinear: empty weight");
     VH_ARG(w.dtype == VLRF_DT_F32 || w.dtype == VLRF_DT_Q8_0 || w.dtype == VLRF_DT_Q4_0,
@@ -190,11 +439,27 @@ int launch_qlinear(hipStream_t s, const DevWeight& w, const float* x, float* y, 
     if (rc) return rc;
     VH_ARG(M >= 1 && M <= 16, "qlinear: M=%d outside [1,16]", M);
     VH_ARG(x && y, "qlinear: null activation pointer");
+    if (M == 1 && gemv_fits(w)) {
+        if (w.dtype == VLRF_DT_Q8_0) return launch_gemv<VLRF_DT_Q8_0, false>(s, w, nullptr, x, y, norm_w, eps, residual);
+        return launch_gemv<VLRF_DT_Q4_0, false>(s, w, nullptr, x, y, norm_w, eps, residual);
+    }
     switch (w.dtype) {
         case VLRF_DT_Q8_0: return dispatch_m<VLRF_DT_Q8_0, false>(s, w, nullptr, x, y, M, norm_w, eps, residual);
         case VLRF_DT_Q4_0: return dispatch_m<VLRF_DT_Q4_0, false>(s, w, nullptr, x, y, M, norm_w, eps, residual);
         default:           return dispatch_m<VLRF_DT_F32, false>(s, w, nullptr, x, y, M, norm_w, eps, residual);
     }
+}
+
+bool qlinear_gather_supported(const DevWeight& w) { return gemv_fits(w); }
+
+int launch_qlinear_gather(hipStream_t s, const DevWeight& w, const float* table, const int* row,
+                          float* x_copy, float* y, const float* norm_w, float eps) {
+    int rc = check_weight(w);
+    if (rc) return rc;
+    VH_ARG(gemv_fits(w), "qlinear_gather: weight dtype %d / K %d not supported", w.dtype, w.K);
+    if (w.dtype == VLRF_DT_Q8_0)
+        return launch_gemv<VLRF_DT_Q8_0, false>(s, w, nullptr, table, y, norm_w, eps, nullptr, row, x_copy);
+    return launch_gemv<VLRF_DT_Q4_0, false>(s, w, nullptr, table, y, norm_w, eps, nullptr, row, x_copy);
 }
 
 int launch_qlinear_swiglu(hipStream_t s, const DevWeight& wg, const DevWeight& wu,
@@ -206,6 +471,10 @@ int launch_qlinear_swiglu(hipStream_t s, const DevWeight& wg, const DevWeight& w
     VH_ARG(wg.N == wu.N && wg.K == wu.K && wg.dtype == wu.dtype,
            "swiglu: gate/up shapes or dtypes differ");
     VH_ARG(M >= 1 && M <= 16, "swiglu: M=%d outside [1,16]", M);
+    if (M == 1 && gemv_fits(wg)) {
+        if (wg.dtype == VLRF_DT_Q8_0) return launch_gemv<VLRF_DT_Q8_0, true>(s, wg, &wu, x, h, norm_w, eps, nullptr);
+        return launch_gemv<VLRF_DT_Q4_0, true>(s, wg, &wu, x, h, norm_w, eps, nullptr);
+    }
     switch (wg.dtype) {
         case VLRF_DT_Q8_0: return dispatch_m<VLRF_DT_Q8_0, true>(s, wg, &wu, x, h, M, norm_w, eps, nullptr);
         case VLRF_DT_Q4_0: return dispatch_m<VLRF_DT_Q4_0, true>(s, wg, &wu, x, h, M, norm_w, eps, nullptr);

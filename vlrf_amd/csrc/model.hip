@@ -6,10 +6,12 @@
 // FeedForward::forward SwiGLU (feedforward.hpp:50-77), greedy argmax
 // (transformer.hpp:43-47).
 //
-// Per layer the step queues five kernels:
+// Per layer the step queues six kernels:
 //   qlinear(Wqkv, rmsnorm(x; ln1))        Q,K,V in one pass over the fused rows
-//   rope_append                           RoPE on q,k; Q8_0 quantize k,v at pos
-//   attn_decode (+ combine)               split-K over the quantized cache
+//   attn_decode                           RoPE on q,k and the Q8_0 append of the
+//                                         token's K/V row, fused with split-K
+//                                         attention over the quantized cache
+//   attn_combine                          log-sum-exp merge of the chunks
 //   qlinear(Wo, att) + x                  residual in the epilogue
 //   swiglu(Wg, Wu, rmsnorm(x; ln2))       silu(g) * u in the epilogue
 //   qlinear(Wd, h) + x
@@ -21,6 +23,7 @@
 #include "runtime.hpp"
 
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <new>
 #include <string>
@@ -61,6 +64,7 @@ struct vlrf_hip_model {
     int n_splits = 0;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
+    bool use_graph = true;     // VLRF_HIP_GRAPH=0: queue the step's kernels directly
     int pos = 0;               // host mirror of state[1]
 
     bool ready() const {
@@ -74,7 +78,9 @@ struct vlrf_hip_model {
 namespace {
 
 int enqueue_step(vlrf_hip_model* m, hipStream_t s) {
-    int rc = launch_embed(s, m->embed, m->state, m->x, m->D);
+    // Layer 0's QKV projection gathers the embedding row itself when it can.
+    const bool gather = qlinear_gather_supported(m->layers[0].wqkv);
+    int rc = gather ? VLRF_HIP_OK : launch_embed(s, m->embed, m->state, m->x, m->D);
     const float eps = m->cfg.norm_eps;
     const float scale = 1.f / std::sqrt((float)m->dh);   // attention.hpp:373-374
     for (int l = 0; l < m->L && !rc; ++l) {
@@ -82,12 +88,26 @@ int enqueue_step(vlrf_hip_model* m, hipStream_t s) {
         float* q = m->qkv;
         float* k = m->qkv + m->D;
         float* v = m->qkv + m->D + m->dkv;
-        if (!rc) rc = launch_qlinear(s, Ly.wqkv, m->x, m->qkv, 1, Ly.ln1, eps, nullptr);
-        if (!rc) rc = launch_rope_append(s, Ly.kv, q, k, v, m->H, m->G, m->dh, m->S, m->state + 1,
-                                         m->cos_t, m->sin_t);
+        if (!rc) {
+            if (l == 0 && gather)   // embedding_lookup (ops.hpp:615-626) fused: x = embed[token]
+                rc = launch_qlinear_gather(s, Ly.wqkv, m->embed, m->state, m->x, m->qkv, Ly.ln1, eps);
+            else
+                rc = launch_qlinear(s, Ly.wqkv, m->x, m->qkv, 1, Ly.ln1, eps, nullptr);
+        }
+        DecodeFuse fz;
+        fz.k_new = k;
+        fz.v_new = v;
+        fz.cos_t = m->cos_t;
+        fz.sin_t = m->sin_t;
+        fz.kq_w = Ly.kv.k;
+        fz.vq_w = Ly.kv.v;
+        fz.ks_w = Ly.kv.ks;
+        fz.vs_w = Ly.kv.vs;
+        fz.n_kv = m->G;
+        fz.max_seq = m->S;
         if (!rc) rc = launch_attn_decode(s, q, Ly.kv.k, Ly.kv.v, Ly.kv.ks, Ly.kv.vs, nullptr, nullptr,
                                          (long)m->S * m->dh, m->H, m->G, m->dh, 1, m->state + 1,
-                                         m->n_splits, scale, m->part, m->att);
+                                         m->n_splits, scale, m->part, m->att, &fz);
         if (!rc) rc = launch_qlinear(s, Ly.wo, m->att, m->x, 1, nullptr, 0.f, m->x);
         if (!rc) rc = launch_qlinear_swiglu(s, Ly.wg, Ly.wu, m->x, m->h, 1, Ly.ln2, eps);
         if (!rc) rc = launch_qlinear(s, Ly.wd, m->h, m->x, 1, nullptr, 0.f, m->x);
@@ -98,7 +118,7 @@ int enqueue_step(vlrf_hip_model* m, hipStream_t s) {
 }
 
 int ensure_graph(vlrf_hip_model* m) {
-    if (m->exec) return VLRF_HIP_OK;
+    if (m->exec || !m->use_graph) return VLRF_HIP_OK;
     hipStream_t s = m->ctx->stream;
     VH_CHECK(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
     int rc = enqueue_step(m, s);
@@ -114,6 +134,14 @@ int ensure_graph(vlrf_hip_model* m) {
     }
     m->graph = g;
     VH_CHECK(hipGraphInstantiate(&m->exec, g, nullptr, nullptr, 0));
+    return VLRF_HIP_OK;
+}
+
+// One decode step on the context stream: the captured graph, or the same
+// kernels queued one by one when graphs are switched off.
+int launch_step(vlrf_hip_model* m) {
+    if (!m->use_graph) return enqueue_step(m, m->ctx->stream);
+    VH_CHECK(hipGraphLaunch(m->exec, m->ctx->stream));
     return VLRF_HIP_OK;
 }
 
@@ -169,6 +197,7 @@ int vlrf_hip_model_create(vlrf_hip_ctx_t ctx, const vlrf_hip_model_config* cfg, 
     m->dkv = c.n_kv_heads * dh; m->L = c.n_layers; m->V = c.vocab_size; m->S = c.max_seq_len;
     m->n_splits = attn_decode_splits(m->S);
     m->layers.resize(m->L);
+    if (const char* g = std::getenv("VLRF_HIP_GRAPH")) m->use_graph = std::strcmp(g, "0") != 0;
 
     int rc = VLRF_HIP_OK;
     auto dalloc = [&](void** p, size_t bytes) {
@@ -347,7 +376,7 @@ int vlrf_hip_model_step(vlrf_hip_model_t m, int32_t token, int32_t* next, float*
     hipStream_t s = m->ctx->stream;
     m->pinned[0] = token;
     VH_CHECK(hipMemcpyAsync(m->state, m->pinned, sizeof(int), hipMemcpyHostToDevice, s));
-    VH_CHECK(hipGraphLaunch(m->exec, s));
+    if ((rc = launch_step(m))) return rc;
     VH_CHECK(hipMemcpyAsync(m->pinned, m->state, sizeof(int), hipMemcpyDeviceToHost, s));
     if (logits) VH_CHECK(hipMemcpyAsync(logits, m->logits, (size_t)m->V * 4, hipMemcpyDeviceToHost, s));
     VH_CHECK(hipStreamSynchronize(s));
@@ -371,7 +400,7 @@ int vlrf_hip_model_prefill(vlrf_hip_model_t m, const int32_t* ids, int n, int32_
     VH_CHECK(hipStreamSynchronize(s));
     for (int i = 0; i < n; ++i) {
         VH_CHECK(hipMemcpyAsync(m->state, m->prompt + i, sizeof(int), hipMemcpyDeviceToDevice, s));
-        VH_CHECK(hipGraphLaunch(m->exec, s));
+        if ((rc = launch_step(m))) return rc;
     }
     VH_CHECK(hipMemcpyAsync(m->pinned, m->state, sizeof(int), hipMemcpyDeviceToHost, s));
     VH_CHECK(hipStreamSynchronize(s));
@@ -395,7 +424,8 @@ int vlrf_hip_model_generate_async(vlrf_hip_model_t m, int32_t first, int n_steps
     m->pinned[1] = m->pos;
     m->pinned[2] = 0;
     VH_CHECK(hipMemcpyAsync(m->state, m->pinned, 3 * sizeof(int), hipMemcpyHostToDevice, s));
-    for (int i = 0; i < n_steps; ++i) VH_CHECK(hipGraphLaunch(m->exec, s));
+    for (int i = 0; i < n_steps; ++i)
+        if ((rc = launch_step(m))) return rc;
     m->pos += n_steps;
     return VLRF_HIP_OK;
 }
