@@ -12,12 +12,17 @@ roofline: the dominant kernel of the step, the fused RMSNorm + gate/up
 dequant-GEMV with the SwiGLU epilogue (52% of a step's bytes), timed live
 with HIP events over launches that rotate through 12 distinct weight pairs
 (295 MB, more than the 256 MB Infinity Cache), so the bytes come from HBM.
+`traffic` is the HBM bytes per launch that rocprofv3 counted (FETCH_SIZE and
+WRITE_SIZE passes over `bench.py --roofline-only`, each scaled by the same
+counter on a plain 256 MiB device copy), read from the committed summary
+profiles/gemv_swiglu_q8_1b_pmc.txt; null when that file is absent.
 
 cpu_baseline: the oracle's restatement of the reference decode step
 (oracle/vlrf_oracle.c: f32 decoded weights, AVX2 streaming GEMV, full-cache
 dequant, per-head flash attention) on the host's cores at context 2048.
 
     python bench.py [--gpus 1] [--steps 128] [--warmup 8] [--dtype q8_0|q4_0]
+    python bench.py --roofline-only     # copy calibration + roofline launches only
 """
 import argparse
 import json
@@ -31,6 +36,8 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0   # MI355X published HBM3E bandwidth
+PMC_SUMMARY = os.path.join(ROOT, "profiles", "gemv_swiglu_q8_1b_pmc.txt")
+COPY_BYTES = 256 << 20  # calibration copy size for the PMC passes
 
 
 def log(*a):
@@ -61,10 +68,35 @@ def gemv_roofline(ctx, V, F, cfg, dtype, launches=96):
     wbytes = 2 * pairs[0][0].device_bytes
     algo = wbytes + D * 4 * 2 + Fd * 4          # weights + x + norm weight + h
     achieved = algo / per_launch_s / 1e9
-    return {"kernel": "qlinear_kernel<Q8_0,1,swiglu> (gate/up 2x5632x2048)",
+    chunk = 64 * (16 if dtype == V.DT_Q8_0 else 32)      # K columns per lane-chunk of one wave
+    name = "gemv_kernel<%d, %d, 1, true>" % (dtype, (D + chunk - 1) // chunk)
+    return {"kernel": name + " (RMSNorm + gate/up %dx%d + SwiGLU)" % (Fd, D),
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-            "bytes_per_launch": int(algo), "us_per_launch": round(per_launch_s * 1e6, 3)}
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": pmc_traffic(dtype),
+            "bytes_per_launch": int(algo), "us_per_launch": round(per_launch_s * 1e6, 3),
+            "launches": launches}
+
+
+def pmc_traffic(dtype):
+    """HBM bytes per launch from the committed rocprofv3 PMC summary (Q8_0 only)."""
+    if dtype != 8 or not os.path.exists(PMC_SUMMARY):
+        return None
+    for line in open(PMC_SUMMARY):
+        if line.startswith("traffic_bytes_per_launch"):
+            return int(float(line.split("=")[1]))
+    return None
+
+
+def copy_calibration():
+    """One plain device copy of COPY_BYTES (a torch copy kernel), so that a PMC
+    pass can relate FETCH_SIZE / WRITE_SIZE to a known byte count."""
+    import torch
+    src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"[bench] copy calibration: 3 x {COPY_BYTES} B device copy")
 
 
 def cpu_baseline(cfg, f32w, ctx_len, budget_s=12.0, max_steps=8):
@@ -104,11 +136,13 @@ def main():
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-roofline", action="store_true")
+    ap.add_argument("--roofline-only", action="store_true",
+                    help="run the copy calibration and the roofline launches only (PMC passes)")
     a = ap.parse_args()
 
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(see DESIGN.md, 'How the path would shard').", file=sys.stderr)
+        print("bench.py measures one GPU only: this build has no multi-GPU path; "
+              "the sharding of the decode step is described, not built.", file=sys.stderr)
         sys.exit(2)
 
     import vlrf_amd as V
@@ -118,6 +152,10 @@ def main():
     cfg = F.llama_1b(max_seq_len=a.ctx + a.steps, weight_dtype=dtype)
     ctx = V.Context(0)
     log("[bench]", ctx.device_info())
+    if a.roofline_only:
+        copy_calibration()
+        print(json.dumps({"roofline": gemv_roofline(ctx, V, F, cfg, dtype)}), flush=True)
+        return
 
     t0 = time.time()
     model = V.Model(ctx, cfg)
