@@ -87,16 +87,18 @@ def pmc_traffic(dtype):
     return None
 
 
-def copy_calibration():
-    """One plain device copy of COPY_BYTES (a torch copy kernel), so that a PMC
-    pass can relate FETCH_SIZE / WRITE_SIZE to a known byte count."""
-    import torch
-    src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device="cuda:0")
-    dst = torch.empty_like(src)
+def copy_calibration(ctx):
+    """Three plain device copies of COPY_BYTES (the runtime's blit copy
+    kernel), so that a PMC pass can relate FETCH_SIZE / WRITE_SIZE to a known
+    byte count."""
+    src, dst = ctx.alloc(COPY_BYTES), ctx.alloc(COPY_BYTES)
+    src.zero()
     for _ in range(3):
-        dst.copy_(src)
-    torch.cuda.synchronize()
+        dst.copy_from(src)
+    ctx.sync()
     log(f"[bench] copy calibration: 3 x {COPY_BYTES} B device copy")
+    src.free()
+    dst.free()
 
 
 def cpu_baseline(cfg, f32w, ctx_len, budget_s=12.0, max_steps=8):
@@ -153,7 +155,7 @@ def main():
     ctx = V.Context(0)
     log("[bench]", ctx.device_info())
     if a.roofline_only:
-        copy_calibration()
+        copy_calibration(ctx)
         print(json.dumps({"roofline": gemv_roofline(ctx, V, F, cfg, dtype)}), flush=True)
         return
 

@@ -68,6 +68,8 @@ int   vlrf_hip_free(vlrf_hip_ctx_t ctx, void* dptr);
 int   vlrf_hip_h2d(vlrf_hip_ctx_t ctx, void* dst, const void* src, size_t bytes);
 int   vlrf_hip_d2h(vlrf_hip_ctx_t ctx, void* dst, const void* src, size_t bytes);
 int   vlrf_hip_memset(vlrf_hip_ctx_t ctx, void* dst, int value, size_t bytes);
+/* Device-to-device copy, queued on the context stream (does not wait). */
+int   vlrf_hip_d2d(vlrf_hip_ctx_t ctx, void* dst, const void* src, size_t bytes);
 /* Event timing on the context stream: records start/stop around queued work. */
 int   vlrf_hip_timer_start(vlrf_hip_ctx_t ctx);
 int   vlrf_hip_timer_stop(vlrf_hip_ctx_t ctx, float* ms);  /* waits for the stop event */

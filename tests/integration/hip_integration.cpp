@@ -1,0 +1,212 @@
+// hip_integration.cpp - exercises the engine-side adapters of
+// vlrf_amd/integration/ (HipBackend : IBackend, HipDecoder) with the reference
+// engine's own types: its Tensor, ModelConfig, WeightMap, CpuBackend and
+// TransformerModel, compiled from the reference's headers where they lie.
+//
+// TEST INFRASTRUCTURE ONLY.  oracle/Makefile builds it into
+// oracle/_ref/hip_integration (with the reference tree present); the test
+// tests/test_integration.py runs it.  Checks:
+//   attention  HipBackend::sdp_attention vs a float64 softmax attention with
+//              the causal rule key > query + (ctx - T) (attention.hpp:232,253-261),
+//              including T != ctx, where the reference's default is wrong;
+//   gemm       HipBackend::gemm (x . W^T) vs the reference CpuBackend::gemm;
+//   decode     HipDecoder::generate vs TransformerModel::generate, greedy,
+//              on a tiny Llama-style model with Q8_0 weights and KV cache:
+//              the token streams must be identical.
+// Without a usable device (or with --cpu) the first two run through
+// HipBackend's CPU fallback and `decode` is skipped.  Exit status 0 = all pass.
+
+// The unpatched reference enum has no HIP value; the integration patch appends
+// it after SYCL.
+#define VLRF_HIP_BACKEND_TYPE static_cast<BackendType>(3)
+
+#include "transformer.hpp"
+#include "hip_backend.hpp"
+#include "hip_decoder.hpp"
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+using vlrf::Tensor;
+using vlrf::backend::CpuBackend;
+using vlrf::backend::HipBackend;
+
+namespace {
+
+int g_fail = 0;
+
+void report(bool ok, const std::string& what, double err) {
+    std::printf("%s %s (err %.3g)\n", ok ? "PASS" : "FAIL", what.c_str(), err);
+    std::fflush(stdout);
+    if (!ok) ++g_fail;
+}
+
+Tensor normal_tensor(std::initializer_list<int32_t> dims, uint64_t stream, float std_dev) {
+    Tensor t(dims);
+    vlrf_synth_normal(77, stream, std_dev, t.data_ptr(), t.numel());
+    return t;
+}
+
+double rel_err(const float* a, const std::vector<double>& b) {
+    double num = 0, den = 0;
+    for (size_t i = 0; i < b.size(); ++i) {
+        num = std::fmax(num, std::fabs(a[i] - b[i]));
+        den = std::fmax(den, std::fabs(b[i]));
+    }
+    return den > 0 ? num / den : num;
+}
+
+void check_attention(HipBackend const& be) {
+    struct Case { int n_h, T, ctx, d; bool causal; };
+    const Case cases[] = {{8, 1, 512, 64, false}, {4, 16, 16, 64, true}, {2, 5, 40, 128, true},
+                          {3, 1, 300, 64, false}, {2, 7, 7, 32, false}};
+    uint64_t stream = 100;
+    for (const Case& c : cases) {
+        Tensor Q = normal_tensor({c.n_h, c.T, c.d}, stream++, 1.f);
+        Tensor K = normal_tensor({c.n_h, c.ctx, c.d}, stream++, 1.f);
+        Tensor V = normal_tensor({c.n_h, c.ctx, c.d}, stream++, 1.f);
+        Tensor O = be.sdp_attention(Q, K, V, c.causal);
+        std::vector<double> ref((size_t)c.n_h * c.T * c.d, 0.0), s(c.ctx);
+        const double scale = 1.0 / std::sqrt((double)c.d);
+        for (int h = 0; h < c.n_h; ++h)
+            for (int i = 0; i < c.T; ++i) {
+                const int last = c.causal ? i + (c.ctx - c.T) : c.ctx - 1;
+                double mx = -1e300;
+                for (int j = 0; j <= last; ++j) {
+                    double dot = 0;
+                    for (int k = 0; k < c.d; ++k)
+                        dot += (double)Q.data_ptr()[((size_t)h * c.T + i) * c.d + k] *
+                               K.data_ptr()[((size_t)h * c.ctx + j) * c.d + k];
+                    s[j] = dot * scale;
+                    mx = std::fmax(mx, s[j]);
+                }
+                double l = 0;
+                for (int j = 0; j <= last; ++j) l += (s[j] = std::exp(s[j] - mx));
+                for (int k = 0; k < c.d; ++k) {
+                    double acc = 0;
+                    for (int j = 0; j <= last; ++j) acc += s[j] * V.data_ptr()[((size_t)h * c.ctx + j) * c.d + k];
+                    ref[((size_t)h * c.T + i) * c.d + k] = acc / l;
+                }
+            }
+        const bool shape_ok = O.ndim() == 3 && O.dim(0) == c.n_h && O.dim(1) == c.T && O.dim(2) == c.d;
+        const double e = shape_ok ? rel_err(O.data_ptr(), ref) : 1e9;
+        char name[128];
+        std::snprintf(name, sizeof(name), "attention n_h=%d T=%d ctx=%d d=%d causal=%d", c.n_h, c.T, c.ctx,
+                      c.d, (int)c.causal);
+        report(shape_ok && e <= 1e-3, name, e);
+    }
+}
+
+void check_gemm(HipBackend const& be) {
+    CpuBackend cpu;
+    const int shapes[][3] = {{1, 2048, 300}, {4, 512, 77}, {16, 256, 264}, {3, 100, 40}};
+    uint64_t stream = 200;
+    for (auto const& sh : shapes) {
+        const int M = sh[0], K = sh[1], N = sh[2];
+        Tensor A = normal_tensor({M, K}, stream++, 1.f);
+        Tensor B = normal_tensor({N, K}, stream++, 0.02f);
+        Tensor C({M, N}), R({M, N});
+        be.gemm(A, B, C, 1.f, 0.f, false, true);
+        cpu.gemm(A, B, R, 1.f, 0.f, false, true);
+        std::vector<double> ref(R.data_ptr(), R.data_ptr() + R.numel());
+        const double e = rel_err(C.data_ptr(), ref);
+        char name[96];
+        std::snprintf(name, sizeof(name), "gemm x.W^T M=%d K=%d N=%d", M, K, N);
+        report(e <= 1e-3, name, e);
+    }
+}
+
+// Q8_0 round trip so the reference runs on exactly the weights the device holds.
+void q8_roundtrip(Tensor& t) {
+    std::vector<unsigned char> blocks((size_t)t.numel() / 32 * 34);
+    vlrf_quantize_q8_0(t.data_ptr(), blocks.data(), t.numel());
+    vlrf_dequantize(blocks.data(), VLRF_DT_Q8_0, t.data_ptr(), t.numel());
+}
+
+void check_decode(HipBackend const& be) {
+    vlrf::ModelConfig c;
+    c.vocab_size = 512;
+    c.d_model = 256;
+    c.d_ff = 704;
+    c.n_heads = 4;
+    c.n_kv_heads = 1;
+    c.n_layers = 2;
+    c.max_seq_len = 160;
+    c.layer_norm_eps = 1e-5f;
+    c.rope_theta = 10000.f;
+    c.use_rms_norm = true;
+    c.pre_norm = true;
+    c.activation = vlrf::Activation::SILU;
+    c.pos_embedding = vlrf::PosEmbedding::ROTARY;
+    c.tie_embeddings = false;
+    c.kv_cache_dtype = static_cast<int>(vlrf::KVCacheDType::Q8_0);
+    c.eos_token_id = -1;
+    c.do_sample = false;
+
+    vlrf::TransformerModel m;
+    m.init(c);
+    uint64_t stream = 300;
+    auto put = [&](const std::string& name, std::initializer_list<int32_t> dims, float sd, bool q8,
+                   float offset) {
+        Tensor t = normal_tensor(dims, stream++, sd);
+        if (offset != 0.f)
+            for (int64_t i = 0; i < t.numel(); ++i) t.data_ptr()[i] += offset;
+        if (q8) q8_roundtrip(t);
+        m.wm.tensors[name] = t;
+    };
+    put("embed.weight", {c.vocab_size, c.d_model}, 1.f, false, 0.f);
+    put("ln_final.weight", {c.d_model}, 0.1f, false, 1.f);
+    put("lm_head.weight", {c.vocab_size, c.d_model}, 0.05f, true, 0.f);
+    const int dkv = c.d_model / c.n_heads * c.n_kv_heads;
+    for (int l = 0; l < c.n_layers; ++l) {
+        const std::string p = "layers." + std::to_string(l) + ".";
+        put(p + "ln1.weight", {c.d_model}, 0.1f, false, 1.f);
+        put(p + "ln2.weight", {c.d_model}, 0.1f, false, 1.f);
+        put(p + "attn.q_proj.weight", {c.d_model, c.d_model}, 0.05f, true, 0.f);
+        put(p + "attn.k_proj.weight", {dkv, c.d_model}, 0.05f, true, 0.f);
+        put(p + "attn.v_proj.weight", {dkv, c.d_model}, 0.05f, true, 0.f);
+        put(p + "attn.o_proj.weight", {c.d_model, c.d_model}, 0.05f, true, 0.f);
+        put(p + "ffn.gate.weight", {c.d_ff, c.d_model}, 0.05f, true, 0.f);
+        put(p + "ffn.fc1.weight", {c.d_ff, c.d_model}, 0.05f, true, 0.f);
+        put(p + "ffn.fc2.weight", {c.d_model, c.d_ff}, 0.05f, true, 0.f);
+    }
+    m.bind_weights();
+
+    std::vector<int32_t> p32(40);
+    vlrf_synth_tokens(77, 400, c.vocab_size, p32.data(), (int64_t)p32.size());
+    std::vector<int> prompt(p32.begin(), p32.end());
+    vlrf::GenerationConfig gc;
+    gc.max_new_tokens = 64;
+    gc.do_sample = false;
+    const std::vector<int> ref = m.generate(prompt, gc).token_ids;
+
+    vlrf::HipDecoder dec(be.context(), c, m.wm, VLRF_DT_Q8_0);
+    const std::vector<int> got = dec.generate(prompt, gc.max_new_tokens);
+    int first_diff = -1;
+    for (size_t i = 0; i < ref.size() && i < got.size(); ++i)
+        if (ref[i] != got[i]) { first_diff = (int)i; break; }
+    const bool ok = got.size() == ref.size() && first_diff < 0;
+    report(ok, "decode: HipDecoder::generate == TransformerModel::generate (64 greedy steps)",
+           first_diff < 0 ? 0.0 : (double)first_diff);
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+    const bool cpu_only = argc > 1 && std::strcmp(argv[1], "--cpu") == 0;
+    HipBackend be;
+    const bool dev = !cpu_only && be.try_init(0);
+    std::printf("[backend] %s\n", be.device_info().c_str());
+    std::fflush(stdout);
+    check_attention(be);
+    check_gemm(be);
+    if (dev)
+        check_decode(be);
+    else
+        std::printf("SKIP decode (no HIP device)\n");
+    std::printf("%s: %d failure(s)\n", g_fail ? "FAILED" : "OK", g_fail);
+    return g_fail ? 1 : 0;
+}

@@ -74,3 +74,15 @@ def test_tensor_specs_cover_the_reference_weight_names():
                   "ffn.fc2.weight"):
             assert f"layers.{l}.{k}" in names
     assert {"embed.weight", "ln_final.weight", "lm_head.weight"} <= names
+
+
+@pytest.mark.parametrize("dtype", [F.DT_Q8_0, F.DT_Q4_0])
+def test_reencoding_decoded_blocks_is_lossless(dtype):
+    """Weights that reach the engine as f32 after the GGUF converter decoded
+    them (convert_gguf.py:233-263) re-encode to the identical blocks, so the
+    device model built from a WeightMap holds exactly the file's weights."""
+    x = F.normal(9, "reenc", 32 * 512, 0.05)
+    x[:32] = 0.0
+    blocks = F.quantize(x, dtype)
+    dec = F.dequantize(blocks, dtype, x.size)
+    assert np.array_equal(F.quantize(dec, dtype), blocks)

@@ -31,3 +31,12 @@ def test_rope_bit_exact(ctx, orc, T, n_heads, d_head, pos, max_seq):
     tabs = orc.rope_tables(max_seq, d_head, 10000.0)
     ref = orc.rope_apply(x, n_heads, d_head, pos, tabs, max_seq)
     assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+
+
+def test_device_copy_roundtrip(ctx):
+    """vlrf_hip_d2d: a device-to-device copy returns the bytes unchanged."""
+    a = np.arange(1 << 20, dtype=np.int32) * 7 - 5
+    src, dst = ctx.to_device(a), ctx.alloc(a.nbytes)
+    dst.copy_from(src)
+    ctx.sync()
+    assert np.array_equal(dst.download(a.shape, np.int32), a)

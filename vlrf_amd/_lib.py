@@ -39,6 +39,7 @@ _SIGS = {
     "vlrf_hip_h2d": (i32, [vp, vp, vp, sz]),
     "vlrf_hip_d2h": (i32, [vp, vp, vp, sz]),
     "vlrf_hip_memset": (i32, [vp, vp, i32, sz]),
+    "vlrf_hip_d2d": (i32, [vp, vp, vp, sz]),
     "vlrf_hip_timer_start": (i32, [vp]),
     "vlrf_hip_timer_stop": (i32, [vp, C.POINTER(f32)]),
     "vlrf_hip_attn_f32": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, i32, f32, i32]),

@@ -287,6 +287,14 @@ int vlrf_hip_d2h(vlrf_hip_ctx_t ctx, void* dst, const void* src, size_t bytes) {
     return VLRF_HIP_OK;
 }
 
+int vlrf_hip_d2d(vlrf_hip_ctx_t ctx, void* dst, const void* src, size_t bytes) {
+    VH_CTX(ctx);
+    if (!bytes) return VLRF_HIP_OK;
+    VH_ARG(dst && src, "d2d: null pointer");
+    VH_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, ctx->stream));
+    return VLRF_HIP_OK;
+}
+
 int vlrf_hip_memset(vlrf_hip_ctx_t ctx, void* dst, int value, size_t bytes) {
     VH_CTX(ctx);
     if (!bytes) return VLRF_HIP_OK;

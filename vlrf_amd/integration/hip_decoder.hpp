@@ -1,7 +1,7 @@
 // hip_decoder.hpp - device-resident greedy decode for a VLRF TransformerModel.
 //
 // Drop-in location in the engine tree: include/model/hip_decoder.hpp, used by
-// the C API / CLI when the HIP backend is active (INTEGRATION.md).  It builds a
+// the C API / CLI when the HIP backend is active.  It builds a
 // vlrf_hip_model from the engine's ModelConfig and WeightMap (reference
 // include/model/config.hpp, weights.hpp) and reproduces the greedy path of
 // TransformerModel::generate (transformer.hpp:439-547): reset the KV cache,

@@ -41,6 +41,12 @@ class DeviceBuffer:
     def zero(self):
         check(lib().vlrf_hip_memset(self.ctx.h, self.ptr, 0, self.nbytes))
 
+    def copy_from(self, src, nbytes=None):
+        """Device-to-device copy from another DeviceBuffer (queued, no wait)."""
+        n = src.nbytes if nbytes is None else nbytes
+        assert n <= self.nbytes and n <= src.nbytes, "copy larger than a buffer"
+        check(lib().vlrf_hip_d2d(self.ctx.h, self.ptr, src.ptr, n))
+
     def free(self):
         if self.ptr:
             check(lib().vlrf_hip_free(self.ctx.h, self.ptr))
