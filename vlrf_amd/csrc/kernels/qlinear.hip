@@ -202,9 +202,14 @@ __device__ __forceinline__ float ub(uint32_t v, int k) { return (float)((v >> (8
 template <int NM, int RPW, int NC>
 struct GemvRegs {
     uint4 w[NM][RPW][NC];
-    float s[NM][RPW][NC];
+    uint32_t s[NM][RPW][NC];      // raw f16 scale bits, converted at use
 };
 
+// Branch-free loads: a lane whose (row, chunk) lies outside the matrix reads
+// the first 16 bytes and the first scale of the matrix instead (always in
+// bounds) and gemv_compute gives it a zero scale.  A load inside a bounds
+// branch would be followed by a wait for its result at the end of the branch,
+// and since loads return in issue order that wait would serialise the stream.
 template <int WT, int NM, int RPW, int NC>
 __device__ __forceinline__ void gemv_load(GemvRegs<NM, RPW, NC>& R, const uint8_t* __restrict__ qa,
                                           const __half* __restrict__ da, const uint8_t* __restrict__ qb,
@@ -217,20 +222,18 @@ __device__ __forceinline__ void gemv_load(GemvRegs<NM, RPW, NC>& R, const uint8_
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
         const uint8_t* q = m ? qb : qa;
-        const __half* d = m ? db : da;
+        const uint16_t* d = reinterpret_cast<const uint16_t*>(m ? db : da);
 #pragma unroll
         for (int r = 0; r < RPW; ++r) {
             const int row = row0 + r;
 #pragma unroll
             for (int c = 0; c < NC; ++c) {
                 const int e0 = c * CW + lane * EPL;
-                if (row < N && e0 < K) {
-                    R.w[m][r][c] = *reinterpret_cast<const uint4*>(q + (size_t)row * qrow + (size_t)c * 1024 + lane * 16);
-                    R.s[m][r][c] = __half2float(d[(size_t)row * kb + e0 / 32]);
-                } else {
-                    R.w[m][r][c] = make_uint4(0, 0, 0, 0);
-                    R.s[m][r][c] = 0.f;
-                }
+                const bool in = row < N && e0 < K;
+                const size_t qo = in ? (size_t)row * qrow + (size_t)c * 1024 + lane * 16 : 0;
+                const size_t so = in ? (size_t)row * kb + e0 / 32 : 0;
+                R.w[m][r][c] = *reinterpret_cast<const uint4*>(q + qo);
+                R.s[m][r][c] = d[so];
             }
         }
     }
@@ -238,7 +241,7 @@ __device__ __forceinline__ void gemv_load(GemvRegs<NM, RPW, NC>& R, const uint8_
 
 template <int WT, int NM, int RPW, int NC, bool SWIGLU>
 __device__ __forceinline__ void gemv_compute(const GemvRegs<NM, RPW, NC>& R, const float4* xs4,
-                                             const float (&xsum)[NC], int row0, int N, int lane,
+                                             const float (&xsum)[NC], int row0, int N, int K, int lane,
                                              const float* residual, float* y) {
     constexpr int EPL = Gemv<WT>::EPL;
     float acc[NM][RPW];
@@ -279,7 +282,9 @@ __device__ __forceinline__ void gemv_compute(const GemvRegs<NM, RPW, NC>& R, con
                         }
                     }
                 }
-                acc[m][r] = fmaf(R.s[m][r][c], p - xsum[c], acc[m][r]);
+                const bool in = row0 + r < N && c * (64 * EPL) + lane * EPL < K;
+                const float sc = in ? __half2float(__ushort_as_half((unsigned short)R.s[m][r][c])) : 0.f;
+                acc[m][r] = fmaf(sc, p - xsum[c], acc[m][r]);
             }
     }
 #pragma unroll
@@ -317,23 +322,40 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(
     int row0 = (blockIdx.x * kGemvWaves + wave) * RPW;
     const int rstep = nwaves * RPW;
 
-    // The first two row groups of this wave are requested before anything else.
-    GemvRegs<NM, RPW, NC> A, B;
-    if (row0 < N) gemv_load<WT, NM, RPW, NC>(A, qa, da, qb, db, row0, N, K, lane);
-    if (row0 + rstep < N) gemv_load<WT, NM, RPW, NC>(B, qa, da, qb, db, row0 + rstep, N, K, lane);
-
     // x_row: x is row *x_row of a table (the embedding gather of the first
     // layer, ops.hpp:615-626); workgroup 0 copies the raw row to x_copy.
     const float* xr = x_row ? x + (size_t)(*x_row) * K : x;
 
-    // Stage x (optionally RMS-normalised, ops.hpp:488-498) in the lane-interleaved layout.
-    float4 v[PER];
-    float ss = 0.f;
+    // Vector loads return in issue order, so the activations and the norm
+    // weight are requested first: the staging below then overlaps the weight
+    // stream instead of waiting behind it.
+    float4 v[PER], gw[PER];
 #pragma unroll
     for (int p = 0; p < PER; ++p) {
         const int f = tid + p * NT;            // float4 index in x
-        v[p] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (f < XF4 && 4 * f < K) v[p] = reinterpret_cast<const float4*>(xr)[f];
+        const bool in = f < XF4 && 4 * f < K;
+        const float4 t = reinterpret_cast<const float4*>(xr)[in ? f : 0];
+        v[p] = in ? t : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    if (norm_w) {
+#pragma unroll
+        for (int p = 0; p < PER; ++p) {
+            const int f = tid + p * NT;
+            gw[p] = reinterpret_cast<const float4*>(norm_w)[(f < XF4 && 4 * f < K) ? f : 0];
+        }
+    }
+
+    // Then the first two row groups of this wave, unconditionally (rows past N
+    // read in-bounds dummies), so that the wait for x above stays exact.
+    GemvRegs<NM, RPW, NC> A, B;
+    gemv_load<WT, NM, RPW, NC>(A, qa, da, qb, db, row0, N, K, lane);
+    gemv_load<WT, NM, RPW, NC>(B, qa, da, qb, db, row0 + rstep, N, K, lane);
+
+    // Stage x (optionally RMS-normalised, ops.hpp:488-498) in the lane-interleaved layout.
+    float ss = 0.f;
+#pragma unroll
+    for (int p = 0; p < PER; ++p) {
+        const int f = tid + p * NT;
         ss += v[p].x * v[p].x + v[p].y * v[p].y + v[p].z * v[p].z + v[p].w * v[p].w;
         if (x_copy && blockIdx.x == 0 && f < XF4 && 4 * f < K) reinterpret_cast<float4*>(x_copy)[f] = v[p];
     }
@@ -353,7 +375,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(
         if (f < XF4) {
             float4 o = v[p];
             if (norm_w && 4 * f < K) {
-                const float4 g = reinterpret_cast<const float4*>(norm_w)[f];
+                const float4 g = gw[p];
                 o.x = o.x * inv * g.x; o.y = o.y * inv * g.y;
                 o.z = o.z * inv * g.z; o.w = o.w * inv * g.w;
             }
@@ -374,15 +396,16 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(
         xsum[c] = sacc * Gemv<WT>::BIAS;
     }
 
+    // Loads stay unconditional inside the loop as well (see gemv_load).
     for (; row0 < N; row0 += 2 * rstep) {
         const int r1 = row0 + rstep;
-        gemv_compute<WT, NM, RPW, NC, SWIGLU>(A, xs4, xsum, row0, N, lane, residual, y);
-        const int r2 = r1 + rstep;
-        if (r2 < N) gemv_load<WT, NM, RPW, NC>(A, qa, da, qb, db, r2, N, K, lane);
+        gemv_compute<WT, NM, RPW, NC, SWIGLU>(A, xs4, xsum, row0, N, K, lane, residual, y);
         if (r1 >= N) break;
-        gemv_compute<WT, NM, RPW, NC, SWIGLU>(B, xs4, xsum, r1, N, lane, residual, y);
-        const int r3 = r2 + rstep;
-        if (r3 < N) gemv_load<WT, NM, RPW, NC>(B, qa, da, qb, db, r3, N, K, lane);
+        const int r2 = r1 + rstep;
+        gemv_load<WT, NM, RPW, NC>(A, qa, da, qb, db, r2, N, K, lane);
+        gemv_compute<WT, NM, RPW, NC, SWIGLU>(B, xs4, xsum, r1, N, K, lane, residual, y);
+        if (r2 >= N) break;
+        gemv_load<WT, NM, RPW, NC>(B, qa, da, qb, db, r2 + rstep, N, K, lane);
     }
 }
 
