@@ -117,6 +117,21 @@ void check_gemm(HipBackend const& be) {
         std::snprintf(name, sizeof(name), "gemm x.W^T M=%d K=%d N=%d", M, K, N);
         report(e <= 1e-3, name, e);
     }
+    // Weights freed between calls: a new tensor may reuse the old one's
+    // address, and must not hit the device copy of the old weight.
+    double worst = 0;
+    for (int i = 0; i < 3; ++i) {
+        Tensor A = normal_tensor({4, 512}, stream++, 1.f);
+        Tensor C({4, 96}), R({4, 96});
+        {
+            Tensor B = normal_tensor({96, 512}, stream++, 0.02f);
+            be.gemm(A, B, C, 1.f, 0.f, false, true);
+            cpu.gemm(A, B, R, 1.f, 0.f, false, true);
+        }
+        std::vector<double> ref(R.data_ptr(), R.data_ptr() + R.numel());
+        worst = std::fmax(worst, rel_err(C.data_ptr(), ref));
+    }
+    report(worst <= 1e-3, "gemm with a fresh weight tensor per call", worst);
 }
 
 // Q8_0 round trip so the reference runs on exactly the weights the device holds.

@@ -8,14 +8,17 @@
 // (attention.hpp:171) and attends over the dequantized cache including the
 // token just appended (attention.hpp:127-145).
 //
-// Decode design (gfx950): split-K over the context.  A workgroup owns one KV
-// head and a 256-token chunk, so each K/V byte is loaded and dequantized once
-// and reused by all REP query heads of the GQA group.  Phase 1: thread t
-// scores token c0+t against the REP queries (LDS broadcast reads of q).
-// Phase 2: per-head chunk max / sum with DPP + shuffle wave reductions.
-// Phase 3: P.V with lanes along d_head (coalesced 64 B rows per token),
-// reduced across waves in LDS.  Partials (m, l, acc[d]) per (head, chunk) are
-// merged by a small combine kernel with the log-sum-exp rescale.
+// Decode design (gfx950): split-K over the context.  A 256-lane workgroup owns
+// one KV head and a 64-token chunk, so each K/V byte is loaded and dequantized
+// once and reused by all REP query heads of the GQA group.  Phase 1: lane t of
+// wave w scores token c0+t over dimension quarter w against the REP queries
+// (LDS broadcast reads of q); the quarters are summed in LDS.  Phase 2:
+// per-head chunk max / sum with DPP + shuffle wave reductions.  Phase 3: P.V
+// with lanes along d_head (coalesced rows per token), reduced across waves in
+// LDS.  Partials (m, l, acc[d]) per (head, chunk) are merged by a combine
+// kernel with the log-sum-exp rescale.  With a device-side position the
+// kernel also applies RoPE to q and to the new k and quantizes + stores the
+// new K/V row before attending (the decode step's fused form).
 #include "../internal.hpp"
 
 #include <cmath>
@@ -87,108 +90,129 @@ __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
     const int nt = min(kChunk, ctx - c0);       // valid tokens of the chunk
     const bool has_new = FUSED && pos >= c0 && pos < c0 + kChunk;
 
-    // ---- loads first: this thread's K slice (token lane, dims of this wave) and
-    // its V words (tokens wave*16 + t4 + 4i, dims 4dg..) -------------------------
-    const int t4 = lane >> 4, dg = lane & 15;
-    float kv[DQ];
-    float vv[4][DL][4];
-    float ksc = 0.f, vsc[4];
-    {
-        const int jt = c0 + lane;
-        const bool ok = lane < nt && !(has_new && jt == pos);
+    // Vector loads complete in issue order, so the small L2-resident operands
+    // (queries, RoPE tables, the new K/V row) are requested first, then the
+    // cache stream, and every load is branch-free (out-of-range tokens read
+    // row c0, which is in bounds, and are masked where they are used): a load
+    // in a branch, or a value converted right after its load, would make the
+    // wave wait for the whole stream early.
+    constexpr int PAIRS = REP * HALF, PPT = (PAIRS + 255) / 256;
+    const bool rot = FUSED && pos < fz.max_seq;   // rope.hpp:84: positions >= max_seq stay unrotated
+    float qlo[PPT], qhi[PPT];
 #pragma unroll
-        for (int i = 0; i < DQ; i += 16) {
-            if constexpr (Q8) {
-                uint4 u = make_uint4(0, 0, 0, 0);
-                if (ok) u = *reinterpret_cast<const uint4*>(kq + hb + (size_t)jt * D + wave * DQ + i);
-                const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+    for (int p = 0; p < PPT; ++p) {
+        const int i = min(tid + 256 * p, PAIRS - 1), h = i / HALF, j = i - h * HALF;
+        const float* qh = q + (size_t)(g * REP + h) * D;
+        qlo[p] = qh[j];
+        qhi[p] = qh[j + HALF];
+    }
+    float cw = 1.f, sw = 0.f;
+    if (rot) {
+        cw = fz.cos_t[(size_t)pos * HALF + (tid & (HALF - 1))];
+        sw = fz.sin_t[(size_t)pos * HALF + (tid & (HALF - 1))];
+    }
+    constexpr int NPT = FUSED ? 4 : 1;            // new-row floats per thread (row <= 1024)
+    float kn[NPT], vn[NPT];
+    if constexpr (FUSED) {
+        const int row = fz.n_kv * D;
 #pragma unroll
-                for (int k = 0; k < 16; ++k) kv[i + k] = (float)(int8_t)(w[k >> 2] >> (8 * (k & 3)));
-            } else {
-#pragma unroll
-                for (int k = 0; k < 16; k += 4) {
-                    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-                    if (ok) v = *reinterpret_cast<const float4*>(kf + hb + (size_t)jt * D + wave * DQ + i + k);
-                    kv[i + k] = v.x; kv[i + k + 1] = v.y; kv[i + k + 2] = v.z; kv[i + k + 3] = v.w;
-                }
-            }
+        for (int p = 0; p < NPT; ++p) {
+            const int i = min(tid + 256 * p, row - 1);
+            kn[p] = fz.k_new[i];
+            vn[p] = fz.v_new[i];
         }
-        if (Q8 && ok) ksc = ks[jt];
+    }
+
+    // The cache stream: this thread's K slice (token lane, dims of this wave)
+    // and its V words (tokens wave*16 + t4 + 4i, dims 4dg..), kept as raw codes.
+    const int t4 = lane >> 4, dg = lane & 15;
+    constexpr int KW = Q8 ? DQ / 16 : DQ / 4;      // 16-byte words of the K slice
+    uint4 kraw[KW];
+    uint4 vraw[4][DL];                             // Q8: .x holds 4 codes; f32: 4 floats
+    float ksc = 1.f, vsc[4] = {1.f, 1.f, 1.f, 1.f};
+    {
+        const int jt = lane < nt ? c0 + lane : c0;
+#pragma unroll
+        for (int i = 0; i < KW; ++i) {
+            if constexpr (Q8)
+                kraw[i] = *reinterpret_cast<const uint4*>(kq + hb + (size_t)jt * D + wave * DQ + 16 * i);
+            else
+                kraw[i] = *reinterpret_cast<const uint4*>(kf + hb + (size_t)jt * D + wave * DQ + 4 * i);
+        }
+        if constexpr (Q8) ksc = ks[jt];
 #pragma unroll
         for (int it = 0; it < 4; ++it) {
             const int t = wave * 16 + t4 + 4 * it;
-            const int jj = c0 + t;
-            const bool okv = t < nt && !(has_new && jj == pos);
-            vsc[it] = (Q8 && okv) ? vs[jj] : 0.f;
+            const int jj = t < nt ? c0 + t : c0;
+            if constexpr (Q8) vsc[it] = vs[jj];
 #pragma unroll
             for (int dl = 0; dl < DL; ++dl) {
                 if constexpr (Q8) {
-                    uint32_t u = 0;
-                    if (okv) u = *reinterpret_cast<const uint32_t*>(vq + hb + (size_t)jj * D + dl * 64 + dg * 4);
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) vv[it][dl][k] = (float)(int8_t)(u >> (8 * k));
+                    vraw[it][dl].x = *reinterpret_cast<const uint32_t*>(vq + hb + (size_t)jj * D + dl * 64 + dg * 4);
                 } else {
-                    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-                    if (okv) v = *reinterpret_cast<const float4*>(vf + hb + (size_t)jj * D + dl * 64 + dg * 4);
-                    vv[it][dl][0] = v.x; vv[it][dl][1] = v.y; vv[it][dl][2] = v.z; vv[it][dl][3] = v.w;
+                    vraw[it][dl] = *reinterpret_cast<const uint4*>(vf + hb + (size_t)jj * D + dl * 64 + dg * 4);
                 }
             }
         }
     }
 
     // ---- queries of the GQA group (RoPE at the device position when fused) -------
-    if (FUSED && pos < fz.max_seq) {   // rope.hpp:84: positions >= max_seq stay unrotated
-        const float* cs = fz.cos_t + (size_t)pos * HALF;
-        const float* sn = fz.sin_t + (size_t)pos * HALF;
-        for (int i = tid; i < REP * HALF; i += 256) {
-            const int h = i / HALF, j = i - h * HALF;
-            const float* qh = q + (size_t)(g * REP + h) * D;
-            rope2(qh[j], qh[j + HALF], cs[j], sn[j], &qs[h][j], &qs[h][j + HALF]);
+    {
+        float* cst = sp4[0][0];                    // RoPE table row, staged before phase 1 reuses sp4
+        if (rot && tid < HALF) { cst[tid] = cw; cst[HALF + tid] = sw; }
+        __syncthreads();
+#pragma unroll
+        for (int p = 0; p < PPT; ++p) {
+            const int i = tid + 256 * p;
+            if (i < PAIRS) {
+                const int h = i / HALF, j = i - h * HALF;
+                if (rot) rope2(qlo[p], qhi[p], cst[j], cst[HALF + j], &qs[h][j], &qs[h][j + HALF]);
+                else { qs[h][j] = qlo[p]; qs[h][j + HALF] = qhi[p]; }
+            }
         }
-    } else {
-        for (int i = tid; i < REP * D; i += 256) qs[i / D][i % D] = q[(size_t)(g * REP) * D + i];
-    }
-
-    // ---- decode fusion: the current token's K/V row --------------------------------
-    // attention.hpp:109-128: RoPE on k, then KVCache::append quantizes the whole
-    // row (quantize_row_q8_0, kv_cache.hpp:102-117) before attention reads it.
-    // Every chunk holding `pos` quantizes the row itself and uses the dequantized
-    // values for that token; the workgroup of KV head g stores head g's codes,
-    // KV head 0 stores the row scales.
-    if constexpr (FUSED) {
-        if (has_new) {
-            const int row = fz.n_kv * D;
-            for (int i = tid; i < row; i += 256) { krow[i] = fz.k_new[i]; vrow[i] = fz.v_new[i]; }
-            __syncthreads();
-            if (pos < fz.max_seq) {
-                const float* cs = fz.cos_t + (size_t)pos * HALF;
-                const float* sn = fz.sin_t + (size_t)pos * HALF;
-                for (int i = tid; i < fz.n_kv * HALF; i += 256) {
-                    const int h = i / HALF, j = i - h * HALF;
-                    float* kh = krow + h * D;
-                    const float x0 = kh[j], x1 = kh[j + HALF];
-                    rope2(x0, x1, cs[j], sn[j], &kh[j], &kh[j + HALF]);
+        // ---- decode fusion: the current token's K/V row ----------------------------
+        // attention.hpp:109-128: RoPE on k, then KVCache::append quantizes the whole
+        // row (quantize_row_q8_0, kv_cache.hpp:102-117) before attention reads it.
+        // Every chunk holding `pos` quantizes the row itself and uses the dequantized
+        // values for that token; the workgroup of KV head g stores head g's codes,
+        // KV head 0 stores the row scales.
+        if constexpr (FUSED) {
+            if (has_new) {
+                const int row = fz.n_kv * D;
+#pragma unroll
+                for (int p = 0; p < NPT; ++p) {
+                    const int i = tid + 256 * p;
+                    if (i < row) { krow[i] = kn[p]; vrow[i] = vn[p]; }
                 }
+                __syncthreads();
+                if (rot) {
+                    for (int i = tid; i < fz.n_kv * HALF; i += 256) {
+                        const int h = i / HALF, j = i - h * HALF;
+                        float* kh = krow + h * D;
+                        const float x0 = kh[j], x1 = kh[j + HALF];
+                        rope2(x0, x1, cst[j], cst[HALF + j], &kh[j], &kh[j + HALF]);
+                    }
+                }
+                __syncthreads();
+                float ak = 0.f, av = 0.f;
+                for (int i = tid; i < row; i += 256) { ak = fmaxf(ak, fabsf(krow[i])); av = fmaxf(av, fabsf(vrow[i])); }
+                ak = block_max256(ak, rmax);
+                av = block_max256(av, rmax);
+                const float sk = ak != 0.f ? ak / 127.f : 0.f, sv = av != 0.f ? av / 127.f : 0.f;
+                const float ik = ak != 0.f ? 1.f / sk : 0.f, iv = av != 0.f ? 1.f / sv : 0.f;
+                for (int i = tid; i < D; i += 256) {
+                    const int a = ak != 0.f ? min(127, max(-127, (int)roundf(krow[g * D + i] * ik))) : 0;
+                    const int b = av != 0.f ? min(127, max(-127, (int)roundf(vrow[g * D + i] * iv))) : 0;
+                    newk[i] = (float)a * sk;
+                    newv[i] = (float)b * sv;
+                    fz.kq_w[hb + (size_t)pos * D + i] = (int8_t)a;
+                    fz.vq_w[hb + (size_t)pos * D + i] = (int8_t)b;
+                }
+                if (g == 0 && tid == 0) { fz.ks_w[pos] = sk; fz.vs_w[pos] = sv; }
             }
-            __syncthreads();
-            float ak = 0.f, av = 0.f;
-            for (int i = tid; i < row; i += 256) { ak = fmaxf(ak, fabsf(krow[i])); av = fmaxf(av, fabsf(vrow[i])); }
-            ak = block_max256(ak, rmax);
-            av = block_max256(av, rmax);
-            const float sk = ak != 0.f ? ak / 127.f : 0.f, sv = av != 0.f ? av / 127.f : 0.f;
-            const float ik = ak != 0.f ? 1.f / sk : 0.f, iv = av != 0.f ? 1.f / sv : 0.f;
-            for (int i = tid; i < D; i += 256) {
-                const int a = ak != 0.f ? min(127, max(-127, (int)roundf(krow[g * D + i] * ik))) : 0;
-                const int b = av != 0.f ? min(127, max(-127, (int)roundf(vrow[g * D + i] * iv))) : 0;
-                newk[i] = (float)a * sk;
-                newv[i] = (float)b * sv;
-                fz.kq_w[hb + (size_t)pos * D + i] = (int8_t)a;
-                fz.vq_w[hb + (size_t)pos * D + i] = (int8_t)b;
-            }
-            if (g == 0 && tid == 0) { fz.ks_w[pos] = sk; fz.vs_w[pos] = sv; }
         }
+        __syncthreads();
     }
-    __syncthreads();
 
     // ---- phase 1: partial scores over this wave's quarter of d_head --------------
     {
@@ -198,7 +222,17 @@ __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
             for (int i = 0; i < DQ; ++i) kd[i] = newk[wave * DQ + i];
         } else {
 #pragma unroll
-            for (int i = 0; i < DQ; ++i) kd[i] = Q8 ? kv[i] * ksc : kv[i];   // dequantize_row_q8_0
+            for (int i = 0; i < KW; ++i) {
+                const uint32_t w[4] = {kraw[i].x, kraw[i].y, kraw[i].z, kraw[i].w};
+                if constexpr (Q8) {
+#pragma unroll
+                    for (int k = 0; k < 16; ++k)   // dequantize_row_q8_0
+                        kd[16 * i + k] = (float)(int8_t)(w[k >> 2] >> (8 * (k & 3))) * ksc;
+                } else {
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) kd[4 * i + k] = __uint_as_float(w[k]);
+                }
+            }
         }
 #pragma unroll
         for (int h = 0; h < REP; ++h) {
@@ -245,9 +279,16 @@ __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
                     for (int k = 0; k < 4; ++k) vd[dl][k] = newv[dl * 64 + dg * 4 + k];
             } else {
 #pragma unroll
-                for (int dl = 0; dl < DL; ++dl)
+                for (int dl = 0; dl < DL; ++dl) {
+                    if constexpr (Q8) {
 #pragma unroll
-                    for (int k = 0; k < 4; ++k) vd[dl][k] = Q8 ? vv[it][dl][k] * vsc[it] : vv[it][dl][k];
+                        for (int k = 0; k < 4; ++k)
+                            vd[dl][k] = (float)(int8_t)(vraw[it][dl].x >> (8 * k)) * vsc[it];
+                    } else {
+                        vd[dl][0] = __uint_as_float(vraw[it][dl].x); vd[dl][1] = __uint_as_float(vraw[it][dl].y);
+                        vd[dl][2] = __uint_as_float(vraw[it][dl].z); vd[dl][3] = __uint_as_float(vraw[it][dl].w);
+                    }
+                }
             }
 #pragma unroll
             for (int h = 0; h < REP; ++h) {
@@ -282,33 +323,69 @@ __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
     }
 }
 
-// Log-sum-exp merge of the per-chunk partials of one query head.  The chunk
-// maxima and sums are staged in LDS; the accumulators are read with the loop
-// unrolled so that their loads are in flight together.
+// Log-sum-exp merge of the per-chunk partials of one query head.  The 256
+// threads form G = 256/D groups of D lanes (one lane per dimension); group gi
+// merges splits gi, gi+G, ... in passes of B splits whose loads are all issued
+// before any is used (index clamped, masked afterwards), then the G group
+// results are merged through LDS.
 template <int D>
-__global__ __launch_bounds__(D) void attn_combine_kernel(const float* __restrict__ part, int n_splits,
-                                                         float* __restrict__ out) {
-    __shared__ float pm[kMaxSplits], pl[kMaxSplits];
-    const int h = blockIdx.x, d = threadIdx.x;
+__global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restrict__ part, int n_splits,
+                                                           float* __restrict__ out) {
+    constexpr int G = 256 / D, B = 16;
+    __shared__ float sm[G][D], sl[G][D], so[G][D];
+    const int h = blockIdx.x, gi = threadIdx.x / D, d = threadIdx.x - gi * D;
     const float* p = part + (size_t)h * n_splits * (D + 2);
-    for (int s = d; s < n_splits; s += D) {
-        pm[s] = p[(size_t)s * (D + 2) + D];
-        pl[s] = p[(size_t)s * (D + 2) + D + 1];
-    }
-    __syncthreads();
-    float M = kNegInf;
-    for (int s = 0; s < n_splits; ++s) M = fmaxf(M, pm[s]);
-    float L = 0.f, o = 0.f;
-    if (M != kNegInf) {
-#pragma unroll 8
-        for (int s = 0; s < n_splits; ++s) {
-            const float ms = pm[s];
-            const float w = ms == kNegInf ? 0.f : expf(ms - M);
-            L += w * pl[s];
-            o += w * p[(size_t)s * (D + 2) + d];
+    float M = kNegInf, L = 0.f, o = 0.f;
+    for (int s0 = gi; s0 < n_splits; s0 += G * B) {
+        float pm[B], pl[B], po[B];
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            const float* ps = p + (size_t)min(s0 + b * G, n_splits - 1) * (D + 2);
+            pm[b] = ps[D];
+            pl[b] = ps[D + 1];
+            po[b] = ps[d];
+        }
+        float mb = kNegInf;
+#pragma unroll
+        for (int b = 0; b < B; ++b)
+            if (s0 + b * G < n_splits) mb = fmaxf(mb, pm[b]);
+        const float mn = fmaxf(M, mb);
+        if (mn != kNegInf) {
+            const float c = M == kNegInf ? 0.f : expf(M - mn);
+            L *= c;
+            o *= c;
+#pragma unroll
+            for (int b = 0; b < B; ++b) {
+                if (s0 + b * G < n_splits && pm[b] != kNegInf) {
+                    const float w = expf(pm[b] - mn);
+                    L += w * pl[b];
+                    o += w * po[b];
+                }
+            }
+            M = mn;
         }
     }
-    out[(size_t)h * D + d] = (L > 0.f) ? o * (1.f / L) : 0.f;
+    sm[gi][d] = M;
+    sl[gi][d] = L;
+    so[gi][d] = o;
+    __syncthreads();
+    if (gi == 0) {
+        float mt = kNegInf;
+#pragma unroll
+        for (int k = 0; k < G; ++k) mt = fmaxf(mt, sm[k][d]);
+        float lt = 0.f, ot = 0.f;
+        if (mt != kNegInf) {
+#pragma unroll
+            for (int k = 0; k < G; ++k) {
+                if (sm[k][d] != kNegInf) {
+                    const float w = expf(sm[k][d] - mt);
+                    lt += w * sl[k][d];
+                    ot += w * so[k][d];
+                }
+            }
+        }
+        out[(size_t)h * D + d] = (lt > 0.f) ? ot * (1.f / lt) : 0.f;
+    }
 }
 
 // ---- general f32 attention: one thread per query row, 64x64 tiles --------------
@@ -443,9 +520,9 @@ int launch_attn_decode(hipStream_t s, const float* q, const int8_t* kq, const in
 #undef VH_AD
     VH_LAUNCHED();
     if (d_head == 64)
-        hipLaunchKernelGGL((attn_combine_kernel<64>), dim3(n_heads), dim3(64), 0, s, part, n_splits, out);
+        hipLaunchKernelGGL((attn_combine_kernel<64>), dim3(n_heads), dim3(256), 0, s, part, n_splits, out);
     else
-        hipLaunchKernelGGL((attn_combine_kernel<128>), dim3(n_heads), dim3(128), 0, s, part, n_splits, out);
+        hipLaunchKernelGGL((attn_combine_kernel<128>), dim3(n_heads), dim3(256), 0, s, part, n_splits, out);
     VH_LAUNCHED();
     return VLRF_HIP_OK;
 }

@@ -302,6 +302,11 @@ __device__ __forceinline__ void gemv_compute(const GemvRegs<NM, RPW, NC>& R, con
     }
 }
 
+// The activation row: x itself, or row *x_row of the table x.
+__device__ __forceinline__ const float* xr_src(const float* x, const int* x_row, int K) {
+    return x_row ? x + (size_t)(*x_row) * K : x;
+}
+
 template <int WT, int NC, int RPW, bool SWIGLU>
 __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(
     const uint8_t* __restrict__ qa, const __half* __restrict__ da, const uint8_t* __restrict__ qb,
@@ -324,76 +329,78 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(
 
     // x_row: x is row *x_row of a table (the embedding gather of the first
     // layer, ops.hpp:615-626); workgroup 0 copies the raw row to x_copy.
-    const float* xr = x_row ? x + (size_t)(*x_row) * K : x;
-
+    //
     // Vector loads return in issue order, so the activations and the norm
     // weight are requested first: the staging below then overlaps the weight
-    // stream instead of waiting behind it.
-    float4 v[PER], gw[PER];
+    // stream instead of waiting behind it.  (Loading each wave's slice of x
+    // into registers instead of staging it once per workgroup was measured
+    // slower: 16 waves per CU re-reading x and the norm weight cost more L1
+    // bandwidth than the two barriers.)
+    float xsum[NC];
+    GemvRegs<NM, RPW, NC> A, B;
+    {
+        const float* xs = xr_src(x, x_row, K);
+        float4 v[PER], gw[PER];
 #pragma unroll
-    for (int p = 0; p < PER; ++p) {
-        const int f = tid + p * NT;            // float4 index in x
-        const bool in = f < XF4 && 4 * f < K;
-        const float4 t = reinterpret_cast<const float4*>(xr)[in ? f : 0];
-        v[p] = in ? t : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-    if (norm_w) {
+        for (int p = 0; p < PER; ++p) {
+            const int f = tid + p * NT;            // float4 index in x
+            const bool in = f < XF4 && 4 * f < K;
+            const float4 t = reinterpret_cast<const float4*>(xs)[in ? f : 0];
+            v[p] = in ? t : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        if (norm_w) {
+#pragma unroll
+            for (int p = 0; p < PER; ++p) {
+                const int f = tid + p * NT;
+                gw[p] = reinterpret_cast<const float4*>(norm_w)[(f < XF4 && 4 * f < K) ? f : 0];
+            }
+        }
+        gemv_load<WT, NM, RPW, NC>(A, qa, da, qb, db, row0, N, K, lane);
+        gemv_load<WT, NM, RPW, NC>(B, qa, da, qb, db, row0 + rstep, N, K, lane);
+
+        // Stage x (optionally RMS-normalised, ops.hpp:488-498) in the lane-interleaved layout.
+        float ss = 0.f;
 #pragma unroll
         for (int p = 0; p < PER; ++p) {
             const int f = tid + p * NT;
-            gw[p] = reinterpret_cast<const float4*>(norm_w)[(f < XF4 && 4 * f < K) ? f : 0];
+            ss += v[p].x * v[p].x + v[p].y * v[p].y + v[p].z * v[p].z + v[p].w * v[p].w;
+            if (x_copy && blockIdx.x == 0 && f < XF4 && 4 * f < K) reinterpret_cast<float4*>(x_copy)[f] = v[p];
         }
-    }
-
-    // Then the first two row groups of this wave, unconditionally (rows past N
-    // read in-bounds dummies), so that the wait for x above stays exact.
-    GemvRegs<NM, RPW, NC> A, B;
-    gemv_load<WT, NM, RPW, NC>(A, qa, da, qb, db, row0, N, K, lane);
-    gemv_load<WT, NM, RPW, NC>(B, qa, da, qb, db, row0 + rstep, N, K, lane);
-
-    // Stage x (optionally RMS-normalised, ops.hpp:488-498) in the lane-interleaved layout.
-    float ss = 0.f;
+        float inv = 1.f;
+        if (norm_w) {
+            ss = wave_sum(ss);
+            if (lane == 0) red[wave] = ss;
+            __syncthreads();
+            ss = 0.f;
 #pragma unroll
-    for (int p = 0; p < PER; ++p) {
-        const int f = tid + p * NT;
-        ss += v[p].x * v[p].x + v[p].y * v[p].y + v[p].z * v[p].z + v[p].w * v[p].w;
-        if (x_copy && blockIdx.x == 0 && f < XF4 && 4 * f < K) reinterpret_cast<float4*>(x_copy)[f] = v[p];
-    }
-    float inv = 1.f;
-    if (norm_w) {
-        ss = wave_sum(ss);
-        if (lane == 0) red[wave] = ss;
-        __syncthreads();
-        ss = 0.f;
+            for (int w = 0; w < kGemvWaves; ++w) ss += red[w];
+            inv = 1.f / sqrtf(ss / (float)K + eps);
+        }
 #pragma unroll
-        for (int w = 0; w < kGemvWaves; ++w) ss += red[w];
-        inv = 1.f / sqrtf(ss / (float)K + eps);
-    }
-#pragma unroll
-    for (int p = 0; p < PER; ++p) {
-        const int f = tid + p * NT;
-        if (f < XF4) {
-            float4 o = v[p];
-            if (norm_w && 4 * f < K) {
-                const float4 g = gw[p];
-                o.x = o.x * inv * g.x; o.y = o.y * inv * g.y;
-                o.z = o.z * inv * g.z; o.w = o.w * inv * g.w;
+        for (int p = 0; p < PER; ++p) {
+            const int f = tid + p * NT;
+            if (f < XF4) {
+                float4 o = v[p];
+                if (norm_w && 4 * f < K) {
+                    const float4 g = gw[p];
+                    o.x = o.x * inv * g.x; o.y = o.y * inv * g.y;
+                    o.z = o.z * inv * g.z; o.w = o.w * inv * g.w;
+                }
+                const int e = 4 * f, c = e / CW, r = e - c * CW, l = r / EPL, i = (r - l * EPL) / 4;
+                xs4[(c * (EPL / 4) + i) * 64 + l] = o;
             }
-            const int e = 4 * f, c = e / CW, r = e - c * CW, l = r / EPL, i = (r - l * EPL) / 4;
-            xs4[(c * (EPL / 4) + i) * 64 + l] = o;
         }
-    }
-    __syncthreads();
-    float xsum[NC];
+        __syncthreads();
 #pragma unroll
-    for (int c = 0; c < NC; ++c) {
-        float sacc = 0.f;
+        for (int c = 0; c < NC; ++c) {
+            float sacc = 0.f;
 #pragma unroll
-        for (int i = 0; i < EPL / 4; ++i) {
-            const float4 o = xs4[(c * (EPL / 4) + i) * 64 + lane];
-            sacc += (o.x + o.y) + (o.z + o.w);
+            for (int i = 0; i < EPL / 4; ++i) {
+                const float4 o = xs4[(c * (EPL / 4) + i) * 64 + lane];
+                sacc += (o.x + o.y) + (o.z + o.w);
+            }
+            xsum[c] = sacc * Gemv<WT>::BIAS;
         }
-        xsum[c] = sacc * Gemv<WT>::BIAS;
     }
 
     // Loads stay unconditional inside the loop as well (see gemv_load).
@@ -432,7 +439,9 @@ int launch_gemv(hipStream_t s, const DevWeight& a, const DevWeight* b, const flo
     } else if (nc <= 3) {
         VH_GEMV(3, 1);
     } else {
-        VH_GEMV(6, 1);
+        // Q4_0 chunks are 2048 wide, so K <= kGemvMaxK needs at most 3 of them.
+        VH_ARG(WT == VLRF_DT_Q8_0 && nc <= 6, "gemv: K %d too large for the M=1 path", a.K);
+        if constexpr (WT == VLRF_DT_Q8_0) VH_GEMV(6, 1);
     }
 #undef VH_GEMV
     VH_LAUNCHED();

@@ -24,8 +24,10 @@
 #include <cmath>
 #include <cstring>
 #include <limits>
+#include <map>
+#include <memory>
 #include <string>
-#include <unordered_map>
+#include <utility>
 #include <vector>
 
 #ifndef VLRF_HIP_BACKEND_TYPE
@@ -114,21 +116,32 @@ private:
         return true;
     }
 
-    // compute::linear: C[M,N] = A[M,K] . B[N,K]^T with B a weight tensor that
-    // lives as long as the WeightMap; it is uploaded once and reused.
+    // compute::linear: C[M,N] = A[M,K] . B[N,K]^T.  B is usually a weight of
+    // the WeightMap, uploaded once and reused; the cache is keyed by B's
+    // storage and offset, holds a weak reference to the storage (a freed
+    // tensor's address can be reused by a new one) and the shape, as the SYCL
+    // backend's device cache does (sycl_backend.hpp:715-749).  Contents are
+    // taken as immutable while the storage lives, as for every engine weight.
     bool linear_on_device(Tensor const& A, Tensor const& B, Tensor& C) const {
-        if (A.ndim() != 2 || B.ndim() != 2 || C.ndim() != 2) return false;
+        if (A.ndim() != 2 || B.ndim() != 2 || C.ndim() != 2 || !B.storage) return false;
         const int M = A.dim(0), K = A.dim(1), N = B.dim(0);
         if (B.dim(1) != K || C.dim(0) != M || C.dim(1) != N) return false;
         if (M < 1 || M > 16 || K % 32 != 0) return false;
+        const auto key = std::make_pair(static_cast<const void*>(B.storage.get()), B.offset);
+        auto it = wcache_.find(key);
+        if (it != wcache_.end() &&
+            (it->second.owner.expired() || it->second.N != N || it->second.K != K)) {
+            vlrf_hip_weight_free(it->second.w);
+            wcache_.erase(it);
+            it = wcache_.end();
+        }
         vlrf_hip_weight_t w = nullptr;
-        auto it = wcache_.find(B.data_ptr());
         if (it != wcache_.end()) {
-            w = it->second;
+            w = it->second.w;
         } else {
             if (vlrf_hip_weight_upload(ctx_, B.data_ptr(), VLRF_DT_F32, N, K, &w) != VLRF_HIP_OK)
                 return false;
-            wcache_.emplace(B.data_ptr(), w);
+            wcache_.emplace(key, Cached{w, B.storage, N, K});
         }
         const size_t xb = sizeof(float) * (size_t)M * K, yb = sizeof(float) * (size_t)M * N;
         if (!grow(bx_, xb) || !grow(by_, yb)) return false;
@@ -197,7 +210,7 @@ private:
 
     void release() {
         if (!ctx_) return;
-        for (auto& kv : wcache_) vlrf_hip_weight_free(kv.second);
+        for (auto& kv : wcache_) vlrf_hip_weight_free(kv.second.w);
         wcache_.clear();
         for (Buf* b : {&bx_, &by_, &bq_, &bk_, &bv_, &bo_}) {
             if (b->p) vlrf_hip_free(ctx_, b->p);
@@ -211,7 +224,12 @@ private:
     vlrf_hip_ctx_t ctx_ = nullptr;
     std::string info_{"HIP: not initialised"};
     CpuBackend fallback_;
-    mutable std::unordered_map<const float*, vlrf_hip_weight_t> wcache_;
+    struct Cached {
+        vlrf_hip_weight_t w;
+        std::weak_ptr<TensorStorage> owner;
+        int N, K;
+    };
+    mutable std::map<std::pair<const void*, int64_t>, Cached> wcache_;
     mutable Buf bx_, by_, bq_, bk_, bv_, bo_;
 };
 
