@@ -8,17 +8,19 @@
 // (attention.hpp:171) and attends over the dequantized cache including the
 // token just appended (attention.hpp:127-145).
 //
-// Decode design (gfx950): split-K over the context.  A 256-lane workgroup owns
+// Decode design (gfx950): split-K over the context.  A 512-lane workgroup owns
 // one KV head and a 64-token chunk, so each K/V byte is loaded and dequantized
-// once and reused by all REP query heads of the GQA group.  Phase 1: lane t of
-// wave w scores token c0+t over dimension quarter w against the REP queries
-// (LDS broadcast reads of q); the quarters are summed in LDS.  Phase 2:
-// per-head chunk max / sum with DPP + shuffle wave reductions.  Phase 3: P.V
-// with lanes along d_head (coalesced rows per token), reduced across waves in
-// LDS.  Partials (m, l, acc[d]) per (head, chunk) are merged by a combine
-// kernel with the log-sum-exp rescale.  With a device-side position the
-// kernel also applies RoPE to q and to the new k and quantizes + stores the
-// new K/V row before attending (the decode step's fused form).
+// once per workgroup and reused by all REP query heads of the GQA group.
+// Scores: lane t of every wave holds the K row of token c0+t and scores it
+// against REP/8 query heads over the full head dimension (LDS broadcast reads
+// of q); the softmax max and sum are wave reductions (DPP + shuffles), so no
+// workgroup-level reduction is needed.  P.V: the chunk's V rows are staged
+// dequantized in LDS and each thread accumulates its own (head, dim) outputs
+// over the 64 tokens.  Two workgroup barriers in all.  Partials
+// (m, l, acc[d]) per (head, chunk) are merged by a combine kernel with the
+// log-sum-exp rescale.  With a device-side position the kernel also applies
+// RoPE to q and to the new k and quantizes + stores the new K/V row before
+// attending (the decode step's fused form).
 #include "../internal.hpp"
 
 #include <cmath>
@@ -27,18 +29,9 @@ namespace vlrf_hip {
 namespace {
 
 constexpr int kChunk = 64;        // tokens per split-K workgroup
+constexpr int kAttnThreads = 512;  // lanes per decode-attention workgroup (8 waves)
 constexpr int kMaxSplits = 512;   // contexts up to 32768 tokens
 constexpr float kNegInf = -INFINITY;
-
-__device__ __forceinline__ float block_max256(float v, float* red) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    v = wave_max(v);
-    if (lane == 0) red[wave] = v;
-    __syncthreads();
-    v = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    __syncthreads();
-    return v;
-}
 
 // RoPE of one pair (rope.hpp:90-96), each product rounded separately.
 __device__ __forceinline__ void rope2(float x0, float x1, float c, float s, float* y0, float* y1) {
@@ -49,39 +42,91 @@ __device__ __forceinline__ void rope2(float x0, float x1, float c, float s, floa
 }
 
 template <int D, int REP, bool Q8, bool FUSED>
-__global__ __launch_bounds__(256) void attn_decode_partial_kernel(
+__global__ __launch_bounds__(kAttnThreads) void attn_decode_partial_kernel(
     const float* __restrict__ q, const int8_t* kq, const int8_t* vq, const float* ks, const float* vs,
     const float* __restrict__ kf, const float* __restrict__ vf, long head_stride, int ctx_len,
     const int* __restrict__ ctx_dev, int n_splits, float scale, float* __restrict__ part, DecodeFuse fz) {
-    constexpr int DQ = D / 4;                  // dims per wave in the score phase
-    constexpr int DL = D / 64;                 // 4-dim groups per lane in the P.V phase
+    constexpr int HALF = D / 2;
+    static_assert(HALF == 32 || HALF == 64, "a RoPE pair index is tid % HALF only for HALF | 64");
+    constexpr int NT = kAttnThreads, NW = NT / 64;
+    constexpr int HPW = REP >= NW ? REP / NW : 1;        // query heads scored per wave
+    constexpr int KW = Q8 ? D / 16 : D / 4;              // 16-byte words of one K row
+    constexpr int VE = kChunk * D / NT;                  // V elements staged per thread
+    constexpr int VD = Q8 ? VE / 4 : VE;                 // their dwords (Q8: 4 codes each)
+    static_assert(VD % 2 == 0 && VD <= 16, "V staging granularity");
     __shared__ __align__(16) float qs[REP][D];
-    __shared__ float sp4[4][REP][kChunk];      // score partials per dim quarter
-    __shared__ float red[4][REP][D];
+    __shared__ __align__(16) float vsm[kChunk][D];       // the chunk's dequantized V rows
+    __shared__ __align__(16) float pr[REP][kChunk];      // softmax numerators
     __shared__ float mstat[REP], lstat[REP];
-    __shared__ float rmax[4];
-    __shared__ float krow[FUSED ? 1024 : 1], vrow[FUSED ? 1024 : 1];
-    __shared__ __align__(16) float newk[FUSED ? D : 1], newv[FUSED ? D : 1];
+    __shared__ __align__(16) float newk[FUSED ? D : 1];
 
     const int split = blockIdx.x, g = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    constexpr int HALF = D / 2;
-    int pos = -1, ctx;
-    if constexpr (FUSED) {
-        pos = *ctx_dev;          // tokens before this one
-        ctx = pos + 1;
-    } else {
-        ctx = ctx_dev ? (*ctx_dev + ctx_len) : ctx_len;
-    }
-    // Rows past the cache capacity are never read, even if the device-side
-    // position were corrupt (the host checks capacity before queuing).
-    ctx = min(ctx, (int)(head_stride / D));
+    const int cap = (int)(head_stride / D);       // cache rows
     const int c0 = split * kChunk;
     const size_t hb = (size_t)g * head_stride;
 
+    // Vector loads complete in issue order, so the small L2-resident operands
+    // (queries, the new K/V row) are requested first, then the cache stream,
+    // and every load is branch-free (rows are clamped into the cache and
+    // masked where they are used): a load in a branch, or a value converted
+    // right after its load, would make the wave wait for the whole stream early.
+    constexpr int PAIRS = REP * HALF, PPT = (PAIRS + NT - 1) / NT;
+    float qlo[PPT], qhi[PPT];
+#pragma unroll
+    for (int p = 0; p < PPT; ++p) {
+        const int i = min(tid + NT * p, PAIRS - 1), h = i / HALF, j = i - h * HALF;
+        const float* qh = q + (size_t)(g * REP + h) * D;
+        qlo[p] = qh[j];
+        qhi[p] = qh[j + HALF];
+    }
+    // Fused decode: wave 0 holds the new token's K row as RoPE pairs and its V
+    // row (row <= 1024 floats: up to 8 pairs and 16 values per lane).
+    constexpr int KP = FUSED ? 8 : 1, VP = FUSED ? 16 : 1;
+    float nk0[KP], nk1[KP], nv[VP];
+    if (FUSED && wave == 0) {
+        const int npairs = fz.n_kv * HALF, nrow = fz.n_kv * D;
+#pragma unroll
+        for (int p = 0; p < KP; ++p) {
+            const int i = min(lane + 64 * p, npairs - 1), h = i / HALF, j = i - h * HALF;
+            nk0[p] = fz.k_new[h * D + j];
+            nk1[p] = fz.k_new[h * D + j + HALF];
+        }
+#pragma unroll
+        for (int p = 0; p < VP; ++p) nv[p] = fz.v_new[min(lane + 64 * p, nrow - 1)];
+    }
+    // The cache stream, kept as raw codes: lane l of every wave reads the whole
+    // K row of token c0+l (the waves' repeats are L1 hits); thread t stages
+    // VE elements of the V row of token c0 + t*VE/D.
+    const int jt = min(c0 + lane, cap - 1);
+    uint4 kraw[KW];
+#pragma unroll
+    for (int i = 0; i < KW; ++i) {
+        if constexpr (Q8) kraw[i] = *reinterpret_cast<const uint4*>(kq + hb + (size_t)jt * D + 16 * i);
+        else kraw[i] = *reinterpret_cast<const uint4*>(kf + hb + (size_t)jt * D + 4 * i);
+    }
+    const float ksc = Q8 ? ks[jt] : 1.f;
+    const int tv = tid / (D / VE), pv = tid % (D / VE);
+    const int jv = min(c0 + tv, cap - 1);
+    uint2 vraw[VD / 2];
+#pragma unroll
+    for (int i = 0; i < VD / 2; ++i) {
+        if constexpr (Q8) vraw[i] = *reinterpret_cast<const uint2*>(vq + hb + (size_t)jv * D + pv * VE + 8 * i);
+        else vraw[i] = *reinterpret_cast<const uint2*>(vf + hb + (size_t)jv * D + pv * VE + 2 * i);
+    }
+    const float vsc = Q8 ? vs[jv] : 1.f;
+
+    // The device position is read only now: none of the addresses above depend
+    // on it, so its latency overlaps the cache stream.
+    const int dpos = ctx_dev ? *ctx_dev : 0;
+    int ctx = FUSED ? dpos + 1 : (ctx_dev ? dpos + ctx_len : ctx_len);   // FUSED: dpos = tokens before this one
+    // Rows past the cache capacity are never read, even if the device-side
+    // position were corrupt (the host checks capacity before queuing).
+    ctx = min(ctx, cap);
+    const int pos = FUSED ? dpos : -1;
     float* pout = part + (size_t)(g * REP) * n_splits * (D + 2) + (size_t)split * (D + 2);
     if (c0 >= ctx) {   // chunk past the context: empty partial
-        for (int i = tid; i < REP * (D + 2); i += 256) {
+        for (int i = tid; i < REP * (D + 2); i += NT) {
             const int h = i / (D + 2), dd = i % (D + 2);
             pout[(size_t)h * n_splits * (D + 2) + dd] = dd == D ? kNegInf : 0.f;
         }
@@ -89,233 +134,184 @@ __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
     }
     const int nt = min(kChunk, ctx - c0);       // valid tokens of the chunk
     const bool has_new = FUSED && pos >= c0 && pos < c0 + kChunk;
-
-    // Vector loads complete in issue order, so the small L2-resident operands
-    // (queries, RoPE tables, the new K/V row) are requested first, then the
-    // cache stream, and every load is branch-free (out-of-range tokens read
-    // row c0, which is in bounds, and are masked where they are used): a load
-    // in a branch, or a value converted right after its load, would make the
-    // wave wait for the whole stream early.
-    constexpr int PAIRS = REP * HALF, PPT = (PAIRS + 255) / 256;
     const bool rot = FUSED && pos < fz.max_seq;   // rope.hpp:84: positions >= max_seq stay unrotated
-    float qlo[PPT], qhi[PPT];
-#pragma unroll
-    for (int p = 0; p < PPT; ++p) {
-        const int i = min(tid + 256 * p, PAIRS - 1), h = i / HALF, j = i - h * HALF;
-        const float* qh = q + (size_t)(g * REP + h) * D;
-        qlo[p] = qh[j];
-        qhi[p] = qh[j + HALF];
-    }
-    float cw = 1.f, sw = 0.f;
-    if (rot) {
-        cw = fz.cos_t[(size_t)pos * HALF + (tid & (HALF - 1))];
-        sw = fz.sin_t[(size_t)pos * HALF + (tid & (HALF - 1))];
-    }
-    constexpr int NPT = FUSED ? 4 : 1;            // new-row floats per thread (row <= 1024)
-    float kn[NPT], vn[NPT];
+    // Every RoPE pair this thread rotates (q pairs tid + NT*p, and for wave 0
+    // the new k pairs lane + 64p) has pair index tid % HALF, so one table entry
+    // per thread serves them all.
+    float rc = 1.f, rs = 0.f;
     if constexpr (FUSED) {
-        const int row = fz.n_kv * D;
-#pragma unroll
-        for (int p = 0; p < NPT; ++p) {
-            const int i = min(tid + 256 * p, row - 1);
-            kn[p] = fz.k_new[i];
-            vn[p] = fz.v_new[i];
-        }
-    }
-
-    // The cache stream: this thread's K slice (token lane, dims of this wave)
-    // and its V words (tokens wave*16 + t4 + 4i, dims 4dg..), kept as raw codes.
-    const int t4 = lane >> 4, dg = lane & 15;
-    constexpr int KW = Q8 ? DQ / 16 : DQ / 4;      // 16-byte words of the K slice
-    uint4 kraw[KW];
-    uint4 vraw[4][DL];                             // Q8: .x holds 4 codes; f32: 4 floats
-    float ksc = 1.f, vsc[4] = {1.f, 1.f, 1.f, 1.f};
-    {
-        const int jt = lane < nt ? c0 + lane : c0;
-#pragma unroll
-        for (int i = 0; i < KW; ++i) {
-            if constexpr (Q8)
-                kraw[i] = *reinterpret_cast<const uint4*>(kq + hb + (size_t)jt * D + wave * DQ + 16 * i);
-            else
-                kraw[i] = *reinterpret_cast<const uint4*>(kf + hb + (size_t)jt * D + wave * DQ + 4 * i);
-        }
-        if constexpr (Q8) ksc = ks[jt];
-#pragma unroll
-        for (int it = 0; it < 4; ++it) {
-            const int t = wave * 16 + t4 + 4 * it;
-            const int jj = t < nt ? c0 + t : c0;
-            if constexpr (Q8) vsc[it] = vs[jj];
-#pragma unroll
-            for (int dl = 0; dl < DL; ++dl) {
-                if constexpr (Q8) {
-                    vraw[it][dl].x = *reinterpret_cast<const uint32_t*>(vq + hb + (size_t)jj * D + dl * 64 + dg * 4);
-                } else {
-                    vraw[it][dl] = *reinterpret_cast<const uint4*>(vf + hb + (size_t)jj * D + dl * 64 + dg * 4);
-                }
-            }
-        }
+        const int trow = min(pos, fz.max_seq - 1);   // used only when rot
+        rc = fz.cos_t[(size_t)trow * HALF + (tid & (HALF - 1))];
+        rs = fz.sin_t[(size_t)trow * HALF + (tid & (HALF - 1))];
     }
 
     // ---- queries of the GQA group (RoPE at the device position when fused) -------
-    {
-        float* cst = sp4[0][0];                    // RoPE table row, staged before phase 1 reuses sp4
-        if (rot && tid < HALF) { cst[tid] = cw; cst[HALF + tid] = sw; }
-        __syncthreads();
 #pragma unroll
-        for (int p = 0; p < PPT; ++p) {
-            const int i = tid + 256 * p;
-            if (i < PAIRS) {
-                const int h = i / HALF, j = i - h * HALF;
-                if (rot) rope2(qlo[p], qhi[p], cst[j], cst[HALF + j], &qs[h][j], &qs[h][j + HALF]);
-                else { qs[h][j] = qlo[p]; qs[h][j + HALF] = qhi[p]; }
-            }
-        }
-        // ---- decode fusion: the current token's K/V row ----------------------------
-        // attention.hpp:109-128: RoPE on k, then KVCache::append quantizes the whole
-        // row (quantize_row_q8_0, kv_cache.hpp:102-117) before attention reads it.
-        // Every chunk holding `pos` quantizes the row itself and uses the dequantized
-        // values for that token; the workgroup of KV head g stores head g's codes,
-        // KV head 0 stores the row scales.
-        if constexpr (FUSED) {
-            if (has_new) {
-                const int row = fz.n_kv * D;
-#pragma unroll
-                for (int p = 0; p < NPT; ++p) {
-                    const int i = tid + 256 * p;
-                    if (i < row) { krow[i] = kn[p]; vrow[i] = vn[p]; }
-                }
-                __syncthreads();
-                if (rot) {
-                    for (int i = tid; i < fz.n_kv * HALF; i += 256) {
-                        const int h = i / HALF, j = i - h * HALF;
-                        float* kh = krow + h * D;
-                        const float x0 = kh[j], x1 = kh[j + HALF];
-                        rope2(x0, x1, cst[j], cst[HALF + j], &kh[j], &kh[j + HALF]);
-                    }
-                }
-                __syncthreads();
-                float ak = 0.f, av = 0.f;
-                for (int i = tid; i < row; i += 256) { ak = fmaxf(ak, fabsf(krow[i])); av = fmaxf(av, fabsf(vrow[i])); }
-                ak = block_max256(ak, rmax);
-                av = block_max256(av, rmax);
-                const float sk = ak != 0.f ? ak / 127.f : 0.f, sv = av != 0.f ? av / 127.f : 0.f;
-                const float ik = ak != 0.f ? 1.f / sk : 0.f, iv = av != 0.f ? 1.f / sv : 0.f;
-                for (int i = tid; i < D; i += 256) {
-                    const int a = ak != 0.f ? min(127, max(-127, (int)roundf(krow[g * D + i] * ik))) : 0;
-                    const int b = av != 0.f ? min(127, max(-127, (int)roundf(vrow[g * D + i] * iv))) : 0;
-                    newk[i] = (float)a * sk;
-                    newv[i] = (float)b * sv;
-                    fz.kq_w[hb + (size_t)pos * D + i] = (int8_t)a;
-                    fz.vq_w[hb + (size_t)pos * D + i] = (int8_t)b;
-                }
-                if (g == 0 && tid == 0) { fz.ks_w[pos] = sk; fz.vs_w[pos] = sv; }
-            }
-        }
-        __syncthreads();
-    }
-
-    // ---- phase 1: partial scores over this wave's quarter of d_head --------------
-    {
-        float kd[DQ];
-        if (FUSED && has_new && c0 + lane == pos) {
-#pragma unroll
-            for (int i = 0; i < DQ; ++i) kd[i] = newk[wave * DQ + i];
-        } else {
-#pragma unroll
-            for (int i = 0; i < KW; ++i) {
-                const uint32_t w[4] = {kraw[i].x, kraw[i].y, kraw[i].z, kraw[i].w};
-                if constexpr (Q8) {
-#pragma unroll
-                    for (int k = 0; k < 16; ++k)   // dequantize_row_q8_0
-                        kd[16 * i + k] = (float)(int8_t)(w[k >> 2] >> (8 * (k & 3))) * ksc;
-                } else {
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) kd[4 * i + k] = __uint_as_float(w[k]);
-                }
-            }
-        }
-#pragma unroll
-        for (int h = 0; h < REP; ++h) {
-            float dsum = 0.f;
-#pragma unroll
-            for (int i = 0; i < DQ; i += 4) {
-                const float4 qv = *reinterpret_cast<const float4*>(&qs[h][wave * DQ + i]);
-                dsum += qv.x * kd[i] + qv.y * kd[i + 1] + qv.z * kd[i + 2] + qv.w * kd[i + 3];
-            }
-            sp4[wave][h][lane] = dsum;
+    for (int p = 0; p < PPT; ++p) {
+        const int i = tid + NT * p;
+        if (i < PAIRS) {
+            const int h = i / HALF, j = i - h * HALF;
+            if (rot) rope2(qlo[p], qhi[p], rc, rs, &qs[h][j], &qs[h][j + HALF]);
+            else { qs[h][j] = qlo[p]; qs[h][j + HALF] = qhi[p]; }
         }
     }
-    __syncthreads();
 
-    // ---- phase 2: per-head chunk max and sum (DPP/shuffle wave reductions) --------
-    for (int h = wave; h < REP; h += 4) {
-        float sc = kNegInf;
-        if (lane < nt) sc = ((sp4[0][h][lane] + sp4[1][h][lane]) + (sp4[2][h][lane] + sp4[3][h][lane])) * scale;
-        const float mx = wave_max(sc);   // finite: token c0 < ctx is in this chunk
-        const float p = expf(sc - mx);
-        sp4[0][h][lane] = p;
-        const float sum = wave_sum(p);
-        if (lane == 0) { mstat[h] = mx; lstat[h] = sum; }
+    // ---- V chunk into LDS, dequantized (dequantize_row_q8_0); rows past the
+    // context are zero, and the new token's row is written by wave 0 below.
+    if (!(has_new && c0 + tv == pos)) {
+        float* dst = &vsm[tv][pv * VE];
+        const bool live = c0 + tv < ctx;
+#pragma unroll
+        for (int i = 0; i < VD / 2; ++i) {
+            const uint32_t w[2] = {vraw[i].x, vraw[i].y};
+            if constexpr (Q8) {
+#pragma unroll
+                for (int k = 0; k < 2; ++k) {
+                    float4 o;
+                    o.x = live ? (float)(int8_t)(w[k]) * vsc : 0.f;
+                    o.y = live ? (float)(int8_t)(w[k] >> 8) * vsc : 0.f;
+                    o.z = live ? (float)(int8_t)(w[k] >> 16) * vsc : 0.f;
+                    o.w = live ? (float)(int8_t)(w[k] >> 24) * vsc : 0.f;
+                    *reinterpret_cast<float4*>(dst + 8 * i + 4 * k) = o;
+                }
+            } else {
+                float2 o;
+                o.x = live ? __uint_as_float(w[0]) : 0.f;
+                o.y = live ? __uint_as_float(w[1]) : 0.f;
+                *reinterpret_cast<float2*>(dst + 2 * i) = o;
+            }
+        }
+    }
+
+    // ---- decode fusion: the current token's K/V row (wave 0 of the chunk holding it)
+    // attention.hpp:109-128: RoPE on k, then KVCache::append quantizes the whole
+    // row (quantize_row_q8_0, kv_cache.hpp:102-117) before attention reads it.
+    // Every chunk holding `pos` quantizes the row itself and uses the dequantized
+    // values for that token; the workgroup of KV head g stores head g's codes,
+    // KV head 0 stores the row scales.  Wave reductions only: no workgroup barrier.
+    if constexpr (FUSED) {
+        if (has_new && wave == 0) {
+            const int npairs = fz.n_kv * HALF, nrow = fz.n_kv * D;
+            float ak = 0.f, av = 0.f;
+#pragma unroll
+            for (int p = 0; p < KP; ++p) {
+                if (lane + 64 * p < npairs) {
+                    if (rot) rope2(nk0[p], nk1[p], rc, rs, &nk0[p], &nk1[p]);
+                    ak = fmaxf(ak, fmaxf(fabsf(nk0[p]), fabsf(nk1[p])));
+                }
+            }
+#pragma unroll
+            for (int p = 0; p < VP; ++p)
+                if (lane + 64 * p < nrow) av = fmaxf(av, fabsf(nv[p]));
+            ak = wave_max(ak);
+            av = wave_max(av);
+            const float sk = ak != 0.f ? ak / 127.f : 0.f, sv = av != 0.f ? av / 127.f : 0.f;
+            const float ik = ak != 0.f ? 1.f / sk : 0.f, iv = av != 0.f ? 1.f / sv : 0.f;
+            int8_t* krow_w = fz.kq_w + hb + (size_t)pos * D;
+            int8_t* vrow_w = fz.vq_w + hb + (size_t)pos * D;
+            float* vnew = vsm[pos - c0];
+#pragma unroll
+            for (int p = 0; p < KP; ++p) {
+                const int i = lane + 64 * p;
+                if (i < npairs && i / HALF == g) {
+                    const int j = i % HALF;
+                    const int a0 = ak != 0.f ? min(127, max(-127, (int)roundf(nk0[p] * ik))) : 0;
+                    const int a1 = ak != 0.f ? min(127, max(-127, (int)roundf(nk1[p] * ik))) : 0;
+                    newk[j] = (float)a0 * sk;
+                    newk[j + HALF] = (float)a1 * sk;
+                    krow_w[j] = (int8_t)a0;
+                    krow_w[j + HALF] = (int8_t)a1;
+                }
+            }
+#pragma unroll
+            for (int p = 0; p < VP; ++p) {
+                const int i = lane + 64 * p;
+                if (i < nrow && i / D == g) {
+                    const int dd = i % D;
+                    const int b = av != 0.f ? min(127, max(-127, (int)roundf(nv[p] * iv))) : 0;
+                    vnew[dd] = (float)b * sv;
+                    vrow_w[dd] = (int8_t)b;
+                }
+            }
+            if (g == 0 && lane == 0) { fz.ks_w[pos] = sk; fz.vs_w[pos] = sv; }
+        }
     }
     __syncthreads();
 
-    // ---- phase 3: P.V (lane = 4 dims x token offset t4, wave = 16 tokens) ----------
-    float acc[REP][DL][4];
+    // ---- scores and softmax: lane = token, HPW heads per wave, full d_head ------
+    // One wave per SIMD leaves no other wave to hide LDS latency, so each
+    // head's q row is read in one batch and the dot products use four
+    // independent accumulators.  Codes are converted once; the row scale is
+    // applied to the finished dot (exact integers times q, then one scale).
+    {
+        const bool live = lane < nt;
+        float kv[D];
+        float kscale = ksc;
 #pragma unroll
-    for (int h = 0; h < REP; ++h)
+        for (int i = 0; i < KW; ++i) {
+            const uint32_t w[4] = {kraw[i].x, kraw[i].y, kraw[i].z, kraw[i].w};
+            if constexpr (Q8) {
 #pragma unroll
-        for (int dl = 0; dl < DL; ++dl)
-#pragma unroll
-            for (int k = 0; k < 4; ++k) acc[h][dl][k] = 0.f;
-#pragma unroll
-    for (int it = 0; it < 4; ++it) {
-        const int t = wave * 16 + t4 + 4 * it;
-        if (t < nt) {
-            float vd[DL][4];
-            if (FUSED && has_new && c0 + t == pos) {
-#pragma unroll
-                for (int dl = 0; dl < DL; ++dl)
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) vd[dl][k] = newv[dl * 64 + dg * 4 + k];
+                for (int k = 0; k < 16; ++k) kv[16 * i + k] = (float)(int8_t)(w[k >> 2] >> (8 * (k & 3)));
             } else {
 #pragma unroll
-                for (int dl = 0; dl < DL; ++dl) {
-                    if constexpr (Q8) {
-#pragma unroll
-                        for (int k = 0; k < 4; ++k)
-                            vd[dl][k] = (float)(int8_t)(vraw[it][dl].x >> (8 * k)) * vsc[it];
-                    } else {
-                        vd[dl][0] = __uint_as_float(vraw[it][dl].x); vd[dl][1] = __uint_as_float(vraw[it][dl].y);
-                        vd[dl][2] = __uint_as_float(vraw[it][dl].z); vd[dl][3] = __uint_as_float(vraw[it][dl].w);
-                    }
-                }
+                for (int k = 0; k < 4; ++k) kv[4 * i + k] = __uint_as_float(w[k]);
             }
+        }
+        if constexpr (FUSED) {
+            if (has_new && c0 + lane == pos) {     // the new token: its dequantized row
 #pragma unroll
-            for (int h = 0; h < REP; ++h) {
-                const float p = sp4[0][h][t];
+                for (int j = 0; j < D; ++j) kv[j] = newk[j];
+                kscale = 1.f;
+            }
+        }
 #pragma unroll
-                for (int dl = 0; dl < DL; ++dl)
+        for (int hh = 0; hh < HPW; ++hh) {
+            const int h = wave * HPW + hh;
+            if (h < REP) {
+                float4 qv[D / 4];
 #pragma unroll
-                    for (int k = 0; k < 4; ++k) acc[h][dl][k] += p * vd[dl][k];
+                for (int i = 0; i < D / 4; ++i) qv[i] = *reinterpret_cast<const float4*>(&qs[h][4 * i]);
+                float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+#pragma unroll
+                for (int i = 0; i < D / 4; ++i) {
+                    s0 += qv[i].x * kv[4 * i];
+                    s1 += qv[i].y * kv[4 * i + 1];
+                    s2 += qv[i].z * kv[4 * i + 2];
+                    s3 += qv[i].w * kv[4 * i + 3];
+                }
+                const float sdot = ((s0 + s1) + (s2 + s3)) * kscale;
+                const float sc = live ? sdot * scale : kNegInf;
+                const float mx = wave_max(sc);   // finite: token c0 < ctx is in this chunk
+                const float pe = live ? expf(sc - mx) : 0.f;
+                const float sum = wave_sum(pe);
+                pr[h][lane] = pe;
+                if (lane == 0) { mstat[h] = mx; lstat[h] = sum; }
             }
         }
     }
+    __syncthreads();
+
+    // ---- P.V: thread = (head, dim), over the chunk's tokens from LDS -------------
+    // LDS reads in batches of 16 tokens, two accumulators per output.
+    for (int i = tid; i < REP * D; i += NT) {
+        const int h = i / D, d = i - h * D;
+        float a = 0.f, b = 0.f;
 #pragma unroll
-    for (int h = 0; h < REP; ++h)
+        for (int t0 = 0; t0 < kChunk; t0 += 16) {
+            float4 pp[4];
+            float vv[16];
 #pragma unroll
-        for (int dl = 0; dl < DL; ++dl)
+            for (int k = 0; k < 4; ++k) pp[k] = *reinterpret_cast<const float4*>(&pr[h][t0 + 4 * k]);
+#pragma unroll
+            for (int k = 0; k < 16; ++k) vv[k] = vsm[t0 + k][d];
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                float a = acc[h][dl][k];
-                a += __shfl_xor(a, 16);
-                a += __shfl_xor(a, 32);
-                if (t4 == 0) red[wave][h][dl * 64 + dg * 4 + k] = a;
+                a += pp[k].x * vv[4 * k] + pp[k].y * vv[4 * k + 1];
+                b += pp[k].z * vv[4 * k + 2] + pp[k].w * vv[4 * k + 3];
             }
-    __syncthreads();
-    for (int i = tid; i < REP * D; i += 256) {
-        const int h = i / D, dd = i % D;
-        pout[(size_t)h * n_splits * (D + 2) + dd] =
-            (red[0][h][dd] + red[1][h][dd]) + (red[2][h][dd] + red[3][h][dd]);
+        }
+        pout[(size_t)h * n_splits * (D + 2) + d] = a + b;
     }
     if (tid < REP) {
         pout[(size_t)tid * n_splits * (D + 2) + D] = mstat[tid];
@@ -496,7 +492,7 @@ int launch_attn_decode(hipStream_t s, const float* q, const int8_t* kq, const in
         VH_ARG(fuse->n_kv == n_kv && n_kv * d_head <= 1024, "attn_decode: bad fusion row");
         fz = *fuse;
     }
-    dim3 grid(n_splits, n_kv), block(256);
+    dim3 grid(n_splits, n_kv), block(kAttnThreads);
 #define VH_AD(D, R, Q, FU)                                                                          \
     hipLaunchKernelGGL((attn_decode_partial_kernel<D, R, Q, FU>), grid, block, 0, s, q, kq, vq, ks,  \
                        vs, kf, vf, head_stride, ctx_len, ctx_dev, n_splits, scale, part, fz)
