@@ -134,10 +134,14 @@ int vlrf_hip_weight_upload(vlrf_hip_ctx_t ctx, const void* host, int dtype, int 
                            vlrf_hip_weight_t* out);
 void vlrf_hip_weight_free(vlrf_hip_weight_t w);
 size_t vlrf_hip_weight_bytes(vlrf_hip_weight_t w);   /* device bytes of the packed weight */
-/* x, y device f32, 1 <= M <= 16.  norm_w (nullable, device f32 [K]): x rows
+/* x, y device f32, M >= 1.  norm_w (nullable, device f32 [K]): x rows
  * are first RMS-normalised with weight norm_w and `eps` (ops.hpp:478-499).
  * residual (nullable, device f32 [M,N], may alias y): added after the product
- * (the residual adds of transformer_block.hpp:149-159). */
+ * (the residual adds of transformer_block.hpp:149-159).
+ * M <= 16 (decode, ops.hpp:238-310 for M = 1..16) computes in f32.  M > 16
+ * (prefill, ops.hpp:254-305) runs on the matrix cores: x (normalised) and the
+ * decoded weights are rounded to bf16, accumulation is f32; it takes Q8_0 or
+ * Q4_0 weights with K % 64 == 0 and uses the context's scratch buffer. */
 int vlrf_hip_qlinear(vlrf_hip_ctx_t ctx, vlrf_hip_weight_t w, const float* x, float* y, int M,
                      const float* norm_w, float eps, const float* residual);
 
@@ -145,7 +149,7 @@ int vlrf_hip_qlinear(vlrf_hip_ctx_t ctx, vlrf_hip_weight_t w, const float* x, fl
  * h[M,F] = silu(rmsnorm(x).Wg^T) * (rmsnorm(x).Wu^T), silu(g) = g/(1+exp(-g)).
  * Replaces: linear(x, fc1), linear(x, gate), silu_inplace, multiply_inplace
  * (feedforward.hpp:54-62, ops.hpp:409-441).  norm_w nullable as above;
- * wg and wu have the same shape and dtype. */
+ * wg and wu have the same shape and dtype.  M ranges as vlrf_hip_qlinear. */
 int vlrf_hip_qlinear_swiglu(vlrf_hip_ctx_t ctx, vlrf_hip_weight_t wg, vlrf_hip_weight_t wu,
                             const float* x, float* h, int M, const float* norm_w, float eps);
 

@@ -1,0 +1,64 @@
+"""GPU parity of the prefill (M > 16) linear: the MFMA GEMM on bf16 operands
+with f32 accumulation, against ops::gemm restated in f32 (oracle) on the
+decoded weights (compute.hpp:58-68, ops.hpp:254-305, convert_gguf.py:233-263).
+Tolerance: the 1e-2 class of bf16 paths (max |diff| / max |ref|); measured
+errors are ~3e-3."""
+import numpy as np
+import pytest
+
+import vlrf_amd as V
+from conftest import rel_err
+from vlrf_amd import formats as F
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-2
+
+
+def _weight(ctx, seed, name, N, K, dtype):
+    w = F.normal(seed, name, N * K, 0.02)
+    blocks = F.quantize(w, dtype)
+    dec = F.dequantize(blocks, dtype, N * K).reshape(N, K)
+    return V.QuantWeight(ctx, blocks, dtype, N, K), dec
+
+
+@pytest.mark.parametrize("dtype", [V.DT_Q8_0, V.DT_Q4_0])
+@pytest.mark.parametrize("M,N,K", [(256, 6144, 4096), (128, 4096, 14336), (2048, 1024, 4096)])
+def test_prefill_gemm_config5_shapes(ctx, orc, dtype, M, N, K):
+    """The 8B-layer projections (QKV 6144x4096, down 4096x14336) at prompt rows."""
+    print(f"[case] qgemm dtype={dtype} M={M} N={N} K={K}", flush=True)
+    w, dec = _weight(ctx, 21, f"P{N}x{K}", N, K, dtype)
+    x = F.normal(21, f"px{M}x{K}", M * K).reshape(M, K)
+    dx, dy = ctx.to_device(x), ctx.alloc(M * N * 4)
+    ctx.qlinear(w, dx, dy, M)
+    ref = x.astype(np.float64) @ dec.astype(np.float64).T
+    assert rel_err(dy.download((M, N)), ref) <= TOL
+
+
+@pytest.mark.parametrize("M,N,K", [(17, 37, 64), (200, 300, 128), (129, 130, 704), (300, 256, 2048)])
+def test_prefill_gemm_ragged_with_norm_and_residual(ctx, orc, M, N, K):
+    """Row/column counts off the 128x128 tile, with the fused RMSNorm prologue
+    and the residual epilogue (in place on the residual)."""
+    print(f"[case] qgemm ragged M={M} N={N} K={K}", flush=True)
+    w, dec = _weight(ctx, 22, f"G{N}x{K}", N, K, V.DT_Q8_0)
+    x = F.normal(22, f"gx{M}", M * K).reshape(M, K) * 3
+    g = 1.0 + F.normal(22, f"gg{K}", K, 0.1)
+    res = F.normal(22, f"gr{M}x{N}", M * N).reshape(M, N)
+    dx, dg, dr = ctx.to_device(x), ctx.to_device(g), ctx.to_device(res)
+    ctx.qlinear(w, dx, dr, M, norm_w=dg, eps=1e-5, residual=dr)
+    ref = orc.linear(orc.rms_norm(x, g, 1e-5), dec) + res
+    assert rel_err(dr.download((M, N)), ref) <= TOL
+
+
+@pytest.mark.parametrize("dtype", [V.DT_Q8_0, V.DT_Q4_0])
+def test_prefill_swiglu(ctx, orc, dtype):
+    """h = silu(x.Wg^T) * (x.Wu^T) at M = 192 rows (feedforward.hpp:54-62)."""
+    M, Fd, K = 192, 1408, 1024
+    wg, gdec = _weight(ctx, 23, "PWg", Fd, K, dtype)
+    wu, udec = _weight(ctx, 23, "PWu", Fd, K, dtype)
+    x = F.normal(23, "psx", M * K).reshape(M, K)
+    g = np.ones(K, np.float32)
+    dx, dg, dh = ctx.to_device(x), ctx.to_device(g), ctx.alloc(M * Fd * 4)
+    ctx.qlinear_swiglu(wg, wu, dx, dh, M, norm_w=dg, eps=1e-5)
+    xn = orc.rms_norm(x, g, 1e-5)
+    ref = orc.silu_mul(orc.linear(xn, udec), orc.linear(xn, gdec))
+    assert rel_err(dh.download((M, Fd)), ref) <= TOL

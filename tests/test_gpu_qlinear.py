@@ -81,9 +81,12 @@ def test_swiglu_gate_up(ctx, orc, dtype, M):
 
 
 def test_qlinear_rejects_bad_shapes(ctx):
-    w, _ = _weight(ctx, 11, "Wbad", 64, 64, V.DT_Q8_0)
-    x = ctx.alloc(64 * 4 * 17)
+    w, _ = _weight(ctx, 11, "Wbad", 64, 96, V.DT_Q8_0)
+    x = ctx.alloc(96 * 4 * 17)
     with pytest.raises(V.HipError):
-        ctx.qlinear(w, x, ctx.alloc(64 * 4 * 17), 17)      # M above 16
+        ctx.qlinear(w, x, ctx.alloc(64 * 4 * 17), 17)      # M > 16 (MFMA path) needs K % 64 == 0
+    wf, _ = _weight(ctx, 11, "Wbadf", 64, 64, V.DT_F32)
+    with pytest.raises(V.HipError):
+        ctx.qlinear(wf, x, ctx.alloc(64 * 4 * 17), 17)     # and a block-quantized weight
     with pytest.raises(V.HipError):
         ctx.qlinear(w, x, x, 1)                             # x aliasing y

@@ -510,12 +510,23 @@ size_t vlrf_hip_weight_bytes(vlrf_hip_weight_t w) {
     return w ? weight_device_bytes(w->w.dtype, w->w.N, w->w.K) : 0;
 }
 
+// M <= 16 runs the f32 GEMV / small-M kernels; larger M (prefill) runs the
+// MFMA GEMM on bf16 operands (x, optionally RMS-normalised, is rounded to bf16
+// in the context's scratch buffer first).
 int vlrf_hip_qlinear(vlrf_hip_ctx_t ctx, vlrf_hip_weight_t w, const float* x, float* y, int M,
                      const float* norm_w, float eps, const float* residual) {
     VH_CTX(ctx);
     VH_ARG(w != nullptr, "qlinear: null weight");
     VH_ARG(x != y, "qlinear: x must not alias y");
-    return launch_qlinear(ctx->stream, w->w, x, y, M, norm_w, eps, residual);
+    if (M <= 16) return launch_qlinear(ctx->stream, w->w, x, y, M, norm_w, eps, residual);
+    VH_ARG(x && y, "qlinear: null activation pointer");
+    float* scratch = nullptr;
+    int rc = ctx->scratch((size_t)M * w->w.K * sizeof(uint16_t), &scratch);
+    if (rc) return rc;
+    uint16_t* a = reinterpret_cast<uint16_t*>(scratch);
+    rc = launch_rows_to_bf16(ctx->stream, x, norm_w, a, M, w->w.K, eps);
+    if (rc) return rc;
+    return launch_qgemm(ctx->stream, w->w, a, M, residual, y);
 }
 
 int vlrf_hip_qlinear_swiglu(vlrf_hip_ctx_t ctx, vlrf_hip_weight_t wg, vlrf_hip_weight_t wu,
@@ -523,7 +534,15 @@ int vlrf_hip_qlinear_swiglu(vlrf_hip_ctx_t ctx, vlrf_hip_weight_t wg, vlrf_hip_w
     VH_CTX(ctx);
     VH_ARG(wg && wu, "swiglu: null weight");
     VH_ARG(x != h, "swiglu: x must not alias h");
-    return launch_qlinear_swiglu(ctx->stream, wg->w, wu->w, x, h, M, norm_w, eps);
+    if (M <= 16) return launch_qlinear_swiglu(ctx->stream, wg->w, wu->w, x, h, M, norm_w, eps);
+    VH_ARG(x && h, "swiglu: null activation pointer");
+    float* scratch = nullptr;
+    int rc = ctx->scratch((size_t)M * wg->w.K * sizeof(uint16_t), &scratch);
+    if (rc) return rc;
+    uint16_t* a = reinterpret_cast<uint16_t*>(scratch);
+    rc = launch_rows_to_bf16(ctx->stream, x, norm_w, a, M, wg->w.K, eps);
+    if (rc) return rc;
+    return launch_qgemm_swiglu(ctx->stream, wg->w, wu->w, a, M, h, false);
 }
 
 // ---- edge ops ----------------------------------------------------------------------

@@ -91,6 +91,17 @@ int launch_qlinear_swiglu(hipStream_t s, const DevWeight& wg, const DevWeight& w
 
 int launch_rmsnorm(hipStream_t s, const float* x, const float* w, float* out, int rows, int D,
                    float eps);
+
+// ---- prefill (MFMA) path: bf16 operands, f32 accumulate -------------------------
+// out[r] = bf16(w ? rmsnorm(x[r]) * w : x[r]) for rows x D
+int launch_rows_to_bf16(hipStream_t s, const float* x, const float* w, uint16_t* out, int rows, int D,
+                        float eps);
+// y[M,N] = a[M,K] . W^T (+ residual), a in bf16, W Q8_0/Q4_0 with K % 64 == 0
+int launch_qgemm(hipStream_t s, const DevWeight& w, const uint16_t* a, int M, const float* residual,
+                 float* y);
+// h[M,N] = silu(a.Wg^T) * (a.Wu^T), stored as bf16 (h_bf16) or f32
+int launch_qgemm_swiglu(hipStream_t s, const DevWeight& wg, const DevWeight& wu, const uint16_t* a,
+                        int M, void* h, bool h_bf16);
 int launch_rope(hipStream_t s, float* x, int T, int n_heads, int d_head, int pos_offset,
                 int max_seq, const float* cos_t, const float* sin_t);
 
