@@ -214,8 +214,23 @@ int  vlrf_hip_model_used(vlrf_hip_model_t m);
  * logits is non-NULL, copies the logits [vocab] to host. Synchronous. */
 int  vlrf_hip_model_step(vlrf_hip_model_t m, int32_t token, int32_t* next, float* logits);
 /* Feeds `n` tokens one step at a time (the prompt), without reading logits
- * back; *next receives the greedy id after the last one. */
+ * back; *next receives the greedy id after the last one.  The f32 decode
+ * path: the KV cache it leaves matches the reference's prefill to f32
+ * rounding, so generation after it reproduces the reference's streams. */
 int  vlrf_hip_model_prefill(vlrf_hip_model_t m, const int32_t* ids, int n, int32_t* next);
+/* Batched prefill on the matrix cores: TransformerModel::forward over the
+ * whole prompt (transformer.hpp:335-424; AttentionBlock::forward with T = n,
+ * attention.hpp:89-186: causal attention over the Q8_0 cache, K/V appended
+ * before attending).  GEMMs and attention take bf16 operands with f32
+ * accumulation (the 1e-2 class), norms / RoPE / KV quantization are f32.
+ * Needs Q8_0/Q4_0 weights and d_model, d_ff multiples of 64.  *next receives
+ * the greedy id of the last row.  Synchronous. */
+int  vlrf_hip_model_prefill_mfma(vlrf_hip_model_t m, const int32_t* ids, int n, int32_t* next);
+/* The same layers over T embedded rows: x (device f32 [T][d_model], the first
+ * layer's input) is not modified; out (device f32 [T][d_model], may alias x)
+ * receives the residual stream after the last layer.  Appends T positions to
+ * the KV cache.  Synchronous. */
+int  vlrf_hip_model_forward_hidden(vlrf_hip_model_t m, const float* x, int T, float* out);
 /* Greedy generation of n_steps tokens starting from `first` entirely on the
  * device (token feedback on the GPU, replayed HIP graph); out_ids (host,
  * n_steps) receives the generated ids.  Synchronous. */
@@ -224,6 +239,10 @@ int  vlrf_hip_model_generate(vlrf_hip_model_t m, int32_t first, int n_steps, int
  * the device and are fetched by vlrf_hip_model_read_generated. */
 int  vlrf_hip_model_generate_async(vlrf_hip_model_t m, int32_t first, int n_steps);
 int  vlrf_hip_model_read_generated(vlrf_hip_model_t m, int32_t* out_ids, int n);
+/* Rows [row0,row0+n) of layer `layer` of the model's KV cache, as
+ * vlrf_hip_kv_read (token-major int8 codes, f32 row scales).  Synchronous. */
+int  vlrf_hip_model_kv_read(vlrf_hip_model_t m, int layer, int row0, int n, int8_t* k_q,
+                            int8_t* v_q, float* k_s, float* v_s);
 /* Device bytes read per decode step at context length ctx_len, by stream:
  * [0] projection + LM-head weights, [1] KV cache, [2] everything else
  * (norm weights, embedding row, activations).  For roofline accounting. */

@@ -70,6 +70,8 @@ def lib():
     L.orc_model_used.restype = C.c_int
     L.orc_model_forward.argtypes = [C.c_void_p, i32p, C.c_int, C.c_void_p]
     L.orc_model_forward.restype = C.c_int
+    L.orc_model_forward_hidden.argtypes = [C.c_void_p, f32p, C.c_int]
+    L.orc_model_forward_hidden.restype = C.c_int
     L.orc_model_kv.argtypes = [C.c_void_p, C.c_int] + [C.c_void_p] * 4
     L.orc_model_fill_kv.argtypes = [C.c_void_p, C.c_int, C.c_uint64]
     _LIB = L
@@ -234,6 +236,14 @@ class Model:
         if tok < 0:
             raise RuntimeError("oracle forward failed (cache overflow or bad token id)")
         return (tok, logits) if want_logits else tok
+
+    def forward_hidden(self, x):
+        """The layers over embedded rows x [T, d_model]; returns the residual
+        stream after the last layer (a new array) and appends T cache rows."""
+        y = np.ascontiguousarray(x, np.float32).copy()
+        if lib().orc_model_forward_hidden(self.h, y, y.shape[0]) != 0:
+            raise RuntimeError("oracle forward_hidden failed (cache overflow)")
+        return y
 
     def fill_kv(self, used, seed=1):
         lib().orc_model_fill_kv(self.h, int(used), int(seed))

@@ -513,17 +513,17 @@ void orc_model_fill_kv(orc_model* m, int used, uint64_t seed)
     m->used = used;
 }
 
-int orc_model_forward(orc_model* m, const int* ids, int T, float* logits)
+/* The layers over T embedded rows x [T][D] (in place), appending T cache rows:
+ * the body of TransformerModel::forward between the embedding and the final
+ * norm (transformer.hpp:335-398). */
+int orc_model_forward_hidden(orc_model* m, float* x, int T)
 {
     const orc_config* c = &m->c;
     const int D = c->d_model, F = c->d_ff, H = c->n_heads, G = c->n_kv_heads;
     const int dh = D / H, dkv = G * dh, rep = H / G, nt = c->n_threads;
     if (T <= 0 || m->used + T > c->max_seq_len) return -1;
-    for (int t = 0; t < T; ++t)
-        if (ids[t] < 0 || ids[t] >= c->vocab_size) return -1;
 
     size_t TD = (size_t)T * D;
-    float* x = (float*)malloc(TD * sizeof(float));
     float* hn = (float*)malloc(TD * sizeof(float));
     float* q = (float*)malloc(TD * sizeof(float));
     float* k = (float*)malloc((size_t)T * dkv * sizeof(float));
@@ -538,9 +538,6 @@ int orc_model_forward(orc_model* m, const int* ids, int T, float* logits)
     const int pos_offset = m->used;                      /* attention.hpp:110 */
     const int causal = (T == 1) ? 0 : 1;                 /* attention.hpp:166-174 */
     const int ctx = m->used + T;
-
-    for (int t = 0; t < T; ++t)                          /* ops.hpp:615-626 */
-        memcpy(x + (size_t)t * D, m->embed + (size_t)ids[t] * D, sizeof(float) * D);
 
     for (int l = 0; l < c->n_layers; ++l) {
         struct orc_layer* L = &m->L[l];
@@ -575,14 +572,30 @@ int orc_model_forward(orc_model* m, const int* ids, int T, float* logits)
         for (size_t i = 0; i < TD; ++i) x[i] += a[i];   /* add_inplace(f, a) */
     }
     m->used += T;
+    free(hn); free(q); free(k); free(v); free(att); free(a);
+    free(u); free(g); free(kd); free(vd);
+    return 0;
+}
+
+int orc_model_forward(orc_model* m, const int* ids, int T, float* logits)
+{
+    const orc_config* c = &m->c;
+    const int D = c->d_model, nt = c->n_threads;
+    if (T <= 0 || m->used + T > c->max_seq_len) return -1;
+    for (int t = 0; t < T; ++t)
+        if (ids[t] < 0 || ids[t] >= c->vocab_size) return -1;
+
+    float* x = (float*)malloc((size_t)T * D * sizeof(float));
+    float* hn = (float*)malloc((size_t)D * sizeof(float));
+    for (int t = 0; t < T; ++t)                          /* ops.hpp:615-626 */
+        memcpy(x + (size_t)t * D, m->embed + (size_t)ids[t] * D, sizeof(float) * D);
+    orc_model_forward_hidden(m, x, T);
 
     orc_rms_norm(x + (size_t)(T - 1) * D, m->ln_final, hn, 1, D, c->norm_eps);
     float* lg = logits ? logits : (float*)malloc(sizeof(float) * (size_t)c->vocab_size);
     orc_linear(hn, m->lm_head, lg, 1, D, c->vocab_size, nt);
     int best = orc_argmax(lg, c->vocab_size);
     if (!logits) free(lg);
-
-    free(x); free(hn); free(q); free(k); free(v); free(att); free(a);
-    free(u); free(g); free(kd); free(vd);
+    free(x); free(hn);
     return best;
 }

@@ -73,6 +73,9 @@ int  orc_model_used(const orc_model* m);
  * KV cache; writes logits of the last row (may be NULL) and returns the greedy
  * argmax, or -1 on error (cache overflow / bad id). */
 int  orc_model_forward(orc_model* m, const int* ids, int T, float* logits);
+/* The layers only: x [T][d_model] embedded rows in, residual stream after the
+ * last layer out (in place); appends T cache rows.  0, or -1 on overflow. */
+int  orc_model_forward_hidden(orc_model* m, float* x, int T);
 /* Token-major reference layout of layer l's cache: K/V int8 [max_seq, row_dim],
  * scales [max_seq]. */
 void orc_model_kv(orc_model* m, int l, int8_t** kq, int8_t** vq, float** ks, float** vs);

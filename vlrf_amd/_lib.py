@@ -70,6 +70,9 @@ _SIGS = {
     "vlrf_hip_model_used": (i32, [vp]),
     "vlrf_hip_model_step": (i32, [vp, i32, C.POINTER(C.c_int32), vp]),
     "vlrf_hip_model_prefill": (i32, [vp, vp, i32, C.POINTER(C.c_int32)]),
+    "vlrf_hip_model_prefill_mfma": (i32, [vp, vp, i32, C.POINTER(C.c_int32)]),
+    "vlrf_hip_model_forward_hidden": (i32, [vp, vp, i32, vp]),
+    "vlrf_hip_model_kv_read": (i32, [vp, i32, i32, i32, vp, vp, vp, vp]),
     "vlrf_hip_model_generate": (i32, [vp, i32, i32, vp]),
     "vlrf_hip_model_generate_async": (i32, [vp, i32, i32]),
     "vlrf_hip_model_read_generated": (i32, [vp, vp, i32]),

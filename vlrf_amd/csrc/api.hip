@@ -189,6 +189,30 @@ struct vlrf_hip_kv {
         VH_CHECK(hipSetDevice((c)->device));                       \
     } while (0)
 
+namespace vlrf_hip {
+// Rows [row0, row0+n) of a head-major cache layer to host, token-major.
+int kv_rows_to_host(hipStream_t s, const KVLayer& L, int G, int D, int max_seq, int row0, int n,
+                    int8_t* k_q, int8_t* v_q, float* k_s, float* v_s) {
+    const int row = G * D;
+    std::vector<int8_t> hk((size_t)G * n * D), hv((size_t)G * n * D);
+    for (int g = 0; g < G; ++g) {
+        const size_t off = ((size_t)g * max_seq + row0) * D;
+        VH_CHECK(hipMemcpyAsync(hk.data() + (size_t)g * n * D, L.k + off, (size_t)n * D, hipMemcpyDeviceToHost, s));
+        VH_CHECK(hipMemcpyAsync(hv.data() + (size_t)g * n * D, L.v + off, (size_t)n * D, hipMemcpyDeviceToHost, s));
+    }
+    if (k_s) VH_CHECK(hipMemcpyAsync(k_s, L.ks + row0, n * sizeof(float), hipMemcpyDeviceToHost, s));
+    if (v_s) VH_CHECK(hipMemcpyAsync(v_s, L.vs + row0, n * sizeof(float), hipMemcpyDeviceToHost, s));
+    VH_CHECK(hipStreamSynchronize(s));
+    for (int t = 0; t < n; ++t)
+        for (int g = 0; g < G; ++g)
+            for (int d = 0; d < D; ++d) {
+                if (k_q) k_q[(size_t)t * row + g * D + d] = hk[((size_t)g * n + t) * D + d];
+                if (v_q) v_q[(size_t)t * row + g * D + d] = hv[((size_t)g * n + t) * D + d];
+            }
+    return VLRF_HIP_OK;
+}
+}  // namespace vlrf_hip
+
 extern "C" {
 
 const char* vlrf_hip_last_error(void) { return g_error.c_str(); }
@@ -424,31 +448,15 @@ int vlrf_hip_kv_append(vlrf_hip_kv_t kv, int layer, const float* k, const float*
     return VLRF_HIP_OK;
 }
 
+
 int vlrf_hip_kv_read(vlrf_hip_kv_t kv, int layer, int row0, int n, int8_t* k_q, int8_t* v_q,
                      float* k_s, float* v_s) {
     VH_ARG(kv != nullptr, "kv_read: null cache");
     VH_CTX(kv->ctx);
     VH_ARG(layer >= 0 && layer < kv->n_layers, "kv_read: layer %d out of range", layer);
     VH_ARG(row0 >= 0 && n >= 0 && row0 + n <= kv->max_seq, "kv_read: rows out of range");
-    const KVLayer& L = kv->layers[layer];
-    const int D = kv->d_head, G = kv->n_kv, row = G * D;
-    hipStream_t s = kv->ctx->stream;
-    std::vector<int8_t> hk((size_t)G * n * D), hv((size_t)G * n * D);
-    for (int g = 0; g < G; ++g) {
-        const size_t off = ((size_t)g * kv->max_seq + row0) * D;
-        VH_CHECK(hipMemcpyAsync(hk.data() + (size_t)g * n * D, L.k + off, (size_t)n * D, hipMemcpyDeviceToHost, s));
-        VH_CHECK(hipMemcpyAsync(hv.data() + (size_t)g * n * D, L.v + off, (size_t)n * D, hipMemcpyDeviceToHost, s));
-    }
-    if (k_s) VH_CHECK(hipMemcpyAsync(k_s, L.ks + row0, n * sizeof(float), hipMemcpyDeviceToHost, s));
-    if (v_s) VH_CHECK(hipMemcpyAsync(v_s, L.vs + row0, n * sizeof(float), hipMemcpyDeviceToHost, s));
-    VH_CHECK(hipStreamSynchronize(s));
-    for (int t = 0; t < n; ++t)
-        for (int g = 0; g < G; ++g)
-            for (int d = 0; d < D; ++d) {
-                if (k_q) k_q[(size_t)t * row + g * D + d] = hk[((size_t)g * n + t) * D + d];
-                if (v_q) v_q[(size_t)t * row + g * D + d] = hv[((size_t)g * n + t) * D + d];
-            }
-    return VLRF_HIP_OK;
+    return kv_rows_to_host(kv->ctx->stream, kv->layers[layer], kv->n_kv, kv->d_head, kv->max_seq, row0, n,
+                           k_q, v_q, k_s, v_s);
 }
 
 int vlrf_hip_kv_dequant(vlrf_hip_kv_t kv, int layer, int ctx_len, float* K_out, float* V_out) {

@@ -76,6 +76,11 @@ struct KVLayer {
     float* vs = nullptr;
 };
 
+// Rows [row0, row0+n) of a head-major cache layer to host in the reference's
+// token-major layout (synchronous).
+int kv_rows_to_host(hipStream_t s, const KVLayer& L, int G, int D, int max_seq, int row0, int n,
+                    int8_t* k_q, int8_t* v_q, float* k_s, float* v_s);
+
 // ---- launchers (all queue on `s`) -----------------------------------------------
 // y[M,N] = (norm_w ? rmsnorm(x) : x) . W^T (+ residual)
 int launch_qlinear(hipStream_t s, const DevWeight& w, const float* x, float* y, int M,
@@ -115,6 +120,18 @@ int launch_rope_append(hipStream_t s, const KVLayer& L, float* q, const float* k
                        const int* pos_dev, const float* cos_t, const float* sin_t);
 int launch_kv_dequant(hipStream_t s, const KVLayer& L, int n_kv, int d_head, int max_seq,
                       int ctx_len, float* K_out, float* V_out);
+// Prefill: RoPE on q (in place) and k of T tokens of a [T][ld] QKV buffer at
+// positions pos0.., then the Q8_0 append of their K/V rows.
+int launch_prefill_rope_append(hipStream_t s, const KVLayer& L, float* qkv, int ld, int T, int n_heads,
+                               int n_kv, int d_head, int max_seq, int pos0, const float* cos_t,
+                               const float* sin_t);
+// x[t] = table[ids[t]] for T device ids
+int launch_embed_rows(hipStream_t s, const float* table, const int* ids, float* x, int T, int D);
+// Causal attention of T new tokens (positions pos0..) over the Q8_0 cache on
+// the matrix cores: q (rotated, f32) read from the [T][ld] QKV buffer, the
+// cache rows [0, pos0+T) dequantized to bf16, out bf16 [T][n_heads*d_head].
+int launch_attn_prefill(hipStream_t s, const float* qkv, int ld, const KVLayer& L, int T, int pos0,
+                        int n_heads, int n_kv, int d_head, int max_seq, float scale, uint16_t* out);
 
 // Decode fusion of the attention kernel (model step): RoPE of q and of the
 // token's k at the device position, and the Q8_0 append of its K/V row.
@@ -153,6 +170,12 @@ int launch_argmax_step(hipStream_t s, const float* logits, int n, int* state, in
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float v) {
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+
+// f32 -> bf16 bits, round to nearest even (finite inputs).
+__device__ __forceinline__ uint32_t bf16_bits(float f) {
+    const uint32_t u = __float_as_uint(f);
+    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
 }
 
 __device__ __forceinline__ float wave_sum(float v) {

@@ -384,6 +384,167 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
     }
 }
 
+// ---- prefill: causal attention of T new tokens on the matrix cores ------------
+// Reference: AttentionBlock::forward with T > 1 (attention.hpp:89-186): the new
+// K/V rows are quantized into the cache first (N6 order), then each query row
+// attends the dequantized cache rows kpos <= qpos (attention.hpp:232,253-261)
+// with scale 1/sqrt(d_h); flash_attn_head's online softmax (attention.hpp:207-309).
+//
+// Design: a workgroup = one KV head g and 32 consecutive query tokens; wave w
+// serves query head g*REP + w, so each K/V tile (64 keys, dequantized to bf16
+// in LDS, V transposed) is shared by the REP heads of the GQA group.  The wave
+// computes S^T = K.Q^T and O^T = V^T.P^T with v_mfma_f32_32x32x16_bf16: in that
+// orientation lane l owns query l%32 (both lane halves), so the softmax max and
+// sum are one cross-half shuffle, the rescale multiplies the lane's own
+// accumulators, and P re-enters the second product through register shuffles.
+constexpr int kPQ = 32, kPK = 64;         // queries per workgroup, keys per tile
+
+template <int D, int REP>
+__global__ __launch_bounds__(64 * REP) void attn_prefill_kernel(
+    const float* __restrict__ qkv, int ld, const int8_t* __restrict__ kq, const int8_t* __restrict__ vq,
+    const float* __restrict__ ks, const float* __restrict__ vs, long head_stride, int T, int pos0,
+    float scale, int n_heads, uint16_t* __restrict__ out) {
+    typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+    typedef float f32x16 __attribute__((ext_vector_type(16)));
+    constexpr int NT = 64 * REP;
+    constexpr int KS = D + 8, VS = kPK + 8;          // padded LDS row strides (bf16)
+    __shared__ __align__(16) __bf16 Ks[kPK * KS];    // K tile [key][d]
+    __shared__ __align__(16) __bf16 Vt[D * VS];      // V tile transposed [d][key]
+
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, hh = lane >> 5, lq = lane & 31;
+    const int g = blockIdx.y, h = g * REP + w;
+    const int q0 = blockIdx.x * kPQ;
+    const int qi = min(q0 + lq, T - 1);              // clamped: rows past T are not stored
+    const int qpos = pos0 + qi;
+    const size_t hb = (size_t)g * head_stride;
+
+    bf16x8 qf[D / 16];                               // B operand: query lq, dims 16kk + 8hh + e
+    {
+        const float* qr = qkv + (size_t)qi * ld + (size_t)h * D;
+#pragma unroll
+        for (int kk = 0; kk < D / 16; ++kk) {
+            const float4 a = *reinterpret_cast<const float4*>(qr + 16 * kk + 8 * hh);
+            const float4 b = *reinterpret_cast<const float4*>(qr + 16 * kk + 8 * hh + 4);
+            qf[kk] = bf16x8{(__bf16)a.x, (__bf16)a.y, (__bf16)a.z, (__bf16)a.w,
+                            (__bf16)b.x, (__bf16)b.y, (__bf16)b.z, (__bf16)b.w};
+        }
+    }
+    f32x16 o[D / 32];
+#pragma unroll
+    for (int c = 0; c < D / 32; ++c) o[c] = f32x16{};
+    float m_run = kNegInf, l_run = 0.f;
+
+    const int qlast = pos0 + min(q0 + kPQ, T) - 1;   // last query position of the workgroup
+    const int kv_end = pos0 + T;                     // cache rows written
+    const int ntile = qlast / kPK + 1;
+    for (int kt = 0; kt < ntile; ++kt) {
+        const int kv0 = kt * kPK;
+        // Stage the tile: 16 dims of one key per item; rows past kv_end are zero.
+        for (int i = threadIdx.x; i < kPK * (D / 16); i += NT) {
+            const int key = i / (D / 16), part = i - key * (D / 16);
+            const int kp = kv0 + key;
+            const bool live = kp < kv_end;
+            const int kr = live ? kp : 0;
+            const uint4 kc = *reinterpret_cast<const uint4*>(kq + hb + (size_t)kr * D + 16 * part);
+            const uint4 vc = *reinterpret_cast<const uint4*>(vq + hb + (size_t)kr * D + 16 * part);
+            const float sk = live ? ks[kr] : 0.f, sv = live ? vs[kr] : 0.f;   // dequantize_row_q8_0
+            const uint32_t ku[4] = {kc.x, kc.y, kc.z, kc.w}, vu[4] = {vc.x, vc.y, vc.z, vc.w};
+            bf16x8 k0, k1;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                k0[e] = (__bf16)((float)(int8_t)(ku[e >> 2] >> (8 * (e & 3))) * sk);
+                k1[e] = (__bf16)((float)(int8_t)(ku[2 + (e >> 2)] >> (8 * (e & 3))) * sk);
+            }
+            *reinterpret_cast<bf16x8*>(&Ks[key * KS + 16 * part]) = k0;
+            *reinterpret_cast<bf16x8*>(&Ks[key * KS + 16 * part + 8]) = k1;
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+                Vt[(16 * part + e) * VS + key] = (__bf16)((float)(int8_t)(vu[e >> 2] >> (8 * (e & 3))) * sv);
+        }
+        __syncthreads();
+
+        // S^T = K . Q^T for the two 32-key blocks of the tile.
+        f32x16 sc[2] = {f32x16{}, f32x16{}};
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int kk = 0; kk < D / 16; ++kk) {
+                const bf16x8 a = *reinterpret_cast<const bf16x8*>(&Ks[(32 * kb + lq) * KS + 16 * kk + 8 * hh]);
+                sc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[kk], sc[kb], 0, 0, 0);
+            }
+        // Scale, causal mask (key r(v) = 8(v/4) + 4hh + v%4 of the block), online softmax.
+        float mx = kNegInf;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int kp = kv0 + 32 * kb + 8 * (v >> 2) + 4 * hh + (v & 3);
+                const float x = kp <= qpos ? sc[kb][v] * scale : kNegInf;
+                sc[kb][v] = x;
+                mx = fmaxf(mx, x);
+            }
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float mn = fmaxf(m_run, mx);           // finite: key 0 is in the first tile
+        const float corr = m_run == kNegInf ? 0.f : expf(m_run - mn);
+        float sum = 0.f;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const float p = sc[kb][v] == kNegInf ? 0.f : expf(sc[kb][v] - mn);
+                sc[kb][v] = p;
+                sum += p;
+            }
+        sum += __shfl_xor(sum, 32);
+        l_run = l_run * corr + sum;
+        m_run = mn;
+#pragma unroll
+        for (int c = 0; c < D / 32; ++c)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) o[c][v] *= corr;
+
+        // O^T += V^T . P^T, 16 keys per step.  The B operand needs keys
+        // 16s + 8hh + e of the lane's query: group 2s+hh of this half and of
+        // the other half (v-groups of 4 keys), exchanged with one xor-32 shuffle.
+#pragma unroll
+        for (int kk2 = 0; kk2 < kPK / 16; ++kk2) {
+            const int kb = kk2 >> 1, s2 = kk2 & 1;
+            const int gown = 2 * s2 + hh, gsend = 2 * s2 + 1 - hh;
+            float y[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) y[e] = __shfl_xor(sc[kb][4 * gsend + e], 32);
+            bf16x8 b;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float mine = sc[kb][4 * gown + e];
+                b[e] = (__bf16)(hh == 0 ? mine : y[e]);
+                b[4 + e] = (__bf16)(hh == 0 ? y[e] : mine);
+            }
+#pragma unroll
+            for (int c = 0; c < D / 32; ++c) {
+                const bf16x8 a = *reinterpret_cast<const bf16x8*>(&Vt[(32 * c + lq) * VS + 16 * kk2 + 8 * hh]);
+                o[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, o[c], 0, 0, 0);
+            }
+        }
+        __syncthreads();                             // before the next tile overwrites Ks / Vt
+    }
+
+    // out[q][h*D + d] = O / l (output acc * (1/l), attention.hpp:300-307), d = 32c + 8(v/4) + 4hh + v%4.
+    if (q0 + lq < T) {
+        const float inv = 1.f / l_run;
+        uint16_t* orow = out + (size_t)(q0 + lq) * n_heads * D + (size_t)h * D;
+#pragma unroll
+        for (int c = 0; c < D / 32; ++c)
+#pragma unroll
+            for (int vg = 0; vg < 4; ++vg) {
+                uint2 pk;
+                pk.x = bf16_bits(o[c][4 * vg] * inv) | (bf16_bits(o[c][4 * vg + 1] * inv) << 16);
+                pk.y = bf16_bits(o[c][4 * vg + 2] * inv) | (bf16_bits(o[c][4 * vg + 3] * inv) << 16);
+                *reinterpret_cast<uint2*>(orow + 32 * c + 8 * vg + 4 * hh) = pk;
+            }
+    }
+}
+
 // ---- general f32 attention: one thread per query row, 64x64 tiles --------------
 template <int D>
 __global__ __launch_bounds__(64) void attn_f32_tiled_kernel(const float* __restrict__ Q,
@@ -537,6 +698,33 @@ int launch_attn_f32_tiled(hipStream_t s, const float* Q, const float* K, const f
     else if (d_h <= 64) VH_AT(64);
     else VH_AT(128);
 #undef VH_AT
+    VH_LAUNCHED();
+    return VLRF_HIP_OK;
+}
+
+int launch_attn_prefill(hipStream_t s, const float* qkv, int ld, const KVLayer& L, int T, int pos0,
+                        int n_heads, int n_kv, int d_head, int max_seq, float scale, uint16_t* out) {
+    VH_ARG(n_kv > 0 && n_heads % n_kv == 0, "attn_prefill: n_heads %d not a multiple of n_kv %d", n_heads, n_kv);
+    const int rep = n_heads / n_kv;
+    VH_ARG(d_head == 64 || d_head == 128, "attn_prefill: d_head %d not in {64,128}", d_head);
+    VH_ARG(rep == 1 || rep == 2 || rep == 4 || rep == 8, "attn_prefill: GQA group %d not in {1,2,4,8}", rep);
+    VH_ARG(T >= 1 && pos0 >= 0 && pos0 + T <= max_seq, "attn_prefill: positions [%d,%d) outside the cache",
+           pos0, pos0 + T);
+    VH_ARG(ld % 4 == 0, "attn_prefill: row stride %d not a multiple of 4", ld);
+    dim3 grid((T + kPQ - 1) / kPQ, n_kv);
+#define VH_AP(D, R)                                                                                   \
+    hipLaunchKernelGGL((attn_prefill_kernel<D, R>), grid, dim3(64 * R), 0, s, qkv, ld, L.k, L.v, L.ks, \
+                       L.vs, (long)max_seq * d_head, T, pos0, scale, n_heads, out)
+#define VH_AP_R(D)                      \
+    switch (rep) {                      \
+        case 1: VH_AP(D, 1); break;     \
+        case 2: VH_AP(D, 2); break;     \
+        case 4: VH_AP(D, 4); break;     \
+        default: VH_AP(D, 8); break;    \
+    }
+    if (d_head == 64) { VH_AP_R(64) } else { VH_AP_R(128) }
+#undef VH_AP_R
+#undef VH_AP
     VH_LAUNCHED();
     return VLRF_HIP_OK;
 }

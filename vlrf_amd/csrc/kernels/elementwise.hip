@@ -117,6 +117,47 @@ __global__ __launch_bounds__(256) void rope_append_kernel(int8_t* kq, int8_t* vq
     quantize_row_to_cache(v, vq, vs, p, n_kv, D, max_seq, red);
 }
 
+// Prefill: token t of a [T][ld] QKV buffer (q: n_heads*D at column 0, k and v:
+// n_kv*D each after it) at position pos0 + t: q rotated in place, k rotated,
+// then the K and V rows quantized into the cache (attention.hpp:109-128 order).
+__global__ __launch_bounds__(256) void prefill_rope_append_kernel(
+    int8_t* kq, int8_t* vq, float* ks, float* vs, float* qkv, int ld, int n_heads, int n_kv, int D,
+    int max_seq, int pos0, const float* __restrict__ cos_t, const float* __restrict__ sin_t) {
+    __shared__ float red[4];
+    __shared__ float kr[1024];
+    const int t = blockIdx.x, p = pos0 + t;
+    if (p < 0 || p >= max_seq) return;   // host checks capacity; never write past the cache
+    const int half = D / 2, row = n_kv * D;
+    float* q = qkv + (size_t)t * ld;
+    const float* k = q + (size_t)n_heads * D;
+    const float* v = k + row;
+    const float* c = cos_t + (size_t)p * half;
+    const float* s = sin_t + (size_t)p * half;
+    for (int i = threadIdx.x; i < row; i += 256) kr[i] = k[i];
+    __syncthreads();
+    for (int i = threadIdx.x; i < n_heads * half; i += 256) {
+        const int h = i / half, j = i - h * half;
+        rope_pair(q + (size_t)h * D, j, half, c[j], s[j]);
+    }
+    for (int i = threadIdx.x; i < n_kv * half; i += 256) {
+        const int h = i / half, j = i - h * half;
+        rope_pair(kr + h * D, j, half, c[j], s[j]);
+    }
+    __syncthreads();
+    quantize_row_to_cache(kr, kq, ks, p, n_kv, D, max_seq, red);
+    quantize_row_to_cache(v, vq, vs, p, n_kv, D, max_seq, red);
+}
+
+// x[t] = table[ids[t]] (ops.hpp:615-626), one workgroup per token.
+__global__ __launch_bounds__(256) void embed_rows_kernel(const float* __restrict__ table,
+                                                         const int* __restrict__ ids, float* __restrict__ x,
+                                                         int D) {
+    const int t = blockIdx.x;
+    const float4* src = reinterpret_cast<const float4*>(table + (size_t)ids[t] * D);
+    float4* dst = reinterpret_cast<float4*>(x + (size_t)t * D);
+    for (int i = threadIdx.x; i < D / 4; i += 256) dst[i] = src[i];
+}
+
 __global__ __launch_bounds__(256) void kv_dequant_kernel(const int8_t* __restrict__ kq,
                                                          const int8_t* __restrict__ vq,
                                                          const float* __restrict__ ks,
@@ -244,6 +285,26 @@ int launch_rope_append(hipStream_t s, const KVLayer& L, float* q, const float* k
     VH_ARG(d_head % 2 == 0, "rope_append: odd d_head");
     hipLaunchKernelGGL(rope_append_kernel, dim3(1), dim3(256), 0, s, L.k, L.v, L.ks, L.vs, q, k, v,
                        n_heads, n_kv, d_head, max_seq, pos_dev, cos_t, sin_t);
+    VH_LAUNCHED();
+    return VLRF_HIP_OK;
+}
+
+int launch_prefill_rope_append(hipStream_t s, const KVLayer& L, float* qkv, int ld, int T, int n_heads,
+                               int n_kv, int d_head, int max_seq, int pos0, const float* cos_t,
+                               const float* sin_t) {
+    VH_ARG(n_kv * d_head <= 1024, "prefill_rope_append: kv row %d exceeds 1024", n_kv * d_head);
+    VH_ARG(d_head % 2 == 0 && T >= 1, "prefill_rope_append: bad shape");
+    VH_ARG(pos0 >= 0 && pos0 + T <= max_seq, "prefill_rope_append: positions [%d,%d) outside the cache",
+           pos0, pos0 + T);
+    hipLaunchKernelGGL(prefill_rope_append_kernel, dim3(T), dim3(256), 0, s, L.k, L.v, L.ks, L.vs, qkv, ld,
+                       n_heads, n_kv, d_head, max_seq, pos0, cos_t, sin_t);
+    VH_LAUNCHED();
+    return VLRF_HIP_OK;
+}
+
+int launch_embed_rows(hipStream_t s, const float* table, const int* ids, float* x, int T, int D) {
+    VH_ARG(T >= 1 && D % 4 == 0, "embed_rows: bad shape");
+    hipLaunchKernelGGL(embed_rows_kernel, dim3(T), dim3(256), 0, s, table, ids, x, D);
     VH_LAUNCHED();
     return VLRF_HIP_OK;
 }

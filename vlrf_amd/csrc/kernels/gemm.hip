@@ -29,11 +29,6 @@ constexpr int kBM = 128, kBN = 128, kBK = 64;
 constexpr int kGemmThreads = 256;
 constexpr int kLds = kBK + 8;            // bf16 per LDS row (16 bytes of padding)
 
-// f32 -> bf16 bits, round to nearest even (finite inputs).
-__device__ __forceinline__ uint32_t bf16_bits(float f) {
-    const uint32_t u = __float_as_uint(f);
-    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
-}
 __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
     return bf16_bits(lo) | (bf16_bits(hi) << 16);
 }

@@ -66,6 +66,14 @@ struct vlrf_hip_model {
     hipGraphExec_t exec = nullptr;
     bool use_graph = true;     // VLRF_HIP_GRAPH=0: queue the step's kernels directly
     int pos = 0;               // host mirror of state[1]
+    // Batched prefill (matrix cores) work buffers, sized for pf_cap rows.
+    int pf_cap = 0;
+    float* pf_x = nullptr;         // [T][D] residual stream
+    float* pf_qkv = nullptr;       // [T][D + 2*dkv]
+    uint16_t* pf_a = nullptr;      // [T][D] bf16 normalised rows
+    uint16_t* pf_att = nullptr;    // [T][D] bf16 attention output
+    uint16_t* pf_h = nullptr;      // [T][F] bf16 SwiGLU output
+    int* pf_ids = nullptr;         // [T]
 
     bool ready() const {
         if (!embed_set || !ln_final_set || !lm_head_set) return false;
@@ -267,6 +275,9 @@ void vlrf_hip_model_destroy(vlrf_hip_model_t m) {
                     (void*)m->h, (void*)m->logits, (void*)m->part, (void*)m->state,
                     (void*)m->gen_ids, (void*)m->prompt})
         if (p) (void)hipFree(p);
+    for (void* p : {(void*)m->pf_x, (void*)m->pf_qkv, (void*)m->pf_a, (void*)m->pf_att, (void*)m->pf_h,
+                    (void*)m->pf_ids})
+        if (p) (void)hipFree(p);
     if (m->pinned) (void)hipHostFree(m->pinned);
     delete m;
 }
@@ -407,6 +418,128 @@ int vlrf_hip_model_prefill(vlrf_hip_model_t m, const int32_t* ids, int n, int32_
     m->pos += n;
     if (next) *next = m->pinned[0];
     return VLRF_HIP_OK;
+}
+
+namespace {
+
+// Grows the batched-prefill buffers to hold T rows (waits for queued work first).
+int prefill_reserve(vlrf_hip_model* m, int T) {
+    if (T <= m->pf_cap) return VLRF_HIP_OK;
+    VH_CHECK(hipStreamSynchronize(m->ctx->stream));
+    for (void** p : {(void**)&m->pf_x, (void**)&m->pf_qkv, (void**)&m->pf_a, (void**)&m->pf_att,
+                     (void**)&m->pf_h, (void**)&m->pf_ids}) {
+        if (*p) (void)hipFree(*p);
+        *p = nullptr;
+    }
+    m->pf_cap = 0;
+    const size_t t = (size_t)T;
+    const size_t sizes[6] = {t * m->D * 4, t * (m->D + 2 * m->dkv) * 4, t * m->D * 2, t * m->D * 2,
+                             t * m->F * 2, t * 4};
+    void** ptrs[6] = {(void**)&m->pf_x, (void**)&m->pf_qkv, (void**)&m->pf_a, (void**)&m->pf_att,
+                      (void**)&m->pf_h, (void**)&m->pf_ids};
+    for (int i = 0; i < 6; ++i) {
+        if (hipMalloc(ptrs[i], sizes[i]) != hipSuccess) {
+            set_error("prefill: hipMalloc(%zu) failed", sizes[i]);
+            return VLRF_HIP_ERR_NOMEM;
+        }
+    }
+    m->pf_cap = T;
+    return VLRF_HIP_OK;
+}
+
+// All layers over T embedded rows x (device [T][D], updated in place) at cache
+// positions m->pos..: TransformerBlock::forward_v2 pre-norm order
+// (transformer_block.hpp:141-159) with AttentionBlock::forward's T > 1 path
+// (attention.hpp:89-186: RoPE, K/V appended to the cache, causal attention).
+int enqueue_prefill_layers(vlrf_hip_model* m, float* x, int T) {
+    hipStream_t s = m->ctx->stream;
+    const float eps = m->cfg.norm_eps;
+    const float scale = 1.f / std::sqrt((float)m->dh);          // attention.hpp:373-374
+    const int ld = m->D + 2 * m->dkv;
+    int rc = VLRF_HIP_OK;
+    for (int l = 0; l < m->L && !rc; ++l) {
+        Layer& Ly = m->layers[l];
+        rc = launch_rows_to_bf16(s, x, Ly.ln1, m->pf_a, T, m->D, eps);
+        if (!rc) rc = launch_qgemm(s, Ly.wqkv, m->pf_a, T, nullptr, m->pf_qkv);
+        if (!rc) rc = launch_prefill_rope_append(s, Ly.kv, m->pf_qkv, ld, T, m->H, m->G, m->dh, m->S, m->pos,
+                                                 m->cos_t, m->sin_t);
+        if (!rc) rc = launch_attn_prefill(s, m->pf_qkv, ld, Ly.kv, T, m->pos, m->H, m->G, m->dh, m->S, scale,
+                                          m->pf_att);
+        if (!rc) rc = launch_qgemm(s, Ly.wo, m->pf_att, T, x, x);              // x += att . Wo^T
+        if (!rc) rc = launch_rows_to_bf16(s, x, Ly.ln2, m->pf_a, T, m->D, eps);
+        if (!rc) rc = launch_qgemm_swiglu(s, Ly.wg, Ly.wu, m->pf_a, T, m->pf_h, true);
+        if (!rc) rc = launch_qgemm(s, Ly.wd, m->pf_h, T, x, x);                // x += h . Wd^T
+    }
+    return rc;
+}
+
+int check_prefill(vlrf_hip_model* m, int T) {
+    int rc = check_ready(m);
+    if (rc) return rc;
+    VH_ARG(T >= 1, "prefill: no rows");
+    VH_ARG(m->cfg.weight_dtype == VLRF_DT_Q8_0 || m->cfg.weight_dtype == VLRF_DT_Q4_0,
+           "prefill_mfma: needs Q8_0/Q4_0 weights (dtype %d)", m->cfg.weight_dtype);
+    VH_ARG(m->D % 64 == 0 && m->F % 64 == 0, "prefill_mfma: d_model %d / d_ff %d not multiples of 64",
+           m->D, m->F);
+    if (m->pos + T > m->S) {
+        set_error("KVCache::append: exceeds max_seq_len (%d + %d > %d)", m->pos, T, m->S);
+        return VLRF_HIP_ERR_OVERFLOW;
+    }
+    return prefill_reserve(m, T);
+}
+
+}  // namespace
+
+int vlrf_hip_model_forward_hidden(vlrf_hip_model_t m, const float* x, int T, float* out) {
+    int rc = check_prefill(m, T);
+    if (rc) return rc;
+    VH_ARG(x && out, "forward_hidden: null buffer");
+    hipStream_t s = m->ctx->stream;
+    VH_CHECK(hipMemcpyAsync(m->pf_x, x, (size_t)T * m->D * 4, hipMemcpyDeviceToDevice, s));
+    if ((rc = enqueue_prefill_layers(m, m->pf_x, T))) return rc;
+    VH_CHECK(hipMemcpyAsync(out, m->pf_x, (size_t)T * m->D * 4, hipMemcpyDeviceToDevice, s));
+    m->pos += T;
+    m->pinned[0] = 0;
+    m->pinned[1] = m->pos;
+    m->pinned[2] = 0;
+    VH_CHECK(hipMemcpyAsync(m->state, m->pinned, 3 * sizeof(int), hipMemcpyHostToDevice, s));
+    VH_CHECK(hipStreamSynchronize(s));
+    return VLRF_HIP_OK;
+}
+
+int vlrf_hip_model_prefill_mfma(vlrf_hip_model_t m, const int32_t* ids, int n, int32_t* next) {
+    int rc = check_prefill(m, n);
+    if (rc) return rc;
+    VH_ARG(ids != nullptr, "prefill_mfma: null ids");
+    for (int i = 0; i < n; ++i)
+        VH_ARG(ids[i] >= 0 && ids[i] < m->V, "prefill_mfma: token %d outside [0,%d)", ids[i], m->V);
+    hipStream_t s = m->ctx->stream;
+    VH_CHECK(hipMemcpyAsync(m->pf_ids, ids, (size_t)n * sizeof(int), hipMemcpyHostToDevice, s));
+    if ((rc = launch_embed_rows(s, m->embed, m->pf_ids, m->pf_x, n, m->D))) return rc;   // ops.hpp:615-626
+    if ((rc = enqueue_prefill_layers(m, m->pf_x, n))) return rc;
+    // transformer.hpp:399-414: final norm and LM head on the last row, greedy argmax.
+    if ((rc = launch_qlinear(s, m->lm_head, m->pf_x + (size_t)(n - 1) * m->D, m->logits, 1, m->ln_final,
+                             m->cfg.norm_eps, nullptr)))
+        return rc;
+    if ((rc = launch_argmax_step(s, m->logits, m->V, m->state, m->gen_ids, m->S))) return rc;
+    VH_CHECK(hipMemcpyAsync(m->pinned, m->state, sizeof(int), hipMemcpyDeviceToHost, s));
+    VH_CHECK(hipStreamSynchronize(s));
+    if (next) *next = m->pinned[0];
+    m->pos += n;
+    m->pinned[1] = m->pos;
+    m->pinned[2] = 0;
+    VH_CHECK(hipMemcpyAsync(m->state + 1, m->pinned + 1, 2 * sizeof(int), hipMemcpyHostToDevice, s));
+    VH_CHECK(hipStreamSynchronize(s));
+    return VLRF_HIP_OK;
+}
+
+int vlrf_hip_model_kv_read(vlrf_hip_model_t m, int layer, int row0, int n, int8_t* k_q, int8_t* v_q,
+                           float* k_s, float* v_s) {
+    VH_ARG(m != nullptr, "model_kv_read: null handle");
+    VH_ARG(layer >= 0 && layer < m->L, "model_kv_read: layer %d out of range", layer);
+    VH_ARG(row0 >= 0 && n >= 0 && row0 + n <= m->S, "model_kv_read: rows out of range");
+    VH_CHECK(hipSetDevice(m->ctx->device));
+    return kv_rows_to_host(m->ctx->stream, m->layers[layer].kv, m->G, m->dh, m->S, row0, n, k_q, v_q, k_s, v_s);
 }
 
 int vlrf_hip_model_generate_async(vlrf_hip_model_t m, int32_t first, int n_steps) {

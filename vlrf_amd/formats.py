@@ -53,6 +53,15 @@ def llama_1b(max_seq_len=2048 + 128, weight_dtype=DT_Q8_0):
                 weight_dtype=weight_dtype)
 
 
+def llama8b_layer(weight_dtype=DT_Q8_0, max_seq_len=2048, n_layers=1, vocab_size=256):
+    """One Llama-8B-shape decoder layer (the prefill benchmark configuration:
+    hidden 4096, 32/8 heads, head_dim 128, FFN 14336 SwiGLU).  The vocabulary
+    is small: the layer's input is given as embedded rows."""
+    return dict(vocab_size=vocab_size, d_model=4096, d_ff=14336, n_heads=32, n_kv_heads=8,
+                n_layers=n_layers, max_seq_len=max_seq_len, norm_eps=1e-5, rope_theta=10000.0,
+                weight_dtype=weight_dtype)
+
+
 def tiny(weight_dtype=DT_Q8_0, n_layers=2, max_seq_len=160):
     """A small configuration with the same structure (GQA 4:1, d_head 64)."""
     return dict(vocab_size=512, d_model=256, d_ff=704, n_heads=4, n_kv_heads=1,

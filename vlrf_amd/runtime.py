@@ -235,6 +235,31 @@ class Model:
         check(lib().vlrf_hip_model_prefill(self.h, ids.ctypes.data, ids.size, C.byref(nxt)))
         return nxt.value
 
+    def prefill_mfma(self, ids):
+        """Batched prefill on the matrix cores (bf16 GEMMs and attention)."""
+        ids = np.ascontiguousarray(ids, np.int32)
+        nxt = C.c_int32()
+        check(lib().vlrf_hip_model_prefill_mfma(self.h, ids.ctypes.data, ids.size, C.byref(nxt)))
+        return nxt.value
+
+    def forward_hidden(self, x, out=None):
+        """All layers over embedded rows x (DeviceBuffer [T][d_model]); returns
+        the output DeviceBuffer (out, or a new one)."""
+        T = x.nbytes // (4 * self.cfg["d_model"])
+        out = out if out is not None else self.ctx.alloc(x.nbytes)
+        check(lib().vlrf_hip_model_forward_hidden(self.h, x.ptr, T, out.ptr))
+        return out
+
+    def kv_rows(self, layer, row0, n):
+        """(K int8 [n,row], V int8, K scales [n], V scales) of the model's cache."""
+        c = self.cfg
+        row = c["n_kv_heads"] * (c["d_model"] // c["n_heads"])
+        kq, vq = np.zeros((n, row), np.int8), np.zeros((n, row), np.int8)
+        ks, vs = np.zeros(n, np.float32), np.zeros(n, np.float32)
+        check(lib().vlrf_hip_model_kv_read(self.h, layer, row0, n, kq.ctypes.data, vq.ctypes.data,
+                                           ks.ctypes.data, vs.ctypes.data))
+        return kq, vq, ks, vs
+
     def generate_ids(self, first, n_steps):
         out = np.zeros(n_steps, np.int32)
         check(lib().vlrf_hip_model_generate(self.h, int(first), n_steps, out.ctypes.data))
