@@ -23,6 +23,14 @@ dequant, per-head flash attention) on the host's cores at context 2048.
 
     python bench.py [--gpus 1] [--steps 128] [--warmup 8] [--dtype q8_0|q4_0]
     python bench.py --roofline-only     # copy calibration + roofline launches only
+    python bench.py --prefill           # config 5: one Llama-8B-shape layer, T=2048 prefill
+
+--prefill prints its own line: one Llama-8B-shape
+layer (hidden 4096, 32/8 heads, head_dim 128, FFN 14336 SwiGLU, Q8_0 weights)
+over a causal 2048-token prompt of N(0,1) embedded rows, on the matrix cores
+(bf16 operands, f32 accumulation), each run from an empty cache.  FLOPs per
+layer = 2*T*(D*(D+2*dkv) + D*D + 3*D*F) + 4*H*d*T*T/2 = 927.7 GFLOP; the
+roofline is the dense bf16 MFMA peak (2.5 PFLOP/s).
 """
 import argparse
 import json
@@ -101,6 +109,56 @@ def copy_calibration(ctx):
     dst.free()
 
 
+MFMA_BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 matrix peak
+
+
+def prefill_flops(cfg, T):
+    D, F, H = cfg["d_model"], cfg["d_ff"], cfg["n_heads"]
+    dh = D // H
+    dkv = cfg["n_kv_heads"] * dh
+    gemm = 2.0 * T * (D * (D + 2 * dkv) + D * D + 3 * D * F)
+    attn = 4.0 * H * dh * T * T / 2          # QK^T and PV over the causal half
+    return gemm + attn
+
+
+def prefill_bench(a, V, F):
+    """One Llama-8B-shape layer, T-token causal prefill (MFMA path)."""
+    dtype = V.DT_Q8_0 if a.dtype == "q8_0" else V.DT_Q4_0
+    T = a.prefill_tokens
+    cfg = F.llama8b_layer(dtype, max_seq_len=T)
+    ctx = V.Context(0)
+    log("[prefill]", ctx.device_info())
+    t0 = time.time()
+    model = V.Model(ctx, cfg)
+    F.load_model(model, a.seed)
+    log(f"[prefill] weights generated and uploaded in {time.time() - t0:.1f}s")
+    x = ctx.to_device(F.normal(a.seed, "prefill.x", T * cfg["d_model"]))
+    out = ctx.alloc(T * cfg["d_model"] * 4)
+    times = []
+    for i in range(a.warmup + a.steps):
+        model.reset()
+        ctx.timer_start()
+        model.forward_hidden(x, out)
+        ms = ctx.timer_stop()
+        if i >= a.warmup:
+            times.append(ms)
+    ms = float(np.mean(times))
+    fl = prefill_flops(cfg, T)
+    tflops = fl / (ms / 1e3) / 1e12
+    return {
+        "metric": "prefill TFLOP/s of one Llama-8B-shape layer, T=%d" % T,
+        "value": round(tflops, 1), "unit": "TFLOP/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16 operands, f32 accumulate, %s weights, q8_0 KV" % a.dtype,
+        "data": "synthetic: seeded N(0,0.02) weights, N(0,1) embedded rows",
+        "config": {"workload": "llama-8B-shape layer prefill, causal T=%d from an empty cache" % T,
+                   "weights": a.dtype, "hidden": 4096, "ffn": 14336, "heads": "32/8", "head_dim": 128},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
+                     "flops_per_step": fl},
+    }
+
+
 def cpu_baseline(cfg, f32w, ctx_len, budget_s=12.0, max_steps=8):
     """Oracle decode steps at context ctx_len on the host cores."""
     import oracle
@@ -140,6 +198,9 @@ def main():
     ap.add_argument("--no-roofline", action="store_true")
     ap.add_argument("--roofline-only", action="store_true",
                     help="run the copy calibration and the roofline launches only (PMC passes)")
+    ap.add_argument("--prefill", action="store_true",
+                    help="config 5: one Llama-8B-shape layer prefill on the matrix cores")
+    ap.add_argument("--prefill-tokens", type=int, default=2048)
     a = ap.parse_args()
 
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -149,6 +210,12 @@ def main():
 
     import vlrf_amd as V
     from vlrf_amd import formats as F
+
+    if a.prefill:
+        if a.steps == 128:           # the decode default; a layer prefill is ~ms
+            a.steps = 10
+        print(json.dumps(prefill_bench(a, V, F)), flush=True)
+        return
 
     dtype = V.DT_Q8_0 if a.dtype == "q8_0" else V.DT_Q4_0
     cfg = F.llama_1b(max_seq_len=a.ctx + a.steps, weight_dtype=dtype)
