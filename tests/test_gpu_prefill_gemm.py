@@ -22,7 +22,10 @@ def _weight(ctx, seed, name, N, K, dtype):
 
 
 @pytest.mark.parametrize("dtype", [V.DT_Q8_0, V.DT_Q4_0])
-@pytest.mark.parametrize("M,N,K", [(256, 6144, 4096), (128, 4096, 14336), (2048, 1024, 4096)])
+# Tile selection: M <= 128 -> 128-row tiles; 257..512 tiles of 256x128 -> the two-per-CU
+# configuration (520 x 16600: 390 tiles); otherwise 256x128 tiles, one per CU.
+@pytest.mark.parametrize("M,N,K", [(256, 6144, 4096), (128, 4096, 14336), (2048, 1024, 4096),
+                                   (520, 16600, 64)])
 def test_prefill_gemm_config5_shapes(ctx, orc, dtype, M, N, K):
     """The 8B-layer projections (QKV 6144x4096, down 4096x14336) at prompt rows."""
     print(f"[case] qgemm dtype={dtype} M={M} N={N} K={K}", flush=True)
@@ -34,7 +37,8 @@ def test_prefill_gemm_config5_shapes(ctx, orc, dtype, M, N, K):
     assert rel_err(dy.download((M, N)), ref) <= TOL
 
 
-@pytest.mark.parametrize("M,N,K", [(17, 37, 64), (200, 300, 128), (129, 130, 704), (300, 256, 2048)])
+@pytest.mark.parametrize("M,N,K", [(17, 37, 64), (200, 300, 128), (129, 130, 704), (300, 256, 2048),
+                                   (1000, 8300, 192)])
 def test_prefill_gemm_ragged_with_norm_and_residual(ctx, orc, M, N, K):
     """Row/column counts off the 128x128 tile, with the fused RMSNorm prologue
     and the residual epilogue (in place on the residual)."""
@@ -50,9 +54,11 @@ def test_prefill_gemm_ragged_with_norm_and_residual(ctx, orc, M, N, K):
 
 
 @pytest.mark.parametrize("dtype", [V.DT_Q8_0, V.DT_Q4_0])
-def test_prefill_swiglu(ctx, orc, dtype):
-    """h = silu(x.Wg^T) * (x.Wu^T) at M = 192 rows (feedforward.hpp:54-62)."""
-    M, Fd, K = 192, 1408, 1024
+@pytest.mark.parametrize("M", [100, 192])
+def test_prefill_swiglu(ctx, orc, dtype, M):
+    """h = silu(x.Wg^T) * (x.Wu^T) at M rows (feedforward.hpp:54-62); M = 100 takes
+    the 128-row tiles, M = 192 the 256-row ones."""
+    Fd, K = 1408, 1024
     wg, gdec = _weight(ctx, 23, "PWg", Fd, K, dtype)
     wu, udec = _weight(ctx, 23, "PWu", Fd, K, dtype)
     x = F.normal(23, "psx", M * K).reshape(M, K)

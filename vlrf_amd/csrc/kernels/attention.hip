@@ -538,8 +538,8 @@ __global__ __launch_bounds__(64 * REP) void attn_prefill_kernel(
 #pragma unroll
             for (int vg = 0; vg < 4; ++vg) {
                 uint2 pk;
-                pk.x = bf16_bits(o[c][4 * vg] * inv) | (bf16_bits(o[c][4 * vg + 1] * inv) << 16);
-                pk.y = bf16_bits(o[c][4 * vg + 2] * inv) | (bf16_bits(o[c][4 * vg + 3] * inv) << 16);
+                pk.x = pack_bf16(o[c][4 * vg] * inv, o[c][4 * vg + 1] * inv);
+                pk.y = pack_bf16(o[c][4 * vg + 2] * inv, o[c][4 * vg + 3] * inv);
                 *reinterpret_cast<uint2*>(orow + 32 * c + 8 * vg + 4 * hh) = pk;
             }
     }

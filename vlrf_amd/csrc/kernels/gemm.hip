@@ -25,74 +25,102 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int kBM = 128, kBN = 128, kBK = 64;
-constexpr int kGemmThreads = 256;
-constexpr int kLds = kBK + 8;            // bf16 per LDS row (16 bytes of padding)
+// Tile configuration: BM x BN tile of C per workgroup, K steps of BK, WM x WN
+// waves each owning a (BM/WM) x (BN/WN) block of 32x32 MFMA tiles.
+template <int BM_, int BN_, int BK_, int WM_, int WN_>
+struct TileCfg {
+    static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_;
+    static constexpr int NT = 64 * WM * WN;
+    static constexpr int LDS = BK + 8;            // bf16 per LDS row (16 bytes of padding)
+    static constexpr int EA = BM * BK / NT;       // A elements (bf16) staged per thread
+    static constexpr int EB = BN * BK / NT;       // weight elements staged per thread (per matrix)
+    static constexpr int MI = BM / WM / 32, NI = BN / WN / 32;
+    static_assert(EA % 8 == 0 && BK % EA == 0, "A staging granularity");
+    static_assert((EB == 8 || EB == 16 || EB == 32) && BK % EB == 0, "weight staging granularity");
+    static_assert(MI >= 1 && NI >= 1 && BK % 32 == 0, "tile shape");
+};
 
-__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
-    return bf16_bits(lo) | (bf16_bits(hi) << 16);
+// Raw weight bytes of EB elements: Q8_0 one byte each, Q4_0 a nibble each.
+template <int WT, int EB>
+struct WBytes { static constexpr int DW = WT == VLRF_DT_Q8_0 ? EB / 4 : EB / 8; };
+
+template <int DW>
+__device__ __forceinline__ void load_dwords(uint32_t (&o)[DW], const uint8_t* p) {
+    if constexpr (DW == 8) {
+        const uint4 a = reinterpret_cast<const uint4*>(p)[0], b = reinterpret_cast<const uint4*>(p)[1];
+        o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w; o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
+    } else if constexpr (DW == 4) {
+        const uint4 a = *reinterpret_cast<const uint4*>(p);
+        o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
+    } else if constexpr (DW == 2) {
+        const uint2 a = *reinterpret_cast<const uint2*>(p);
+        o[0] = a.x; o[1] = a.y;
+    } else {
+        o[0] = *reinterpret_cast<const uint32_t*>(p);
+    }
 }
 
 // One K step of global operands held in registers between load and LDS store.
-// Thread t covers row t/2 of the tile and half t%2 of the 64 columns.
-template <int WT, int NM>
+template <class C, int WT, int NM>
 struct GemmStage {
-    uint4 a[4];                          // 32 bf16 of A
-    uint4 w[NM][WT == VLRF_DT_Q8_0 ? 2 : 1];   // 32 codes (Q8_0) or 32 nibbles (Q4_0)
+    uint4 a[C::EA / 8];
+    uint32_t w[NM][WBytes<WT, C::EB>::DW];
     uint32_t s[NM];                      // raw f16 scale of the 32-element block
 };
 
-template <int WT, int NM>
-__device__ __forceinline__ void gemm_load(GemmStage<WT, NM>& st, const uint16_t* __restrict__ A,
+template <class C, int WT, int NM>
+__device__ __forceinline__ void gemm_load(GemmStage<C, WT, NM>& st, const uint16_t* __restrict__ A,
                                           const uint8_t* qa, const __half* da, const uint8_t* qb,
                                           const __half* db, int m0, int n0, int k0, int M, int N, int K) {
-    const int t = threadIdx.x, r = t >> 1, hf = t & 1;
-    const int am = min(m0 + r, M - 1), wn = min(n0 + r, N - 1);   // clamped: rows past M/N are not stored
-    const uint4* ap = reinterpret_cast<const uint4*>(A + (size_t)am * K + k0 + 32 * hf);
+    const int t = threadIdx.x;
+    {
+        const int r = t / (C::BK / C::EA), pa = t % (C::BK / C::EA);
+        const int am = min(m0 + r, M - 1);          // clamped: rows past M are not stored
+        const uint4* ap = reinterpret_cast<const uint4*>(A + (size_t)am * K + k0 + pa * C::EA);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) st.a[i] = ap[i];
+        for (int i = 0; i < C::EA / 8; ++i) st.a[i] = ap[i];
+    }
+    const int r = t / (C::BK / C::EB), pb = t % (C::BK / C::EB);
+    const int wn = min(n0 + r, N - 1);              // clamped: rows past N are not stored
+    const int kb = k0 + pb * C::EB;                 // first element; one 32-block per thread
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
         const uint8_t* q = m ? qb : qa;
         const uint16_t* d = reinterpret_cast<const uint16_t*>(m ? db : da);
-        if constexpr (WT == VLRF_DT_Q8_0) {
-            const uint4* wp = reinterpret_cast<const uint4*>(q + (size_t)wn * K + k0 + 32 * hf);
-            st.w[m][0] = wp[0];
-            st.w[m][1] = wp[1];
-        } else {
-            st.w[m][0] = *reinterpret_cast<const uint4*>(q + (size_t)wn * (K / 2) + (k0 + 32 * hf) / 2);
-        }
-        st.s[m] = d[(size_t)wn * (K / 32) + k0 / 32 + hf];
+        if constexpr (WT == VLRF_DT_Q8_0) load_dwords(st.w[m], q + (size_t)wn * K + kb);
+        else load_dwords(st.w[m], q + (size_t)wn * (K / 2) + kb / 2);
+        st.s[m] = d[(size_t)wn * (K / 32) + kb / 32];
     }
 }
 
-template <int WT, int NM>
-__device__ __forceinline__ void gemm_store(const GemmStage<WT, NM>& st, uint16_t* As, uint16_t* Bs) {
-    const int t = threadIdx.x, r = t >> 1, hf = t & 1;
-    uint4* ad = reinterpret_cast<uint4*>(As + r * kLds + 32 * hf);
+template <class C, int WT, int NM>
+__device__ __forceinline__ void gemm_store(const GemmStage<C, WT, NM>& st, uint16_t* As, uint16_t* Bs) {
+    const int t = threadIdx.x;
+    {
+        const int r = t / (C::BK / C::EA), pa = t % (C::BK / C::EA);
+        uint4* ad = reinterpret_cast<uint4*>(As + r * C::LDS + pa * C::EA);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) ad[i] = st.a[i];
+        for (int i = 0; i < C::EA / 8; ++i) ad[i] = st.a[i];
+    }
+    const int r = t / (C::BK / C::EB), pb = t % (C::BK / C::EB);
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
         const float sc = __half2float(__ushort_as_half((unsigned short)st.s[m]));
-        float v[32];
+        float v[C::EB];
         if constexpr (WT == VLRF_DT_Q8_0) {
-            const uint32_t u[8] = {st.w[m][0].x, st.w[m][0].y, st.w[m][0].z, st.w[m][0].w,
-                                   st.w[m][1].x, st.w[m][1].y, st.w[m][1].z, st.w[m][1].w};
 #pragma unroll
-            for (int j = 0; j < 32; ++j) v[j] = (float)(int8_t)(u[j >> 2] >> (8 * (j & 3))) * sc;
+            for (int j = 0; j < C::EB; ++j) v[j] = (float)(int8_t)(st.w[m][j >> 2] >> (8 * (j & 3))) * sc;
         } else {
-            const uint32_t u[4] = {st.w[m][0].x, st.w[m][0].y, st.w[m][0].z, st.w[m][0].w};
 #pragma unroll
-            for (int j = 0; j < 16; ++j) {    // byte j: element 2j (low nibble), 2j+1 (high)
-                const uint32_t b = (u[j >> 2] >> (8 * (j & 3))) & 0xFFu;
+            for (int j = 0; j < C::EB / 2; ++j) {    // byte j: element 2j (low nibble), 2j+1 (high)
+                const uint32_t b = (st.w[m][j >> 2] >> (8 * (j & 3))) & 0xFFu;
                 v[2 * j] = (float)((int)(b & 0xFu) - 8) * sc;
                 v[2 * j + 1] = (float)((int)(b >> 4) - 8) * sc;
             }
         }
-        uint4* bd = reinterpret_cast<uint4*>(Bs + (size_t)m * kBN * kLds + r * kLds + 32 * hf);
+        uint4* bd = reinterpret_cast<uint4*>(Bs + (size_t)m * C::BN * C::LDS + r * C::LDS + pb * C::EB);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < C::EB / 8; ++i)
             bd[i] = make_uint4(pack_bf16(v[8 * i], v[8 * i + 1]), pack_bf16(v[8 * i + 2], v[8 * i + 3]),
                                pack_bf16(v[8 * i + 4], v[8 * i + 5]), pack_bf16(v[8 * i + 6], v[8 * i + 7]));
     }
@@ -100,75 +128,77 @@ __device__ __forceinline__ void gemm_store(const GemmStage<WT, NM>& st, uint16_t
 
 // EPI: 0 = store f32, 1 = f32 + residual, 2 = SwiGLU silu(g)*u (NM = 2) stored
 // as bf16 (the next GEMM's operand), 3 = SwiGLU stored as f32.
-template <int WT, int EPI>
-__global__ __launch_bounds__(kGemmThreads) void mfma_qgemm_kernel(
+template <class C, int WT, int EPI>
+__global__ __launch_bounds__(C::NT) void mfma_qgemm_kernel(
     const uint16_t* __restrict__ A, const uint8_t* __restrict__ qa, const __half* __restrict__ da,
     const uint8_t* __restrict__ qb, const __half* __restrict__ db, int M, int N, int K,
     const float* __restrict__ residual, void* __restrict__ out) {
     constexpr int NM = EPI >= 2 ? 2 : 1;
-    __shared__ __align__(16) uint16_t As[2][kBM * kLds];
-    __shared__ __align__(16) uint16_t Bs[2][NM * kBN * kLds];
+    constexpr int MI = C::MI, NI = C::NI, LD = C::LDS;
+    __shared__ __align__(16) uint16_t As[2][C::BM * LD];
+    __shared__ __align__(16) uint16_t Bs[2][NM * C::BN * LD];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    const int m0 = blockIdx.y * kBM, n0 = blockIdx.x * kBN;
+    const int wm = wave / C::WN, wn = wave % C::WN;
+    const int m0 = blockIdx.y * C::BM, n0 = blockIdx.x * C::BN;
+    const int rm = wm * (C::BM / C::WM), rn = wn * (C::BN / C::WN);
 
-    f32x16 acc[NM][2][2];
+    f32x16 acc[NM][MI][NI];
 #pragma unroll
     for (int m = 0; m < NM; ++m)
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < MI; ++i)
 #pragma unroll
-            for (int j = 0; j < 2; ++j) acc[m][i][j] = f32x16{};
+            for (int j = 0; j < NI; ++j) acc[m][i][j] = f32x16{};
 
-    GemmStage<WT, NM> st;
-    gemm_load<WT, NM>(st, A, qa, da, qb, db, m0, n0, 0, M, N, K);
-    gemm_store<WT, NM>(st, As[0], Bs[0]);
+    GemmStage<C, WT, NM> st;
+    gemm_load<C, WT, NM>(st, A, qa, da, qb, db, m0, n0, 0, M, N, K);
+    gemm_store<C, WT, NM>(st, As[0], Bs[0]);
     __syncthreads();
 
-    const int nk = K / kBK;
+    const int nk = K / C::BK;
     for (int kt = 0; kt < nk; ++kt) {
         const int cur = kt & 1;
         // Unconditional (the last step reloads its own tile, unused): a conditional
         // load would leave the staging registers to a merge the compiler spills.
-        gemm_load<WT, NM>(st, A, qa, da, qb, db, m0, n0, min(kt + 1, nk - 1) * kBK, M, N, K);
+        gemm_load<C, WT, NM>(st, A, qa, da, qb, db, m0, n0, min(kt + 1, nk - 1) * C::BK, M, N, K);
         const uint16_t* as = As[cur];
         const uint16_t* bs = Bs[cur];
 #pragma unroll
-        for (int kk = 0; kk < kBK / 16; ++kk) {
+        for (int kk = 0; kk < C::BK / 16; ++kk) {
             const int kc = kk * 16 + 8 * (lane >> 5);      // this lane's 8 k of the 16
-            bf16x8 af[2], bf[NM][2];
+            bf16x8 af[MI], bf[NM][NI];
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
-                af[i] = *reinterpret_cast<const bf16x8*>(as + (64 * wm + 32 * i + (lane & 31)) * kLds + kc);
-#pragma unroll
-            for (int m = 0; m < NM; ++m)
-#pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    bf[m][j] = *reinterpret_cast<const bf16x8*>(bs + (size_t)m * kBN * kLds +
-                                                                 (64 * wn + 32 * j + (lane & 31)) * kLds + kc);
+            for (int i = 0; i < MI; ++i)
+                af[i] = *reinterpret_cast<const bf16x8*>(as + (rm + 32 * i + (lane & 31)) * LD + kc);
 #pragma unroll
             for (int m = 0; m < NM; ++m)
 #pragma unroll
-                for (int i = 0; i < 2; ++i)
+                for (int j = 0; j < NI; ++j)
+                    bf[m][j] = *reinterpret_cast<const bf16x8*>(bs + (size_t)m * C::BN * LD +
+                                                                 (rn + 32 * j + (lane & 31)) * LD + kc);
 #pragma unroll
-                    for (int j = 0; j < 2; ++j)
+            for (int m = 0; m < NM; ++m)
+#pragma unroll
+                for (int i = 0; i < MI; ++i)
+#pragma unroll
+                    for (int j = 0; j < NI; ++j)
                         acc[m][i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[m][j], acc[m][i][j], 0, 0, 0);
         }
-        if (kt + 1 < nk) gemm_store<WT, NM>(st, As[cur ^ 1], Bs[cur ^ 1]);
+        if (kt + 1 < nk) gemm_store<C, WT, NM>(st, As[cur ^ 1], Bs[cur ^ 1]);
         __syncthreads();
     }
 
     // Accumulator v of block (i, j) holds C[row][col] with
-    // row = 32i + 8(v/4) + 4(lane/32) + v%4 and col = 32j + lane%32 (of the wave's 64x64).
+    // row = 32i + 8(v/4) + 4(lane/32) + v%4 and col = 32j + lane%32 (of the wave's block).
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < MI; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < NI; ++j)
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
-                const int row = m0 + 64 * wm + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-                const int col = n0 + 64 * wn + 32 * j + (lane & 31);
+                const int row = m0 + rm + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+                const int col = n0 + rn + 32 * j + (lane & 31);
                 if (row < M && col < N) {
                     const size_t o = (size_t)row * N + col;
                     if constexpr (EPI >= 2) {
@@ -183,6 +213,34 @@ __global__ __launch_bounds__(kGemmThreads) void mfma_qgemm_kernel(
                     }
                 }
             }
+}
+
+// Tile configurations, chosen by measurement at the 8B-layer shapes (M = 2048):
+//   CfgWide  256x128x64, 16 waves: one workgroup per CU (108 KB LDS); O and down.
+//   CfgFill  256x128x32, 8 waves: two per CU (60 KB), for grids of 257..512 tiles
+//            that would leave half the CUs idle in a second round (QKV, N = 6144).
+//   CfgSwi   256x128x64, 8 waves, gate and up tiles together (144 KB).
+//   CfgSmall 128x128x64, 4 waves: M <= 128, where 256-row tiles are mostly padding.
+// Every configuration steps K by at most 64, so K % 64 == 0 covers them all.
+using CfgWide = TileCfg<256, 128, 64, 4, 4>;
+using CfgFill = TileCfg<256, 128, 32, 4, 2>;
+using CfgSwi = TileCfg<256, 128, 64, 4, 2>;
+using CfgSmall = TileCfg<128, 128, 64, 2, 2>;
+constexpr int kBK = 64;
+constexpr int kCUs = 256;
+
+template <class C, int EPI>
+void launch_cfg(hipStream_t s, int wt, const uint16_t* a, const DevWeight& w0, const DevWeight* w1, int M,
+                const float* residual, void* out) {
+    const dim3 grid((w0.N + C::BN - 1) / C::BN, (M + C::BM - 1) / C::BM), block(C::NT);
+    const uint8_t* qb = w1 ? w1->q : nullptr;
+    const __half* db = w1 ? w1->d : nullptr;
+    if (wt == VLRF_DT_Q8_0)
+        hipLaunchKernelGGL((mfma_qgemm_kernel<C, VLRF_DT_Q8_0, EPI>), grid, block, 0, s, a, w0.q, w0.d, qb, db,
+                           M, w0.N, w0.K, residual, out);
+    else
+        hipLaunchKernelGGL((mfma_qgemm_kernel<C, VLRF_DT_Q4_0, EPI>), grid, block, 0, s, a, w0.q, w0.d, qb, db,
+                           M, w0.N, w0.K, residual, out);
 }
 
 // out[r][:] = bf16(w ? rmsnorm(x[r]) * w : x[r]), one 256-lane workgroup per row
@@ -230,16 +288,17 @@ int launch_qgemm(hipStream_t s, const DevWeight& w, const uint16_t* a, int M, co
     int rc = check_qgemm(w, M);
     if (rc) return rc;
     VH_ARG(a && y, "qgemm: null operand");
-    dim3 grid((w.N + kBN - 1) / kBN, (M + kBM - 1) / kBM), block(kGemmThreads);
-#define VH_QG(WT, EPI)                                                                                 \
-    hipLaunchKernelGGL((mfma_qgemm_kernel<WT, EPI>), grid, block, 0, s, a, w.q, w.d, nullptr, nullptr, \
-                       M, w.N, w.K, residual, (void*)y)
-    if (w.dtype == VLRF_DT_Q8_0) {
-        if (residual) VH_QG(VLRF_DT_Q8_0, 1); else VH_QG(VLRF_DT_Q8_0, 0);
+    const int tiles = ((w.N + 127) / 128) * ((M + 255) / 256);
+    if (M <= 128) {
+        if (residual) launch_cfg<CfgSmall, 1>(s, w.dtype, a, w, nullptr, M, residual, y);
+        else launch_cfg<CfgSmall, 0>(s, w.dtype, a, w, nullptr, M, nullptr, y);
+    } else if (tiles > kCUs && tiles <= 2 * kCUs) {
+        if (residual) launch_cfg<CfgFill, 1>(s, w.dtype, a, w, nullptr, M, residual, y);
+        else launch_cfg<CfgFill, 0>(s, w.dtype, a, w, nullptr, M, nullptr, y);
     } else {
-        if (residual) VH_QG(VLRF_DT_Q4_0, 1); else VH_QG(VLRF_DT_Q4_0, 0);
+        if (residual) launch_cfg<CfgWide, 1>(s, w.dtype, a, w, nullptr, M, residual, y);
+        else launch_cfg<CfgWide, 0>(s, w.dtype, a, w, nullptr, M, nullptr, y);
     }
-#undef VH_QG
     VH_LAUNCHED();
     return VLRF_HIP_OK;
 }
@@ -252,16 +311,13 @@ int launch_qgemm_swiglu(hipStream_t s, const DevWeight& wg, const DevWeight& wu,
     if (rc) return rc;
     VH_ARG(wg.N == wu.N && wg.K == wu.K && wg.dtype == wu.dtype, "qgemm_swiglu: gate/up differ");
     VH_ARG(a && h, "qgemm_swiglu: null operand");
-    dim3 grid((wg.N + kBN - 1) / kBN, (M + kBM - 1) / kBM), block(kGemmThreads);
-#define VH_QS(WT, EPI)                                                                                  \
-    hipLaunchKernelGGL((mfma_qgemm_kernel<WT, EPI>), grid, block, 0, s, a, wg.q, wg.d, wu.q, wu.d, M, wg.N, \
-                       wg.K, nullptr, h)
-    if (wg.dtype == VLRF_DT_Q8_0) {
-        if (h_bf16) VH_QS(VLRF_DT_Q8_0, 2); else VH_QS(VLRF_DT_Q8_0, 3);
+    if (M <= 128) {
+        if (h_bf16) launch_cfg<CfgSmall, 2>(s, wg.dtype, a, wg, &wu, M, nullptr, h);
+        else launch_cfg<CfgSmall, 3>(s, wg.dtype, a, wg, &wu, M, nullptr, h);
     } else {
-        if (h_bf16) VH_QS(VLRF_DT_Q4_0, 2); else VH_QS(VLRF_DT_Q4_0, 3);
+        if (h_bf16) launch_cfg<CfgSwi, 2>(s, wg.dtype, a, wg, &wu, M, nullptr, h);
+        else launch_cfg<CfgSwi, 3>(s, wg.dtype, a, wg, &wu, M, nullptr, h);
     }
-#undef VH_QS
     VH_LAUNCHED();
     return VLRF_HIP_OK;
 }
