@@ -24,6 +24,7 @@ dequant, per-head flash attention) on the host's cores at context 2048.
     python bench.py [--gpus 1] [--steps 128] [--warmup 8] [--dtype q8_0|q4_0]
     python bench.py --roofline-only     # copy calibration + roofline launches only
     python bench.py --prefill           # config 5: one Llama-8B-shape layer, T=2048 prefill
+    python bench.py --configs           # configs 1-3: kernel-level GB/s, one JSON line each
 
 --prefill prints its own line: one Llama-8B-shape
 layer (hidden 4096, 32/8 heads, head_dim 128, FFN 14336 SwiGLU, Q8_0 weights)
@@ -31,6 +32,16 @@ over a causal 2048-token prompt of N(0,1) embedded rows, on the matrix cores
 (bf16 operands, f32 accumulation), each run from an empty cache.  FLOPs per
 layer = 2*T*(D*(D+2*dkv) + D*D + 3*D*F) + 4*H*d*T*T/2 = 927.7 GFLOP; the
 roofline is the dense bf16 MFMA peak (2.5 PFLOP/s).
+
+--configs (BASELINE.json configs[0..2]) prints one line per kernel case, each
+timed with HIP events over launches that rotate through distinct instances
+totalling more than the 256 MB Infinity Cache, plus the latency of one
+instance repeated (cache-warm):
+  cfg1  f32 attention Q[8,1,64], K/V[8,512,64], non-causal: 2,101,248 B/call;
+  cfg2  decode attention over a Q8_0 cache, 32 q / 4 kv heads, d 64, ctx 4096:
+        2,146,304 B/call (codes, row scales, q, out);
+  cfg3  quantized linear up 5632x2048 and down 2048x5632, Q8_0 and Q4_0,
+        M = 1, 4, 16: weight bytes + 4*M*(K+N) per call.
 """
 import argparse
 import json
@@ -159,6 +170,97 @@ def prefill_bench(a, V, F):
     }
 
 
+def timed(ctx, fn, n_inst, launches):
+    """Mean ms per launch over `launches` calls fn(i % n_inst), after a warm-up."""
+    for i in range(min(launches, 2 * n_inst)):
+        fn(i % n_inst)
+    ctx.sync()
+    ctx.timer_start()
+    for i in range(launches):
+        fn(i % n_inst)
+    return ctx.timer_stop() / launches
+
+
+def config_line(name, workload, bytes_per_call, ms_rot, ms_warm, extra=None):
+    gbs = bytes_per_call / (ms_rot / 1e3) / 1e9
+    out = {"metric": name, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "higher_is_better": True,
+           "config": {"workload": workload}, "bytes_per_call": int(bytes_per_call),
+           "us_per_call_rotating": round(ms_rot * 1e3, 3), "us_per_call_repeated": round(ms_warm * 1e3, 3),
+           "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": round(gbs / HBM_PEAK_GBS, 4)}}
+    if extra:
+        out.update(extra)
+    return out
+
+
+def configs_bench(V, F):
+    """Kernel-level measurements of configs 1-3 through the C ABI."""
+    ctx = V.Context(0)
+    log("[configs]", ctx.device_info())
+    lines = []
+
+    # cfg1: f32 fused attention, 8 heads, T=1, ctx 512, d 64, non-causal.
+    nh, T, L, d = 8, 1, 512, 64
+    n1 = 128
+    kv_elems = nh * L * d
+    K = ctx.to_device(np.tile(F.normal(5, "cfg1.k", kv_elems), n1))
+    Vb = ctx.to_device(np.tile(F.normal(5, "cfg1.v", kv_elems), n1))
+    Q = ctx.to_device(np.tile(F.normal(5, "cfg1.q", nh * d), n1))
+    O = ctx.alloc(n1 * nh * d * 4)
+    f4 = 4
+
+    def cfg1(i):
+        V.check(V.lib().vlrf_hip_attn_f32(ctx.h, Q.ptr + i * nh * d * f4, K.ptr + i * kv_elems * f4,
+                                          Vb.ptr + i * kv_elems * f4, O.ptr + i * nh * d * f4,
+                                          nh, T, L, d, 0.125, 0))
+    b1 = 2 * kv_elems * 4 + 2 * nh * d * 4
+    lines.append(config_line("cfg1 f32 attention GB/s", "Q[8,1,64] K/V[8,512,64] f32, non-causal, "
+                             "128 instances rotating", b1, timed(ctx, cfg1, n1, 512),
+                             timed(ctx, cfg1, 1, 512)))
+    del K, Vb, Q, O
+
+    # cfg2: decode attention over a Q8_0 cache, 128 caches (one per "layer").
+    n2, ctxl, nkv, nq = 128, 4096, 4, 32
+    kv = V.KVCache(ctx, n2, ctxl, nkv, d)
+    k = ctx.to_device(F.normal(6, "cfg2.k", ctxl * nkv * d))
+    v = ctx.to_device(F.normal(6, "cfg2.v", ctxl * nkv * d))
+    for layer in range(n2):
+        kv.append(layer, k, v, ctxl)
+    del k, v
+    q = ctx.to_device(F.normal(6, "cfg2.q", nq * d))
+    o = ctx.alloc(nq * d * 4)
+
+    def cfg2(i):
+        kv.attention_decode(i, q, o, nq, ctxl, 0.125)
+    b2 = 2 * ctxl * nkv * d + 2 * ctxl * 4 + 2 * nq * d * 4
+    lines.append(config_line("cfg2 Q8_0-KV GQA decode attention GB/s",
+                             "32 q / 4 kv heads, d 64, ctx 4096, 128 caches rotating", b2,
+                             timed(ctx, cfg2, n2, 512), timed(ctx, cfg2, 1, 512)))
+    del kv
+
+    # cfg3: quantized linear, 24 weight copies per shape (> 256 MB for Q8_0).
+    for dtype, dname in ((V.DT_Q8_0, "q8_0"), (V.DT_Q4_0, "q4_0")):
+        for wname, N, Kd in (("up", 5632, 2048), ("down", 2048, 5632)):
+            n3 = 24 if dtype == V.DT_Q8_0 else 48
+            base = F.quantize(F.normal(7, f"cfg3.{wname}", N * Kd, 0.02), dtype)
+            ws = [V.QuantWeight(ctx, base, dtype, N, Kd) for _ in range(n3)]
+            for M in (1, 4, 16):
+                x = ctx.to_device(F.normal(7, f"cfg3.x{M}", M * Kd))
+                y = ctx.alloc(M * N * 4)
+
+                def cfg3(i):
+                    ctx.qlinear(ws[i], x, y, M)
+                b3 = ws[0].device_bytes + 4 * M * (Kd + N)
+                lines.append(config_line(
+                    f"cfg3 quantized linear GB/s ({wname} {N}x{Kd} {dname} M={M})",
+                    f"y[{M},{N}] = x[{M},{Kd}] . W^T, {dname} weights, {n3} copies rotating", b3,
+                    timed(ctx, cfg3, n3, 8 * n3), timed(ctx, cfg3, 1, 8 * n3),
+                    {"gflop_per_call": round(2e-9 * M * N * Kd, 4)}))
+            del ws
+    for line in lines:
+        print(json.dumps(line), flush=True)
+
+
 def cpu_baseline(cfg, f32w, ctx_len, budget_s=12.0, max_steps=8):
     """Oracle decode steps at context ctx_len on the host cores."""
     import oracle
@@ -201,6 +303,8 @@ def main():
     ap.add_argument("--prefill", action="store_true",
                     help="config 5: one Llama-8B-shape layer prefill on the matrix cores")
     ap.add_argument("--prefill-tokens", type=int, default=2048)
+    ap.add_argument("--configs", action="store_true",
+                    help="configs 1-3: kernel-level GB/s of attention and quantized linear")
     a = ap.parse_args()
 
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -210,6 +314,10 @@ def main():
 
     import vlrf_amd as V
     from vlrf_amd import formats as F
+
+    if a.configs:
+        configs_bench(V, F)
+        return
 
     if a.prefill:
         if a.steps == 128:           # the decode default; a layer prefill is ~ms

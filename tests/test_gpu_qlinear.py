@@ -80,6 +80,43 @@ def test_swiglu_gate_up(ctx, orc, dtype, M):
     assert rel_err(dh.download((M, Fd)), ref) <= 1e-3
 
 
+@pytest.mark.parametrize("dtype", [V.DT_Q8_0, V.DT_Q4_0])
+@pytest.mark.parametrize("M,N,K", [(2, 37, 256), (7, 300, 2304), (16, 1000, 4352), (5, 16, 512)])
+def test_small_m_matrix_core_path(ctx, orc, dtype, M, N, K):
+    """2 <= M <= 16 with K % 256 == 0 runs on the matrix cores (codes exact in
+    bf16, activations split into bf16 hi + lo): row counts off the 16-row tile,
+    one 256-column slice, 9 slices over 16 waves (7 idle), 17 slices (one wave
+    takes two).  Fused norm, then the residual added in place.  The split keeps
+    the f32 class: 1e-4, ten times tighter than the path's stated 1e-3."""
+    print(f"[case] qlinear small-M dtype={dtype} M={M} N={N} K={K}", flush=True)
+    w, dec = _weight(ctx, 12, f"S{N}x{K}", N, K, dtype)
+    x = F.normal(12, f"xs{M}x{K}", M * K).reshape(M, K)
+    g = 1.0 + F.normal(12, f"gs{K}", K, 0.1)
+    res = F.normal(12, f"rs{M}x{N}", M * N).reshape(M, N)
+    dx, dg, dr, dy = ctx.to_device(x), ctx.to_device(g), ctx.to_device(res), ctx.alloc(M * N * 4)
+    ctx.qlinear(w, dx, dy, M)
+    assert rel_err(dy.download((M, N)), orc.linear(x, dec)) <= 1e-4
+    ref = orc.linear(orc.rms_norm(x, g, 1e-5), dec)
+    ctx.qlinear(w, dx, dr, M, norm_w=dg, eps=1e-5, residual=dr)
+    assert rel_err(dr.download((M, N)), ref + res) <= 1e-4
+
+
+@pytest.mark.parametrize("dtype", [V.DT_Q8_0, V.DT_Q4_0])
+def test_small_m_swiglu_ragged(ctx, orc, dtype):
+    """SwiGLU on the small-M matrix-core path: M = 13, F = 1000 (not a multiple
+    of 16), K = 4352 (17 slices)."""
+    M, Fd, K = 13, 1000, 4352
+    wg, gdec = _weight(ctx, 13, "SWg", Fd, K, dtype)
+    wu, udec = _weight(ctx, 13, "SWu", Fd, K, dtype)
+    x = F.normal(13, "sxs", M * K).reshape(M, K)
+    g = 1.0 + F.normal(13, "sgs", K, 0.1)
+    dx, dg, dh = ctx.to_device(x), ctx.to_device(g), ctx.alloc(M * Fd * 4)
+    ctx.qlinear_swiglu(wg, wu, dx, dh, M, norm_w=dg, eps=1e-5)
+    xn = orc.rms_norm(x, g, 1e-5)
+    ref = orc.silu_mul(orc.linear(xn, udec), orc.linear(xn, gdec))
+    assert rel_err(dh.download((M, Fd)), ref) <= 1e-4
+
+
 def test_qlinear_rejects_bad_shapes(ctx):
     w, _ = _weight(ctx, 11, "Wbad", 64, 96, V.DT_Q8_0)
     x = ctx.alloc(96 * 4 * 17)

@@ -526,6 +526,12 @@ int vlrf_hip_qlinear(vlrf_hip_ctx_t ctx, vlrf_hip_weight_t w, const float* x, fl
     VH_CTX(ctx);
     VH_ARG(w != nullptr, "qlinear: null weight");
     VH_ARG(x != y, "qlinear: x must not alias y");
+    if (M >= 2 && M <= 16 && qlinear_small_supported(w->w)) {
+        float* scratch = nullptr;
+        int rc = ctx->scratch(qlinear_small_scratch(w->w.N, w->w.K, false), &scratch);
+        if (rc) return rc;
+        return launch_qlinear_small(ctx->stream, w->w, nullptr, x, M, norm_w, eps, residual, scratch, y);
+    }
     if (M <= 16) return launch_qlinear(ctx->stream, w->w, x, y, M, norm_w, eps, residual);
     VH_ARG(x && y, "qlinear: null activation pointer");
     float* scratch = nullptr;
@@ -542,6 +548,12 @@ int vlrf_hip_qlinear_swiglu(vlrf_hip_ctx_t ctx, vlrf_hip_weight_t wg, vlrf_hip_w
     VH_CTX(ctx);
     VH_ARG(wg && wu, "swiglu: null weight");
     VH_ARG(x != h, "swiglu: x must not alias h");
+    if (M >= 2 && M <= 16 && qlinear_small_supported(wg->w)) {
+        float* scratch = nullptr;
+        int rc = ctx->scratch(qlinear_small_scratch(wg->w.N, wg->w.K, true), &scratch);
+        if (rc) return rc;
+        return launch_qlinear_small(ctx->stream, wg->w, &wu->w, x, M, norm_w, eps, nullptr, scratch, h);
+    }
     if (M <= 16) return launch_qlinear_swiglu(ctx->stream, wg->w, wu->w, x, h, M, norm_w, eps);
     VH_ARG(x && h, "swiglu: null activation pointer");
     float* scratch = nullptr;

@@ -107,6 +107,14 @@ int launch_qgemm(hipStream_t s, const DevWeight& w, const uint16_t* a, int M, co
 // h[M,N] = silu(a.Wg^T) * (a.Wu^T), stored as bf16 (h_bf16) or f32
 int launch_qgemm_swiglu(hipStream_t s, const DevWeight& wg, const DevWeight& wu, const uint16_t* a,
                         int M, void* h, bool h_bf16);
+// Small M (2..16) on the matrix cores with f32-class accuracy (x split into
+// bf16 hi + lo): y = x.W0^T (+ residual), or silu(x.W0^T) * (x.W1^T) when w1
+// is given.  Per-slice partial sums go to scratch (qlinear_small_scratch bytes).
+bool qlinear_small_supported(const DevWeight& w);
+size_t qlinear_small_scratch(int N, int K, bool two);
+int launch_qlinear_small(hipStream_t s, const DevWeight& w0, const DevWeight* w1, const float* x,
+                         int M, const float* norm_w, float eps, const float* residual, float* scratch,
+                         float* y);
 int launch_rope(hipStream_t s, float* x, int T, int n_heads, int d_head, int pos_offset,
                 int max_seq, const float* cos_t, const float* sin_t);
 

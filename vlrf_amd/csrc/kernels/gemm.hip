@@ -1,28 +1,38 @@
-// gemm.hip - dequant-fused MFMA GEMM for the prefill path (M > 16 rows).
+// gemm.hip - dequant-fused linear layers on the matrix cores.
 //
 // Reference contract: compute::linear -> ops::gemm(x, W, y, 1, 0, false, true)
-// (include/model/compute.hpp:58-68, ops.hpp:254-305 for M >= 4) on weights
-// decoded from GGUF Q8_0/Q4_0 blocks (tools/converter/convert_gguf.py:233-263).
-// The reference computes in f32; this path rounds the activations and the
-// decoded weights to bf16 and accumulates in f32 on the matrix cores (the
-// 1e-2 tolerance class of bf16 paths).
+// (include/model/compute.hpp:58-68, ops.hpp:170-310) on weights decoded from
+// GGUF Q8_0/Q4_0 blocks (tools/converter/convert_gguf.py:233-263).
 //
-// Design (gfx950): C[M,N] = A[M,K] . W[N,K]^T with A in bf16 and W as split
-// GGUF blocks (codes [N][K], f16 scales [N][K/32]).  A 256-lane workgroup owns
-// a 128x128 tile of C; each wave a 64x64 quarter as 2x2 v_mfma_f32_32x32x16_bf16
-// blocks.  K advances in steps of 64: the next step's A rows and weight codes
-// are loaded into registers while the matrix cores work on the current step,
-// then the codes are dequantized (code * scale -> bf16) on their way into the
-// other LDS buffer, so W is read from HBM once per tile column as 1.06 B
-// (Q8_0) or 0.56 B (Q4_0) per weight.  LDS rows are padded by 16 bytes so the
-// 32 lanes of an operand read hit distinct banks.  Epilogues: store f32,
-// add a residual, or SwiGLU (two weights, silu(g)*u) with bf16 output.
+// 1. Prefill GEMM (M > 16 rows).  The reference computes in f32; this path
+// rounds the activations and the decoded weights to bf16 and accumulates in
+// f32 (the 1e-2 tolerance class of bf16 paths).  C[M,N] = A[M,K] . W[N,K]^T
+// with A in bf16 and W as split GGUF blocks (codes [N][K], f16 scales
+// [N][K/32]).  A workgroup owns a BM x BN tile of C, each wave a block of
+// v_mfma_f32_32x32x16_bf16 tiles.  K advances in steps of BK: the next step's
+// A rows and weight codes are loaded into registers while the matrix cores
+// work on the current step, then the codes are dequantized (code * scale ->
+// bf16) on their way into the other LDS buffer, so W is read from HBM once per
+// tile column as 1.06 B (Q8_0) or 0.56 B (Q4_0) per weight.  LDS rows are
+// padded by 16 bytes so the lanes of an operand read hit distinct banks.
+// Epilogues: store f32, add a residual, or SwiGLU (two weights, silu(g)*u).
+//
+// 2. Small M (2..16 rows, ops.hpp:142-168,254-305 for M = 2..16) with
+// f32-class accuracy.  Q8_0/Q4_0 codes are integers of at most 8 bits, exact
+// in bf16, so one v_mfma_f32_16x16x32_bf16 multiplies the codes of one 32-wide
+// block of 16 weight rows with 32 activations of 16 rows exactly, and the
+// block scale is applied to the f32 result afterwards.  The activations are
+// split into bf16 hi + lo (x = hi + lo to about 2^-17 relative), two MFMAs per
+// block, so the products carry ~16 significant bits of x and accumulate in
+// f32: results agree with the f32 reference to ~1e-5 relative.
+#include "../internal.hpp"
 #include "../internal.hpp"
 
 namespace vlrf_hip {
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 // Tile configuration: BM x BN tile of C per workgroup, K steps of BK, WM x WN
@@ -264,6 +274,229 @@ __global__ __launch_bounds__(256) void rows_to_bf16_kernel(const float* __restri
     for (int i = tid; i < D; i += 256) o[i] = (uint16_t)bf16_bits(w ? xr[i] * inv * w[i] : xr[i]);
 }
 
+// ---- small M on the matrix cores ------------------------------------------------
+// y[M,N] = x[M,K] . W^T for 2 <= M <= 16, W Q8_0/Q4_0 with K % 256 == 0, in two
+// kernels.  qlinear_small_partial_kernel: workgroup (gx, gy) owns weight rows
+// 128gx .. +127 and the 256-column slices gy, gy + gridDim.y, ...  Per slice it
+// stages the 16 x 256 activations (rows >= M zero, times the norm weight when
+// given) in LDS as bf16 hi and lo planes, laid out [block][row][32] so that
+// lane (c, g) of a wave reads its MFMA operand, row c, columns 8g..8g+7 of a
+// block, as 16 contiguous bytes and the wave's 64 reads cover one KiB.  Wave w
+// owns rows 16w..16w+15 of the 128.  It loads their codes and scales with
+// 16-byte (codes) and 4-byte (scales) lane loads over contiguous runs of each
+// row, as the M = 1 GEMV does, and transposes them through LDS: lane (c, g)
+// then reads the codes of row c, columns 8g..8g+7 of each block (A operand),
+// one MFMA per plane multiplies them with the block's activations, and the
+// f32 result D (lane (m, g) holds rows 4g+v, v = 0..3, column m) takes the
+// block scales of those rows.  The workgroup's partial [128][16]
+// tile goes to P[gy][mat][n][16], and with a norm the slice's sum of x^2 per
+// row to SS[gy][16].  qlinear_small_reduce_kernel adds the partials in slice
+// order (deterministic) and applies the epilogue.  With a norm, x is scaled by
+// w before the product and by inv_rms after it: rms_norm is per row, so
+// W.((x*inv)*w) = inv * W.(x*w) (ops.hpp:488-498, rounded differently).
+constexpr int kSmallRows = 128;          // weight rows per workgroup (8 waves x 16)
+constexpr int kSmallSlice = 256;         // K columns per slice (8 blocks)
+
+__device__ __forceinline__ float wave32_sum(float v) {     // sum over each half-wave
+    v += dpp_f<0xB1>(v);
+    v += dpp_f<0x4E>(v);
+    v += dpp_f<0x141>(v);
+    v += dpp_f<0x140>(v);
+    v += __shfl_xor(v, 16);
+    return v;
+}
+
+// Codes of one lane's 8 columns of a block -> bf16 (exact).
+template <int WT>
+__device__ __forceinline__ bf16x8 codes_bf16(uint2 c) {
+    bf16x8 r;
+    if constexpr (WT == VLRF_DT_Q8_0) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            r[e] = (__bf16)(float)(int8_t)(c.x >> (8 * e));
+            r[4 + e] = (__bf16)(float)(int8_t)(c.y >> (8 * e));
+        }
+    } else {                                  // byte j: element 2j low nibble, 2j+1 high
+#pragma unroll
+        for (int e = 0; e < 8; ++e) r[e] = (__bf16)(float)((int)((c.x >> (4 * e)) & 0xFu) - 8);
+    }
+    return r;
+}
+
+template <int WT, int NM>
+__global__ __launch_bounds__(512) void qlinear_small_partial_kernel(
+    const uint8_t* __restrict__ qa, const __half* __restrict__ da, const uint8_t* __restrict__ qb,
+    const __half* __restrict__ db, int N, int K, int M, const float* __restrict__ x,
+    const float* __restrict__ norm_w, float* __restrict__ P, float* __restrict__ SS) {
+    constexpr int CB = WT == VLRF_DT_Q8_0 ? 256 : 128;   // code bytes of a row per slice
+    constexpr int CS = CB + 16;                          // padded LDS row stride
+    constexpr int LPR = CB / 16;                         // lanes per row in a coalesced load
+    constexpr int CL = 16 * LPR / 64;                    // 16-byte code loads per lane and matrix
+    __shared__ __align__(16) uint16_t xh[8 * 16 * 32];
+    __shared__ __align__(16) uint16_t xl[8 * 16 * 32];
+    __shared__ __align__(16) uint8_t cs[NM][8][16 * CS];  // per wave: its 16 rows' codes
+    __shared__ __align__(16) uint32_t ssc[NM][8][16 * 4]; // per wave: 16 rows x 8 f16 scales
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 4, c = lane & 15;
+    const int rbase = blockIdx.x * kSmallRows + 16 * wave;
+    const int ns = K / kSmallSlice;
+    const size_t rowb = WT == VLRF_DT_Q8_0 ? (size_t)K : (size_t)K / 2;
+    // staging: thread t converts row t/32, columns 8(t%32) .. +7 of the slice
+    const int sm = tid >> 5, sk = 8 * (tid & 31);
+    float ss = 0.f;
+    f32x4 acc[NM];
+#pragma unroll
+    for (int m = 0; m < NM; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    for (int sl = blockIdx.y; sl < ns; sl += gridDim.y) {
+        const int k0 = sl * kSmallSlice;
+        // Activations first (L2, needed first), then the codes and scales (HBM):
+        // loads complete in order, so the staging below waits for x only.
+        float4 a0 = make_float4(0.f, 0.f, 0.f, 0.f), a1 = a0;
+        if (sm < M) {
+            const float4* xp = reinterpret_cast<const float4*>(x + (size_t)sm * K + k0 + sk);
+            a0 = xp[0];
+            a1 = xp[1];
+        }
+        // Codes: load i of lane l covers row LPR-group i*64/LPR + l/LPR, bytes
+        // 16(l % LPR) .. +15 of the row's slice: runs of CB contiguous bytes.
+        uint4 cv[NM][CL];
+        uint32_t sv[NM];
+#pragma unroll
+        for (int m = 0; m < NM; ++m) {
+            const uint8_t* q = m ? qb : qa;
+            const __half* d = m ? db : da;
+#pragma unroll
+            for (int i = 0; i < CL; ++i) {
+                const int r = min(rbase + i * (64 / LPR) + lane / LPR, N - 1);
+                cv[m][i] = *reinterpret_cast<const uint4*>(q + r * rowb + (size_t)k0 * CB / kSmallSlice +
+                                                           16 * (lane % LPR));
+            }
+            const int r = min(rbase + (lane >> 2), N - 1);      // 16 rows x 4 dwords of scales
+            sv[m] = *reinterpret_cast<const uint32_t*>(d + (size_t)r * (K / 32) + k0 / 32 + 2 * (lane & 3));
+        }
+        {
+            if (sm < M) {
+                ss += a0.x * a0.x + a0.y * a0.y + a0.z * a0.z + a0.w * a0.w +
+                      a1.x * a1.x + a1.y * a1.y + a1.z * a1.z + a1.w * a1.w;
+                if (norm_w) {
+                    const float4* wp = reinterpret_cast<const float4*>(norm_w + k0 + sk);
+                    const float4 w0 = wp[0], w1 = wp[1];
+                    a0 = make_float4(a0.x * w0.x, a0.y * w0.y, a0.z * w0.z, a0.w * w0.w);
+                    a1 = make_float4(a1.x * w1.x, a1.y * w1.y, a1.z * w1.z, a1.w * w1.w);
+                }
+            }
+            const float v[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+            uint32_t h[4], l[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                h[i] = pack_bf16(v[2 * i], v[2 * i + 1]);
+                l[i] = pack_bf16(v[2 * i] - __uint_as_float(h[i] << 16),
+                                 v[2 * i + 1] - __uint_as_float(h[i] & 0xFFFF0000u));
+            }
+            const int o = (sk >> 5) * 512 + sm * 32 + (sk & 31);
+            *reinterpret_cast<uint4*>(xh + o) = make_uint4(h[0], h[1], h[2], h[3]);
+            *reinterpret_cast<uint4*>(xl + o) = make_uint4(l[0], l[1], l[2], l[3]);
+        }
+#pragma unroll
+        for (int m = 0; m < NM; ++m) {
+#pragma unroll
+            for (int i = 0; i < CL; ++i)
+                *reinterpret_cast<uint4*>(&cs[m][wave][(i * (64 / LPR) + lane / LPR) * CS + 16 * (lane % LPR)]) =
+                    cv[m][i];
+            ssc[m][wave][lane] = sv[m];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int xo = (j * 16 + c) * 32 + 8 * g;
+            const bf16x8 bh = *reinterpret_cast<const bf16x8*>(xh + xo);
+            const bf16x8 bl = *reinterpret_cast<const bf16x8*>(xl + xo);
+#pragma unroll
+            for (int m = 0; m < NM; ++m) {
+                uint2 code;
+                if constexpr (WT == VLRF_DT_Q8_0)
+                    code = *reinterpret_cast<const uint2*>(&cs[m][wave][c * CS + 32 * j + 8 * g]);
+                else
+                    code = make_uint2(*reinterpret_cast<const uint32_t*>(&cs[m][wave][c * CS + 16 * j + 4 * g]), 0u);
+                const bf16x8 a = codes_bf16<WT>(code);
+                f32x4 t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bh, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bl, t, 0, 0, 0);
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const uint32_t wd = ssc[m][wave][(4 * g + v) * 4 + (j >> 1)];
+                    const float sv2 = __half2float(__ushort_as_half((unsigned short)(wd >> (16 * (j & 1)))));
+                    acc[m][v] += sv2 * t[v];
+                }
+            }
+        }
+        __syncthreads();                      // before the next slice overwrites the staging
+    }
+
+    float* Pw = P + (size_t)blockIdx.y * NM * N * 16;
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int n = rbase + 4 * g + v;
+            if (n < N) Pw[((size_t)m * N + n) * 16 + c] = acc[m][v];
+        }
+    if (SS) {
+        ss = wave32_sum(ss);                  // threads 32r .. 32r+31 hold row r
+        if ((tid & 31) == 0 && blockIdx.x == 0) SS[blockIdx.y * 16 + sm] = ss;
+    }
+}
+
+// y[m][n] = epilogue(sum over slices of P[s][.][n][m]): EPI 0 store, 1 add the
+// residual, 3 SwiGLU silu(g) * u; with SS, times inv_rms of row m first.
+template <int NM, int EPI>
+__global__ __launch_bounds__(256) void qlinear_small_reduce_kernel(const float* __restrict__ P,
+                                                                   const float* __restrict__ SS, int S,
+                                                                   int N, int K, int M, float eps,
+                                                                   const float* residual, float* y) {
+    const int n = blockIdx.x * 16 + (threadIdx.x >> 4), m = threadIdx.x & 15;
+    if (n >= N || m >= M) return;
+    // Four independent chains, combined in a fixed order: the loads of a
+    // chain do not wait for each other's L2 round trips.
+    const size_t st = (size_t)NM * N * 16;
+    float o[NM];
+#pragma unroll
+    for (int j = 0; j < NM; ++j) {
+        const float* p = P + ((size_t)j * N + n) * 16 + m;
+        float t0 = 0.f, t1 = 0.f, t2 = 0.f, t3 = 0.f;
+        int s = 0;
+        for (; s + 4 <= S; s += 4) {
+            t0 += p[s * st];
+            t1 += p[(s + 1) * st];
+            t2 += p[(s + 2) * st];
+            t3 += p[(s + 3) * st];
+        }
+        for (; s < S; ++s) t0 += p[s * st];
+        o[j] = (t0 + t1) + (t2 + t3);
+    }
+    if (SS) {
+        float ss = 0.f;
+        for (int s = 0; s < S; ++s) ss += SS[s * 16 + m];
+        const float inv = 1.f / sqrtf(ss / (float)K + eps);
+#pragma unroll
+        for (int j = 0; j < NM; ++j) o[j] *= inv;
+    }
+    const size_t off = (size_t)m * N + n;
+    float out = o[0];
+    if constexpr (EPI >= 2) out = o[1] * (o[0] / (1.f + expf(-o[0])));   // silu(g) * u, ops.hpp:409-441
+    if constexpr (EPI == 1) out += residual[off];
+    y[off] = out;
+}
+
+// Workgroup columns: one per slice (every workgroup loads once and computes
+// once) up to about 1024 workgroups (4 per CU); beyond that columns take
+// several slices, which bounds the partial-sum scratch.
+int small_grid_y(int N, int K) {
+    const int groups = (N + kSmallRows - 1) / kSmallRows, ns = K / kSmallSlice;
+    const int want = (1024 + groups - 1) / groups;
+    return want < ns ? want : ns;
+}
+
 int check_qgemm(const DevWeight& w, int M) {
     VH_ARG(w.dtype == VLRF_DT_Q8_0 || w.dtype == VLRF_DT_Q4_0,
            "qgemm: the MFMA path takes Q8_0/Q4_0 weights (dtype %d)", w.dtype);
@@ -318,6 +551,52 @@ int launch_qgemm_swiglu(hipStream_t s, const DevWeight& wg, const DevWeight& wu,
         if (h_bf16) launch_cfg<CfgSwi, 2>(s, wg.dtype, a, wg, &wu, M, nullptr, h);
         else launch_cfg<CfgSwi, 3>(s, wg.dtype, a, wg, &wu, M, nullptr, h);
     }
+    VH_LAUNCHED();
+    return VLRF_HIP_OK;
+}
+
+bool qlinear_small_supported(const DevWeight& w) {
+    return (w.dtype == VLRF_DT_Q8_0 || w.dtype == VLRF_DT_Q4_0) && w.q && w.d && w.K % kSmallSlice == 0;
+}
+
+size_t qlinear_small_scratch(int N, int K, bool two) {
+    const size_t S = (size_t)small_grid_y(N, K);
+    return S * (two ? 2 : 1) * (size_t)N * 16 * sizeof(float) + S * 16 * sizeof(float);
+}
+
+int launch_qlinear_small(hipStream_t s, const DevWeight& w0, const DevWeight* w1, const float* x,
+                         int M, const float* norm_w, float eps, const float* residual, float* scratch,
+                         float* y) {
+    VH_ARG(M >= 2 && M <= 16, "qlinear_small: M=%d outside [2,16]", M);
+    VH_ARG(qlinear_small_supported(w0), "qlinear_small: dtype %d / K %d not supported", w0.dtype, w0.K);
+    if (w1) VH_ARG(w1->N == w0.N && w1->K == w0.K && w1->dtype == w0.dtype && w1->q && w1->d,
+                   "qlinear_small: gate/up differ");
+    VH_ARG(x && y && scratch, "qlinear_small: null pointer");
+    const int N = w0.N, K = w0.K, S = small_grid_y(N, K), NM = w1 ? 2 : 1;
+    float* P = scratch;
+    float* SS = norm_w ? scratch + (size_t)S * NM * N * 16 : nullptr;
+    const dim3 grid((N + kSmallRows - 1) / kSmallRows, S), rgrid((N + 15) / 16);
+    const uint8_t* qb = w1 ? w1->q : nullptr;
+    const __half* db = w1 ? w1->d : nullptr;
+#define VH_PART(WT, NMV)                                                                            \
+    hipLaunchKernelGGL((qlinear_small_partial_kernel<WT, NMV>), grid, dim3(512), 0, s, w0.q, w0.d, qb, \
+                       db, N, K, M, x, norm_w, P, SS)
+    if (w0.dtype == VLRF_DT_Q8_0) {
+        if (w1) VH_PART(VLRF_DT_Q8_0, 2); else VH_PART(VLRF_DT_Q8_0, 1);
+    } else {
+        if (w1) VH_PART(VLRF_DT_Q4_0, 2); else VH_PART(VLRF_DT_Q4_0, 1);
+    }
+#undef VH_PART
+    VH_LAUNCHED();
+    if (w1)
+        hipLaunchKernelGGL((qlinear_small_reduce_kernel<2, 3>), rgrid, dim3(256), 0, s, P, SS, S, N, K, M, eps,
+                           nullptr, y);
+    else if (residual)
+        hipLaunchKernelGGL((qlinear_small_reduce_kernel<1, 1>), rgrid, dim3(256), 0, s, P, SS, S, N, K, M, eps,
+                           residual, y);
+    else
+        hipLaunchKernelGGL((qlinear_small_reduce_kernel<1, 0>), rgrid, dim3(256), 0, s, P, SS, S, N, K, M, eps,
+                           nullptr, y);
     VH_LAUNCHED();
     return VLRF_HIP_OK;
 }
