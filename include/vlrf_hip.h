@@ -206,6 +206,8 @@ void vlrf_hip_model_destroy(vlrf_hip_model_t m);
  * LM-head weights are in `dtype` host blocks.  Synchronous. */
 int  vlrf_hip_model_set_weight(vlrf_hip_model_t m, const char* name, const void* host,
                                int dtype, int rows, int cols);
+/* The configuration the model was created with. */
+int  vlrf_hip_model_get_config(vlrf_hip_model_t m, vlrf_hip_model_config* out);
 /* TransformerModel::reset_kv_cache (transformer.hpp:311-315). */
 int  vlrf_hip_model_reset(vlrf_hip_model_t m);
 int  vlrf_hip_model_used(vlrf_hip_model_t m);
@@ -247,6 +249,44 @@ int  vlrf_hip_model_kv_read(vlrf_hip_model_t m, int layer, int row0, int n, int8
  * [0] projection + LM-head weights, [1] KV cache, [2] everything else
  * (norm weights, embedding row, activations).  For roofline accounting. */
 int  vlrf_hip_model_step_bytes(vlrf_hip_model_t m, int ctx_len, double out[3]);
+
+/* ============================================================================
+ * NFW weight files (host side, no device needed) and loading them.
+ * Replaces: WeightMap's NFW reader (weights.hpp:58-62 constants, parse_header
+ * :289-339, f16 widening :76-96) for versions 1 (f32) and 2 (dtype byte, F32 /
+ * F16), extended by version 3: the same layout with block dtypes whose payload
+ * is the GGUF blocks (numel/32 blocks, row-major element order), so GGUF
+ * Q8_0/Q4_0 tensors are stored as they are instead of being decoded to f32
+ * (convert_gguf.py:193-263).  dtype numbers are GGML's.
+ * ========================================================================== */
+#define VLRF_NFW_F32   0
+#define VLRF_NFW_F16   1
+#define VLRF_NFW_Q4_0  2   /* 18 B per 32 elements */
+#define VLRF_NFW_Q8_0  8   /* 34 B per 32 elements */
+typedef struct vlrf_nfw* vlrf_nfw_t;
+/* Parses the header and every tensor descriptor; bad magic, unknown version
+ * or dtype, inconsistent sizes and truncation are VLRF_HIP_ERR_ARG. */
+int  vlrf_nfw_open(const char* path, vlrf_nfw_t* out);
+void vlrf_nfw_close(vlrf_nfw_t f);
+int  vlrf_nfw_version(vlrf_nfw_t f);
+int  vlrf_nfw_count(vlrf_nfw_t f);
+/* Index of the tensor called `name`, or -1. */
+int  vlrf_nfw_find(vlrf_nfw_t f, const char* name);
+/* name (valid until close), dtype, ndim, dims[ndim] (up to 8), numel, payload bytes. */
+int  vlrf_nfw_tensor_info(vlrf_nfw_t f, int i, const char** name, int* dtype, int* ndim,
+                          int32_t* dims, int64_t* numel, int64_t* bytes);
+/* Raw payload of tensor i into dst (cap bytes). */
+int  vlrf_nfw_read(vlrf_nfw_t f, int i, void* dst, int64_t cap);
+/* Tensor i as f32 (F16 widened as weights.hpp:76-96, blocks decoded as
+ * convert_gguf.py:233-263) into dst (n floats). */
+int  vlrf_nfw_read_f32(vlrf_nfw_t f, int i, float* dst, int64_t n);
+/* Sets every tensor of an NFW file that the model uses, by the engine's names
+ * (vlrf_hip_model_set_weight): norms and the embedding as f32, projections in
+ * the model's weight dtype (blocks uploaded unchanged), the LM head as blocks
+ * or f32.  All-zero bias tensors are accepted and dropped; a non-zero bias or
+ * an f32 projection for a block-typed model is VLRF_HIP_ERR_ARG.  *n_loaded
+ * receives the number of tensors set.  Synchronous. */
+int  vlrf_hip_model_load_nfw(vlrf_hip_model_t m, const char* path, int* n_loaded);
 
 #ifdef __cplusplus
 }

@@ -66,6 +66,17 @@ _SIGS = {
     "vlrf_hip_model_create": (i32, [vp, C.POINTER(ModelConfig), C.POINTER(vp)]),
     "vlrf_hip_model_destroy": (None, [vp]),
     "vlrf_hip_model_set_weight": (i32, [vp, C.c_char_p, vp, i32, i32, i32]),
+    "vlrf_hip_model_get_config": (i32, [vp, C.POINTER(ModelConfig)]),
+    "vlrf_hip_model_load_nfw": (i32, [vp, C.c_char_p, C.POINTER(C.c_int)]),
+    "vlrf_nfw_open": (i32, [C.c_char_p, C.POINTER(vp)]),
+    "vlrf_nfw_close": (None, [vp]),
+    "vlrf_nfw_version": (i32, [vp]),
+    "vlrf_nfw_count": (i32, [vp]),
+    "vlrf_nfw_find": (i32, [vp, C.c_char_p]),
+    "vlrf_nfw_tensor_info": (i32, [vp, i32, C.POINTER(C.c_char_p), C.POINTER(C.c_int), C.POINTER(C.c_int),
+                                   C.POINTER(C.c_int32), C.POINTER(C.c_int64), C.POINTER(C.c_int64)]),
+    "vlrf_nfw_read": (i32, [vp, i32, vp, i64]),
+    "vlrf_nfw_read_f32": (i32, [vp, i32, vp, i64]),
     "vlrf_hip_model_reset": (i32, [vp]),
     "vlrf_hip_model_used": (i32, [vp]),
     "vlrf_hip_model_step": (i32, [vp, i32, C.POINTER(C.c_int32), vp]),

@@ -29,7 +29,7 @@ CXX_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-pthread"]
 
 HIP_SOURCES = ["api.hip", "model.hip", "kernels/qlinear.hip", "kernels/attention.hip",
                "kernels/elementwise.hip", "kernels/gemm.hip"]
-CXX_SOURCES = ["host/format.cpp"]
+CXX_SOURCES = ["host/format.cpp", "host/nfw.cpp"]
 
 
 def _obj(src):

@@ -376,6 +376,12 @@ int vlrf_hip_model_reset(vlrf_hip_model_t m) {
 
 int vlrf_hip_model_used(vlrf_hip_model_t m) { return m ? m->pos : -1; }
 
+int vlrf_hip_model_get_config(vlrf_hip_model_t m, vlrf_hip_model_config* out) {
+    VH_ARG(m && out, "model_get_config: null argument");
+    *out = m->cfg;
+    return VLRF_HIP_OK;
+}
+
 int vlrf_hip_model_step(vlrf_hip_model_t m, int32_t token, int32_t* next, float* logits) {
     int rc = check_ready(m);
     if (rc) return rc;

@@ -215,6 +215,13 @@ class Model:
         check(lib().vlrf_hip_model_set_weight(self.h, name.encode(), host.ctypes.data, dtype,
                                               rows, cols))
 
+    def load_nfw(self, path):
+        """Sets the model's tensors from an NFW v1/v2/v3 file (vlrf_hip_model_load_nfw);
+        returns how many were set."""
+        n = C.c_int()
+        check(lib().vlrf_hip_model_load_nfw(self.h, str(path).encode(), C.byref(n)))
+        return n.value
+
     def reset(self):
         check(lib().vlrf_hip_model_reset(self.h))
 
