@@ -41,6 +41,7 @@ extern "C" {
 
 /* KV cache dtypes: reference include/model/kv_cache.hpp:36-40 (KVCacheDType). */
 #define VLRF_KV_F32   0
+#define VLRF_KV_F16   1   /* the reference's f32_to_f16 (kv_cache.hpp:68-97), bit-exact */
 #define VLRF_KV_Q8_0  2
 
 typedef struct vlrf_hip_ctx*    vlrf_hip_ctx_t;
@@ -86,10 +87,11 @@ int vlrf_hip_attn_f32(vlrf_hip_ctx_t ctx, const float* Q, const float* K, const 
                       float* O, int n_h, int T, int ctx_len, int d_h, float scale, int causal);
 
 /* ============================================================================
- * KV cache (Q8_0 per token row, reference kv_cache.hpp:14-17,132-293).
- * Device layout: per layer, K and V int8 [n_kv_heads][max_seq][d_head]
- * (head-major, so one head's history is one contiguous stream) and one f32
- * scale per token row for K and for V.
+ * KV cache (reference kv_cache.hpp:14-17,132-293), dtype VLRF_KV_F32, _F16 or
+ * _Q8_0 (per token row).  Device layout: per layer, K and V elements
+ * [n_kv_heads][max_seq][d_head] (head-major, so one head's history is one
+ * contiguous stream): f32, f16 bits, or int8 codes with one f32 scale per
+ * token row for K and for V.
  * ========================================================================== */
 /* Replaces: KVCache::KVCache (kv_cache.hpp:152-177), per layer. */
 int vlrf_hip_kv_create(vlrf_hip_ctx_t ctx, int n_layers, int max_seq, int n_kv_heads,
@@ -99,19 +101,22 @@ void vlrf_hip_kv_destroy(vlrf_hip_kv_t kv);
 int vlrf_hip_kv_reset(vlrf_hip_kv_t kv);
 /* Tokens stored so far in `layer` (KVCache::used). */
 int vlrf_hip_kv_used(vlrf_hip_kv_t kv, int layer);
-/* Replaces: KVCache::append (kv_cache.hpp:215-251): quantizes T rows of
- * device f32 k/v [T, n_kv_heads*d_head] bit-exactly as quantize_row_q8_0
- * (kv_cache.hpp:102-117) at positions [used, used+T), then used += T.
+/* Replaces: KVCache::append (kv_cache.hpp:215-251): stores T rows of device
+ * f32 k/v [T, n_kv_heads*d_head] at positions [used, used+T), then used += T,
+ * bit-exactly as the reference: Q8_0 quantize_row_q8_0 (kv_cache.hpp:102-117),
+ * F16 its f32_to_f16 (:68-97, half-up rounding, flush to zero), F32 a copy.
  * VLRF_HIP_ERR_OVERFLOW when used+T > max_seq (the reference throws). */
 int vlrf_hip_kv_append(vlrf_hip_kv_t kv, int layer, const float* k, const float* v, int T);
 /* Copies rows [row0,row0+n) of `layer` to host in the reference's token-major
- * layout: k_q/v_q int8 [n, n_kv_heads*d_head], k_s/v_s f32 [n]. Synchronous. */
+ * layout: k_q/v_q [n, n_kv_heads*d_head] elements of the cache's dtype (int8
+ * codes, f16 bits or f32; the pointers address bytes), k_s/v_s f32 [n] row
+ * scales for Q8_0 (ignored otherwise; any pointer may be NULL). Synchronous. */
 int vlrf_hip_kv_read(vlrf_hip_kv_t kv, int layer, int row0, int n, int8_t* k_q, int8_t* v_q,
                      float* k_s, float* v_s);
 /* Replaces: KVCache::dequant_into (kv_cache.hpp:259-286): device f32
  * K_out/V_out [ctx_len, n_kv_heads*d_head], token-major like the reference. */
 int vlrf_hip_kv_dequant(vlrf_hip_kv_t kv, int layer, int ctx_len, float* K_out, float* V_out);
-/* Decode attention of one token over the quantized cache, GQA-aware split-K:
+/* Decode attention of one token over the cache (any dtype), GQA-aware split-K:
  * q [n_heads*d_head] (already rotated), out [n_heads*d_head]; query head h
  * reads kv head h/(n_heads/n_kv_heads); non-causal over [0, ctx_len).
  * Replaces the decode branch of AttentionBlock::forward: dequant_into +
@@ -184,7 +189,8 @@ int vlrf_synth_normal(uint64_t seed, uint64_t stream, float std_dev, float* out,
 int vlrf_synth_tokens(uint64_t seed, uint64_t stream, int vocab, int32_t* out, int64_t n);
 
 /* ============================================================================
- * Decoder model (Llama-style: RMSNorm, RoPE half-split, SwiGLU, GQA, Q8_0 KV).
+ * Decoder model (Llama-style: RMSNorm, RoPE half-split, SwiGLU, GQA; F32, F16
+ * or Q8_0 KV cache).
  * Replaces the decode hot loop of TransformerModel::forward/generate
  * (transformer.hpp:335-424, 439-547) with a device-resident step: only token
  * ids cross PCIe.
@@ -193,6 +199,8 @@ typedef struct vlrf_hip_model_config {
     int32_t vocab_size, d_model, d_ff, n_heads, n_kv_heads, n_layers, max_seq_len;
     float   norm_eps, rope_theta;
     int32_t weight_dtype;   /* VLRF_DT_Q8_0 / VLRF_DT_Q4_0 / VLRF_DT_F32 for the projections */
+    int32_t kv_dtype;       /* VLRF_KV_F32 / _F16 / _Q8_0: ModelConfig::kv_cache_dtype (config.hpp),
+                               the reference's KVCacheDType numbering, whose default F32 is 0 */
 } vlrf_hip_model_config;
 
 int  vlrf_hip_model_create(vlrf_hip_ctx_t ctx, const vlrf_hip_model_config* cfg,
@@ -242,7 +250,7 @@ int  vlrf_hip_model_generate(vlrf_hip_model_t m, int32_t first, int n_steps, int
 int  vlrf_hip_model_generate_async(vlrf_hip_model_t m, int32_t first, int n_steps);
 int  vlrf_hip_model_read_generated(vlrf_hip_model_t m, int32_t* out_ids, int n);
 /* Rows [row0,row0+n) of layer `layer` of the model's KV cache, as
- * vlrf_hip_kv_read (token-major int8 codes, f32 row scales).  Synchronous. */
+ * vlrf_hip_kv_read (token-major elements of the cache dtype, Q8_0 row scales).  Synchronous. */
 int  vlrf_hip_model_kv_read(vlrf_hip_model_t m, int layer, int row0, int n, int8_t* k_q,
                             int8_t* v_q, float* k_s, float* v_s);
 /* Device bytes read per decode step at context length ctx_len, by stream:

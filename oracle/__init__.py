@@ -32,7 +32,11 @@ def build(with_ref=True):
 class OrcConfig(C.Structure):
     _fields_ = [(n, C.c_int) for n in ("vocab_size", "d_model", "d_ff", "n_heads",
                                        "n_kv_heads", "n_layers", "max_seq_len")] + \
-               [("norm_eps", C.c_float), ("rope_theta", C.c_float), ("n_threads", C.c_int)]
+               [("norm_eps", C.c_float), ("rope_theta", C.c_float), ("n_threads", C.c_int),
+                ("kv_dtype", C.c_int)]
+
+
+KV_F32, KV_F16, KV_Q8_0 = 0, 1, 2     # KVCacheDType (kv_cache.hpp:37-41)
 
 
 def lib():
@@ -60,6 +64,9 @@ def lib():
     L.orc_dequant_q4_0.argtypes = [u8p, f32p, C.c_int64]
     L.orc_f16_to_f32.argtypes = [C.c_uint16]
     L.orc_f16_to_f32.restype = C.c_float
+    L.orc_f32_to_f16_kv.argtypes = [C.c_float]
+    L.orc_f32_to_f16_kv.restype = C.c_uint16
+    L.orc_model_kv_raw.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p]
     L.orc_model_create.argtypes = [C.POINTER(OrcConfig)]
     L.orc_model_create.restype = C.c_void_p
     L.orc_model_destroy.argtypes = [C.c_void_p]
@@ -98,6 +105,11 @@ def ref():
     R.ref_hw_threads.restype = C.c_int
     R.ref_model_create.argtypes = [C.c_int] * 7 + [C.c_float, C.c_float]
     R.ref_model_create.restype = C.c_void_p
+    R.ref_model_create_kv.argtypes = [C.c_int] * 7 + [C.c_float, C.c_float, C.c_int]
+    R.ref_model_create_kv.restype = C.c_void_p
+    R.ref_model_kv_raw.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p]
+    R.ref_f32_to_f16.argtypes = [C.c_float]
+    R.ref_f32_to_f16.restype = C.c_uint16
     R.ref_model_set_tensor.argtypes = [C.c_void_p, C.c_char_p, f32p, C.c_int, C.c_int]
     R.ref_model_bind.argtypes = [C.c_void_p]
     R.ref_model_reset.argtypes = [C.c_void_p]
@@ -197,8 +209,16 @@ def dequant_q4_0(blocks, numel):
     return out
 
 
+def f32_to_f16_kv(x):
+    """KVCache's f32 -> f16 element conversion (kv_cache.hpp:68-97), elementwise."""
+    x = np.ascontiguousarray(x, np.float32).ravel()
+    f = lib().orc_f32_to_f16_kv
+    return np.array([f(float(v)) for v in x], np.uint16)
+
+
 class Model:
-    """Llama-style decoder with a Q8_0 KV cache (TransformerModel restatement).
+    """Llama-style decoder with an F32, F16 or Q8_0 KV cache (TransformerModel
+    restatement; cfg["kv_dtype"], default Q8_0).
 
     `weights` is a dict of f32 numpy arrays keyed like the reference WeightMap
     (transformer.hpp:566-629 names plus `layers.{l}.ffn.gate.weight`)."""
@@ -208,7 +228,7 @@ class Model:
         self.w = weights  # keep arrays alive
         c = OrcConfig(cfg["vocab_size"], cfg["d_model"], cfg["d_ff"], cfg["n_heads"],
                       cfg["n_kv_heads"], cfg["n_layers"], cfg["max_seq_len"],
-                      cfg["norm_eps"], cfg["rope_theta"], n_threads)
+                      cfg["norm_eps"], cfg["rope_theta"], n_threads, cfg.get("kv_dtype", KV_Q8_0))
         L = lib()
         self.h = L.orc_model_create(C.byref(c))
         L.orc_model_set_globals(self.h, weights["embed.weight"], weights["ln_final.weight"],
@@ -260,6 +280,18 @@ class Model:
         ks = np.ctypeslib.as_array(C.cast(ptrs[2], C.POINTER(C.c_float)), (n,))
         vs = np.ctypeslib.as_array(C.cast(ptrs[3], C.POINTER(C.c_float)), (n,))
         return kq, vq, ks, vs
+
+    def kv_raw(self, l):
+        """Layer l's K and V storage [max_seq, row] in the cache's own element
+        type: float32 (F32), uint16 f16 bits (F16) or int8 codes (Q8_0)."""
+        k, v = C.c_void_p(), C.c_void_p()
+        lib().orc_model_kv_raw(self.h, l, C.byref(k), C.byref(v))
+        c = self.cfg
+        row = c["n_kv_heads"] * (c["d_model"] // c["n_heads"])
+        ct = {KV_F32: C.c_float, KV_F16: C.c_uint16}.get(c.get("kv_dtype", KV_Q8_0), C.c_int8)
+        shape = (c["max_seq_len"], row)
+        return (np.ctypeslib.as_array(C.cast(k, C.POINTER(ct)), shape),
+                np.ctypeslib.as_array(C.cast(v, C.POINTER(ct)), shape))
 
     def __del__(self):
         try:

@@ -70,8 +70,11 @@ struct RefModel {
     vlrf::TransformerModel m;
 };
 
-void* ref_model_create(int vocab, int d_model, int d_ff, int n_heads, int n_kv_heads,
-                       int n_layers, int max_seq, float eps, float theta) {
+// kv_cache.hpp:68-97
+uint16_t ref_f32_to_f16(float f) { return vlrf::detail::f32_to_f16(f); }
+
+void* ref_model_create_kv(int vocab, int d_model, int d_ff, int n_heads, int n_kv_heads,
+                          int n_layers, int max_seq, float eps, float theta, int kv_dtype) {
     auto* r = new RefModel();
     vlrf::ModelConfig c;
     c.vocab_size = vocab;
@@ -88,11 +91,16 @@ void* ref_model_create(int vocab, int d_model, int d_ff, int n_heads, int n_kv_h
     c.activation = vlrf::Activation::SILU;
     c.pos_embedding = vlrf::PosEmbedding::ROTARY;
     c.tie_embeddings = false;
-    c.kv_cache_dtype = 2;  // Q8_0
+    c.kv_cache_dtype = kv_dtype;  // KVCacheDType: 0 F32, 1 F16, 2 Q8_0
     c.eos_token_id = -1;   // never stop early in fixture runs
     c.do_sample = false;
     r->m.init(c);
     return r;
+}
+
+void* ref_model_create(int vocab, int d_model, int d_ff, int n_heads, int n_kv_heads,
+                       int n_layers, int max_seq, float eps, float theta) {
+    return ref_model_create_kv(vocab, d_model, d_ff, n_heads, n_kv_heads, n_layers, max_seq, eps, theta, 2);
 }
 
 // Borrowed pointer (no copy): the caller keeps `data` alive.
@@ -122,6 +130,16 @@ void ref_model_kv(void* h, int l, int8_t** kq, int8_t** vq, float** ks, float** 
     *vq = c.V_q8.data();
     *ks = c.K_scale.data();
     *vs = c.V_scale.data();
+}
+
+// Layer l's K/V storage in the cache's own element type (kv_cache.hpp:141-150).
+void ref_model_kv_raw(void* h, int l, void** k, void** v) {
+    auto& c = static_cast<RefModel*>(h)->m.kv_caches[l];
+    switch (c.dtype) {
+        case vlrf::KVCacheDType::F32: *k = c.K.data_ptr(); *v = c.V.data_ptr(); break;
+        case vlrf::KVCacheDType::F16: *k = c.K_f16.data(); *v = c.V_f16.data(); break;
+        default: *k = c.K_q8.data(); *v = c.V_q8.data(); break;
+    }
 }
 
 void ref_model_destroy(void* h) { delete static_cast<RefModel*>(h); }

@@ -27,6 +27,31 @@
 #define ORC_AVX2 __attribute__((target("avx2,fma")))
 
 /* ------------------------------------------------------------------------ */
+/* KV cache F16 element conversion: reference kv_cache.hpp:68-97 (f32_to_f16: */
+/* mantissa rounded half up by +0x1000, exponent <= 0 flushed to signed zero, */
+/* overflow to inf, NaN keeps only a quiet bit).  The read side widens with   */
+/* weights.hpp:76-96 (orc_f16_to_f32 below).                                   */
+/* ------------------------------------------------------------------------ */
+uint16_t orc_f32_to_f16_kv(float f)
+{
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    uint32_t sign = (x >> 16) & 0x8000u;
+    int32_t e = (int32_t)((x >> 23) & 0xFF) - 127 + 15;
+    uint32_t mant = x & 0x7FFFFFu;
+    if (((x >> 23) & 0xFF) == 0xFF) return (uint16_t)(sign | 0x7C00u | (mant ? 0x0200u : 0u));
+    if (e <= 0) return (uint16_t)sign;
+    if (e >= 0x1F) return (uint16_t)(sign | 0x7C00u);
+    uint32_t r = (mant + 0x00001000u) >> 13;
+    if (r & 0x0400u) {
+        r = 0;
+        e += 1;
+        if (e >= 0x1F) return (uint16_t)(sign | 0x7C00u);
+    }
+    return (uint16_t)(sign | ((uint32_t)e << 10) | r);
+}
+
+/* ------------------------------------------------------------------------ */
 /* KV cache Q8_0: reference kv_cache.hpp:102-117 (quantize), :119-121 (dequant) */
 /* ------------------------------------------------------------------------ */
 float orc_quantize_row_q8_0(const float* src, int8_t* dst, int n)
@@ -412,12 +437,14 @@ void orc_dequant_q4_0(const uint8_t* blocks, float* out, int64_t numel)
 /* Whole model: TransformerModel::forward transformer.hpp:335-424,            */
 /* TransformerBlock::forward_v2 (pre-norm) transformer_block.hpp:141-159,     */
 /* AttentionBlock::forward attention.hpp:89-186, FeedForward::forward        */
-/* feedforward.hpp:50-77, KVCache Q8_0 kv_cache.hpp:215-286.                  */
+/* feedforward.hpp:50-77, KVCache F32 / F16 / Q8_0 kv_cache.hpp:152-286.     */
 /* ------------------------------------------------------------------------ */
 struct orc_layer {
     const float *ln1, *ln2, *wq, *wk, *wv, *wo, *wg, *w1, *w2;
-    int8_t *kq, *vq;
-    float *ks, *vs;
+    int8_t *kq, *vq;          /* Q8_0 codes [max_seq][row] */
+    float *ks, *vs;           /* Q8_0 row scales [max_seq] */
+    uint16_t *kh, *vh;        /* F16 [max_seq][row] */
+    float *kf, *vf;           /* F32 [max_seq][row] */
 };
 
 struct orc_model {
@@ -436,11 +463,21 @@ orc_model* orc_model_create(const orc_config* cfg)
     int d_head = cfg->d_model / cfg->n_heads;
     int row = cfg->n_kv_heads * d_head;
     m->L = (struct orc_layer*)calloc((size_t)cfg->n_layers, sizeof(struct orc_layer));
-    for (int l = 0; l < cfg->n_layers; ++l) {
-        m->L[l].kq = (int8_t*)calloc((size_t)cfg->max_seq_len * row, 1);
-        m->L[l].vq = (int8_t*)calloc((size_t)cfg->max_seq_len * row, 1);
-        m->L[l].ks = (float*)calloc((size_t)cfg->max_seq_len, sizeof(float));
-        m->L[l].vs = (float*)calloc((size_t)cfg->max_seq_len, sizeof(float));
+    size_t n = (size_t)cfg->max_seq_len * row;
+    for (int l = 0; l < cfg->n_layers; ++l) {      /* KVCache::KVCache kv_cache.hpp:152-177 */
+        struct orc_layer* L = &m->L[l];
+        if (cfg->kv_dtype == ORC_KV_F32) {
+            L->kf = (float*)calloc(n, sizeof(float));
+            L->vf = (float*)calloc(n, sizeof(float));
+        } else if (cfg->kv_dtype == ORC_KV_F16) {
+            L->kh = (uint16_t*)calloc(n, sizeof(uint16_t));
+            L->vh = (uint16_t*)calloc(n, sizeof(uint16_t));
+        } else {
+            L->kq = (int8_t*)calloc(n, 1);
+            L->vq = (int8_t*)calloc(n, 1);
+            L->ks = (float*)calloc((size_t)cfg->max_seq_len, sizeof(float));
+            L->vs = (float*)calloc((size_t)cfg->max_seq_len, sizeof(float));
+        }
     }
     size_t nt = (size_t)cfg->max_seq_len * (d_head / 2);
     m->cos_t = (float*)malloc(nt * sizeof(float));
@@ -453,7 +490,9 @@ void orc_model_destroy(orc_model* m)
 {
     if (!m) return;
     for (int l = 0; l < m->c.n_layers; ++l) {
-        free(m->L[l].kq); free(m->L[l].vq); free(m->L[l].ks); free(m->L[l].vs);
+        struct orc_layer* L = &m->L[l];
+        free(L->kq); free(L->vq); free(L->ks); free(L->vs);
+        free(L->kh); free(L->vh); free(L->kf); free(L->vf);
     }
     free(m->L); free(m->cos_t); free(m->sin_t); free(m);
 }
@@ -478,11 +517,14 @@ void orc_model_reset(orc_model* m)
 {
     int d_head = m->c.d_model / m->c.n_heads;
     size_t row = (size_t)m->c.n_kv_heads * d_head;
+    size_t n = (size_t)m->c.max_seq_len * row;
     for (int l = 0; l < m->c.n_layers; ++l) {
-        memset(m->L[l].kq, 0, (size_t)m->c.max_seq_len * row);
-        memset(m->L[l].vq, 0, (size_t)m->c.max_seq_len * row);
-        memset(m->L[l].ks, 0, (size_t)m->c.max_seq_len * sizeof(float));
-        memset(m->L[l].vs, 0, (size_t)m->c.max_seq_len * sizeof(float));
+        struct orc_layer* L = &m->L[l];
+        if (L->kq) { memset(L->kq, 0, n); memset(L->vq, 0, n); }
+        if (L->ks) { memset(L->ks, 0, (size_t)m->c.max_seq_len * sizeof(float));
+                     memset(L->vs, 0, (size_t)m->c.max_seq_len * sizeof(float)); }
+        if (L->kh) { memset(L->kh, 0, n * sizeof(uint16_t)); memset(L->vh, 0, n * sizeof(uint16_t)); }
+        if (L->kf) { memset(L->kf, 0, n * sizeof(float)); memset(L->vf, 0, n * sizeof(float)); }
     }
     m->used = 0;
 }
@@ -494,11 +536,23 @@ void orc_model_kv(orc_model* m, int l, int8_t** kq, int8_t** vq, float** ks, flo
     *kq = m->L[l].kq; *vq = m->L[l].vq; *ks = m->L[l].ks; *vs = m->L[l].vs;
 }
 
+void orc_model_kv_raw(orc_model* m, int l, void** k, void** v)
+{
+    struct orc_layer* L = &m->L[l];
+    if (L->kf) { *k = L->kf; *v = L->vf; }
+    else if (L->kh) { *k = L->kh; *v = L->vh; }
+    else { *k = L->kq; *v = L->vq; }
+}
+
 void orc_model_fill_kv(orc_model* m, int used, uint64_t seed)
 {
     int d_head = m->c.d_model / m->c.n_heads;
     size_t row = (size_t)m->c.n_kv_heads * d_head;
     if (used > m->c.max_seq_len) used = m->c.max_seq_len;
+    if (m->c.kv_dtype != ORC_KV_Q8_0) {      /* only the Q8_0 baseline fills codes */
+        m->used = 0;
+        return;
+    }
     uint64_t z = seed * 0x9E3779B97F4A7C15ull + 1;
     for (int l = 0; l < m->c.n_layers; ++l)
         for (int r = 0; r < used; ++r) {
@@ -547,14 +601,31 @@ int orc_model_forward_hidden(orc_model* m, float* x, int T)
         orc_linear(hn, L->wv, v, T, D, dkv, nt);
         orc_rope_apply(q, T, H, dh, pos_offset, m->cos_t, m->sin_t, c->max_seq_len);
         orc_rope_apply(k, T, G, dh, pos_offset, m->cos_t, m->sin_t, c->max_seq_len);
-        for (int t = 0; t < T; ++t) {                    /* KVCache::append */
-            int r = m->used + t;
-            L->ks[r] = orc_quantize_row_q8_0(k + (size_t)t * dkv, L->kq + (size_t)r * dkv, dkv);
-            L->vs[r] = orc_quantize_row_q8_0(v + (size_t)t * dkv, L->vq + (size_t)r * dkv, dkv);
-        }
-        for (int r = 0; r < ctx; ++r) {                  /* KVCache::dequant_into */
-            orc_dequantize_row_q8_0(L->kq + (size_t)r * dkv, L->ks[r], kd + (size_t)r * dkv, dkv);
-            orc_dequantize_row_q8_0(L->vq + (size_t)r * dkv, L->vs[r], vd + (size_t)r * dkv, dkv);
+        size_t r0 = (size_t)m->used * dkv, nr = (size_t)T * dkv, nc = (size_t)ctx * dkv;
+        if (c->kv_dtype == ORC_KV_F32) {                 /* KVCache::append / raw f32 view */
+            memcpy(L->kf + r0, k, nr * sizeof(float));
+            memcpy(L->vf + r0, v, nr * sizeof(float));
+            memcpy(kd, L->kf, nc * sizeof(float));
+            memcpy(vd, L->vf, nc * sizeof(float));
+        } else if (c->kv_dtype == ORC_KV_F16) {          /* append f32_to_f16, dequant_into f16_to_f32 */
+            for (size_t i = 0; i < nr; ++i) {
+                L->kh[r0 + i] = orc_f32_to_f16_kv(k[i]);
+                L->vh[r0 + i] = orc_f32_to_f16_kv(v[i]);
+            }
+            for (size_t i = 0; i < nc; ++i) {
+                kd[i] = orc_f16_to_f32(L->kh[i]);
+                vd[i] = orc_f16_to_f32(L->vh[i]);
+            }
+        } else {
+            for (int t = 0; t < T; ++t) {                /* KVCache::append */
+                int r = m->used + t;
+                L->ks[r] = orc_quantize_row_q8_0(k + (size_t)t * dkv, L->kq + (size_t)r * dkv, dkv);
+                L->vs[r] = orc_quantize_row_q8_0(v + (size_t)t * dkv, L->vq + (size_t)r * dkv, dkv);
+            }
+            for (int r = 0; r < ctx; ++r) {              /* KVCache::dequant_into */
+                orc_dequantize_row_q8_0(L->kq + (size_t)r * dkv, L->ks[r], kd + (size_t)r * dkv, dkv);
+                orc_dequantize_row_q8_0(L->vq + (size_t)r * dkv, L->vs[r], vd + (size_t)r * dkv, dkv);
+            }
         }
 #pragma omp parallel for num_threads(nt) schedule(static)
         for (int h = 0; h < H; ++h) {                    /* sdp_heads, head h -> kv head h/rep */

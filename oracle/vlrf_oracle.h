@@ -49,12 +49,20 @@ void orc_linear(const float* x, const float* W, float* y, int M, int K, int N, i
 void orc_dequant_q8_0(const uint8_t* blocks, float* out, int64_t numel);
 void orc_dequant_q4_0(const uint8_t* blocks, float* out, int64_t numel);
 float orc_f16_to_f32(uint16_t h);
+/* KVCache F16 element conversion (kv_cache.hpp:68-97). */
+uint16_t orc_f32_to_f16_kv(float f);
 
 /* ---- whole model (Llama-style, RMSNorm / RoPE / SwiGLU / GQA, Q8_0 KV) --- */
+/* KV cache dtypes, the reference's KVCacheDType values (kv_cache.hpp:37-41). */
+#define ORC_KV_F32  0
+#define ORC_KV_F16  1
+#define ORC_KV_Q8_0 2
+
 typedef struct orc_config {
     int vocab_size, d_model, d_ff, n_heads, n_kv_heads, n_layers, max_seq_len;
     float norm_eps, rope_theta;
     int n_threads;
+    int kv_dtype;          /* ORC_KV_* */
 } orc_config;
 
 typedef struct orc_model orc_model;
@@ -79,6 +87,8 @@ int  orc_model_forward_hidden(orc_model* m, float* x, int T);
 /* Token-major reference layout of layer l's cache: K/V int8 [max_seq, row_dim],
  * scales [max_seq]. */
 void orc_model_kv(orc_model* m, int l, int8_t** kq, int8_t** vq, float** ks, float** vs);
+/* Layer l's K/V storage of any dtype: f32, f16 bits or int8 codes [max_seq, row_dim]. */
+void orc_model_kv_raw(orc_model* m, int l, void** k, void** v);
 /* Timing support for the CPU baseline: marks `used` rows of every layer as
  * filled with seeded pseudo-random codes and scales, so decode steps can be
  * timed at a long context without a CPU prefill. */

@@ -11,8 +11,9 @@
 //              including T != ctx, where the reference's default is wrong;
 //   gemm       HipBackend::gemm (x . W^T) vs the reference CpuBackend::gemm;
 //   decode     HipDecoder::generate vs TransformerModel::generate, greedy,
-//              on a tiny Llama-style model with Q8_0 weights and KV cache:
-//              the token streams must be identical.
+//              on a tiny Llama-style model with Q8_0 weights, for each KV
+//              cache dtype (F32, the engine's default, F16 and Q8_0): the
+//              token streams must be identical.
 // Without a usable device (or with --cpu) the first two run through
 // HipBackend's CPU fallback and `decode` is skipped.  Exit status 0 = all pass.
 
@@ -141,7 +142,7 @@ void q8_roundtrip(Tensor& t) {
     vlrf_dequantize(blocks.data(), VLRF_DT_Q8_0, t.data_ptr(), t.numel());
 }
 
-void check_decode(HipBackend const& be) {
+void check_decode(HipBackend const& be, vlrf::KVCacheDType kv_dtype) {
     vlrf::ModelConfig c;
     c.vocab_size = 512;
     c.d_model = 256;
@@ -157,7 +158,7 @@ void check_decode(HipBackend const& be) {
     c.activation = vlrf::Activation::SILU;
     c.pos_embedding = vlrf::PosEmbedding::ROTARY;
     c.tie_embeddings = false;
-    c.kv_cache_dtype = static_cast<int>(vlrf::KVCacheDType::Q8_0);
+    c.kv_cache_dtype = static_cast<int>(kv_dtype);
     c.eos_token_id = -1;
     c.do_sample = false;
 
@@ -204,8 +205,9 @@ void check_decode(HipBackend const& be) {
     for (size_t i = 0; i < ref.size() && i < got.size(); ++i)
         if (ref[i] != got[i]) { first_diff = (int)i; break; }
     const bool ok = got.size() == ref.size() && first_diff < 0;
-    report(ok, "decode: HipDecoder::generate == TransformerModel::generate (64 greedy steps)",
-           first_diff < 0 ? 0.0 : (double)first_diff);
+    const std::string what = std::string("decode: HipDecoder::generate == TransformerModel::generate (64 greedy "
+                                         "steps, KV ") + vlrf::kv_cache_dtype_name(kv_dtype) + ")";
+    report(ok, what, first_diff < 0 ? 0.0 : (double)first_diff);
 }
 
 }  // namespace
@@ -219,7 +221,8 @@ int main(int argc, char** argv) {
     check_attention(be);
     check_gemm(be);
     if (dev)
-        check_decode(be);
+        for (auto dt : {vlrf::KVCacheDType::F32, vlrf::KVCacheDType::F16, vlrf::KVCacheDType::Q8_0})
+            check_decode(be, dt);
     else
         std::printf("SKIP decode (no HIP device)\n");
     std::printf("%s: %d failure(s)\n", g_fail ? "FAILED" : "OK", g_fail);

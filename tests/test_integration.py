@@ -35,4 +35,6 @@ def test_adapter_on_device_matches_reference_engine():
     print("[case] hip_integration driver on device", flush=True)
     p = run([], 300)
     assert p.returncode == 0, p.stdout
-    assert "PASS decode" in p.stdout, p.stdout
+    for kv in ("f32", "f16", "q8_0"):
+        assert f"PASS decode: HipDecoder::generate == TransformerModel::generate (64 greedy steps, KV {kv})" \
+            in p.stdout, p.stdout

@@ -277,3 +277,72 @@ def test_model_prefill_matches_incremental():
         tb, lb = b.forward([int(t)], True)
     assert ta == tb
     assert np.max(np.abs(la - lb)) <= 1e-3 * np.max(np.abs(la))
+
+
+# ---- F32 / F16 KV caches (kv_cache.hpp:37-41, 68-97, 152-286) --------------------
+def test_f32_to_f16_kv_known_answers():
+    """Closed-form answers of the reference's conversion, chosen where it
+    differs from IEEE round-to-nearest-even: exact halfway cases round up in
+    magnitude, values below 2^-14 flush to signed zero, 65520 overflows."""
+    cases = {1.0: 0x3C00, -2.0: 0xC000, 65504.0: 0x7BFF, 65520.0: 0x7C00, 1e9: 0x7C00,
+             2.0 ** -14: 0x0400, 2.0 ** -15: 0x0000, -1e-6: 0x8000, 0.0: 0x0000,
+             1.0 + 2.0 ** -11: 0x3C01,            # tie: RNE would give 0x3C00
+             1.0 + 3 * 2.0 ** -11: 0x3C02,        # tie between 0x3C01 and 0x3C02
+             float("inf"): 0x7C00, float("-inf"): 0xFC00}
+    for x, want in cases.items():
+        assert oracle.lib().orc_f32_to_f16_kv(x) == want, (x, hex(oracle.lib().orc_f32_to_f16_kv(x)))
+    nan = oracle.lib().orc_f32_to_f16_kv(float("nan"))
+    assert nan & 0x7C00 == 0x7C00 and nan & 0x3FF == 0x200
+
+
+@needs_ref
+def test_f32_to_f16_kv_bit_exact_vs_reference():
+    rng = np.random.default_rng(5)
+    bits = np.concatenate([rng.integers(0, 2 ** 32, 200000, dtype=np.uint64).astype(np.uint32),
+                           np.array([0x7F800000, 0xFF800000, 0x7FC00000, 0x7F800001, 0x00000001,
+                                     0x387FFFFF, 0x38800000, 0x477FEFFF, 0x477FF000, 0x33800000], np.uint32)])
+    xs = bits.view(np.float32)
+    # inputs around every rounding boundary of the 10-bit mantissa
+    base = (rng.integers(0x38800000, 0x47800000, 2000).astype(np.uint32) & ~np.uint32(0x1FFF)) | np.uint32(0x1000)
+    xs = np.concatenate([xs, base.view(np.float32), (base - 1).view(np.float32), (base + 1).view(np.float32)])
+    f_orc, f_ref = oracle.lib().orc_f32_to_f16_kv, R.ref_f32_to_f16
+    for x in xs:
+        assert f_orc(float(x)) == f_ref(float(x)), hex(np.float32(x).view(np.uint32))
+
+
+@needs_ref
+@pytest.mark.parametrize("kv_dtype", [oracle.KV_F32, oracle.KV_F16])
+def test_model_f32_f16_kv_bit_exact_vs_reference(kv_dtype):
+    """Prefill then 24 decode steps with the reference's F32 / F16 caches:
+    logits and the caches' raw contents equal the reference's bit for bit."""
+    import ctypes as C
+    cfg, w = _tiny(33)
+    cfg["kv_dtype"] = kv_dtype
+    nt = R.ref_hw_threads()
+    om = oracle.Model(cfg, w, n_threads=nt)
+    h = R.ref_model_create_kv(cfg["vocab_size"], cfg["d_model"], cfg["d_ff"], cfg["n_heads"],
+                              cfg["n_kv_heads"], cfg["n_layers"], cfg["max_seq_len"],
+                              cfg["norm_eps"], cfg["rope_theta"], kv_dtype)
+    try:
+        for k, v in w.items():
+            R.ref_model_set_tensor(h, k.encode(), v, v.shape[0] if v.ndim == 2 else 0, v.shape[-1])
+        R.ref_model_bind(h)
+        prompt = F.tokens(33, "prompt", 20, cfg["vocab_size"])
+        lg = np.zeros(cfg["vocab_size"], np.float32)
+        t1, l1 = om.forward(prompt, True)
+        t2 = R.ref_model_forward(h, prompt, 20, lg.ctypes.data)
+        assert t1 == t2 and np.array_equal(l1, lg)
+        for _ in range(24):
+            t1, l1 = om.forward([t1], True)
+            t2 = R.ref_model_forward(h, np.array([t2], np.int32), 1, lg.ctypes.data)
+            assert t1 == t2 and np.array_equal(l1, lg)
+        ct = C.c_float if kv_dtype == oracle.KV_F32 else C.c_uint16
+        for layer in range(cfg["n_layers"]):
+            ok, ov = om.kv_raw(layer)
+            rk, rv = C.c_void_p(), C.c_void_p()
+            R.ref_model_kv_raw(h, layer, C.byref(rk), C.byref(rv))
+            assert np.array_equal(np.ctypeslib.as_array(C.cast(rk, C.POINTER(ct)), ok.shape), ok)
+            assert np.array_equal(np.ctypeslib.as_array(C.cast(rv, C.POINTER(ct)), ov.shape), ov)
+            assert ok[:44].any() and not ok[44:].any()       # 20 + 24 rows written
+    finally:
+        R.ref_model_destroy(h)

@@ -6,7 +6,7 @@ PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(PKG, "libvlrf_hip.so")
 
 DT_F32, DT_Q4_0, DT_Q8_0 = 0, 2, 8
-KV_Q8_0 = 2
+KV_F32, KV_F16, KV_Q8_0 = 0, 1, 2     # KVCacheDType (kv_cache.hpp:37-41)
 
 OK, ERR_ARG, ERR_RUNTIME, ERR_NOMEM, ERR_OVERFLOW, ERR_NODEV = 0, -1, -2, -3, -4, -5
 
@@ -20,7 +20,8 @@ class HipError(RuntimeError):
 class ModelConfig(C.Structure):
     _fields_ = [(n, C.c_int32) for n in ("vocab_size", "d_model", "d_ff", "n_heads", "n_kv_heads",
                                          "n_layers", "max_seq_len")] + \
-               [("norm_eps", C.c_float), ("rope_theta", C.c_float), ("weight_dtype", C.c_int32)]
+               [("norm_eps", C.c_float), ("rope_theta", C.c_float), ("weight_dtype", C.c_int32),
+                ("kv_dtype", C.c_int32)]
 
 
 vp, i32, i64, u64, f32, sz = C.c_void_p, C.c_int, C.c_int64, C.c_uint64, C.c_float, C.c_size_t

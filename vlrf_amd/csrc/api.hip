@@ -190,25 +190,27 @@ struct vlrf_hip_kv {
     } while (0)
 
 namespace vlrf_hip {
-// Rows [row0, row0+n) of a head-major cache layer to host, token-major.
+// Rows [row0, row0+n) of a head-major cache layer to host, token-major, as
+// the cache's own elements (int8 codes, f16 bits or f32); scales for Q8_0.
 int kv_rows_to_host(hipStream_t s, const KVLayer& L, int G, int D, int max_seq, int row0, int n,
                     int8_t* k_q, int8_t* v_q, float* k_s, float* v_s) {
-    const int row = G * D;
-    std::vector<int8_t> hk((size_t)G * n * D), hv((size_t)G * n * D);
+    const size_t eb = (size_t)kv_elem_bytes(L.dtype), hd = (size_t)D * eb, row = (size_t)G * hd;
+    std::vector<int8_t> hk((size_t)G * n * hd), hv((size_t)G * n * hd);
     for (int g = 0; g < G; ++g) {
-        const size_t off = ((size_t)g * max_seq + row0) * D;
-        VH_CHECK(hipMemcpyAsync(hk.data() + (size_t)g * n * D, L.k + off, (size_t)n * D, hipMemcpyDeviceToHost, s));
-        VH_CHECK(hipMemcpyAsync(hv.data() + (size_t)g * n * D, L.v + off, (size_t)n * D, hipMemcpyDeviceToHost, s));
+        const size_t off = ((size_t)g * max_seq + row0) * hd;
+        VH_CHECK(hipMemcpyAsync(hk.data() + (size_t)g * n * hd, L.k + off, n * hd, hipMemcpyDeviceToHost, s));
+        VH_CHECK(hipMemcpyAsync(hv.data() + (size_t)g * n * hd, L.v + off, n * hd, hipMemcpyDeviceToHost, s));
     }
-    if (k_s) VH_CHECK(hipMemcpyAsync(k_s, L.ks + row0, n * sizeof(float), hipMemcpyDeviceToHost, s));
-    if (v_s) VH_CHECK(hipMemcpyAsync(v_s, L.vs + row0, n * sizeof(float), hipMemcpyDeviceToHost, s));
+    const bool q8 = L.dtype == VLRF_KV_Q8_0;
+    if (k_s && q8) VH_CHECK(hipMemcpyAsync(k_s, L.ks + row0, n * sizeof(float), hipMemcpyDeviceToHost, s));
+    if (v_s && q8) VH_CHECK(hipMemcpyAsync(v_s, L.vs + row0, n * sizeof(float), hipMemcpyDeviceToHost, s));
     VH_CHECK(hipStreamSynchronize(s));
     for (int t = 0; t < n; ++t)
-        for (int g = 0; g < G; ++g)
-            for (int d = 0; d < D; ++d) {
-                if (k_q) k_q[(size_t)t * row + g * D + d] = hk[((size_t)g * n + t) * D + d];
-                if (v_q) v_q[(size_t)t * row + g * D + d] = hv[((size_t)g * n + t) * D + d];
-            }
+        for (int g = 0; g < G; ++g) {
+            const size_t src = ((size_t)g * n + t) * hd, dst = (size_t)t * row + g * hd;
+            if (k_q) std::memcpy(k_q + dst, hk.data() + src, hd);
+            if (v_q) std::memcpy(v_q + dst, hv.data() + src, hd);
+        }
     return VLRF_HIP_OK;
 }
 }  // namespace vlrf_hip
@@ -354,9 +356,8 @@ int vlrf_hip_attn_f32(vlrf_hip_ctx_t ctx, const float* Q, const float* K, const 
         float* part = nullptr;
         int rc = ctx->scratch((size_t)n_h * splits * (d_h + 2) * sizeof(float), &part);
         if (rc) return rc;
-        return launch_attn_decode(ctx->stream, Q, nullptr, nullptr, nullptr, nullptr, K, V,
-                                  (long)ctx_len * d_h, n_h, n_h, d_h, ctx_len, nullptr, splits, scale,
-                                  part, O);
+        return launch_attn_decode(ctx->stream, Q, K, V, nullptr, nullptr, VLRF_KV_F32, (long)ctx_len * d_h, n_h,
+                                  n_h, d_h, ctx_len, nullptr, splits, scale, part, O);
     }
     return launch_attn_f32_tiled(ctx->stream, Q, K, V, O, n_h, T, ctx_len, d_h, scale, causal);
 }
@@ -367,7 +368,8 @@ int vlrf_hip_kv_create(vlrf_hip_ctx_t ctx, int n_layers, int max_seq, int n_kv_h
     VH_CTX(ctx);
     VH_ARG(out != nullptr, "kv_create: null output");
     *out = nullptr;
-    VH_ARG(dtype == VLRF_KV_Q8_0, "kv_create: only the Q8_0 cache is device-resident (dtype %d)", dtype);
+    VH_ARG(dtype == VLRF_KV_Q8_0 || dtype == VLRF_KV_F16 || dtype == VLRF_KV_F32,
+           "kv_create: cache dtype %d is not F32, F16 or Q8_0", dtype);
     VH_ARG(n_layers >= 1 && max_seq >= 1 && n_kv_heads >= 1 && d_head >= 2 && d_head % 16 == 0,
            "kv_create: bad shape layers=%d max_seq=%d n_kv=%d d_head=%d", n_layers, max_seq,
            n_kv_heads, d_head);
@@ -380,11 +382,13 @@ int vlrf_hip_kv_create(vlrf_hip_ctx_t ctx, int n_layers, int max_seq, int n_kv_h
     kv->d_head = d_head;
     kv->layers.resize(n_layers);
     kv->used.assign(n_layers, 0);
-    const size_t data = (size_t)n_kv_heads * max_seq * d_head;
+    const size_t data = (size_t)n_kv_heads * max_seq * d_head * kv_elem_bytes(dtype);
     for (auto& L : kv->layers) {
+        L.dtype = dtype;
+        const bool q8 = dtype == VLRF_KV_Q8_0;
         if (hipMalloc(&L.k, data) != hipSuccess || hipMalloc(&L.v, data) != hipSuccess ||
-            hipMalloc(&L.ks, max_seq * sizeof(float)) != hipSuccess ||
-            hipMalloc(&L.vs, max_seq * sizeof(float)) != hipSuccess) {
+            (q8 && hipMalloc(&L.ks, max_seq * sizeof(float)) != hipSuccess) ||
+            (q8 && hipMalloc(&L.vs, max_seq * sizeof(float)) != hipSuccess)) {
             vlrf_hip_kv_destroy(kv);
             set_error("kv_create: hipMalloc failed");
             return VLRF_HIP_ERR_NOMEM;
@@ -415,12 +419,12 @@ void vlrf_hip_kv_destroy(vlrf_hip_kv_t kv) {
 int vlrf_hip_kv_reset(vlrf_hip_kv_t kv) {
     VH_ARG(kv != nullptr, "kv_reset: null cache");
     VH_CTX(kv->ctx);
-    const size_t data = (size_t)kv->n_kv * kv->max_seq * kv->d_head;
     for (auto& L : kv->layers) {
+        const size_t data = (size_t)kv->n_kv * kv->max_seq * kv->d_head * kv_elem_bytes(L.dtype);
         VH_CHECK(hipMemsetAsync(L.k, 0, data, kv->ctx->stream));
         VH_CHECK(hipMemsetAsync(L.v, 0, data, kv->ctx->stream));
-        VH_CHECK(hipMemsetAsync(L.ks, 0, kv->max_seq * sizeof(float), kv->ctx->stream));
-        VH_CHECK(hipMemsetAsync(L.vs, 0, kv->max_seq * sizeof(float), kv->ctx->stream));
+        if (L.ks) VH_CHECK(hipMemsetAsync(L.ks, 0, kv->max_seq * sizeof(float), kv->ctx->stream));
+        if (L.vs) VH_CHECK(hipMemsetAsync(L.vs, 0, kv->max_seq * sizeof(float), kv->ctx->stream));
     }
     VH_CHECK(hipStreamSynchronize(kv->ctx->stream));
     kv->used.assign(kv->n_layers, 0);
@@ -481,9 +485,8 @@ int vlrf_hip_attn_decode(vlrf_hip_kv_t kv, int layer, const float* q, float* out
     int rc = kv->ctx->scratch((size_t)n_heads * splits * (kv->d_head + 2) * sizeof(float), &part);
     if (rc) return rc;
     const KVLayer& L = kv->layers[layer];
-    return launch_attn_decode(kv->ctx->stream, q, L.k, L.v, L.ks, L.vs, nullptr, nullptr,
-                              (long)kv->max_seq * kv->d_head, n_heads, kv->n_kv, kv->d_head, ctx_len,
-                              nullptr, splits, scale, part, out);
+    return launch_attn_decode(kv->ctx->stream, q, L.k, L.v, L.ks, L.vs, L.dtype, (long)kv->max_seq * kv->d_head,
+                              n_heads, kv->n_kv, kv->d_head, ctx_len, nullptr, splits, scale, part, out);
 }
 
 // ---- quantized linear ----------------------------------------------------------

@@ -69,12 +69,43 @@ int weight_alloc(DevWeight& w, int dtype, int N, int K);
 void weight_release(DevWeight& w);
 
 // ---- KV cache ------------------------------------------------------------------
+// k and v address [n_kv][max_seq][d_head] elements of the layer's dtype: int8
+// codes (Q8_0, with one f32 scale per token row in ks/vs), f16 bits or f32.
 struct KVLayer {
-    int8_t* k = nullptr;   // [n_kv][max_seq][d_head]
+    int8_t* k = nullptr;
     int8_t* v = nullptr;
-    float* ks = nullptr;   // [max_seq]
+    float* ks = nullptr;   // [max_seq], Q8_0 only
     float* vs = nullptr;
+    int dtype = VLRF_KV_Q8_0;
 };
+
+__host__ __device__ inline int kv_elem_bytes(int dtype) {
+    return dtype == VLRF_KV_F32 ? 4 : dtype == VLRF_KV_F16 ? 2 : 1;
+}
+
+// KVCache's f32 -> f16 element conversion (kv_cache.hpp:68-97): the mantissa is
+// rounded half up (+0x1000 then >> 13), exponents <= 0 flush to signed zero,
+// overflow gives inf, NaN keeps one quiet bit.  Not IEEE round-to-nearest-even.
+__device__ __forceinline__ uint16_t f32_to_f16_kv(float f) {
+    const uint32_t x = __float_as_uint(f);
+    const uint32_t sign = (x >> 16) & 0x8000u, mant = x & 0x7FFFFFu;
+    int e = (int)((x >> 23) & 0xFFu) - 112;
+    if (((x >> 23) & 0xFFu) == 0xFFu) return (uint16_t)(sign | 0x7C00u | (mant ? 0x0200u : 0u));
+    if (e <= 0) return (uint16_t)sign;
+    if (e >= 0x1F) return (uint16_t)(sign | 0x7C00u);
+    uint32_t r = (mant + 0x1000u) >> 13;
+    if (r & 0x400u) {
+        r = 0;
+        if (++e >= 0x1F) return (uint16_t)(sign | 0x7C00u);
+    }
+    return (uint16_t)(sign | ((uint32_t)e << 10) | r);
+}
+
+// f16 -> f32 widening: exact (v_cvt_f32_f16); the cache never holds the
+// subnormals where the reference's loop and the hardware could differ.
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+    return __half2float(__ushort_as_half((unsigned short)h));
+}
 
 // Rows [row0, row0+n) of a head-major cache layer to host in the reference's
 // token-major layout (synchronous).
@@ -142,27 +173,28 @@ int launch_attn_prefill(hipStream_t s, const float* qkv, int ld, const KVLayer& 
                         int n_heads, int n_kv, int d_head, int max_seq, float scale, uint16_t* out);
 
 // Decode fusion of the attention kernel (model step): RoPE of q and of the
-// token's k at the device position, and the Q8_0 append of its K/V row.
+// token's k at the device position, and the append of its K/V row.
 struct DecodeFuse {
     const float* k_new = nullptr;   // [n_kv*d_head] unrotated k of the token
     const float* v_new = nullptr;
     const float* cos_t = nullptr;   // [max_seq][d_head/2]
     const float* sin_t = nullptr;
-    int8_t* kq_w = nullptr;         // the layer's cache (same as kq/vq)
+    int8_t* kq_w = nullptr;         // the layer's cache elements, as bytes (same as kc/vc)
     int8_t* vq_w = nullptr;
-    float* ks_w = nullptr;
+    float* ks_w = nullptr;          // Q8_0 row scales
     float* vs_w = nullptr;
     int n_kv = 0, max_seq = 0;
 };
 
-// Split-K decode attention. KV either Q8 cache (kq/vq + scales, head stride
-// max_seq*d) or f32 [n_kv][ctx][d] (kf/vf).  ctx from *ctx_dev (+1 when
-// ctx_plus_one) when non-null.  part must hold n_heads*n_splits*(d+2) floats.
+// Split-K decode attention over K/V elements of kv_dtype (VLRF_KV_Q8_0 codes
+// with row scales ks/vs, VLRF_KV_F16 bits, VLRF_KV_F32) laid out
+// [n_kv][head_stride/d][d]: a cache layer (head_stride = max_seq*d) or plain
+// f32 K/V.  ctx from *ctx_dev (+1 when fused) when non-null.  part must hold
+// n_heads*n_splits*(d+2) floats.
 int attn_decode_splits(int max_ctx);
-int launch_attn_decode(hipStream_t s, const float* q, const int8_t* kq, const int8_t* vq,
-                       const float* ks, const float* vs, const float* kf, const float* vf,
-                       long head_stride, int n_heads, int n_kv, int d_head, int ctx_len,
-                       const int* ctx_dev, int n_splits, float scale, float* part, float* out,
+int launch_attn_decode(hipStream_t s, const float* q, const void* kc, const void* vc, const float* ks,
+                       const float* vs, int kv_dtype, long head_stride, int n_heads, int n_kv, int d_head,
+                       int ctx_len, const int* ctx_dev, int n_splits, float scale, float* part, float* out,
                        const DecodeFuse* fuse = nullptr);
 int launch_attn_f32_tiled(hipStream_t s, const float* Q, const float* K, const float* V,
                           float* O, int n_h, int T, int ctx_len, int d_h, float scale,

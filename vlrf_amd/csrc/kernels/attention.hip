@@ -41,18 +41,24 @@ __device__ __forceinline__ void rope2(float x0, float x1, float c, float s, floa
     *y1 = e + f;
 }
 
-template <int D, int REP, bool Q8, bool FUSED>
+// KVT: cache element type VLRF_KV_Q8_0 (int8 codes, f32 scale per token row),
+// VLRF_KV_F16 (the reference's f16 bits) or VLRF_KV_F32; kc/vc address the
+// elements ([n_kv][head_stride/D][D]) as bytes.
+template <int D, int REP, int KVT, bool FUSED>
 __global__ __launch_bounds__(kAttnThreads) void attn_decode_partial_kernel(
-    const float* __restrict__ q, const int8_t* kq, const int8_t* vq, const float* ks, const float* vs,
-    const float* __restrict__ kf, const float* __restrict__ vf, long head_stride, int ctx_len,
-    const int* __restrict__ ctx_dev, int n_splits, float scale, float* __restrict__ part, DecodeFuse fz) {
+    const float* __restrict__ q, const int8_t* kc, const int8_t* vc, const float* ks, const float* vs,
+    long head_stride, int ctx_len, const int* __restrict__ ctx_dev, int n_splits, float scale,
+    float* __restrict__ part, DecodeFuse fz) {
+    constexpr bool Q8 = KVT == VLRF_KV_Q8_0, H16 = KVT == VLRF_KV_F16;
+    constexpr int EB = Q8 ? 1 : H16 ? 2 : 4;             // bytes per cache element
     constexpr int HALF = D / 2;
     static_assert(HALF == 32 || HALF == 64, "a RoPE pair index is tid % HALF only for HALF | 64");
     constexpr int NT = kAttnThreads, NW = NT / 64;
     constexpr int HPW = REP >= NW ? REP / NW : 1;        // query heads scored per wave
-    constexpr int KW = Q8 ? D / 16 : D / 4;              // 16-byte words of one K row
+    constexpr int KW = D * EB / 16;                      // 16-byte words of one K row
+    constexpr int EPW = 16 / EB;                         // elements per 16-byte word
     constexpr int VE = kChunk * D / NT;                  // V elements staged per thread
-    constexpr int VD = Q8 ? VE / 4 : VE;                 // their dwords (Q8: 4 codes each)
+    constexpr int VD = VE * EB / 4;                      // their dwords
     static_assert(VD % 2 == 0 && VD <= 16, "V staging granularity");
     __shared__ __align__(16) float qs[REP][D];
     __shared__ __align__(16) float vsm[kChunk][D];       // the chunk's dequantized V rows
@@ -101,19 +107,15 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_partial_kernel(
     const int jt = min(c0 + lane, cap - 1);
     uint4 kraw[KW];
 #pragma unroll
-    for (int i = 0; i < KW; ++i) {
-        if constexpr (Q8) kraw[i] = *reinterpret_cast<const uint4*>(kq + hb + (size_t)jt * D + 16 * i);
-        else kraw[i] = *reinterpret_cast<const uint4*>(kf + hb + (size_t)jt * D + 4 * i);
-    }
+    for (int i = 0; i < KW; ++i)
+        kraw[i] = *reinterpret_cast<const uint4*>(kc + (hb + (size_t)jt * D) * EB + 16 * i);
     const float ksc = Q8 ? ks[jt] : 1.f;
     const int tv = tid / (D / VE), pv = tid % (D / VE);
     const int jv = min(c0 + tv, cap - 1);
     uint2 vraw[VD / 2];
 #pragma unroll
-    for (int i = 0; i < VD / 2; ++i) {
-        if constexpr (Q8) vraw[i] = *reinterpret_cast<const uint2*>(vq + hb + (size_t)jv * D + pv * VE + 8 * i);
-        else vraw[i] = *reinterpret_cast<const uint2*>(vf + hb + (size_t)jv * D + pv * VE + 2 * i);
-    }
+    for (int i = 0; i < VD / 2; ++i)
+        vraw[i] = *reinterpret_cast<const uint2*>(vc + (hb + (size_t)jv * D + pv * VE) * EB + 8 * i);
     const float vsc = Q8 ? vs[jv] : 1.f;
 
     // The device position is read only now: none of the addresses above depend
@@ -156,8 +158,8 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_partial_kernel(
         }
     }
 
-    // ---- V chunk into LDS, dequantized (dequantize_row_q8_0); rows past the
-    // context are zero, and the new token's row is written by wave 0 below.
+    // ---- V chunk into LDS as f32 (dequantize_row_q8_0 / f16_to_f32); rows past
+    // the context are zero, and the new token's row is written by wave 0 below.
     if (!(has_new && c0 + tv == pos)) {
         float* dst = &vsm[tv][pv * VE];
         const bool live = c0 + tv < ctx;
@@ -174,6 +176,13 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_partial_kernel(
                     o.w = live ? (float)(int8_t)(w[k] >> 24) * vsc : 0.f;
                     *reinterpret_cast<float4*>(dst + 8 * i + 4 * k) = o;
                 }
+            } else if constexpr (H16) {
+                float4 o;
+                o.x = live ? f16_bits_to_f32(w[0] & 0xFFFFu) : 0.f;
+                o.y = live ? f16_bits_to_f32(w[0] >> 16) : 0.f;
+                o.z = live ? f16_bits_to_f32(w[1] & 0xFFFFu) : 0.f;
+                o.w = live ? f16_bits_to_f32(w[1] >> 16) : 0.f;
+                *reinterpret_cast<float4*>(dst + 4 * i) = o;
             } else {
                 float2 o;
                 o.x = live ? __uint_as_float(w[0]) : 0.f;
@@ -184,11 +193,12 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_partial_kernel(
     }
 
     // ---- decode fusion: the current token's K/V row (wave 0 of the chunk holding it)
-    // attention.hpp:109-128: RoPE on k, then KVCache::append quantizes the whole
-    // row (quantize_row_q8_0, kv_cache.hpp:102-117) before attention reads it.
-    // Every chunk holding `pos` quantizes the row itself and uses the dequantized
-    // values for that token; the workgroup of KV head g stores head g's codes,
-    // KV head 0 stores the row scales.  Wave reductions only: no workgroup barrier.
+    // attention.hpp:109-128: RoPE on k, then KVCache::append stores the row
+    // before attention reads it: Q8_0 quantizes the whole row (quantize_row_q8_0,
+    // kv_cache.hpp:102-117), F16 converts each element (f32_to_f16, :68-97), F32
+    // copies.  Every chunk holding `pos` converts the row itself and uses the
+    // stored values for that token; the workgroup of KV head g stores head g's
+    // elements, KV head 0 the Q8_0 row scales.  Wave reductions only.
     if constexpr (FUSED) {
         if (has_new && wave == 0) {
             const int npairs = fz.n_kv * HALF, nrow = fz.n_kv * D;
@@ -200,40 +210,53 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_partial_kernel(
                     ak = fmaxf(ak, fmaxf(fabsf(nk0[p]), fabsf(nk1[p])));
                 }
             }
+            float sk = 1.f, sv = 1.f, ik = 0.f, iv = 0.f;
+            if constexpr (Q8) {
 #pragma unroll
-            for (int p = 0; p < VP; ++p)
-                if (lane + 64 * p < nrow) av = fmaxf(av, fabsf(nv[p]));
-            ak = wave_max(ak);
-            av = wave_max(av);
-            const float sk = ak != 0.f ? ak / 127.f : 0.f, sv = av != 0.f ? av / 127.f : 0.f;
-            const float ik = ak != 0.f ? 1.f / sk : 0.f, iv = av != 0.f ? 1.f / sv : 0.f;
-            int8_t* krow_w = fz.kq_w + hb + (size_t)pos * D;
-            int8_t* vrow_w = fz.vq_w + hb + (size_t)pos * D;
+                for (int p = 0; p < VP; ++p)
+                    if (lane + 64 * p < nrow) av = fmaxf(av, fabsf(nv[p]));
+                ak = wave_max(ak);
+                av = wave_max(av);
+                sk = ak != 0.f ? ak / 127.f : 0.f;
+                sv = av != 0.f ? av / 127.f : 0.f;
+                ik = ak != 0.f ? 1.f / sk : 0.f;
+                iv = av != 0.f ? 1.f / sv : 0.f;
+            }
+            int8_t* krow_w = fz.kq_w + (hb + (size_t)pos * D) * EB;
+            int8_t* vrow_w = fz.vq_w + (hb + (size_t)pos * D) * EB;
             float* vnew = vsm[pos - c0];
+            // stores element j of a row and returns the value attention reads back
+            auto put = [&](int8_t* row, int j, float x, float sc, float inv, bool nz) -> float {
+                if constexpr (Q8) {
+                    const int c = nz ? min(127, max(-127, (int)roundf(x * inv))) : 0;
+                    row[j] = (int8_t)c;
+                    return (float)c * sc;
+                } else if constexpr (H16) {
+                    const uint16_t h = f32_to_f16_kv(x);
+                    reinterpret_cast<uint16_t*>(row)[j] = h;
+                    return f16_bits_to_f32(h);
+                } else {
+                    reinterpret_cast<float*>(row)[j] = x;
+                    return x;
+                }
+            };
 #pragma unroll
             for (int p = 0; p < KP; ++p) {
                 const int i = lane + 64 * p;
                 if (i < npairs && i / HALF == g) {
                     const int j = i % HALF;
-                    const int a0 = ak != 0.f ? min(127, max(-127, (int)roundf(nk0[p] * ik))) : 0;
-                    const int a1 = ak != 0.f ? min(127, max(-127, (int)roundf(nk1[p] * ik))) : 0;
-                    newk[j] = (float)a0 * sk;
-                    newk[j + HALF] = (float)a1 * sk;
-                    krow_w[j] = (int8_t)a0;
-                    krow_w[j + HALF] = (int8_t)a1;
+                    newk[j] = put(krow_w, j, nk0[p], sk, ik, ak != 0.f);
+                    newk[j + HALF] = put(krow_w, j + HALF, nk1[p], sk, ik, ak != 0.f);
                 }
             }
 #pragma unroll
             for (int p = 0; p < VP; ++p) {
                 const int i = lane + 64 * p;
-                if (i < nrow && i / D == g) {
-                    const int dd = i % D;
-                    const int b = av != 0.f ? min(127, max(-127, (int)roundf(nv[p] * iv))) : 0;
-                    vnew[dd] = (float)b * sv;
-                    vrow_w[dd] = (int8_t)b;
-                }
+                if (i < nrow && i / D == g) vnew[i % D] = put(vrow_w, i % D, nv[p], sv, iv, av != 0.f);
             }
-            if (g == 0 && lane == 0) { fz.ks_w[pos] = sk; fz.vs_w[pos] = sv; }
+            if constexpr (Q8) {
+                if (g == 0 && lane == 0) { fz.ks_w[pos] = sk; fz.vs_w[pos] = sv; }
+            }
         }
     }
     __syncthreads();
@@ -253,13 +276,16 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_partial_kernel(
             if constexpr (Q8) {
 #pragma unroll
                 for (int k = 0; k < 16; ++k) kv[16 * i + k] = (float)(int8_t)(w[k >> 2] >> (8 * (k & 3)));
+            } else if constexpr (H16) {
+#pragma unroll
+                for (int k = 0; k < 8; ++k) kv[8 * i + k] = f16_bits_to_f32((w[k >> 1] >> (16 * (k & 1))) & 0xFFFFu);
             } else {
 #pragma unroll
                 for (int k = 0; k < 4; ++k) kv[4 * i + k] = __uint_as_float(w[k]);
             }
         }
         if constexpr (FUSED) {
-            if (has_new && c0 + lane == pos) {     // the new token: its dequantized row
+            if (has_new && c0 + lane == pos) {     // the new token: its stored row, as read back
 #pragma unroll
                 for (int j = 0; j < D; ++j) kv[j] = newk[j];
                 kscale = 1.f;
@@ -399,11 +425,40 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
 // accumulators, and P re-enters the second product through register shuffles.
 constexpr int kPQ = 32, kPK = 64;         // queries per workgroup, keys per tile
 
-template <int D, int REP>
+// 16 consecutive cache elements of dtype KVT starting at element e0 -> f32
+// (Q8_0 codes times the row scale); zero where !live.
+template <int KVT>
+__device__ __forceinline__ void cache16(const int8_t* base, size_t e0, float scale, bool live, float (&o)[16]) {
+    if constexpr (KVT == VLRF_KV_Q8_0) {
+        const uint4 c = *reinterpret_cast<const uint4*>(base + e0);
+        const uint32_t u[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[e] = (float)(int8_t)(u[e >> 2] >> (8 * (e & 3))) * (live ? scale : 0.f);
+    } else if constexpr (KVT == VLRF_KV_F16) {
+        const uint4 c0 = *reinterpret_cast<const uint4*>(base + 2 * e0);
+        const uint4 c1 = *reinterpret_cast<const uint4*>(base + 2 * e0 + 16);
+        const uint32_t u[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[e] = live ? f16_bits_to_f32((u[e >> 1] >> (16 * (e & 1))) & 0xFFFFu) : 0.f;
+    } else {
+        const float4* f = reinterpret_cast<const float4*>(base + 4 * e0);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float4 v = f[k];
+            o[4 * k] = live ? v.x : 0.f;
+            o[4 * k + 1] = live ? v.y : 0.f;
+            o[4 * k + 2] = live ? v.z : 0.f;
+            o[4 * k + 3] = live ? v.w : 0.f;
+        }
+    }
+}
+
+template <int D, int REP, int KVT>
 __global__ __launch_bounds__(64 * REP) void attn_prefill_kernel(
     const float* __restrict__ qkv, int ld, const int8_t* __restrict__ kq, const int8_t* __restrict__ vq,
     const float* __restrict__ ks, const float* __restrict__ vs, long head_stride, int T, int pos0,
     float scale, int n_heads, uint16_t* __restrict__ out) {
+    constexpr bool Q8 = KVT == VLRF_KV_Q8_0;
     typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
     typedef float f32x16 __attribute__((ext_vector_type(16)));
     constexpr int NT = 64 * REP;
@@ -445,21 +500,20 @@ __global__ __launch_bounds__(64 * REP) void attn_prefill_kernel(
             const int kp = kv0 + key;
             const bool live = kp < kv_end;
             const int kr = live ? kp : 0;
-            const uint4 kc = *reinterpret_cast<const uint4*>(kq + hb + (size_t)kr * D + 16 * part);
-            const uint4 vc = *reinterpret_cast<const uint4*>(vq + hb + (size_t)kr * D + 16 * part);
-            const float sk = live ? ks[kr] : 0.f, sv = live ? vs[kr] : 0.f;   // dequantize_row_q8_0
-            const uint32_t ku[4] = {kc.x, kc.y, kc.z, kc.w}, vu[4] = {vc.x, vc.y, vc.z, vc.w};
+            const size_t e0 = hb + (size_t)kr * D + 16 * part;
+            float kf[16], vf[16];                           // dequantize_row_q8_0 / f16_to_f32
+            cache16<KVT>(kq, e0, Q8 ? ks[kr] : 1.f, live, kf);
+            cache16<KVT>(vq, e0, Q8 ? vs[kr] : 1.f, live, vf);
             bf16x8 k0, k1;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                k0[e] = (__bf16)((float)(int8_t)(ku[e >> 2] >> (8 * (e & 3))) * sk);
-                k1[e] = (__bf16)((float)(int8_t)(ku[2 + (e >> 2)] >> (8 * (e & 3))) * sk);
+                k0[e] = (__bf16)kf[e];
+                k1[e] = (__bf16)kf[8 + e];
             }
             *reinterpret_cast<bf16x8*>(&Ks[key * KS + 16 * part]) = k0;
             *reinterpret_cast<bf16x8*>(&Ks[key * KS + 16 * part + 8]) = k1;
 #pragma unroll
-            for (int e = 0; e < 16; ++e)
-                Vt[(16 * part + e) * VS + key] = (__bf16)((float)(int8_t)(vu[e >> 2] >> (8 * (e & 3))) * sv);
+            for (int e = 0; e < 16; ++e) Vt[(16 * part + e) * VS + key] = (__bf16)vf[e];
         }
         __syncthreads();
 
@@ -630,10 +684,9 @@ __global__ __launch_bounds__(64) void attn_f32_tiled_kernel(const float* __restr
 
 int attn_decode_splits(int max_ctx) { return (max_ctx + kChunk - 1) / kChunk; }
 
-int launch_attn_decode(hipStream_t s, const float* q, const int8_t* kq, const int8_t* vq,
-                       const float* ks, const float* vs, const float* kf, const float* vf,
-                       long head_stride, int n_heads, int n_kv, int d_head, int ctx_len,
-                       const int* ctx_dev, int n_splits, float scale, float* part, float* out,
+int launch_attn_decode(hipStream_t s, const float* q, const void* kc, const void* vc, const float* ks,
+                       const float* vs, int kv_dtype, long head_stride, int n_heads, int n_kv, int d_head,
+                       int ctx_len, const int* ctx_dev, int n_splits, float scale, float* part, float* out,
                        const DecodeFuse* fuse) {
     VH_ARG(n_kv > 0 && n_heads % n_kv == 0, "attn_decode: n_heads %d not a multiple of n_kv %d",
            n_heads, n_kv);
@@ -642,37 +695,45 @@ int launch_attn_decode(hipStream_t s, const float* q, const int8_t* kq, const in
     VH_ARG(rep == 1 || rep == 2 || rep == 4 || rep == 8, "attn_decode: GQA group %d not in {1,2,4,8}", rep);
     VH_ARG(n_splits >= 1 && n_splits <= kMaxSplits, "attn_decode: %d splits outside [1,%d]", n_splits,
            kMaxSplits);
+    VH_ARG(kv_dtype == VLRF_KV_F32 || kv_dtype == VLRF_KV_F16 || kv_dtype == VLRF_KV_Q8_0,
+           "attn_decode: cache dtype %d", kv_dtype);
     if (!ctx_dev)
         VH_ARG(ctx_len >= 1 && ctx_len <= n_splits * kChunk, "attn_decode: ctx_len %d outside [1,%d]",
                ctx_len, n_splits * kChunk);
-    const bool q8 = kq != nullptr;
-    VH_ARG(q8 ? (vq && ks && vs) : (kf && vf), "attn_decode: missing K/V operands");
+    VH_ARG(kc && vc && (kv_dtype != VLRF_KV_Q8_0 || (ks && vs)), "attn_decode: missing K/V operands");
     DecodeFuse fz{};
     if (fuse) {
-        VH_ARG(q8 && ctx_dev, "attn_decode: fusion needs the Q8 cache and a device position");
+        VH_ARG(ctx_dev, "attn_decode: fusion needs a device position");
         VH_ARG(fuse->n_kv == n_kv && n_kv * d_head <= 1024, "attn_decode: bad fusion row");
         fz = *fuse;
     }
+    const int8_t* k8 = static_cast<const int8_t*>(kc);
+    const int8_t* v8 = static_cast<const int8_t*>(vc);
     dim3 grid(n_splits, n_kv), block(kAttnThreads);
-#define VH_AD(D, R, Q, FU)                                                                          \
-    hipLaunchKernelGGL((attn_decode_partial_kernel<D, R, Q, FU>), grid, block, 0, s, q, kq, vq, ks,  \
-                       vs, kf, vf, head_stride, ctx_len, ctx_dev, n_splits, scale, part, fz)
-#define VH_AD_R(D, Q, FU)                       \
+#define VH_AD(D, R, T, FU)                                                                          \
+    hipLaunchKernelGGL((attn_decode_partial_kernel<D, R, T, FU>), grid, block, 0, s, q, k8, v8, ks,  \
+                       vs, head_stride, ctx_len, ctx_dev, n_splits, scale, part, fz)
+#define VH_AD_R(D, T, FU)                       \
     switch (rep) {                              \
-        case 1: VH_AD(D, 1, Q, FU); break;      \
-        case 2: VH_AD(D, 2, Q, FU); break;      \
-        case 4: VH_AD(D, 4, Q, FU); break;      \
-        default: VH_AD(D, 8, Q, FU); break;     \
+        case 1: VH_AD(D, 1, T, FU); break;      \
+        case 2: VH_AD(D, 2, T, FU); break;      \
+        case 4: VH_AD(D, 4, T, FU); break;      \
+        default: VH_AD(D, 8, T, FU); break;     \
+    }
+#define VH_AD_T(D, FU)                                                   \
+    switch (kv_dtype) {                                                  \
+        case VLRF_KV_Q8_0: VH_AD_R(D, VLRF_KV_Q8_0, FU) break;           \
+        case VLRF_KV_F16: VH_AD_R(D, VLRF_KV_F16, FU) break;             \
+        default: VH_AD_R(D, VLRF_KV_F32, FU) break;                      \
     }
     if (d_head == 64) {
-        if (fuse) { VH_AD_R(64, true, true) }
-        else if (q8) { VH_AD_R(64, true, false) }
-        else { VH_AD_R(64, false, false) }
+        if (fuse) { VH_AD_T(64, true) }
+        else { VH_AD_T(64, false) }
     } else {
-        if (fuse) { VH_AD_R(128, true, true) }
-        else if (q8) { VH_AD_R(128, true, false) }
-        else { VH_AD_R(128, false, false) }
+        if (fuse) { VH_AD_T(128, true) }
+        else { VH_AD_T(128, false) }
     }
+#undef VH_AD_T
 #undef VH_AD_R
 #undef VH_AD
     VH_LAUNCHED();
@@ -712,17 +773,24 @@ int launch_attn_prefill(hipStream_t s, const float* qkv, int ld, const KVLayer& 
            pos0, pos0 + T);
     VH_ARG(ld % 4 == 0, "attn_prefill: row stride %d not a multiple of 4", ld);
     dim3 grid((T + kPQ - 1) / kPQ, n_kv);
-#define VH_AP(D, R)                                                                                   \
-    hipLaunchKernelGGL((attn_prefill_kernel<D, R>), grid, dim3(64 * R), 0, s, qkv, ld, L.k, L.v, L.ks, \
+#define VH_AP(D, R, KT)                                                                                   \
+    hipLaunchKernelGGL((attn_prefill_kernel<D, R, KT>), grid, dim3(64 * R), 0, s, qkv, ld, L.k, L.v, L.ks, \
                        L.vs, (long)max_seq * d_head, T, pos0, scale, n_heads, out)
-#define VH_AP_R(D)                      \
-    switch (rep) {                      \
-        case 1: VH_AP(D, 1); break;     \
-        case 2: VH_AP(D, 2); break;     \
-        case 4: VH_AP(D, 4); break;     \
-        default: VH_AP(D, 8); break;    \
+#define VH_AP_R(D, KT)                      \
+    switch (rep) {                          \
+        case 1: VH_AP(D, 1, KT); break;     \
+        case 2: VH_AP(D, 2, KT); break;     \
+        case 4: VH_AP(D, 4, KT); break;     \
+        default: VH_AP(D, 8, KT); break;    \
     }
-    if (d_head == 64) { VH_AP_R(64) } else { VH_AP_R(128) }
+#define VH_AP_T(D)                                                  \
+    switch (L.dtype) {                                              \
+        case VLRF_KV_Q8_0: VH_AP_R(D, VLRF_KV_Q8_0) break;          \
+        case VLRF_KV_F16: VH_AP_R(D, VLRF_KV_F16) break;            \
+        default: VH_AP_R(D, VLRF_KV_F32) break;                     \
+    }
+    if (d_head == 64) { VH_AP_T(64) } else { VH_AP_T(128) }
+#undef VH_AP_T
 #undef VH_AP_R
 #undef VH_AP
     VH_LAUNCHED();

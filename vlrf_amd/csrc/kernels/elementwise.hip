@@ -1,5 +1,6 @@
-// elementwise.hip - edge ops of the decode step: RMSNorm, RoPE, the Q8_0 KV
-// append (quantize) and dequant, embedding gather and greedy argmax.
+// elementwise.hip - edge ops of the decode step: RMSNorm, RoPE, the KV append
+// (Q8_0 quantize, F16 convert, F32 copy) and dequant, embedding gather and
+// greedy argmax.
 #include "../internal.hpp"
 
 #include <cmath>
@@ -72,7 +73,23 @@ __device__ void quantize_row_to_cache(const float* __restrict__ src, int8_t* __r
     }
 }
 
-__global__ __launch_bounds__(256) void kv_append_kernel(int8_t* kq, int8_t* vq, float* ks, float* vs,
+// KVCache::append of one row (kv_cache.hpp:215-251) for any cache dtype:
+// Q8_0 quantize_row_q8_0, F16 the reference's f32_to_f16 per element, F32 copy.
+__device__ void store_row_to_cache(const float* __restrict__ src, int8_t* dst, float* sc, int dtype,
+                                   int p, int n_kv, int D, int max_seq, float* red) {
+    if (dtype == VLRF_KV_Q8_0) {
+        quantize_row_to_cache(src, dst, sc, p, n_kv, D, max_seq, red);
+        return;
+    }
+    for (int i = threadIdx.x; i < n_kv * D; i += 256) {
+        const int h = i / D, d = i - h * D;
+        const size_t o = ((size_t)h * max_seq + p) * D + d;
+        if (dtype == VLRF_KV_F16) reinterpret_cast<uint16_t*>(dst)[o] = f32_to_f16_kv(src[i]);
+        else reinterpret_cast<float*>(dst)[o] = src[i];
+    }
+}
+
+__global__ __launch_bounds__(256) void kv_append_kernel(int8_t* kq, int8_t* vq, float* ks, float* vs, int dtype,
                                                         const float* __restrict__ k,
                                                         const float* __restrict__ v, int n_kv, int D,
                                                         int max_seq, int pos, const int* pos_dev) {
@@ -81,14 +98,14 @@ __global__ __launch_bounds__(256) void kv_append_kernel(int8_t* kq, int8_t* vq, 
     const int p = (pos_dev ? *pos_dev : pos) + t;
     if (p < 0 || p >= max_seq) return;   // host checks capacity; never write past the cache
     const size_t row = (size_t)n_kv * D;
-    quantize_row_to_cache(k + t * row, kq, ks, p, n_kv, D, max_seq, red);
-    quantize_row_to_cache(v + t * row, vq, vs, p, n_kv, D, max_seq, red);
+    store_row_to_cache(k + t * row, kq, ks, dtype, p, n_kv, D, max_seq, red);
+    store_row_to_cache(v + t * row, vq, vs, dtype, p, n_kv, D, max_seq, red);
 }
 
 // Decode fusion: rotate q (n_heads) in place and k (n_kv) at position *pos_dev,
-// then quantize k and v into the cache (attention.hpp:109-128 order).
+// then append k and v to the cache (attention.hpp:109-128 order).
 __global__ __launch_bounds__(256) void rope_append_kernel(int8_t* kq, int8_t* vq, float* ks,
-                                                          float* vs, float* q, const float* __restrict__ k,
+                                                          float* vs, int dtype, float* q, const float* __restrict__ k,
                                                           const float* __restrict__ v, int n_heads,
                                                           int n_kv, int D, int max_seq,
                                                           const int* __restrict__ pos_dev,
@@ -113,15 +130,15 @@ __global__ __launch_bounds__(256) void rope_append_kernel(int8_t* kq, int8_t* vq
         rope_pair(kr + h * D, j, half, c[j], s[j]);
     }
     __syncthreads();
-    quantize_row_to_cache(kr, kq, ks, p, n_kv, D, max_seq, red);
-    quantize_row_to_cache(v, vq, vs, p, n_kv, D, max_seq, red);
+    store_row_to_cache(kr, kq, ks, dtype, p, n_kv, D, max_seq, red);
+    store_row_to_cache(v, vq, vs, dtype, p, n_kv, D, max_seq, red);
 }
 
 // Prefill: token t of a [T][ld] QKV buffer (q: n_heads*D at column 0, k and v:
 // n_kv*D each after it) at position pos0 + t: q rotated in place, k rotated,
-// then the K and V rows quantized into the cache (attention.hpp:109-128 order).
+// then the K and V rows appended to the cache (attention.hpp:109-128 order).
 __global__ __launch_bounds__(256) void prefill_rope_append_kernel(
-    int8_t* kq, int8_t* vq, float* ks, float* vs, float* qkv, int ld, int n_heads, int n_kv, int D,
+    int8_t* kq, int8_t* vq, float* ks, float* vs, int dtype, float* qkv, int ld, int n_heads, int n_kv, int D,
     int max_seq, int pos0, const float* __restrict__ cos_t, const float* __restrict__ sin_t) {
     __shared__ float red[4];
     __shared__ float kr[1024];
@@ -144,8 +161,8 @@ __global__ __launch_bounds__(256) void prefill_rope_append_kernel(
         rope_pair(kr + h * D, j, half, c[j], s[j]);
     }
     __syncthreads();
-    quantize_row_to_cache(kr, kq, ks, p, n_kv, D, max_seq, red);
-    quantize_row_to_cache(v, vq, vs, p, n_kv, D, max_seq, red);
+    store_row_to_cache(kr, kq, ks, dtype, p, n_kv, D, max_seq, red);
+    store_row_to_cache(v, vq, vs, dtype, p, n_kv, D, max_seq, red);
 }
 
 // x[t] = table[ids[t]] (ops.hpp:615-626), one workgroup per token.
@@ -158,18 +175,30 @@ __global__ __launch_bounds__(256) void embed_rows_kernel(const float* __restrict
     for (int i = threadIdx.x; i < D / 4; i += 256) dst[i] = src[i];
 }
 
+// KVCache::dequant_into (kv_cache.hpp:259-286) for any cache dtype.
 __global__ __launch_bounds__(256) void kv_dequant_kernel(const int8_t* __restrict__ kq,
                                                          const int8_t* __restrict__ vq,
                                                          const float* __restrict__ ks,
-                                                         const float* __restrict__ vs, int n_kv, int D,
-                                                         int max_seq, float* K_out, float* V_out) {
+                                                         const float* __restrict__ vs, int dtype, int n_kv,
+                                                         int D, int max_seq, float* K_out, float* V_out) {
     const int t = blockIdx.x;
     const int row = n_kv * D;
     for (int i = threadIdx.x; i < row; i += 256) {
         const int h = i / D, d = i - h * D;
         const size_t src = ((size_t)h * max_seq + t) * D + d;
-        K_out[(size_t)t * row + i] = (float)kq[src] * ks[t];
-        V_out[(size_t)t * row + i] = (float)vq[src] * vs[t];
+        float kv, vv;
+        if (dtype == VLRF_KV_Q8_0) {
+            kv = (float)kq[src] * ks[t];
+            vv = (float)vq[src] * vs[t];
+        } else if (dtype == VLRF_KV_F16) {
+            kv = f16_bits_to_f32(reinterpret_cast<const uint16_t*>(kq)[src]);
+            vv = f16_bits_to_f32(reinterpret_cast<const uint16_t*>(vq)[src]);
+        } else {
+            kv = reinterpret_cast<const float*>(kq)[src];
+            vv = reinterpret_cast<const float*>(vq)[src];
+        }
+        K_out[(size_t)t * row + i] = kv;
+        V_out[(size_t)t * row + i] = vv;
     }
 }
 
@@ -272,7 +301,7 @@ int launch_kv_append(hipStream_t s, const KVLayer& L, int n_kv, int d_head, int 
     VH_ARG(T >= 1 && n_kv >= 1 && d_head >= 1, "kv_append: empty shape");
     if (!pos_dev) VH_ARG(pos >= 0 && pos + T <= max_seq, "kv_append: rows [%d,%d) beyond max_seq %d",
                          pos, pos + T, max_seq);
-    hipLaunchKernelGGL(kv_append_kernel, dim3(T), dim3(256), 0, s, L.k, L.v, L.ks, L.vs, k, v, n_kv,
+    hipLaunchKernelGGL(kv_append_kernel, dim3(T), dim3(256), 0, s, L.k, L.v, L.ks, L.vs, L.dtype, k, v, n_kv,
                        d_head, max_seq, pos, pos_dev);
     VH_LAUNCHED();
     return VLRF_HIP_OK;
@@ -283,7 +312,7 @@ int launch_rope_append(hipStream_t s, const KVLayer& L, float* q, const float* k
                        const float* cos_t, const float* sin_t) {
     VH_ARG(n_kv * d_head <= 1024, "rope_append: kv row %d exceeds 1024", n_kv * d_head);
     VH_ARG(d_head % 2 == 0, "rope_append: odd d_head");
-    hipLaunchKernelGGL(rope_append_kernel, dim3(1), dim3(256), 0, s, L.k, L.v, L.ks, L.vs, q, k, v,
+    hipLaunchKernelGGL(rope_append_kernel, dim3(1), dim3(256), 0, s, L.k, L.v, L.ks, L.vs, L.dtype, q, k, v,
                        n_heads, n_kv, d_head, max_seq, pos_dev, cos_t, sin_t);
     VH_LAUNCHED();
     return VLRF_HIP_OK;
@@ -296,7 +325,7 @@ int launch_prefill_rope_append(hipStream_t s, const KVLayer& L, float* qkv, int 
     VH_ARG(d_head % 2 == 0 && T >= 1, "prefill_rope_append: bad shape");
     VH_ARG(pos0 >= 0 && pos0 + T <= max_seq, "prefill_rope_append: positions [%d,%d) outside the cache",
            pos0, pos0 + T);
-    hipLaunchKernelGGL(prefill_rope_append_kernel, dim3(T), dim3(256), 0, s, L.k, L.v, L.ks, L.vs, qkv, ld,
+    hipLaunchKernelGGL(prefill_rope_append_kernel, dim3(T), dim3(256), 0, s, L.k, L.v, L.ks, L.vs, L.dtype, qkv, ld,
                        n_heads, n_kv, d_head, max_seq, pos0, cos_t, sin_t);
     VH_LAUNCHED();
     return VLRF_HIP_OK;
@@ -313,7 +342,7 @@ int launch_kv_dequant(hipStream_t s, const KVLayer& L, int n_kv, int d_head, int
                       int ctx_len, float* K_out, float* V_out) {
     VH_ARG(ctx_len >= 0 && ctx_len <= max_seq, "kv_dequant: ctx_len %d outside [0,%d]", ctx_len, max_seq);
     if (ctx_len == 0) return VLRF_HIP_OK;
-    hipLaunchKernelGGL(kv_dequant_kernel, dim3(ctx_len), dim3(256), 0, s, L.k, L.v, L.ks, L.vs, n_kv,
+    hipLaunchKernelGGL(kv_dequant_kernel, dim3(ctx_len), dim3(256), 0, s, L.k, L.v, L.ks, L.vs, L.dtype, n_kv,
                        d_head, max_seq, K_out, V_out);
     VH_LAUNCHED();
     return VLRF_HIP_OK;

@@ -113,7 +113,7 @@ int enqueue_step(vlrf_hip_model* m, hipStream_t s) {
         fz.vs_w = Ly.kv.vs;
         fz.n_kv = m->G;
         fz.max_seq = m->S;
-        if (!rc) rc = launch_attn_decode(s, q, Ly.kv.k, Ly.kv.v, Ly.kv.ks, Ly.kv.vs, nullptr, nullptr,
+        if (!rc) rc = launch_attn_decode(s, q, Ly.kv.k, Ly.kv.v, Ly.kv.ks, Ly.kv.vs, Ly.kv.dtype,
                                          (long)m->S * m->dh, m->H, m->G, m->dh, 1, m->state + 1,
                                          m->n_splits, scale, m->part, m->att, &fz);
         if (!rc) rc = launch_qlinear(s, Ly.wo, m->att, m->x, 1, nullptr, 0.f, m->x);
@@ -196,6 +196,8 @@ int vlrf_hip_model_create(vlrf_hip_ctx_t ctx, const vlrf_hip_model_config* cfg, 
     VH_ARG(c.d_model % 32 == 0 && c.d_ff % 32 == 0, "model: d_model and d_ff must be multiples of 32");
     VH_ARG(c.weight_dtype == VLRF_DT_Q8_0 || c.weight_dtype == VLRF_DT_Q4_0 || c.weight_dtype == VLRF_DT_F32,
            "model: unsupported weight dtype %d", c.weight_dtype);
+    VH_ARG(c.kv_dtype == VLRF_KV_F32 || c.kv_dtype == VLRF_KV_F16 || c.kv_dtype == VLRF_KV_Q8_0,
+           "model: unsupported KV cache dtype %d", c.kv_dtype);
 
     auto* m = new (std::nothrow) vlrf_hip_model();
     if (!m) return VLRF_HIP_ERR_NOMEM;
@@ -226,14 +228,17 @@ int vlrf_hip_model_create(vlrf_hip_ctx_t ctx, const vlrf_hip_model_config* cfg, 
     dalloc((void**)&m->state, 4 * sizeof(int));
     dalloc((void**)&m->gen_ids, (size_t)m->S * sizeof(int));
     dalloc((void**)&m->prompt, (size_t)m->S * sizeof(int));
-    const size_t kvdata = (size_t)m->G * m->S * dh;
+    const size_t kvdata = (size_t)m->G * m->S * dh * kv_elem_bytes(c.kv_dtype);
     for (auto& Ly : m->layers) {
         dalloc((void**)&Ly.ln1, (size_t)m->D * 4);
         dalloc((void**)&Ly.ln2, (size_t)m->D * 4);
+        Ly.kv.dtype = c.kv_dtype;
         dalloc((void**)&Ly.kv.k, kvdata);
         dalloc((void**)&Ly.kv.v, kvdata);
-        dalloc((void**)&Ly.kv.ks, (size_t)m->S * 4);
-        dalloc((void**)&Ly.kv.vs, (size_t)m->S * 4);
+        if (c.kv_dtype == VLRF_KV_Q8_0) {
+            dalloc((void**)&Ly.kv.ks, (size_t)m->S * 4);
+            dalloc((void**)&Ly.kv.vs, (size_t)m->S * 4);
+        }
         if (!rc) rc = weight_alloc(Ly.wqkv, c.weight_dtype, m->D + 2 * m->dkv, m->D);
         if (!rc) rc = weight_alloc(Ly.wo, c.weight_dtype, m->D, m->D);
         if (!rc) rc = weight_alloc(Ly.wg, c.weight_dtype, m->F, m->D);
@@ -361,12 +366,12 @@ int vlrf_hip_model_reset(vlrf_hip_model_t m) {
     VH_ARG(m != nullptr, "model_reset: null handle");
     VH_CHECK(hipSetDevice(m->ctx->device));
     hipStream_t s = m->ctx->stream;
-    const size_t kvdata = (size_t)m->G * m->S * m->dh;
+    const size_t kvdata = (size_t)m->G * m->S * m->dh * kv_elem_bytes(m->cfg.kv_dtype);
     for (auto& Ly : m->layers) {
         VH_CHECK(hipMemsetAsync(Ly.kv.k, 0, kvdata, s));
         VH_CHECK(hipMemsetAsync(Ly.kv.v, 0, kvdata, s));
-        VH_CHECK(hipMemsetAsync(Ly.kv.ks, 0, (size_t)m->S * 4, s));
-        VH_CHECK(hipMemsetAsync(Ly.kv.vs, 0, (size_t)m->S * 4, s));
+        if (Ly.kv.ks) VH_CHECK(hipMemsetAsync(Ly.kv.ks, 0, (size_t)m->S * 4, s));
+        if (Ly.kv.vs) VH_CHECK(hipMemsetAsync(Ly.kv.vs, 0, (size_t)m->S * 4, s));
     }
     VH_CHECK(hipMemsetAsync(m->state, 0, 4 * sizeof(int), s));
     VH_CHECK(hipStreamSynchronize(s));
@@ -591,8 +596,10 @@ int vlrf_hip_model_step_bytes(vlrf_hip_model_t m, int ctx_len, double out[3]) {
         for (const DevWeight* dw : {&Ly.wqkv, &Ly.wo, &Ly.wg, &Ly.wu, &Ly.wd})
             w += (double)weight_device_bytes(dw->dtype, dw->N, dw->K);
     w += (double)weight_device_bytes(m->lm_head.dtype, m->V, m->D);
-    // K and V codes of the context plus one f32 scale per row, per layer.
-    const double kv = (double)m->L * (2.0 * ctx_len * m->dkv + 2.0 * ctx_len * 4.0);
+    // K and V elements of the context (plus one f32 scale per row for Q8_0), per layer.
+    const bool q8 = m->cfg.kv_dtype == VLRF_KV_Q8_0;
+    const double kv = (double)m->L * (2.0 * ctx_len * m->dkv * kv_elem_bytes(m->cfg.kv_dtype) +
+                                      (q8 ? 2.0 * ctx_len * 4.0 : 0.0));
     // Norm weights (2 per layer + final) and the embedding row.
     const double other = (2.0 * m->L + 1.0) * m->D * 4.0 + m->D * 4.0;
     out[0] = w;

@@ -29,7 +29,9 @@ public:
         if (!c.use_rms_norm || c.activation != Activation::SILU ||
             c.pos_embedding != PosEmbedding::ROTARY || !c.pre_norm || c.embedding_multiplier != 1.f ||
             c.attention_multiplier != 0.f || c.residual_multiplier != 1.f || c.logits_scaling != 1.f ||
-            c.kv_cache_dtype != static_cast<int>(KVCacheDType::Q8_0))
+            (c.kv_cache_dtype != static_cast<int>(KVCacheDType::F32) &&
+             c.kv_cache_dtype != static_cast<int>(KVCacheDType::F16) &&
+             c.kv_cache_dtype != static_cast<int>(KVCacheDType::Q8_0)))
             throw std::runtime_error("HipDecoder: unsupported model family");
         for (int l = 0; l < c.n_layers; ++l) {
             const std::string p = "layers." + std::to_string(l) + ".";
@@ -50,6 +52,7 @@ public:
         mc.norm_eps = c.layer_norm_eps;
         mc.rope_theta = c.rope_theta;
         mc.weight_dtype = weight_dtype;
+        mc.kv_dtype = c.kv_cache_dtype;          // KVCacheDType values are the ABI's VLRF_KV_*
         check(vlrf_hip_model_create(ctx_, &mc, &m_));
         auto put_f32 = [&](const std::string& name, const std::string& key) {
             Tensor& t = wm.get(key);

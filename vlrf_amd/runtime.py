@@ -7,7 +7,7 @@ import ctypes as C
 
 import numpy as np
 
-from ._lib import lib, check, ModelConfig, DT_F32, KV_Q8_0
+from ._lib import lib, check, ModelConfig, DT_F32, KV_F16, KV_F32, KV_Q8_0
 
 
 class DeviceBuffer:
@@ -156,6 +156,7 @@ class KVCache:
         self.n_layers, self.max_seq_len, self.n_kv_heads, self.d_head = (n_layers, max_seq_len,
                                                                          n_kv_heads, d_head)
         self.row_dim = n_kv_heads * d_head
+        self.dtype = dtype
         h = C.c_void_p()
         check(lib().vlrf_hip_kv_create(ctx.h, n_layers, max_seq_len, n_kv_heads, d_head, dtype,
                                        C.byref(h)))
@@ -171,14 +172,17 @@ class KVCache:
         check(lib().vlrf_hip_kv_append(self.h, layer, k.ptr, v.ptr, T))
 
     def read(self, layer, row0, n):
-        """(K int8 [n,row], V int8 [n,row], K scales [n], V scales [n]) in the
-        reference's token-major layout."""
-        kq = np.zeros((n, self.row_dim), np.int8)
-        vq = np.zeros((n, self.row_dim), np.int8)
-        ks = np.zeros(n, np.float32)
-        vs = np.zeros(n, np.float32)
+        """(K [n,row], V [n,row], K scales [n], V scales [n]) in the reference's
+        token-major layout: int8 codes with f32 scales (Q8_0), or uint16 f16
+        bits / float32 elements with the scales None."""
+        et = {KV_F32: np.float32, KV_F16: np.uint16}.get(self.dtype, np.int8)
+        kq = np.zeros((n, self.row_dim), et)
+        vq = np.zeros((n, self.row_dim), et)
+        q8 = self.dtype == KV_Q8_0
+        ks = np.zeros(n, np.float32) if q8 else None
+        vs = np.zeros(n, np.float32) if q8 else None
         check(lib().vlrf_hip_kv_read(self.h, layer, row0, n, kq.ctypes.data, vq.ctypes.data,
-                                     ks.ctypes.data, vs.ctypes.data))
+                                     ks.ctypes.data if q8 else None, vs.ctypes.data if q8 else None))
         return kq, vq, ks, vs
 
     def dequant_into(self, layer, ctx_len, K_out, V_out):
@@ -205,7 +209,7 @@ class Model:
         self.cfg = dict(cfg)
         c = ModelConfig(cfg["vocab_size"], cfg["d_model"], cfg["d_ff"], cfg["n_heads"],
                         cfg["n_kv_heads"], cfg["n_layers"], cfg["max_seq_len"], cfg["norm_eps"],
-                        cfg["rope_theta"], cfg["weight_dtype"])
+                        cfg["rope_theta"], cfg["weight_dtype"], cfg.get("kv_dtype", KV_Q8_0))
         h = C.c_void_p()
         check(lib().vlrf_hip_model_create(ctx.h, C.byref(c), C.byref(h)))
         self.h = h.value
@@ -258,13 +262,18 @@ class Model:
         return out
 
     def kv_rows(self, layer, row0, n):
-        """(K int8 [n,row], V int8, K scales [n], V scales) of the model's cache."""
+        """(K [n,row], V, K scales [n], V scales) of the model's cache: int8 codes
+        and f32 scales (Q8_0), or uint16 f16 bits / float32 with scales None."""
         c = self.cfg
         row = c["n_kv_heads"] * (c["d_model"] // c["n_heads"])
-        kq, vq = np.zeros((n, row), np.int8), np.zeros((n, row), np.int8)
-        ks, vs = np.zeros(n, np.float32), np.zeros(n, np.float32)
+        dt = c.get("kv_dtype", KV_Q8_0)
+        et = {KV_F32: np.float32, KV_F16: np.uint16}.get(dt, np.int8)
+        kq, vq = np.zeros((n, row), et), np.zeros((n, row), et)
+        q8 = dt == KV_Q8_0
+        ks = np.zeros(n, np.float32) if q8 else None
+        vs = np.zeros(n, np.float32) if q8 else None
         check(lib().vlrf_hip_model_kv_read(self.h, layer, row0, n, kq.ctypes.data, vq.ctypes.data,
-                                           ks.ctypes.data, vs.ctypes.data))
+                                           ks.ctypes.data if q8 else None, vs.ctypes.data if q8 else None))
         return kq, vq, ks, vs
 
     def generate_ids(self, first, n_steps):
