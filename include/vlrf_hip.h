@@ -171,6 +171,30 @@ int vlrf_hip_rope(vlrf_hip_ctx_t ctx, float* x, int T, int n_heads, int d_head,
                   int pos_offset, int max_seq, float theta);
 
 /* ============================================================================
+ * The engine's remaining per-op backend calls (IBackend, ibackend.hpp:61-70),
+ * on device f32 buffers, for GPT-2-family models.  Asynchronous on the
+ * context's stream.
+ * ========================================================================== */
+/* Replaces: IBackend::gemm -> ops::gemm (ops.hpp:170-310): C[M,N] =
+ * beta*C + alpha*op(A).op(B), op(A) [M,K] = transA ? A^T : A (A row-major with
+ * leading dimension lda), op(B) [K,N] likewise; beta == 0 writes C without
+ * reading it.  f32 FMA accumulation. */
+int vlrf_hip_gemm_f32(vlrf_hip_ctx_t ctx, const float* A, const float* B, float* C, int M, int N, int K,
+                      int lda, int ldb, int ldc, float alpha, float beta, int transA, int transB);
+/* Replaces: IBackend::layer_norm -> ops::layer_norm (ops.hpp:443-476) over rows
+ * of D: (x - mean) * (1/sqrt(var + eps)) * w + b. */
+int vlrf_hip_layer_norm(vlrf_hip_ctx_t ctx, const float* x, const float* w, const float* b, float* out,
+                        int rows, int D, float eps);
+/* Replaces: IBackend::softmax_inplace -> ops::softmax_inplace (ops.hpp:501-540)
+ * over rows of D: exp(x - max) * (1/(sum + 1e-9)). */
+int vlrf_hip_softmax(vlrf_hip_ctx_t ctx, float* x, int rows, int D);
+/* Replaces: IBackend::gelu_inplace -> ops::gelu_inplace (ops.hpp:390-404), the
+ * tanh approximation. */
+int vlrf_hip_gelu(vlrf_hip_ctx_t ctx, float* x, int64_t n);
+/* Replaces: IBackend::add_inplace -> ops::add_inplace (ops.hpp:344-356). */
+int vlrf_hip_add(vlrf_hip_ctx_t ctx, float* dst, const float* src, int64_t n);
+
+/* ============================================================================
  * Host-side format helpers (no device needed)
  * ========================================================================== */
 /* This build's block encoders (the reference ships decoders only):

@@ -67,6 +67,10 @@ def lib():
     L.orc_f32_to_f16_kv.argtypes = [C.c_float]
     L.orc_f32_to_f16_kv.restype = C.c_uint16
     L.orc_model_kv_raw.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p]
+    L.orc_layer_norm.argtypes = [f32p, f32p, f32p, f32p, C.c_int, C.c_int, C.c_float]
+    L.orc_softmax.argtypes = [f32p, C.c_int, C.c_int]
+    L.orc_gelu.argtypes = [f32p, C.c_int64]
+    L.orc_gemm.argtypes = [f32p, f32p, f32p] + [C.c_int] * 6 + [C.c_float, C.c_float, C.c_int, C.c_int]
     L.orc_model_create.argtypes = [C.POINTER(OrcConfig)]
     L.orc_model_create.restype = C.c_void_p
     L.orc_model_destroy.argtypes = [C.c_void_p]
@@ -110,6 +114,11 @@ def ref():
     R.ref_model_kv_raw.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p]
     R.ref_f32_to_f16.argtypes = [C.c_float]
     R.ref_f32_to_f16.restype = C.c_uint16
+    R.ref_layer_norm.argtypes = [f32p, f32p, f32p, f32p, C.c_int, C.c_int, C.c_float]
+    R.ref_softmax.argtypes = [f32p, C.c_int, C.c_int]
+    R.ref_gelu.argtypes = [f32p, C.c_int64]
+    R.ref_gemm.argtypes = [f32p, C.c_int, C.c_int, f32p, C.c_int, C.c_int, f32p, C.c_int, C.c_int,
+                           C.c_float, C.c_float, C.c_int, C.c_int]
     R.ref_model_set_tensor.argtypes = [C.c_void_p, C.c_char_p, f32p, C.c_int, C.c_int]
     R.ref_model_bind.argtypes = [C.c_void_p]
     R.ref_model_reset.argtypes = [C.c_void_p]
@@ -207,6 +216,39 @@ def dequant_q4_0(blocks, numel):
     out = np.zeros(numel, np.float32)
     lib().orc_dequant_q4_0(np.ascontiguousarray(blocks, np.uint8), out, numel)
     return out
+
+
+def layer_norm(x, w, b, eps):
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.zeros_like(x)
+    rows, D = x.shape
+    lib().orc_layer_norm(x, np.ascontiguousarray(w, np.float32), np.ascontiguousarray(b, np.float32), out, rows,
+                         D, float(eps))
+    return out
+
+
+def softmax(x):
+    y = np.ascontiguousarray(x, np.float32).copy()
+    lib().orc_softmax(y, y.shape[0], y.shape[1])
+    return y
+
+
+def gelu(x):
+    y = np.ascontiguousarray(x, np.float32).copy()
+    lib().orc_gelu(y.ravel(), y.size)
+    return y
+
+
+def gemm(A, B, C, alpha, beta, trans_a, trans_b):
+    """ops::gemm semantics on stored A [rA, cA], B [rB, cB]; returns the new C."""
+    A = np.ascontiguousarray(A, np.float32)
+    B = np.ascontiguousarray(B, np.float32)
+    C = np.ascontiguousarray(C, np.float32).copy()
+    M, K = (A.shape[1], A.shape[0]) if trans_a else A.shape
+    N = B.shape[0] if trans_b else B.shape[1]
+    lib().orc_gemm(A, B, C, M, N, K, A.shape[1], B.shape[1], N, float(alpha), float(beta), int(trans_a),
+                   int(trans_b))
+    return C
 
 
 def f32_to_f16_kv(x):

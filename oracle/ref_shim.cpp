@@ -65,6 +65,31 @@ void ref_silu_mul(float* h, float* g, int64_t n) {
 
 int ref_hw_threads(void) { return vlrf::ops::hw_threads(); }
 
+// ops.hpp:443-476
+void ref_layer_norm(const float* x, const float* w, const float* b, float* out, int rows, int D, float eps) {
+    Tensor X = wrap(x, {rows, D}), W = wrap(w, {D}), Bb = wrap(b, {D}), O = wrap(out, {rows, D});
+    vlrf::ops::layer_norm(X, W, Bb, O, eps);
+}
+
+// ops.hpp:501-540
+void ref_softmax(float* x, int rows, int D) {
+    Tensor X = wrap(x, {rows, D});
+    vlrf::ops::softmax_inplace(X);
+}
+
+// ops.hpp:390-404
+void ref_gelu(float* x, int64_t n) {
+    Tensor X = wrap(x, {(int32_t)n});
+    vlrf::ops::gelu_inplace(X);
+}
+
+// ops.hpp:170-310 with the operands' stored shapes: A [rA, cA], B [rB, cB].
+void ref_gemm(const float* A, int rA, int cA, const float* B, int rB, int cB, float* C, int M, int N,
+              float alpha, float beta, int transA, int transB) {
+    Tensor At = wrap(A, {rA, cA}), Bt = wrap(B, {rB, cB}), Ct = wrap(C, {M, N});
+    vlrf::ops::gemm(At, Bt, Ct, alpha, beta, transA != 0, transB != 0);
+}
+
 // ---- whole model: TransformerModel (transformer.hpp) -------------------------
 struct RefModel {
     vlrf::TransformerModel m;

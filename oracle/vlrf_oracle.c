@@ -380,6 +380,74 @@ void orc_linear(const float* x, const float* W, float* y, int M, int K, int N, i
 }
 
 /* ------------------------------------------------------------------------ */
+/* The engine's remaining per-op backend calls (ops.hpp), sequential order.   */
+/* ------------------------------------------------------------------------ */
+/* ops::layer_norm ops.hpp:443-476, per row. */
+void orc_layer_norm(const float* x, const float* w, const float* b, float* out, int rows, int D, float eps)
+{
+    for (int r = 0; r < rows; ++r) {
+        const float* row = x + (size_t)r * D;
+        float* dst = out + (size_t)r * D;
+        float mean = 0.f;
+        for (int j = 0; j < D; ++j) mean += row[j];
+        mean /= D;
+        float var = 0.f;
+        for (int j = 0; j < D; ++j) {
+            float diff = row[j] - mean;
+            var += diff * diff;
+        }
+        var = var / D + eps;
+        float inv_std = 1.f / sqrtf(var);
+        for (int j = 0; j < D; ++j) dst[j] = (row[j] - mean) * inv_std * w[j] + b[j];
+    }
+}
+
+/* ops::softmax_inplace ops.hpp:501-520 (the serial branch, D < 4096). */
+void orc_softmax(float* x, int rows, int D)
+{
+    for (int r = 0; r < rows; ++r) {
+        float* row = x + (size_t)r * D;
+        float mx = row[0];
+        for (int j = 1; j < D; ++j)
+            if (mx < row[j]) mx = row[j];        /* std::max_element: first maximum */
+        float sum = 0.f;
+        for (int j = 0; j < D; ++j) { row[j] = expf(row[j] - mx); sum += row[j]; }
+        float inv = 1.f / (sum + 1e-9f);
+        for (int j = 0; j < D; ++j) row[j] *= inv;
+    }
+}
+
+/* ops::gelu_inplace ops.hpp:390-404. */
+void orc_gelu(float* x, int64_t n)
+{
+    const float c1 = 0.7978845608028654f, c2 = 0.044715f;
+    for (int64_t i = 0; i < n; ++i) {
+        float v = x[i];
+        float inner = c1 * (v + c2 * v * v * v);
+        x[i] = 0.5f * v * (1.f + tanhf(inner));
+    }
+}
+
+/* ops::gemm semantics ops.hpp:170-191: C = beta*C (0 when beta == 0) then
+ * + alpha*op(A)*op(B); a plain f32 triple loop, k ascending. */
+void orc_gemm(const float* A, const float* B, float* C, int M, int N, int K, int lda, int ldb, int ldc,
+              float alpha, float beta, int transA, int transB)
+{
+    for (int m = 0; m < M; ++m)
+        for (int n = 0; n < N; ++n) {
+            float acc = 0.f;
+            for (int k = 0; k < K; ++k) {
+                float a = transA ? A[(size_t)k * lda + m] : A[(size_t)m * lda + k];
+                float b = transB ? B[(size_t)n * ldb + k] : B[(size_t)k * ldb + n];
+                acc += a * b;
+            }
+            float* c = C + (size_t)m * ldc + n;
+            float prev = beta == 0.f ? 0.f : (beta == 1.f ? *c : *c * beta);
+            *c = prev + alpha * acc;
+        }
+}
+
+/* ------------------------------------------------------------------------ */
 /* GGUF block decode: reference tools/converter/convert_gguf.py:233-263        */
 /* ------------------------------------------------------------------------ */
 float orc_f16_to_f32(uint16_t h)

@@ -49,6 +49,13 @@ void orc_linear(const float* x, const float* W, float* y, int M, int K, int N, i
 void orc_dequant_q8_0(const uint8_t* blocks, float* out, int64_t numel);
 void orc_dequant_q4_0(const uint8_t* blocks, float* out, int64_t numel);
 float orc_f16_to_f32(uint16_t h);
+/* The engine's remaining per-op backend calls (ops.hpp:170-191, 390-404,
+ * 443-476, 501-520). */
+void orc_layer_norm(const float* x, const float* w, const float* b, float* out, int rows, int D, float eps);
+void orc_softmax(float* x, int rows, int D);
+void orc_gelu(float* x, int64_t n);
+void orc_gemm(const float* A, const float* B, float* C, int M, int N, int K, int lda, int ldb, int ldc,
+              float alpha, float beta, int transA, int transB);
 /* KVCache F16 element conversion (kv_cache.hpp:68-97). */
 uint16_t orc_f32_to_f16_kv(float f);
 

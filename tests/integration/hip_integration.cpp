@@ -10,6 +10,9 @@
 //              the causal rule key > query + (ctx - T) (attention.hpp:232,253-261),
 //              including T != ctx, where the reference's default is wrong;
 //   gemm       HipBackend::gemm (x . W^T) vs the reference CpuBackend::gemm;
+//   ops        HipBackend::gemm (all transposes, alpha/beta), layer_norm,
+//              softmax_inplace, gelu_inplace, add_inplace at sizes that run on
+//              the device vs CpuBackend;
 //   decode     HipDecoder::generate vs TransformerModel::generate, greedy,
 //              on a tiny Llama-style model with Q8_0 weights, for each KV
 //              cache dtype (F32, the engine's default, F16 and Q8_0): the
@@ -135,6 +138,62 @@ void check_gemm(HipBackend const& be) {
     report(worst <= 1e-3, "gemm with a fresh weight tensor per call", worst);
 }
 
+void check_ops(HipBackend const& be) {
+    CpuBackend cpu;
+    uint64_t stream = 500;
+    const int M = 160, K = 256, N = 192;   // 7.9M multiply-adds: the device path
+    for (int ta = 0; ta < 2; ++ta)
+        for (int tb = 0; tb < 2; ++tb)
+            for (float beta : {0.f, 0.5f}) {
+                Tensor A = ta ? normal_tensor({K, M}, stream++, 1.f) : normal_tensor({M, K}, stream++, 1.f);
+                Tensor B = tb ? normal_tensor({N, K}, stream++, 1.f) : normal_tensor({K, N}, stream++, 1.f);
+                Tensor C = normal_tensor({M, N}, stream++, 1.f), R({M, N});
+                std::memcpy(R.data_ptr(), C.data_ptr(), sizeof(float) * C.numel());
+                be.gemm(A, B, C, 1.25f, beta, ta != 0, tb != 0);
+                cpu.gemm(A, B, R, 1.25f, beta, ta != 0, tb != 0);
+                std::vector<double> ref(R.data_ptr(), R.data_ptr() + R.numel());
+                const double e = rel_err(C.data_ptr(), ref);
+                char name[96];
+                std::snprintf(name, sizeof(name), "gemm %dx%dx%d transA=%d transB=%d beta=%g", M, N, K, ta, tb,
+                              (double)beta);
+                report(e <= 1e-3, name, e);
+            }
+    {
+        Tensor x = normal_tensor({96, 768}, stream++, 2.f), w = normal_tensor({768}, stream++, 0.1f),
+               b = normal_tensor({768}, stream++, 0.1f), o1, o2;
+        be.layer_norm(x, w, b, o1, 1e-5f);
+        cpu.layer_norm(x, w, b, o2, 1e-5f);
+        std::vector<double> ref(o2.data_ptr(), o2.data_ptr() + o2.numel());
+        const double e = o1.numel() == o2.numel() ? rel_err(o1.data_ptr(), ref) : 1e9;
+        report(e <= 1e-3, "layer_norm [96,768]", e);
+    }
+    {
+        Tensor t = normal_tensor({64, 2048}, stream++, 3.f), r({64, 2048});
+        std::memcpy(r.data_ptr(), t.data_ptr(), sizeof(float) * t.numel());
+        be.softmax_inplace(t);
+        cpu.softmax_inplace(r);
+        std::vector<double> ref(r.data_ptr(), r.data_ptr() + r.numel());
+        const double e = rel_err(t.data_ptr(), ref);
+        report(e <= 1e-3, "softmax_inplace [64,2048]", e);
+    }
+    {
+        Tensor t = normal_tensor({300000}, stream++, 4.f), r({300000});
+        std::memcpy(r.data_ptr(), t.data_ptr(), sizeof(float) * t.numel());
+        be.gelu_inplace(t);
+        cpu.gelu_inplace(r);
+        std::vector<double> ref(r.data_ptr(), r.data_ptr() + r.numel());
+        const double e = rel_err(t.data_ptr(), ref);
+        report(e <= 1e-5, "gelu_inplace [300000]", e);
+        Tensor a = normal_tensor({300000}, stream++, 1.f), c({300000});
+        std::memcpy(c.data_ptr(), t.data_ptr(), sizeof(float) * t.numel());
+        be.add_inplace(t, a);
+        cpu.add_inplace(c, a);
+        std::vector<double> ref2(c.data_ptr(), c.data_ptr() + c.numel());
+        const double e2 = rel_err(t.data_ptr(), ref2);
+        report(e2 == 0.0, "add_inplace [300000]", e2);
+    }
+}
+
 // Q8_0 round trip so the reference runs on exactly the weights the device holds.
 void q8_roundtrip(Tensor& t) {
     std::vector<unsigned char> blocks((size_t)t.numel() / 32 * 34);
@@ -220,6 +279,7 @@ int main(int argc, char** argv) {
     std::fflush(stdout);
     check_attention(be);
     check_gemm(be);
+    check_ops(be);
     if (dev)
         for (auto dt : {vlrf::KVCacheDType::F32, vlrf::KVCacheDType::F16, vlrf::KVCacheDType::Q8_0})
             check_decode(be, dt);

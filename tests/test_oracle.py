@@ -346,3 +346,59 @@ def test_model_f32_f16_kv_bit_exact_vs_reference(kv_dtype):
             assert ok[:44].any() and not ok[44:].any()       # 20 + 24 rows written
     finally:
         R.ref_model_destroy(h)
+
+
+# ---- the engine's remaining per-op calls (ops.hpp) -------------------------------
+def test_per_op_closed_forms():
+    x = F.normal(50, "lnx", 6 * 333).reshape(6, 333) * 3 + 1
+    y = oracle.layer_norm(x, np.ones(333), np.zeros(333), 1e-5).astype(np.float64)
+    assert np.allclose(y.mean(axis=1), 0, atol=1e-5) and np.allclose(y.var(axis=1), 1, atol=1e-3)
+    w, b = F.normal(50, "lnw", 333), F.normal(50, "lnb", 333)
+    x64 = x.astype(np.float64)
+    want = (x64 - x64.mean(1, keepdims=True)) / np.sqrt(x64.var(1, keepdims=True) + 1e-5) * w + b
+    assert np.max(np.abs(oracle.layer_norm(x, w, b, 1e-5) - want)) <= 1e-5 * np.max(np.abs(want))
+    s = oracle.softmax(x)
+    assert np.allclose(s.sum(axis=1), 1, atol=1e-6)
+    assert np.allclose(oracle.softmax(x + 7.5), s, atol=1e-6)          # shift invariance
+    g = F.normal(51, "gx", 5000) * 4
+    assert np.allclose(oracle.gelu(g) - oracle.gelu(-g), g, atol=1e-5 * 16)   # gelu(x) - gelu(-x) = x
+    assert oracle.gelu(np.zeros(3)).tolist() == [0.0, 0.0, 0.0]
+    A, B = F.normal(52, "gA", 7 * 13).reshape(7, 13), F.normal(52, "gB", 13 * 5).reshape(13, 5)
+    C0 = F.normal(52, "gC", 35).reshape(7, 5)
+    for ta in (False, True):
+        for tb in (False, True):
+            Ai = A.T.copy() if ta else A
+            Bi = B.T.copy() if tb else B
+            got = oracle.gemm(Ai, Bi, C0, 1.5, 0.5, ta, tb)
+            want = 0.5 * C0.astype(np.float64) + 1.5 * (A.astype(np.float64) @ B.astype(np.float64))
+            assert np.max(np.abs(got - want)) <= 1e-5 * np.max(np.abs(want)), (ta, tb)
+
+
+@needs_ref
+def test_per_op_vs_reference():
+    x = F.normal(53, "rx", 5 * 300).reshape(5, 300) * 2
+    w, b = F.normal(53, "rw", 300), F.normal(53, "rb", 300)
+    o1, o2 = np.zeros_like(x), np.zeros_like(x)
+    oracle.lib().orc_layer_norm(x, w, b, o1, 5, 300, 1e-5)
+    R.ref_layer_norm(x, w, b, o2, 5, 300, 1e-5)
+    assert np.array_equal(o1, o2)
+    s1, s2 = (F.normal(53, "rs", 4 * 1000).reshape(4, 1000) * 5 for _ in range(2))
+    oracle.lib().orc_softmax(s1, 4, 1000)
+    R.ref_softmax(s2, 4, 1000)
+    assert np.array_equal(s1, s2)
+    g1, g2 = (F.normal(53, "rg", 9000) * 6 for _ in range(2))
+    oracle.lib().orc_gelu(g1, g1.size)
+    R.ref_gelu(g2, g2.size)
+    assert np.array_equal(g1, g2)
+    A, B = F.normal(53, "rA", 37 * 64).reshape(37, 64), F.normal(53, "rB", 64 * 29).reshape(64, 29)
+    C0 = F.normal(53, "rC", 37 * 29).reshape(37, 29)
+    for ta in (False, True):
+        for tb in (False, True):
+            for alpha, beta in ((1.0, 0.0), (0.7, 1.0), (-1.25, 0.5)):
+                Ai = A.T.copy() if ta else A
+                Bi = B.T.copy() if tb else B
+                got = oracle.gemm(Ai, Bi, C0, alpha, beta, ta, tb)
+                ref = C0.copy()
+                R.ref_gemm(Ai, Ai.shape[0], Ai.shape[1], Bi, Bi.shape[0], Bi.shape[1], ref, 37, 29, alpha, beta,
+                           int(ta), int(tb))
+                assert np.max(np.abs(got - ref)) <= 1e-5 * np.max(np.abs(ref)), (ta, tb, alpha, beta)

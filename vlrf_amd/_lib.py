@@ -68,6 +68,11 @@ _SIGS = {
     "vlrf_hip_model_destroy": (None, [vp]),
     "vlrf_hip_model_set_weight": (i32, [vp, C.c_char_p, vp, i32, i32, i32]),
     "vlrf_hip_model_get_config": (i32, [vp, C.POINTER(ModelConfig)]),
+    "vlrf_hip_gemm_f32": (i32, [vp, vp, vp, vp] + [i32] * 6 + [f32, f32, i32, i32]),
+    "vlrf_hip_layer_norm": (i32, [vp, vp, vp, vp, vp, i32, i32, f32]),
+    "vlrf_hip_softmax": (i32, [vp, vp, i32, i32]),
+    "vlrf_hip_gelu": (i32, [vp, vp, i64]),
+    "vlrf_hip_add": (i32, [vp, vp, vp, i64]),
     "vlrf_hip_model_load_nfw": (i32, [vp, C.c_char_p, C.POINTER(C.c_int)]),
     "vlrf_nfw_open": (i32, [C.c_char_p, C.POINTER(vp)]),
     "vlrf_nfw_close": (None, [vp]),

@@ -568,6 +568,34 @@ int vlrf_hip_qlinear_swiglu(vlrf_hip_ctx_t ctx, vlrf_hip_weight_t wg, vlrf_hip_w
     return launch_qgemm_swiglu(ctx->stream, wg->w, wu->w, a, M, h, false);
 }
 
+// ---- the engine's remaining per-op backend calls --------------------------------------
+int vlrf_hip_gemm_f32(vlrf_hip_ctx_t ctx, const float* A, const float* B, float* C, int M, int N, int K,
+                      int lda, int ldb, int ldc, float alpha, float beta, int transA, int transB) {
+    VH_CTX(ctx);
+    return launch_gemm_f32(ctx->stream, A, B, C, M, N, K, lda, ldb, ldc, alpha, beta, transA != 0, transB != 0);
+}
+
+int vlrf_hip_layer_norm(vlrf_hip_ctx_t ctx, const float* x, const float* w, const float* b, float* out,
+                        int rows, int D, float eps) {
+    VH_CTX(ctx);
+    return launch_layer_norm(ctx->stream, x, w, b, out, rows, D, eps);
+}
+
+int vlrf_hip_softmax(vlrf_hip_ctx_t ctx, float* x, int rows, int D) {
+    VH_CTX(ctx);
+    return launch_softmax(ctx->stream, x, rows, D);
+}
+
+int vlrf_hip_gelu(vlrf_hip_ctx_t ctx, float* x, int64_t n) {
+    VH_CTX(ctx);
+    return launch_gelu(ctx->stream, x, n);
+}
+
+int vlrf_hip_add(vlrf_hip_ctx_t ctx, float* dst, const float* src, int64_t n) {
+    VH_CTX(ctx);
+    return launch_add(ctx->stream, dst, src, n);
+}
+
 // ---- edge ops ----------------------------------------------------------------------
 int vlrf_hip_rmsnorm(vlrf_hip_ctx_t ctx, const float* x, const float* w, float* out, int rows, int D,
                      float eps) {

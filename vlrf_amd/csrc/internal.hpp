@@ -128,6 +128,15 @@ int launch_qlinear_swiglu(hipStream_t s, const DevWeight& wg, const DevWeight& w
 int launch_rmsnorm(hipStream_t s, const float* x, const float* w, float* out, int rows, int D,
                    float eps);
 
+// ---- the engine's remaining per-op backend calls (kernels/ops.hip) ---------------
+int launch_gemm_f32(hipStream_t s, const float* A, const float* B, float* C, int M, int N, int K, int lda,
+                    int ldb, int ldc, float alpha, float beta, bool transA, bool transB);
+int launch_layer_norm(hipStream_t s, const float* x, const float* w, const float* b, float* out, int rows, int D,
+                      float eps);
+int launch_softmax(hipStream_t s, float* x, int rows, int D);
+int launch_gelu(hipStream_t s, float* x, int64_t n);
+int launch_add(hipStream_t s, float* dst, const float* src, int64_t n);
+
 // ---- prefill (MFMA) path: bf16 operands, f32 accumulate -------------------------
 // out[r] = bf16(w ? rmsnorm(x[r]) * w : x[r]) for rows x D
 int launch_rows_to_bf16(hipStream_t s, const float* x, const float* w, uint16_t* out, int rows, int D,

@@ -65,10 +65,11 @@ public:
     bool is_available() const override { return ctx_ != nullptr; }
     std::string capabilities() const override {
         return "HIP backend (gfx950)\n"
-               "  gemm: linear x.W^T, 1<=M<=16, K%32==0 on device (weights cached); others CPU\n"
+               "  gemm: linear x.W^T, 1<=M<=16, K%32==0 on device (weights cached); other shapes\n"
+               "        with >= 2^22 multiply-adds on device (f32), smaller ones CPU\n"
                "  sdp_attention: fused flash attention on device (d_h<=128)\n"
-               "  layer_norm/softmax/gelu/add: CPU\n"
-               "  decode step: HipDecoder (device-resident Q8_0/Q4_0 weights, Q8_0 KV cache)";
+               "  layer_norm/softmax/gelu/add: device for >= 65536 elements, CPU below\n"
+               "  decode step: HipDecoder (device-resident Q8_0/Q4_0 weights, F32/F16/Q8_0 KV cache)";
     }
     void synchronize() const override {
         if (ctx_) vlrf_hip_sync(ctx_);
@@ -81,15 +82,36 @@ public:
     void gemm(Tensor const& A, Tensor const& B, Tensor& C, float alpha, float beta, bool tA,
               bool tB) const override {
         if (ctx_ && !tA && tB && alpha == 1.f && beta == 0.f && linear_on_device(A, B, C)) return;
+        if (ctx_ && gemm_on_device(A, B, C, alpha, beta, tA, tB)) return;
         fallback_.gemm(A, B, C, alpha, beta, tA, tB);
     }
     void layer_norm(Tensor const& x, Tensor const& w, Tensor const& b, Tensor& out,
                     float eps) const override {
+        if (ctx_ && layer_norm_on_device(x, w, b, out, eps)) return;
         fallback_.layer_norm(x, w, b, out, eps);
     }
-    void softmax_inplace(Tensor& t) const override { fallback_.softmax_inplace(t); }
-    void gelu_inplace(Tensor& t) const override { fallback_.gelu_inplace(t); }
-    void add_inplace(Tensor& dst, Tensor const& src) const override { fallback_.add_inplace(dst, src); }
+    void softmax_inplace(Tensor& t) const override {
+        if (ctx_ && t.ndim() >= 1 && t.numel() >= kDeviceMin &&
+            inplace_on_device(t, nullptr, [&](float* p) {
+                return vlrf_hip_softmax(ctx_, p, (int)(t.numel() / t.dim(t.ndim() - 1)), t.dim(t.ndim() - 1));
+            }))
+            return;
+        fallback_.softmax_inplace(t);
+    }
+    void gelu_inplace(Tensor& t) const override {
+        if (ctx_ && t.numel() >= kDeviceMin &&
+            inplace_on_device(t, nullptr, [&](float* p) { return vlrf_hip_gelu(ctx_, p, t.numel()); }))
+            return;
+        fallback_.gelu_inplace(t);
+    }
+    void add_inplace(Tensor& dst, Tensor const& src) const override {
+        if (ctx_ && dst.numel() >= kDeviceMin && src.numel() == dst.numel() &&
+            inplace_on_device(dst, &src, [&](float* p) {
+                return vlrf_hip_add(ctx_, p, static_cast<const float*>(bq_.p), dst.numel());
+            }))
+            return;
+        fallback_.add_inplace(dst, src);
+    }
 
     // Q [n_h,T,d_h], K/V [n_h,ctx,d_h] -> [n_h,T,d_h]; scale 1/sqrt(d_h) as the
     // fused-kernel contract of the reference (attention.hpp:376-392).
@@ -101,6 +123,11 @@ public:
     }
 
 private:
+    // Elementwise and row ops go to the device from this many elements on:
+    // below it the host round trip costs more than the CPU op.
+    static constexpr int64_t kDeviceMin = 1 << 16;
+    static constexpr double kGemmDeviceMin = 4194304.0;   // multiply-adds
+
     struct Buf {
         void* p = nullptr;
         size_t n = 0;
@@ -150,6 +177,53 @@ private:
                              nullptr, 0.f, nullptr) != VLRF_HIP_OK)
             return false;
         return vlrf_hip_d2h(ctx_, C.data_ptr(), by_.p, yb) == VLRF_HIP_OK;
+    }
+
+    // ops::gemm (ops.hpp:170-310) on the device: A, B and C (when beta != 0)
+    // uploaded, C downloaded.
+    bool gemm_on_device(Tensor const& A, Tensor const& B, Tensor& C, float alpha, float beta, bool tA,
+                        bool tB) const {
+        if (A.ndim() != 2 || B.ndim() != 2 || C.ndim() != 2) return false;
+        const int M = tA ? A.dim(1) : A.dim(0), K = tA ? A.dim(0) : A.dim(1);
+        const int N = tB ? B.dim(0) : B.dim(1), KB = tB ? B.dim(1) : B.dim(0);
+        if (KB != K || C.dim(0) != M || C.dim(1) != N || (double)M * N * K < kGemmDeviceMin) return false;
+        const size_t ab = sizeof(float) * A.numel(), bb = sizeof(float) * B.numel(), cb = sizeof(float) * C.numel();
+        if (!grow(bq_, ab) || !grow(bk_, bb) || !grow(bo_, cb)) return false;
+        if (vlrf_hip_h2d(ctx_, bq_.p, A.data_ptr(), ab) || vlrf_hip_h2d(ctx_, bk_.p, B.data_ptr(), bb) ||
+            (beta != 0.f && vlrf_hip_h2d(ctx_, bo_.p, C.data_ptr(), cb)))
+            return false;
+        if (vlrf_hip_gemm_f32(ctx_, static_cast<const float*>(bq_.p), static_cast<const float*>(bk_.p),
+                              static_cast<float*>(bo_.p), M, N, K, A.dim(1), B.dim(1), N, alpha, beta, tA, tB))
+            return false;
+        return vlrf_hip_d2h(ctx_, C.data_ptr(), bo_.p, cb) == VLRF_HIP_OK;
+    }
+
+    bool layer_norm_on_device(Tensor const& x, Tensor const& w, Tensor const& b, Tensor& out, float eps) const {
+        if (x.ndim() < 1 || x.numel() < kDeviceMin) return false;
+        const int D = x.dim(x.ndim() - 1);
+        if (w.numel() != D || b.numel() != D) return false;
+        const size_t xb = sizeof(float) * x.numel(), wb = sizeof(float) * D;
+        if (!grow(bq_, xb) || !grow(bk_, wb) || !grow(bv_, wb) || !grow(bo_, xb)) return false;
+        if (vlrf_hip_h2d(ctx_, bq_.p, x.data_ptr(), xb) || vlrf_hip_h2d(ctx_, bk_.p, w.data_ptr(), wb) ||
+            vlrf_hip_h2d(ctx_, bv_.p, b.data_ptr(), wb))
+            return false;
+        if (vlrf_hip_layer_norm(ctx_, static_cast<const float*>(bq_.p), static_cast<const float*>(bk_.p),
+                                static_cast<const float*>(bv_.p), static_cast<float*>(bo_.p),
+                                (int)(x.numel() / D), D, eps))
+            return false;
+        if (out.numel() != x.numel()) out = Tensor(x.shape);   // ops::layer_norm's like(x)
+        return vlrf_hip_d2h(ctx_, out.data_ptr(), bo_.p, xb) == VLRF_HIP_OK;
+    }
+
+    // t uploaded to bo_ (and src, when given, to bq_), op(bo_) run, t downloaded.
+    template <class Op>
+    bool inplace_on_device(Tensor& t, Tensor const* src, Op op) const {
+        const size_t tb = sizeof(float) * t.numel();
+        if (!grow(bo_, tb) || (src && !grow(bq_, tb))) return false;
+        if (vlrf_hip_h2d(ctx_, bo_.p, t.data_ptr(), tb) || (src && vlrf_hip_h2d(ctx_, bq_.p, src->data_ptr(), tb)))
+            return false;
+        if (op(static_cast<float*>(bo_.p)) != VLRF_HIP_OK) return false;
+        return vlrf_hip_d2h(ctx_, t.data_ptr(), bo_.p, tb) == VLRF_HIP_OK;
     }
 
     bool attention_on_device(Tensor const& Q, Tensor const& K, Tensor const& V, bool causal,

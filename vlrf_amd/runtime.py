@@ -111,6 +111,27 @@ class Context:
         check(lib().vlrf_hip_qlinear_swiglu(self.h, wg.h, wu.h, x.ptr, h.ptr, M,
                                             norm_w.ptr if norm_w else None, float(eps)))
 
+    def gemm_f32(self, A, B, C, M, N, K, alpha=1.0, beta=0.0, trans_a=False, trans_b=False,
+                 lda=None, ldb=None, ldc=None):
+        """IBackend::gemm (ops.hpp:170-310) on device buffers: C = beta*C + alpha*op(A).op(B)."""
+        lda = lda or (M if trans_a else K)
+        ldb = ldb or (K if trans_b else N)
+        ldc = ldc or N
+        check(lib().vlrf_hip_gemm_f32(self.h, A.ptr, B.ptr, C.ptr, M, N, K, lda, ldb, ldc, float(alpha),
+                                      float(beta), int(trans_a), int(trans_b)))
+
+    def layer_norm(self, x, w, b, out, rows, D, eps):
+        check(lib().vlrf_hip_layer_norm(self.h, x.ptr, w.ptr, b.ptr, out.ptr, rows, D, float(eps)))
+
+    def softmax(self, x, rows, D):
+        check(lib().vlrf_hip_softmax(self.h, x.ptr, rows, D))
+
+    def gelu(self, x, n):
+        check(lib().vlrf_hip_gelu(self.h, x.ptr, n))
+
+    def add(self, dst, src, n):
+        check(lib().vlrf_hip_add(self.h, dst.ptr, src.ptr, n))
+
     def rms_norm(self, x, w, out, rows, D, eps):
         check(lib().vlrf_hip_rmsnorm(self.h, x.ptr, w.ptr, out.ptr, rows, D, float(eps)))
 
