@@ -57,6 +57,22 @@ def test_forward_hidden_tiny(ctx, dtype, chunks):
     assert m.used == om.used == n
 
 
+@pytest.mark.parametrize("n_heads,n_kv,d_model", [(4, 4, 256), (4, 2, 256), (8, 1, 512), (2, 2, 256),
+                                                  (4, 1, 512), (8, 2, 1024)])
+def test_forward_hidden_gqa_shapes(ctx, n_heads, n_kv, d_model):
+    """Every GQA group size the prefill attention takes (1, 2, 4, 8) at d_head
+    64 and 128, with odd counts of 32-query blocks (the zig-zag pairing's
+    unpaired middle block) and a second chunk that starts past position 0."""
+    cfg = dict(F.tiny(V.DT_Q8_0, n_layers=1, max_seq_len=256), n_heads=n_heads, n_kv_heads=n_kv,
+               d_model=d_model, d_ff=2 * d_model)
+    print(f"[case] forward_hidden gqa heads={n_heads}/{n_kv} d_model={d_model}", flush=True)
+    m, om = _pair(ctx, cfg, 39)
+    for i, T in enumerate((45, 150)):
+        x = F.normal(39, f"gqa{i}", T * d_model).reshape(T, d_model)
+        got = m.forward_hidden(ctx.to_device(x)).download((T, d_model))
+        check(got, om.forward_hidden(x), f"chunk {i}")
+
+
 def test_prefill_mfma_then_decode_matches_oracle(ctx):
     """prefill_mfma over a 90-token prompt, then decode steps: the logits after
     it agree with the oracle's (whole-prompt forward, then single tokens)."""

@@ -416,62 +416,104 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
 // attends the dequantized cache rows kpos <= qpos (attention.hpp:232,253-261)
 // with scale 1/sqrt(d_h); flash_attn_head's online softmax (attention.hpp:207-309).
 //
-// Design: a workgroup = one KV head g and 32 consecutive query tokens; wave w
-// serves query head g*REP + w, so each K/V tile (64 keys, dequantized to bf16
-// in LDS, V transposed) is shared by the REP heads of the GQA group.  The wave
+// Design: a workgroup = one KV head g and 8/REP blocks of 32 consecutive query
+// tokens, 8 waves; wave w serves query head g*REP + w%REP on query block w/REP,
+// so each K/V tile (64 keys, dequantized to bf16 in LDS, V transposed) is
+// shared by the REP heads of the GQA group and 256/REP queries.  Each thread
+// stages 16 elements of one key; the next tile's elements are loaded into
+// registers before the current tile is computed, so their latency hides
+// behind the matrix work.  A wave skips tiles that lie wholly past its last
+// query (it still joins the barriers).  The wave
 // computes S^T = K.Q^T and O^T = V^T.P^T with v_mfma_f32_32x32x16_bf16: in that
 // orientation lane l owns query l%32 (both lane halves), so the softmax max and
 // sum are one cross-half shuffle, the rescale multiplies the lane's own
 // accumulators, and P re-enters the second product through register shuffles.
-constexpr int kPQ = 32, kPK = 64;         // queries per workgroup, keys per tile
+constexpr int kPQ = 32, kPK = 64;         // queries per wave, keys per tile
 
-// 16 consecutive cache elements of dtype KVT starting at element e0 -> f32
-// (Q8_0 codes times the row scale); zero where !live.
+// Raw cache elements of one staging item (16 consecutive elements of one key
+// row, K and V) held in registers between their load and the LDS store.
 template <int KVT>
-__device__ __forceinline__ void cache16(const int8_t* base, size_t e0, float scale, bool live, float (&o)[16]) {
+struct RawKV {
+    static constexpr int W = KVT == VLRF_KV_Q8_0 ? 1 : KVT == VLRF_KV_F16 ? 2 : 4;   // uint4 per 16 elements
+    uint4 k[W], v[W];
+    float sk, sv;
+};
+
+template <int KVT>
+__device__ __forceinline__ void load_raw(RawKV<KVT>& r, const int8_t* kq, const int8_t* vq, const float* ks,
+                                         const float* vs, size_t e0, int row) {
+    constexpr int EB = RawKV<KVT>::W;                 // bytes per element = uint4 per 16 elements
+#pragma unroll
+    for (int i = 0; i < RawKV<KVT>::W; ++i) {
+        r.k[i] = *reinterpret_cast<const uint4*>(kq + e0 * EB + 16 * i);
+        r.v[i] = *reinterpret_cast<const uint4*>(vq + e0 * EB + 16 * i);
+    }
     if constexpr (KVT == VLRF_KV_Q8_0) {
-        const uint4 c = *reinterpret_cast<const uint4*>(base + e0);
-        const uint32_t u[4] = {c.x, c.y, c.z, c.w};
+        r.sk = ks[row];
+        r.sv = vs[row];
+    }
+}
+
+// The 16 elements -> f32 (Q8_0 codes times the row scale, f16 widened); zero where !live.
+template <int KVT>
+__device__ __forceinline__ void raw_f32(const uint4 (&w)[RawKV<KVT>::W], float scale, bool live, float (&o)[16]) {
+    if constexpr (KVT == VLRF_KV_Q8_0) {
+        const uint32_t u[4] = {w[0].x, w[0].y, w[0].z, w[0].w};
 #pragma unroll
         for (int e = 0; e < 16; ++e) o[e] = (float)(int8_t)(u[e >> 2] >> (8 * (e & 3))) * (live ? scale : 0.f);
     } else if constexpr (KVT == VLRF_KV_F16) {
-        const uint4 c0 = *reinterpret_cast<const uint4*>(base + 2 * e0);
-        const uint4 c1 = *reinterpret_cast<const uint4*>(base + 2 * e0 + 16);
-        const uint32_t u[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+        const uint32_t u[8] = {w[0].x, w[0].y, w[0].z, w[0].w, w[1].x, w[1].y, w[1].z, w[1].w};
 #pragma unroll
         for (int e = 0; e < 16; ++e) o[e] = live ? f16_bits_to_f32((u[e >> 1] >> (16 * (e & 1))) & 0xFFFFu) : 0.f;
     } else {
-        const float4* f = reinterpret_cast<const float4*>(base + 4 * e0);
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            const float4 v = f[k];
-            o[4 * k] = live ? v.x : 0.f;
-            o[4 * k + 1] = live ? v.y : 0.f;
-            o[4 * k + 2] = live ? v.z : 0.f;
-            o[4 * k + 3] = live ? v.w : 0.f;
+            o[4 * k] = live ? __uint_as_float(w[k].x) : 0.f;
+            o[4 * k + 1] = live ? __uint_as_float(w[k].y) : 0.f;
+            o[4 * k + 2] = live ? __uint_as_float(w[k].z) : 0.f;
+            o[4 * k + 3] = live ? __uint_as_float(w[k].w) : 0.f;
         }
     }
 }
 
+// Column (key) of V^T row d in LDS: groups of 8 keys XOR-swizzled by the row's
+// 16-dim block, so the 8 stagers of one key (8 blocks of 16 dims) hit distinct
+// banks, while every 8-key run an MFMA operand reads stays contiguous.
+__device__ __forceinline__ int vt_col(int d, int key) { return key ^ (8 * ((d >> 4) & 7)); }
+
 template <int D, int REP, int KVT>
-__global__ __launch_bounds__(64 * REP) void attn_prefill_kernel(
+__global__ __launch_bounds__(512) void attn_prefill_kernel(
     const float* __restrict__ qkv, int ld, const int8_t* __restrict__ kq, const int8_t* __restrict__ vq,
     const float* __restrict__ ks, const float* __restrict__ vs, long head_stride, int T, int pos0,
     float scale, int n_heads, uint16_t* __restrict__ out) {
-    constexpr bool Q8 = KVT == VLRF_KV_Q8_0;
     typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
     typedef float f32x16 __attribute__((ext_vector_type(16)));
-    constexpr int NT = 64 * REP;
+    constexpr int NT = 512, NQB = 8 / REP;           // waves: REP heads x NQB query blocks
     constexpr int KS = D + 8, VS = kPK + 8;          // padded LDS row strides (bf16)
+    constexpr int ITEMS = kPK * (D / 16);            // staging items of 16 elements per tile
+    static_assert(ITEMS <= NT, "one staging item per thread");
     __shared__ __align__(16) __bf16 Ks[kPK * KS];    // K tile [key][d]
-    __shared__ __align__(16) __bf16 Vt[D * VS];      // V tile transposed [d][key]
+    __shared__ __align__(16) __bf16 Vt[D * VS];      // V tile transposed [d][vt_col(d, key)]
 
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, hh = lane >> 5, lq = lane & 31;
-    const int g = blockIdx.y, h = g * REP + w;
-    const int q0 = blockIdx.x * kPQ;
+    const int g = blockIdx.y, h = g * REP + w % REP;
+    // Query blocks of 32 in zig-zag order 0, n-1, 1, n-2, ...: the workgroup's
+    // NQB consecutive entries pair early (short) and late (long) causal rows,
+    // so every workgroup holds about the same number of wave-tiles.
+    const int nblk = (T + kPQ - 1) / kPQ;
+    auto zigzag = [nblk](int i) { return (i & 1) ? nblk - 1 - (i >> 1) : i >> 1; };
+    int qlast = 0;                                   // the workgroup's last query position
+#pragma unroll
+    for (int j = 0; j < NQB; ++j) {
+        const int i = blockIdx.x * NQB + j;
+        if (i < nblk) qlast = max(qlast, pos0 + min(kPQ * zigzag(i) + kPQ, T) - 1);
+    }
+    const int iw = blockIdx.x * NQB + w / REP;
+    const int q0 = iw < nblk ? kPQ * zigzag(iw) : T; // this wave's first query (T: no block)
     const int qi = min(q0 + lq, T - 1);              // clamped: rows past T are not stored
     const int qpos = pos0 + qi;
     const size_t hb = (size_t)g * head_stride;
+    const int wave_last = pos0 + min(q0 + kPQ, T) - 1;   // this wave's last query position (q0 < T)
 
     bf16x8 qf[D / 16];                               // B operand: query lq, dims 16kk + 8hh + e
     {
@@ -487,97 +529,116 @@ __global__ __launch_bounds__(64 * REP) void attn_prefill_kernel(
     f32x16 o[D / 32];
 #pragma unroll
     for (int c = 0; c < D / 32; ++c) o[c] = f32x16{};
-    float m_run = kNegInf, l_run = 0.f;
+    float m_run = kNegInf, l_run = 0.f;              // running max (base-2 scaled) and sum
+    const float sl2 = scale * 1.4426950408889634f;   // scale * log2(e)
 
-    const int qlast = pos0 + min(q0 + kPQ, T) - 1;   // last query position of the workgroup
-    const int kv_end = pos0 + T;                     // cache rows written
+    const int kv_end = pos0 + T;                             // cache rows written
     const int ntile = qlast / kPK + 1;
+    // Staging item of this thread: key it / (D/16), dims 16 * (it % (D/16)) .. +15.
+    const int it = threadIdx.x, skey = it / (D / 16), spart = it % (D / 16);
+    const bool stager = it < ITEMS;
+    RawKV<KVT> raw;
+    auto fetch = [&](int kt) {                       // tile kt's elements into registers
+        const int kp = kt * kPK + skey, kr = kp < kv_end ? kp : 0;
+        load_raw<KVT>(raw, kq, vq, ks, vs, hb + (size_t)kr * D + 16 * spart, kr);
+    };
+    if (stager) fetch(0);
     for (int kt = 0; kt < ntile; ++kt) {
         const int kv0 = kt * kPK;
-        // Stage the tile: 16 dims of one key per item; rows past kv_end are zero.
-        for (int i = threadIdx.x; i < kPK * (D / 16); i += NT) {
-            const int key = i / (D / 16), part = i - key * (D / 16);
-            const int kp = kv0 + key;
-            const bool live = kp < kv_end;
-            const int kr = live ? kp : 0;
-            const size_t e0 = hb + (size_t)kr * D + 16 * part;
-            float kf[16], vf[16];                           // dequantize_row_q8_0 / f16_to_f32
-            cache16<KVT>(kq, e0, Q8 ? ks[kr] : 1.f, live, kf);
-            cache16<KVT>(vq, e0, Q8 ? vs[kr] : 1.f, live, vf);
+        if (stager) {                                // registers -> LDS as bf16 (rows past kv_end zero)
+            const bool live = kv0 + skey < kv_end;
+            float kf[16], vf[16];                    // dequantize_row_q8_0 / f16_to_f32
+            raw_f32<KVT>(raw.k, KVT == VLRF_KV_Q8_0 ? raw.sk : 1.f, live, kf);
+            raw_f32<KVT>(raw.v, KVT == VLRF_KV_Q8_0 ? raw.sv : 1.f, live, vf);
             bf16x8 k0, k1;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 k0[e] = (__bf16)kf[e];
                 k1[e] = (__bf16)kf[8 + e];
             }
-            *reinterpret_cast<bf16x8*>(&Ks[key * KS + 16 * part]) = k0;
-            *reinterpret_cast<bf16x8*>(&Ks[key * KS + 16 * part + 8]) = k1;
+            *reinterpret_cast<bf16x8*>(&Ks[skey * KS + 16 * spart]) = k0;
+            *reinterpret_cast<bf16x8*>(&Ks[skey * KS + 16 * spart + 8]) = k1;
 #pragma unroll
-            for (int e = 0; e < 16; ++e) Vt[(16 * part + e) * VS + key] = (__bf16)vf[e];
+            for (int e = 0; e < 16; ++e) {
+                const int d = 16 * spart + e;
+                Vt[d * VS + vt_col(d, skey)] = (__bf16)vf[e];
+            }
         }
         __syncthreads();
+        // The next tile's loads go out now and land while this tile is computed.
+        if (stager && kt + 1 < ntile) fetch(kt + 1);
 
-        // S^T = K . Q^T for the two 32-key blocks of the tile.
-        f32x16 sc[2] = {f32x16{}, f32x16{}};
+        if (q0 < T && kv0 <= wave_last) {            // tiles wholly past this wave's queries: nothing to do
+            // S^T = K . Q^T for the two 32-key blocks of the tile.
+            f32x16 sc[2] = {f32x16{}, f32x16{}};
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+            for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-            for (int kk = 0; kk < D / 16; ++kk) {
-                const bf16x8 a = *reinterpret_cast<const bf16x8*>(&Ks[(32 * kb + lq) * KS + 16 * kk + 8 * hh]);
-                sc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[kk], sc[kb], 0, 0, 0);
+                for (int kk = 0; kk < D / 16; ++kk) {
+                    const bf16x8 a = *reinterpret_cast<const bf16x8*>(&Ks[(32 * kb + lq) * KS + 16 * kk + 8 * hh]);
+                    sc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[kk], sc[kb], 0, 0, 0);
+                }
+            // Causal mask (key r(v) = 8(v/4) + 4hh + v%4 of the block), only on
+            // tiles that cross the wave's diagonal.
+            if (kv0 + kPK - 1 > pos0 + q0) {
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) {
+                        const int kp = kv0 + 32 * kb + 8 * (v >> 2) + 4 * hh + (v & 3);
+                        if (kp > qpos) sc[kb][v] = kNegInf;
+                    }
             }
-        // Scale, causal mask (key r(v) = 8(v/4) + 4hh + v%4 of the block), online softmax.
-        float mx = kNegInf;
+            // Online softmax in base 2: exp(s*scale - m) = 2^(s*scale*log2(e) - m'),
+            // the max taken on raw scores (scale > 0); masked scores give 2^-inf = 0.
+            float mx = kNegInf;
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+            for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int kp = kv0 + 32 * kb + 8 * (v >> 2) + 4 * hh + (v & 3);
-                const float x = kp <= qpos ? sc[kb][v] * scale : kNegInf;
-                sc[kb][v] = x;
-                mx = fmaxf(mx, x);
-            }
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float mn = fmaxf(m_run, mx);           // finite: key 0 is in the first tile
-        const float corr = m_run == kNegInf ? 0.f : expf(m_run - mn);
-        float sum = 0.f;
+                for (int v = 0; v < 16; ++v) mx = fmaxf(mx, sc[kb][v]);
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            const float mn = fmaxf(m_run, mx * sl2); // finite: key 0 is in the first tile
+            const float corr = __builtin_amdgcn_exp2f(m_run - mn);   // 0 on the first tile
+            float sum = 0.f;
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+            for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const float p = sc[kb][v] == kNegInf ? 0.f : expf(sc[kb][v] - mn);
-                sc[kb][v] = p;
-                sum += p;
-            }
-        sum += __shfl_xor(sum, 32);
-        l_run = l_run * corr + sum;
-        m_run = mn;
+                for (int v = 0; v < 16; ++v) {
+                    const float p = __builtin_amdgcn_exp2f(fmaf(sc[kb][v], sl2, -mn));
+                    sc[kb][v] = p;
+                    sum += p;
+                }
+            sum += __shfl_xor(sum, 32);
+            l_run = l_run * corr + sum;
+            m_run = mn;
 #pragma unroll
-        for (int c = 0; c < D / 32; ++c)
+            for (int c = 0; c < D / 32; ++c)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) o[c][v] *= corr;
+                for (int v = 0; v < 16; ++v) o[c][v] *= corr;
 
-        // O^T += V^T . P^T, 16 keys per step.  The B operand needs keys
-        // 16s + 8hh + e of the lane's query: group 2s+hh of this half and of
-        // the other half (v-groups of 4 keys), exchanged with one xor-32 shuffle.
+            // O^T += V^T . P^T, 16 keys per step.  The B operand needs keys
+            // 16s + 8hh + e of the lane's query: group 2s+hh of this half and of
+            // the other half (v-groups of 4 keys), exchanged with one xor-32 shuffle.
 #pragma unroll
-        for (int kk2 = 0; kk2 < kPK / 16; ++kk2) {
-            const int kb = kk2 >> 1, s2 = kk2 & 1;
-            const int gown = 2 * s2 + hh, gsend = 2 * s2 + 1 - hh;
-            float y[4];
+            for (int kk2 = 0; kk2 < kPK / 16; ++kk2) {
+                const int kb = kk2 >> 1, s2 = kk2 & 1;
+                const int gown = 2 * s2 + hh, gsend = 2 * s2 + 1 - hh;
+                float y[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) y[e] = __shfl_xor(sc[kb][4 * gsend + e], 32);
-            bf16x8 b;
+                for (int e = 0; e < 4; ++e) y[e] = __shfl_xor(sc[kb][4 * gsend + e], 32);
+                bf16x8 b;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float mine = sc[kb][4 * gown + e];
-                b[e] = (__bf16)(hh == 0 ? mine : y[e]);
-                b[4 + e] = (__bf16)(hh == 0 ? y[e] : mine);
-            }
+                for (int e = 0; e < 4; ++e) {
+                    const float mine = sc[kb][4 * gown + e];
+                    b[e] = (__bf16)(hh == 0 ? mine : y[e]);
+                    b[4 + e] = (__bf16)(hh == 0 ? y[e] : mine);
+                }
 #pragma unroll
-            for (int c = 0; c < D / 32; ++c) {
-                const bf16x8 a = *reinterpret_cast<const bf16x8*>(&Vt[(32 * c + lq) * VS + 16 * kk2 + 8 * hh]);
-                o[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, o[c], 0, 0, 0);
+                for (int c = 0; c < D / 32; ++c) {
+                    const int d = 32 * c + lq;
+                    const bf16x8 a = *reinterpret_cast<const bf16x8*>(&Vt[d * VS + vt_col(d, 16 * kk2 + 8 * hh)]);
+                    o[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, o[c], 0, 0, 0);
+                }
             }
         }
         __syncthreads();                             // before the next tile overwrites Ks / Vt
@@ -772,9 +833,10 @@ int launch_attn_prefill(hipStream_t s, const float* qkv, int ld, const KVLayer& 
     VH_ARG(T >= 1 && pos0 >= 0 && pos0 + T <= max_seq, "attn_prefill: positions [%d,%d) outside the cache",
            pos0, pos0 + T);
     VH_ARG(ld % 4 == 0, "attn_prefill: row stride %d not a multiple of 4", ld);
-    dim3 grid((T + kPQ - 1) / kPQ, n_kv);
-#define VH_AP(D, R, KT)                                                                                   \
-    hipLaunchKernelGGL((attn_prefill_kernel<D, R, KT>), grid, dim3(64 * R), 0, s, qkv, ld, L.k, L.v, L.ks, \
+    const int nqb = 8 / rep;                        // query blocks of 32 per workgroup (8 waves)
+    dim3 grid(((T + kPQ - 1) / kPQ + nqb - 1) / nqb, n_kv);
+#define VH_AP(D, R, KT)                                                                               \
+    hipLaunchKernelGGL((attn_prefill_kernel<D, R, KT>), grid, dim3(512), 0, s, qkv, ld, L.k, L.v, L.ks, \
                        L.vs, (long)max_seq * d_head, T, pos0, scale, n_heads, out)
 #define VH_AP_R(D, KT)                      \
     switch (rep) {                          \
