@@ -173,8 +173,9 @@ int dispatch_m(hipStream_t s, const DevWeight& a, const DevWeight* b, const floa
 }
 
 // ---- M = 1 decode GEMV ---------------------------------------------------------
-// The workgroup stages the (RMS-normalised) activation vector in LDS once, in
-// a lane-interleaved layout: the i-th float4 of lane l for chunk c sits at
+// The workgroup stages the activation vector (times the norm weight when
+// RMSNorm is fused; 1/rms multiplies the finished dots) in LDS once, behind a
+// single barrier, in a lane-interleaved layout: the i-th float4 of lane l for chunk c sits at
 // [(c*EPL/4 + i)*64 + l], so every ds_read_b128 of a wave touches 64
 // consecutive float4 (no bank conflicts).  A wave owns RPW rows (SwiGLU: RPW
 // gate/up row pairs) at a time; lane l covers EPL consecutive columns of each
@@ -182,7 +183,10 @@ int dispatch_m(hipStream_t s, const DevWeight& a, const DevWeight* b, const floa
 // contiguous 1 KiB run of a row (Q8_0: 16 codes, Q4_0: 32 nibbles).  Waves
 // walk their rows with a two-deep register pipeline: the next rows' weights
 // are in flight while the current ones are reduced, and the first rows' loads
-// are issued before the activations are staged.  Codes are decoded with
+// are issued before the activations are staged -- after a barrier that puts
+// every wave's activation loads ahead of them, since a CU's vector memory
+// requests are served in order.  Codes are loaded nontemporal (streamed once
+// per step).  Codes are decoded with
 // v_cvt_f32_ubyte*: Q8_0 codes are biased by 128 (xor 0x80), Q4_0 nibbles are
 // used as stored, and the bias is removed once per chunk with the lane's sum
 // of x (sum (q+b)x - b*sum x = sum qx).
@@ -198,6 +202,8 @@ constexpr int kGemvMaxGroups = 512;      // workgroups of the row loop (2 per CU
 constexpr int kGemvWaves = 8;            // waves per workgroup (one staged copy of x)
 
 __device__ __forceinline__ float ub(uint32_t v, int k) { return (float)((v >> (8 * k)) & 0xFFu); }
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 template <int NM, int RPW, int NC>
 struct GemvRegs {
@@ -232,7 +238,10 @@ __device__ __forceinline__ void gemv_load(GemvRegs<NM, RPW, NC>& R, const uint8_
                 const bool in = row < N && e0 < K;
                 const size_t qo = in ? (size_t)row * qrow + (size_t)c * 1024 + lane * 16 : 0;
                 const size_t so = in ? (size_t)row * kb + e0 / 32 : 0;
-                R.w[m][r][c] = *reinterpret_cast<const uint4*>(q + qo);
+                // Streamed once per step: nontemporal, so the codes do not
+                // displace the activations and scales from the caches.
+                const u32x4 t = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(q + qo));
+                R.w[m][r][c] = make_uint4(t.x, t.y, t.z, t.w);
                 R.s[m][r][c] = d[so];
             }
         }
@@ -241,8 +250,8 @@ __device__ __forceinline__ void gemv_load(GemvRegs<NM, RPW, NC>& R, const uint8_
 
 template <int WT, int NM, int RPW, int NC, bool SWIGLU>
 __device__ __forceinline__ void gemv_compute(const GemvRegs<NM, RPW, NC>& R, const float4* xs4,
-                                             const float (&xsum)[NC], int row0, int N, int K, int lane,
-                                             const float* residual, float* y) {
+                                             const float (&xsum)[NC], float inv, int row0, int N, int K,
+                                             int lane, const float* residual, float* y) {
     constexpr int EPL = Gemv<WT>::EPL;
     float acc[NM][RPW];
 #pragma unroll
@@ -290,9 +299,9 @@ __device__ __forceinline__ void gemv_compute(const GemvRegs<NM, RPW, NC>& R, con
 #pragma unroll
     for (int r = 0; r < RPW; ++r) {
         const int row = row0 + r;
-        float out = wave_sum(acc[0][r]);
+        float out = wave_sum(acc[0][r]) * inv;
         if constexpr (SWIGLU) {
-            const float u = wave_sum(acc[1][r]);
+            const float u = wave_sum(acc[1][r]) * inv;
             out = u * (out / (1.f + expf(-out)));   // silu(g) * u, ops.hpp:409-441
         }
         if (lane == 0 && row < N) {
@@ -337,6 +346,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(
     // slower: 16 waves per CU re-reading x and the norm weight cost more L1
     // bandwidth than the two barriers.)
     float xsum[NC];
+    float inv = 1.f;                                  // 1/rms, applied to the finished dots
     GemvRegs<NM, RPW, NC> A, B;
     {
         const float* xs = xr_src(x, x_row, K);
@@ -355,10 +365,15 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(
                 gw[p] = reinterpret_cast<const float4*>(norm_w)[(f < XF4 && 4 * f < K) ? f : 0];
             }
         }
+        // Every wave's activation requests enter the CU's memory pipeline
+        // before any weight request, so x is not queued behind the stream.
+        __builtin_amdgcn_s_barrier();
         gemv_load<WT, NM, RPW, NC>(A, qa, da, qb, db, row0, N, K, lane);
         gemv_load<WT, NM, RPW, NC>(B, qa, da, qb, db, row0 + rstep, N, K, lane);
 
-        // Stage x (optionally RMS-normalised, ops.hpp:488-498) in the lane-interleaved layout.
+        // Stage x (times the norm weight when fused) in the lane-interleaved
+        // layout, with one barrier: RMSNorm (ops.hpp:488-498) is per row, so
+        // W.((x*inv)*w) = inv * W.(x*w) and 1/rms is applied to the dots.
         float ss = 0.f;
 #pragma unroll
         for (int p = 0; p < PER; ++p) {
@@ -366,15 +381,9 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(
             ss += v[p].x * v[p].x + v[p].y * v[p].y + v[p].z * v[p].z + v[p].w * v[p].w;
             if (x_copy && blockIdx.x == 0 && f < XF4 && 4 * f < K) reinterpret_cast<float4*>(x_copy)[f] = v[p];
         }
-        float inv = 1.f;
         if (norm_w) {
             ss = wave_sum(ss);
             if (lane == 0) red[wave] = ss;
-            __syncthreads();
-            ss = 0.f;
-#pragma unroll
-            for (int w = 0; w < kGemvWaves; ++w) ss += red[w];
-            inv = 1.f / sqrtf(ss / (float)K + eps);
         }
 #pragma unroll
         for (int p = 0; p < PER; ++p) {
@@ -383,14 +392,20 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(
                 float4 o = v[p];
                 if (norm_w && 4 * f < K) {
                     const float4 g = gw[p];
-                    o.x = o.x * inv * g.x; o.y = o.y * inv * g.y;
-                    o.z = o.z * inv * g.z; o.w = o.w * inv * g.w;
+                    o.x = o.x * g.x; o.y = o.y * g.y;
+                    o.z = o.z * g.z; o.w = o.w * g.w;
                 }
                 const int e = 4 * f, c = e / CW, r = e - c * CW, l = r / EPL, i = (r - l * EPL) / 4;
                 xs4[(c * (EPL / 4) + i) * 64 + l] = o;
             }
         }
         __syncthreads();
+        if (norm_w) {
+            ss = 0.f;
+#pragma unroll
+            for (int w = 0; w < kGemvWaves; ++w) ss += red[w];
+            inv = 1.f / sqrtf(ss / (float)K + eps);
+        }
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
             float sacc = 0.f;
@@ -406,11 +421,11 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(
     // Loads stay unconditional inside the loop as well (see gemv_load).
     for (; row0 < N; row0 += 2 * rstep) {
         const int r1 = row0 + rstep;
-        gemv_compute<WT, NM, RPW, NC, SWIGLU>(A, xs4, xsum, row0, N, K, lane, residual, y);
+        gemv_compute<WT, NM, RPW, NC, SWIGLU>(A, xs4, xsum, inv, row0, N, K, lane, residual, y);
         if (r1 >= N) break;
         const int r2 = r1 + rstep;
         gemv_load<WT, NM, RPW, NC>(A, qa, da, qb, db, r2, N, K, lane);
-        gemv_compute<WT, NM, RPW, NC, SWIGLU>(B, xs4, xsum, r1, N, K, lane, residual, y);
+        gemv_compute<WT, NM, RPW, NC, SWIGLU>(B, xs4, xsum, inv, r1, N, K, lane, residual, y);
         if (r2 >= N) break;
         gemv_load<WT, NM, RPW, NC>(B, qa, da, qb, db, r2 + rstep, N, K, lane);
     }
