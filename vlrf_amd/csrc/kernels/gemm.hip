@@ -16,6 +16,9 @@
 // tile column as 1.06 B (Q8_0) or 0.56 B (Q4_0) per weight.  LDS rows are
 // padded by 16 bytes so the lanes of an operand read hit distinct banks.
 // Epilogues: store f32, add a residual, or SwiGLU (two weights, silu(g)*u).
+// Q8_0 weights with M > 128 take mfma_q8gemm_lds_kernel instead (below): the
+// same arithmetic with operands brought into a 3-stage LDS ring by
+// direct-to-LDS loads and codes decoded in registers next to the MFMAs.
 //
 // 2. Small M (2..16 rows, ops.hpp:142-168,254-305 for M = 2..16) with
 // f32-class accuracy.  Q8_0/Q4_0 codes are integers of at most 8 bits, exact
@@ -25,7 +28,6 @@
 // split into bf16 hi + lo (x = hi + lo to about 2^-17 relative), two MFMAs per
 // block, so the products carry ~16 significant bits of x and accumulate in
 // f32: results agree with the f32 reference to ~1e-5 relative.
-#include "../internal.hpp"
 #include "../internal.hpp"
 
 namespace vlrf_hip {
@@ -251,6 +253,211 @@ void launch_cfg(hipStream_t s, int wt, const uint16_t* a, const DevWeight& w0, c
     else
         hipLaunchKernelGGL((mfma_qgemm_kernel<C, VLRF_DT_Q4_0, EPI>), grid, block, 0, s, a, w0.q, w0.d, qb, db,
                            M, w0.N, w0.K, residual, out);
+}
+
+// ---- Q8_0 prefill GEMM with direct-to-LDS loads --------------------------------
+// C[M,N] = A[M,K] . W[N,K]^T for Q8_0 W and M > 128: workgroup tile 256 x 128
+// (per weight matrix; SwiGLU computes gate and up tiles together), 8 waves as
+// 2 along M x 4 along N, so each wave owns a 128 x 32 block per matrix (four
+// 32x32 MFMA tiles) and each weight code is decoded by only two waves.
+// K advances in steps of 64 through a 3-stage LDS ring filled by
+// global_load_lds_dwordx4 (the loads write LDS without passing through
+// registers): stage = A rows as bf16 (32 KB), the raw codes of the tile's weight
+// rows (8 KB per matrix) and their two f16 block scales.  16-byte chunks are
+// XOR-swizzled within a row (A: chunk ^ ((row >> 1) & 7); codes:
+// chunk ^ ((row >> 2) & 3)) so the MFMA operand reads of 16 consecutive rows hit
+// distinct banks; the loads realise the swizzle by choosing which global chunk
+// each lane fetches (lane l always writes LDS bytes 16l..16l+15 of its wave's
+// 1 KB destination).  One barrier per K step: wait until this wave's loads of
+// the step have landed, barrier, issue the loads of step k+2 into the buffer
+// step k-1 used, compute step k.  The MFMA k order within a 32-element block
+// is permuted (lane half h takes code chunk 2p+h, slices q = 0, 1 its two 8-byte
+// halves; A uses the same permutation), so a lane reads 16 code bytes at once;
+// codes are decoded in registers (code * scale rounded to bf16) just before use.
+namespace lds_gemm {
+
+constexpr int BM = 256, BN = 128, NT = 512, WM = 128, WN = 32, MI = WM / 32;
+constexpr int A_B = BM * 128;                 // one K step of A: 256 rows x 64 bf16
+constexpr int A_IT = A_B / (NT * 16);         // 16-byte loads per thread
+template <int NM> struct Stage {
+    static constexpr int W_B = NM * BN * 64;  // codes: NM*BN rows x 64 bytes
+    static constexpr int S_B = NM * BN * 4;   // two f16 block scales per row
+    static constexpr int W_IT = W_B / (NT * 16);
+    static constexpr int S_WAVES = NM * BN / 64;
+    // Loads of one step by a wave that issues no scale load: waiting until at most
+    // this many are outstanding leaves only the newer step in flight for every wave.
+    static constexpr int LPS = A_IT + W_IT;
+    static constexpr int WAIT = (LPS & 15) | (7 << 4) | (15 << 8) | ((LPS >> 4) << 14);   // s_waitcnt vmcnt(LPS)
+    static_assert(W_IT >= 1 && S_WAVES <= 8, "stage shape");
+};
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(size_t)(const __attribute__((address_space(3))) char*)(p);
+}
+// Direct-to-LDS loads (lane l writes LDS base + size*l; base wave-uniform, in M0).
+// Written as asm so that the compiler's wait insertion, which cannot tell these
+// LDS writes apart from the stage being read, does not wait for every load in
+// flight before each LDS read; the kernel orders them with explicit vmcnt waits
+// and barriers instead.  Loads complete in issue order, so these extra loads
+// only make the compiler's own vmcnt waits stricter.
+__device__ __forceinline__ void dma16(const void* g, uint32_t base) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                 :: "v"(g), "s"(__builtin_amdgcn_readfirstlane(base)) : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(const void* g, uint32_t base) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
+                 :: "v"(g), "s"(__builtin_amdgcn_readfirstlane(base)) : "memory", "m0");
+}
+__device__ __forceinline__ int swz_a(int r) { return (r >> 1) & 7; }
+__device__ __forceinline__ int swz_w(int n) { return (n >> 2) & 3; }
+
+}  // namespace lds_gemm
+
+template <int NM, int EPI>
+__global__ __launch_bounds__(lds_gemm::NT) void mfma_q8gemm_lds_kernel(
+    const uint16_t* __restrict__ A, const uint8_t* __restrict__ qa, const __half* __restrict__ da,
+    const uint8_t* __restrict__ qb, const __half* __restrict__ db, int M, int N, int K,
+    const float* __restrict__ residual, void* __restrict__ out) {
+    using namespace lds_gemm;
+    using S = Stage<NM>;
+    __shared__ __align__(16) uint8_t A0[A_B], A1[A_B], A2[A_B];
+    __shared__ __align__(16) uint8_t W0[S::W_B], W1[S::W_B], W2[S::W_B];
+    __shared__ __align__(16) uint8_t S0[S::S_B], S1[S::S_B], S2[S::S_B];
+    const int lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave >> 2, wn = wave & 3;
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+
+    // Load sources of K step 0 (step k adds 128 B of A, 64 B of codes, 4 B of
+    // scales) and the wave-uniform offsets of their destinations in a stage.
+    // Rows past M or N load the last row (in bounds; never stored).
+    const char* ga[A_IT];
+    uint32_t la[A_IT];
+#pragma unroll
+    for (int it = 0; it < A_IT; ++it) {
+        const int r0 = (it * 8 + wave) * 8, r = r0 + (lane >> 3), c = (lane & 7) ^ swz_a(r);
+        ga[it] = reinterpret_cast<const char*>(A + (size_t)min(m0 + r, M - 1) * K + c * 8);
+        la[it] = r0 * 128;
+    }
+    const char* gw[S::W_IT];
+    uint32_t lw[S::W_IT];
+#pragma unroll
+    for (int it = 0; it < S::W_IT; ++it) {
+        const int r0 = (it * 8 + wave) * 16, n = r0 + (lane >> 2), c = (lane & 3) ^ swz_w(n);
+        const int gn = min(n0 + n % BN, N - 1);
+        gw[it] = reinterpret_cast<const char*>((n / BN ? qb : qa) + (size_t)gn * K + c * 16);
+        lw[it] = r0 * 64;
+    }
+    const bool sload = wave < S::S_WAVES;
+    const char* gs = nullptr;
+    if (sload) {
+        const int n = wave * 64 + lane, gn = min(n0 + n % BN, N - 1);
+        gs = reinterpret_cast<const char*>((n / BN ? db : da) + (size_t)gn * (K / 32));
+    }
+    const uint32_t bA[3] = {lds_addr(A0), lds_addr(A1), lds_addr(A2)};
+    const uint32_t bW[3] = {lds_addr(W0), lds_addr(W1), lds_addr(W2)};
+    const uint32_t bS[3] = {lds_addr(S0), lds_addr(S1), lds_addr(S2)};
+    auto load = [&](int kt, int buf) {
+#pragma unroll
+        for (int it = 0; it < A_IT; ++it) dma16(ga[it] + (size_t)kt * 128, bA[buf] + la[it]);
+#pragma unroll
+        for (int it = 0; it < S::W_IT; ++it) dma16(gw[it] + (size_t)kt * 64, bW[buf] + lw[it]);
+        if (sload) dma4(gs + (size_t)kt * 4, bS[buf] + wave * 256);
+    };
+
+    f32x16 acc[NM][MI];
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+        for (int i = 0; i < MI; ++i) acc[m][i] = f32x16{};
+
+    auto compute = [&](const uint8_t* As, const uint8_t* Ws, const uint8_t* Ss) {
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {             // 32-element block p of the step
+            bf16x8 bfr[NM][2];
+#pragma unroll
+            for (int m = 0; m < NM; ++m) {
+                const int n = m * BN + wn * WN + l32, c = 2 * p + h;
+                const uint4 u = *reinterpret_cast<const uint4*>(Ws + n * 64 + 16 * (c ^ swz_w(n)));
+                const uint32_t s2 = *reinterpret_cast<const uint32_t*>(Ss + n * 4);
+                const float sc = __half2float(__ushort_as_half((unsigned short)(p ? s2 >> 16 : s2 & 0xFFFFu)));
+                const uint32_t w4[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+                for (int q = 0; q < 2; ++q)
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        bfr[m][q][e] = (__bf16)((float)(int8_t)(w4[2 * q + (e >> 2)] >> (8 * (e & 3))) * sc);
+            }
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                bf16x8 afr[MI];
+#pragma unroll
+                for (int i = 0; i < MI; ++i) {
+                    const int r = wm * WM + 32 * i + l32, c = 2 * (2 * p + h) + q;
+                    afr[i] = *reinterpret_cast<const bf16x8*>(As + r * 128 + 16 * (c ^ swz_a(r)));
+                }
+#pragma unroll
+                for (int m = 0; m < NM; ++m)
+#pragma unroll
+                    for (int i = 0; i < MI; ++i)
+                        acc[m][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(afr[i], bfr[m][q], acc[m][i], 0, 0, 0);
+            }
+        }
+    };
+
+    const int nk = K / 64;
+    load(0, 0);
+    if (nk > 1) load(1, 1);
+    // Unrolled by the ring size so each step names its buffers statically.
+    for (int kt = 0; kt < nk; kt += 3) {
+#define VH_LDS_STEP(KT, AS, WS, SS, NEXT)                                                     \
+        if (KT < nk) {                                                                     \
+            if (KT + 1 < nk) __builtin_amdgcn_s_waitcnt(S::WAIT);                          \
+            else __builtin_amdgcn_s_waitcnt(0);                                            \
+            __builtin_amdgcn_s_barrier();                                                  \
+            asm volatile("" ::: "memory");                                                 \
+            if (KT + 2 < nk) load(KT + 2, NEXT);                                           \
+            compute(AS, WS, SS);                                                           \
+        }
+        VH_LDS_STEP(kt, A0, W0, S0, 2)
+        VH_LDS_STEP(kt + 1, A1, W1, S1, 0)
+        VH_LDS_STEP(kt + 2, A2, W2, S2, 1)
+#undef VH_LDS_STEP
+    }
+
+    // Accumulator v of tile i holds row 32i + 8(v/4) + 4h + v%4, column l32 of the wave block.
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int row = m0 + wm * WM + 32 * i + 8 * (v >> 2) + 4 * h + (v & 3);
+            const int col = n0 + wn * WN + l32;
+            if (row < M && col < N) {
+                const size_t o = (size_t)row * N + col;
+                if constexpr (EPI >= 2) {
+                    const float g = acc[0][i][v], u = acc[NM - 1][i][v];
+                    const float hv = u * (g / (1.f + expf(-g)));   // silu(g) * u, ops.hpp:409-441
+                    if constexpr (EPI == 2) reinterpret_cast<uint16_t*>(out)[o] = (uint16_t)bf16_bits(hv);
+                    else reinterpret_cast<float*>(out)[o] = hv;
+                } else if constexpr (EPI == 1) {
+                    reinterpret_cast<float*>(out)[o] = acc[0][i][v] + residual[o];
+                } else {
+                    reinterpret_cast<float*>(out)[o] = acc[0][i][v];
+                }
+            }
+        }
+}
+
+template <int EPI>
+void launch_q8_lds(hipStream_t s, const uint16_t* a, const DevWeight& w0, const DevWeight* w1, int M,
+                   const float* residual, void* out) {
+    const dim3 grid((w0.N + lds_gemm::BN - 1) / lds_gemm::BN, (M + lds_gemm::BM - 1) / lds_gemm::BM);
+    if constexpr (EPI >= 2)   // SwiGLU: gate and up tiles together
+        hipLaunchKernelGGL((mfma_q8gemm_lds_kernel<2, EPI>), grid, dim3(lds_gemm::NT), 0, s, a, w0.q, w0.d, w1->q,
+                           w1->d, M, w0.N, w0.K, residual, out);
+    else
+        hipLaunchKernelGGL((mfma_q8gemm_lds_kernel<1, EPI>), grid, dim3(lds_gemm::NT), 0, s, a, w0.q, w0.d, w0.q,
+                           w0.d, M, w0.N, w0.K, residual, out);
 }
 
 // out[r][:] = bf16(w ? rmsnorm(x[r]) * w : x[r]), one 256-lane workgroup per row
@@ -522,7 +729,10 @@ int launch_qgemm(hipStream_t s, const DevWeight& w, const uint16_t* a, int M, co
     if (rc) return rc;
     VH_ARG(a && y, "qgemm: null operand");
     const int tiles = ((w.N + 127) / 128) * ((M + 255) / 256);
-    if (M <= 128) {
+    if (M > 128 && w.dtype == VLRF_DT_Q8_0) {
+        if (residual) launch_q8_lds<1>(s, a, w, nullptr, M, residual, y);
+        else launch_q8_lds<0>(s, a, w, nullptr, M, nullptr, y);
+    } else if (M <= 128) {
         if (residual) launch_cfg<CfgSmall, 1>(s, w.dtype, a, w, nullptr, M, residual, y);
         else launch_cfg<CfgSmall, 0>(s, w.dtype, a, w, nullptr, M, nullptr, y);
     } else if (tiles > kCUs && tiles <= 2 * kCUs) {
@@ -544,7 +754,10 @@ int launch_qgemm_swiglu(hipStream_t s, const DevWeight& wg, const DevWeight& wu,
     if (rc) return rc;
     VH_ARG(wg.N == wu.N && wg.K == wu.K && wg.dtype == wu.dtype, "qgemm_swiglu: gate/up differ");
     VH_ARG(a && h, "qgemm_swiglu: null operand");
-    if (M <= 128) {
+    if (M > 128 && wg.dtype == VLRF_DT_Q8_0) {
+        if (h_bf16) launch_q8_lds<2>(s, a, wg, &wu, M, nullptr, h);
+        else launch_q8_lds<3>(s, a, wg, &wu, M, nullptr, h);
+    } else if (M <= 128) {
         if (h_bf16) launch_cfg<CfgSmall, 2>(s, wg.dtype, a, wg, &wu, M, nullptr, h);
         else launch_cfg<CfgSmall, 3>(s, wg.dtype, a, wg, &wu, M, nullptr, h);
     } else {
