@@ -86,9 +86,14 @@ def _gqa_reference(orc, q, kq, vq, ks, vs, n_heads, n_kv, d, ctx_len, scale):
 
 @pytest.mark.parametrize("n_heads,n_kv,d,ctx_len", [(32, 4, 64, 4096), (32, 4, 64, 2048),
                                                     (8, 8, 64, 300), (16, 2, 128, 777),
-                                                    (8, 1, 64, 1)])
+                                                    (8, 1, 64, 1), (16, 8, 64, 509),
+                                                    (32, 8, 64, 65), (32, 4, 64, 510),
+                                                    (8, 2, 64, 4600)])
 def test_q8_decode_attention(ctx, orc, n_heads, n_kv, d, ctx_len):
-    """BASELINE config 2 (32q/4kv, d 64, ctx 4096) and other GQA groupings."""
+    """BASELINE config 2 (32q/4kv, d 64, ctx 4096) and other GQA groupings.
+    Caches of up to 512 rows at d_head 64 take the single-pass kernel (one
+    workgroup per query head; 509 + 3 rows fill every wave's round), larger
+    ones and d_head 128 the split-K kernel and its combine."""
     import vlrf_amd as V_
     print(f"[case] q8 decode heads={n_heads}/{n_kv} d={d} ctx={ctx_len}", flush=True)
     row = n_kv * d

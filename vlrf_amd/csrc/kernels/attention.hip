@@ -345,6 +345,252 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_partial_kernel(
     }
 }
 
+// ---- single-pass decode over a short Q8_0 cache (d_head 64, <= 512 rows) --------
+// One 512-lane workgroup per query head and no split partials: the combine
+// kernel's launch and its round trip through memory disappear.
+// Wave w takes the 64-token rounds r*8 + w; in a round lane t scores token
+// (r*8 + w)*64 + t against q (from LDS), the wave keeps its own online
+// softmax (m, l) with wave reductions, and accumulates P.V with lane
+// (tg, dg) = (lane/4, lane%4) owning dims 16dg..16dg+15 over tokens tg + 16j,
+// reading the V codes as 16-byte row pieces (each load a contiguous KiB) and
+// the row scales folded into p.  kSPDepth rounds of K/V are loaded up front
+// and each round's registers are refilled that many rounds ahead.  At the end the 16 lanes
+// of a dim group are summed with xor shuffles and the waves' (m, l, acc) are
+// merged in LDS with the log-sum-exp rule.  The fused form rotates and
+// quantizes the new token's row in every workgroup (identical results), stores
+// it from the group's first head, leaves the token at `pos` out of the rounds
+// (its cache row may not be written yet) and adds it to the final merge as one
+// more entry: score q.k_stored, weight 1, value the stored V row.
+// Measured on the MI355X (32q/4kv, d 64, stream launches): single pass 5.8 / 7.0 /
+// 8.6 / 11.9 us at ctx 64 / 512 / 1024 / 2048 against 6.9 / 7.7 / 7.8 / 8.1 us
+// for split-K + combine.  One workgroup's memory parallelism caps the single
+// pass beyond a few hundred tokens, so it takes caches of up to 512 rows.
+constexpr int kSPWaves = 8, kSPRounds = 1, kSPDepth = 1;   // rounds per wave, rounds in flight
+constexpr int kSPMaxCtx = kSPWaves * 64 * kSPRounds;   // cache rows the single pass covers
+
+template <int REP, bool FUSED>
+__global__ __launch_bounds__(64 * kSPWaves) void attn_decode_q8_single_kernel(
+    const float* __restrict__ q, const int8_t* kc, const int8_t* vc, const float* ks, const float* vs,
+    long head_stride, int ctx_len, const int* __restrict__ ctx_dev, float scale, float* __restrict__ out,
+    DecodeFuse fz) {
+    constexpr int D = 64, HALF = 32, NW = kSPWaves;
+    __shared__ __align__(16) float qs[D];
+    __shared__ __align__(16) float nk[D], nv[D];     // the new token's stored row of KV head g, read back
+    __shared__ __align__(16) float pbuf[NW][64];     // p * v row scale of the wave's current round
+    __shared__ float wm[NW], wl[NW];
+    __shared__ __align__(16) float wacc[NW][D];
+
+    const int h = blockIdx.x, g = h / REP;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int tg = lane >> 2, dg = lane & 3;
+    const int cap = (int)(head_stride / D);
+    const size_t hb = (size_t)g * head_stride;
+
+    // Loads first, all branch-free with rows clamped into the cache (masked at use):
+    // q, the new row (fused), two rounds of K/V, and only then the device position.
+    float q0 = 0.f, q1 = 0.f;
+    if (w == 0) {
+        const int j = lane & (HALF - 1);
+        q0 = q[(size_t)h * D + j];
+        q1 = q[(size_t)h * D + j + HALF];
+    }
+    constexpr int KP = 4, VP = 8;                   // new row: up to 512 elements (n_kv <= 8)
+    float k0[KP], k1[KP], vn[VP];
+    if (FUSED && w == 0) {
+        const int npairs = fz.n_kv * HALF, nrow = fz.n_kv * D;
+#pragma unroll
+        for (int p = 0; p < KP; ++p) {
+            const int i = min(lane + 64 * p, npairs - 1), hh = i / HALF, j = i - hh * HALF;
+            k0[p] = fz.k_new[hh * D + j];
+            k1[p] = fz.k_new[hh * D + j + HALF];
+        }
+#pragma unroll
+        for (int p = 0; p < VP; ++p) vn[p] = fz.v_new[min(lane + 64 * p, nrow - 1)];
+    }
+    // A round's K/V in registers: K row of token base+lane, V pieces of tokens base+tg+16j.
+    uint4 kr[kSPDepth][4], vr[kSPDepth][4];
+    float ksr[kSPDepth], vsr[kSPDepth];
+    auto load_round = [&](int r, int b) {
+        const int base = (r * NW + w) * 64;
+        const int t = min(base + lane, cap - 1);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) kr[b][i] = *reinterpret_cast<const uint4*>(kc + hb + (size_t)t * D + 16 * i);
+        ksr[b] = ks[t];
+        vsr[b] = vs[t];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int tv = min(base + tg + 16 * j, cap - 1);
+            vr[b][j] = *reinterpret_cast<const uint4*>(vc + hb + (size_t)tv * D + 16 * dg);
+        }
+    };
+#pragma unroll
+    for (int r = 0; r < kSPDepth; ++r) load_round(r, r);
+
+    const int dpos = ctx_dev ? *ctx_dev : 0;
+    int ctx = FUSED ? dpos + 1 : (ctx_dev ? dpos + ctx_len : ctx_len);
+    ctx = min(ctx, cap);
+    const int pos = FUSED ? dpos : -1;
+    const bool rot = FUSED && pos < fz.max_seq;      // rope.hpp:84: positions >= max_seq stay unrotated
+
+    // ---- wave 0: q of head h and (fused) the new K/V row ------------------------
+    if (w == 0) {
+        float rc = 1.f, rs = 0.f;
+        if constexpr (FUSED) {
+            const int trow = min(pos, fz.max_seq - 1);
+            rc = fz.cos_t[(size_t)trow * HALF + (lane & (HALF - 1))];
+            rs = fz.sin_t[(size_t)trow * HALF + (lane & (HALF - 1))];
+        }
+        if (lane < HALF) {
+            if (rot) rope2(q0, q1, rc, rs, &qs[lane], &qs[lane + HALF]);
+            else { qs[lane] = q0; qs[lane + HALF] = q1; }
+        }
+        if constexpr (FUSED) {
+            // attention.hpp:109-128: RoPE on k, then the Q8_0 row quantizer over the
+            // whole row (kv_cache.hpp:102-117) before attention reads it back.
+            const int npairs = fz.n_kv * HALF, nrow = fz.n_kv * D;
+            float ak = 0.f, av = 0.f;
+#pragma unroll
+            for (int p = 0; p < KP; ++p)
+                if (lane + 64 * p < npairs) {
+                    if (rot) rope2(k0[p], k1[p], rc, rs, &k0[p], &k1[p]);
+                    ak = fmaxf(ak, fmaxf(fabsf(k0[p]), fabsf(k1[p])));
+                }
+#pragma unroll
+            for (int p = 0; p < VP; ++p)
+                if (lane + 64 * p < nrow) av = fmaxf(av, fabsf(vn[p]));
+            ak = wave_max(ak);
+            av = wave_max(av);
+            const float sk = ak != 0.f ? ak / 127.f : 0.f, sv = av != 0.f ? av / 127.f : 0.f;
+            const float ik = ak != 0.f ? 1.f / sk : 0.f, iv = av != 0.f ? 1.f / sv : 0.f;
+            // the group's first head stores head g's codes (never past the cache)
+            const bool writer = h % REP == 0 && pos < cap;
+            int8_t* krow = fz.kq_w + hb + (size_t)pos * D;
+            int8_t* vrow = fz.vq_w + hb + (size_t)pos * D;
+#pragma unroll
+            for (int p = 0; p < KP; ++p) {
+                const int i = lane + 64 * p;
+                if (i < npairs && i / HALF == g) {
+                    const int j = i % HALF;
+                    const int c0 = ak != 0.f ? min(127, max(-127, (int)roundf(k0[p] * ik))) : 0;
+                    const int c1 = ak != 0.f ? min(127, max(-127, (int)roundf(k1[p] * ik))) : 0;
+                    if (writer) { krow[j] = (int8_t)c0; krow[j + HALF] = (int8_t)c1; }
+                    nk[j] = (float)c0 * sk;
+                    nk[j + HALF] = (float)c1 * sk;
+                }
+            }
+#pragma unroll
+            for (int p = 0; p < VP; ++p) {
+                const int i = lane + 64 * p;
+                if (i < nrow && i / D == g) {
+                    const int c = av != 0.f ? min(127, max(-127, (int)roundf(vn[p] * iv))) : 0;
+                    if (writer) vrow[i % D] = (int8_t)c;
+                    nv[i % D] = (float)c * sv;
+                }
+            }
+            if (h == 0 && lane == 0 && pos < cap) { fz.ks_w[pos] = sk; fz.vs_w[pos] = sv; }
+        }
+    }
+    __syncthreads();
+
+    // ---- rounds ----------------------------------------------------------------------
+    const int nrounds = (ctx + 63) / 64;
+    float m_run = kNegInf, l_run = 0.f, acc[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+#pragma unroll
+    for (int r = 0; r < kSPRounds; ++r) {
+        if (r * NW + w >= nrounds) break;
+        const int b = r % kSPDepth, base = (r * NW + w) * 64;
+        // scores: lane = token base + lane; the new token (fused) is merged at the end
+        const int t = base + lane;
+        float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+#pragma unroll
+        for (int i = 0; i < D / 4; ++i) {
+            const float4 qv = *reinterpret_cast<const float4*>(&qs[4 * i]);
+            const uint4 kw = kr[b][i >> 2];
+            const uint32_t u = (i & 3) == 0 ? kw.x : (i & 3) == 1 ? kw.y : (i & 3) == 2 ? kw.z : kw.w;
+            s0 += qv.x * (float)(int8_t)u;
+            s1 += qv.y * (float)(int8_t)(u >> 8);
+            s2 += qv.z * (float)(int8_t)(u >> 16);
+            s3 += qv.w * (float)(int8_t)(u >> 24);
+        }
+        const bool live = t < ctx && t != pos;
+        const float sc = live ? ((s0 + s1) + (s2 + s3)) * ksr[b] * scale : kNegInf;
+        const float mx = fmaxf(m_run, wave_max(sc));
+        const float corr = m_run == kNegInf ? 0.f : expf(m_run - mx);
+        const float pe = live ? expf(sc - mx) : 0.f;
+        l_run = l_run * corr + wave_sum(pe);
+        m_run = mx;
+        pbuf[w][lane] = pe * vsr[b];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // P.V: lane (tg, dg) over tokens tg + 16j of the round, dims 16dg..16dg+15
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[e] *= corr;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float pp = pbuf[w][tg + 16 * j];
+            const uint32_t u[4] = {vr[b][j].x, vr[b][j].y, vr[b][j].z, vr[b][j].w};
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[e] += pp * (float)(int8_t)(u[e >> 2] >> (8 * (e & 3)));
+        }
+        __builtin_amdgcn_wave_barrier();               // pbuf is rewritten next round
+        if (r + kSPDepth < kSPRounds && (r + kSPDepth) * NW + w < nrounds) load_round(r + kSPDepth, b);
+    }
+
+    // ---- merge: lanes of a dim group, then the waves -------------------------------
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        float v = acc[e];
+        v += __shfl_xor(v, 4);
+        v += __shfl_xor(v, 8);
+        v += __shfl_xor(v, 16);
+        v += __shfl_xor(v, 32);   // lanes tg = 0..15 of dim group dg
+        acc[e] = v;
+    }
+    if (tg == 0) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) wacc[w][16 * dg + e] = acc[e];
+    }
+    if (lane == 0) { wm[w] = m_run; wl[w] = l_run; }
+    __syncthreads();
+    if (tid < D) {
+        // The new token (fused): score q . k_stored, weight 1, value its stored V row.
+        float sn = kNegInf;
+        if constexpr (FUSED) {
+            float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+#pragma unroll
+            for (int i = 0; i < D / 4; ++i) {
+                const float4 qv = *reinterpret_cast<const float4*>(&qs[4 * i]);
+                const float4 kv = *reinterpret_cast<const float4*>(&nk[4 * i]);
+                a0 += qv.x * kv.x;
+                a1 += qv.y * kv.y;
+                a2 += qv.z * kv.z;
+                a3 += qv.w * kv.w;
+            }
+            sn = ((a0 + a1) + (a2 + a3)) * scale;
+        }
+        float mt = sn;
+#pragma unroll
+        for (int k = 0; k < NW; ++k) mt = fmaxf(mt, wm[k]);
+        float lt = 0.f, ot = 0.f;
+        if (FUSED) {
+            lt = expf(sn - mt);
+            ot = lt * nv[tid];
+        }
+#pragma unroll
+        for (int k = 0; k < NW; ++k) {
+            if (wm[k] != kNegInf) {
+                const float c = expf(wm[k] - mt);
+                lt += c * wl[k];
+                ot += c * wacc[k][tid];
+            }
+        }
+        out[(size_t)h * D + tid] = lt > 0.f ? ot * (1.f / lt) : 0.f;
+    }
+}
+
 // Log-sum-exp merge of the per-chunk partials of one query head.  The 256
 // threads form G = 256/D groups of D lanes (one lane per dimension); group gi
 // merges splits gi, gi+G, ... in passes of B splits whose loads are all issued
@@ -770,6 +1016,24 @@ int launch_attn_decode(hipStream_t s, const float* q, const void* kc, const void
     }
     const int8_t* k8 = static_cast<const int8_t*>(kc);
     const int8_t* v8 = static_cast<const int8_t*>(vc);
+    if (kv_dtype == VLRF_KV_Q8_0 && d_head == 64 && head_stride / d_head <= kSPMaxCtx && n_kv <= 8) {
+#define VH_SP(R, FU)                                                                                       \
+    hipLaunchKernelGGL((attn_decode_q8_single_kernel<R, FU>), dim3(n_heads), dim3(64 * kSPWaves), 0, s, q, k8, v8, ks, \
+                       vs, head_stride, ctx_len, ctx_dev, scale, out, fz)
+#define VH_SP_R(FU)                           \
+    switch (rep) {                            \
+        case 1: VH_SP(1, FU); break;          \
+        case 2: VH_SP(2, FU); break;          \
+        case 4: VH_SP(4, FU); break;          \
+        default: VH_SP(8, FU); break;         \
+    }
+        if (fuse) { VH_SP_R(true) }
+        else { VH_SP_R(false) }
+#undef VH_SP_R
+#undef VH_SP
+        VH_LAUNCHED();
+        return VLRF_HIP_OK;
+    }
     dim3 grid(n_splits, n_kv), block(kAttnThreads);
 #define VH_AD(D, R, T, FU)                                                                          \
     hipLaunchKernelGGL((attn_decode_partial_kernel<D, R, T, FU>), grid, block, 0, s, q, k8, v8, ks,  \
