@@ -22,8 +22,9 @@ def _weight(ctx, seed, name, N, K, dtype):
 
 
 @pytest.mark.parametrize("dtype", [V.DT_Q8_0, V.DT_Q4_0])
-# Tile selection: M <= 128 -> 128-row tiles; 257..512 tiles of 256x128 -> the two-per-CU
-# configuration (520 x 16600: 390 tiles); otherwise 256x128 tiles, one per CU.
+# Kernel selection: M <= 128 -> 128-row register-staged tiles; Q8_0 with M > 128 -> the
+# direct-to-LDS kernel (256x128 tiles); Q4_0 with M > 128 -> the register-staged 256x128
+# tiles (two per CU for 257..512 tiles, as 520 x 16600's 390).
 @pytest.mark.parametrize("M,N,K", [(256, 6144, 4096), (128, 4096, 14336), (2048, 1024, 4096),
                                    (520, 16600, 64)])
 def test_prefill_gemm_config5_shapes(ctx, orc, dtype, M, N, K):
@@ -38,7 +39,7 @@ def test_prefill_gemm_config5_shapes(ctx, orc, dtype, M, N, K):
 
 
 @pytest.mark.parametrize("M,N,K", [(17, 37, 64), (200, 300, 128), (129, 130, 704), (300, 256, 2048),
-                                   (1000, 8300, 192)])
+                                   (1000, 8300, 192), (300, 100, 256), (129, 37, 64)])
 def test_prefill_gemm_ragged_with_norm_and_residual(ctx, orc, M, N, K):
     """Row/column counts off the 128x128 tile, with the fused RMSNorm prologue
     and the residual epilogue (in place on the residual)."""
@@ -63,6 +64,23 @@ def test_prefill_swiglu(ctx, orc, dtype, M):
     wu, udec = _weight(ctx, 23, "PWu", Fd, K, dtype)
     x = F.normal(23, "psx", M * K).reshape(M, K)
     g = np.ones(K, np.float32)
+    dx, dg, dh = ctx.to_device(x), ctx.to_device(g), ctx.alloc(M * Fd * 4)
+    ctx.qlinear_swiglu(wg, wu, dx, dh, M, norm_w=dg, eps=1e-5)
+    xn = orc.rms_norm(x, g, 1e-5)
+    ref = orc.silu_mul(orc.linear(xn, udec), orc.linear(xn, gdec))
+    assert rel_err(dh.download((M, Fd)), ref) <= TOL
+
+
+@pytest.mark.parametrize("dtype", [V.DT_Q8_0, V.DT_Q4_0])
+@pytest.mark.parametrize("M,Fd,K", [(257, 1000, 192), (300, 100, 64)])
+def test_prefill_swiglu_ragged(ctx, orc, dtype, M, Fd, K):
+    """SwiGLU with the FFN width and the row count off the 256x128 tile (the
+    gate and up tiles of the direct-to-LDS kernel share one workgroup)."""
+    print(f"[case] swiglu ragged dtype={dtype} M={M} F={Fd} K={K}", flush=True)
+    wg, gdec = _weight(ctx, 24, f"RWg{Fd}x{K}", Fd, K, dtype)
+    wu, udec = _weight(ctx, 24, f"RWu{Fd}x{K}", Fd, K, dtype)
+    x = F.normal(24, f"rsx{M}x{K}", M * K).reshape(M, K)
+    g = 1.0 + F.normal(24, f"rsg{K}", K, 0.1)
     dx, dg, dh = ctx.to_device(x), ctx.to_device(g), ctx.alloc(M * Fd * 4)
     ctx.qlinear_swiglu(wg, wu, dx, dh, M, norm_w=dg, eps=1e-5)
     xn = orc.rms_norm(x, g, 1e-5)
