@@ -53,8 +53,11 @@ def test_append_matches_reference_conversion(ctx, orc, dtype, n_kv, d, T):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("n_heads,n_kv,d,ctx_len", [(32, 4, 64, 2048), (16, 2, 128, 777), (8, 1, 64, 1)])
+@pytest.mark.parametrize("n_heads,n_kv,d,ctx_len", [(32, 4, 64, 2048), (16, 2, 128, 777), (8, 1, 64, 1),
+                                                    (16, 4, 64, 500)])
 def test_decode_attention(ctx, orc, dtype, n_heads, n_kv, d, ctx_len):
+    """Split-K (2048 and 777 tokens) and the single-pass kernel (caches of <= 512
+    rows: 1 and 500 tokens) over the F32 / F16 cache."""
     print(f"[case] decode attention dtype={dtype} heads={n_heads}/{n_kv} d={d} ctx={ctx_len}", flush=True)
     row = n_kv * d
     kv = V.KVCache(ctx, 1, ctx_len + 3, n_kv, d, dtype)

@@ -345,38 +345,62 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_partial_kernel(
     }
 }
 
-// ---- single-pass decode over a short Q8_0 cache (d_head 64, <= 512 rows) --------
+// ---- single-pass decode over a short cache (d_head 64, <= 512 rows) -------------
 // One 512-lane workgroup per query head and no split partials: the combine
 // kernel's launch and its round trip through memory disappear.
 // Wave w takes the 64-token rounds r*8 + w; in a round lane t scores token
 // (r*8 + w)*64 + t against q (from LDS), the wave keeps its own online
 // softmax (m, l) with wave reductions, and accumulates P.V with lane
 // (tg, dg) = (lane/4, lane%4) owning dims 16dg..16dg+15 over tokens tg + 16j,
-// reading the V codes as 16-byte row pieces (each load a contiguous KiB) and
-// the row scales folded into p.  kSPDepth rounds of K/V are loaded up front
-// and each round's registers are refilled that many rounds ahead.  At the end the 16 lanes
-// of a dim group are summed with xor shuffles and the waves' (m, l, acc) are
-// merged in LDS with the log-sum-exp rule.  The fused form rotates and
-// quantizes the new token's row in every workgroup (identical results), stores
-// it from the group's first head, leaves the token at `pos` out of the rounds
-// (its cache row may not be written yet) and adds it to the final merge as one
-// more entry: score q.k_stored, weight 1, value the stored V row.
-// Measured on the MI355X (32q/4kv, d 64, stream launches): single pass 5.8 / 7.0 /
-// 8.6 / 11.9 us at ctx 64 / 512 / 1024 / 2048 against 6.9 / 7.7 / 7.8 / 8.1 us
-// for split-K + combine.  One workgroup's memory parallelism caps the single
-// pass beyond a few hundred tokens, so it takes caches of up to 512 rows.
+// reading the V elements as 16-element row pieces (each load a contiguous run)
+// and the Q8_0 row scales folded into p.  kSPDepth rounds of K/V are loaded up
+// front and each round's registers are refilled that many rounds ahead.  At
+// the end the 16 lanes of a dim group are summed with xor shuffles and the
+// waves' (m, l, acc) are merged in LDS with the log-sum-exp rule.  The fused
+// form rotates and stores the new token's row in every workgroup (identical
+// results; the group's first head writes it), leaves the token at `pos` out
+// of the rounds (its cache row may not be written yet) and adds it to the
+// final merge as one more entry: score q.k_stored, weight 1, value the stored
+// V row.  KVT: VLRF_KV_Q8_0 codes + row scales, VLRF_KV_F16 bits, VLRF_KV_F32.
+// Measured on the MI355X (32q/4kv Q8_0, d 64, stream launches): single pass
+// 5.8 / 7.0 / 8.6 / 11.9 us at ctx 64 / 512 / 1024 / 2048 against 6.9 / 7.7 /
+// 7.8 / 8.1 us for split-K + combine.  One workgroup's memory parallelism caps
+// the single pass beyond a few hundred tokens, so it takes caches of up to 512
+// rows.
 constexpr int kSPWaves = 8, kSPRounds = 1, kSPDepth = 1;   // rounds per wave, rounds in flight
 constexpr int kSPMaxCtx = kSPWaves * 64 * kSPRounds;   // cache rows the single pass covers
 
-template <int REP, bool FUSED>
-__global__ __launch_bounds__(64 * kSPWaves) void attn_decode_q8_single_kernel(
+// Elements 4i..4i+3 of a 64-element row held as 16-byte words, as f32.
+template <int KVT>
+__device__ __forceinline__ float4 row4(const uint4* wds, int i) {
+    if constexpr (KVT == VLRF_KV_Q8_0) {
+        const uint4 k = wds[i >> 2];
+        const uint32_t u = (i & 3) == 0 ? k.x : (i & 3) == 1 ? k.y : (i & 3) == 2 ? k.z : k.w;
+        return make_float4((float)(int8_t)u, (float)(int8_t)(u >> 8), (float)(int8_t)(u >> 16),
+                           (float)(int8_t)(u >> 24));
+    } else if constexpr (KVT == VLRF_KV_F16) {
+        const uint4 k = wds[i >> 1];
+        const uint32_t a = (i & 1) ? k.z : k.x, b = (i & 1) ? k.w : k.y;
+        return make_float4(f16_bits_to_f32(a & 0xFFFFu), f16_bits_to_f32(a >> 16), f16_bits_to_f32(b & 0xFFFFu),
+                           f16_bits_to_f32(b >> 16));
+    } else {
+        const uint4 k = wds[i];
+        return make_float4(__uint_as_float(k.x), __uint_as_float(k.y), __uint_as_float(k.z), __uint_as_float(k.w));
+    }
+}
+
+template <int KVT, int REP, bool FUSED>
+__global__ __launch_bounds__(64 * kSPWaves) void attn_decode_single_kernel(
     const float* __restrict__ q, const int8_t* kc, const int8_t* vc, const float* ks, const float* vs,
     long head_stride, int ctx_len, const int* __restrict__ ctx_dev, float scale, float* __restrict__ out,
     DecodeFuse fz) {
+    constexpr bool Q8 = KVT == VLRF_KV_Q8_0, H16 = KVT == VLRF_KV_F16;
     constexpr int D = 64, HALF = 32, NW = kSPWaves;
+    constexpr int EB = Q8 ? 1 : H16 ? 2 : 4;         // bytes per element
+    constexpr int KW = D * EB / 16, VW = EB;         // 16-byte words: a K row, a 16-element V piece
     __shared__ __align__(16) float qs[D];
     __shared__ __align__(16) float nk[D], nv[D];     // the new token's stored row of KV head g, read back
-    __shared__ __align__(16) float pbuf[NW][64];     // p * v row scale of the wave's current round
+    __shared__ __align__(16) float pbuf[NW][64];     // p (times the V row scale) of the wave's current round
     __shared__ float wm[NW], wl[NW];
     __shared__ __align__(16) float wacc[NW][D];
 
@@ -387,7 +411,7 @@ __global__ __launch_bounds__(64 * kSPWaves) void attn_decode_q8_single_kernel(
     const size_t hb = (size_t)g * head_stride;
 
     // Loads first, all branch-free with rows clamped into the cache (masked at use):
-    // q, the new row (fused), two rounds of K/V, and only then the device position.
+    // q, the new row (fused), the rounds' K/V, and only then the device position.
     float q0 = 0.f, q1 = 0.f;
     if (w == 0) {
         const int j = lane & (HALF - 1);
@@ -408,19 +432,22 @@ __global__ __launch_bounds__(64 * kSPWaves) void attn_decode_q8_single_kernel(
         for (int p = 0; p < VP; ++p) vn[p] = fz.v_new[min(lane + 64 * p, nrow - 1)];
     }
     // A round's K/V in registers: K row of token base+lane, V pieces of tokens base+tg+16j.
-    uint4 kr[kSPDepth][4], vr[kSPDepth][4];
+    uint4 kr[kSPDepth][KW], vr[kSPDepth][4][VW];
     float ksr[kSPDepth], vsr[kSPDepth];
     auto load_round = [&](int r, int b) {
         const int base = (r * NW + w) * 64;
         const int t = min(base + lane, cap - 1);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) kr[b][i] = *reinterpret_cast<const uint4*>(kc + hb + (size_t)t * D + 16 * i);
-        ksr[b] = ks[t];
-        vsr[b] = vs[t];
+        for (int i = 0; i < KW; ++i)
+            kr[b][i] = *reinterpret_cast<const uint4*>(kc + (hb + (size_t)t * D) * EB + 16 * i);
+        ksr[b] = Q8 ? ks[t] : 1.f;
+        vsr[b] = Q8 ? vs[t] : 1.f;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int tv = min(base + tg + 16 * j, cap - 1);
-            vr[b][j] = *reinterpret_cast<const uint4*>(vc + hb + (size_t)tv * D + 16 * dg);
+#pragma unroll
+            for (int i = 0; i < VW; ++i)
+                vr[b][j][i] = *reinterpret_cast<const uint4*>(vc + (hb + (size_t)tv * D + 16 * dg) * EB + 16 * i);
         }
     };
 #pragma unroll
@@ -445,8 +472,9 @@ __global__ __launch_bounds__(64 * kSPWaves) void attn_decode_q8_single_kernel(
             else { qs[lane] = q0; qs[lane + HALF] = q1; }
         }
         if constexpr (FUSED) {
-            // attention.hpp:109-128: RoPE on k, then the Q8_0 row quantizer over the
-            // whole row (kv_cache.hpp:102-117) before attention reads it back.
+            // attention.hpp:109-128: RoPE on k, then KVCache::append stores the row
+            // before attention reads it back: Q8_0 quantizes the whole row
+            // (kv_cache.hpp:102-117), F16 converts each element (:68-97), F32 copies.
             const int npairs = fz.n_kv * HALF, nrow = fz.n_kv * D;
             float ak = 0.f, av = 0.f;
 #pragma unroll
@@ -455,39 +483,54 @@ __global__ __launch_bounds__(64 * kSPWaves) void attn_decode_q8_single_kernel(
                     if (rot) rope2(k0[p], k1[p], rc, rs, &k0[p], &k1[p]);
                     ak = fmaxf(ak, fmaxf(fabsf(k0[p]), fabsf(k1[p])));
                 }
+            float sk = 1.f, sv = 1.f, ik = 0.f, iv = 0.f;
+            if constexpr (Q8) {
 #pragma unroll
-            for (int p = 0; p < VP; ++p)
-                if (lane + 64 * p < nrow) av = fmaxf(av, fabsf(vn[p]));
-            ak = wave_max(ak);
-            av = wave_max(av);
-            const float sk = ak != 0.f ? ak / 127.f : 0.f, sv = av != 0.f ? av / 127.f : 0.f;
-            const float ik = ak != 0.f ? 1.f / sk : 0.f, iv = av != 0.f ? 1.f / sv : 0.f;
-            // the group's first head stores head g's codes (never past the cache)
+                for (int p = 0; p < VP; ++p)
+                    if (lane + 64 * p < nrow) av = fmaxf(av, fabsf(vn[p]));
+                ak = wave_max(ak);
+                av = wave_max(av);
+                sk = ak != 0.f ? ak / 127.f : 0.f;
+                sv = av != 0.f ? av / 127.f : 0.f;
+                ik = ak != 0.f ? 1.f / sk : 0.f;
+                iv = av != 0.f ? 1.f / sv : 0.f;
+            }
+            // the group's first head stores head g's elements (never past the cache)
             const bool writer = h % REP == 0 && pos < cap;
-            int8_t* krow = fz.kq_w + hb + (size_t)pos * D;
-            int8_t* vrow = fz.vq_w + hb + (size_t)pos * D;
+            int8_t* krow = fz.kq_w + (hb + (size_t)pos * D) * EB;
+            int8_t* vrow = fz.vq_w + (hb + (size_t)pos * D) * EB;
+            // stores element j of a row (when writer) and returns the value attention reads back
+            auto put = [&](int8_t* row, int j, float x, float sc, float inv, bool nz) -> float {
+                if constexpr (Q8) {
+                    const int c = nz ? min(127, max(-127, (int)roundf(x * inv))) : 0;
+                    if (writer) row[j] = (int8_t)c;
+                    return (float)c * sc;
+                } else if constexpr (H16) {
+                    const uint16_t hb16 = f32_to_f16_kv(x);
+                    if (writer) reinterpret_cast<uint16_t*>(row)[j] = hb16;
+                    return f16_bits_to_f32(hb16);
+                } else {
+                    if (writer) reinterpret_cast<float*>(row)[j] = x;
+                    return x;
+                }
+            };
 #pragma unroll
             for (int p = 0; p < KP; ++p) {
                 const int i = lane + 64 * p;
                 if (i < npairs && i / HALF == g) {
                     const int j = i % HALF;
-                    const int c0 = ak != 0.f ? min(127, max(-127, (int)roundf(k0[p] * ik))) : 0;
-                    const int c1 = ak != 0.f ? min(127, max(-127, (int)roundf(k1[p] * ik))) : 0;
-                    if (writer) { krow[j] = (int8_t)c0; krow[j + HALF] = (int8_t)c1; }
-                    nk[j] = (float)c0 * sk;
-                    nk[j + HALF] = (float)c1 * sk;
+                    nk[j] = put(krow, j, k0[p], sk, ik, ak != 0.f);
+                    nk[j + HALF] = put(krow, j + HALF, k1[p], sk, ik, ak != 0.f);
                 }
             }
 #pragma unroll
             for (int p = 0; p < VP; ++p) {
                 const int i = lane + 64 * p;
-                if (i < nrow && i / D == g) {
-                    const int c = av != 0.f ? min(127, max(-127, (int)roundf(vn[p] * iv))) : 0;
-                    if (writer) vrow[i % D] = (int8_t)c;
-                    nv[i % D] = (float)c * sv;
-                }
+                if (i < nrow && i / D == g) nv[i % D] = put(vrow, i % D, vn[p], sv, iv, av != 0.f);
             }
-            if (h == 0 && lane == 0 && pos < cap) { fz.ks_w[pos] = sk; fz.vs_w[pos] = sv; }
+            if constexpr (Q8) {
+                if (h == 0 && lane == 0 && pos < cap) { fz.ks_w[pos] = sk; fz.vs_w[pos] = sv; }
+            }
         }
     }
     __syncthreads();
@@ -507,12 +550,11 @@ __global__ __launch_bounds__(64 * kSPWaves) void attn_decode_q8_single_kernel(
 #pragma unroll
         for (int i = 0; i < D / 4; ++i) {
             const float4 qv = *reinterpret_cast<const float4*>(&qs[4 * i]);
-            const uint4 kw = kr[b][i >> 2];
-            const uint32_t u = (i & 3) == 0 ? kw.x : (i & 3) == 1 ? kw.y : (i & 3) == 2 ? kw.z : kw.w;
-            s0 += qv.x * (float)(int8_t)u;
-            s1 += qv.y * (float)(int8_t)(u >> 8);
-            s2 += qv.z * (float)(int8_t)(u >> 16);
-            s3 += qv.w * (float)(int8_t)(u >> 24);
+            const float4 kf = row4<KVT>(kr[b], i);
+            s0 += qv.x * kf.x;
+            s1 += qv.y * kf.y;
+            s2 += qv.z * kf.z;
+            s3 += qv.w * kf.w;
         }
         const bool live = t < ctx && t != pos;
         const float sc = live ? ((s0 + s1) + (s2 + s3)) * ksr[b] * scale : kNegInf;
@@ -531,9 +573,14 @@ __global__ __launch_bounds__(64 * kSPWaves) void attn_decode_q8_single_kernel(
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const float pp = pbuf[w][tg + 16 * j];
-            const uint32_t u[4] = {vr[b][j].x, vr[b][j].y, vr[b][j].z, vr[b][j].w};
 #pragma unroll
-            for (int e = 0; e < 16; ++e) acc[e] += pp * (float)(int8_t)(u[e >> 2] >> (8 * (e & 3)));
+            for (int i = 0; i < 4; ++i) {
+                const float4 v4 = row4<KVT>(vr[b][j], i);
+                acc[4 * i] += pp * v4.x;
+                acc[4 * i + 1] += pp * v4.y;
+                acc[4 * i + 2] += pp * v4.z;
+                acc[4 * i + 3] += pp * v4.w;
+            }
         }
         __builtin_amdgcn_wave_barrier();               // pbuf is rewritten next round
         if (r + kSPDepth < kSPRounds && (r + kSPDepth) * NW + w < nrounds) load_round(r + kSPDepth, b);
@@ -1016,19 +1063,26 @@ int launch_attn_decode(hipStream_t s, const float* q, const void* kc, const void
     }
     const int8_t* k8 = static_cast<const int8_t*>(kc);
     const int8_t* v8 = static_cast<const int8_t*>(vc);
-    if (kv_dtype == VLRF_KV_Q8_0 && d_head == 64 && head_stride / d_head <= kSPMaxCtx && n_kv <= 8) {
-#define VH_SP(R, FU)                                                                                       \
-    hipLaunchKernelGGL((attn_decode_q8_single_kernel<R, FU>), dim3(n_heads), dim3(64 * kSPWaves), 0, s, q, k8, v8, ks, \
-                       vs, head_stride, ctx_len, ctx_dev, scale, out, fz)
-#define VH_SP_R(FU)                           \
+    if (d_head == 64 && head_stride / d_head <= kSPMaxCtx && (!fuse || n_kv <= 8)) {
+#define VH_SP(KT, R, FU)                                                                                     \
+    hipLaunchKernelGGL((attn_decode_single_kernel<KT, R, FU>), dim3(n_heads), dim3(64 * kSPWaves), 0, s, q, k8, \
+                       v8, ks, vs, head_stride, ctx_len, ctx_dev, scale, out, fz)
+#define VH_SP_R(KT, FU)                       \
     switch (rep) {                            \
-        case 1: VH_SP(1, FU); break;          \
-        case 2: VH_SP(2, FU); break;          \
-        case 4: VH_SP(4, FU); break;          \
-        default: VH_SP(8, FU); break;         \
+        case 1: VH_SP(KT, 1, FU); break;      \
+        case 2: VH_SP(KT, 2, FU); break;      \
+        case 4: VH_SP(KT, 4, FU); break;      \
+        default: VH_SP(KT, 8, FU); break;     \
     }
-        if (fuse) { VH_SP_R(true) }
-        else { VH_SP_R(false) }
+#define VH_SP_T(FU)                                                 \
+    switch (kv_dtype) {                                             \
+        case VLRF_KV_Q8_0: VH_SP_R(VLRF_KV_Q8_0, FU) break;         \
+        case VLRF_KV_F16: VH_SP_R(VLRF_KV_F16, FU) break;           \
+        default: VH_SP_R(VLRF_KV_F32, FU) break;                    \
+    }
+        if (fuse) { VH_SP_T(true) }
+        else { VH_SP_T(false) }
+#undef VH_SP_T
 #undef VH_SP_R
 #undef VH_SP
         VH_LAUNCHED();
