@@ -6,7 +6,8 @@
 //
 // 1. Prefill GEMM (M > 16 rows).  The reference computes in f32; this path
 // rounds the activations and the decoded weights to bf16 and accumulates in
-// f32 (the 1e-2 tolerance class of bf16 paths).  C[M,N] = A[M,K] . W[N,K]^T
+// f32 (the 1e-2 tolerance class of bf16 paths).  For 17 <= M <= 128,
+// mfma_qgemm_kernel:  C[M,N] = A[M,K] . W[N,K]^T
 // with A in bf16 and W as split GGUF blocks (codes [N][K], f16 scales
 // [N][K/32]).  A workgroup owns a BM x BN tile of C, each wave a block of
 // v_mfma_f32_32x32x16_bf16 tiles.  K advances in steps of BK: the next step's
@@ -16,7 +17,7 @@
 // tile column as 1.06 B (Q8_0) or 0.56 B (Q4_0) per weight.  LDS rows are
 // padded by 16 bytes so the lanes of an operand read hit distinct banks.
 // Epilogues: store f32, add a residual, or SwiGLU (two weights, silu(g)*u).
-// Q8_0 weights with M > 128 take mfma_q8gemm_lds_kernel instead (below): the
+// Weights with M > 128 take mfma_qgemm_lds_kernel instead (below): the
 // same arithmetic with operands brought into a 3-stage LDS ring by
 // direct-to-LDS loads and codes decoded in registers next to the MFMAs.
 //
@@ -227,19 +228,11 @@ __global__ __launch_bounds__(C::NT) void mfma_qgemm_kernel(
             }
 }
 
-// Tile configurations, chosen by measurement at the 8B-layer shapes (M = 2048):
-//   CfgWide  256x128x64, 16 waves: one workgroup per CU (108 KB LDS); O and down.
-//   CfgFill  256x128x32, 8 waves: two per CU (60 KB), for grids of 257..512 tiles
-//            that would leave half the CUs idle in a second round (QKV, N = 6144).
-//   CfgSwi   256x128x64, 8 waves, gate and up tiles together (144 KB).
-//   CfgSmall 128x128x64, 4 waves: M <= 128, where 256-row tiles are mostly padding.
-// Every configuration steps K by at most 64, so K % 64 == 0 covers them all.
-using CfgWide = TileCfg<256, 128, 64, 4, 4>;
-using CfgFill = TileCfg<256, 128, 32, 4, 2>;
-using CfgSwi = TileCfg<256, 128, 64, 4, 2>;
+// The register-staged configuration for 17 <= M <= 128 (128-row tiles, where
+// the direct-to-LDS kernel's 256-row tiles would be mostly padding): 128x128x64,
+// 4 waves.  Both prefill kernels step K by 64, so K % 64 == 0 covers them.
 using CfgSmall = TileCfg<128, 128, 64, 2, 2>;
 constexpr int kBK = 64;
-constexpr int kCUs = 256;
 
 template <class C, int EPI>
 void launch_cfg(hipStream_t s, int wt, const uint16_t* a, const DevWeight& w0, const DevWeight* w1, int M,
@@ -255,40 +248,45 @@ void launch_cfg(hipStream_t s, int wt, const uint16_t* a, const DevWeight& w0, c
                            M, w0.N, w0.K, residual, out);
 }
 
-// ---- Q8_0 prefill GEMM with direct-to-LDS loads --------------------------------
-// C[M,N] = A[M,K] . W[N,K]^T for Q8_0 W and M > 128: workgroup tile 256 x 128
+// ---- prefill GEMM with direct-to-LDS loads ---------------------------------------
+// C[M,N] = A[M,K] . W[N,K]^T for Q8_0/Q4_0 W and M > 128: workgroup tile 256 x 128
 // (per weight matrix; SwiGLU computes gate and up tiles together), 8 waves as
 // 2 along M x 4 along N, so each wave owns a 128 x 32 block per matrix (four
 // 32x32 MFMA tiles) and each weight code is decoded by only two waves.
 // K advances in steps of 64 through a 3-stage LDS ring filled by
 // global_load_lds_dwordx4 (the loads write LDS without passing through
 // registers): stage = A rows as bf16 (32 KB), the raw codes of the tile's weight
-// rows (8 KB per matrix) and their two f16 block scales.  16-byte chunks are
-// XOR-swizzled within a row (A: chunk ^ ((row >> 1) & 7); codes:
-// chunk ^ ((row >> 2) & 3)) so the MFMA operand reads of 16 consecutive rows hit
-// distinct banks; the loads realise the swizzle by choosing which global chunk
+// rows (8 KB per matrix for Q8_0, 4 KB for Q4_0) and their two f16 block
+// scales.  16-byte chunks are XOR-swizzled within a row (A: chunk ^
+// ((row >> 1) & 7); Q8_0 codes: chunk ^ ((row >> 2) & 3); Q4_0: chunk ^
+// ((row >> 3) & 1)) so the MFMA operand reads of consecutive rows spread over
+// the banks; the loads realise the swizzle by choosing which global chunk
 // each lane fetches (lane l always writes LDS bytes 16l..16l+15 of its wave's
 // 1 KB destination).  One barrier per K step: wait until this wave's loads of
 // the step have landed, barrier, issue the loads of step k+2 into the buffer
 // step k-1 used, compute step k.  The MFMA k order within a 32-element block
-// is permuted (lane half h takes code chunk 2p+h, slices q = 0, 1 its two 8-byte
-// halves; A uses the same permutation), so a lane reads 16 code bytes at once;
-// codes are decoded in registers (code * scale rounded to bf16) just before use.
+// is permuted (lane half h takes elements 16h..16h+15 of block p -- Q8_0 code
+// chunk 2p+h, Q4_0 bytes 8h..8h+7 of chunk p -- and slices q = 0, 1 their two
+// halves; A uses the same permutation), so a lane reads its codes in one LDS
+// read; codes are decoded in registers (code * scale rounded to bf16) just
+// before use.
 namespace lds_gemm {
 
 constexpr int BM = 256, BN = 128, NT = 512, WM = 128, WN = 32, MI = WM / 32;
 constexpr int A_B = BM * 128;                 // one K step of A: 256 rows x 64 bf16
 constexpr int A_IT = A_B / (NT * 16);         // 16-byte loads per thread
-template <int NM> struct Stage {
-    static constexpr int W_B = NM * BN * 64;  // codes: NM*BN rows x 64 bytes
+template <int WT, int NM> struct Stage {
+    static constexpr int CB = WT == VLRF_DT_Q8_0 ? 64 : 32;   // code bytes of a row per K step
+    static constexpr int W_B = NM * BN * CB;  // codes: NM*BN rows
     static constexpr int S_B = NM * BN * 4;   // two f16 block scales per row
-    static constexpr int W_IT = W_B / (NT * 16);
+    static constexpr int W_TI = W_B / 1024;   // 1 KB code loads per step (wave w issues w, w+8, ...)
+    static constexpr int W_IT = (W_TI + 7) / 8;
     static constexpr int S_WAVES = NM * BN / 64;
-    // Loads of one step by a wave that issues no scale load: waiting until at most
-    // this many are outstanding leaves only the newer step in flight for every wave.
-    static constexpr int LPS = A_IT + W_IT;
+    // Loads of one step by the wave that issues fewest: waiting until at most this
+    // many are outstanding leaves only the newer step in flight for every wave.
+    static constexpr int LPS = A_IT + W_TI / 8 + (S_WAVES >= 8 ? 1 : 0);
     static constexpr int WAIT = (LPS & 15) | (7 << 4) | (15 << 8) | ((LPS >> 4) << 14);   // s_waitcnt vmcnt(LPS)
-    static_assert(W_IT >= 1 && S_WAVES <= 8, "stage shape");
+    static_assert(W_TI >= 1 && S_WAVES <= 8, "stage shape");
 };
 
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
@@ -309,17 +307,21 @@ __device__ __forceinline__ void dma4(const void* g, uint32_t base) {
                  :: "v"(g), "s"(__builtin_amdgcn_readfirstlane(base)) : "memory", "m0");
 }
 __device__ __forceinline__ int swz_a(int r) { return (r >> 1) & 7; }
-__device__ __forceinline__ int swz_w(int n) { return (n >> 2) & 3; }
+// code chunk swizzle within a row: Q8_0 rows of 4 chunks, Q4_0 rows of 2
+template <int WT> __device__ __forceinline__ int swz_w(int n) {
+    return WT == VLRF_DT_Q8_0 ? (n >> 2) & 3 : (n >> 3) & 1;
+}
 
 }  // namespace lds_gemm
 
-template <int NM, int EPI>
-__global__ __launch_bounds__(lds_gemm::NT) void mfma_q8gemm_lds_kernel(
+template <int WT, int NM, int EPI>
+__global__ __launch_bounds__(lds_gemm::NT) void mfma_qgemm_lds_kernel(
     const uint16_t* __restrict__ A, const uint8_t* __restrict__ qa, const __half* __restrict__ da,
     const uint8_t* __restrict__ qb, const __half* __restrict__ db, int M, int N, int K,
     const float* __restrict__ residual, void* __restrict__ out) {
     using namespace lds_gemm;
-    using S = Stage<NM>;
+    using S = Stage<WT, NM>;
+    constexpr int CB = S::CB, RPI = 1024 / CB, CPR = CB / 16;   // rows / chunks per 1 KB load
     __shared__ __align__(16) uint8_t A0[A_B], A1[A_B], A2[A_B];
     __shared__ __align__(16) uint8_t W0[S::W_B], W1[S::W_B], W2[S::W_B];
     __shared__ __align__(16) uint8_t S0[S::S_B], S1[S::S_B], S2[S::S_B];
@@ -341,12 +343,14 @@ __global__ __launch_bounds__(lds_gemm::NT) void mfma_q8gemm_lds_kernel(
     }
     const char* gw[S::W_IT];
     uint32_t lw[S::W_IT];
+    const size_t rowb = WT == VLRF_DT_Q8_0 ? (size_t)K : (size_t)K / 2;   // code bytes of a weight row
 #pragma unroll
     for (int it = 0; it < S::W_IT; ++it) {
-        const int r0 = (it * 8 + wave) * 16, n = r0 + (lane >> 2), c = (lane & 3) ^ swz_w(n);
+        const int li = min(it * 8 + wave, S::W_TI - 1);   // waves past the last load: never issued
+        const int r0 = li * RPI, n = r0 + lane / CPR, c = (lane % CPR) ^ swz_w<WT>(n);
         const int gn = min(n0 + n % BN, N - 1);
-        gw[it] = reinterpret_cast<const char*>((n / BN ? qb : qa) + (size_t)gn * K + c * 16);
-        lw[it] = r0 * 64;
+        gw[it] = reinterpret_cast<const char*>((n / BN ? qb : qa) + (size_t)gn * rowb + c * 16);
+        lw[it] = r0 * CB;
     }
     const bool sload = wave < S::S_WAVES;
     const char* gs = nullptr;
@@ -361,7 +365,8 @@ __global__ __launch_bounds__(lds_gemm::NT) void mfma_q8gemm_lds_kernel(
 #pragma unroll
         for (int it = 0; it < A_IT; ++it) dma16(ga[it] + (size_t)kt * 128, bA[buf] + la[it]);
 #pragma unroll
-        for (int it = 0; it < S::W_IT; ++it) dma16(gw[it] + (size_t)kt * 64, bW[buf] + lw[it]);
+        for (int it = 0; it < S::W_IT; ++it)
+            if (it * 8 + wave < S::W_TI) dma16(gw[it] + (size_t)kt * CB, bW[buf] + lw[it]);
         if (sload) dma4(gs + (size_t)kt * 4, bS[buf] + wave * 256);
     };
 
@@ -377,16 +382,31 @@ __global__ __launch_bounds__(lds_gemm::NT) void mfma_q8gemm_lds_kernel(
             bf16x8 bfr[NM][2];
 #pragma unroll
             for (int m = 0; m < NM; ++m) {
-                const int n = m * BN + wn * WN + l32, c = 2 * p + h;
-                const uint4 u = *reinterpret_cast<const uint4*>(Ws + n * 64 + 16 * (c ^ swz_w(n)));
+                const int n = m * BN + wn * WN + l32;
                 const uint32_t s2 = *reinterpret_cast<const uint32_t*>(Ss + n * 4);
                 const float sc = __half2float(__ushort_as_half((unsigned short)(p ? s2 >> 16 : s2 & 0xFFFFu)));
-                const uint32_t w4[4] = {u.x, u.y, u.z, u.w};
+                if constexpr (WT == VLRF_DT_Q8_0) {
+                    // Q8_0: lane half h takes code chunk 2p + h (16 codes), slice q its half q
+                    const int c = 2 * p + h;
+                    const uint4 u = *reinterpret_cast<const uint4*>(Ws + n * CB + 16 * (c ^ swz_w<WT>(n)));
+                    const uint32_t w4[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
-                for (int q = 0; q < 2; ++q)
+                    for (int q = 0; q < 2; ++q)
 #pragma unroll
-                    for (int e = 0; e < 8; ++e)
-                        bfr[m][q][e] = (__bf16)((float)(int8_t)(w4[2 * q + (e >> 2)] >> (8 * (e & 3))) * sc);
+                        for (int e = 0; e < 8; ++e)
+                            bfr[m][q][e] = (__bf16)((float)(int8_t)(w4[2 * q + (e >> 2)] >> (8 * (e & 3))) * sc);
+                } else {
+                    // Q4_0: chunk p is the block; lane half h takes its bytes 8h..8h+7 (elements
+                    // 16h..16h+15, byte j = element 2j low nibble, 2j+1 high), slice q 4 of them
+                    const uint2 u = *reinterpret_cast<const uint2*>(Ws + n * CB + 16 * (p ^ swz_w<WT>(n)) + 8 * h);
+#pragma unroll
+                    for (int q = 0; q < 2; ++q) {
+                        const uint32_t wd = q ? u.y : u.x;
+#pragma unroll
+                        for (int e = 0; e < 8; ++e)
+                            bfr[m][q][e] = (__bf16)((float)((int)((wd >> (4 * e)) & 0xFu) - 8) * sc);
+                    }
+                }
             }
 #pragma unroll
             for (int q = 0; q < 2; ++q) {
@@ -448,16 +468,23 @@ __global__ __launch_bounds__(lds_gemm::NT) void mfma_q8gemm_lds_kernel(
         }
 }
 
-template <int EPI>
-void launch_q8_lds(hipStream_t s, const uint16_t* a, const DevWeight& w0, const DevWeight* w1, int M,
+template <int WT, int EPI>
+void launch_lds_wt(hipStream_t s, const uint16_t* a, const DevWeight& w0, const DevWeight* w1, int M,
                    const float* residual, void* out) {
     const dim3 grid((w0.N + lds_gemm::BN - 1) / lds_gemm::BN, (M + lds_gemm::BM - 1) / lds_gemm::BM);
     if constexpr (EPI >= 2)   // SwiGLU: gate and up tiles together
-        hipLaunchKernelGGL((mfma_q8gemm_lds_kernel<2, EPI>), grid, dim3(lds_gemm::NT), 0, s, a, w0.q, w0.d, w1->q,
-                           w1->d, M, w0.N, w0.K, residual, out);
+        hipLaunchKernelGGL((mfma_qgemm_lds_kernel<WT, 2, EPI>), grid, dim3(lds_gemm::NT), 0, s, a, w0.q, w0.d,
+                           w1->q, w1->d, M, w0.N, w0.K, residual, out);
     else
-        hipLaunchKernelGGL((mfma_q8gemm_lds_kernel<1, EPI>), grid, dim3(lds_gemm::NT), 0, s, a, w0.q, w0.d, w0.q,
-                           w0.d, M, w0.N, w0.K, residual, out);
+        hipLaunchKernelGGL((mfma_qgemm_lds_kernel<WT, 1, EPI>), grid, dim3(lds_gemm::NT), 0, s, a, w0.q, w0.d,
+                           w0.q, w0.d, M, w0.N, w0.K, residual, out);
+}
+
+template <int EPI>
+void launch_lds(hipStream_t s, const uint16_t* a, const DevWeight& w0, const DevWeight* w1, int M,
+                const float* residual, void* out) {
+    if (w0.dtype == VLRF_DT_Q8_0) launch_lds_wt<VLRF_DT_Q8_0, EPI>(s, a, w0, w1, M, residual, out);
+    else launch_lds_wt<VLRF_DT_Q4_0, EPI>(s, a, w0, w1, M, residual, out);
 }
 
 // out[r][:] = bf16(w ? rmsnorm(x[r]) * w : x[r]), one 256-lane workgroup per row
@@ -728,19 +755,12 @@ int launch_qgemm(hipStream_t s, const DevWeight& w, const uint16_t* a, int M, co
     int rc = check_qgemm(w, M);
     if (rc) return rc;
     VH_ARG(a && y, "qgemm: null operand");
-    const int tiles = ((w.N + 127) / 128) * ((M + 255) / 256);
-    if (M > 128 && w.dtype == VLRF_DT_Q8_0) {
-        if (residual) launch_q8_lds<1>(s, a, w, nullptr, M, residual, y);
-        else launch_q8_lds<0>(s, a, w, nullptr, M, nullptr, y);
-    } else if (M <= 128) {
+    if (M > 128) {
+        if (residual) launch_lds<1>(s, a, w, nullptr, M, residual, y);
+        else launch_lds<0>(s, a, w, nullptr, M, nullptr, y);
+    } else {
         if (residual) launch_cfg<CfgSmall, 1>(s, w.dtype, a, w, nullptr, M, residual, y);
         else launch_cfg<CfgSmall, 0>(s, w.dtype, a, w, nullptr, M, nullptr, y);
-    } else if (tiles > kCUs && tiles <= 2 * kCUs) {
-        if (residual) launch_cfg<CfgFill, 1>(s, w.dtype, a, w, nullptr, M, residual, y);
-        else launch_cfg<CfgFill, 0>(s, w.dtype, a, w, nullptr, M, nullptr, y);
-    } else {
-        if (residual) launch_cfg<CfgWide, 1>(s, w.dtype, a, w, nullptr, M, residual, y);
-        else launch_cfg<CfgWide, 0>(s, w.dtype, a, w, nullptr, M, nullptr, y);
     }
     VH_LAUNCHED();
     return VLRF_HIP_OK;
@@ -754,15 +774,12 @@ int launch_qgemm_swiglu(hipStream_t s, const DevWeight& wg, const DevWeight& wu,
     if (rc) return rc;
     VH_ARG(wg.N == wu.N && wg.K == wu.K && wg.dtype == wu.dtype, "qgemm_swiglu: gate/up differ");
     VH_ARG(a && h, "qgemm_swiglu: null operand");
-    if (M > 128 && wg.dtype == VLRF_DT_Q8_0) {
-        if (h_bf16) launch_q8_lds<2>(s, a, wg, &wu, M, nullptr, h);
-        else launch_q8_lds<3>(s, a, wg, &wu, M, nullptr, h);
-    } else if (M <= 128) {
+    if (M > 128) {
+        if (h_bf16) launch_lds<2>(s, a, wg, &wu, M, nullptr, h);
+        else launch_lds<3>(s, a, wg, &wu, M, nullptr, h);
+    } else {
         if (h_bf16) launch_cfg<CfgSmall, 2>(s, wg.dtype, a, wg, &wu, M, nullptr, h);
         else launch_cfg<CfgSmall, 3>(s, wg.dtype, a, wg, &wu, M, nullptr, h);
-    } else {
-        if (h_bf16) launch_cfg<CfgSwi, 2>(s, wg.dtype, a, wg, &wu, M, nullptr, h);
-        else launch_cfg<CfgSwi, 3>(s, wg.dtype, a, wg, &wu, M, nullptr, h);
     }
     VH_LAUNCHED();
     return VLRF_HIP_OK;
