@@ -489,23 +489,57 @@ void launch_lds(hipStream_t s, const uint16_t* a, const DevWeight& w0, const Dev
 
 // out[r][:] = bf16(w ? rmsnorm(x[r]) * w : x[r]), one 256-lane workgroup per row
 // (ops.hpp:488-498: sum of squares, 1/sqrt(mean + eps), (x * inv) * w).
+// Rows of D % 4 == 0 and D <= 4096 are read once, as float4 held in registers
+// (VEC = 4 per thread), and written as 4 packed bf16; others take the scalar loop.
+constexpr int kRowVec = 4;
+template <bool VEC>
 __global__ __launch_bounds__(256) void rows_to_bf16_kernel(const float* __restrict__ x,
                                                            const float* __restrict__ w,
                                                            uint16_t* __restrict__ out, int D, float eps) {
     __shared__ float red[4];
     const int r = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float* xr = x + (size_t)r * D;
-    float inv = 1.f;
-    if (w) {
-        float ss = 0.f;
-        for (int i = tid; i < D; i += 256) ss += xr[i] * xr[i];
+    uint16_t* o = out + (size_t)r * D;
+    auto inv_rms = [&](float ss) {
         ss = wave_sum(ss);
         if (lane == 0) red[wave] = ss;
         __syncthreads();
-        inv = 1.f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)D + eps);
+        return 1.f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)D + eps);
+    };
+    if constexpr (VEC) {
+        const int n4 = D / 4;
+        float4 v[kRowVec], g[kRowVec];
+#pragma unroll
+        for (int p = 0; p < kRowVec; ++p) {
+            const int f = tid + 256 * p;
+            v[p] = f < n4 ? reinterpret_cast<const float4*>(xr)[f] : make_float4(0.f, 0.f, 0.f, 0.f);
+            if (w) g[p] = f < n4 ? reinterpret_cast<const float4*>(w)[f] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        float inv = 1.f;
+        if (w) {
+            float ss = 0.f;
+#pragma unroll
+            for (int p = 0; p < kRowVec; ++p) ss += v[p].x * v[p].x + v[p].y * v[p].y + v[p].z * v[p].z + v[p].w * v[p].w;
+            inv = inv_rms(ss);
+        }
+#pragma unroll
+        for (int p = 0; p < kRowVec; ++p) {
+            const int f = tid + 256 * p;
+            if (f < n4) {
+                float4 t = v[p];
+                if (w) t = make_float4(t.x * inv * g[p].x, t.y * inv * g[p].y, t.z * inv * g[p].z, t.w * inv * g[p].w);
+                reinterpret_cast<uint2*>(o)[f] = make_uint2(pack_bf16(t.x, t.y), pack_bf16(t.z, t.w));
+            }
+        }
+    } else {
+        float inv = 1.f;
+        if (w) {
+            float ss = 0.f;
+            for (int i = tid; i < D; i += 256) ss += xr[i] * xr[i];
+            inv = inv_rms(ss);
+        }
+        for (int i = tid; i < D; i += 256) o[i] = (uint16_t)bf16_bits(w ? xr[i] * inv * w[i] : xr[i]);
     }
-    uint16_t* o = out + (size_t)r * D;
-    for (int i = tid; i < D; i += 256) o[i] = (uint16_t)bf16_bits(w ? xr[i] * inv * w[i] : xr[i]);
 }
 
 // ---- small M on the matrix cores ------------------------------------------------
@@ -745,7 +779,10 @@ int check_qgemm(const DevWeight& w, int M) {
 int launch_rows_to_bf16(hipStream_t s, const float* x, const float* w, uint16_t* out, int rows, int D,
                         float eps) {
     VH_ARG(x && out && rows >= 1 && D >= 1, "rows_to_bf16: bad arguments");
-    hipLaunchKernelGGL(rows_to_bf16_kernel, dim3(rows), dim3(256), 0, s, x, w, out, D, eps);
+    if (D % 4 == 0 && D <= 4 * 256 * kRowVec)
+        hipLaunchKernelGGL(rows_to_bf16_kernel<true>, dim3(rows), dim3(256), 0, s, x, w, out, D, eps);
+    else
+        hipLaunchKernelGGL(rows_to_bf16_kernel<false>, dim3(rows), dim3(256), 0, s, x, w, out, D, eps);
     VH_LAUNCHED();
     return VLRF_HIP_OK;
 }
