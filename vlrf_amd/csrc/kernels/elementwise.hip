@@ -43,6 +43,17 @@ __device__ __forceinline__ void rope_pair(float* v, int i, int half, float c, fl
     v[i + half] = e + f;
 }
 
+// rope_pair on values in registers: (x0, x1) -> (x0 c - x1 s, x1 c + x0 s).
+__device__ __forceinline__ void rope2v(float x0, float x1, float c, float s, float* y0, float* y1) {
+#pragma clang fp contract(off)
+    const float a = x0 * c;
+    const float b = x1 * s;
+    const float e = x1 * c;
+    const float f = x0 * s;
+    *y0 = a - b;
+    *y1 = e + f;
+}
+
 // quantize_row_q8_0 (kv_cache.hpp:102-117) of one row of n_kv*D floats into
 // the head-major cache at token position p.  Bit-exact: max is
 // order-independent, amax/127 and 1/scale are correctly rounded (HIP default,
@@ -121,9 +132,28 @@ __global__ __launch_bounds__(256) void rope_append_kernel(int8_t* kq, int8_t* vq
     const float* s = sin_t + (size_t)p * half;
     for (int i = threadIdx.x; i < row; i += 256) kr[i] = k[i];
     __syncthreads();
-    for (int i = threadIdx.x; i < n_heads * half; i += 256) {
-        const int h = i / half, j = i - h * half;
-        rope_pair(q + (size_t)h * D, j, half, c[j], s[j]);
+    if (half % 4 == 0) {
+        // four pairs per thread: float4 loads and stores of x0 and x1, the same
+        // separately rounded products per element as rope_pair
+        for (int i4 = threadIdx.x; i4 < n_heads * half / 4; i4 += 256) {
+            const int h = 4 * i4 / half, j = 4 * i4 - h * half;
+            float4* x0p = reinterpret_cast<float4*>(q + (size_t)h * D + j);
+            float4* x1p = reinterpret_cast<float4*>(q + (size_t)h * D + half + j);
+            const float4 x0 = *x0p, x1 = *x1p;
+            const float4 c4 = *reinterpret_cast<const float4*>(c + j), s4 = *reinterpret_cast<const float4*>(s + j);
+            float4 y0, y1;
+            rope2v(x0.x, x1.x, c4.x, s4.x, &y0.x, &y1.x);
+            rope2v(x0.y, x1.y, c4.y, s4.y, &y0.y, &y1.y);
+            rope2v(x0.z, x1.z, c4.z, s4.z, &y0.z, &y1.z);
+            rope2v(x0.w, x1.w, c4.w, s4.w, &y0.w, &y1.w);
+            *x0p = y0;
+            *x1p = y1;
+        }
+    } else {
+        for (int i = threadIdx.x; i < n_heads * half; i += 256) {
+            const int h = i / half, j = i - h * half;
+            rope_pair(q + (size_t)h * D, j, half, c[j], s[j]);
+        }
     }
     for (int i = threadIdx.x; i < n_kv * half; i += 256) {
         const int h = i / half, j = i - h * half;
@@ -152,9 +182,28 @@ __global__ __launch_bounds__(256) void prefill_rope_append_kernel(
     const float* s = sin_t + (size_t)p * half;
     for (int i = threadIdx.x; i < row; i += 256) kr[i] = k[i];
     __syncthreads();
-    for (int i = threadIdx.x; i < n_heads * half; i += 256) {
-        const int h = i / half, j = i - h * half;
-        rope_pair(q + (size_t)h * D, j, half, c[j], s[j]);
+    if (half % 4 == 0) {
+        // four pairs per thread: float4 loads and stores of x0 and x1, the same
+        // separately rounded products per element as rope_pair
+        for (int i4 = threadIdx.x; i4 < n_heads * half / 4; i4 += 256) {
+            const int h = 4 * i4 / half, j = 4 * i4 - h * half;
+            float4* x0p = reinterpret_cast<float4*>(q + (size_t)h * D + j);
+            float4* x1p = reinterpret_cast<float4*>(q + (size_t)h * D + half + j);
+            const float4 x0 = *x0p, x1 = *x1p;
+            const float4 c4 = *reinterpret_cast<const float4*>(c + j), s4 = *reinterpret_cast<const float4*>(s + j);
+            float4 y0, y1;
+            rope2v(x0.x, x1.x, c4.x, s4.x, &y0.x, &y1.x);
+            rope2v(x0.y, x1.y, c4.y, s4.y, &y0.y, &y1.y);
+            rope2v(x0.z, x1.z, c4.z, s4.z, &y0.z, &y1.z);
+            rope2v(x0.w, x1.w, c4.w, s4.w, &y0.w, &y1.w);
+            *x0p = y0;
+            *x1p = y1;
+        }
+    } else {
+        for (int i = threadIdx.x; i < n_heads * half; i += 256) {
+            const int h = i / half, j = i - h * half;
+            rope_pair(q + (size_t)h * D, j, half, c[j], s[j]);
+        }
     }
     for (int i = threadIdx.x; i < n_kv * half; i += 256) {
         const int h = i / half, j = i - h * half;
