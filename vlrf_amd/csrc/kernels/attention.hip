@@ -719,8 +719,9 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
 // query (it still joins the barriers).  The wave
 // computes S^T = K.Q^T and O^T = V^T.P^T with v_mfma_f32_32x32x16_bf16: in that
 // orientation lane l owns query l%32 (both lane halves), so the softmax max and
-// sum are one cross-half shuffle, the rescale multiplies the lane's own
-// accumulators, and P re-enters the second product through register shuffles.
+// sum are one cross-half exchange (v_permlane32_swap), the rescale multiplies
+// the lane's own accumulators, and P re-enters the second product through the
+// same register exchange.
 constexpr int kPQ = 32, kPK = 64;         // queries per wave, keys per tile
 
 // Raw cache elements of one staging item (16 consecutive elements of one key
@@ -767,6 +768,13 @@ __device__ __forceinline__ void raw_f32(const uint4 (&w)[RawKV<KVT>::W], float s
             o[4 * k + 3] = live ? __uint_as_float(w[k].w) : 0.f;
         }
     }
+}
+
+// v_permlane32_swap: returns ([a lanes 0-31, b lanes 0-31], [a lanes 32-63,
+// b lanes 32-63]) -- a VALU exchange of the two wave halves, no LDS round trip.
+__device__ __forceinline__ float2 half_swap(float a, float b) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
 // Column (key) of V^T row d in LDS: groups of 8 keys XOR-swizzled by the row's
@@ -889,7 +897,10 @@ __global__ __launch_bounds__(512) void attn_prefill_kernel(
             for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
                 for (int v = 0; v < 16; ++v) mx = fmaxf(mx, sc[kb][v]);
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            {
+                const float2 t = half_swap(mx, mx);    // [lo, lo], [hi, hi]
+                mx = fmaxf(t.x, t.y);
+            }
             const float mn = fmaxf(m_run, mx * sl2); // finite: key 0 is in the first tile
             const float corr = __builtin_amdgcn_exp2f(m_run - mn);   // 0 on the first tile
             float sum = 0.f;
@@ -901,7 +912,10 @@ __global__ __launch_bounds__(512) void attn_prefill_kernel(
                     sc[kb][v] = p;
                     sum += p;
                 }
-            sum += __shfl_xor(sum, 32);
+            {
+                const float2 t = half_swap(sum, sum);
+                sum = t.x + t.y;                         // lo + hi in both halves
+            }
             l_run = l_run * corr + sum;
             m_run = mn;
 #pragma unroll
@@ -909,22 +923,20 @@ __global__ __launch_bounds__(512) void attn_prefill_kernel(
 #pragma unroll
                 for (int v = 0; v < 16; ++v) o[c][v] *= corr;
 
-            // O^T += V^T . P^T, 16 keys per step.  The B operand needs keys
-            // 16s + 8hh + e of the lane's query: group 2s+hh of this half and of
-            // the other half (v-groups of 4 keys), exchanged with one xor-32 shuffle.
+            // O^T += V^T . P^T, 16 keys per step.  The B operand of lane (hh, q)
+            // needs keys 16s + 8hh + e: v-group 2s+hh, elements 0..3 from lane
+            // half 0 and 4..7 from half 1.  One half-swap of (group 2s, group
+            // 2s+1) delivers exactly that in both halves: [A_lo, B_lo] gives
+            // elements 0..3, [A_hi, B_hi] elements 4..7.
 #pragma unroll
             for (int kk2 = 0; kk2 < kPK / 16; ++kk2) {
                 const int kb = kk2 >> 1, s2 = kk2 & 1;
-                const int gown = 2 * s2 + hh, gsend = 2 * s2 + 1 - hh;
-                float y[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) y[e] = __shfl_xor(sc[kb][4 * gsend + e], 32);
                 bf16x8 b;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const float mine = sc[kb][4 * gown + e];
-                    b[e] = (__bf16)(hh == 0 ? mine : y[e]);
-                    b[4 + e] = (__bf16)(hh == 0 ? y[e] : mine);
+                    const float2 t = half_swap(sc[kb][8 * s2 + e], sc[kb][8 * s2 + 4 + e]);
+                    b[e] = (__bf16)t.x;
+                    b[4 + e] = (__bf16)t.y;
                 }
 #pragma unroll
                 for (int c = 0; c < D / 32; ++c) {
