@@ -233,14 +233,31 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, v);
 }
 
+// Row exchanges in VALU (no LDS round trip): v_permlane16_swap(a, b) returns
+// ([a row0, b row0, a row2, b row2], [a row1, b row1, a row3, b row3]) over the
+// wave's four 16-lane rows, v_permlane32_swap(a, b) ([a lo, b lo], [a hi, b hi])
+// over its 32-lane halves.  Swapping a value with itself puts the partner
+// row's (half's) value beside the lane's own.
+__device__ __forceinline__ float2 swap_rows16(float a, float b) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float2 swap_halves32(float a, float b) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+// Sum / max over the wave; every lane gets the result (the pairwise order is
+// the same in all lanes: row 0 + row 1, then half 0 + half 1).
 __device__ __forceinline__ float wave_sum(float v) {
     v += dpp_f<0xB1>(v);    // quad_perm [1,0,3,2]
     v += dpp_f<0x4E>(v);    // quad_perm [2,3,0,1]
     v += dpp_f<0x141>(v);   // row_half_mirror
     v += dpp_f<0x140>(v);   // row_mirror
-    v += __shfl_xor(v, 16);
-    v += __shfl_xor(v, 32);
-    return v;
+    float2 t = swap_rows16(v, v);
+    v = t.x + t.y;
+    t = swap_halves32(v, v);
+    return t.x + t.y;
 }
 
 __device__ __forceinline__ float wave_max(float v) {
@@ -248,9 +265,10 @@ __device__ __forceinline__ float wave_max(float v) {
     v = fmaxf(v, dpp_f<0x4E>(v));
     v = fmaxf(v, dpp_f<0x141>(v));
     v = fmaxf(v, dpp_f<0x140>(v));
-    v = fmaxf(v, __shfl_xor(v, 16));
-    v = fmaxf(v, __shfl_xor(v, 32));
-    return v;
+    float2 t = swap_rows16(v, v);
+    v = fmaxf(t.x, t.y);
+    t = swap_halves32(v, v);
+    return fmaxf(t.x, t.y);
 }
 
 }  // namespace vlrf_hip

@@ -589,12 +589,15 @@ __global__ __launch_bounds__(64 * kSPWaves) void attn_decode_single_kernel(
     // ---- merge: lanes of a dim group, then the waves -------------------------------
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
+        // sum over the 16 lanes tg of dim group dg: rotations by 4 and 8 within a
+        // 16-lane row (DPP row_ror), then the row and half exchanges
         float v = acc[e];
-        v += __shfl_xor(v, 4);
-        v += __shfl_xor(v, 8);
-        v += __shfl_xor(v, 16);
-        v += __shfl_xor(v, 32);   // lanes tg = 0..15 of dim group dg
-        acc[e] = v;
+        v += dpp_f<0x124>(v);
+        v += dpp_f<0x128>(v);
+        float2 t = swap_rows16(v, v);
+        v = t.x + t.y;
+        t = swap_halves32(v, v);
+        acc[e] = t.x + t.y;
     }
     if (tg == 0) {
 #pragma unroll
@@ -770,12 +773,7 @@ __device__ __forceinline__ void raw_f32(const uint4 (&w)[RawKV<KVT>::W], float s
     }
 }
 
-// v_permlane32_swap: returns ([a lanes 0-31, b lanes 0-31], [a lanes 32-63,
-// b lanes 32-63]) -- a VALU exchange of the two wave halves, no LDS round trip.
-__device__ __forceinline__ float2 half_swap(float a, float b) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
-    return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
+__device__ __forceinline__ float2 half_swap(float a, float b) { return swap_halves32(a, b); }
 
 // Column (key) of V^T row d in LDS: groups of 8 keys XOR-swizzled by the row's
 // 16-dim block, so the 8 stagers of one key (8 blocks of 16 dims) hit distinct

@@ -570,8 +570,8 @@ __device__ __forceinline__ float wave32_sum(float v) {     // sum over each half
     v += dpp_f<0x4E>(v);
     v += dpp_f<0x141>(v);
     v += dpp_f<0x140>(v);
-    v += __shfl_xor(v, 16);
-    return v;
+    const float2 t = swap_rows16(v, v);
+    return t.x + t.y;
 }
 
 // Codes of one lane's 8 columns of a block -> bf16 (exact).
