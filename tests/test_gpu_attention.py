@@ -48,7 +48,7 @@ def test_sdp_attention_reference_shapes(ctx, orc, T, ctx_len, d, causal, seed):
 
 
 def test_config1_decode_f32(ctx, orc):
-    """1 query, 8 heads, d 64, KV 512, non-causal, scale 1/8."""
+    """Benchmark config 1: 1 query, 8 heads, d 64, KV 512, non-causal, scale 1/8."""
     Q, K, V = _qkv(11, 8, 1, 512, 64)
     out = _run_gpu(ctx, Q, K, V, np.float32(0.125), False)
     ref = orc.sdp_attention(Q, K, V, np.float32(0.125), False)
@@ -90,7 +90,7 @@ def _gqa_reference(orc, q, kq, vq, ks, vs, n_heads, n_kv, d, ctx_len, scale):
                                                     (32, 8, 64, 65), (32, 4, 64, 510),
                                                     (8, 2, 64, 4600)])
 def test_q8_decode_attention(ctx, orc, n_heads, n_kv, d, ctx_len):
-    """BASELINE config 2 (32q/4kv, d 64, ctx 4096) and other GQA groupings.
+    """Benchmark config 2 (32q/4kv, d 64, ctx 4096) and other GQA groupings.
     Caches of up to 512 rows at d_head 64 take the single-pass kernel (one
     workgroup per query head; 509 + 3 rows fill every wave's round), larger
     ones and d_head 128 the split-K kernel and its combine."""

@@ -1,5 +1,5 @@
 """GPU parity: dequant-fused quantized linear (compute::linear on weights
-decoded from GGUF Q8_0/Q4_0 blocks, convert_gguf.py:233-263), BASELINE
+decoded from GGUF Q8_0/Q4_0 blocks, convert_gguf.py:233-263), benchmark
 config 3 shapes, plus the fused RMSNorm prologue, residual epilogue and the
 SwiGLU gate/up variant.  Oracle: ops::gemm restated (oracle/vlrf_oracle.c)
 on the decoded f32 weights.  Tolerance: 1e-3 relative (fp32 path)."""
