@@ -311,12 +311,11 @@ __device__ __forceinline__ void gemv_compute(const GemvRegs<NM, RPW, NC>& R, con
     }
 }
 
-// The activation row: x itself, or row *x_row of the table x.
-__device__ __forceinline__ const float* xr_src(const float* x, const int* x_row, int K) {
-    return x_row ? x + (size_t)(*x_row) * K : x;
-}
-
-template <int WT, int NC, int RPW, bool SWIGLU>
+// XM: bit 0 = RMSNorm fused (norm_w), bit 1 = x is row *x_row of a table (with
+// the raw row copied to x_copy).  Compile-time, so that no branch on a kernel
+// argument splits the prologue: all arguments arrive in one scalar round trip
+// before the first activation and weight loads are issued.
+template <int WT, int NC, int RPW, bool SWIGLU, int XM>
 __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(
     const uint8_t* __restrict__ qa, const __half* __restrict__ da, const uint8_t* __restrict__ qb,
     const __half* __restrict__ db, int N, int K, const float* __restrict__ x,
@@ -349,7 +348,8 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(
     float inv = 1.f;                                  // 1/rms, applied to the finished dots
     GemvRegs<NM, RPW, NC> A, B;
     {
-        const float* xs = xr_src(x, x_row, K);
+        constexpr bool NORM = XM & 1, GATHER = XM & 2;
+        const float* xs = GATHER ? x + (size_t)(*x_row) * K : x;
         float4 v[PER], gw[PER];
 #pragma unroll
         for (int p = 0; p < PER; ++p) {
@@ -358,7 +358,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(
             const float4 t = reinterpret_cast<const float4*>(xs)[in ? f : 0];
             v[p] = in ? t : make_float4(0.f, 0.f, 0.f, 0.f);
         }
-        if (norm_w) {
+        if constexpr (NORM) {
 #pragma unroll
             for (int p = 0; p < PER; ++p) {
                 const int f = tid + p * NT;
@@ -379,9 +379,9 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(
         for (int p = 0; p < PER; ++p) {
             const int f = tid + p * NT;
             ss += v[p].x * v[p].x + v[p].y * v[p].y + v[p].z * v[p].z + v[p].w * v[p].w;
-            if (x_copy && blockIdx.x == 0 && f < XF4 && 4 * f < K) reinterpret_cast<float4*>(x_copy)[f] = v[p];
+            if (GATHER && x_copy && blockIdx.x == 0 && f < XF4 && 4 * f < K) reinterpret_cast<float4*>(x_copy)[f] = v[p];
         }
-        if (norm_w) {
+        if constexpr (NORM) {
             ss = wave_sum(ss);
             if (lane == 0) red[wave] = ss;
         }
@@ -390,7 +390,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(
             const int f = tid + p * NT;
             if (f < XF4) {
                 float4 o = v[p];
-                if (norm_w && 4 * f < K) {
+                if (NORM && 4 * f < K) {
                     const float4 g = gw[p];
                     o.x = o.x * g.x; o.y = o.y * g.y;
                     o.z = o.z * g.z; o.w = o.w * g.w;
@@ -400,7 +400,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(
             }
         }
         __syncthreads();
-        if (norm_w) {
+        if constexpr (NORM) {
             ss = 0.f;
 #pragma unroll
             for (int w = 0; w < kGemvWaves; ++w) ss += red[w];
@@ -439,13 +439,20 @@ int launch_gemv(hipStream_t s, const DevWeight& a, const DevWeight* b, const flo
     const int nc = (a.K + CW - 1) / CW;
     const uint8_t* qb = b ? b->q : nullptr;
     const __half* db = b ? b->d : nullptr;
-#define VH_GEMV(NC, RPW)                                                                               \
-    do {                                                                                              \
-        const int groups = (a.N + kGemvWaves * (RPW)-1) / (kGemvWaves * (RPW));                        \
-        dim3 grid(groups < kGemvMaxGroups ? groups : kGemvMaxGroups);                                  \
-        hipLaunchKernelGGL((gemv_kernel<WT, NC, RPW, SWIGLU>), grid, dim3(64 * kGemvWaves), 0, s, a.q, \
-                           a.d, qb, db,                                                                \
-                           a.N, a.K, x, x_row, x_copy, norm_w, eps, residual, y);                      \
+    VH_ARG(!x_row || (norm_w && !SWIGLU), "gemv: a gathered row needs the fused norm");
+    const int xm = (x_row ? 2 : 0) | (norm_w ? 1 : 0);
+#define VH_GEMV_XM(NC, RPW, XM)                                                                            \
+    do {                                                                                                  \
+        const int groups = (a.N + kGemvWaves * (RPW)-1) / (kGemvWaves * (RPW));                            \
+        dim3 grid(groups < kGemvMaxGroups ? groups : kGemvMaxGroups);                                      \
+        hipLaunchKernelGGL((gemv_kernel<WT, NC, RPW, SWIGLU, XM>), grid, dim3(64 * kGemvWaves), 0, s, a.q, \
+                           a.d, qb, db, a.N, a.K, x, x_row, x_copy, norm_w, eps, residual, y);              \
+    } while (0)
+#define VH_GEMV(NC, RPW)                                                   \
+    do {                                                                  \
+        if (xm == 0) VH_GEMV_XM(NC, RPW, 0);                              \
+        else if (xm == 1) VH_GEMV_XM(NC, RPW, 1);                         \
+        else if constexpr (!SWIGLU) VH_GEMV_XM(NC, RPW, 3);               \
     } while (0)
     if (nc <= 1) {
         VH_GEMV(1, 1);
@@ -459,6 +466,7 @@ int launch_gemv(hipStream_t s, const DevWeight& a, const DevWeight* b, const flo
         if constexpr (WT == VLRF_DT_Q8_0) VH_GEMV(6, 1);
     }
 #undef VH_GEMV
+#undef VH_GEMV_XM
     VH_LAUNCHED();
     return VLRF_HIP_OK;
 }
