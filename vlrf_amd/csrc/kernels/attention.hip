@@ -120,7 +120,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_partial_kernel(
 
     // The device position is read only now: none of the addresses above depend
     // on it, so its latency overlaps the cache stream.
-    const int dpos = ctx_dev ? *ctx_dev : 0;
+    const int dpos = (FUSED || ctx_dev) ? *ctx_dev : 0;   // fused: always a device position
     int ctx = FUSED ? dpos + 1 : (ctx_dev ? dpos + ctx_len : ctx_len);   // FUSED: dpos = tokens before this one
     // Rows past the cache capacity are never read, even if the device-side
     // position were corrupt (the host checks capacity before queuing).
@@ -453,7 +453,7 @@ __global__ __launch_bounds__(64 * kSPWaves) void attn_decode_single_kernel(
 #pragma unroll
     for (int r = 0; r < kSPDepth; ++r) load_round(r, r);
 
-    const int dpos = ctx_dev ? *ctx_dev : 0;
+    const int dpos = (FUSED || ctx_dev) ? *ctx_dev : 0;   // fused: always a device position
     int ctx = FUSED ? dpos + 1 : (ctx_dev ? dpos + ctx_len : ctx_len);
     ctx = min(ctx, cap);
     const int pos = FUSED ? dpos : -1;
