@@ -65,6 +65,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_partial_kernel(
     __shared__ __align__(16) float pr[REP][kChunk];      // softmax numerators
     __shared__ float mstat[REP], lstat[REP];
     __shared__ __align__(16) float newk[FUSED ? D : 1];
+    __shared__ float amax[FUSED ? 2 * NW : 1];          // per-wave maxima of the new K and V rows
 
     const int split = blockIdx.x, g = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -86,20 +87,16 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_partial_kernel(
         qlo[p] = qh[j];
         qhi[p] = qh[j + HALF];
     }
-    // Fused decode: wave 0 holds the new token's K row as RoPE pairs and its V
-    // row (row <= 1024 floats: up to 8 pairs and 16 values per lane).
-    constexpr int KP = FUSED ? 8 : 1, VP = FUSED ? 16 : 1;
-    float nk0[KP], nk1[KP], nv[VP];
-    if (FUSED && wave == 0) {
+    // Fused decode: the new token's row spread over the workgroup (rows of at
+    // most 1024 elements): thread t holds K RoPE pair t and V elements t, t + NT.
+    float nk0 = 0.f, nk1 = 0.f, nv0 = 0.f, nv1 = 0.f;
+    if constexpr (FUSED) {
         const int npairs = fz.n_kv * HALF, nrow = fz.n_kv * D;
-#pragma unroll
-        for (int p = 0; p < KP; ++p) {
-            const int i = min(lane + 64 * p, npairs - 1), h = i / HALF, j = i - h * HALF;
-            nk0[p] = fz.k_new[h * D + j];
-            nk1[p] = fz.k_new[h * D + j + HALF];
-        }
-#pragma unroll
-        for (int p = 0; p < VP; ++p) nv[p] = fz.v_new[min(lane + 64 * p, nrow - 1)];
+        const int i = min(tid, npairs - 1), h = i / HALF, j = i - h * HALF;
+        nk0 = fz.k_new[h * D + j];
+        nk1 = fz.k_new[h * D + j + HALF];
+        nv0 = fz.v_new[min(tid, nrow - 1)];
+        nv1 = fz.v_new[min(tid + NT, nrow - 1)];
     }
     // The cache stream, kept as raw codes: lane l of every wave reads the whole
     // K row of token c0+l (the waves' repeats are L1 hits); thread t stages
@@ -192,31 +189,40 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_partial_kernel(
         }
     }
 
-    // ---- decode fusion: the current token's K/V row (wave 0 of the chunk holding it)
+    // ---- decode fusion: the current token's K/V row (the chunk holding it)
     // attention.hpp:109-128: RoPE on k, then KVCache::append stores the row
     // before attention reads it: Q8_0 quantizes the whole row (quantize_row_q8_0,
     // kv_cache.hpp:102-117), F16 converts each element (f32_to_f16, :68-97), F32
     // copies.  Every chunk holding `pos` converts the row itself and uses the
     // stored values for that token; the workgroup of KV head g stores head g's
-    // elements, KV head 0 the Q8_0 row scales.  Wave reductions only.
+    // elements, KV head 0 the Q8_0 row scales.  The whole workgroup shares the
+    // work (one pair and up to two V elements per thread): the row maxima are
+    // wave reductions merged through LDS at the barrier below, so the chain
+    // before the scores is a few dozen instructions long.
+    const int npairs = FUSED ? fz.n_kv * HALF : 0, nrow = FUSED ? fz.n_kv * D : 0;
     if constexpr (FUSED) {
-        if (has_new && wave == 0) {
-            const int npairs = fz.n_kv * HALF, nrow = fz.n_kv * D;
-            float ak = 0.f, av = 0.f;
-#pragma unroll
-            for (int p = 0; p < KP; ++p) {
-                if (lane + 64 * p < npairs) {
-                    if (rot) rope2(nk0[p], nk1[p], rc, rs, &nk0[p], &nk1[p]);
-                    ak = fmaxf(ak, fmaxf(fabsf(nk0[p]), fabsf(nk1[p])));
-                }
-            }
-            float sk = 1.f, sv = 1.f, ik = 0.f, iv = 0.f;
+        if (has_new) {
+            if (tid < npairs && rot) rope2(nk0, nk1, rc, rs, &nk0, &nk1);
             if constexpr (Q8) {
-#pragma unroll
-                for (int p = 0; p < VP; ++p)
-                    if (lane + 64 * p < nrow) av = fmaxf(av, fabsf(nv[p]));
+                float ak = tid < npairs ? fmaxf(fabsf(nk0), fabsf(nk1)) : 0.f;
+                float av = tid < nrow ? fabsf(nv0) : 0.f;
+                if (tid + NT < nrow) av = fmaxf(av, fabsf(nv1));
                 ak = wave_max(ak);
                 av = wave_max(av);
+                if (lane == 0) { amax[wave] = ak; amax[NW + wave] = av; }
+            }
+        }
+    }
+    __syncthreads();
+    if constexpr (FUSED) {
+        if (has_new) {
+            float ak = 0.f, av = 0.f, sk = 1.f, sv = 1.f, ik = 0.f, iv = 0.f;
+            if constexpr (Q8) {
+#pragma unroll
+                for (int w = 0; w < NW; ++w) {
+                    ak = fmaxf(ak, amax[w]);
+                    av = fmaxf(av, amax[NW + w]);
+                }
                 sk = ak != 0.f ? ak / 127.f : 0.f;
                 sv = av != 0.f ? av / 127.f : 0.f;
                 ik = ak != 0.f ? 1.f / sk : 0.f;
@@ -240,26 +246,20 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_partial_kernel(
                     return x;
                 }
             };
-#pragma unroll
-            for (int p = 0; p < KP; ++p) {
-                const int i = lane + 64 * p;
-                if (i < npairs && i / HALF == g) {
-                    const int j = i % HALF;
-                    newk[j] = put(krow_w, j, nk0[p], sk, ik, ak != 0.f);
-                    newk[j + HALF] = put(krow_w, j + HALF, nk1[p], sk, ik, ak != 0.f);
-                }
+            if (tid < npairs && tid / HALF == g) {
+                const int j = tid % HALF;
+                newk[j] = put(krow_w, j, nk0, sk, ik, ak != 0.f);
+                newk[j + HALF] = put(krow_w, j + HALF, nk1, sk, ik, ak != 0.f);
             }
-#pragma unroll
-            for (int p = 0; p < VP; ++p) {
-                const int i = lane + 64 * p;
-                if (i < nrow && i / D == g) vnew[i % D] = put(vrow_w, i % D, nv[p], sv, iv, av != 0.f);
-            }
+            if (tid < nrow && tid / D == g) vnew[tid % D] = put(vrow_w, tid % D, nv0, sv, iv, av != 0.f);
+            if (tid + NT < nrow && (tid + NT) / D == g)
+                vnew[(tid + NT) % D] = put(vrow_w, (tid + NT) % D, nv1, sv, iv, av != 0.f);
             if constexpr (Q8) {
-                if (g == 0 && lane == 0) { fz.ks_w[pos] = sk; fz.vs_w[pos] = sv; }
+                if (g == 0 && tid == 0) { fz.ks_w[pos] = sk; fz.vs_w[pos] = sv; }
             }
+            __syncthreads();   // the stored K row, before the scores read it
         }
     }
-    __syncthreads();
 
     // ---- scores and softmax: lane = token, HPW heads per wave, full d_head ------
     // One wave per SIMD leaves no other wave to hide LDS latency, so each
