@@ -400,6 +400,7 @@ __global__ __launch_bounds__(64 * kSPWaves) void attn_decode_single_kernel(
     constexpr int KW = D * EB / 16, VW = EB;         // 16-byte words: a K row, a 16-element V piece
     __shared__ __align__(16) float qs[D];
     __shared__ __align__(16) float nk[D], nv[D];     // the new token's stored row of KV head g, read back
+    __shared__ float amax[2 * NW];                   // per-wave maxima of the new K and V rows
     __shared__ __align__(16) float pbuf[NW][64];     // p (times the V row scale) of the wave's current round
     __shared__ float wm[NW], wl[NW];
     __shared__ __align__(16) float wacc[NW][D];
@@ -418,18 +419,16 @@ __global__ __launch_bounds__(64 * kSPWaves) void attn_decode_single_kernel(
         q0 = q[(size_t)h * D + j];
         q1 = q[(size_t)h * D + j + HALF];
     }
-    constexpr int KP = 4, VP = 8;                   // new row: up to 512 elements (n_kv <= 8)
-    float k0[KP], k1[KP], vn[VP];
-    if (FUSED && w == 0) {
-        const int npairs = fz.n_kv * HALF, nrow = fz.n_kv * D;
-#pragma unroll
-        for (int p = 0; p < KP; ++p) {
-            const int i = min(lane + 64 * p, npairs - 1), hh = i / HALF, j = i - hh * HALF;
-            k0[p] = fz.k_new[hh * D + j];
-            k1[p] = fz.k_new[hh * D + j + HALF];
-        }
-#pragma unroll
-        for (int p = 0; p < VP; ++p) vn[p] = fz.v_new[min(lane + 64 * p, nrow - 1)];
+    // The new row (fused; n_kv <= 8, so at most 512 elements): thread t holds K
+    // RoPE pair t and V element t.
+    constexpr int NT = 64 * NW;
+    const int npairs = FUSED ? fz.n_kv * HALF : 0, nrow = FUSED ? fz.n_kv * D : 0;
+    float k0 = 0.f, k1 = 0.f, vn = 0.f;
+    if constexpr (FUSED) {
+        const int i = min(tid, npairs - 1), hh = i / HALF, j = i - hh * HALF;
+        k0 = fz.k_new[hh * D + j];
+        k1 = fz.k_new[hh * D + j + HALF];
+        vn = fz.v_new[min(tid, nrow - 1)];
     }
     // A round's K/V in registers: K row of token base+lane, V pieces of tokens base+tg+16j.
     uint4 kr[kSPDepth][KW], vr[kSPDepth][4][VW];
@@ -459,78 +458,28 @@ __global__ __launch_bounds__(64 * kSPWaves) void attn_decode_single_kernel(
     const int pos = FUSED ? dpos : -1;
     const bool rot = FUSED && pos < fz.max_seq;      // rope.hpp:84: positions >= max_seq stay unrotated
 
-    // ---- wave 0: q of head h and (fused) the new K/V row ------------------------
-    if (w == 0) {
-        float rc = 1.f, rs = 0.f;
-        if constexpr (FUSED) {
-            const int trow = min(pos, fz.max_seq - 1);
-            rc = fz.cos_t[(size_t)trow * HALF + (lane & (HALF - 1))];
-            rs = fz.sin_t[(size_t)trow * HALF + (lane & (HALF - 1))];
-        }
-        if (lane < HALF) {
-            if (rot) rope2(q0, q1, rc, rs, &qs[lane], &qs[lane + HALF]);
-            else { qs[lane] = q0; qs[lane + HALF] = q1; }
-        }
-        if constexpr (FUSED) {
-            // attention.hpp:109-128: RoPE on k, then KVCache::append stores the row
-            // before attention reads it back: Q8_0 quantizes the whole row
-            // (kv_cache.hpp:102-117), F16 converts each element (:68-97), F32 copies.
-            const int npairs = fz.n_kv * HALF, nrow = fz.n_kv * D;
-            float ak = 0.f, av = 0.f;
-#pragma unroll
-            for (int p = 0; p < KP; ++p)
-                if (lane + 64 * p < npairs) {
-                    if (rot) rope2(k0[p], k1[p], rc, rs, &k0[p], &k1[p]);
-                    ak = fmaxf(ak, fmaxf(fabsf(k0[p]), fabsf(k1[p])));
-                }
-            float sk = 1.f, sv = 1.f, ik = 0.f, iv = 0.f;
-            if constexpr (Q8) {
-#pragma unroll
-                for (int p = 0; p < VP; ++p)
-                    if (lane + 64 * p < nrow) av = fmaxf(av, fabsf(vn[p]));
-                ak = wave_max(ak);
-                av = wave_max(av);
-                sk = ak != 0.f ? ak / 127.f : 0.f;
-                sv = av != 0.f ? av / 127.f : 0.f;
-                ik = ak != 0.f ? 1.f / sk : 0.f;
-                iv = av != 0.f ? 1.f / sv : 0.f;
-            }
-            // the group's first head stores head g's elements (never past the cache)
-            const bool writer = h % REP == 0 && pos < cap;
-            int8_t* krow = fz.kq_w + (hb + (size_t)pos * D) * EB;
-            int8_t* vrow = fz.vq_w + (hb + (size_t)pos * D) * EB;
-            // stores element j of a row (when writer) and returns the value attention reads back
-            auto put = [&](int8_t* row, int j, float x, float sc, float inv, bool nz) -> float {
-                if constexpr (Q8) {
-                    const int c = nz ? min(127, max(-127, (int)roundf(x * inv))) : 0;
-                    if (writer) row[j] = (int8_t)c;
-                    return (float)c * sc;
-                } else if constexpr (H16) {
-                    const uint16_t hb16 = f32_to_f16_kv(x);
-                    if (writer) reinterpret_cast<uint16_t*>(row)[j] = hb16;
-                    return f16_bits_to_f32(hb16);
-                } else {
-                    if (writer) reinterpret_cast<float*>(row)[j] = x;
-                    return x;
-                }
-            };
-#pragma unroll
-            for (int p = 0; p < KP; ++p) {
-                const int i = lane + 64 * p;
-                if (i < npairs && i / HALF == g) {
-                    const int j = i % HALF;
-                    nk[j] = put(krow, j, k0[p], sk, ik, ak != 0.f);
-                    nk[j + HALF] = put(krow, j + HALF, k1[p], sk, ik, ak != 0.f);
-                }
-            }
-#pragma unroll
-            for (int p = 0; p < VP; ++p) {
-                const int i = lane + 64 * p;
-                if (i < nrow && i / D == g) nv[i % D] = put(vrow, i % D, vn[p], sv, iv, av != 0.f);
-            }
-            if constexpr (Q8) {
-                if (h == 0 && lane == 0 && pos < cap) { fz.ks_w[pos] = sk; fz.vs_w[pos] = sv; }
-            }
+    // ---- q of head h (wave 0) and, fused, the new row's RoPE and maxima -------------
+    // Every RoPE pair a thread rotates has pair index tid % HALF.
+    float rc = 1.f, rs = 0.f;
+    if constexpr (FUSED) {
+        const int trow = min(pos, fz.max_seq - 1);
+        rc = fz.cos_t[(size_t)trow * HALF + (lane & (HALF - 1))];
+        rs = fz.sin_t[(size_t)trow * HALF + (lane & (HALF - 1))];
+    }
+    if (w == 0 && lane < HALF) {
+        if (rot) rope2(q0, q1, rc, rs, &qs[lane], &qs[lane + HALF]);
+        else { qs[lane] = q0; qs[lane + HALF] = q1; }
+    }
+    if constexpr (FUSED) {
+        // attention.hpp:109-128: RoPE on k, then KVCache::append stores the row
+        // before attention reads it back: Q8_0 quantizes the whole row with one
+        // scale (kv_cache.hpp:102-117); the row maxima are merged through LDS and
+        // the row is quantized after the rounds, off their critical path.
+        if (tid < npairs && rot) rope2(k0, k1, rc, rs, &k0, &k1);
+        if constexpr (Q8) {
+            float ak = wave_max(tid < npairs ? fmaxf(fabsf(k0), fabsf(k1)) : 0.f);
+            float av = wave_max(tid < nrow ? fabsf(vn) : 0.f);
+            if (lane == 0) { amax[w] = ak; amax[NW + w] = av; }
         }
     }
     __syncthreads();
@@ -584,6 +533,51 @@ __global__ __launch_bounds__(64 * kSPWaves) void attn_decode_single_kernel(
         }
         __builtin_amdgcn_wave_barrier();               // pbuf is rewritten next round
         if (r + kSPDepth < kSPRounds && (r + kSPDepth) * NW + w < nrounds) load_round(r + kSPDepth, b);
+    }
+
+    // ---- fused: quantize and store the new row; the merge reads it back from LDS -----
+    // (F16 converts each element, kv_cache.hpp:68-97; F32 copies.)  The group's
+    // first head stores head g's elements, never past the cache.
+    if constexpr (FUSED) {
+        float ak = 0.f, av = 0.f, sk = 1.f, sv = 1.f, ik = 0.f, iv = 0.f;
+        if constexpr (Q8) {
+#pragma unroll
+            for (int k = 0; k < NW; ++k) {
+                ak = fmaxf(ak, amax[k]);
+                av = fmaxf(av, amax[NW + k]);
+            }
+            sk = ak != 0.f ? ak / 127.f : 0.f;
+            sv = av != 0.f ? av / 127.f : 0.f;
+            ik = ak != 0.f ? 1.f / sk : 0.f;
+            iv = av != 0.f ? 1.f / sv : 0.f;
+        }
+        const bool writer = h % REP == 0 && pos < cap;
+        int8_t* krow = fz.kq_w + (hb + (size_t)pos * D) * EB;
+        int8_t* vrow = fz.vq_w + (hb + (size_t)pos * D) * EB;
+        // stores element j of a row (when writer) and returns the value attention reads back
+        auto put = [&](int8_t* row, int j, float x, float sc, float inv, bool nz) -> float {
+            if constexpr (Q8) {
+                const int c = nz ? min(127, max(-127, (int)roundf(x * inv))) : 0;
+                if (writer) row[j] = (int8_t)c;
+                return (float)c * sc;
+            } else if constexpr (H16) {
+                const uint16_t hb16 = f32_to_f16_kv(x);
+                if (writer) reinterpret_cast<uint16_t*>(row)[j] = hb16;
+                return f16_bits_to_f32(hb16);
+            } else {
+                if (writer) reinterpret_cast<float*>(row)[j] = x;
+                return x;
+            }
+        };
+        if (tid < npairs && tid / HALF == g) {
+            const int j = tid % HALF;
+            nk[j] = put(krow, j, k0, sk, ik, ak != 0.f);
+            nk[j + HALF] = put(krow, j + HALF, k1, sk, ik, ak != 0.f);
+        }
+        if (tid < nrow && tid / D == g) nv[tid % D] = put(vrow, tid % D, vn, sv, iv, av != 0.f);
+        if constexpr (Q8) {
+            if (h == 0 && tid == 0 && pos < cap) { fz.ks_w[pos] = sk; fz.vs_w[pos] = sv; }
+        }
     }
 
     // ---- merge: lanes of a dim group, then the waves -------------------------------
