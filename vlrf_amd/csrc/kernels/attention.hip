@@ -214,9 +214,15 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_partial_kernel(
         }
     }
     __syncthreads();
+    // The row's stored form stays in registers and is written to the cache at
+    // the end of the kernel: one counter covers vector loads and stores, so a
+    // store issued here would make the later waits for the cache stream wait
+    // for the store as well.
+    uint32_t kb0 = 0, kb1 = 0, vb0 = 0, vb1 = 0;
+    float sk = 1.f, sv = 1.f;
     if constexpr (FUSED) {
         if (has_new) {
-            float ak = 0.f, av = 0.f, sk = 1.f, sv = 1.f, ik = 0.f, iv = 0.f;
+            float ak = 0.f, av = 0.f, ik = 0.f, iv = 0.f;
             if constexpr (Q8) {
 #pragma unroll
                 for (int w = 0; w < NW; ++w) {
@@ -228,35 +234,29 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_partial_kernel(
                 ik = ak != 0.f ? 1.f / sk : 0.f;
                 iv = av != 0.f ? 1.f / sv : 0.f;
             }
-            int8_t* krow_w = fz.kq_w + (hb + (size_t)pos * D) * EB;
-            int8_t* vrow_w = fz.vq_w + (hb + (size_t)pos * D) * EB;
             float* vnew = vsm[pos - c0];
-            // stores element j of a row and returns the value attention reads back
-            auto put = [&](int8_t* row, int j, float x, float sc, float inv, bool nz) -> float {
+            // the stored bits of one element; *back = the value attention reads back
+            auto enc = [&](float x, float sc, float inv, bool nz, float* back) -> uint32_t {
                 if constexpr (Q8) {
                     const int c = nz ? min(127, max(-127, (int)roundf(x * inv))) : 0;
-                    row[j] = (int8_t)c;
-                    return (float)c * sc;
+                    *back = (float)c * sc;
+                    return (uint32_t)c;
                 } else if constexpr (H16) {
-                    const uint16_t h = f32_to_f16_kv(x);
-                    reinterpret_cast<uint16_t*>(row)[j] = h;
-                    return f16_bits_to_f32(h);
+                    const uint16_t hb16 = f32_to_f16_kv(x);
+                    *back = f16_bits_to_f32(hb16);
+                    return hb16;
                 } else {
-                    reinterpret_cast<float*>(row)[j] = x;
-                    return x;
+                    *back = x;
+                    return __float_as_uint(x);
                 }
             };
             if (tid < npairs && tid / HALF == g) {
                 const int j = tid % HALF;
-                newk[j] = put(krow_w, j, nk0, sk, ik, ak != 0.f);
-                newk[j + HALF] = put(krow_w, j + HALF, nk1, sk, ik, ak != 0.f);
+                kb0 = enc(nk0, sk, ik, ak != 0.f, &newk[j]);
+                kb1 = enc(nk1, sk, ik, ak != 0.f, &newk[j + HALF]);
             }
-            if (tid < nrow && tid / D == g) vnew[tid % D] = put(vrow_w, tid % D, nv0, sv, iv, av != 0.f);
-            if (tid + NT < nrow && (tid + NT) / D == g)
-                vnew[(tid + NT) % D] = put(vrow_w, (tid + NT) % D, nv1, sv, iv, av != 0.f);
-            if constexpr (Q8) {
-                if (g == 0 && tid == 0) { fz.ks_w[pos] = sk; fz.vs_w[pos] = sv; }
-            }
+            if (tid < nrow && tid / D == g) vb0 = enc(nv0, sv, iv, av != 0.f, &vnew[tid % D]);
+            if (tid + NT < nrow && (tid + NT) / D == g) vb1 = enc(nv1, sv, iv, av != 0.f, &vnew[(tid + NT) % D]);
             __syncthreads();   // the stored K row, before the scores read it
         }
     }
@@ -342,6 +342,27 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_partial_kernel(
     if (tid < REP) {
         pout[(size_t)tid * n_splits * (D + 2) + D] = mstat[tid];
         pout[(size_t)tid * n_splits * (D + 2) + D + 1] = lstat[tid];
+    }
+    // ---- fused: the new row into the cache (head g's elements; KV head 0 the scales)
+    if constexpr (FUSED) {
+        if (has_new) {
+            int8_t* krow_w = fz.kq_w + (hb + (size_t)pos * D) * EB;
+            int8_t* vrow_w = fz.vq_w + (hb + (size_t)pos * D) * EB;
+            auto st = [&](int8_t* row, int j, uint32_t b) {
+                if constexpr (Q8) row[j] = (int8_t)b;
+                else if constexpr (H16) reinterpret_cast<uint16_t*>(row)[j] = (uint16_t)b;
+                else reinterpret_cast<uint32_t*>(row)[j] = b;
+            };
+            if (tid < npairs && tid / HALF == g) {
+                st(krow_w, tid % HALF, kb0);
+                st(krow_w, tid % HALF + HALF, kb1);
+            }
+            if (tid < nrow && tid / D == g) st(vrow_w, tid % D, vb0);
+            if (tid + NT < nrow && (tid + NT) / D == g) st(vrow_w, (tid + NT) % D, vb1);
+            if constexpr (Q8) {
+                if (g == 0 && tid == 0) { fz.ks_w[pos] = sk; fz.vs_w[pos] = sv; }
+            }
+        }
     }
 }
 
