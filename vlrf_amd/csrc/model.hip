@@ -458,28 +458,34 @@ int prefill_reserve(vlrf_hip_model* m, int T) {
     return VLRF_HIP_OK;
 }
 
-// All layers over T embedded rows x (device [T][D], updated in place) at cache
-// positions m->pos..: TransformerBlock::forward_v2 pre-norm order
-// (transformer_block.hpp:141-159) with AttentionBlock::forward's T > 1 path
-// (attention.hpp:89-186: RoPE, K/V appended to the cache, causal attention).
-int enqueue_prefill_layers(vlrf_hip_model* m, float* x, int T) {
+// All layers over T embedded rows (device [T][D]) at cache positions m->pos..:
+// TransformerBlock::forward_v2 pre-norm order (transformer_block.hpp:141-159)
+// with AttentionBlock::forward's T > 1 path (attention.hpp:89-186: RoPE, K/V
+// appended to the cache, causal attention).  Layer 0 reads the rows from
+// x_in, the residual stream lives in pf_x, and the last layer's down
+// projection writes x_out (either may be pf_x; x_out may be x_in), so the
+// rows are never copied in or out.
+int enqueue_prefill_layers(vlrf_hip_model* m, const float* x_in, float* x_out, int T) {
     hipStream_t s = m->ctx->stream;
     const float eps = m->cfg.norm_eps;
     const float scale = 1.f / std::sqrt((float)m->dh);          // attention.hpp:373-374
     const int ld = m->D + 2 * m->dkv;
+    float* x = m->pf_x;
     int rc = VLRF_HIP_OK;
     for (int l = 0; l < m->L && !rc; ++l) {
         Layer& Ly = m->layers[l];
-        rc = launch_rows_to_bf16(s, x, Ly.ln1, m->pf_a, T, m->D, eps);
+        const float* src = l == 0 ? x_in : x;                    // the stream entering layer l
+        float* dst = l == m->L - 1 ? x_out : x;                  // and leaving it
+        rc = launch_rows_to_bf16(s, src, Ly.ln1, m->pf_a, T, m->D, eps);
         if (!rc) rc = launch_qgemm(s, Ly.wqkv, m->pf_a, T, nullptr, m->pf_qkv);
         if (!rc) rc = launch_prefill_rope_append(s, Ly.kv, m->pf_qkv, ld, T, m->H, m->G, m->dh, m->S, m->pos,
                                                  m->cos_t, m->sin_t);
         if (!rc) rc = launch_attn_prefill(s, m->pf_qkv, ld, Ly.kv, T, m->pos, m->H, m->G, m->dh, m->S, scale,
                                           m->pf_att);
-        if (!rc) rc = launch_qgemm(s, Ly.wo, m->pf_att, T, x, x);              // x += att . Wo^T
+        if (!rc) rc = launch_qgemm(s, Ly.wo, m->pf_att, T, src, x);            // x = src + att . Wo^T
         if (!rc) rc = launch_rows_to_bf16(s, x, Ly.ln2, m->pf_a, T, m->D, eps);
         if (!rc) rc = launch_qgemm_swiglu(s, Ly.wg, Ly.wu, m->pf_a, T, m->pf_h, true);
-        if (!rc) rc = launch_qgemm(s, Ly.wd, m->pf_h, T, x, x);                // x += h . Wd^T
+        if (!rc) rc = launch_qgemm(s, Ly.wd, m->pf_h, T, x, dst);              // dst = x + h . Wd^T
     }
     return rc;
 }
@@ -506,9 +512,7 @@ int vlrf_hip_model_forward_hidden(vlrf_hip_model_t m, const float* x, int T, flo
     if (rc) return rc;
     VH_ARG(x && out, "forward_hidden: null buffer");
     hipStream_t s = m->ctx->stream;
-    VH_CHECK(hipMemcpyAsync(m->pf_x, x, (size_t)T * m->D * 4, hipMemcpyDeviceToDevice, s));
-    if ((rc = enqueue_prefill_layers(m, m->pf_x, T))) return rc;
-    VH_CHECK(hipMemcpyAsync(out, m->pf_x, (size_t)T * m->D * 4, hipMemcpyDeviceToDevice, s));
+    if ((rc = enqueue_prefill_layers(m, x, out, T))) return rc;
     m->pos += T;
     m->pinned[0] = 0;
     m->pinned[1] = m->pos;
@@ -527,7 +531,7 @@ int vlrf_hip_model_prefill_mfma(vlrf_hip_model_t m, const int32_t* ids, int n, i
     hipStream_t s = m->ctx->stream;
     VH_CHECK(hipMemcpyAsync(m->pf_ids, ids, (size_t)n * sizeof(int), hipMemcpyHostToDevice, s));
     if ((rc = launch_embed_rows(s, m->embed, m->pf_ids, m->pf_x, n, m->D))) return rc;   // ops.hpp:615-626
-    if ((rc = enqueue_prefill_layers(m, m->pf_x, n))) return rc;
+    if ((rc = enqueue_prefill_layers(m, m->pf_x, m->pf_x, n))) return rc;
     // transformer.hpp:399-414: final norm and LM head on the last row, greedy argmax.
     if ((rc = launch_qlinear(s, m->lm_head, m->pf_x + (size_t)(n - 1) * m->D, m->logits, 1, m->ln_final,
                              m->cfg.norm_eps, nullptr)))
