@@ -118,6 +118,11 @@ int launch_qlinear(hipStream_t s, const DevWeight& w, const float* x, float* y, 
                    const float* norm_w, float eps, const float* residual);
 // y = rmsnorm(table[*row]) . W^T (M = 1, Q8_0/Q4_0): the embedding gather fused
 // into the first projection; the raw row is also copied to x_copy.
+// y = W . x + residual (M = 1) where x is the decode attention output in its
+// chunked form (DecodeFuse::chunks, nch chunks per head), merged in the GEMV's
+// prologue.
+int launch_qlinear_merge(hipStream_t s, const DevWeight& w, const float* chunks, int nch, const float* residual,
+                         float* y);
 int launch_qlinear_gather(hipStream_t s, const DevWeight& w, const float* table, const int* row,
                           float* x_copy, float* y, const float* norm_w, float eps);
 bool qlinear_gather_supported(const DevWeight& w);
@@ -193,7 +198,18 @@ struct DecodeFuse {
     float* ks_w = nullptr;          // Q8_0 row scales
     float* vs_w = nullptr;
     int n_kv = 0, max_seq = 0;
+    // Chunked form (nch > 0, see attn_decode_chunks): per query head and chunk
+    // of the cache, the partial (acc[0..d-1] unnormalised, m, l) at
+    // chunks[(h*nch + s)*kAttnChunkStride], merged by the next GEMV's prologue
+    // (launch_qlinear_merge) instead of a combine launch.
+    float* chunks = nullptr;
+    int nch = 0;
 };
+constexpr int kAttnChunkStride = 68, kAttnMaxChunks = 16;
+// Chunks of the decode attention's chunked form for a cache of cap rows, or 0
+// where it does not apply (d_head != 64, more than 8 KV heads, caches the
+// single-pass kernel covers, or more than kAttnMaxChunks chunks).
+int attn_decode_chunks(int cap, int d_head, int n_kv);
 
 // Split-K decode attention over K/V elements of kv_dtype (VLRF_KV_Q8_0 codes
 // with row scales ks/vs, VLRF_KV_F16 bits, VLRF_KV_F32) laid out

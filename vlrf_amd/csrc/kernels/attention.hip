@@ -390,6 +390,10 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_partial_kernel(
 // rows.
 constexpr int kSPWaves = 8, kSPRounds = 1, kSPDepth = 1;   // rounds per wave, rounds in flight
 constexpr int kSPMaxCtx = kSPWaves * 64 * kSPRounds;   // cache rows the single pass covers
+// Chunked form (CH tokens per workgroup, one query head each): partials of
+// kChunkStride floats -- acc[0..63] (unnormalised), m at 64, l at 65 --
+// merged by the next GEMV's prologue.
+constexpr int kCH = 256, kChunkStride = kAttnChunkStride;
 
 // Elements 4i..4i+3 of a 64-element row held as 16-byte words, as f32.
 template <int KVT>
@@ -410,13 +414,18 @@ __device__ __forceinline__ float4 row4(const uint4* wds, int i) {
     }
 }
 
-template <int KVT, int REP, bool FUSED>
-__global__ __launch_bounds__(64 * kSPWaves) void attn_decode_single_kernel(
+// CH > 0 (fused decode only): the same algorithm on one CH-token chunk of the
+// cache per workgroup, NW = CH/64 waves of one round, for query head h of
+// chunk s; the result is the chunk's partial (m, l, acc) at out[h][s][*]
+// (kChunkStride floats), the new token merged only by the chunk holding it.
+template <int KVT, int REP, bool FUSED, int CH = 0>
+__global__ __launch_bounds__(CH ? CH : 64 * kSPWaves) void attn_decode_single_kernel(
     const float* __restrict__ q, const int8_t* kc, const int8_t* vc, const float* ks, const float* vs,
     long head_stride, int ctx_len, const int* __restrict__ ctx_dev, float scale, float* __restrict__ out,
-    DecodeFuse fz) {
+    DecodeFuse fz, int nch) {
+    static_assert(CH == 0 || (FUSED && CH % 64 == 0), "chunks: fused decode, whole rounds");
     constexpr bool Q8 = KVT == VLRF_KV_Q8_0, H16 = KVT == VLRF_KV_F16;
-    constexpr int D = 64, HALF = 32, NW = kSPWaves;
+    constexpr int D = 64, HALF = 32, NW = CH ? CH / 64 : kSPWaves;
     constexpr int EB = Q8 ? 1 : H16 ? 2 : 4;         // bytes per element
     constexpr int KW = D * EB / 16, VW = EB;         // 16-byte words: a K row, a 16-element V piece
     __shared__ __align__(16) float qs[D];
@@ -426,7 +435,21 @@ __global__ __launch_bounds__(64 * kSPWaves) void attn_decode_single_kernel(
     __shared__ float wm[NW], wl[NW];
     __shared__ __align__(16) float wacc[NW][D];
 
-    const int h = blockIdx.x, g = h / REP;
+    int h, g, c0 = 0, chunk = 0;
+    if constexpr (CH > 0) {
+        // The REP query heads of chunk (g, s) run on one XCD (workgroup b on XCD
+        // b % 8), so the chunk's K/V rows come from HBM once and then from that
+        // L2; placement only affects speed.
+        const int b = blockIdx.x, k = b >> 3, r = k % REP, pc = (b & 7) + 8 * (k / REP);
+        if (pc >= fz.n_kv * nch) return;
+        g = pc / nch;
+        chunk = pc - g * nch;
+        h = g * REP + r;
+        c0 = chunk * CH;
+    } else {
+        h = blockIdx.x;
+        g = h / REP;
+    }
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int tg = lane >> 2, dg = lane & 3;
     const int cap = (int)(head_stride / D);
@@ -441,21 +464,23 @@ __global__ __launch_bounds__(64 * kSPWaves) void attn_decode_single_kernel(
         q1 = q[(size_t)h * D + j + HALF];
     }
     // The new row (fused; n_kv <= 8, so at most 512 elements): thread t holds K
-    // RoPE pair t and V element t.
+    // RoPE pair t and V elements t and (with 256 threads) t + NT.
     constexpr int NT = 64 * NW;
+    constexpr bool V2 = NT < 512;
     const int npairs = FUSED ? fz.n_kv * HALF : 0, nrow = FUSED ? fz.n_kv * D : 0;
-    float k0 = 0.f, k1 = 0.f, vn = 0.f;
+    float k0 = 0.f, k1 = 0.f, vn = 0.f, vn2 = 0.f;
     if constexpr (FUSED) {
         const int i = min(tid, npairs - 1), hh = i / HALF, j = i - hh * HALF;
         k0 = fz.k_new[hh * D + j];
         k1 = fz.k_new[hh * D + j + HALF];
         vn = fz.v_new[min(tid, nrow - 1)];
+        if constexpr (V2) vn2 = fz.v_new[min(tid + NT, nrow - 1)];
     }
     // A round's K/V in registers: K row of token base+lane, V pieces of tokens base+tg+16j.
     uint4 kr[kSPDepth][KW], vr[kSPDepth][4][VW];
     float ksr[kSPDepth], vsr[kSPDepth];
     auto load_round = [&](int r, int b) {
-        const int base = (r * NW + w) * 64;
+        const int base = c0 + (r * NW + w) * 64;
         const int t = min(base + lane, cap - 1);
 #pragma unroll
         for (int i = 0; i < KW; ++i)
@@ -478,6 +503,15 @@ __global__ __launch_bounds__(64 * kSPWaves) void attn_decode_single_kernel(
     ctx = min(ctx, cap);
     const int pos = FUSED ? dpos : -1;
     const bool rot = FUSED && pos < fz.max_seq;      // rope.hpp:84: positions >= max_seq stay unrotated
+    const bool has_new = FUSED && (CH == 0 || (pos >= c0 && pos < c0 + CH));
+    if constexpr (CH > 0) {
+        if (c0 >= ctx) {                             // chunk past the context: empty partial
+            float* pp = out + ((size_t)h * nch + chunk) * kChunkStride;
+            if (tid < D) pp[tid] = 0.f;
+            if (tid == 0) { pp[D] = kNegInf; pp[D + 1] = 0.f; }
+            return;
+        }
+    }
 
     // ---- q of head h (wave 0) and, fused, the new row's RoPE and maxima -------------
     // Every RoPE pair a thread rotates has pair index tid % HALF.
@@ -496,24 +530,28 @@ __global__ __launch_bounds__(64 * kSPWaves) void attn_decode_single_kernel(
         // before attention reads it back: Q8_0 quantizes the whole row with one
         // scale (kv_cache.hpp:102-117); the row maxima are merged through LDS and
         // the row is quantized after the rounds, off their critical path.
-        if (tid < npairs && rot) rope2(k0, k1, rc, rs, &k0, &k1);
-        if constexpr (Q8) {
-            float ak = wave_max(tid < npairs ? fmaxf(fabsf(k0), fabsf(k1)) : 0.f);
-            float av = wave_max(tid < nrow ? fabsf(vn) : 0.f);
-            if (lane == 0) { amax[w] = ak; amax[NW + w] = av; }
+        if (has_new) {
+            if (tid < npairs && rot) rope2(k0, k1, rc, rs, &k0, &k1);
+            if constexpr (Q8) {
+                float ak = wave_max(tid < npairs ? fmaxf(fabsf(k0), fabsf(k1)) : 0.f);
+                float av = tid < nrow ? fabsf(vn) : 0.f;
+                if (V2 && tid + NT < nrow) av = fmaxf(av, fabsf(vn2));
+                av = wave_max(av);
+                if (lane == 0) { amax[w] = ak; amax[NW + w] = av; }
+            }
         }
     }
     __syncthreads();
 
     // ---- rounds ----------------------------------------------------------------------
-    const int nrounds = (ctx + 63) / 64;
+    const int nrounds = (ctx - c0 + 63) / 64;
     float m_run = kNegInf, l_run = 0.f, acc[16];
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[e] = 0.f;
 #pragma unroll
     for (int r = 0; r < kSPRounds; ++r) {
         if (r * NW + w >= nrounds) break;
-        const int b = r % kSPDepth, base = (r * NW + w) * 64;
+        const int b = r % kSPDepth, base = c0 + (r * NW + w) * 64;
         // scores: lane = token base + lane; the new token (fused) is merged at the end
         const int t = base + lane;
         float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
@@ -559,7 +597,7 @@ __global__ __launch_bounds__(64 * kSPWaves) void attn_decode_single_kernel(
     // ---- fused: quantize and store the new row; the merge reads it back from LDS -----
     // (F16 converts each element, kv_cache.hpp:68-97; F32 copies.)  The group's
     // first head stores head g's elements, never past the cache.
-    if constexpr (FUSED) {
+    if (FUSED && has_new) {
         float ak = 0.f, av = 0.f, sk = 1.f, sv = 1.f, ik = 0.f, iv = 0.f;
         if constexpr (Q8) {
 #pragma unroll
@@ -596,6 +634,8 @@ __global__ __launch_bounds__(64 * kSPWaves) void attn_decode_single_kernel(
             nk[j + HALF] = put(krow, j + HALF, k1, sk, ik, ak != 0.f);
         }
         if (tid < nrow && tid / D == g) nv[tid % D] = put(vrow, tid % D, vn, sv, iv, av != 0.f);
+        if (V2 && tid + NT < nrow && (tid + NT) / D == g)
+            nv[(tid + NT) % D] = put(vrow, (tid + NT) % D, vn2, sv, iv, av != 0.f);
         if constexpr (Q8) {
             if (h == 0 && tid == 0 && pos < cap) { fz.ks_w[pos] = sk; fz.vs_w[pos] = sv; }
         }
@@ -623,7 +663,7 @@ __global__ __launch_bounds__(64 * kSPWaves) void attn_decode_single_kernel(
     if (tid < D) {
         // The new token (fused): score q . k_stored, weight 1, value its stored V row.
         float sn = kNegInf;
-        if constexpr (FUSED) {
+        if (FUSED && has_new) {
             float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
 #pragma unroll
             for (int i = 0; i < D / 4; ++i) {
@@ -640,7 +680,7 @@ __global__ __launch_bounds__(64 * kSPWaves) void attn_decode_single_kernel(
 #pragma unroll
         for (int k = 0; k < NW; ++k) mt = fmaxf(mt, wm[k]);
         float lt = 0.f, ot = 0.f;
-        if (FUSED) {
+        if (FUSED && has_new) {
             lt = expf(sn - mt);
             ot = lt * nv[tid];
         }
@@ -652,7 +692,13 @@ __global__ __launch_bounds__(64 * kSPWaves) void attn_decode_single_kernel(
                 ot += c * wacc[k][tid];
             }
         }
-        out[(size_t)h * D + tid] = lt > 0.f ? ot * (1.f / lt) : 0.f;
+        if constexpr (CH > 0) {                      // the chunk's partial, unnormalised
+            float* pp = out + ((size_t)h * nch + chunk) * kChunkStride;
+            pp[tid] = ot;
+            if (tid == 0) { pp[D] = mt; pp[D + 1] = lt; }
+        } else {
+            out[(size_t)h * D + tid] = lt > 0.f ? ot * (1.f / lt) : 0.f;
+        }
     }
 }
 
@@ -1063,6 +1109,11 @@ __global__ __launch_bounds__(64) void attn_f32_tiled_kernel(const float* __restr
 
 int attn_decode_splits(int max_ctx) { return (max_ctx + kChunk - 1) / kChunk; }
 
+int attn_decode_chunks(int cap, int d_head, int n_kv) {
+    const int n = (cap + kCH - 1) / kCH;
+    return d_head == 64 && n_kv <= 8 && cap > kSPMaxCtx && n <= kAttnMaxChunks ? n : 0;
+}
+
 int launch_attn_decode(hipStream_t s, const float* q, const void* kc, const void* vc, const float* ks,
                        const float* vs, int kv_dtype, long head_stride, int n_heads, int n_kv, int d_head,
                        int ctx_len, const int* ctx_dev, int n_splits, float scale, float* part, float* out,
@@ -1088,10 +1139,36 @@ int launch_attn_decode(hipStream_t s, const float* q, const void* kc, const void
     }
     const int8_t* k8 = static_cast<const int8_t*>(kc);
     const int8_t* v8 = static_cast<const int8_t*>(vc);
+    if (fuse && fz.nch > 0) {
+        // Chunked form: REP workgroups per (KV head, chunk), grouped by XCD
+        // (8 slots per group of 8 chunk indices); partials for the next GEMV.
+        VH_ARG(fz.chunks && fz.nch == attn_decode_chunks((int)(head_stride / d_head), d_head, n_kv),
+               "attn_decode: chunked form for %d chunks does not apply", fz.nch);
+        const dim3 cgrid(8 * rep * ((n_kv * fz.nch + 7) / 8));
+#define VH_CHK(KT, R)                                                                                         \
+    hipLaunchKernelGGL((attn_decode_single_kernel<KT, R, true, kCH>), cgrid, dim3(kCH), 0, s, q, k8, v8, ks, vs, \
+                       head_stride, ctx_len, ctx_dev, scale, fz.chunks, fz, fz.nch)
+#define VH_CHK_R(KT)                     \
+    switch (rep) {                       \
+        case 1: VH_CHK(KT, 1); break;    \
+        case 2: VH_CHK(KT, 2); break;    \
+        case 4: VH_CHK(KT, 4); break;    \
+        default: VH_CHK(KT, 8); break;   \
+    }
+        switch (kv_dtype) {
+            case VLRF_KV_Q8_0: VH_CHK_R(VLRF_KV_Q8_0) break;
+            case VLRF_KV_F16: VH_CHK_R(VLRF_KV_F16) break;
+            default: VH_CHK_R(VLRF_KV_F32) break;
+        }
+#undef VH_CHK_R
+#undef VH_CHK
+        VH_LAUNCHED();
+        return VLRF_HIP_OK;
+    }
     if (d_head == 64 && head_stride / d_head <= kSPMaxCtx && (!fuse || n_kv <= 8)) {
 #define VH_SP(KT, R, FU)                                                                                     \
     hipLaunchKernelGGL((attn_decode_single_kernel<KT, R, FU>), dim3(n_heads), dim3(64 * kSPWaves), 0, s, q, k8, \
-                       v8, ks, vs, head_stride, ctx_len, ctx_dev, scale, out, fz)
+                       v8, ks, vs, head_stride, ctx_len, ctx_dev, scale, out, fz, 0)
 #define VH_SP_R(KT, FU)                       \
     switch (rep) {                            \
         case 1: VH_SP(KT, 1, FU); break;      \

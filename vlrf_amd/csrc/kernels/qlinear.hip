@@ -197,6 +197,7 @@ struct Gemv<VLRF_DT_Q8_0> { static constexpr int EPL = 16; static constexpr floa
 template <>
 struct Gemv<VLRF_DT_Q4_0> { static constexpr int EPL = 32; static constexpr float BIAS = 8.f; };
 
+constexpr float kNegInfF = -INFINITY;
 constexpr int kGemvMaxK = 6144;          // staged activations: 24 KiB of LDS
 constexpr int kGemvMaxGroups = 512;      // workgroups of the row loop (2 per CU)
 constexpr int kGemvWaves = 8;            // waves per workgroup (one staged copy of x)
@@ -320,16 +321,22 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(
     const uint8_t* __restrict__ qa, const __half* __restrict__ da, const uint8_t* __restrict__ qb,
     const __half* __restrict__ db, int N, int K, const float* __restrict__ x,
     const int* __restrict__ x_row, float* x_copy, const float* __restrict__ norm_w, float eps,
-    const float* residual, float* y) {
+    const float* residual, float* y, int nparts) {
     constexpr int EPL = Gemv<WT>::EPL;
     constexpr int CW = 64 * EPL;
     constexpr int NM = SWIGLU ? 2 : 1;
     constexpr int NT = 64 * kGemvWaves;
     constexpr bool RES = XM & 4;
+    // XM & 8: x is decode attention output in its chunked form (head dim 64):
+    // element e is dim e % 64 of head e / 64, merged here from the nparts
+    // chunk partials of that head (log-sum-exp, attention.hpp:207-309's rule).
+    constexpr bool MERGE = XM & 8;
+    constexpr int NP = MERGE ? kAttnMaxChunks : 1;
     constexpr int XF4 = NC * CW / 4;                  // staged float4 slots
     constexpr int PER = (XF4 + NT - 1) / NT;          // float4 per thread
     __shared__ float4 xs4[XF4];
     __shared__ float red[kGemvWaves];
+    __shared__ float2 mls[MERGE ? kGemvMaxK / 64 * kAttnMaxChunks : 1];   // (m, l) per head and chunk
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nwaves = gridDim.x * kGemvWaves;
@@ -352,12 +359,35 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(
         constexpr bool NORM = XM & 1, GATHER = XM & 2;
         const float* xs = GATHER ? x + (size_t)(*x_row) * K : x;
         float4 v[PER], gw[PER];
+        float4 pa[PER][NP];
+        float2 ml[MERGE ? (kGemvMaxK / 64 * kAttnMaxChunks + NT - 1) / NT : 1];
+        if constexpr (MERGE) {
+            // (m, l) of every head and chunk once per workgroup, first: they are
+            // shared by the 16 threads of a head and staged in LDS below.
+            const int nml = (K >> 6) * nparts;
+#pragma unroll
+            for (int i = 0; i < (int)(sizeof(ml) / sizeof(ml[0])); ++i) {
+                const int k = tid + i * NT;
+                if (k < nml) {
+                    const int hh = k / nparts, c = k - hh * nparts;
+                    ml[i] = *reinterpret_cast<const float2*>(x + ((size_t)hh * nparts + c) * kAttnChunkStride + 64);
+                }
+            }
+        }
 #pragma unroll
         for (int p = 0; p < PER; ++p) {
             const int f = tid + p * NT;            // float4 index in x
             const bool in = f < XF4 && 4 * f < K;
-            const float4 t = reinterpret_cast<const float4*>(xs)[in ? f : 0];
-            v[p] = in ? t : make_float4(0.f, 0.f, 0.f, 0.f);
+            if constexpr (MERGE) {                 // the head's chunk sums, before any use
+                const int e = in ? 4 * f : 0;
+                const float* ph = x + (size_t)(e >> 6) * nparts * kAttnChunkStride + (e & 63);
+#pragma unroll
+                for (int c = 0; c < NP; ++c)
+                    if (c < nparts) pa[p][c] = *reinterpret_cast<const float4*>(ph + (size_t)c * kAttnChunkStride);
+            } else {
+                const float4 t = reinterpret_cast<const float4*>(xs)[in ? f : 0];
+                v[p] = in ? t : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
         }
         if constexpr (NORM) {
 #pragma unroll
@@ -372,6 +402,38 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(
         gemv_load<WT, NM, RPW, NC>(A, qa, da, qb, db, row0, N, K, lane);
         gemv_load<WT, NM, RPW, NC>(B, qa, da, qb, db, row0 + rstep, N, K, lane);
 
+        if constexpr (MERGE) {
+            const int nml = (K >> 6) * nparts;
+#pragma unroll
+            for (int i = 0; i < (int)(sizeof(ml) / sizeof(ml[0])); ++i)
+                if (tid + i * NT < nml) mls[tid + i * NT] = ml[i];
+            __syncthreads();
+#pragma unroll
+            for (int p = 0; p < PER; ++p) {
+                const int f = tid + p * NT;
+                const bool in = f < XF4 && 4 * f < K;
+                const float2* mh = mls + (size_t)((in ? 4 * f : 0) >> 6) * nparts;
+                float mt = kNegInfF;
+#pragma unroll
+                for (int c = 0; c < NP; ++c)
+                    if (c < nparts) mt = fmaxf(mt, mh[c].x);
+                float lt = 0.f;
+                float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+                for (int c = 0; c < NP; ++c) {
+                    if (c < nparts && mh[c].x != kNegInfF) {
+                        const float wgt = expf(mh[c].x - mt);
+                        lt += wgt * mh[c].y;
+                        o.x += wgt * pa[p][c].x;
+                        o.y += wgt * pa[p][c].y;
+                        o.z += wgt * pa[p][c].z;
+                        o.w += wgt * pa[p][c].w;
+                    }
+                }
+                const float il = lt > 0.f ? 1.f / lt : 0.f;
+                v[p] = in ? make_float4(o.x * il, o.y * il, o.z * il, o.w * il) : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+        }
         // Stage x (times the norm weight when fused) in the lane-interleaved
         // layout, with one barrier: RMSNorm (ops.hpp:488-498) is per row, so
         // W.((x*inv)*w) = inv * W.(x*w) and 1/rms is applied to the dots.
@@ -435,20 +497,22 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(
 template <int WT, bool SWIGLU>
 int launch_gemv(hipStream_t s, const DevWeight& a, const DevWeight* b, const float* x, float* y,
                 const float* norm_w, float eps, const float* residual, const int* x_row = nullptr,
-                float* x_copy = nullptr) {
+                float* x_copy = nullptr, int nparts = 0) {
     constexpr int CW = 64 * Gemv<WT>::EPL;
     const int nc = (a.K + CW - 1) / CW;
     const uint8_t* qb = b ? b->q : nullptr;
     const __half* db = b ? b->d : nullptr;
     VH_ARG(!x_row || (norm_w && !SWIGLU), "gemv: a gathered row needs the fused norm");
     VH_ARG(!(residual && SWIGLU), "gemv: no residual on the SwiGLU form");
-    const int xm = (x_row ? 2 : 0) | (norm_w ? 1 : 0) | (residual ? 4 : 0);
+    VH_ARG(!nparts || (!x_row && !norm_w && !SWIGLU && nparts <= kAttnMaxChunks && a.K % 64 == 0),
+           "gemv: chunk merge takes a plain x of whole 64-wide heads and at most %d chunks", kAttnMaxChunks);
+    const int xm = (x_row ? 2 : 0) | (norm_w ? 1 : 0) | (residual ? 4 : 0) | (nparts ? 8 : 0);
 #define VH_GEMV_XM(NC, RPW, XM)                                                                            \
     do {                                                                                                  \
         const int groups = (a.N + kGemvWaves * (RPW)-1) / (kGemvWaves * (RPW));                            \
         dim3 grid(groups < kGemvMaxGroups ? groups : kGemvMaxGroups);                                      \
         hipLaunchKernelGGL((gemv_kernel<WT, NC, RPW, SWIGLU, XM>), grid, dim3(64 * kGemvWaves), 0, s, a.q, \
-                           a.d, qb, db, a.N, a.K, x, x_row, x_copy, norm_w, eps, residual, y);              \
+                           a.d, qb, db, a.N, a.K, x, x_row, x_copy, norm_w, eps, residual, y, nparts);      \
     } while (0)
 #define VH_GEMV(NC, RPW)                                                   \
     do {                                                                  \
@@ -458,7 +522,8 @@ int launch_gemv(hipStream_t s, const DevWeight& a, const DevWeight* b, const flo
             if (xm == 3) VH_GEMV_XM(NC, RPW, 3);                          \
             else if (xm == 4) VH_GEMV_XM(NC, RPW, 4);                     \
             else if (xm == 5) VH_GEMV_XM(NC, RPW, 5);                     \
-            else VH_GEMV_XM(NC, RPW, 7);                                  \
+            else if (xm == 7) VH_GEMV_XM(NC, RPW, 7);                     \
+            else if (xm == 12) VH_GEMV_XM(NC, RPW, 12);                   \
         }                                                                 \
     } while (0)
     if (nc <= 1) {
@@ -513,6 +578,17 @@ int launch_qlinear(hipStream_t s, const DevWeight& w, const float* x, float* y, 
 }
 
 bool qlinear_gather_supported(const DevWeight& w) { return gemv_fits(w); }
+
+int launch_qlinear_merge(hipStream_t s, const DevWeight& w, const float* chunks, int nch, const float* residual,
+                         float* y) {
+    int rc = check_weight(w);
+    if (rc) return rc;
+    VH_ARG(chunks && y && residual && nch >= 1, "qlinear_merge: bad arguments");
+    VH_ARG(gemv_fits(w), "qlinear_merge: weight does not take the M=1 GEMV path");
+    if (w.dtype == VLRF_DT_Q8_0)
+        return launch_gemv<VLRF_DT_Q8_0, false>(s, w, nullptr, chunks, y, nullptr, 0.f, residual, nullptr, nullptr, nch);
+    return launch_gemv<VLRF_DT_Q4_0, false>(s, w, nullptr, chunks, y, nullptr, 0.f, residual, nullptr, nullptr, nch);
+}
 
 int launch_qlinear_gather(hipStream_t s, const DevWeight& w, const float* table, const int* row,
                           float* x_copy, float* y, const float* norm_w, float eps) {

@@ -57,6 +57,8 @@ struct vlrf_hip_model {
     const float* cos_t = nullptr;
     const float* sin_t = nullptr;
     float *x = nullptr, *qkv = nullptr, *att = nullptr, *h = nullptr, *logits = nullptr, *part = nullptr;
+    int nch = 0;               // decode attention in chunked form (merged by the O GEMV) when > 0
+    float* chunks = nullptr;   // its partials [H][nch][kAttnChunkStride]
     int* state = nullptr;      // [0] token, [1] position, [2] generated count
     int* gen_ids = nullptr;    // [S]
     int* prompt = nullptr;     // [S] staged prompt ids
@@ -113,10 +115,13 @@ int enqueue_step(vlrf_hip_model* m, hipStream_t s) {
         fz.vs_w = Ly.kv.vs;
         fz.n_kv = m->G;
         fz.max_seq = m->S;
+        fz.chunks = m->chunks;
+        fz.nch = m->nch;
         if (!rc) rc = launch_attn_decode(s, q, Ly.kv.k, Ly.kv.v, Ly.kv.ks, Ly.kv.vs, Ly.kv.dtype,
                                          (long)m->S * m->dh, m->H, m->G, m->dh, 1, m->state + 1,
                                          m->n_splits, scale, m->part, m->att, &fz);
-        if (!rc) rc = launch_qlinear(s, Ly.wo, m->att, m->x, 1, nullptr, 0.f, m->x);
+        if (!rc) rc = m->nch ? launch_qlinear_merge(s, Ly.wo, m->chunks, m->nch, m->x, m->x)
+                             : launch_qlinear(s, Ly.wo, m->att, m->x, 1, nullptr, 0.f, m->x);
         if (!rc) rc = launch_qlinear_swiglu(s, Ly.wg, Ly.wu, m->x, m->h, 1, Ly.ln2, eps);
         if (!rc) rc = launch_qlinear(s, Ly.wd, m->h, m->x, 1, nullptr, 0.f, m->x);
     }
@@ -225,6 +230,15 @@ int vlrf_hip_model_create(vlrf_hip_ctx_t ctx, const vlrf_hip_model_config* cfg, 
     dalloc((void**)&m->h, (size_t)m->F * 4);
     dalloc((void**)&m->logits, (size_t)m->V * 4);
     dalloc((void**)&m->part, (size_t)m->H * m->n_splits * (dh + 2) * 4);
+    // Chunked decode attention when the O projection's GEMV can merge it.
+    m->nch = c.weight_dtype == VLRF_DT_Q8_0 || c.weight_dtype == VLRF_DT_Q4_0
+                 ? attn_decode_chunks(m->S, dh, m->G) : 0;
+    DevWeight wo_shape;
+    wo_shape.dtype = c.weight_dtype;
+    wo_shape.N = m->D;
+    wo_shape.K = m->H * dh;
+    if (m->nch && (wo_shape.K != m->D || !qlinear_gather_supported(wo_shape))) m->nch = 0;
+    if (m->nch) dalloc((void**)&m->chunks, (size_t)m->H * m->nch * kAttnChunkStride * 4);
     dalloc((void**)&m->state, 4 * sizeof(int));
     dalloc((void**)&m->gen_ids, (size_t)m->S * sizeof(int));
     dalloc((void**)&m->prompt, (size_t)m->S * sizeof(int));
@@ -277,7 +291,7 @@ void vlrf_hip_model_destroy(vlrf_hip_model_t m) {
     }
     weight_release(m->lm_head);
     for (void* p : {(void*)m->embed, (void*)m->ln_final, (void*)m->x, (void*)m->qkv, (void*)m->att,
-                    (void*)m->h, (void*)m->logits, (void*)m->part, (void*)m->state,
+                    (void*)m->h, (void*)m->logits, (void*)m->part, (void*)m->chunks, (void*)m->state,
                     (void*)m->gen_ids, (void*)m->prompt})
         if (p) (void)hipFree(p);
     for (void* p : {(void*)m->pf_x, (void*)m->pf_qkv, (void*)m->pf_a, (void*)m->pf_att, (void*)m->pf_h,
