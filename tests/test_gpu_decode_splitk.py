@@ -1,13 +1,14 @@
-"""GPU parity of the decode step's split-K attention (caches of more than 512
-rows; smaller caches take the single-pass kernel): AttentionBlock::forward
+"""GPU parity of the decode step's long-cache attention (caches of more than
+512 rows; smaller caches take the single-pass kernel): AttentionBlock::forward
 with the cache (attention.hpp:89-186), the append (kv_cache.hpp:215-251) and
 flash_attn_head's online softmax (attention.hpp:207-309), with RoPE and the
-new row's quantization fused into the chunk that holds the new token and the
-chunks merged by the log-sum-exp combine.  Every GQA group size and both
-head sizes, all three cache dtypes, decode positions on both sides of the
-64-token chunk boundaries (the new token as the first, a middle and the last
-row of its chunk), and generations after resets.  Bars: greedy streams
-identical to the oracle's; logits within 1e-3 (f32 paths)."""
+new row's quantization fused into the chunk that holds the new token.  The
+step runs the chunked form (512 cached rows per workgroup and query head,
+merged by the O projection's GEMV) where it applies, else split-K + combine.
+Every GQA group size and both head sizes, all three cache dtypes, decode
+positions on both sides of the chunk boundaries (the new token as the first,
+a middle and the last row of a chunk), and generations after resets.  Bars:
+greedy streams identical to the oracle's; logits within 1e-3 (f32 paths)."""
 import numpy as np
 import pytest
 
@@ -17,7 +18,7 @@ from vlrf_amd import formats as F
 
 pytestmark = pytest.mark.gpu
 
-CAP = 600   # > 512 rows: the split-K path, 10 chunks of 64
+CAP = 1100  # > 512 rows: the chunked path, 3 chunks of 512 (and 18 split-K chunks of 64)
 
 
 def _cfg(n_heads, n_kv, d_model, kv_dtype=V.KV_Q8_0, n_layers=2):
@@ -46,20 +47,21 @@ def _oracle_stream(om, prompt, n):
 @pytest.mark.parametrize("n_heads,n_kv,d_model", [(4, 4, 256), (4, 1, 256), (8, 2, 512), (8, 1, 512),
                                                   (8, 8, 1024), (8, 1, 1024)])
 def test_greedy_stream_gqa_shapes(ctx, orc, n_heads, n_kv, d_model):
-    """GQA groups 1, 4 and 8 at d_head 64 and 128: a 130-token prompt through
-    the decode step, then 30 greedy steps (positions 130..159)."""
+    """GQA groups 1, 4 and 8 at d_head 64 and 128: a 520-token prompt through
+    the decode step, then 30 greedy steps (positions 520..549, past the first
+    512-row chunk)."""
     print(f"[case] split-K decode heads={n_heads}/{n_kv} d_model={d_model}", flush=True)
     cfg = _cfg(n_heads, n_kv, d_model)
     m, om = _models(ctx, orc, cfg, 61)
-    prompt = F.tokens(61, "skp", 130, cfg["vocab_size"])
+    prompt = F.tokens(61, "skp", 520, cfg["vocab_size"])
     assert list(m.generate(prompt, 30)) == _oracle_stream(om, prompt, 30)
-    assert m.used == om.used == 160
+    assert m.used == om.used == 550
 
 
 @pytest.mark.parametrize("kv_dtype", [V.KV_Q8_0, V.KV_F16, V.KV_F32])
 def test_logits_across_chunk_boundaries(ctx, orc, kv_dtype):
-    """Teacher-forced logits at every position 0..139 (chunk boundaries at 64
-    and 128, so the new token is the first, a middle and the last row of a
+    """Teacher-forced logits at every position 0..539 (chunk boundaries at 64
+    and 512, so the new token is the first, a middle and the last row of a
     chunk) for each cache dtype."""
     print(f"[case] split-K logits kv_dtype={kv_dtype}", flush=True)
     cfg = _cfg(8, 2, 512, kv_dtype)
@@ -67,7 +69,7 @@ def test_logits_across_chunk_boundaries(ctx, orc, kv_dtype):
     m.reset()
     om.reset()
     worst = 0.0
-    for t in F.tokens(62, "skf", 140, cfg["vocab_size"]):
+    for t in F.tokens(62, "skf", 540, cfg["vocab_size"]):
         g_next, gl = m.step(int(t), want_logits=True)
         _, ol = om.forward([int(t)], want_logits=True)
         worst = max(worst, rel_err(gl, ol))
@@ -81,7 +83,7 @@ def test_generations_after_resets(ctx, orc):
     equals the oracle's."""
     cfg = _cfg(4, 1, 256, n_layers=1)
     m, om = _models(ctx, orc, cfg, 63)
-    for i, n in enumerate((63, 64, 129)):
+    for i, n in enumerate((511, 512, 513)):
         print(f"[case] split-K generation {i}: prompt {n}", flush=True)
         prompt = F.tokens(63, f"skr{i}", n, cfg["vocab_size"])
         m.reset()

@@ -393,7 +393,7 @@ constexpr int kSPMaxCtx = kSPWaves * 64 * kSPRounds;   // cache rows the single 
 // Chunked form (CH tokens per workgroup, one query head each): partials of
 // kChunkStride floats -- acc[0..63] (unnormalised), m at 64, l at 65 --
 // merged by the next GEMV's prologue.
-constexpr int kCH = 256, kChunkStride = kAttnChunkStride;
+constexpr int kCH = 512, kChunkStride = kAttnChunkStride;   // 256 / 1024: 0.645 / 0.673 ms per step against 0.620
 
 // Elements 4i..4i+3 of a 64-element row held as 16-byte words, as f32.
 template <int KVT>
