@@ -6,13 +6,16 @@
 // FeedForward::forward SwiGLU (feedforward.hpp:50-77), greedy argmax
 // (transformer.hpp:43-47).
 //
-// Per layer the step queues six kernels:
+// Per layer the step queues five kernels (six where the chunked attention
+// form does not apply):
 //   qlinear(Wqkv, rmsnorm(x; ln1))        Q,K,V in one pass over the fused rows
 //   attn_decode                           RoPE on q,k and the Q8_0 append of the
-//                                         token's K/V row, fused with split-K
-//                                         attention over the quantized cache
-//   attn_combine                          log-sum-exp merge of the chunks
-//   qlinear(Wo, att) + x                  residual in the epilogue
+//                                         token's K/V row, fused with attention
+//                                         over the quantized cache: per query head
+//                                         and 512-row chunk a (m, l, acc) partial
+//                                         (else split-K partials + attn_combine)
+//   qlinear(Wo, merge(chunks)) + x        the chunks' log-sum-exp merge in the
+//                                         GEMV prologue, residual in the epilogue
 //   swiglu(Wg, Wu, rmsnorm(x; ln2))       silu(g) * u in the epilogue
 //   qlinear(Wd, h) + x
 // then rmsnorm + LM head and argmax, which writes the next token id and
