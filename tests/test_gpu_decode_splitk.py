@@ -44,10 +44,11 @@ def _oracle_stream(om, prompt, n):
     return ref
 
 
-@pytest.mark.parametrize("n_heads,n_kv,d_model", [(4, 4, 256), (4, 1, 256), (8, 2, 512), (8, 1, 512),
-                                                  (8, 8, 1024), (8, 1, 1024)])
+@pytest.mark.parametrize("n_heads,n_kv,d_model", [(4, 4, 256), (8, 4, 512), (4, 1, 256), (8, 2, 512),
+                                                  (8, 1, 512), (8, 8, 512), (8, 8, 1024), (8, 1, 1024)])
 def test_greedy_stream_gqa_shapes(ctx, orc, n_heads, n_kv, d_model):
-    """GQA groups 1, 4 and 8 at d_head 64 and 128: a 520-token prompt through
+    """GQA groups 1, 2, 4 and 8 at d_head 64 (up to 8 KV heads: a 512-element
+    new row) and 128: a 520-token prompt through
     the decode step, then 30 greedy steps (positions 520..549, past the first
     512-row chunk)."""
     print(f"[case] split-K decode heads={n_heads}/{n_kv} d_model={d_model}", flush=True)
