@@ -336,7 +336,6 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(
     constexpr int PER = (XF4 + NT - 1) / NT;          // float4 per thread
     __shared__ float4 xs4[XF4];
     __shared__ float red[kGemvWaves];
-    __shared__ float2 mls[MERGE ? kGemvMaxK / 64 * kAttnMaxChunks : 1];   // (m, l) per head and chunk
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nwaves = gridDim.x * kGemvWaves;
@@ -360,30 +359,21 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(
         const float* xs = GATHER ? x + (size_t)(*x_row) * K : x;
         float4 v[PER], gw[PER];
         float4 pa[PER][NP];
-        float2 ml[MERGE ? (kGemvMaxK / 64 * kAttnMaxChunks + NT - 1) / NT : 1];
-        if constexpr (MERGE) {
-            // (m, l) of every head and chunk once per workgroup, first: they are
-            // shared by the 16 threads of a head and staged in LDS below.
-            const int nml = (K >> 6) * nparts;
-#pragma unroll
-            for (int i = 0; i < (int)(sizeof(ml) / sizeof(ml[0])); ++i) {
-                const int k = tid + i * NT;
-                if (k < nml) {
-                    const int hh = k / nparts, c = k - hh * nparts;
-                    ml[i] = *reinterpret_cast<const float2*>(x + ((size_t)hh * nparts + c) * kAttnChunkStride + 64);
-                }
-            }
-        }
+        float2 pml[PER][NP];
 #pragma unroll
         for (int p = 0; p < PER; ++p) {
             const int f = tid + p * NT;            // float4 index in x
             const bool in = f < XF4 && 4 * f < K;
-            if constexpr (MERGE) {                 // the head's chunk sums, before any use
+            if constexpr (MERGE) {                 // the head's chunk words, before any use (the 16
+                                                   // threads of a head share the (m, l) loads in L1)
                 const int e = in ? 4 * f : 0;
                 const float* ph = x + (size_t)(e >> 6) * nparts * kAttnChunkStride + (e & 63);
 #pragma unroll
                 for (int c = 0; c < NP; ++c)
-                    if (c < nparts) pa[p][c] = *reinterpret_cast<const float4*>(ph + (size_t)c * kAttnChunkStride);
+                    if (c < nparts) {
+                        pa[p][c] = *reinterpret_cast<const float4*>(ph + (size_t)c * kAttnChunkStride);
+                        pml[p][c] = *reinterpret_cast<const float2*>(ph - (e & 63) + (size_t)c * kAttnChunkStride + 64);
+                    }
             } else {
                 const float4 t = reinterpret_cast<const float4*>(xs)[in ? f : 0];
                 v[p] = in ? t : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -403,16 +393,11 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(
         gemv_load<WT, NM, RPW, NC>(B, qa, da, qb, db, row0 + rstep, N, K, lane);
 
         if constexpr (MERGE) {
-            const int nml = (K >> 6) * nparts;
-#pragma unroll
-            for (int i = 0; i < (int)(sizeof(ml) / sizeof(ml[0])); ++i)
-                if (tid + i * NT < nml) mls[tid + i * NT] = ml[i];
-            __syncthreads();
 #pragma unroll
             for (int p = 0; p < PER; ++p) {
                 const int f = tid + p * NT;
                 const bool in = f < XF4 && 4 * f < K;
-                const float2* mh = mls + (size_t)((in ? 4 * f : 0) >> 6) * nparts;
+                const float2* mh = pml[p];
                 float mt = kNegInfF;
 #pragma unroll
                 for (int c = 0; c < NP; ++c)
