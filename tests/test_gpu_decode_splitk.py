@@ -21,8 +21,8 @@ pytestmark = pytest.mark.gpu
 CAP = 1100  # > 512 rows: the chunked path, 3 chunks of 512 (and 18 split-K chunks of 64)
 
 
-def _cfg(n_heads, n_kv, d_model, kv_dtype=V.KV_Q8_0, n_layers=2):
-    cfg = dict(F.tiny(V.DT_Q8_0, n_layers=n_layers, max_seq_len=CAP), n_heads=n_heads, n_kv_heads=n_kv,
+def _cfg(n_heads, n_kv, d_model, kv_dtype=V.KV_Q8_0, n_layers=2, weight_dtype=V.DT_Q8_0):
+    cfg = dict(F.tiny(weight_dtype, n_layers=n_layers, max_seq_len=CAP), n_heads=n_heads, n_kv_heads=n_kv,
                d_model=d_model, d_ff=2 * d_model)
     cfg["kv_dtype"] = kv_dtype
     return cfg
@@ -89,3 +89,12 @@ def test_generations_after_resets(ctx, orc):
         prompt = F.tokens(63, f"skr{i}", n, cfg["vocab_size"])
         m.reset()
         assert list(m.generate(prompt, 20)) == _oracle_stream(om, prompt, 20), i
+
+
+def test_greedy_stream_q4_weights(ctx, orc):
+    """Q4_0 weights: the O projection's chunk merge on the Q4_0 GEMV."""
+    print("[case] long-cache decode, Q4_0 weights", flush=True)
+    cfg = _cfg(8, 2, 512, weight_dtype=V.DT_Q4_0)
+    m, om = _models(ctx, orc, cfg, 64)
+    prompt = F.tokens(64, "skq4", 520, cfg["vocab_size"])
+    assert list(m.generate(prompt, 30)) == _oracle_stream(om, prompt, 30)
