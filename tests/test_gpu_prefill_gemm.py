@@ -25,8 +25,10 @@ def _weight(ctx, seed, name, N, K, dtype):
 # Kernel selection: M <= 128 -> 128-row register-staged tiles; Q8_0 with M > 128 -> the
 # direct-to-LDS kernel (256x128 tiles); Q4_0 with M > 128 -> the register-staged 256x128
 # tiles (two per CU for 257..512 tiles, as 520 x 16600's 390).
+# Wide 256x256 tiles (two 128-row halves of the one weight) where they give at
+# least 192 workgroups: 520 x 16600 and 2048 x 6144 (the 8B layer's QKV at T = 2048).
 @pytest.mark.parametrize("M,N,K", [(256, 6144, 4096), (128, 4096, 14336), (2048, 1024, 4096),
-                                   (520, 16600, 64)])
+                                   (520, 16600, 64), (2048, 6144, 512)])
 def test_prefill_gemm_config5_shapes(ctx, orc, dtype, M, N, K):
     """The 8B-layer projections (QKV 6144x4096, down 4096x14336) at prompt rows."""
     print(f"[case] qgemm dtype={dtype} M={M} N={N} K={K}", flush=True)
@@ -39,7 +41,7 @@ def test_prefill_gemm_config5_shapes(ctx, orc, dtype, M, N, K):
 
 
 @pytest.mark.parametrize("M,N,K", [(17, 37, 64), (200, 300, 128), (129, 130, 704), (300, 256, 2048),
-                                   (1000, 8300, 192), (300, 100, 256), (129, 37, 64)])
+                                   (1000, 8300, 192), (1500, 8300, 192), (300, 100, 256), (129, 37, 64)])
 def test_prefill_gemm_ragged_with_norm_and_residual(ctx, orc, M, N, K):
     """Row/column counts off the 128x128 tile, with the fused RMSNorm prologue
     and the residual epilogue (in place on the residual)."""

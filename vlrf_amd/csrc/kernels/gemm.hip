@@ -328,7 +328,11 @@ __global__ __launch_bounds__(lds_gemm::NT) void mfma_qgemm_lds_kernel(
     const int lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wave >> 2, wn = wave & 3;
-    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    // EPI 4 / 5 (wide): one matrix, NM = 2 halves of a 2*BN-row tile (its rows
+    // n0 .. n0 + 2*BN - 1), stored as is / plus the residual.
+    constexpr bool WIDE = EPI >= 4;
+    static_assert(!WIDE || NM == 2, "a wide tile is two halves");
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN * (WIDE ? 2 : 1);
 
     // Load sources of K step 0 (step k adds 128 B of A, 64 B of codes, 4 B of
     // scales) and the wave-uniform offsets of their destinations in a stage.
@@ -348,14 +352,14 @@ __global__ __launch_bounds__(lds_gemm::NT) void mfma_qgemm_lds_kernel(
     for (int it = 0; it < S::W_IT; ++it) {
         const int li = min(it * 8 + wave, S::W_TI - 1);   // waves past the last load: never issued
         const int r0 = li * RPI, n = r0 + lane / CPR, c = (lane % CPR) ^ swz_w<WT>(n);
-        const int gn = min(n0 + n % BN, N - 1);
+        const int gn = min(n0 + (WIDE ? n : n % BN), N - 1);
         gw[it] = reinterpret_cast<const char*>((n / BN ? qb : qa) + (size_t)gn * rowb + c * 16);
         lw[it] = r0 * CB;
     }
     const bool sload = wave < S::S_WAVES;
     const char* gs = nullptr;
     if (sload) {
-        const int n = wave * 64 + lane, gn = min(n0 + n % BN, N - 1);
+        const int n = wave * 64 + lane, gn = min(n0 + (WIDE ? n : n % BN), N - 1);
         gs = reinterpret_cast<const char*>((n / BN ? db : da) + (size_t)gn * (K / 32));
     }
     const uint32_t bA[3] = {lds_addr(A0), lds_addr(A1), lds_addr(A2)};
@@ -452,7 +456,16 @@ __global__ __launch_bounds__(lds_gemm::NT) void mfma_qgemm_lds_kernel(
         for (int v = 0; v < 16; ++v) {
             const int row = m0 + wm * WM + 32 * i + 8 * (v >> 2) + 4 * h + (v & 3);
             const int col = n0 + wn * WN + l32;
-            if (row < M && col < N) {
+            if constexpr (WIDE) {
+#pragma unroll
+                for (int m = 0; m < 2; ++m) {
+                    if (row < M && col + m * BN < N) {
+                        const size_t o = (size_t)row * N + col + m * BN;
+                        if constexpr (EPI == 5) reinterpret_cast<float*>(out)[o] = acc[m][i][v] + residual[o];
+                        else reinterpret_cast<float*>(out)[o] = acc[m][i][v];
+                    }
+                }
+            } else if (row < M && col < N) {
                 const size_t o = (size_t)row * N + col;
                 if constexpr (EPI >= 2) {
                     const float g = acc[0][i][v], u = acc[NM - 1][i][v];
@@ -471,8 +484,12 @@ __global__ __launch_bounds__(lds_gemm::NT) void mfma_qgemm_lds_kernel(
 template <int WT, int EPI>
 void launch_lds_wt(hipStream_t s, const uint16_t* a, const DevWeight& w0, const DevWeight* w1, int M,
                    const float* residual, void* out) {
-    const dim3 grid((w0.N + lds_gemm::BN - 1) / lds_gemm::BN, (M + lds_gemm::BM - 1) / lds_gemm::BM);
-    if constexpr (EPI >= 2)   // SwiGLU: gate and up tiles together
+    constexpr int TN = lds_gemm::BN * (EPI >= 4 ? 2 : 1);
+    const dim3 grid((w0.N + TN - 1) / TN, (M + lds_gemm::BM - 1) / lds_gemm::BM);
+    if constexpr (EPI >= 4)   // wide: both halves from the one matrix
+        hipLaunchKernelGGL((mfma_qgemm_lds_kernel<WT, 2, EPI>), grid, dim3(lds_gemm::NT), 0, s, a, w0.q, w0.d,
+                           w0.q, w0.d, M, w0.N, w0.K, residual, out);
+    else if constexpr (EPI >= 2)   // SwiGLU: gate and up tiles together
         hipLaunchKernelGGL((mfma_qgemm_lds_kernel<WT, 2, EPI>), grid, dim3(lds_gemm::NT), 0, s, a, w0.q, w0.d,
                            w1->q, w1->d, M, w0.N, w0.K, residual, out);
     else
@@ -765,6 +782,9 @@ int small_grid_y(int N, int K) {
     return want < ns ? want : ns;
 }
 
+constexpr long kWideGroups = 192;   // 3/4 of the CUs (at 128, O and down of the 8B layer at
+                                    // T = 2048 go wide and the layer runs 1.335 against 1.166 ms)
+
 int check_qgemm(const DevWeight& w, int M) {
     VH_ARG(w.dtype == VLRF_DT_Q8_0 || w.dtype == VLRF_DT_Q4_0,
            "qgemm: the MFMA path takes Q8_0/Q4_0 weights (dtype %d)", w.dtype);
@@ -793,7 +813,14 @@ int launch_qgemm(hipStream_t s, const DevWeight& w, const uint16_t* a, int M, co
     if (rc) return rc;
     VH_ARG(a && y, "qgemm: null operand");
     if (M > 128) {
-        if (residual) launch_lds<1>(s, a, w, nullptr, M, residual, y);
+        // 2*BN-wide tiles (twice the MFMA work per byte staged) where they still
+        // give at least kWideGroups workgroups
+        const long groups = (long)((w.N + 2 * lds_gemm::BN - 1) / (2 * lds_gemm::BN)) *
+                            ((M + lds_gemm::BM - 1) / lds_gemm::BM);
+        if (groups >= kWideGroups) {
+            if (residual) launch_lds<5>(s, a, w, nullptr, M, residual, y);
+            else launch_lds<4>(s, a, w, nullptr, M, nullptr, y);
+        } else if (residual) launch_lds<1>(s, a, w, nullptr, M, residual, y);
         else launch_lds<0>(s, a, w, nullptr, M, nullptr, y);
     } else {
         if (residual) launch_cfg<CfgSmall, 1>(s, w.dtype, a, w, nullptr, M, residual, y);
