@@ -98,3 +98,14 @@ def test_greedy_stream_q4_weights(ctx, orc):
     m, om = _models(ctx, orc, cfg, 64)
     prompt = F.tokens(64, "skq4", 520, cfg["vocab_size"])
     assert list(m.generate(prompt, 30)) == _oracle_stream(om, prompt, 30)
+
+
+def test_greedy_stream_wide_model(ctx, orc):
+    """d_model 4096 at d_head 64 (64 query heads, 8 KV heads): the O
+    projection's chunk merge with three float4 of x per thread (a 4096-wide
+    GEMV row), which holds up to 5 chunks in registers."""
+    print("[case] long-cache decode, d_model 4096 d_head 64", flush=True)
+    cfg = _cfg(64, 8, 4096, n_layers=1)
+    m, om = _models(ctx, orc, cfg, 65)
+    prompt = F.tokens(65, "skw", 520, cfg["vocab_size"])
+    assert list(m.generate(prompt, 12)) == _oracle_stream(om, prompt, 12)

@@ -123,6 +123,8 @@ int launch_qlinear(hipStream_t s, const DevWeight& w, const float* x, float* y, 
 // prologue.
 int launch_qlinear_merge(hipStream_t s, const DevWeight& w, const float* chunks, int nch, const float* residual,
                          float* y);
+// Most chunks launch_qlinear_merge takes for w (0: not on that path).
+int qlinear_merge_max_chunks(const DevWeight& w);
 int launch_qlinear_gather(hipStream_t s, const DevWeight& w, const float* table, const int* row,
                           float* x_copy, float* y, const float* norm_w, float eps);
 bool qlinear_gather_supported(const DevWeight& w);

@@ -331,9 +331,9 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(
     // element e is dim e % 64 of head e / 64, merged here from the nparts
     // chunk partials of that head (log-sum-exp, attention.hpp:207-309's rule).
     constexpr bool MERGE = XM & 8;
-    constexpr int NP = MERGE ? kAttnMaxChunks : 1;
     constexpr int XF4 = NC * CW / 4;                  // staged float4 slots
     constexpr int PER = (XF4 + NT - 1) / NT;          // float4 per thread
+    constexpr int NP = MERGE ? kAttnMaxChunks / PER : 1;   // chunks a merge holds in registers
     __shared__ float4 xs4[XF4];
     __shared__ float red[kGemvWaves];
 
@@ -564,12 +564,23 @@ int launch_qlinear(hipStream_t s, const DevWeight& w, const float* x, float* y, 
 
 bool qlinear_gather_supported(const DevWeight& w) { return gemv_fits(w); }
 
+int qlinear_merge_max_chunks(const DevWeight& w) {
+    if (!gemv_fits(w) || w.K % 64) return 0;
+    const int cw = w.dtype == VLRF_DT_Q8_0 ? 64 * Gemv<VLRF_DT_Q8_0>::EPL : 64 * Gemv<VLRF_DT_Q4_0>::EPL;
+    int nc = (w.K + cw - 1) / cw;
+    if (nc > 3) nc = 6;                                  // the instantiated chunk counts: 1, 2, 3, 6
+    const int per = (nc * cw / 4 + 64 * kGemvWaves - 1) / (64 * kGemvWaves);
+    return kAttnMaxChunks / per;
+}
+
 int launch_qlinear_merge(hipStream_t s, const DevWeight& w, const float* chunks, int nch, const float* residual,
                          float* y) {
     int rc = check_weight(w);
     if (rc) return rc;
     VH_ARG(chunks && y && residual && nch >= 1, "qlinear_merge: bad arguments");
     VH_ARG(gemv_fits(w), "qlinear_merge: weight does not take the M=1 GEMV path");
+    VH_ARG(nch <= qlinear_merge_max_chunks(w), "qlinear_merge: %d chunks, at most %d for K %d", nch,
+           qlinear_merge_max_chunks(w), w.K);
     if (w.dtype == VLRF_DT_Q8_0)
         return launch_gemv<VLRF_DT_Q8_0, false>(s, w, nullptr, chunks, y, nullptr, 0.f, residual, nullptr, nullptr, nch);
     return launch_gemv<VLRF_DT_Q4_0, false>(s, w, nullptr, chunks, y, nullptr, 0.f, residual, nullptr, nullptr, nch);

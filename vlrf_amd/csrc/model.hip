@@ -240,7 +240,7 @@ int vlrf_hip_model_create(vlrf_hip_ctx_t ctx, const vlrf_hip_model_config* cfg, 
     wo_shape.dtype = c.weight_dtype;
     wo_shape.N = m->D;
     wo_shape.K = m->H * dh;
-    if (m->nch && (wo_shape.K != m->D || !qlinear_gather_supported(wo_shape))) m->nch = 0;
+    if (m->nch && (wo_shape.K != m->D || m->nch > qlinear_merge_max_chunks(wo_shape))) m->nch = 0;
     if (m->nch) dalloc((void**)&m->chunks, (size_t)m->H * m->nch * kAttnChunkStride * 4);
     dalloc((void**)&m->state, 4 * sizeof(int));
     dalloc((void**)&m->gen_ids, (size_t)m->S * sizeof(int));
