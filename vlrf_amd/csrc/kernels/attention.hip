@@ -21,6 +21,12 @@
 // log-sum-exp rescale.  With a device-side position the kernel also applies
 // RoPE to q and to the new k and quantizes + stores the new K/V row before
 // attending (the decode step's fused form).
+//
+// The decode step itself (d_head 64, caches of 513..8192 rows) runs the
+// single-pass kernel below in chunked form instead: one query head and one
+// 512-row chunk per workgroup, a (m, l, acc) partial per chunk, merged by the
+// O projection's GEMV prologue, so the step has no combine launch; caches of
+// at most 512 rows take the single pass over the whole context.
 #include "../internal.hpp"
 
 #include <cmath>
