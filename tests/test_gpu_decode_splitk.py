@@ -109,3 +109,24 @@ def test_greedy_stream_wide_model(ctx, orc):
     m, om = _models(ctx, orc, cfg, 65)
     prompt = F.tokens(65, "skw", 520, cfg["vocab_size"])
     assert list(m.generate(prompt, 12)) == _oracle_stream(om, prompt, 12)
+
+
+def test_last_row_and_overflow(ctx, orc):
+    """The cache filled to its last row (the third chunk partly past the
+    capacity): the logits of the final position match the oracle's, and one
+    more step is refused (KVCache::append's capacity error, kv_cache.hpp:215-251)."""
+    print("[case] long-cache decode to the last cache row", flush=True)
+    cfg = _cfg(4, 1, 256, n_layers=1)
+    m, om = _models(ctx, orc, cfg, 66)
+    ids = F.tokens(66, "skl", CAP, cfg["vocab_size"])
+    m.reset()
+    om.reset()
+    m.prefill(ids[:-1])
+    om.forward(ids[:-1])
+    _, gl = m.step(int(ids[-1]), want_logits=True)
+    _, ol = om.forward([int(ids[-1])], want_logits=True)
+    assert m.used == om.used == CAP
+    assert rel_err(gl, ol) <= 1e-3
+    with pytest.raises(V.HipError) as e:
+        m.step(int(ids[0]))
+    assert e.value.rc == -4
