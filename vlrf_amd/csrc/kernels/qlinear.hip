@@ -331,6 +331,9 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(
     // element e is dim e % 64 of head e / 64, merged here from the nparts
     // chunk partials of that head (log-sum-exp, attention.hpp:207-309's rule).
     constexpr bool MERGE = XM & 8;
+    // XM & 16: every wave has at most one row (N <= the grid's row step), so
+    // the second register set of the pipeline is neither loaded nor held.
+    constexpr bool ONE = XM & 16;
     constexpr int XF4 = NC * CW / 4;                  // staged float4 slots
     constexpr int PER = (XF4 + NT - 1) / NT;          // float4 per thread
     constexpr int NP = MERGE ? kAttnMaxChunks / PER : 1;   // chunks a merge holds in registers
@@ -390,7 +393,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(
         // before any weight request, so x is not queued behind the stream.
         __builtin_amdgcn_s_barrier();
         gemv_load<WT, NM, RPW, NC>(A, qa, da, qb, db, row0, N, K, lane);
-        gemv_load<WT, NM, RPW, NC>(B, qa, da, qb, db, row0 + rstep, N, K, lane);
+        if constexpr (!ONE) gemv_load<WT, NM, RPW, NC>(B, qa, da, qb, db, row0 + rstep, N, K, lane);
 
         if constexpr (MERGE) {
 #pragma unroll
@@ -466,6 +469,10 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(
         }
     }
 
+    if constexpr (ONE) {
+        if (row0 < N) gemv_compute<WT, NM, RPW, NC, SWIGLU, RES>(A, xs4, xsum, inv, row0, N, K, lane, residual, y);
+        return;
+    }
     // Loads stay unconditional inside the loop as well (see gemv_load).
     for (; row0 < N; row0 += 2 * rstep) {
         const int r1 = row0 + rstep;
@@ -491,7 +498,9 @@ int launch_gemv(hipStream_t s, const DevWeight& a, const DevWeight* b, const flo
     VH_ARG(!(residual && SWIGLU), "gemv: no residual on the SwiGLU form");
     VH_ARG(!nparts || (!x_row && !norm_w && !SWIGLU && nparts <= kAttnMaxChunks && a.K % 64 == 0),
            "gemv: chunk merge takes a plain x of whole 64-wide heads and at most %d chunks", kAttnMaxChunks);
-    const int xm = (x_row ? 2 : 0) | (norm_w ? 1 : 0) | (residual ? 4 : 0) | (nparts ? 8 : 0);
+    const int groups1 = (a.N + kGemvWaves - 1) / kGemvWaves;
+    const bool one = groups1 <= kGemvMaxGroups;          // RPW 1: one row per wave
+    const int xm = (x_row ? 2 : 0) | (norm_w ? 1 : 0) | (residual ? 4 : 0) | (nparts ? 8 : 0) | (one ? 16 : 0);
 #define VH_GEMV_XM(NC, RPW, XM)                                                                            \
     do {                                                                                                  \
         const int groups = (a.N + kGemvWaves * (RPW)-1) / (kGemvWaves * (RPW));                            \
@@ -503,12 +512,19 @@ int launch_gemv(hipStream_t s, const DevWeight& a, const DevWeight* b, const flo
     do {                                                                  \
         if (xm == 0) VH_GEMV_XM(NC, RPW, 0);                              \
         else if (xm == 1) VH_GEMV_XM(NC, RPW, 1);                         \
+        else if (xm == 16) VH_GEMV_XM(NC, RPW, 16);                       \
+        else if (xm == 17) VH_GEMV_XM(NC, RPW, 17);                       \
         else if constexpr (!SWIGLU) {                                     \
             if (xm == 3) VH_GEMV_XM(NC, RPW, 3);                          \
             else if (xm == 4) VH_GEMV_XM(NC, RPW, 4);                     \
             else if (xm == 5) VH_GEMV_XM(NC, RPW, 5);                     \
             else if (xm == 7) VH_GEMV_XM(NC, RPW, 7);                     \
             else if (xm == 12) VH_GEMV_XM(NC, RPW, 12);                   \
+            else if (xm == 19) VH_GEMV_XM(NC, RPW, 19);                   \
+            else if (xm == 20) VH_GEMV_XM(NC, RPW, 20);                   \
+            else if (xm == 21) VH_GEMV_XM(NC, RPW, 21);                   \
+            else if (xm == 23) VH_GEMV_XM(NC, RPW, 23);                   \
+            else if (xm == 28) VH_GEMV_XM(NC, RPW, 28);                   \
         }                                                                 \
     } while (0)
     if (nc <= 1) {
