@@ -200,6 +200,7 @@ struct Gemv<VLRF_DT_Q4_0> { static constexpr int EPL = 32; static constexpr floa
 constexpr float kNegInfF = -INFINITY;
 constexpr int kGemvMaxK = 6144;          // staged activations: 24 KiB of LDS
 constexpr int kGemvMaxGroups = 512;      // workgroups of the row loop (2 per CU)
+constexpr int kGemvMaxOneGroups = 768;   // one row per wave up to 3 workgroups per CU
 constexpr int kGemvWaves = 8;            // waves per workgroup (one staged copy of x)
 
 __device__ __forceinline__ float ub(uint32_t v, int k) { return (float)((v >> (8 * k)) & 0xFFu); }
@@ -499,12 +500,12 @@ int launch_gemv(hipStream_t s, const DevWeight& a, const DevWeight* b, const flo
     VH_ARG(!nparts || (!x_row && !norm_w && !SWIGLU && nparts <= kAttnMaxChunks && a.K % 64 == 0),
            "gemv: chunk merge takes a plain x of whole 64-wide heads and at most %d chunks", kAttnMaxChunks);
     const int groups1 = (a.N + kGemvWaves - 1) / kGemvWaves;
-    const bool one = groups1 <= kGemvMaxGroups;          // RPW 1: one row per wave
+    const bool one = groups1 <= kGemvMaxOneGroups;       // RPW 1: one row per wave
     const int xm = (x_row ? 2 : 0) | (norm_w ? 1 : 0) | (residual ? 4 : 0) | (nparts ? 8 : 0) | (one ? 16 : 0);
 #define VH_GEMV_XM(NC, RPW, XM)                                                                            \
     do {                                                                                                  \
         const int groups = (a.N + kGemvWaves * (RPW)-1) / (kGemvWaves * (RPW));                            \
-        dim3 grid(groups < kGemvMaxGroups ? groups : kGemvMaxGroups);                                      \
+        dim3 grid(((XM)&16) || groups < kGemvMaxGroups ? groups : kGemvMaxGroups);                         \
         hipLaunchKernelGGL((gemv_kernel<WT, NC, RPW, SWIGLU, XM>), grid, dim3(64 * kGemvWaves), 0, s, a.q, \
                            a.d, qb, db, a.N, a.K, x, x_row, x_copy, norm_w, eps, residual, y, nparts);      \
     } while (0)
