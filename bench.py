@@ -88,7 +88,9 @@ def gemv_roofline(ctx, V, F, cfg, dtype, launches=96):
     algo = wbytes + D * 4 * 2 + Fd * 4          # weights + x + norm weight + h
     achieved = algo / per_launch_s / 1e9
     chunk = 64 * (16 if dtype == V.DT_Q8_0 else 32)      # K columns per lane-chunk of one wave
-    name = "gemv_kernel<%d, %d, 1, true, 1>" % (dtype, (D + chunk - 1) // chunk)   # XM 1: fused RMSNorm
+    # XM: 1 fused RMSNorm, + 16 when every wave holds one row (at most 768 workgroups of 8 rows)
+    xm = 1 | (16 if (Fd + 7) // 8 <= 768 else 0)
+    name = "gemv_kernel<%d, %d, 1, true, %d>" % (dtype, (D + chunk - 1) // chunk, xm)
     return {"kernel": name + " (RMSNorm + gate/up %dx%d + SwiGLU)" % (Fd, D),
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": pmc_traffic(dtype),
