@@ -503,6 +503,10 @@ __global__ __launch_bounds__(CH ? CH : 64 * kSPWaves) void attn_decode_single_ke
     };
 #pragma unroll
     for (int r = 0; r < kSPDepth; ++r) load_round(r, r);
+    // Every K/V load is issued before the device position's load and the wait on
+    // it (the RoPE table rows depend on it): left to the scheduler, that wait
+    // lands between the K and the V loads.
+    __builtin_amdgcn_sched_barrier(0);
 
     const int dpos = (FUSED || ctx_dev) ? *ctx_dev : 0;   // fused: always a device position
     int ctx = FUSED ? dpos + 1 : (ctx_dev ? dpos + ctx_len : ctx_len);
@@ -510,14 +514,10 @@ __global__ __launch_bounds__(CH ? CH : 64 * kSPWaves) void attn_decode_single_ke
     const int pos = FUSED ? dpos : -1;
     const bool rot = FUSED && pos < fz.max_seq;      // rope.hpp:84: positions >= max_seq stay unrotated
     const bool has_new = FUSED && (CH == 0 || (pos >= c0 && pos < c0 + CH));
-    if constexpr (CH > 0) {
-        if (c0 >= ctx) {                             // chunk past the context: empty partial
-            float* pp = out + ((size_t)h * nch + chunk) * kChunkStride;
-            if (tid < D) pp[tid] = 0.f;
-            if (tid == 0) { pp[D] = kNegInf; pp[D + 1] = 0.f; }
-            return;
-        }
-    }
+    // A chunk past the context takes no early exit: it runs no round and the merge
+    // writes its empty partial (acc 0, m -inf, l 0).  An exit on the device
+    // position here lets the compiler sink the K/V loads below that position's
+    // load, adding its round trip to every workgroup.
 
     // ---- q of head h (wave 0) and, fused, the new row's RoPE and maxima -------------
     // Every RoPE pair a thread rotates has pair index tid % HALF.
