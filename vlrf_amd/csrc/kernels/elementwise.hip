@@ -292,8 +292,8 @@ __global__ __launch_bounds__(256) void embed_kernel(const float* __restrict__ ta
 constexpr int kArgmaxPer = 16;   // float4 per thread: n <= 1024*4*16 = 65536
 __global__ __launch_bounds__(1024) void argmax_step_kernel(const float* __restrict__ logits, int n,
                                                            int* state, int* gen_ids, int gen_cap) {
-    __shared__ float bv[1024];
-    __shared__ int bi[1024];
+    __shared__ float bv[16];
+    __shared__ int bi[16];
     const int tid = threadIdx.x;
     const int n4 = n / 4;
     float4 v[kArgmaxPer];
@@ -318,23 +318,32 @@ __global__ __launch_bounds__(1024) void argmax_step_kernel(const float* __restri
         const float e = logits[i];
         if (idx < 0 || best < e || (best == e && i < idx)) { best = e; idx = i; }
     }
-    bv[tid] = best;
-    bi[tid] = idx;
+    // Wave butterfly, then wave 0 over the 16 wave results: one barrier.  The
+    // rule (larger value; the lower index on equal values) gives the same
+    // winner in any combining order.
+    auto take = [&](float ov, int oi) {
+        if (oi >= 0 && (idx < 0 || best < ov || (best == ov && oi < idx))) { best = ov; idx = oi; }
+    };
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(best, o);
+        const int oi = __shfl_xor(idx, o);
+        take(ov, oi);
+    }
+    if ((tid & 63) == 0) { bv[tid >> 6] = best; bi[tid >> 6] = idx; }
     __syncthreads();
-    for (int off = 512; off > 0; off >>= 1) {
-        if (tid < off) {
-            const float ov = bv[tid + off];
-            const int oi = bi[tid + off];
-            const int mi = bi[tid];
-            if (oi >= 0 && (mi < 0 || bv[tid] < ov || (bv[tid] == ov && oi < mi))) {
-                bv[tid] = ov;
-                bi[tid] = oi;
-            }
+    if (tid < 64) {
+        best = tid < 16 ? bv[tid] : -INFINITY;
+        idx = tid < 16 ? bi[tid] : -1;
+#pragma unroll
+        for (int o = 8; o > 0; o >>= 1) {
+            const float ov = __shfl_xor(best, o);
+            const int oi = __shfl_xor(idx, o);
+            take(ov, oi);
         }
-        __syncthreads();
     }
     if (tid == 0) {
-        const int tok = bi[0] < 0 ? 0 : bi[0];
+        const int tok = idx < 0 ? 0 : idx;
         state[0] = tok;
         const int g = state[2];
         if (g < gen_cap) gen_ids[g] = tok;
