@@ -28,6 +28,7 @@
 // O projection's GEMV prologue, so the step has no combine launch; caches of
 // at most 512 rows take the single pass over the whole context.
 #include "../internal.hpp"
+#include "attn_core.hpp"
 
 #include <cmath>
 
@@ -39,13 +40,7 @@ constexpr int kAttnThreads = 512;  // lanes per decode-attention workgroup (8 wa
 constexpr int kMaxSplits = 512;   // contexts up to 32768 tokens
 constexpr float kNegInf = -INFINITY;
 
-// RoPE of one pair (rope.hpp:90-96), each product rounded separately.
-__device__ __forceinline__ void rope2(float x0, float x1, float c, float s, float* y0, float* y1) {
-#pragma clang fp contract(off)
-    const float a = x0 * c, b = x1 * s, e = x1 * c, f = x0 * s;
-    *y0 = a - b;
-    *y1 = e + f;
-}
+using attn::rope2;
 
 // KVT: cache element type VLRF_KV_Q8_0 (int8 codes, f32 scale per token row),
 // VLRF_KV_F16 (the reference's f16 bits) or VLRF_KV_F32; kc/vc address the
@@ -380,10 +375,10 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_partial_kernel(
 // softmax (m, l) with wave reductions, and accumulates P.V with lane
 // (tg, dg) = (lane/4, lane%4) owning dims 16dg..16dg+15 over tokens tg + 16j,
 // reading the V elements as 16-element row pieces (each load a contiguous run)
-// and the Q8_0 row scales folded into p.  kSPDepth rounds of K/V are loaded up
-// front and each round's registers are refilled that many rounds ahead.  At
-// the end the 16 lanes of a dim group are summed with xor shuffles and the
-// waves' (m, l, acc) are merged in LDS with the log-sum-exp rule.  The fused
+// and the Q8_0 row scales folded into p.  Each wave loads its one round up
+// front (attn::load_round, attn::chunk).  At the end the 16 lanes of a dim
+// group are summed with xor shuffles and the waves' (m, l, acc) are merged in
+// LDS with the log-sum-exp rule.  The fused
 // form rotates and stores the new token's row in every workgroup (identical
 // results; the group's first head writes it), leaves the token at `pos` out
 // of the rounds (its cache row may not be written yet) and adds it to the
@@ -401,25 +396,6 @@ constexpr int kSPMaxCtx = kSPWaves * 64 * kSPRounds;   // cache rows the single 
 // merged by the next GEMV's prologue.
 constexpr int kCH = 512, kChunkStride = kAttnChunkStride;   // 256 / 1024: 0.645 / 0.673 ms per step against 0.620
 
-// Elements 4i..4i+3 of a 64-element row held as 16-byte words, as f32.
-template <int KVT>
-__device__ __forceinline__ float4 row4(const uint4* wds, int i) {
-    if constexpr (KVT == VLRF_KV_Q8_0) {
-        const uint4 k = wds[i >> 2];
-        const uint32_t u = (i & 3) == 0 ? k.x : (i & 3) == 1 ? k.y : (i & 3) == 2 ? k.z : k.w;
-        return make_float4((float)(int8_t)u, (float)(int8_t)(u >> 8), (float)(int8_t)(u >> 16),
-                           (float)(int8_t)(u >> 24));
-    } else if constexpr (KVT == VLRF_KV_F16) {
-        const uint4 k = wds[i >> 1];
-        const uint32_t a = (i & 1) ? k.z : k.x, b = (i & 1) ? k.w : k.y;
-        return make_float4(f16_bits_to_f32(a & 0xFFFFu), f16_bits_to_f32(a >> 16), f16_bits_to_f32(b & 0xFFFFu),
-                           f16_bits_to_f32(b >> 16));
-    } else {
-        const uint4 k = wds[i];
-        return make_float4(__uint_as_float(k.x), __uint_as_float(k.y), __uint_as_float(k.z), __uint_as_float(k.w));
-    }
-}
-
 // CH > 0 (fused decode only): the same algorithm on one CH-token chunk of the
 // cache per workgroup, NW = CH/64 waves of one round, for query head h of
 // chunk s; the result is the chunk's partial (m, l, acc) at out[h][s][*]
@@ -430,16 +406,9 @@ __global__ __launch_bounds__(CH ? CH : 64 * kSPWaves) void attn_decode_single_ke
     long head_stride, int ctx_len, const int* __restrict__ ctx_dev, float scale, float* __restrict__ out,
     DecodeFuse fz, int nch) {
     static_assert(CH == 0 || (FUSED && CH % 64 == 0), "chunks: fused decode, whole rounds");
-    constexpr bool Q8 = KVT == VLRF_KV_Q8_0, H16 = KVT == VLRF_KV_F16;
-    constexpr int D = 64, HALF = 32, NW = CH ? CH / 64 : kSPWaves;
-    constexpr int EB = Q8 ? 1 : H16 ? 2 : 4;         // bytes per element
-    constexpr int KW = D * EB / 16, VW = EB;         // 16-byte words: a K row, a 16-element V piece
-    __shared__ __align__(16) float qs[D];
-    __shared__ __align__(16) float nk[D], nv[D];     // the new token's stored row of KV head g, read back
-    __shared__ float amax[2 * NW];                   // per-wave maxima of the new K and V rows
-    __shared__ __align__(16) float pbuf[NW][64];     // p (times the V row scale) of the wave's current round
-    __shared__ float wm[NW], wl[NW];
-    __shared__ __align__(16) float wacc[NW][D];
+    static_assert(kSPRounds == 1 && kSPDepth == 1, "attn::chunk runs one round per wave");
+    constexpr int D = attn::D, HALF = attn::HALF, NW = CH ? CH / 64 : kSPWaves;
+    __shared__ attn::Smem<NW> sm;
 
     int h, g, c0 = 0, chunk = 0;
     if constexpr (CH > 0) {
@@ -457,12 +426,11 @@ __global__ __launch_bounds__(CH ? CH : 64 * kSPWaves) void attn_decode_single_ke
         g = h / REP;
     }
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int tg = lane >> 2, dg = lane & 3;
     const int cap = (int)(head_stride / D);
     const size_t hb = (size_t)g * head_stride;
 
     // Loads first, all branch-free with rows clamped into the cache (masked at use):
-    // q, the new row (fused), the rounds' K/V, and only then the device position.
+    // q, the new row (fused), the round's K/V, and only then the device position.
     float q0 = 0.f, q1 = 0.f;
     if (w == 0) {
         const int j = lane & (HALF - 1);
@@ -472,37 +440,17 @@ __global__ __launch_bounds__(CH ? CH : 64 * kSPWaves) void attn_decode_single_ke
     // The new row (fused; n_kv <= 8, so at most 512 elements): thread t holds K
     // RoPE pair t and V elements t and (with 256 threads) t + NT.
     constexpr int NT = 64 * NW;
-    constexpr bool V2 = NT < 512;
-    const int npairs = FUSED ? fz.n_kv * HALF : 0, nrow = FUSED ? fz.n_kv * D : 0;
-    float k0 = 0.f, k1 = 0.f, vn = 0.f, vn2 = 0.f;
+    attn::NewRow nr;
     if constexpr (FUSED) {
+        const int npairs = fz.n_kv * HALF, nrow = fz.n_kv * D;
         const int i = min(tid, npairs - 1), hh = i / HALF, j = i - hh * HALF;
-        k0 = fz.k_new[hh * D + j];
-        k1 = fz.k_new[hh * D + j + HALF];
-        vn = fz.v_new[min(tid, nrow - 1)];
-        if constexpr (V2) vn2 = fz.v_new[min(tid + NT, nrow - 1)];
+        nr.k0 = fz.k_new[hh * D + j];
+        nr.k1 = fz.k_new[hh * D + j + HALF];
+        nr.vn = fz.v_new[min(tid, nrow - 1)];
+        if constexpr (NT < 512) nr.vn2 = fz.v_new[min(tid + NT, nrow - 1)];
     }
-    // A round's K/V in registers: K row of token base+lane, V pieces of tokens base+tg+16j.
-    uint4 kr[kSPDepth][KW], vr[kSPDepth][4][VW];
-    float ksr[kSPDepth], vsr[kSPDepth];
-    auto load_round = [&](int r, int b) {
-        const int base = c0 + (r * NW + w) * 64;
-        const int t = min(base + lane, cap - 1);
-#pragma unroll
-        for (int i = 0; i < KW; ++i)
-            kr[b][i] = *reinterpret_cast<const uint4*>(kc + (hb + (size_t)t * D) * EB + 16 * i);
-        ksr[b] = Q8 ? ks[t] : 1.f;
-        vsr[b] = Q8 ? vs[t] : 1.f;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int tv = min(base + tg + 16 * j, cap - 1);
-#pragma unroll
-            for (int i = 0; i < VW; ++i)
-                vr[b][j][i] = *reinterpret_cast<const uint4*>(vc + (hb + (size_t)tv * D + 16 * dg) * EB + 16 * i);
-        }
-    };
-#pragma unroll
-    for (int r = 0; r < kSPDepth; ++r) load_round(r, r);
+    attn::Round<KVT> R;
+    attn::load_round<KVT>(R, kc, vc, ks, vs, hb, c0 + w * 64, cap, lane);
     // Every K/V load is issued before the device position's load and the wait on
     // it (the RoPE table rows depend on it): left to the scheduler, that wait
     // lands between the K and the V loads.
@@ -514,198 +462,21 @@ __global__ __launch_bounds__(CH ? CH : 64 * kSPWaves) void attn_decode_single_ke
     const int pos = FUSED ? dpos : -1;
     const bool rot = FUSED && pos < fz.max_seq;      // rope.hpp:84: positions >= max_seq stay unrotated
     const bool has_new = FUSED && (CH == 0 || (pos >= c0 && pos < c0 + CH));
+    if constexpr (FUSED) attn::rope_row(nr, fz, pos);
     // A chunk past the context takes no early exit: it runs no round and the merge
     // writes its empty partial (acc 0, m -inf, l 0).  An exit on the device
     // position here lets the compiler sink the K/V loads below that position's
     // load, adding its round trip to every workgroup.
-
-    // ---- q of head h (wave 0) and, fused, the new row's RoPE and maxima -------------
-    // Every RoPE pair a thread rotates has pair index tid % HALF.
-    float rc = 1.f, rs = 0.f;
-    if constexpr (FUSED) {
-        const int trow = min(pos, fz.max_seq - 1);
-        rc = fz.cos_t[(size_t)trow * HALF + (lane & (HALF - 1))];
-        rs = fz.sin_t[(size_t)trow * HALF + (lane & (HALF - 1))];
-    }
-    if (w == 0 && lane < HALF) {
-        if (rot) rope2(q0, q1, rc, rs, &qs[lane], &qs[lane + HALF]);
-        else { qs[lane] = q0; qs[lane + HALF] = q1; }
-    }
-    if constexpr (FUSED) {
-        // attention.hpp:109-128: RoPE on k, then KVCache::append stores the row
-        // before attention reads it back: Q8_0 quantizes the whole row with one
-        // scale (kv_cache.hpp:102-117); the row maxima are merged through LDS and
-        // the row is quantized after the rounds, off their critical path.
-        if (has_new) {
-            if (tid < npairs && rot) rope2(k0, k1, rc, rs, &k0, &k1);
-            if constexpr (Q8) {
-                float ak = wave_max(tid < npairs ? fmaxf(fabsf(k0), fabsf(k1)) : 0.f);
-                float av = tid < nrow ? fabsf(vn) : 0.f;
-                if (V2 && tid + NT < nrow) av = fmaxf(av, fabsf(vn2));
-                av = wave_max(av);
-                if (lane == 0) { amax[w] = ak; amax[NW + w] = av; }
-            }
-        }
-    }
-    __syncthreads();
-
-    // ---- rounds ----------------------------------------------------------------------
-    const int nrounds = (ctx - c0 + 63) / 64;
-    float m_run = kNegInf, l_run = 0.f, acc[16];
-#pragma unroll
-    for (int e = 0; e < 16; ++e) acc[e] = 0.f;
-#pragma unroll
-    for (int r = 0; r < kSPRounds; ++r) {
-        if (r * NW + w >= nrounds) break;
-        const int b = r % kSPDepth, base = c0 + (r * NW + w) * 64;
-        // scores: lane = token base + lane; the new token (fused) is merged at the end
-        const int t = base + lane;
-        float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
-#pragma unroll
-        for (int i = 0; i < D / 4; ++i) {
-            const float4 qv = *reinterpret_cast<const float4*>(&qs[4 * i]);
-            const float4 kf = row4<KVT>(kr[b], i);
-            s0 += qv.x * kf.x;
-            s1 += qv.y * kf.y;
-            s2 += qv.z * kf.z;
-            s3 += qv.w * kf.w;
-        }
-        const bool live = t < ctx && t != pos;
-        const float sc = live ? ((s0 + s1) + (s2 + s3)) * ksr[b] * scale : kNegInf;
-        const float mx = fmaxf(m_run, wave_max(sc));
-        const float corr = m_run == kNegInf ? 0.f : expf(m_run - mx);
-        const float pe = live ? expf(sc - mx) : 0.f;
-        l_run = l_run * corr + wave_sum(pe);
-        m_run = mx;
-        pbuf[w][lane] = pe * vsr[b];
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        // P.V: lane (tg, dg) over tokens tg + 16j of the round, dims 16dg..16dg+15
-#pragma unroll
-        for (int e = 0; e < 16; ++e) acc[e] *= corr;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const float pp = pbuf[w][tg + 16 * j];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float4 v4 = row4<KVT>(vr[b][j], i);
-                acc[4 * i] += pp * v4.x;
-                acc[4 * i + 1] += pp * v4.y;
-                acc[4 * i + 2] += pp * v4.z;
-                acc[4 * i + 3] += pp * v4.w;
-            }
-        }
-        __builtin_amdgcn_wave_barrier();               // pbuf is rewritten next round
-        if (r + kSPDepth < kSPRounds && (r + kSPDepth) * NW + w < nrounds) load_round(r + kSPDepth, b);
-    }
-
-    // ---- fused: quantize and store the new row; the merge reads it back from LDS -----
-    // (F16 converts each element, kv_cache.hpp:68-97; F32 copies.)  The group's
-    // first head stores head g's elements, never past the cache.
-    if (FUSED && has_new) {
-        float ak = 0.f, av = 0.f, sk = 1.f, sv = 1.f, ik = 0.f, iv = 0.f;
-        if constexpr (Q8) {
-#pragma unroll
-            for (int k = 0; k < NW; ++k) {
-                ak = fmaxf(ak, amax[k]);
-                av = fmaxf(av, amax[NW + k]);
-            }
-            sk = ak != 0.f ? ak / 127.f : 0.f;
-            sv = av != 0.f ? av / 127.f : 0.f;
-            ik = ak != 0.f ? 1.f / sk : 0.f;
-            iv = av != 0.f ? 1.f / sv : 0.f;
-        }
-        const bool writer = h % REP == 0 && pos < cap;
-        int8_t* krow = fz.kq_w + (hb + (size_t)pos * D) * EB;
-        int8_t* vrow = fz.vq_w + (hb + (size_t)pos * D) * EB;
-        // stores element j of a row (when writer) and returns the value attention reads back
-        auto put = [&](int8_t* row, int j, float x, float sc, float inv, bool nz) -> float {
-            if constexpr (Q8) {
-                const int c = nz ? min(127, max(-127, (int)roundf(x * inv))) : 0;
-                if (writer) row[j] = (int8_t)c;
-                return (float)c * sc;
-            } else if constexpr (H16) {
-                const uint16_t hb16 = f32_to_f16_kv(x);
-                if (writer) reinterpret_cast<uint16_t*>(row)[j] = hb16;
-                return f16_bits_to_f32(hb16);
-            } else {
-                if (writer) reinterpret_cast<float*>(row)[j] = x;
-                return x;
-            }
-        };
-        if (tid < npairs && tid / HALF == g) {
-            const int j = tid % HALF;
-            nk[j] = put(krow, j, k0, sk, ik, ak != 0.f);
-            nk[j + HALF] = put(krow, j + HALF, k1, sk, ik, ak != 0.f);
-        }
-        if (tid < nrow && tid / D == g) nv[tid % D] = put(vrow, tid % D, vn, sv, iv, av != 0.f);
-        if (V2 && tid + NT < nrow && (tid + NT) / D == g)
-            nv[(tid + NT) % D] = put(vrow, (tid + NT) % D, vn2, sv, iv, av != 0.f);
-        if constexpr (Q8) {
-            if (h == 0 && tid == 0 && pos < cap) { fz.ks_w[pos] = sk; fz.vs_w[pos] = sv; }
-        }
-    }
-
-    // ---- merge: lanes of a dim group, then the waves -------------------------------
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-        // sum over the 16 lanes tg of dim group dg: rotations by 4 and 8 within a
-        // 16-lane row (DPP row_ror), then the row and half exchanges
-        float v = acc[e];
-        v += dpp_f<0x124>(v);
-        v += dpp_f<0x128>(v);
-        float2 t = swap_rows16(v, v);
-        v = t.x + t.y;
-        t = swap_halves32(v, v);
-        acc[e] = t.x + t.y;
-    }
-    if (tg == 0) {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) wacc[w][16 * dg + e] = acc[e];
-    }
-    if (lane == 0) { wm[w] = m_run; wl[w] = l_run; }
-    __syncthreads();
-    if (tid < D) {
-        // The new token (fused): score q . k_stored, weight 1, value its stored V row.
-        float sn = kNegInf;
-        if (FUSED && has_new) {
-            float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-#pragma unroll
-            for (int i = 0; i < D / 4; ++i) {
-                const float4 qv = *reinterpret_cast<const float4*>(&qs[4 * i]);
-                const float4 kv = *reinterpret_cast<const float4*>(&nk[4 * i]);
-                a0 += qv.x * kv.x;
-                a1 += qv.y * kv.y;
-                a2 += qv.z * kv.z;
-                a3 += qv.w * kv.w;
-            }
-            sn = ((a0 + a1) + (a2 + a3)) * scale;
-        }
-        float mt = sn;
-#pragma unroll
-        for (int k = 0; k < NW; ++k) mt = fmaxf(mt, wm[k]);
-        float lt = 0.f, ot = 0.f;
-        if (FUSED && has_new) {
-            lt = expf(sn - mt);
-            ot = lt * nv[tid];
-        }
-#pragma unroll
-        for (int k = 0; k < NW; ++k) {
-            if (wm[k] != kNegInf) {
-                const float c = expf(wm[k] - mt);
-                lt += c * wl[k];
-                ot += c * wacc[k][tid];
-            }
-        }
-        if constexpr (CH > 0) {                      // the chunk's partial, unnormalised
-            float* pp = out + ((size_t)h * nch + chunk) * kChunkStride;
-            pp[tid] = ot;
-            if (tid == 0) { pp[D] = mt; pp[D + 1] = lt; }
-        } else {
-            out[(size_t)h * D + tid] = lt > 0.f ? ot * (1.f / lt) : 0.f;
-        }
-    }
+    attn::chunk<KVT, FUSED, NW>(sm, R, q0, q1, nr, h % REP == 0, h == 0, g, c0, cap, hb, ctx, pos, rot, has_new, scale, fz,
+                                [&](int t, float ot, float mt, float lt) {
+                                    if constexpr (CH > 0) {   // the chunk's partial, unnormalised
+                                        float* pp = out + ((size_t)h * nch + chunk) * kChunkStride;
+                                        pp[t] = ot;
+                                        if (t == 0) { pp[D] = mt; pp[D + 1] = lt; }
+                                    } else {
+                                        out[(size_t)h * D + t] = lt > 0.f ? ot * (1.f / lt) : 0.f;
+                                    }
+                                });
 }
 
 // Log-sum-exp merge of the per-chunk partials of one query head.  The 256

@@ -1,0 +1,329 @@
+// attn_core.hpp - the decode attention of one query head over one block of
+// cache rows, shared by the stand-alone decode kernel (attention.hip) and the
+// one-launch decode step (flow.hip).
+//
+// Reference semantics: AttentionBlock::flash_attn_head (attention.hpp:207-309)
+// for T = 1 (non-causal, attention.hpp:171), scale 1/sqrt(d_h)
+// (attention.hpp:373-374); with decode fusion the token's K/V row is rotated
+// (rope.hpp:90-96) and stored (kv_cache.hpp:102-117) before attention reads it
+// back (attention.hpp:109-145).
+//
+// Layout: NW waves of 64 lanes; wave w scores the 64 rows c0 + 64w + lane
+// against q (lane = token; the softmax max and sum are wave reductions) and
+// accumulates P.V with lane (tg, dg) = (lane/4, lane%4) owning dims
+// 16dg..16dg+15 over tokens tg + 16j, the V rows read as 16-element pieces.
+// The waves' (m, l, acc) are merged in LDS with the log-sum-exp rule.  Under
+// fusion the row at `pos` is left out of the rounds (its cache row may not be
+// written yet) and merged as one more entry (score q.k_stored, weight 1, value
+// the stored V row).
+#pragma once
+
+#include "../internal.hpp"
+
+#include <cmath>
+
+namespace vlrf_hip {
+namespace attn {
+
+constexpr int D = 64, HALF = 32;
+constexpr float kNegInf = -INFINITY;
+
+// RoPE of one pair (rope.hpp:90-96), each product rounded separately.
+__device__ __forceinline__ void rope2(float x0, float x1, float c, float s, float* y0, float* y1) {
+#pragma clang fp contract(off)
+    const float a = x0 * c, b = x1 * s, e = x1 * c, f = x0 * s;
+    *y0 = a - b;
+    *y1 = e + f;
+}
+
+// Elements 4i..4i+3 of a 64-element row held as 16-byte words, as f32.
+template <int KVT>
+__device__ __forceinline__ float4 row4(const uint4* wds, int i) {
+    if constexpr (KVT == VLRF_KV_Q8_0) {
+        const uint4 k = wds[i >> 2];
+        const uint32_t u = (i & 3) == 0 ? k.x : (i & 3) == 1 ? k.y : (i & 3) == 2 ? k.z : k.w;
+        return make_float4((float)(int8_t)u, (float)(int8_t)(u >> 8), (float)(int8_t)(u >> 16),
+                           (float)(int8_t)(u >> 24));
+    } else if constexpr (KVT == VLRF_KV_F16) {
+        const uint4 k = wds[i >> 1];
+        const uint32_t a = (i & 1) ? k.z : k.x, b = (i & 1) ? k.w : k.y;
+        return make_float4(f16_bits_to_f32(a & 0xFFFFu), f16_bits_to_f32(a >> 16), f16_bits_to_f32(b & 0xFFFFu),
+                           f16_bits_to_f32(b >> 16));
+    } else {
+        const uint4 k = wds[i];
+        return make_float4(__uint_as_float(k.x), __uint_as_float(k.y), __uint_as_float(k.z), __uint_as_float(k.w));
+    }
+}
+
+template <int KVT>
+struct KV {
+    static constexpr int EB = KVT == VLRF_KV_Q8_0 ? 1 : KVT == VLRF_KV_F16 ? 2 : 4;   // bytes per element
+    static constexpr int KW = D * EB / 16;   // 16-byte words of a K row
+    static constexpr int VW = EB;            // 16-byte words of a 16-element V piece
+};
+
+// One round of cache rows in registers: the K row of token base + lane, the V
+// pieces of tokens base + tg + 16j (dims 16dg..16dg+15), and the Q8_0 row scales.
+template <int KVT>
+struct Round {
+    uint4 k[KV<KVT>::KW];
+    uint4 v[4][KV<KVT>::VW];
+    float ks, vs;
+};
+
+// Loads the round of wave w starting at row base (rows clamped into the cache;
+// rows past the context are masked where they are used).
+// Global-memory views: a pointer read from a table in memory is otherwise a
+// flat pointer, and flat loads also count against the LDS counter.
+typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
+typedef const __attribute__((address_space(1))) u32x4v gu32x4v;
+typedef const __attribute__((address_space(1))) float gfloat;
+__device__ __forceinline__ uint4 gload16(const int8_t* p) {
+    const u32x4v t = *(gu32x4v*)p;
+    return make_uint4(t.x, t.y, t.z, t.w);
+}
+
+template <int KVT>
+__device__ __forceinline__ void load_round(Round<KVT>& R, const int8_t* kc, const int8_t* vc, const float* ks,
+                                           const float* vs, size_t hb, int base, int cap, int lane) {
+    constexpr int EB = KV<KVT>::EB;
+    const int tg = lane >> 2, dg = lane & 3;
+    const int t = min(base + lane, cap - 1);
+#pragma unroll
+    for (int i = 0; i < KV<KVT>::KW; ++i)
+        R.k[i] = gload16(kc + (hb + (size_t)t * D) * EB + 16 * i);
+    R.ks = KVT == VLRF_KV_Q8_0 ? *(gfloat*)(ks + t) : 1.f;
+    R.vs = KVT == VLRF_KV_Q8_0 ? *(gfloat*)(vs + t) : 1.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int tv = min(base + tg + 16 * j, cap - 1);
+#pragma unroll
+        for (int i = 0; i < KV<KVT>::VW; ++i)
+            R.v[j][i] = gload16(vc + (hb + (size_t)tv * D + 16 * dg) * EB + 16 * i);
+    }
+}
+
+template <int NW>
+struct Smem {
+    __align__(16) float qs[D];
+    __align__(16) float nk[D];       // the new token's stored row of KV head g, read back
+    __align__(16) float nv[D];
+    float amax[2 * NW];              // per-wave maxima of the new K and V rows
+    __align__(16) float pbuf[NW][64];   // p (times the V row scale) of the wave's round
+    float wm[NW], wl[NW];
+    __align__(16) float wacc[NW][D];
+};
+
+// Inputs of the new token (fused): thread t holds K RoPE pair t (k0, k1) of
+// the row's n_kv heads and V elements t and t + 64*NW (vn, vn2), and the RoPE
+// table entries (rc, rs) of pair index lane % 32 at the token's position
+// (every pair a thread rotates has that index; cos 1, sin 0 when unfused).
+struct NewRow {
+    float k0 = 0.f, k1 = 0.f, vn = 0.f, vn2 = 0.f;
+    float rc = 1.f, rs = 0.f;
+};
+
+// The RoPE table entries of nr for the token at pos (rope.hpp:62-69 tables).
+__device__ __forceinline__ void rope_row(NewRow& nr, const DecodeFuse& fz, int pos) {
+    const int trow = min(pos, fz.max_seq - 1);
+    const int j = threadIdx.x & (HALF - 1);
+    nr.rc = fz.cos_t[(size_t)trow * HALF + j];
+    nr.rs = fz.sin_t[(size_t)trow * HALF + j];
+}
+
+// The attention of query head h (KV head g, whose rows start at element hb of
+// the cache) over rows [c0, c0 + 64*NW) of a context of ctx rows, for the
+// wave's loaded round R.  q0/q1 (wave 0, lane j < 32): q[j], q[j + 32].
+// FUSED: pos is the new token's row, rot whether RoPE applies, has_new whether
+// the row lies in this block; `writer` (the group's first head) stores head g's
+// elements of the row in the cache and `scale_writer` (query head 0) the Q8_0
+// row scales.  out(tid, acc, m, l) is called for tid < 64 with the
+// unnormalised result.
+template <int KVT, bool FUSED, int NW, class Out>
+__device__ __forceinline__ void chunk(Smem<NW>& sm, const Round<KVT>& R, float q0, float q1, const NewRow& nr, bool writer,
+                                      bool scale_writer, int g, int c0, int cap, size_t hb, int ctx, int pos, bool rot,
+                                      bool has_new, float scale, const DecodeFuse& fz, Out&& out) {
+    constexpr bool Q8 = KVT == VLRF_KV_Q8_0, H16 = KVT == VLRF_KV_F16;
+    constexpr int EB = KV<KVT>::EB, NT = 64 * NW;
+    constexpr bool V2 = NT < 512;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int tg = lane >> 2, dg = lane & 3;
+    const int npairs = FUSED ? fz.n_kv * HALF : 0, nrow = FUSED ? fz.n_kv * D : 0;
+    float k0 = nr.k0, k1 = nr.k1;
+    const float rc = nr.rc, rs = nr.rs;
+
+    // ---- q of head h (wave 0) and, fused, the new row's RoPE and maxima -------------
+    if (w == 0 && lane < HALF) {
+        if (rot) rope2(q0, q1, rc, rs, &sm.qs[lane], &sm.qs[lane + HALF]);
+        else { sm.qs[lane] = q0; sm.qs[lane + HALF] = q1; }
+    }
+    if constexpr (FUSED) {
+        // attention.hpp:109-128: RoPE on k, then KVCache::append stores the row
+        // before attention reads it back: Q8_0 quantizes the whole row with one
+        // scale (kv_cache.hpp:102-117); the row maxima are merged through LDS and
+        // the row is quantized after the rounds, off their critical path.
+        if (has_new) {
+            if (tid < npairs && rot) rope2(k0, k1, rc, rs, &k0, &k1);
+            if constexpr (Q8) {
+                float ak = wave_max(tid < npairs ? fmaxf(fabsf(k0), fabsf(k1)) : 0.f);
+                float av = tid < nrow ? fabsf(nr.vn) : 0.f;
+                if (V2 && tid + NT < nrow) av = fmaxf(av, fabsf(nr.vn2));
+                av = wave_max(av);
+                if (lane == 0) { sm.amax[w] = ak; sm.amax[NW + w] = av; }
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---- the wave's round -----------------------------------------------------------
+    const int nrounds = (ctx - c0 + 63) / 64;
+    float m_run = kNegInf, l_run = 0.f, acc[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+    if (w < nrounds) {
+        const int base = c0 + w * 64;
+        // scores: lane = token base + lane; the new token (fused) is merged at the end
+        const int t = base + lane;
+        float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+#pragma unroll
+        for (int i = 0; i < D / 4; ++i) {
+            const float4 qv = *reinterpret_cast<const float4*>(&sm.qs[4 * i]);
+            const float4 kf = row4<KVT>(R.k, i);
+            s0 += qv.x * kf.x;
+            s1 += qv.y * kf.y;
+            s2 += qv.z * kf.z;
+            s3 += qv.w * kf.w;
+        }
+        const bool live = t < ctx && t != pos;
+        const float sc = live ? ((s0 + s1) + (s2 + s3)) * R.ks * scale : kNegInf;
+        const float mx = fmaxf(m_run, wave_max(sc));
+        const float corr = m_run == kNegInf ? 0.f : expf(m_run - mx);
+        const float pe = live ? expf(sc - mx) : 0.f;
+        l_run = l_run * corr + wave_sum(pe);
+        m_run = mx;
+        sm.pbuf[w][lane] = pe * R.vs;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // P.V: lane (tg, dg) over tokens tg + 16j of the round, dims 16dg..16dg+15
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[e] *= corr;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float pp = sm.pbuf[w][tg + 16 * j];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float4 v4 = row4<KVT>(R.v[j], i);
+                acc[4 * i] += pp * v4.x;
+                acc[4 * i + 1] += pp * v4.y;
+                acc[4 * i + 2] += pp * v4.z;
+                acc[4 * i + 3] += pp * v4.w;
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+
+    // ---- fused: quantize and store the new row; the merge reads it back from LDS -----
+    // (F16 converts each element, kv_cache.hpp:68-97; F32 copies.)  The group's
+    // first head stores head g's elements, never past the cache.
+    if (FUSED && has_new) {
+        float ak = 0.f, av = 0.f, sk = 1.f, sv = 1.f, ik = 0.f, iv = 0.f;
+        if constexpr (Q8) {
+#pragma unroll
+            for (int k = 0; k < NW; ++k) {
+                ak = fmaxf(ak, sm.amax[k]);
+                av = fmaxf(av, sm.amax[NW + k]);
+            }
+            sk = ak != 0.f ? ak / 127.f : 0.f;
+            sv = av != 0.f ? av / 127.f : 0.f;
+            ik = ak != 0.f ? 1.f / sk : 0.f;
+            iv = av != 0.f ? 1.f / sv : 0.f;
+        }
+        const bool wr = writer && pos < cap;
+        int8_t* krow = fz.kq_w + (hb + (size_t)pos * D) * EB;
+        int8_t* vrow = fz.vq_w + (hb + (size_t)pos * D) * EB;
+        // stores element j of a row (when writer) and returns the value attention reads back
+        auto put = [&](int8_t* row, int j, float x, float sc, float inv, bool nz) -> float {
+            if constexpr (Q8) {
+                const int c = nz ? min(127, max(-127, (int)roundf(x * inv))) : 0;
+                if (wr) row[j] = (int8_t)c;
+                return (float)c * sc;
+            } else if constexpr (H16) {
+                const uint16_t hb16 = f32_to_f16_kv(x);
+                if (wr) reinterpret_cast<uint16_t*>(row)[j] = hb16;
+                return f16_bits_to_f32(hb16);
+            } else {
+                if (wr) reinterpret_cast<float*>(row)[j] = x;
+                return x;
+            }
+        };
+        if (tid < npairs && tid / HALF == g) {
+            const int j = tid % HALF;
+            sm.nk[j] = put(krow, j, k0, sk, ik, ak != 0.f);
+            sm.nk[j + HALF] = put(krow, j + HALF, k1, sk, ik, ak != 0.f);
+        }
+        if (tid < nrow && tid / D == g) sm.nv[tid % D] = put(vrow, tid % D, nr.vn, sv, iv, av != 0.f);
+        if (V2 && tid + NT < nrow && (tid + NT) / D == g)
+            sm.nv[(tid + NT) % D] = put(vrow, (tid + NT) % D, nr.vn2, sv, iv, av != 0.f);
+        if constexpr (Q8) {
+            if (scale_writer && tid == 0 && pos < cap) { fz.ks_w[pos] = sk; fz.vs_w[pos] = sv; }
+        }
+    }
+
+    // ---- merge: lanes of a dim group, then the waves -------------------------------
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        // sum over the 16 lanes tg of dim group dg: rotations by 4 and 8 within a
+        // 16-lane row (DPP row_ror), then the row and half exchanges
+        float v = acc[e];
+        v += dpp_f<0x124>(v);
+        v += dpp_f<0x128>(v);
+        float2 t = swap_rows16(v, v);
+        v = t.x + t.y;
+        t = swap_halves32(v, v);
+        acc[e] = t.x + t.y;
+    }
+    if (tg == 0) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) sm.wacc[w][16 * dg + e] = acc[e];
+    }
+    if (lane == 0) { sm.wm[w] = m_run; sm.wl[w] = l_run; }
+    __syncthreads();
+    if (tid < D) {
+        // The new token (fused): score q . k_stored, weight 1, value its stored V row.
+        float sn = kNegInf;
+        if (FUSED && has_new) {
+            float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+#pragma unroll
+            for (int i = 0; i < D / 4; ++i) {
+                const float4 qv = *reinterpret_cast<const float4*>(&sm.qs[4 * i]);
+                const float4 kv = *reinterpret_cast<const float4*>(&sm.nk[4 * i]);
+                a0 += qv.x * kv.x;
+                a1 += qv.y * kv.y;
+                a2 += qv.z * kv.z;
+                a3 += qv.w * kv.w;
+            }
+            sn = ((a0 + a1) + (a2 + a3)) * scale;
+        }
+        float mt = sn;
+#pragma unroll
+        for (int k = 0; k < NW; ++k) mt = fmaxf(mt, sm.wm[k]);
+        float lt = 0.f, ot = 0.f;
+        if (FUSED && has_new) {
+            lt = expf(sn - mt);
+            ot = lt * sm.nv[tid];
+        }
+#pragma unroll
+        for (int k = 0; k < NW; ++k) {
+            if (sm.wm[k] != kNegInf) {
+                const float c = expf(sm.wm[k] - mt);
+                lt += c * sm.wl[k];
+                ot += c * sm.wacc[k][tid];
+            }
+        }
+        out(tid, ot, mt, lt);
+    }
+}
+
+}  // namespace attn
+}  // namespace vlrf_hip

@@ -1,0 +1,260 @@
+// gemv_core.hpp - building blocks of the M = 1 dequant GEMV, shared by the
+// stand-alone kernel (qlinear.hip) and the one-launch decode step (flow.hip).
+//
+// Reference contract: compute::linear -> ops::gemm(x, W, y, 1, 0, false, true)
+// at M = 1 (include/model/compute.hpp:58-68, ops.hpp:212-252) on weights
+// decoded from GGUF Q8_0/Q4_0 blocks (tools/converter/convert_gguf.py:233-263);
+// RMSNorm (ops.hpp:488-498) and SwiGLU (ops.hpp:409-441) fused at its edges.
+//
+// The workgroup (kGemvWaves waves) stages the activation vector (times the
+// norm weight when RMSNorm is fused; 1/rms multiplies the finished dots) in
+// LDS once, behind a single barrier, in a lane-interleaved layout: the i-th
+// float4 of lane l for chunk c sits at [(c*EPL/4 + i)*64 + l], so every
+// ds_read_b128 of a wave touches 64 consecutive float4 (no bank conflicts).  A
+// wave owns RPW rows (SwiGLU: RPW gate/up row pairs) at a time; lane l covers
+// EPL consecutive columns of each chunk of 64*EPL columns, so one 16-byte load
+// per lane per chunk streams a contiguous 1 KiB run of a row (Q8_0: 16 codes,
+// Q4_0: 32 nibbles).  Codes are loaded nontemporal (streamed once per step)
+// and decoded with v_cvt_f32_ubyte*: Q8_0 codes are biased by 128 (xor 0x80),
+// Q4_0 nibbles are used as stored, and the bias is removed once per chunk with
+// the lane's sum of x (sum (q+b)x - b*sum x = sum qx).
+#pragma once
+
+#include "../internal.hpp"
+
+#include <cmath>
+
+namespace vlrf_hip {
+namespace gemv {
+
+template <int WT>
+struct Gemv;
+template <>
+struct Gemv<VLRF_DT_Q8_0> { static constexpr int EPL = 16; static constexpr float BIAS = 128.f; };
+template <>
+struct Gemv<VLRF_DT_Q4_0> { static constexpr int EPL = 32; static constexpr float BIAS = 8.f; };
+
+constexpr float kNegInfF = -INFINITY;
+constexpr int kGemvMaxK = 6144;          // staged activations: 24 KiB of LDS
+constexpr int kGemvMaxGroups = 512;      // workgroups of the row loop (2 per CU)
+constexpr int kGemvMaxOneGroups = 768;   // one row per wave up to 3 workgroups per CU
+constexpr int kGemvWaves = 8;            // waves per workgroup (one staged copy of x)
+constexpr int kGemvThreads = 64 * kGemvWaves;
+
+__device__ __forceinline__ float ub(uint32_t v, int k) { return (float)((v >> (8 * k)) & 0xFFu); }
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+// Global-memory views: a pointer read from a table in memory is otherwise a
+// flat pointer, and flat loads also count against the LDS counter.
+typedef const __attribute__((address_space(1))) u32x4 gu32x4;
+typedef const __attribute__((address_space(1))) uint16_t gu16;
+
+// Activation chunks (NC) of a K-wide row, the float4 slots they stage and the
+// float4 each thread stages.
+template <int WT, int NC>
+struct Shape {
+    static constexpr int EPL = Gemv<WT>::EPL;
+    static constexpr int CW = 64 * EPL;
+    static constexpr int XF4 = NC * CW / 4;
+    static constexpr int PER = (XF4 + kGemvThreads - 1) / kGemvThreads;
+};
+
+template <int NM, int RPW, int NC>
+struct GemvRegs {
+    uint4 w[NM][RPW][NC];
+    uint32_t s[NM][RPW][NC];      // raw f16 scale bits, converted at use
+};
+
+// Branch-free loads: a lane whose (row, chunk) lies outside the matrix reads
+// the first 16 bytes and the first scale of the matrix instead (always in
+// bounds) and gemv_compute gives it a zero scale.  A load inside a bounds
+// branch would be followed by a wait for its result at the end of the branch,
+// and since loads return in issue order that wait would serialise the stream.
+template <int WT, int NM, int RPW, int NC>
+__device__ __forceinline__ void gemv_load(GemvRegs<NM, RPW, NC>& R, const uint8_t* __restrict__ qa,
+                                          const __half* __restrict__ da, const uint8_t* __restrict__ qb,
+                                          const __half* __restrict__ db, int row0, int N, int K,
+                                          int lane) {
+    constexpr int EPL = Gemv<WT>::EPL;
+    constexpr int CW = 64 * EPL;
+    const size_t qrow = WT == VLRF_DT_Q8_0 ? (size_t)K : (size_t)K / 2;
+    const int kb = K / 32;
+#pragma unroll
+    for (int m = 0; m < NM; ++m) {
+        const uint8_t* q = m ? qb : qa;
+        const uint16_t* d = reinterpret_cast<const uint16_t*>(m ? db : da);
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) {
+            const int row = row0 + r;
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                const int e0 = c * CW + lane * EPL;
+                const bool in = row < N && e0 < K;
+                const size_t qo = in ? (size_t)row * qrow + (size_t)c * 1024 + lane * 16 : 0;
+                const size_t so = in ? (size_t)row * kb + e0 / 32 : 0;
+                // Streamed once per step: nontemporal, so the codes do not
+                // displace the activations and scales from the caches.
+                const u32x4 t = __builtin_nontemporal_load((gu32x4*)(q + qo));
+                R.w[m][r][c] = make_uint4(t.x, t.y, t.z, t.w);
+                R.s[m][r][c] = ((gu16*)d)[so];
+            }
+        }
+    }
+}
+
+// The rows' dot products with the staged x; out(row, value) is called by every
+// lane of the wave with the finished value of each of its RPW rows (silu(g)*u
+// for SwiGLU), 1/rms applied.
+template <int WT, int NM, int RPW, int NC, bool SWIGLU, class Out>
+__device__ __forceinline__ void gemv_compute(const GemvRegs<NM, RPW, NC>& R, const float4* xs4,
+                                             const float (&xsum)[NC], float inv, int row0, int N, int K,
+                                             int lane, Out&& out) {
+    constexpr int EPL = Gemv<WT>::EPL;
+    float acc[NM][RPW];
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) acc[m][r] = 0.f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        float xv[EPL];
+#pragma unroll
+        for (int i = 0; i < EPL / 4; ++i) {
+            const float4 v = xs4[(c * (EPL / 4) + i) * 64 + lane];
+            xv[4 * i] = v.x; xv[4 * i + 1] = v.y; xv[4 * i + 2] = v.z; xv[4 * i + 3] = v.w;
+        }
+#pragma unroll
+        for (int m = 0; m < NM; ++m)
+#pragma unroll
+            for (int r = 0; r < RPW; ++r) {
+                const uint32_t u[4] = {R.w[m][r][c].x, R.w[m][r][c].y, R.w[m][r][c].z, R.w[m][r][c].w};
+                float p = 0.f;
+                if constexpr (WT == VLRF_DT_Q8_0) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const uint32_t b = u[j] ^ 0x80808080u;
+#pragma unroll
+                        for (int k = 0; k < 4; ++k) p += ub(b, k) * xv[4 * j + k];
+                    }
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const uint32_t lo = u[j] & 0x0F0F0F0Fu, hi = (u[j] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+                        for (int k = 0; k < 4; ++k) {
+                            // byte 4j+k holds elements 2(4j+k) (low) and 2(4j+k)+1 (high)
+                            p += ub(lo, k) * xv[8 * j + 2 * k];
+                            p += ub(hi, k) * xv[8 * j + 2 * k + 1];
+                        }
+                    }
+                }
+                const bool in = row0 + r < N && c * (64 * EPL) + lane * EPL < K;
+                const float sc = in ? __half2float(__ushort_as_half((unsigned short)R.s[m][r][c])) : 0.f;
+                acc[m][r] = fmaf(sc, p - xsum[c], acc[m][r]);
+            }
+    }
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+        float o = wave_sum(acc[0][r]) * inv;
+        if constexpr (SWIGLU) {
+            const float u = wave_sum(acc[1][r]) * inv;
+            o = u * (o / (1.f + expf(-o)));   // silu(g) * u, ops.hpp:409-441
+        }
+        out(row0 + r, o);
+    }
+}
+
+// Decode attention output in its chunked form (head dim 64) merged into the
+// thread's x slots: slot p holds elements 4f..4f+3 (f = tid + p*threads) of
+// head 4f/64, merged from its nparts chunk partials (pa(p, c): the chunk's
+// unnormalised acc for the slot, pml(p, c): its (m, l)) with the log-sum-exp
+// rule of the reference's online softmax (attention.hpp:207-309).  NP bounds
+// nparts at compile time.
+template <int PER, int NP, class PA, class PML>
+__device__ __forceinline__ void gemv_merge(PA&& pa, PML&& pml, int nparts, int XF4, int K, int tid,
+                                           float4 (&v)[PER]) {
+#pragma unroll
+    for (int p = 0; p < PER; ++p) {
+        const int f = tid + p * kGemvThreads;
+        const bool in = f < XF4 && 4 * f < K;
+        float mt = kNegInfF;
+#pragma unroll
+        for (int c = 0; c < NP; ++c)
+            if (c < nparts) mt = fmaxf(mt, pml(p, c).x);
+        float lt = 0.f;
+        float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int c = 0; c < NP; ++c) {
+            if (c < nparts) {
+                const float2 ml = pml(p, c);
+                if (ml.x != kNegInfF) {
+                    const float4 a = pa(p, c);
+                    const float wgt = expf(ml.x - mt);
+                    lt += wgt * ml.y;
+                    o.x += wgt * a.x;
+                    o.y += wgt * a.y;
+                    o.z += wgt * a.z;
+                    o.w += wgt * a.w;
+                }
+            }
+        }
+        const float il = lt > 0.f ? 1.f / lt : 0.f;
+        v[p] = in ? make_float4(o.x * il, o.y * il, o.z * il, o.w * il) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+}
+
+// Stages the thread's x slots v (times the norm weight gw when NORM) in the
+// lane-interleaved layout with one barrier: RMSNorm (ops.hpp:488-498) is per
+// row, so W.((x*inv)*w) = inv * W.(x*w) and 1/rms (inv) is applied to the
+// dots.  xsum[c] = BIAS times the lane's sum of staged x in chunk c.
+template <int WT, int NC, bool NORM>
+__device__ __forceinline__ void gemv_stage(const float4 (&v)[Shape<WT, NC>::PER], const float4 (&gw)[Shape<WT, NC>::PER],
+                                           float4* xs4, float* red, int K, float eps, float& inv,
+                                           float (&xsum)[NC]) {
+    constexpr int EPL = Gemv<WT>::EPL, CW = Shape<WT, NC>::CW;
+    constexpr int XF4 = Shape<WT, NC>::XF4, PER = Shape<WT, NC>::PER;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float ss = 0.f;
+#pragma unroll
+    for (int p = 0; p < PER; ++p)
+        ss += v[p].x * v[p].x + v[p].y * v[p].y + v[p].z * v[p].z + v[p].w * v[p].w;
+    if constexpr (NORM) {
+        ss = wave_sum(ss);
+        if (lane == 0) red[wave] = ss;
+    }
+#pragma unroll
+    for (int p = 0; p < PER; ++p) {
+        const int f = tid + p * kGemvThreads;
+        if (f < XF4) {
+            float4 o = v[p];
+            if (NORM && 4 * f < K) {
+                const float4 g = gw[p];
+                o.x = o.x * g.x; o.y = o.y * g.y;
+                o.z = o.z * g.z; o.w = o.w * g.w;
+            }
+            const int e = 4 * f, c = e / CW, r = e - c * CW, l = r / EPL, i = (r - l * EPL) / 4;
+            xs4[(c * (EPL / 4) + i) * 64 + l] = o;
+        }
+    }
+    __syncthreads();
+    inv = 1.f;
+    if constexpr (NORM) {
+        ss = 0.f;
+#pragma unroll
+        for (int w = 0; w < kGemvWaves; ++w) ss += red[w];
+        inv = 1.f / sqrtf(ss / (float)K + eps);
+    }
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        float sacc = 0.f;
+#pragma unroll
+        for (int i = 0; i < EPL / 4; ++i) {
+            const float4 o = xs4[(c * (EPL / 4) + i) * 64 + lane];
+            sacc += (o.x + o.y) + (o.z + o.w);
+        }
+        xsum[c] = sacc * Gemv<WT>::BIAS;
+    }
+}
+
+}  // namespace gemv
+}  // namespace vlrf_hip

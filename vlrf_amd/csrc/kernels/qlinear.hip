@@ -14,6 +14,7 @@
 // per-lane partial dot over the lane's EPL elements, then one FMA with the
 // block scale.  The K reduction across lanes is a DPP/shuffle wave sum.
 #include "../internal.hpp"
+#include "gemv_core.hpp"
 
 namespace vlrf_hip {
 namespace {
@@ -172,146 +173,18 @@ int dispatch_m(hipStream_t s, const DevWeight& a, const DevWeight* b, const floa
     return VLRF_HIP_OK;
 }
 
-// ---- M = 1 decode GEMV ---------------------------------------------------------
-// The workgroup stages the activation vector (times the norm weight when
-// RMSNorm is fused; 1/rms multiplies the finished dots) in LDS once, behind a
-// single barrier, in a lane-interleaved layout: the i-th float4 of lane l for chunk c sits at
-// [(c*EPL/4 + i)*64 + l], so every ds_read_b128 of a wave touches 64
-// consecutive float4 (no bank conflicts).  A wave owns RPW rows (SwiGLU: RPW
-// gate/up row pairs) at a time; lane l covers EPL consecutive columns of each
-// chunk of 64*EPL columns, so one 16-byte load per lane per chunk streams a
-// contiguous 1 KiB run of a row (Q8_0: 16 codes, Q4_0: 32 nibbles).  Waves
-// walk their rows with a two-deep register pipeline: the next rows' weights
-// are in flight while the current ones are reduced, and the first rows' loads
-// are issued before the activations are staged -- after a barrier that puts
-// every wave's activation loads ahead of them, since a CU's vector memory
-// requests are served in order.  Codes are loaded nontemporal (streamed once
-// per step).  Codes are decoded with
-// v_cvt_f32_ubyte*: Q8_0 codes are biased by 128 (xor 0x80), Q4_0 nibbles are
-// used as stored, and the bias is removed once per chunk with the lane's sum
-// of x (sum (q+b)x - b*sum x = sum qx).
-template <int WT>
-struct Gemv;
-template <>
-struct Gemv<VLRF_DT_Q8_0> { static constexpr int EPL = 16; static constexpr float BIAS = 128.f; };
-template <>
-struct Gemv<VLRF_DT_Q4_0> { static constexpr int EPL = 32; static constexpr float BIAS = 8.f; };
-
-constexpr float kNegInfF = -INFINITY;
-constexpr int kGemvMaxK = 6144;          // staged activations: 24 KiB of LDS
-constexpr int kGemvMaxGroups = 512;      // workgroups of the row loop (2 per CU)
-constexpr int kGemvMaxOneGroups = 768;   // one row per wave up to 3 workgroups per CU
-constexpr int kGemvWaves = 8;            // waves per workgroup (one staged copy of x)
-
-__device__ __forceinline__ float ub(uint32_t v, int k) { return (float)((v >> (8 * k)) & 0xFFu); }
-
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-
-template <int NM, int RPW, int NC>
-struct GemvRegs {
-    uint4 w[NM][RPW][NC];
-    uint32_t s[NM][RPW][NC];      // raw f16 scale bits, converted at use
-};
-
-// Branch-free loads: a lane whose (row, chunk) lies outside the matrix reads
-// the first 16 bytes and the first scale of the matrix instead (always in
-// bounds) and gemv_compute gives it a zero scale.  A load inside a bounds
-// branch would be followed by a wait for its result at the end of the branch,
-// and since loads return in issue order that wait would serialise the stream.
-template <int WT, int NM, int RPW, int NC>
-__device__ __forceinline__ void gemv_load(GemvRegs<NM, RPW, NC>& R, const uint8_t* __restrict__ qa,
-                                          const __half* __restrict__ da, const uint8_t* __restrict__ qb,
-                                          const __half* __restrict__ db, int row0, int N, int K,
-                                          int lane) {
-    constexpr int EPL = Gemv<WT>::EPL;
-    constexpr int CW = 64 * EPL;
-    const size_t qrow = WT == VLRF_DT_Q8_0 ? (size_t)K : (size_t)K / 2;
-    const int kb = K / 32;
-#pragma unroll
-    for (int m = 0; m < NM; ++m) {
-        const uint8_t* q = m ? qb : qa;
-        const uint16_t* d = reinterpret_cast<const uint16_t*>(m ? db : da);
-#pragma unroll
-        for (int r = 0; r < RPW; ++r) {
-            const int row = row0 + r;
-#pragma unroll
-            for (int c = 0; c < NC; ++c) {
-                const int e0 = c * CW + lane * EPL;
-                const bool in = row < N && e0 < K;
-                const size_t qo = in ? (size_t)row * qrow + (size_t)c * 1024 + lane * 16 : 0;
-                const size_t so = in ? (size_t)row * kb + e0 / 32 : 0;
-                // Streamed once per step: nontemporal, so the codes do not
-                // displace the activations and scales from the caches.
-                const u32x4 t = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(q + qo));
-                R.w[m][r][c] = make_uint4(t.x, t.y, t.z, t.w);
-                R.s[m][r][c] = d[so];
-            }
-        }
-    }
-}
-
-template <int WT, int NM, int RPW, int NC, bool SWIGLU, bool RES>
-__device__ __forceinline__ void gemv_compute(const GemvRegs<NM, RPW, NC>& R, const float4* xs4,
-                                             const float (&xsum)[NC], float inv, int row0, int N, int K,
-                                             int lane, const float* residual, float* y) {
-    constexpr int EPL = Gemv<WT>::EPL;
-    float acc[NM][RPW];
-#pragma unroll
-    for (int m = 0; m < NM; ++m)
-#pragma unroll
-        for (int r = 0; r < RPW; ++r) acc[m][r] = 0.f;
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-        float xv[EPL];
-#pragma unroll
-        for (int i = 0; i < EPL / 4; ++i) {
-            const float4 v = xs4[(c * (EPL / 4) + i) * 64 + lane];
-            xv[4 * i] = v.x; xv[4 * i + 1] = v.y; xv[4 * i + 2] = v.z; xv[4 * i + 3] = v.w;
-        }
-#pragma unroll
-        for (int m = 0; m < NM; ++m)
-#pragma unroll
-            for (int r = 0; r < RPW; ++r) {
-                const uint32_t u[4] = {R.w[m][r][c].x, R.w[m][r][c].y, R.w[m][r][c].z, R.w[m][r][c].w};
-                float p = 0.f;
-                if constexpr (WT == VLRF_DT_Q8_0) {
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const uint32_t b = u[j] ^ 0x80808080u;
-#pragma unroll
-                        for (int k = 0; k < 4; ++k) p += ub(b, k) * xv[4 * j + k];
-                    }
-                } else {
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const uint32_t lo = u[j] & 0x0F0F0F0Fu, hi = (u[j] >> 4) & 0x0F0F0F0Fu;
-#pragma unroll
-                        for (int k = 0; k < 4; ++k) {
-                            // byte 4j+k holds elements 2(4j+k) (low) and 2(4j+k)+1 (high)
-                            p += ub(lo, k) * xv[8 * j + 2 * k];
-                            p += ub(hi, k) * xv[8 * j + 2 * k + 1];
-                        }
-                    }
-                }
-                const bool in = row0 + r < N && c * (64 * EPL) + lane * EPL < K;
-                const float sc = in ? __half2float(__ushort_as_half((unsigned short)R.s[m][r][c])) : 0.f;
-                acc[m][r] = fmaf(sc, p - xsum[c], acc[m][r]);
-            }
-    }
-#pragma unroll
-    for (int r = 0; r < RPW; ++r) {
-        const int row = row0 + r;
-        float out = wave_sum(acc[0][r]) * inv;
-        if constexpr (SWIGLU) {
-            const float u = wave_sum(acc[1][r]) * inv;
-            out = u * (out / (1.f + expf(-out)));   // silu(g) * u, ops.hpp:409-441
-        }
-        if (lane == 0 && row < N) {
-            if constexpr (RES) out = out + residual[row];
-            y[row] = out;
-        }
-    }
-}
+// ---- M = 1 decode GEMV (building blocks in gemv_core.hpp) ------------------------
+// Waves walk their rows with a two-deep register pipeline: the next rows'
+// weights are in flight while the current ones are reduced, and the first
+// rows' loads are issued before the activations are staged -- after a barrier
+// that puts every wave's activation loads ahead of them, since a CU's vector
+// memory requests are served in order.
+using gemv::Gemv;
+using gemv::GemvRegs;
+using gemv::kGemvMaxGroups;
+using gemv::kGemvMaxK;
+using gemv::kGemvMaxOneGroups;
+using gemv::kGemvWaves;
 
 // XM: bit 0 = RMSNorm fused (norm_w), bit 1 = x is row *x_row of a table (with
 // the raw row copied to x_copy), bit 2 = residual added.  Compile-time: the
@@ -323,10 +196,9 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(
     const __half* __restrict__ db, int N, int K, const float* __restrict__ x,
     const int* __restrict__ x_row, float* x_copy, const float* __restrict__ norm_w, float eps,
     const float* residual, float* y, int nparts) {
-    constexpr int EPL = Gemv<WT>::EPL;
-    constexpr int CW = 64 * EPL;
+    using S = gemv::Shape<WT, NC>;
     constexpr int NM = SWIGLU ? 2 : 1;
-    constexpr int NT = 64 * kGemvWaves;
+    constexpr int NT = gemv::kGemvThreads;
     constexpr bool RES = XM & 4;
     // XM & 8: x is decode attention output in its chunked form (head dim 64):
     // element e is dim e % 64 of head e / 64, merged here from the nparts
@@ -335,8 +207,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(
     // XM & 16: every wave has at most one row (N <= the grid's row step), so
     // the second register set of the pipeline is neither loaded nor held.
     constexpr bool ONE = XM & 16;
-    constexpr int XF4 = NC * CW / 4;                  // staged float4 slots
-    constexpr int PER = (XF4 + NT - 1) / NT;          // float4 per thread
+    constexpr int XF4 = S::XF4, PER = S::PER;
     constexpr int NP = MERGE ? kAttnMaxChunks / PER : 1;   // chunks a merge holds in registers
     __shared__ float4 xs4[XF4];
     __shared__ float red[kGemvWaves];
@@ -393,97 +264,42 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(
         // Every wave's activation requests enter the CU's memory pipeline
         // before any weight request, so x is not queued behind the stream.
         __builtin_amdgcn_s_barrier();
-        gemv_load<WT, NM, RPW, NC>(A, qa, da, qb, db, row0, N, K, lane);
-        if constexpr (!ONE) gemv_load<WT, NM, RPW, NC>(B, qa, da, qb, db, row0 + rstep, N, K, lane);
+        gemv::gemv_load<WT, NM, RPW, NC>(A, qa, da, qb, db, row0, N, K, lane);
+        if constexpr (!ONE) gemv::gemv_load<WT, NM, RPW, NC>(B, qa, da, qb, db, row0 + rstep, N, K, lane);
 
-        if constexpr (MERGE) {
+        if constexpr (MERGE)
+            gemv::gemv_merge<PER, NP>([&](int p, int c) { return pa[p][c]; }, [&](int p, int c) { return pml[p][c]; },
+                                      nparts, XF4, K, tid, v);
+        if (GATHER && x_copy && blockIdx.x == 0) {
 #pragma unroll
             for (int p = 0; p < PER; ++p) {
                 const int f = tid + p * NT;
-                const bool in = f < XF4 && 4 * f < K;
-                const float2* mh = pml[p];
-                float mt = kNegInfF;
-#pragma unroll
-                for (int c = 0; c < NP; ++c)
-                    if (c < nparts) mt = fmaxf(mt, mh[c].x);
-                float lt = 0.f;
-                float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-                for (int c = 0; c < NP; ++c) {
-                    if (c < nparts && mh[c].x != kNegInfF) {
-                        const float wgt = expf(mh[c].x - mt);
-                        lt += wgt * mh[c].y;
-                        o.x += wgt * pa[p][c].x;
-                        o.y += wgt * pa[p][c].y;
-                        o.z += wgt * pa[p][c].z;
-                        o.w += wgt * pa[p][c].w;
-                    }
-                }
-                const float il = lt > 0.f ? 1.f / lt : 0.f;
-                v[p] = in ? make_float4(o.x * il, o.y * il, o.z * il, o.w * il) : make_float4(0.f, 0.f, 0.f, 0.f);
+                if (f < XF4 && 4 * f < K) reinterpret_cast<float4*>(x_copy)[f] = v[p];
             }
         }
-        // Stage x (times the norm weight when fused) in the lane-interleaved
-        // layout, with one barrier: RMSNorm (ops.hpp:488-498) is per row, so
-        // W.((x*inv)*w) = inv * W.(x*w) and 1/rms is applied to the dots.
-        float ss = 0.f;
-#pragma unroll
-        for (int p = 0; p < PER; ++p) {
-            const int f = tid + p * NT;
-            ss += v[p].x * v[p].x + v[p].y * v[p].y + v[p].z * v[p].z + v[p].w * v[p].w;
-            if (GATHER && x_copy && blockIdx.x == 0 && f < XF4 && 4 * f < K) reinterpret_cast<float4*>(x_copy)[f] = v[p];
-        }
-        if constexpr (NORM) {
-            ss = wave_sum(ss);
-            if (lane == 0) red[wave] = ss;
-        }
-#pragma unroll
-        for (int p = 0; p < PER; ++p) {
-            const int f = tid + p * NT;
-            if (f < XF4) {
-                float4 o = v[p];
-                if (NORM && 4 * f < K) {
-                    const float4 g = gw[p];
-                    o.x = o.x * g.x; o.y = o.y * g.y;
-                    o.z = o.z * g.z; o.w = o.w * g.w;
-                }
-                const int e = 4 * f, c = e / CW, r = e - c * CW, l = r / EPL, i = (r - l * EPL) / 4;
-                xs4[(c * (EPL / 4) + i) * 64 + l] = o;
-            }
-        }
-        __syncthreads();
-        if constexpr (NORM) {
-            ss = 0.f;
-#pragma unroll
-            for (int w = 0; w < kGemvWaves; ++w) ss += red[w];
-            inv = 1.f / sqrtf(ss / (float)K + eps);
-        }
-#pragma unroll
-        for (int c = 0; c < NC; ++c) {
-            float sacc = 0.f;
-#pragma unroll
-            for (int i = 0; i < EPL / 4; ++i) {
-                const float4 o = xs4[(c * (EPL / 4) + i) * 64 + lane];
-                sacc += (o.x + o.y) + (o.z + o.w);
-            }
-            xsum[c] = sacc * Gemv<WT>::BIAS;
-        }
+        gemv::gemv_stage<WT, NC, NORM>(v, gw, xs4, red, K, eps, inv, xsum);
     }
 
+    auto store = [&](int row, float out) {
+        if (lane == 0 && row < N) {
+            if constexpr (RES) out = out + residual[row];
+            y[row] = out;
+        }
+    };
     if constexpr (ONE) {
-        if (row0 < N) gemv_compute<WT, NM, RPW, NC, SWIGLU, RES>(A, xs4, xsum, inv, row0, N, K, lane, residual, y);
+        if (row0 < N) gemv::gemv_compute<WT, NM, RPW, NC, SWIGLU>(A, xs4, xsum, inv, row0, N, K, lane, store);
         return;
     }
     // Loads stay unconditional inside the loop as well (see gemv_load).
     for (; row0 < N; row0 += 2 * rstep) {
         const int r1 = row0 + rstep;
-        gemv_compute<WT, NM, RPW, NC, SWIGLU, RES>(A, xs4, xsum, inv, row0, N, K, lane, residual, y);
+        gemv::gemv_compute<WT, NM, RPW, NC, SWIGLU>(A, xs4, xsum, inv, row0, N, K, lane, store);
         if (r1 >= N) break;
         const int r2 = r1 + rstep;
-        gemv_load<WT, NM, RPW, NC>(A, qa, da, qb, db, r2, N, K, lane);
-        gemv_compute<WT, NM, RPW, NC, SWIGLU, RES>(B, xs4, xsum, inv, r1, N, K, lane, residual, y);
+        gemv::gemv_load<WT, NM, RPW, NC>(A, qa, da, qb, db, r2, N, K, lane);
+        gemv::gemv_compute<WT, NM, RPW, NC, SWIGLU>(B, xs4, xsum, inv, r1, N, K, lane, store);
         if (r2 >= N) break;
-        gemv_load<WT, NM, RPW, NC>(B, qa, da, qb, db, r2 + rstep, N, K, lane);
+        gemv::gemv_load<WT, NM, RPW, NC>(B, qa, da, qb, db, r2 + rstep, N, K, lane);
     }
 }
 

@@ -22,6 +22,14 @@
 // advances the device-side position.  The token and position live in device
 // memory, so the whole step is captured once as a HIP graph and replayed with
 // no host round trip between steps.
+//
+// VLRF_HIP_FLOW=1 runs the same phases instead as ONE launch per step whose
+// workgroups wait for each other's tagged outputs (kernels/flow.hip), where
+// the shape allows.  It gives the same token streams but is slower on the
+// MI355X (1.1B shape, ctx 2048: 0.754 against 0.594 ms per step, same box): a
+// tagged exchange between workgroups costs 2.7-3 us, no less than a graph
+// kernel boundary plus its first-byte latency, so the per-kernel graph stays
+// the default.
 #include "internal.hpp"
 #include "runtime.hpp"
 
@@ -62,14 +70,21 @@ struct vlrf_hip_model {
     float *x = nullptr, *qkv = nullptr, *att = nullptr, *h = nullptr, *logits = nullptr, *part = nullptr;
     int nch = 0;               // decode attention in chunked form (merged by the O GEMV) when > 0
     float* chunks = nullptr;   // its partials [H][nch][kAttnChunkStride]
-    int* state = nullptr;      // [0] token, [1] position, [2] generated count
+    int* state = nullptr;      // [0] token, [1] position, [2] generated count, [3] epoch (>= 1)
     int* gen_ids = nullptr;    // [S]
     int* prompt = nullptr;     // [S] staged prompt ids
-    int* pinned = nullptr;     // host pinned [4]
+    int* pinned = nullptr;     // host pinned [8]
     int n_splits = 0;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     bool use_graph = true;     // VLRF_HIP_GRAPH=0: queue the step's kernels directly
+    // One-launch step (kernels/flow.hip), planned once every weight is set.
+    bool flow_allowed = false;  // VLRF_HIP_FLOW=1: the one-launch step
+    bool flow_planned = false;
+    FlowShape flow;
+    FlowParams fp;             // everything but the per-launch gate
+    uint64_t* flow_arena = nullptr;
+    int* flow_status = nullptr;         // [4] failure flag, block, phase, layer
     int pos = 0;               // host mirror of state[1]
     // Batched prefill (matrix cores) work buffers, sized for pf_cap rows.
     int pf_cap = 0;
@@ -153,18 +168,126 @@ int ensure_graph(vlrf_hip_model* m) {
     return VLRF_HIP_OK;
 }
 
-// One decode step on the context stream: the captured graph, or the same
-// kernels queued one by one when graphs are switched off.
-int launch_step(vlrf_hip_model* m) {
+void drop_flow(vlrf_hip_model* m) {
+    for (void* p : {(void*)m->flow_arena, (void*)m->flow_status})
+        if (p) (void)hipFree(p);
+    m->flow_arena = nullptr;
+    m->flow_status = nullptr;
+    m->flow = FlowShape();
+    m->flow_planned = false;
+}
+
+// Plans the one-launch step once every weight is set (the LM head's format is
+// known only then): the layer pointers (carried in the kernel arguments), the
+// tagged arena (zero: no word carries an epoch, which starts at 1) and the
+// status words.
+int ensure_flow(vlrf_hip_model* m) {
+    if (m->flow_planned || !m->flow_allowed) return VLRF_HIP_OK;
+    m->flow_planned = true;
+    const FlowShape f = flow_shape(m->cfg.weight_dtype, m->lm_head.dtype, m->cfg.kv_dtype, m->L, m->D, m->F, m->H,
+                                   m->G, m->dh, m->V, m->S);
+    if (!f.ok) return VLRF_HIP_OK;   // the per-kernel step
+    hipStream_t s = m->ctx->stream;
+    FlowParams& p = m->fp;
+    p = FlowParams();
+    for (int l = 0; l < m->L; ++l) {
+        const Layer& Ly = m->layers[l];
+        const DevWeight* ws[5] = {&Ly.wqkv, &Ly.wo, &Ly.wg, &Ly.wu, &Ly.wd};
+        for (int i = 0; i < 5; ++i) {
+            p.layers[l].q[i] = ws[i]->q;
+            p.layers[l].d[i] = ws[i]->d;
+        }
+        p.layers[l].ln1 = Ly.ln1;
+        p.layers[l].ln2 = Ly.ln2;
+        p.layers[l].kc = Ly.kv.k;
+        p.layers[l].vc = Ly.kv.v;
+        p.layers[l].ks = Ly.kv.ks;
+        p.layers[l].vs = Ly.kv.vs;
+    }
+    int rate_khz = 0;
+    VH_CHECK(hipDeviceGetAttribute(&rate_khz, hipDeviceAttributeWallClockRate, m->ctx->device));
+    if (hipMalloc((void**)&m->flow_arena, (size_t)f.a.words * 8) != hipSuccess ||
+        hipMalloc((void**)&m->flow_status, 4 * sizeof(int)) != hipSuccess) {
+        drop_flow(m);
+        set_error("model: hipMalloc of the one-launch step's buffers failed");
+        return VLRF_HIP_ERR_NOMEM;
+    }
+    VH_CHECK(hipMemsetAsync(m->flow_arena, 0, (size_t)f.a.words * 8, s));
+    VH_CHECK(hipMemsetAsync(m->flow_status, 0, 4 * sizeof(int), s));
+    VH_CHECK(hipStreamSynchronize(s));
+    p.L = m->L; p.D = m->D; p.F = m->F; p.H = m->H; p.G = m->G; p.V = m->V; p.S = m->S;
+    p.nch = f.nch;
+    p.rep = m->H / m->G;
+    p.w_dtype = m->cfg.weight_dtype;
+    p.kv_dtype = m->cfg.kv_dtype;
+    p.embed = m->embed;
+    p.lm_q = m->lm_head.q;
+    p.lm_d = m->lm_head.d;
+    p.ln_final = m->ln_final;
+    p.cos_t = m->cos_t;
+    p.sin_t = m->sin_t;
+    p.scale = 1.f / std::sqrt((float)m->dh);   // attention.hpp:373-374
+    p.eps = m->cfg.norm_eps;
+    p.state = m->state;
+    p.gen_ids = m->gen_ids;
+    p.gen_cap = m->S;
+    p.logits = m->logits;
+    p.arena = m->flow_arena;
+    p.a = f.a;
+    p.status = m->flow_status;
+    // A wait may last 0.5 s (VLRF_HIP_FLOW_WAIT_US overrides it: the tests
+    // shorten it to exercise the failure path).
+    long long wait_us = 500000;
+    if (const char* w = std::getenv("VLRF_HIP_FLOW_WAIT_US")) wait_us = std::atoll(w);
+    p.limit = (long long)rate_khz * wait_us / 1000;
+    p.plan = f.plan;
+    m->flow = f;
+    return VLRF_HIP_OK;
+}
+
+// One decode step on the context stream at host position pos: the one-launch
+// step, the captured graph, or the same kernels queued one by one when graphs
+// are switched off.
+int launch_step(vlrf_hip_model* m, int pos) {
+    if (m->flow.ok) {
+        m->fp.gate_chunk = flow_gate_chunk(m->flow, pos);
+        return launch_flow_step(m->ctx->stream, m->fp);
+    }
     if (!m->use_graph) return enqueue_step(m, m->ctx->stream);
     VH_CHECK(hipGraphLaunch(m->exec, m->ctx->stream));
     return VLRF_HIP_OK;
+}
+
+// After the queued steps have finished: a one-launch step whose wait ran out
+// left its flag; report it, clear it and move to a fresh epoch (the failed
+// step may have published words of the old one), and take the device
+// position as the host's.
+int check_flow(vlrf_hip_model* m) {
+    if (!m->flow.ok) return VLRF_HIP_OK;
+    hipStream_t s = m->ctx->stream;
+    int* st = m->pinned + 4;
+    VH_CHECK(hipMemcpyAsync(st, m->flow_status, 4 * sizeof(int), hipMemcpyDeviceToHost, s));
+    VH_CHECK(hipStreamSynchronize(s));
+    if (!st[0]) return VLRF_HIP_OK;
+    const int blk = st[1], ph = st[2], layer = st[3];
+    VH_CHECK(hipMemsetAsync(m->flow_status, 0, 4 * sizeof(int), s));
+    VH_CHECK(hipMemcpyAsync(m->pinned, m->state, 4 * sizeof(int), hipMemcpyDeviceToHost, s));
+    VH_CHECK(hipStreamSynchronize(s));
+    m->pinned[3] += 1;
+    m->pos = m->pinned[1];
+    VH_CHECK(hipMemcpyAsync(m->state, m->pinned, 4 * sizeof(int), hipMemcpyHostToDevice, s));
+    VH_CHECK(hipStreamSynchronize(s));
+    set_error("decode step: a wait for another workgroup's output ran out (workgroup %d, phase %d, layer %d)",
+              blk, ph, layer);
+    return VLRF_HIP_ERR_RUNTIME;
 }
 
 int check_ready(vlrf_hip_model* m) {
     VH_ARG(m != nullptr, "model: null handle");
     VH_CHECK(hipSetDevice(m->ctx->device));
     VH_ARG(m->ready(), "model: not every weight has been set");
+    const int rc = ensure_flow(m);
+    if (rc || m->flow.ok) return rc;
     return ensure_graph(m);
 }
 
@@ -216,6 +339,7 @@ int vlrf_hip_model_create(vlrf_hip_ctx_t ctx, const vlrf_hip_model_config* cfg, 
     m->n_splits = attn_decode_splits(m->S);
     m->layers.resize(m->L);
     if (const char* g = std::getenv("VLRF_HIP_GRAPH")) m->use_graph = std::strcmp(g, "0") != 0;
+    if (const char* g = std::getenv("VLRF_HIP_FLOW")) m->flow_allowed = std::strcmp(g, "1") == 0;
 
     int rc = VLRF_HIP_OK;
     auto dalloc = [&](void** p, size_t bytes) {
@@ -262,9 +386,17 @@ int vlrf_hip_model_create(vlrf_hip_ctx_t ctx, const vlrf_hip_model_config* cfg, 
         if (!rc) rc = weight_alloc(Ly.wu, c.weight_dtype, m->F, m->D);
         if (!rc) rc = weight_alloc(Ly.wd, c.weight_dtype, m->D, m->F);
     }
-    if (!rc && hipHostMalloc((void**)&m->pinned, 4 * sizeof(int), hipHostMallocDefault) != hipSuccess) {
+    if (!rc && hipHostMalloc((void**)&m->pinned, 8 * sizeof(int), hipHostMallocDefault) != hipSuccess) {
         set_error("model_create: hipHostMalloc failed");
         rc = VLRF_HIP_ERR_NOMEM;
+    }
+    if (!rc) {   // the one-launch step's epoch starts at 1 (its arena starts as zero words)
+        m->pinned[0] = m->pinned[1] = m->pinned[2] = 0;
+        m->pinned[3] = 1;
+        if (hipMemcpy(m->state, m->pinned, 4 * sizeof(int), hipMemcpyHostToDevice) != hipSuccess) {
+            set_error("model_create: state upload failed");
+            rc = VLRF_HIP_ERR_RUNTIME;
+        }
     }
     if (!rc) rc = ctx->rope_tables(m->S, dh, c.rope_theta, &m->cos_t, &m->sin_t);
     if (!rc) rc = vlrf_hip_model_reset(m);
@@ -298,7 +430,7 @@ void vlrf_hip_model_destroy(vlrf_hip_model_t m) {
                     (void*)m->gen_ids, (void*)m->prompt})
         if (p) (void)hipFree(p);
     for (void* p : {(void*)m->pf_x, (void*)m->pf_qkv, (void*)m->pf_a, (void*)m->pf_att, (void*)m->pf_h,
-                    (void*)m->pf_ids})
+                    (void*)m->pf_ids, (void*)m->flow_arena, (void*)m->flow_status})
         if (p) (void)hipFree(p);
     if (m->pinned) (void)hipHostFree(m->pinned);
     delete m;
@@ -339,6 +471,7 @@ int vlrf_hip_model_set_weight(vlrf_hip_model_t m, const char* name, const void* 
             if (m->graph) (void)hipGraphDestroy(m->graph);
             m->exec = nullptr;
             m->graph = nullptr;
+            drop_flow(m);   // and the one-launch step's plan (it depends on the LM head's format)
             weight_release(m->lm_head);
             if ((rc = weight_alloc(m->lm_head, dtype, m->V, m->D))) return rc;
         }
@@ -390,7 +523,7 @@ int vlrf_hip_model_reset(vlrf_hip_model_t m) {
         if (Ly.kv.ks) VH_CHECK(hipMemsetAsync(Ly.kv.ks, 0, (size_t)m->S * 4, s));
         if (Ly.kv.vs) VH_CHECK(hipMemsetAsync(Ly.kv.vs, 0, (size_t)m->S * 4, s));
     }
-    VH_CHECK(hipMemsetAsync(m->state, 0, 4 * sizeof(int), s));
+    VH_CHECK(hipMemsetAsync(m->state, 0, 3 * sizeof(int), s));   // the epoch (state[3]) runs on
     VH_CHECK(hipStreamSynchronize(s));
     m->pos = 0;
     return VLRF_HIP_OK;
@@ -415,10 +548,11 @@ int vlrf_hip_model_step(vlrf_hip_model_t m, int32_t token, int32_t* next, float*
     hipStream_t s = m->ctx->stream;
     m->pinned[0] = token;
     VH_CHECK(hipMemcpyAsync(m->state, m->pinned, sizeof(int), hipMemcpyHostToDevice, s));
-    if ((rc = launch_step(m))) return rc;
+    if ((rc = launch_step(m, m->pos))) return rc;
     VH_CHECK(hipMemcpyAsync(m->pinned, m->state, sizeof(int), hipMemcpyDeviceToHost, s));
     if (logits) VH_CHECK(hipMemcpyAsync(logits, m->logits, (size_t)m->V * 4, hipMemcpyDeviceToHost, s));
     VH_CHECK(hipStreamSynchronize(s));
+    if ((rc = check_flow(m))) return rc;
     m->pos += 1;
     if (next) *next = m->pinned[0];
     return VLRF_HIP_OK;
@@ -439,10 +573,11 @@ int vlrf_hip_model_prefill(vlrf_hip_model_t m, const int32_t* ids, int n, int32_
     VH_CHECK(hipStreamSynchronize(s));
     for (int i = 0; i < n; ++i) {
         VH_CHECK(hipMemcpyAsync(m->state, m->prompt + i, sizeof(int), hipMemcpyDeviceToDevice, s));
-        if ((rc = launch_step(m))) return rc;
+        if ((rc = launch_step(m, m->pos + i))) return rc;
     }
     VH_CHECK(hipMemcpyAsync(m->pinned, m->state, sizeof(int), hipMemcpyDeviceToHost, s));
     VH_CHECK(hipStreamSynchronize(s));
+    if ((rc = check_flow(m))) return rc;
     m->pos += n;
     if (next) *next = m->pinned[0];
     return VLRF_HIP_OK;
@@ -590,7 +725,7 @@ int vlrf_hip_model_generate_async(vlrf_hip_model_t m, int32_t first, int n_steps
     m->pinned[2] = 0;
     VH_CHECK(hipMemcpyAsync(m->state, m->pinned, 3 * sizeof(int), hipMemcpyHostToDevice, s));
     for (int i = 0; i < n_steps; ++i)
-        if ((rc = launch_step(m))) return rc;
+        if ((rc = launch_step(m, m->pos + i))) return rc;
     m->pos += n_steps;
     return VLRF_HIP_OK;
 }
@@ -601,7 +736,7 @@ int vlrf_hip_model_read_generated(vlrf_hip_model_t m, int32_t* out_ids, int n) {
     hipStream_t s = m->ctx->stream;
     VH_CHECK(hipMemcpyAsync(out_ids, m->gen_ids, (size_t)n * sizeof(int), hipMemcpyDeviceToHost, s));
     VH_CHECK(hipStreamSynchronize(s));
-    return VLRF_HIP_OK;
+    return check_flow(m);
 }
 
 int vlrf_hip_model_generate(vlrf_hip_model_t m, int32_t first, int n_steps, int32_t* out_ids) {
