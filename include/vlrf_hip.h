@@ -123,6 +123,15 @@ int vlrf_hip_kv_dequant(vlrf_hip_kv_t kv, int layer, int ctx_len, float* K_out, 
  * reshape/expand_kv_heads + sdp_heads (attention.hpp:127-176). */
 int vlrf_hip_attn_decode(vlrf_hip_kv_t kv, int layer, const float* q, float* out,
                          int n_heads, int ctx_len, float scale);
+/* vlrf_hip_attn_decode that allocates nothing: no counterpart in the
+ * reference; for callers that cannot allocate device memory (HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments, kernels and results; the split-K partials go to one fixed 2 MiB
+ * device array per GPU (resolved at vlrf_hip_init), so n_heads * splits *
+ * (d_head + 2) floats must fit in 2^19 (splits = ceil(ctx_len / 64)),
+ * otherwise VLRF_HIP_ERR_ARG.  Calls that overlap on one GPU race. */
+int vlrf_hip_attn_decode_noalloc(vlrf_hip_kv_t kv, int layer, const float* q, float* out,
+                                 int n_heads, int ctx_len, float scale);
 
 /* ============================================================================
  * Quantized linear: y[M,N] = x[M,K] . W[N,K]^T with W in a GGUF block format.

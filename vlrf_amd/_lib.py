@@ -52,6 +52,7 @@ _SIGS = {
     "vlrf_hip_kv_read": (i32, [vp, i32, i32, i32, vp, vp, vp, vp]),
     "vlrf_hip_kv_dequant": (i32, [vp, i32, i32, vp, vp]),
     "vlrf_hip_attn_decode": (i32, [vp, i32, vp, vp, i32, i32, f32]),
+    "vlrf_hip_attn_decode_noalloc": (i32, [vp, i32, vp, vp, i32, i32, f32]),
     "vlrf_hip_weight_upload": (i32, [vp, vp, i32, i32, i32, C.POINTER(vp)]),
     "vlrf_hip_weight_free": (None, [vp]),
     "vlrf_hip_weight_bytes": (sz, [vp]),

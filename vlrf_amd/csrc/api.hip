@@ -225,6 +225,16 @@ int vlrf_hip_device_count(void) {
     return n;
 }
 
+// Split-K partials of vlrf_hip_attn_decode_noalloc: one fixed array per GPU,
+// held until the process ends, so that call allocates nothing.  Host code uses
+// the device address hipGetSymbolAddress returns for the context's GPU
+// (vlrf_hip_ctx::noalloc_scratch), never the symbol itself.  Every call on one
+// GPU shares the array: calls that overlap on one GPU race.
+namespace noalloc {
+constexpr size_t kScratchFloats = size_t(1) << 19;   // 2 MiB
+static __device__ __align__(256) float scratch[kScratchFloats];
+}  // namespace noalloc
+
 int vlrf_hip_init(int device, vlrf_hip_ctx_t* out) {
     VH_ARG(out != nullptr, "init: null output handle");
     *out = nullptr;
@@ -254,6 +264,14 @@ int vlrf_hip_init(int device, vlrf_hip_ctx_t* out) {
         delete c;
         return VLRF_HIP_ERR_RUNTIME;
     }
+    void* fixed = nullptr;   // this device's copy of the fixed scratch array (device is current)
+    const hipError_t se = hipGetSymbolAddress(&fixed, HIP_SYMBOL(noalloc::scratch));
+    if (se != hipSuccess || !fixed) {
+        set_error("init: hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(se));
+        delete c;
+        return VLRF_HIP_ERR_RUNTIME;
+    }
+    c->noalloc_scratch = static_cast<float*>(fixed);
     *out = c;
     return VLRF_HIP_OK;
 }
@@ -487,6 +505,27 @@ int vlrf_hip_attn_decode(vlrf_hip_kv_t kv, int layer, const float* q, float* out
     const KVLayer& L = kv->layers[layer];
     return launch_attn_decode(kv->ctx->stream, q, L.k, L.v, L.ks, L.vs, L.dtype, (long)kv->max_seq * kv->d_head,
                               n_heads, kv->n_kv, kv->d_head, ctx_len, nullptr, splits, scale, part, out);
+}
+
+int vlrf_hip_attn_decode_noalloc(vlrf_hip_kv_t kv, int layer, const float* q, float* out, int n_heads,
+                                 int ctx_len, float scale) {
+    VH_ARG(kv != nullptr, "attn_decode_noalloc: null cache");
+    VH_CTX(kv->ctx);
+    VH_ARG(layer >= 0 && layer < kv->n_layers, "attn_decode_noalloc: layer %d out of range", layer);
+    VH_ARG(q && out, "attn_decode_noalloc: null pointer");
+    VH_ARG(ctx_len >= 1 && ctx_len <= kv->max_seq, "attn_decode_noalloc: ctx_len %d outside [1,%d]", ctx_len,
+           kv->max_seq);
+    VH_ARG(n_heads >= 1, "attn_decode_noalloc: n_heads %d", n_heads);
+    VH_ARG(kv->ctx->noalloc_scratch != nullptr, "attn_decode_noalloc: context has no fixed scratch");
+    const int splits = attn_decode_splits(ctx_len);
+    const size_t need = (size_t)n_heads * splits * (kv->d_head + 2);
+    VH_ARG(need <= noalloc::kScratchFloats,
+           "attn_decode_noalloc: %zu partial floats (n_heads %d x %d splits x %d) exceed the fixed scratch of %zu",
+           need, n_heads, splits, kv->d_head + 2, noalloc::kScratchFloats);
+    const KVLayer& L = kv->layers[layer];
+    return launch_attn_decode(kv->ctx->stream, q, L.k, L.v, L.ks, L.vs, L.dtype, (long)kv->max_seq * kv->d_head,
+                              n_heads, kv->n_kv, kv->d_head, ctx_len, nullptr, splits, scale,
+                              kv->ctx->noalloc_scratch, out);
 }
 
 // ---- quantized linear ----------------------------------------------------------

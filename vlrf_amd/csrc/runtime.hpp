@@ -21,6 +21,7 @@ struct vlrf_hip_ctx {
     std::vector<RopeTab> ropes;      // RoPE tables per (max_seq, d_head, theta)
     void* scratch_buf = nullptr;     // split-K partials of the standalone ops
     size_t scratch_bytes = 0;
+    float* noalloc_scratch = nullptr;   // this device's fixed array for vlrf_hip_attn_decode_noalloc
 
     // Device cos/sin tables built on the host as RopeCache::init does.
     int rope_tables(int max_seq, int d_head, float theta, const float** c, const float** s);
