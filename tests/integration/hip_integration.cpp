@@ -14,9 +14,12 @@
 //              softmax_inplace, gelu_inplace, add_inplace at sizes that run on
 //              the device vs CpuBackend;
 //   decode     HipDecoder::generate vs TransformerModel::generate, greedy,
-//              on a tiny Llama-style model with Q8_0 weights, for each KV
-//              cache dtype (F32, the engine's default, F16 and Q8_0): the
-//              token streams must be identical.
+//              on a tiny Llama-style model: for each KV cache dtype (F32, the
+//              engine's default, F16 and Q8_0) with Q8_0-derived weights; with
+//              Q4_0-derived and with plain f32 weights (the device dtype
+//              follows the weights, a lossy one is refused); stops at EOS, at
+//              max_seq_len, on an on_token veto, and an empty prompt.  Token
+//              ids, tokens_generated and hit_eos must be identical.
 // Without a usable device (or with --cpu) the first two run through
 // HipBackend's CPU fallback and `decode` is skipped.  Exit status 0 = all pass.
 
@@ -194,14 +197,21 @@ void check_ops(HipBackend const& be) {
     }
 }
 
-// Q8_0 round trip so the reference runs on exactly the weights the device holds.
-void q8_roundtrip(Tensor& t) {
-    std::vector<unsigned char> blocks((size_t)t.numel() / 32 * 34);
-    vlrf_quantize_q8_0(t.data_ptr(), blocks.data(), t.numel());
-    vlrf_dequantize(blocks.data(), VLRF_DT_Q8_0, t.data_ptr(), t.numel());
+// Block round trip so the reference runs on exactly what the blocks hold.
+void roundtrip(Tensor& t, int dtype) {
+    std::vector<unsigned char> blocks((size_t)t.numel() / 32 * (dtype == VLRF_DT_Q8_0 ? 34 : 18));
+    if (dtype == VLRF_DT_Q8_0)
+        vlrf_quantize_q8_0(t.data_ptr(), blocks.data(), t.numel());
+    else
+        vlrf_quantize_q4_0(t.data_ptr(), blocks.data(), t.numel());
+    vlrf_dequantize(blocks.data(), dtype, t.data_ptr(), t.numel());
 }
 
-void check_decode(HipBackend const& be, vlrf::KVCacheDType kv_dtype) {
+const char* dtype_name(int dt) { return dt == VLRF_DT_Q8_0 ? "Q8_0" : dt == VLRF_DT_Q4_0 ? "Q4_0" : "F32"; }
+
+// A tiny Llama-style model; `wdt` is the block dtype its projection weights
+// come from (VLRF_DT_F32: plain normal f32 weights that no block holds).
+vlrf::ModelConfig tiny_config(vlrf::KVCacheDType kv_dtype) {
     vlrf::ModelConfig c;
     c.vocab_size = 512;
     c.d_model = 256;
@@ -220,16 +230,17 @@ void check_decode(HipBackend const& be, vlrf::KVCacheDType kv_dtype) {
     c.kv_cache_dtype = static_cast<int>(kv_dtype);
     c.eos_token_id = -1;
     c.do_sample = false;
+    return c;
+}
 
-    vlrf::TransformerModel m;
-    m.init(c);
+void fill_weights(vlrf::TransformerModel& m, vlrf::ModelConfig const& c, int wdt) {
     uint64_t stream = 300;
-    auto put = [&](const std::string& name, std::initializer_list<int32_t> dims, float sd, bool q8,
+    auto put = [&](const std::string& name, std::initializer_list<int32_t> dims, float sd, bool proj,
                    float offset) {
         Tensor t = normal_tensor(dims, stream++, sd);
         if (offset != 0.f)
             for (int64_t i = 0; i < t.numel(); ++i) t.data_ptr()[i] += offset;
-        if (q8) q8_roundtrip(t);
+        if (proj && wdt != VLRF_DT_F32) roundtrip(t, wdt);
         m.wm.tensors[name] = t;
     };
     put("embed.weight", {c.vocab_size, c.d_model}, 1.f, false, 0.f);
@@ -249,24 +260,115 @@ void check_decode(HipBackend const& be, vlrf::KVCacheDType kv_dtype) {
         put(p + "ffn.fc2.weight", {c.d_model, c.d_ff}, 0.05f, true, 0.f);
     }
     m.bind_weights();
+}
 
-    std::vector<int32_t> p32(40);
-    vlrf_synth_tokens(77, 400, c.vocab_size, p32.data(), (int64_t)p32.size());
-    std::vector<int> prompt(p32.begin(), p32.end());
+std::vector<int> prompt_ids(int n, int vocab) {
+    std::vector<int32_t> p32(n);
+    if (n) vlrf_synth_tokens(77, 400, vocab, p32.data(), (int64_t)n);
+    return std::vector<int>(p32.begin(), p32.end());
+}
+
+void compare(const std::string& what, vlrf::TransformerModel::GenerationResult const& ref,
+             vlrf::TransformerModel::GenerationResult const& got) {
+    int first_diff = -1;
+    for (size_t i = 0; i < ref.token_ids.size() && i < got.token_ids.size(); ++i)
+        if (ref.token_ids[i] != got.token_ids[i]) { first_diff = (int)i; break; }
+    const bool ok = got.token_ids.size() == ref.token_ids.size() && first_diff < 0 &&
+                    got.tokens_generated == ref.tokens_generated && got.hit_eos == ref.hit_eos;
+    std::printf("  %s: reference %d generated (hit_eos %d), device %d (hit_eos %d)\n", what.c_str(),
+                ref.tokens_generated, (int)ref.hit_eos, got.tokens_generated, (int)got.hit_eos);
+    report(ok, "decode: HipDecoder::generate == TransformerModel::generate, " + what,
+           first_diff < 0 ? 0.0 : (double)first_diff);
+}
+
+// Greedy streams for each KV cache dtype, with weights that came from Q8_0
+// blocks (the device keeps Q8_0).
+void check_decode(HipBackend const& be, vlrf::KVCacheDType kv_dtype) {
+    const vlrf::ModelConfig c = tiny_config(kv_dtype);
+    vlrf::TransformerModel m;
+    m.init(c);
+    fill_weights(m, c, VLRF_DT_Q8_0);
+    const std::vector<int> prompt = prompt_ids(40, c.vocab_size);
     vlrf::GenerationConfig gc;
     gc.max_new_tokens = 64;
     gc.do_sample = false;
-    const std::vector<int> ref = m.generate(prompt, gc).token_ids;
+    const auto ref = m.generate(prompt, gc);
+    vlrf::HipDecoder dec(be.context(), c, m.wm);
+    report(dec.layer_dtype() == VLRF_DT_Q8_0 && dec.lm_head_dtype() == VLRF_DT_Q8_0,
+           "decode: Q8_0-derived weights kept as Q8_0 blocks", 0.0);
+    compare(std::string("64 greedy steps, KV ") + vlrf::kv_cache_dtype_name(kv_dtype), ref,
+            dec.generate(prompt, gc.max_new_tokens));
+}
 
-    vlrf::HipDecoder dec(be.context(), c, m.wm, VLRF_DT_Q8_0);
-    const std::vector<int> got = dec.generate(prompt, gc.max_new_tokens);
-    int first_diff = -1;
-    for (size_t i = 0; i < ref.size() && i < got.size(); ++i)
-        if (ref[i] != got[i]) { first_diff = (int)i; break; }
-    const bool ok = got.size() == ref.size() && first_diff < 0;
-    const std::string what = std::string("decode: HipDecoder::generate == TransformerModel::generate (64 greedy "
-                                         "steps, KV ") + vlrf::kv_cache_dtype_name(kv_dtype) + ")";
-    report(ok, what, first_diff < 0 ? 0.0 : (double)first_diff);
+// The device dtype follows the weights: Q4_0-derived weights run as Q4_0
+// blocks, plain f32 weights as f32 (a block dtype would change them, and
+// forcing one is refused).
+void check_decode_weights(HipBackend const& be, int wdt) {
+    const vlrf::ModelConfig c = tiny_config(vlrf::KVCacheDType::Q8_0);
+    vlrf::TransformerModel m;
+    m.init(c);
+    fill_weights(m, c, wdt);
+    const std::vector<int> prompt = prompt_ids(40, c.vocab_size);
+    vlrf::GenerationConfig gc;
+    gc.max_new_tokens = 48;
+    gc.do_sample = false;
+    const auto ref = m.generate(prompt, gc);
+    vlrf::HipDecoder dec(be.context(), c, m.wm);
+    report(dec.layer_dtype() == wdt && dec.lm_head_dtype() == wdt,
+           std::string("decode: ") + dtype_name(wdt) + "-derived weights uploaded as " +
+               dtype_name(dec.layer_dtype()) + " / LM head " + dtype_name(dec.lm_head_dtype()),
+           0.0);
+    compare(std::string("48 greedy steps, ") + dtype_name(wdt) + " weights", ref,
+            dec.generate(prompt, gc.max_new_tokens));
+    if (wdt == VLRF_DT_F32) {
+        bool refused = false;
+        try {
+            vlrf::HipDecoder forced(be.context(), c, m.wm, VLRF_DT_Q8_0);
+        } catch (std::runtime_error const& e) {
+            refused = std::strstr(e.what(), "not exactly representable") != nullptr;
+        }
+        report(refused, "decode: forcing Q8_0 on f32 weights is refused", 0.0);
+    }
+}
+
+// Where generation stops: at the first generated eos_token_id, at
+// max_seq_len, on an on_token veto; an empty prompt starts from bos_token_id.
+void check_decode_stops(HipBackend const& be) {
+    vlrf::ModelConfig c = tiny_config(vlrf::KVCacheDType::Q8_0);
+    const std::vector<int> prompt = prompt_ids(40, c.vocab_size);
+    vlrf::GenerationConfig gc;
+    gc.do_sample = false;
+    int eos = -1;
+    {
+        vlrf::TransformerModel m;
+        m.init(c);
+        fill_weights(m, c, VLRF_DT_Q8_0);
+        gc.max_new_tokens = 64;
+        eos = m.generate(prompt, gc).token_ids[prompt.size() + 20];
+    }
+    c.eos_token_id = eos;
+    vlrf::TransformerModel m;
+    m.init(c);
+    fill_weights(m, c, VLRF_DT_Q8_0);
+    vlrf::HipDecoder dec(be.context(), c, m.wm);
+    gc.max_new_tokens = 64;
+    compare("eos_token_id " + std::to_string(eos) + " reached", m.generate(prompt, gc),
+            dec.generate(prompt, gc.max_new_tokens));
+    gc.max_new_tokens = 500;
+    c.eos_token_id = -1;
+    vlrf::TransformerModel m2;
+    m2.init(c);
+    fill_weights(m2, c, VLRF_DT_Q8_0);
+    vlrf::HipDecoder dec2(be.context(), c, m2.wm);
+    compare("max_new_tokens 500 > max_seq_len 160 - 40", m2.generate(prompt, gc),
+            dec2.generate(prompt, gc.max_new_tokens));
+    gc.max_new_tokens = 30;
+    compare("empty prompt (from bos_token_id)", m2.generate(std::vector<int>{}, gc), dec2.generate(std::vector<int>{}, gc.max_new_tokens));
+    int seen = 0;
+    gc.on_token = [&](int) { return ++seen < 7; };
+    const auto ref = m2.generate(prompt, gc);
+    seen = 0;
+    compare("on_token stops after 7", ref, dec2.generate(prompt, gc.max_new_tokens, gc.on_token));
 }
 
 }  // namespace
@@ -280,10 +382,12 @@ int main(int argc, char** argv) {
     check_attention(be);
     check_gemm(be);
     check_ops(be);
-    if (dev)
+    if (dev) {
         for (auto dt : {vlrf::KVCacheDType::F32, vlrf::KVCacheDType::F16, vlrf::KVCacheDType::Q8_0})
             check_decode(be, dt);
-    else
+        for (int wdt : {VLRF_DT_Q4_0, VLRF_DT_F32}) check_decode_weights(be, wdt);
+        check_decode_stops(be);
+    } else
         std::printf("SKIP decode (no HIP device)\n");
     std::printf("%s: %d failure(s)\n", g_fail ? "FAILED" : "OK", g_fail);
     return g_fail ? 1 : 0;

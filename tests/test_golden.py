@@ -65,18 +65,14 @@ def test_gpu_tiny_stream_matches_reference(ctx):
     assert _gpu_stream(ctx, fx) == fx["generated_ids"]
 
 
-# A greedy choice whose top-2 logit gap in the reference is below this may
-# legitimately flip under a different float summation order (the GPU's logits
-# agree with the oracle's to ~1e-4 absolute at this shape).
-NEAR_TIE = 2e-3
-
-
 @pytest.mark.gpu
 def test_gpu_llama1b_128_step_stream_matches_reference(ctx):
     """The 1.1B shape with Q8_0 weights and KV cache, a 2048-token prompt and
-    128 greedy steps, against the reference's own stream.  Free-running, the
-    stream must match up to the first near-tie; teacher-forced with the
-    reference's ids, every step's argmax must match except at near-ties."""
+    128 greedy steps, against the reference's own stream: identical token for
+    token, free-running (the fixture's closest call, step 38, has a reference
+    top-2 logit gap of 1.4e-3; the GPU logits agree with the oracle's to
+    ~1e-4 there).  Teacher-forced with the reference's ids, every step's
+    argmax must match as well, so a divergence would name its step."""
     fx = load("llama1b_q8_stream.json")
     ref, margins = fx["generated_ids"], fx["top2_margins"]
     print("[case] llama1b q8 2048+128 golden stream", flush=True)
@@ -86,15 +82,15 @@ def test_gpu_llama1b_128_step_stream_matches_reference(ctx):
     prompt = prompt_of(fx)
     got = list(m.generate(prompt, len(ref)))
     i = _first_divergence(got, ref)
-    if i is not None and margins[i] >= NEAR_TIE:
-        pytest.fail(f"stream diverges at step {i}: gpu {got[i]} vs reference {ref[i]} "
-                    f"(reference top-2 margin there {margins[i]:.3g})")
+    print(f"  free-running: first divergence {i}", flush=True)
     m.reset()
     m.prefill(prompt)
     feed, bad = int(prompt[-1]), []
     for j, want in enumerate(ref):
         nxt = m.step(feed)
-        if nxt != want and margins[j] >= NEAR_TIE:
+        if nxt != want:
             bad.append((j, nxt, want, margins[j]))
         feed = want
+    assert i is None, (f"stream diverges at step {i}: gpu {got[i]} vs reference {ref[i]} "
+                       f"(reference top-2 margin there {margins[i]:.3g})")
     assert not bad, f"teacher-forced argmax mismatches (step, gpu, ref, margin): {bad[:8]}"

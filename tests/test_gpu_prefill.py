@@ -184,3 +184,23 @@ def test_config5_full_size_t2048(ctx):
     second = run(x[1024:])
     assert m.used == T
     assert np.array_equal(np.concatenate([first, second]), full)
+
+
+def test_config5_attention_t2048_vs_oracle(ctx):
+    """Config 5's attention at its full length against the oracle: d_head 128,
+    GQA 4 (8 query heads over 2 KV heads, a sample of the 32/8 layout; the
+    kernel instance is the same), T = 2048 in one pass.  The last 64 rows
+    attend keys up to 2047, so keys 256-2047 are pinned.  The layer's update
+    (output - input) carries attention through W_o plus the FFN; the FFN is
+    narrow so the oracle finishes in seconds, and the comparison is of the
+    update alone, not of the residual stream that would dilute it."""
+    cfg = dict(F.llama8b_layer(V.DT_Q8_0, max_seq_len=2048), d_model=1024, n_heads=8, n_kv_heads=2, d_ff=256)
+    print("[case] config5 attention d_head 128 GQA 4 T=2048 vs oracle (last 64 rows)", flush=True)
+    m, om = _pair(ctx, cfg, 51, norm_std=0.0)
+    T, D = 2048, cfg["d_model"]
+    x = F.normal(51, "cfg5.att", T * D).reshape(T, D)
+    got = m.forward_hidden(ctx.to_device(x)).download((T, D))
+    ref = om.forward_hidden(x)
+    tail = slice(T - 64, T)
+    check(got[tail] - x[tail], ref[tail] - x[tail], "layer update, rows 1984-2047")
+    check(got[:64] - x[:64], ref[:64] - x[:64], "layer update, rows 0-63")

@@ -94,6 +94,20 @@ def test_nfw_rejects_bad_files(tmp_path):
         "v2_blocks": raw[:4] + struct.pack("<I", 2) + raw[8:],
         "odd_cols": raw.replace(struct.pack("<ii", 2, 32), struct.pack("<ii", 4, 16)),
     }
+    # Headers whose size products overflow int64 or ask for more than the
+    # file holds: refused as bad files, never a wrapped size or an
+    # allocation that escapes the C ABI.
+    def one(dims, numel, dtype=0, payload=b""):
+        name = b"w"
+        body = struct.pack("<H", len(name)) + name + struct.pack("<B", len(dims))
+        body += struct.pack(f"<{len(dims)}i", *dims) + struct.pack("<qB", numel, dtype)
+        return raw[:8] + struct.pack("<I", 1) + raw[12:16] + body + payload
+    cases.update({
+        "wrapping_f32": one((1 << 30, 1 << 30, 4), 1 << 62),            # numel * 4 wraps to 0
+        "negative_dim": one((-4, -8), 32, payload=bytes(128)),
+        "dims_overflow": one((2**31 - 1,) * 3, 0),
+        "numel_beyond_file": one((1 << 20,), 1 << 20, payload=bytes(64)),
+    })
     for name, data in cases.items():
         p = tmp_path / f"{name}.nfw"
         p.write_bytes(data)

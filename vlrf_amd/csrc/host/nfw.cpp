@@ -21,6 +21,8 @@
 #include <cstdio>
 #include <cstring>
 #include <memory>
+#include <new>
+#include <stdexcept>
 #include <string>
 #include <vector>
 
@@ -92,11 +94,25 @@ bool ends_with(const std::string& s, const char* suf) {
     return s.size() >= n && s.compare(s.size() - n, n, suf) == 0;
 }
 
+// Allocation failures (a header that asks for more than the host holds) are
+// returned as VLRF_HIP_ERR_NOMEM instead of escaping the C ABI.
+template <class Fn>
+int guarded(const char* what, Fn&& fn) {
+    try {
+        return fn();
+    } catch (std::bad_alloc const&) {
+        vlrf_hip::set_error("%s: host allocation failed", what);
+    } catch (std::length_error const&) {
+        vlrf_hip::set_error("%s: host allocation failed (size out of range)", what);
+    }
+    return VLRF_HIP_ERR_NOMEM;
+}
+
 }  // namespace
 
 extern "C" {
 
-int vlrf_nfw_open(const char* path, vlrf_nfw_t* out) {
+static int nfw_open(const char* path, vlrf_nfw_t* out) {
     using vlrf_hip::set_error;
     if (!path || !out) { set_error("nfw_open: null argument"); return VLRF_HIP_ERR_ARG; }
     *out = nullptr;
@@ -140,8 +156,19 @@ int vlrf_nfw_open(const char* path, vlrf_nfw_t* out) {
             return VLRF_HIP_ERR_ARG;
         }
         {
+            // Every dtype stores at least 18 bytes per 32 elements, so a numel
+            // beyond twice the bytes left cannot be in the file; checking that
+            // first keeps the size products below in range.
+            const int64_t left = size - std::ftell(f.f);
+            if (e.numel > 2 * left) goto truncated;
             int64_t prod = 1;
-            for (int d = 0; d < nd; ++d) prod *= e.dims[d];
+            bool dims_ok = true;
+            for (int d = 0; d < nd && dims_ok; ++d)
+                dims_ok = e.dims[d] >= 0 && !__builtin_mul_overflow(prod, (int64_t)e.dims[d], &prod);
+            if (!dims_ok) {
+                set_error("nfw_open: tensor '%s' has a negative or overflowing dimension", e.name.c_str());
+                return VLRF_HIP_ERR_ARG;
+            }
             e.bytes = payload_bytes(e.dtype, e.numel);
             if (e.numel < 0 || (nd && prod != e.numel) || e.bytes < 0) {
                 set_error("nfw_open: tensor '%s': dtype %d, numel %lld inconsistent", e.name.c_str(), e.dtype,
@@ -163,6 +190,11 @@ int vlrf_nfw_open(const char* path, vlrf_nfw_t* out) {
 truncated:
     set_error("nfw_open: '%s' is truncated", path);
     return VLRF_HIP_ERR_ARG;
+}
+
+int vlrf_nfw_open(const char* path, vlrf_nfw_t* out) {
+    if (out) *out = nullptr;
+    return guarded("nfw_open", [&] { return nfw_open(path, out); });
 }
 
 void vlrf_nfw_close(vlrf_nfw_t f) { delete f; }
@@ -213,7 +245,7 @@ int vlrf_nfw_read(vlrf_nfw_t f, int i, void* dst, int64_t cap) {
     return VLRF_HIP_OK;
 }
 
-int vlrf_nfw_read_f32(vlrf_nfw_t f, int i, float* dst, int64_t n) {
+static int nfw_read_f32(vlrf_nfw_t f, int i, float* dst, int64_t n) {
     if (!f || !dst || i < 0 || i >= (int)f->t.size()) {
         vlrf_hip::set_error("nfw_read_f32: bad arguments");
         return VLRF_HIP_ERR_ARG;
@@ -236,7 +268,11 @@ int vlrf_nfw_read_f32(vlrf_nfw_t f, int i, float* dst, int64_t n) {
     return vlrf_dequantize(raw.data(), e.dtype == VLRF_NFW_Q8_0 ? VLRF_DT_Q8_0 : VLRF_DT_Q4_0, dst, e.numel);
 }
 
-int vlrf_hip_model_load_nfw(vlrf_hip_model_t m, const char* path, int* n_loaded) {
+int vlrf_nfw_read_f32(vlrf_nfw_t f, int i, float* dst, int64_t n) {
+    return guarded("nfw_read_f32", [&] { return nfw_read_f32(f, i, dst, n); });
+}
+
+static int model_load_nfw(vlrf_hip_model_t m, const char* path, int* n_loaded) {
     using vlrf_hip::set_error;
     if (n_loaded) *n_loaded = 0;
     vlrf_hip_model_config cfg;
@@ -283,6 +319,11 @@ int vlrf_hip_model_load_nfw(vlrf_hip_model_t m, const char* path, int* n_loaded)
     }
     if (n_loaded) *n_loaded = loaded;
     return VLRF_HIP_OK;
+}
+
+int vlrf_hip_model_load_nfw(vlrf_hip_model_t m, const char* path, int* n_loaded) {
+    if (n_loaded) *n_loaded = 0;
+    return guarded("load_nfw", [&] { return model_load_nfw(m, path, n_loaded); });
 }
 
 }  // extern "C"
