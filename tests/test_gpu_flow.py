@@ -20,10 +20,10 @@ pytestmark = pytest.mark.gpu
 
 
 def _model(ctx, cfg, seed, flow, wait_us=None):
-    old = {k: os.environ.get(k) for k in ("VLRF_HIP_FLOW", "VLRF_HIP_FLOW_WAIT_US")}
+    old = {k: os.environ.get(k) for k in ("VLRF_HIP_FLOW", "VLRF_HIP_WAIT_US")}
     os.environ["VLRF_HIP_FLOW"] = "1" if flow else "0"
     if wait_us is not None:
-        os.environ["VLRF_HIP_FLOW_WAIT_US"] = str(wait_us)
+        os.environ["VLRF_HIP_WAIT_US"] = str(wait_us)
     try:
         m = V.Model(ctx, cfg)             # the switches are read when the model is created
     finally:

@@ -208,6 +208,7 @@ struct DecodeFuse {
     int nch = 0;
 };
 constexpr int kAttnChunkStride = 68, kAttnMaxChunks = 16;
+constexpr int kAttnChunkRows = 512;   // cache rows per chunk of the chunked form
 // Chunks of the decode attention's chunked form for a cache of cap rows, or 0
 // where it does not apply (d_head != 64, more than 8 KV heads, caches the
 // single-pass kernel covers, or more than kAttnMaxChunks chunks).
@@ -293,6 +294,36 @@ FlowShape flow_shape(int w_dtype, int lm_dtype, int kv_dtype, int L, int D, int 
 // FlowParams::gate_chunk for a step at position pos.
 int flow_gate_chunk(const FlowShape& f, int pos);
 int launch_flow_step(hipStream_t s, const FlowParams& p);
+
+// A layer's QKV projection and its chunked decode attention in one launch
+// (kernels/qkv_attn.hip): the projection's rows are published as tagged words
+// (value | epoch << 32, epoch = state[3]) in `tags`, which the attention's
+// workgroups wait for.  Per query head, fz.chunks holds fz.nch + 1 partials:
+// the cache chunks (the token's row left out) and then the token's own key.
+constexpr int kQkvAttnMaxD = 2048;   // d_model of the fused form (the new-row workgroup stages q)
+struct QkvAttnParams {
+    const uint8_t* qa = nullptr;      // Wqkv codes / scales
+    const __half* da = nullptr;
+    int N = 0, K = 0;                 // d_model + 2*n_kv*64 rows, d_model columns
+    const float* x = nullptr;         // the residual stream, or (gather) the embedding table
+    float* x_copy = nullptr;          // gather: the token's row is copied here
+    const float* norm_w = nullptr;    // ln1
+    float eps = 0.f;
+    int nq = 0;                       // projection workgroups (a multiple of 8)
+    int na = 0;                       // attention workgroups (then one for the token's K/V row)
+    uint64_t* tags = nullptr;         // [N] this layer's tagged projection outputs
+    long head_stride = 0;             // cache elements per KV head (max_seq * 64)
+    int rep = 1;                      // query heads per KV head
+    DecodeFuse fz;                    // RoPE tables, the cache (written at the token's row), chunks
+    float scale = 0.f;
+    int* state = nullptr;             // [0] token, [1] position, [3] epoch
+    int* status = nullptr;            // [4] failure flag, workgroup, phase, layer
+    long long limit = 0;              // wall-clock ticks a wait may last
+    int layer = 0;
+};
+bool qkv_attn_supported(int w_dtype, int N, int K, int nch, int n_kv);
+int qkv_attn_blocks(int rep, int n_kv, int nch);
+int launch_qkv_attn(hipStream_t s, const QkvAttnParams& p, int w_dtype, int kv_dtype, bool gather);
 
 int launch_embed(hipStream_t s, const float* table, const int* tok_dev, float* x, int D);
 // argmax over logits[n] (first maximum) -> state[0] (token), appends to

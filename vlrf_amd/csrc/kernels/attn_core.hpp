@@ -103,6 +103,26 @@ __device__ __forceinline__ void load_round(Round<KVT>& R, const int8_t* kc, cons
     }
 }
 
+// Element j of the token's stored K or V row: quantized (Q8_0: clamp(round(x
+// * inv)) with the row scale sc, zero for an all-zero row, kv_cache.hpp:102-117),
+// converted to F16 bits (kv_cache.hpp:68-97) or kept (F32); stored when wr, and
+// the value attention reads back returned.
+template <int KVT>
+__device__ __forceinline__ float store_elem(int8_t* row, int j, float x, float sc, float inv, bool nz, bool wr) {
+    if constexpr (KVT == VLRF_KV_Q8_0) {
+        const int c = nz ? min(127, max(-127, (int)roundf(x * inv))) : 0;
+        if (wr) row[j] = (int8_t)c;
+        return (float)c * sc;
+    } else if constexpr (KVT == VLRF_KV_F16) {
+        const uint16_t hb16 = f32_to_f16_kv(x);
+        if (wr) reinterpret_cast<uint16_t*>(row)[j] = hb16;
+        return f16_bits_to_f32(hb16);
+    } else {
+        if (wr) reinterpret_cast<float*>(row)[j] = x;
+        return x;
+    }
+}
+
 template <int NW>
 struct Smem {
     __align__(16) float qs[D];
@@ -143,7 +163,7 @@ template <int KVT, bool FUSED, int NW, class Out>
 __device__ __forceinline__ void chunk(Smem<NW>& sm, const Round<KVT>& R, float q0, float q1, const NewRow& nr, bool writer,
                                       bool scale_writer, int g, int c0, int cap, size_t hb, int ctx, int pos, bool rot,
                                       bool has_new, float scale, const DecodeFuse& fz, Out&& out) {
-    constexpr bool Q8 = KVT == VLRF_KV_Q8_0, H16 = KVT == VLRF_KV_F16;
+    constexpr bool Q8 = KVT == VLRF_KV_Q8_0;
     constexpr int EB = KV<KVT>::EB, NT = 64 * NW;
     constexpr bool V2 = NT < 512;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -242,20 +262,8 @@ __device__ __forceinline__ void chunk(Smem<NW>& sm, const Round<KVT>& R, float q
         const bool wr = writer && pos < cap;
         int8_t* krow = fz.kq_w + (hb + (size_t)pos * D) * EB;
         int8_t* vrow = fz.vq_w + (hb + (size_t)pos * D) * EB;
-        // stores element j of a row (when writer) and returns the value attention reads back
         auto put = [&](int8_t* row, int j, float x, float sc, float inv, bool nz) -> float {
-            if constexpr (Q8) {
-                const int c = nz ? min(127, max(-127, (int)roundf(x * inv))) : 0;
-                if (wr) row[j] = (int8_t)c;
-                return (float)c * sc;
-            } else if constexpr (H16) {
-                const uint16_t hb16 = f32_to_f16_kv(x);
-                if (wr) reinterpret_cast<uint16_t*>(row)[j] = hb16;
-                return f16_bits_to_f32(hb16);
-            } else {
-                if (wr) reinterpret_cast<float*>(row)[j] = x;
-                return x;
-            }
+            return store_elem<KVT>(row, j, x, sc, inv, nz, wr);
         };
         if (tid < npairs && tid / HALF == g) {
             const int j = tid % HALF;

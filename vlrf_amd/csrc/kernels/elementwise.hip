@@ -349,6 +349,9 @@ __global__ __launch_bounds__(1024) void argmax_step_kernel(const float* __restri
         if (g < gen_cap) gen_ids[g] = tok;
         state[2] = g + 1;
         state[1] = state[1] + 1;
+        // The next step's epoch: the tag of the words the fused QKV + attention
+        // launch exchanges (every launch of this step has finished reading it).
+        state[3] = state[3] + 1;
     }
 }
 

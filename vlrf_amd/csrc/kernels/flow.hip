@@ -41,21 +41,20 @@
 #include "../internal.hpp"
 #include "attn_core.hpp"
 #include "gemv_core.hpp"
+#include "tagged.hpp"
 
 #include <algorithm>
 
 namespace vlrf_hip {
 namespace {
 
+using namespace tagged;
 using gemv::Gemv;
 using gemv::GemvRegs;
 using gemv::kGemvThreads;
 using gemv::kGemvWaves;
 using gemv::Shape;
-typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kSc1 = 16;                     // buffer cache policy: device-coherent (sc1)
 constexpr int kPart = kAttnChunkStride;      // words per (head, chunk) partial: acc[64], m, l, 2 pad
 constexpr int kChunkRows = 512;              // cache rows per attention workgroup (8 waves x 64)
 constexpr int kRpwQKV = 2, kRpwGU = 2;       // rows per wave of the QKV and gate/up phases
@@ -64,134 +63,9 @@ enum : int { kPhQKV = 1, kPhAtt, kPhO, kPhGU, kPhDown, kPhLM, kPhArgmax };
 
 static_assert(sizeof(FlowParams) <= 4096, "the one-launch step's arguments exceed 4 KiB");
 
-__device__ __forceinline__ void put_word(uint64_t* p, uint32_t bits, uint32_t tag) {
-    __hip_atomic_store(p, ((uint64_t)tag << 32) | bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-struct Ctl {
-    __amdgpu_buffer_rsrc_t rs;   // the tagged arena
-    uint32_t tag;
-    int* status;
-    long long t0, limit;
-    int phase, layer;
-};
-
-// Records the first failing wait (block, phase, layer) and raises the flag.
-__device__ void fail(const Ctl& c) {
-    int expected = 0;
-    if (__hip_atomic_compare_exchange_strong(&c.status[0], &expected, 1, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
-                                             __HIP_MEMORY_SCOPE_AGENT)) {
-        __hip_atomic_store(&c.status[1], (int)blockIdx.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(&c.status[2], c.phase, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(&c.status[3], c.layer, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-}
-
-// Keeps the loads above it (weights, cache rows) above the wait that follows:
-// their results are used only after the wait, on the path where it succeeds,
-// and the compiler otherwise sinks them there, so the weight stream would
-// start only once the inputs are in.  A compiler-only fence: it emits nothing
-// and, unlike an asm memory clobber, makes the compiler wait for nothing.
-__device__ __forceinline__ void issue_before_wait() { __atomic_signal_fence(__ATOMIC_SEQ_CST); }
-
-// One pass over the wave's N pieces (VT = u32x2: one tagged word at each byte
-// offset; u32x4: two words); true when every used piece carries the tag.
-template <int N, class VT>
-__device__ __forceinline__ bool poll_pass(const Ctl& c, const int (&off)[N], const bool (&use)[N], VT (&v)[N]) {
-#pragma unroll
-    for (int i = 0; i < N; ++i) {
-        if constexpr (sizeof(VT) == 16) v[i] = __builtin_amdgcn_raw_buffer_load_b128(c.rs, off[i], 0, kSc1);
-        else v[i] = __builtin_amdgcn_raw_buffer_load_b64(c.rs, off[i], 0, kSc1);
-    }
-    bool ok = true;
-#pragma unroll
-    for (int i = 0; i < N; ++i) {
-        bool good = v[i].y == c.tag;
-        if constexpr (sizeof(VT) == 16) good = good && v[i].w == c.tag;
-        if (use[i] && !good) ok = false;
-    }
-    return __all(ok);
-}
-
-// Polls until every used piece of the wave is valid; after a failed pass it
-// waits for the gate word (byte offset `gate`) before the next full pass.
-// False when the wait ran out (recorded) or another workgroup failed.
-template <int N, class VT>
-__device__ bool poll(const Ctl& c, const int (&off)[N], const bool (&use)[N], VT (&v)[N], int gate) {
-    if (poll_pass<N, VT>(c, off, use, v)) return true;
-    for (;;) {
-        const u32x2 g = __builtin_amdgcn_raw_buffer_load_b64(c.rs, gate, 0, kSc1);
-        if (__hip_atomic_load(c.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return false;
-        if (wall_clock64() - c.t0 > c.limit) {
-            fail(c);
-            return false;
-        }
-        if (g.y == c.tag) {
-            if (poll_pass<N, VT>(c, off, use, v)) return true;
-            __builtin_amdgcn_s_sleep(1);
-        } else {
-            __builtin_amdgcn_s_sleep(2);
-        }
-    }
-}
-
-// One tagged word (byte offset off, read by the lanes with use set).
-__device__ __forceinline__ bool poll_word(const Ctl& c, int off, bool use, float* out) {
-    int o[1] = {off};
-    bool u[1] = {use};
-    u32x2 r[1];
-    const bool ok = poll<1, u32x2>(c, o, u, r, off);
-    *out = __uint_as_float(r[0].x);
-    return ok;
-}
-
-// Every wave has polled (ok: its own result); true when the whole workgroup may go on.
-__device__ __forceinline__ bool block_ok(bool ok, int* flag) {
-    if (!ok && (threadIdx.x & 63) == 0) *flag = 1;
-    __syncthreads();
-    return *flag == 0;
-}
-
-// The thread's x slots (float4 f = tid + p*threads, elements 4f..4f+3) of a
-// tagged K-vector at word offset w0, polled; gate: its last word.
-template <int WT, int NC>
-__device__ __forceinline__ bool poll_x(const Ctl& c, long long w0, int K, float4 (&v)[Shape<WT, NC>::PER]) {
-    constexpr int PER = Shape<WT, NC>::PER, XF4 = Shape<WT, NC>::XF4;
-    int off[2 * PER];
-    bool use[2 * PER];
-    u32x4 r[2 * PER];
-#pragma unroll
-    for (int p = 0; p < PER; ++p) {
-        const int f = threadIdx.x + p * kGemvThreads;
-        const bool in = f < XF4 && 4 * f < K;
-        off[2 * p] = (int)((w0 + (in ? 4 * f : 0)) * 8);
-        off[2 * p + 1] = off[2 * p] + 16;
-        use[2 * p] = use[2 * p + 1] = in;
-    }
-    const bool ok = poll<2 * PER, u32x4>(c, off, use, r, (int)((w0 + K - 1) * 8));
-#pragma unroll
-    for (int p = 0; p < PER; ++p) {
-        const bool in = use[2 * p];
-        v[p] = in ? make_float4(__uint_as_float(r[2 * p].x), __uint_as_float(r[2 * p].z),
-                                __uint_as_float(r[2 * p + 1].x), __uint_as_float(r[2 * p + 1].z))
-                  : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-    return ok;
-}
-
-template <int WT, int NC>
-__device__ __forceinline__ void load_norm(const float* w, int K, float4 (&gw)[Shape<WT, NC>::PER]) {
-    constexpr int PER = Shape<WT, NC>::PER, XF4 = Shape<WT, NC>::XF4;
-#pragma unroll
-    for (int p = 0; p < PER; ++p) {
-        const int f = threadIdx.x + p * kGemvThreads;
-        gw[p] = reinterpret_cast<const float4*>(w)[(f < XF4 && 4 * f < K) ? f : 0];
-    }
-}
-
 struct Smem {
     float red[kGemvWaves];
-    int flag;
+    int ok[kGemvWaves];   // per-wave poll results (block_ok)
     float best[kGemvWaves];
     int bidx[kGemvWaves];
 };
@@ -237,7 +111,7 @@ struct Step {
             ok = poll_x<WT, NC>(c, xw, K, v);
         }
         if (RPW == 1 && res_w >= 0 && ok) ok = poll_word(c, (int)((res_w + min(row0, N - 1)) * 8), lane == 0, &res);
-        if (!block_ok(ok, &sm.flag)) return;
+        if (!block_ok(ok, sm.ok)) return;
         float inv, xsum[NC];
         gemv::gemv_stage<WT, NC, NORM>(v, gw, xs4, sm.red, K, P.eps, inv, xsum);
         const bool with_res = RPW == 1 && (res_plain || res_w >= 0);
@@ -308,7 +182,7 @@ struct Step {
             bool use[5] = {w == 0, w == 0, tid < npairs, tid < npairs, tid < nrow};
             u32x2 v[5];
             const bool ok = poll<5, u32x2>(c, off, use, v, (int)((qw + P.D + 2 * nrow - 1) * 8));
-            if (!block_ok(ok, &fs.flag)) return;
+            if (!block_ok(ok, fs.ok)) return;
             nr.k0 = __uint_as_float(v[2].x);
             nr.k1 = __uint_as_float(v[3].x);
             nr.vn = __uint_as_float(v[4].x);
@@ -338,7 +212,7 @@ struct Step {
             raw[2 * tid] = __uint_as_float(v[0].x);
             raw[2 * tid + 1] = __uint_as_float(v[0].z);
         }
-        if (!block_ok(ok, &fs.flag)) return;
+        if (!block_ok(ok, fs.ok)) return;
         if (tid < attn::D) {
             float mt = gemv::kNegInfF;
             for (int cc = 0; cc < nch; ++cc) mt = fmaxf(mt, raw[cc * kPart + 64]);
@@ -370,7 +244,7 @@ struct Step {
         load_norm<WT, NCD>(P.ln_final, K, gw);
         issue_before_wait();
         const bool ok = poll_x<WT, NCD>(c, P.a.x2 + (long long)(P.L - 1) * P.a.ld_x, K, v);
-        if (!block_ok(ok, &sm.flag)) return;
+        if (!block_ok(ok, sm.ok)) return;
         float inv, xsum[NCD];
         gemv::gemv_stage<WT, NCD, true>(v, gw, xs4, sm.red, K, P.eps, inv, xsum);
         // First maximum of the rows the wave visits (rows ascend; ties keep the
@@ -417,7 +291,7 @@ struct Step {
         bool use[1] = {tid < n};
         u32x4 r[1];
         const bool ok = poll<1, u32x4>(c, off, use, r, (int)((P.a.lm + 2 * (n - 1) + 1) * 8));
-        if (!block_ok(ok, &sm.flag)) return;
+        if (!block_ok(ok, sm.ok)) return;
         float best = tid < n ? __uint_as_float(r[0].x) : -INFINITY;
         int idx = tid < n ? (int)r[0].z : -1;
         auto take = [&](float ov, int oi) {
@@ -465,7 +339,6 @@ __global__ __launch_bounds__(gemv::kGemvThreads) __attribute__((amdgpu_waves_per
     c.limit = P.limit;
     c.layer = b < P.L * pl.per_layer ? b / pl.per_layer : P.L;
     int r = b - c.layer * pl.per_layer;
-    if (threadIdx.x == 0) sm.flag = 0;
     c.tag = (uint32_t)P.state[3];
     float4* xs4 = reinterpret_cast<float4*>(pool);
     const int l = c.layer;

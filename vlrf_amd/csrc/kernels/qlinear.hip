@@ -186,121 +186,17 @@ using gemv::kGemvMaxK;
 using gemv::kGemvMaxOneGroups;
 using gemv::kGemvWaves;
 
-// XM: bit 0 = RMSNorm fused (norm_w), bit 1 = x is row *x_row of a table (with
-// the raw row copied to x_copy), bit 2 = residual added.  Compile-time: the
-// kernel branches on no argument (measured in the decode step, same box:
-// 0.706 -> 0.686 ms/step for the norm and gather bits).
 template <int WT, int NC, int RPW, bool SWIGLU, int XM>
 __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(
     const uint8_t* __restrict__ qa, const __half* __restrict__ da, const uint8_t* __restrict__ qb,
     const __half* __restrict__ db, int N, int K, const float* __restrict__ x,
     const int* __restrict__ x_row, float* x_copy, const float* __restrict__ norm_w, float eps,
     const float* residual, float* y, int nparts) {
-    using S = gemv::Shape<WT, NC>;
-    constexpr int NM = SWIGLU ? 2 : 1;
-    constexpr int NT = gemv::kGemvThreads;
-    constexpr bool RES = XM & 4;
-    // XM & 8: x is decode attention output in its chunked form (head dim 64):
-    // element e is dim e % 64 of head e / 64, merged here from the nparts
-    // chunk partials of that head (log-sum-exp, attention.hpp:207-309's rule).
-    constexpr bool MERGE = XM & 8;
-    // XM & 16: every wave has at most one row (N <= the grid's row step), so
-    // the second register set of the pipeline is neither loaded nor held.
-    constexpr bool ONE = XM & 16;
-    constexpr int XF4 = S::XF4, PER = S::PER;
-    constexpr int NP = MERGE ? kAttnMaxChunks / PER : 1;   // chunks a merge holds in registers
-    __shared__ float4 xs4[XF4];
-    __shared__ float red[kGemvWaves];
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int nwaves = gridDim.x * kGemvWaves;
-    int row0 = (blockIdx.x * kGemvWaves + wave) * RPW;
-    const int rstep = nwaves * RPW;
-
-    // x_row: x is row *x_row of a table (the embedding gather of the first
-    // layer, ops.hpp:615-626); workgroup 0 copies the raw row to x_copy.
-    //
-    // Vector loads return in issue order, so the activations and the norm
-    // weight are requested first: the staging below then overlaps the weight
-    // stream instead of waiting behind it.  (Loading each wave's slice of x
-    // into registers instead of staging it once per workgroup was measured
-    // slower: 16 waves per CU re-reading x and the norm weight cost more L1
-    // bandwidth than the two barriers.)
-    float xsum[NC];
-    float inv = 1.f;                                  // 1/rms, applied to the finished dots
-    GemvRegs<NM, RPW, NC> A, B;
-    {
-        constexpr bool NORM = XM & 1, GATHER = XM & 2;
-        const float* xs = GATHER ? x + (size_t)(*x_row) * K : x;
-        float4 v[PER], gw[PER];
-        float4 pa[PER][NP];
-        float2 pml[PER][NP];
-#pragma unroll
-        for (int p = 0; p < PER; ++p) {
-            const int f = tid + p * NT;            // float4 index in x
-            const bool in = f < XF4 && 4 * f < K;
-            if constexpr (MERGE) {                 // the head's chunk words, before any use (the 16
-                                                   // threads of a head share the (m, l) loads in L1)
-                const int e = in ? 4 * f : 0;
-                const float* ph = x + (size_t)(e >> 6) * nparts * kAttnChunkStride + (e & 63);
-#pragma unroll
-                for (int c = 0; c < NP; ++c)
-                    if (c < nparts) {
-                        pa[p][c] = *reinterpret_cast<const float4*>(ph + (size_t)c * kAttnChunkStride);
-                        pml[p][c] = *reinterpret_cast<const float2*>(ph - (e & 63) + (size_t)c * kAttnChunkStride + 64);
-                    }
-            } else {
-                const float4 t = reinterpret_cast<const float4*>(xs)[in ? f : 0];
-                v[p] = in ? t : make_float4(0.f, 0.f, 0.f, 0.f);
-            }
-        }
-        if constexpr (NORM) {
-#pragma unroll
-            for (int p = 0; p < PER; ++p) {
-                const int f = tid + p * NT;
-                gw[p] = reinterpret_cast<const float4*>(norm_w)[(f < XF4 && 4 * f < K) ? f : 0];
-            }
-        }
-        // Every wave's activation requests enter the CU's memory pipeline
-        // before any weight request, so x is not queued behind the stream.
-        __builtin_amdgcn_s_barrier();
-        gemv::gemv_load<WT, NM, RPW, NC>(A, qa, da, qb, db, row0, N, K, lane);
-        if constexpr (!ONE) gemv::gemv_load<WT, NM, RPW, NC>(B, qa, da, qb, db, row0 + rstep, N, K, lane);
-
-        if constexpr (MERGE)
-            gemv::gemv_merge<PER, NP>([&](int p, int c) { return pa[p][c]; }, [&](int p, int c) { return pml[p][c]; },
-                                      nparts, XF4, K, tid, v);
-        if (GATHER && x_copy && blockIdx.x == 0) {
-#pragma unroll
-            for (int p = 0; p < PER; ++p) {
-                const int f = tid + p * NT;
-                if (f < XF4 && 4 * f < K) reinterpret_cast<float4*>(x_copy)[f] = v[p];
-            }
-        }
-        gemv::gemv_stage<WT, NC, NORM>(v, gw, xs4, red, K, eps, inv, xsum);
-    }
-
-    auto store = [&](int row, float out) {
-        if (lane == 0 && row < N) {
-            if constexpr (RES) out = out + residual[row];
-            y[row] = out;
-        }
-    };
-    if constexpr (ONE) {
-        if (row0 < N) gemv::gemv_compute<WT, NM, RPW, NC, SWIGLU>(A, xs4, xsum, inv, row0, N, K, lane, store);
-        return;
-    }
-    // Loads stay unconditional inside the loop as well (see gemv_load).
-    for (; row0 < N; row0 += 2 * rstep) {
-        const int r1 = row0 + rstep;
-        gemv::gemv_compute<WT, NM, RPW, NC, SWIGLU>(A, xs4, xsum, inv, row0, N, K, lane, store);
-        if (r1 >= N) break;
-        const int r2 = r1 + rstep;
-        gemv::gemv_load<WT, NM, RPW, NC>(A, qa, da, qb, db, r2, N, K, lane);
-        gemv::gemv_compute<WT, NM, RPW, NC, SWIGLU>(B, xs4, xsum, inv, r1, N, K, lane, store);
-        if (r2 >= N) break;
-        gemv::gemv_load<WT, NM, RPW, NC>(B, qa, da, qb, db, r2 + rstep, N, K, lane);
-    }
+    gemv::gemv_body<WT, NC, RPW, SWIGLU, XM>(qa, da, qb, db, N, K, x, x_row, x_copy, norm_w, eps, nparts, blockIdx.x,
+                                              gridDim.x, [&](int row, float out) {
+                                                  if constexpr ((XM & 4) != 0) out = out + residual[row];
+                                                  y[row] = out;
+                                              });
 }
 
 template <int WT, bool SWIGLU>

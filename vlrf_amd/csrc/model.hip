@@ -69,7 +69,8 @@ struct vlrf_hip_model {
     const float* sin_t = nullptr;
     float *x = nullptr, *qkv = nullptr, *att = nullptr, *h = nullptr, *logits = nullptr, *part = nullptr;
     int nch = 0;               // decode attention in chunked form (merged by the O GEMV) when > 0
-    float* chunks = nullptr;   // its partials [H][nch][kAttnChunkStride]
+    int nparts = 0;            // partials per head: nch, plus the token's own key when fused
+    float* chunks = nullptr;   // its partials [H][nparts][kAttnChunkStride]
     int* state = nullptr;      // [0] token, [1] position, [2] generated count, [3] epoch (>= 1)
     int* gen_ids = nullptr;    // [S]
     int* prompt = nullptr;     // [S] staged prompt ids
@@ -85,6 +86,12 @@ struct vlrf_hip_model {
     FlowParams fp;             // everything but the per-launch gate
     uint64_t* flow_arena = nullptr;
     int* flow_status = nullptr;         // [4] failure flag, block, phase, layer
+    // Fused QKV + attention launch (kernels/qkv_attn.hip) where it applies
+    // (VLRF_HIP_QKV_ATTN=0 queues the two kernels instead).
+    bool qkv_attn = false;
+    uint64_t* qkv_tags = nullptr;   // [L][D + 2*dkv] tagged projection outputs
+    int* step_status = nullptr;     // [4] failure flag, workgroup, phase, layer
+    long long wait_limit = 0;       // wall-clock ticks a wait may last
     int pos = 0;               // host mirror of state[1]
     // Batched prefill (matrix cores) work buffers, sized for pf_cap rows.
     int pf_cap = 0;
@@ -116,12 +123,6 @@ int enqueue_step(vlrf_hip_model* m, hipStream_t s) {
         float* q = m->qkv;
         float* k = m->qkv + m->D;
         float* v = m->qkv + m->D + m->dkv;
-        if (!rc) {
-            if (l == 0 && gather)   // embedding_lookup (ops.hpp:615-626) fused: x = embed[token]
-                rc = launch_qlinear_gather(s, Ly.wqkv, m->embed, m->state, m->x, m->qkv, Ly.ln1, eps);
-            else
-                rc = launch_qlinear(s, Ly.wqkv, m->x, m->qkv, 1, Ly.ln1, eps, nullptr);
-        }
         DecodeFuse fz;
         fz.k_new = k;
         fz.v_new = v;
@@ -135,10 +136,40 @@ int enqueue_step(vlrf_hip_model* m, hipStream_t s) {
         fz.max_seq = m->S;
         fz.chunks = m->chunks;
         fz.nch = m->nch;
-        if (!rc) rc = launch_attn_decode(s, q, Ly.kv.k, Ly.kv.v, Ly.kv.ks, Ly.kv.vs, Ly.kv.dtype,
-                                         (long)m->S * m->dh, m->H, m->G, m->dh, 1, m->state + 1,
-                                         m->n_splits, scale, m->part, m->att, &fz);
-        if (!rc) rc = m->nch ? launch_qlinear_merge(s, Ly.wo, m->chunks, m->nch, m->x, m->x)
+        if (m->qkv_attn) {   // one launch: the projection's rows feed the attention as tagged words
+            QkvAttnParams p;
+            p.qa = Ly.wqkv.q;
+            p.da = Ly.wqkv.d;
+            p.N = Ly.wqkv.N;
+            p.K = Ly.wqkv.K;
+            p.x = l == 0 && gather ? m->embed : m->x;
+            p.x_copy = l == 0 && gather ? m->x : nullptr;
+            p.norm_w = Ly.ln1;
+            p.eps = eps;
+            p.nq = (p.N + 63) / 64 * 8;
+            p.rep = m->H / m->G;
+            p.na = qkv_attn_blocks(p.rep, m->G, m->nch);
+            p.tags = m->qkv_tags + (size_t)l * p.N;
+            p.head_stride = (long)m->S * m->dh;
+            p.fz = fz;
+            p.scale = scale;
+            p.state = m->state;
+            p.status = m->step_status;
+            p.limit = m->wait_limit;
+            p.layer = l;
+            if (!rc) rc = launch_qkv_attn(s, p, m->cfg.weight_dtype, m->cfg.kv_dtype, l == 0 && gather);
+        } else {
+            if (!rc) {
+                if (l == 0 && gather)   // embedding_lookup (ops.hpp:615-626) fused: x = embed[token]
+                    rc = launch_qlinear_gather(s, Ly.wqkv, m->embed, m->state, m->x, m->qkv, Ly.ln1, eps);
+                else
+                    rc = launch_qlinear(s, Ly.wqkv, m->x, m->qkv, 1, Ly.ln1, eps, nullptr);
+            }
+            if (!rc) rc = launch_attn_decode(s, q, Ly.kv.k, Ly.kv.v, Ly.kv.ks, Ly.kv.vs, Ly.kv.dtype,
+                                             (long)m->S * m->dh, m->H, m->G, m->dh, 1, m->state + 1,
+                                             m->n_splits, scale, m->part, m->att, &fz);
+        }
+        if (!rc) rc = m->nch ? launch_qlinear_merge(s, Ly.wo, m->chunks, m->nparts, m->x, m->x)
                              : launch_qlinear(s, Ly.wo, m->att, m->x, 1, nullptr, 0.f, m->x);
         if (!rc) rc = launch_qlinear_swiglu(s, Ly.wg, Ly.wu, m->x, m->h, 1, Ly.ln2, eps);
         if (!rc) rc = launch_qlinear(s, Ly.wd, m->h, m->x, 1, nullptr, 0.f, m->x);
@@ -204,8 +235,6 @@ int ensure_flow(vlrf_hip_model* m) {
         p.layers[l].ks = Ly.kv.ks;
         p.layers[l].vs = Ly.kv.vs;
     }
-    int rate_khz = 0;
-    VH_CHECK(hipDeviceGetAttribute(&rate_khz, hipDeviceAttributeWallClockRate, m->ctx->device));
     if (hipMalloc((void**)&m->flow_arena, (size_t)f.a.words * 8) != hipSuccess ||
         hipMalloc((void**)&m->flow_status, 4 * sizeof(int)) != hipSuccess) {
         drop_flow(m);
@@ -235,11 +264,7 @@ int ensure_flow(vlrf_hip_model* m) {
     p.arena = m->flow_arena;
     p.a = f.a;
     p.status = m->flow_status;
-    // A wait may last 0.5 s (VLRF_HIP_FLOW_WAIT_US overrides it: the tests
-    // shorten it to exercise the failure path).
-    long long wait_us = 500000;
-    if (const char* w = std::getenv("VLRF_HIP_FLOW_WAIT_US")) wait_us = std::atoll(w);
-    p.limit = (long long)rate_khz * wait_us / 1000;
+    p.limit = m->wait_limit;
     p.plan = f.plan;
     m->flow = f;
     return VLRF_HIP_OK;
@@ -258,19 +283,21 @@ int launch_step(vlrf_hip_model* m, int pos) {
     return VLRF_HIP_OK;
 }
 
-// After the queued steps have finished: a one-launch step whose wait ran out
-// left its flag; report it, clear it and move to a fresh epoch (the failed
-// step may have published words of the old one), and take the device
-// position as the host's.
-int check_flow(vlrf_hip_model* m) {
-    if (!m->flow.ok) return VLRF_HIP_OK;
+// After the queued steps have finished: a launch whose wait for another
+// workgroup's output ran out (the one-launch step, or the fused QKV +
+// attention launch) left its flag; report it, clear it and move to a fresh
+// epoch (the failed step may have published words of the old one), and take
+// the device position as the host's.
+int check_waits(vlrf_hip_model* m) {
+    int* status = m->flow.ok ? m->flow_status : m->step_status;
+    if (!status) return VLRF_HIP_OK;
     hipStream_t s = m->ctx->stream;
     int* st = m->pinned + 4;
-    VH_CHECK(hipMemcpyAsync(st, m->flow_status, 4 * sizeof(int), hipMemcpyDeviceToHost, s));
+    VH_CHECK(hipMemcpyAsync(st, status, 4 * sizeof(int), hipMemcpyDeviceToHost, s));
     VH_CHECK(hipStreamSynchronize(s));
     if (!st[0]) return VLRF_HIP_OK;
     const int blk = st[1], ph = st[2], layer = st[3];
-    VH_CHECK(hipMemsetAsync(m->flow_status, 0, 4 * sizeof(int), s));
+    VH_CHECK(hipMemsetAsync(status, 0, 4 * sizeof(int), s));
     VH_CHECK(hipMemcpyAsync(m->pinned, m->state, 4 * sizeof(int), hipMemcpyDeviceToHost, s));
     VH_CHECK(hipStreamSynchronize(s));
     m->pinned[3] += 1;
@@ -365,7 +392,51 @@ int vlrf_hip_model_create(vlrf_hip_ctx_t ctx, const vlrf_hip_model_config* cfg, 
     wo_shape.N = m->D;
     wo_shape.K = m->H * dh;
     if (m->nch && (wo_shape.K != m->D || m->nch > qlinear_merge_max_chunks(wo_shape))) m->nch = 0;
-    if (m->nch) dalloc((void**)&m->chunks, (size_t)m->H * m->nch * kAttnChunkStride * 4);
+    // The fused QKV + attention launch, which always takes the chunked form
+    // (one 512-row chunk for the caches the single-pass kernel would cover):
+    // Q8_0/F16 caches (an F32 cache's rounds need more registers than the
+    // fused kernel keeps: it would spill).
+    const char* qa_env = std::getenv("VLRF_HIP_QKV_ATTN");
+    if (!(qa_env && std::strcmp(qa_env, "0") == 0) && c.kv_dtype != VLRF_KV_F32 && dh == 64 && m->G <= 8 &&
+        wo_shape.K == m->D) {
+        const int n = (m->S + kAttnChunkRows - 1) / kAttnChunkRows;
+        if (n + 1 <= qlinear_merge_max_chunks(wo_shape) &&
+            qkv_attn_supported(c.weight_dtype, m->D + 2 * m->dkv, m->D, n, m->G)) {
+            m->nch = n;
+            m->qkv_attn = true;
+        }
+    }
+    m->nparts = m->nch + (m->qkv_attn ? 1 : 0);
+    if (m->nch) dalloc((void**)&m->chunks, (size_t)m->H * m->nparts * kAttnChunkStride * 4);
+    // Zero words carry no epoch (the epoch starts at 1).
+    auto tagged = [&](uint64_t** p, size_t words) {
+        dalloc((void**)p, words * 8);
+        if (!rc && hipMemset(*p, 0, words * 8) != hipSuccess) {
+            set_error("model_create: clearing the tagged words failed");
+            rc = VLRF_HIP_ERR_RUNTIME;
+        }
+    };
+    if (m->qkv_attn) tagged(&m->qkv_tags, (size_t)m->L * (m->D + 2 * m->dkv));
+    if (m->qkv_attn) {
+        dalloc((void**)&m->step_status, 4 * sizeof(int));
+        if (!rc && hipMemset(m->step_status, 0, 4 * sizeof(int)) != hipSuccess) {
+            set_error("model_create: clearing the status words failed");
+            rc = VLRF_HIP_ERR_RUNTIME;
+        }
+    }
+    {
+        // A wait for another workgroup's output may last 0.5 s
+        // (VLRF_HIP_WAIT_US overrides it: the tests shorten it to exercise the
+        // failure path).
+        int rate_khz = 0;
+        if (!rc && hipDeviceGetAttribute(&rate_khz, hipDeviceAttributeWallClockRate, ctx->device) != hipSuccess) {
+            set_error("model_create: no wall-clock rate");
+            rc = VLRF_HIP_ERR_RUNTIME;
+        }
+        long long wait_us = 500000;
+        if (const char* w = std::getenv("VLRF_HIP_WAIT_US")) wait_us = std::atoll(w);
+        m->wait_limit = (long long)rate_khz * wait_us / 1000;
+    }
     dalloc((void**)&m->state, 4 * sizeof(int));
     dalloc((void**)&m->gen_ids, (size_t)m->S * sizeof(int));
     dalloc((void**)&m->prompt, (size_t)m->S * sizeof(int));
@@ -430,7 +501,8 @@ void vlrf_hip_model_destroy(vlrf_hip_model_t m) {
                     (void*)m->gen_ids, (void*)m->prompt})
         if (p) (void)hipFree(p);
     for (void* p : {(void*)m->pf_x, (void*)m->pf_qkv, (void*)m->pf_a, (void*)m->pf_att, (void*)m->pf_h,
-                    (void*)m->pf_ids, (void*)m->flow_arena, (void*)m->flow_status})
+                    (void*)m->pf_ids, (void*)m->flow_arena, (void*)m->flow_status, (void*)m->qkv_tags,
+                    (void*)m->step_status})
         if (p) (void)hipFree(p);
     if (m->pinned) (void)hipHostFree(m->pinned);
     delete m;
@@ -552,7 +624,7 @@ int vlrf_hip_model_step(vlrf_hip_model_t m, int32_t token, int32_t* next, float*
     VH_CHECK(hipMemcpyAsync(m->pinned, m->state, sizeof(int), hipMemcpyDeviceToHost, s));
     if (logits) VH_CHECK(hipMemcpyAsync(logits, m->logits, (size_t)m->V * 4, hipMemcpyDeviceToHost, s));
     VH_CHECK(hipStreamSynchronize(s));
-    if ((rc = check_flow(m))) return rc;
+    if ((rc = check_waits(m))) return rc;
     m->pos += 1;
     if (next) *next = m->pinned[0];
     return VLRF_HIP_OK;
@@ -577,7 +649,7 @@ int vlrf_hip_model_prefill(vlrf_hip_model_t m, const int32_t* ids, int n, int32_
     }
     VH_CHECK(hipMemcpyAsync(m->pinned, m->state, sizeof(int), hipMemcpyDeviceToHost, s));
     VH_CHECK(hipStreamSynchronize(s));
-    if ((rc = check_flow(m))) return rc;
+    if ((rc = check_waits(m))) return rc;
     m->pos += n;
     if (next) *next = m->pinned[0];
     return VLRF_HIP_OK;
@@ -736,7 +808,7 @@ int vlrf_hip_model_read_generated(vlrf_hip_model_t m, int32_t* out_ids, int n) {
     hipStream_t s = m->ctx->stream;
     VH_CHECK(hipMemcpyAsync(out_ids, m->gen_ids, (size_t)n * sizeof(int), hipMemcpyDeviceToHost, s));
     VH_CHECK(hipStreamSynchronize(s));
-    return check_flow(m);
+    return check_waits(m);
 }
 
 int vlrf_hip_model_generate(vlrf_hip_model_t m, int32_t first, int n_steps, int32_t* out_ids) {
