@@ -6,8 +6,8 @@ head and the token's K/V row.  Parity as for the two kernels it replaces
 AttentionBlock::forward, attention.hpp:89-186): greedy streams identical to
 the oracle's and teacher-forced logits within 1e-3 of them, for Q8_0/Q4_0
 weights, Q8_0/F16 caches, GQA groups 1-8 and one to three 512-row chunks; the
-fused and unfused steps agree to 1e-5; a wait that runs out is reported and
-leaves the model usable."""
+fused step is as close to the oracle as the unfused one over 560 steps; a wait
+that runs out is reported and leaves the model usable."""
 import os
 
 import numpy as np
@@ -81,20 +81,28 @@ def test_fused_stream_and_logits_match_oracle(ctx, orc, wdt, kdt, cap, heads, kv
     assert worst <= 1e-3, worst
 
 
-def test_fused_agrees_with_the_two_kernels(ctx):
-    """Same weights with and without the fusion: logits within 1e-5, the same
-    tokens, across a chunk boundary (cache rows 512+)."""
+def test_fused_as_accurate_as_the_two_kernels(ctx, orc):
+    """Same weights with and without the fusion, fed the same 560 tokens (the
+    cache crosses a 512-row chunk boundary), each against the oracle at every
+    step.  The fused attention exponentiates against the chunk's maximum and
+    merges the token's key as its own partial, so the two paths agree to
+    rounding, not bit for bit, and a rounding difference can flip a Q8_0 code
+    of a cached row; each path's distance from the oracle is what is bounded:
+    within the parity tolerance, and the fused path no further than twice the
+    unfused one's."""
     cfg = _cfg(V.DT_Q8_0, V.KV_Q8_0, 1100)
-    a, _ = _model(ctx, cfg, 62, fused=True)
+    a, w = _model(ctx, cfg, 62, fused=True)
     b, _ = _model(ctx, cfg, 62, fused=False)
-    worst = 0.0
-    for t in F.tokens(62, "feed", 30, cfg["vocab_size"]):
-        na, la = a.step(int(t), want_logits=True)
-        nb, lb = b.step(int(t), want_logits=True)
-        worst = max(worst, rel_err(la, lb))
-        assert na == nb
-    assert worst <= 1e-5, worst
-    assert list(a.generate_ids(na, 520)) == list(b.generate_ids(nb, 520))
+    om = orc.Model(cfg, w, n_threads=4)
+    ea = eb = eab = 0.0
+    for t in F.tokens(62, "feed", 560, cfg["vocab_size"]):
+        _, la = a.step(int(t), want_logits=True)
+        _, lb = b.step(int(t), want_logits=True)
+        _, lo = om.forward([int(t)], want_logits=True)
+        ea, eb, eab = max(ea, rel_err(la, lo)), max(eb, rel_err(lb, lo)), max(eab, rel_err(la, lb))
+    print(f"  560 steps vs oracle: fused {ea:.2e}, two kernels {eb:.2e}; between them {eab:.2e}", flush=True)
+    assert ea <= 1e-3 and eb <= 1e-3, (ea, eb)
+    assert ea <= max(2 * eb, 1e-4), (ea, eb)
 
 
 def test_fused_wait_timeout_is_reported(ctx, orc):

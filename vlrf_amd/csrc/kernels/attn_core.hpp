@@ -19,6 +19,7 @@
 #pragma once
 
 #include "../internal.hpp"
+#include "gemv_core.hpp"
 
 #include <cmath>
 
@@ -27,6 +28,23 @@ namespace attn {
 
 constexpr int D = 64, HALF = 32;
 constexpr float kNegInf = -INFINITY;
+
+// Signed byte K of a word as f32 in one instruction (SDWA source select with
+// sign extension; the compiler otherwise extracts the byte first).
+template <int K>
+__device__ __forceinline__ float s8f(uint32_t w) {
+    float r;
+    if constexpr (K == 0)
+        asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0" : "=v"(r) : "v"(w));
+    else if constexpr (K == 1)
+        asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1" : "=v"(r) : "v"(w));
+    else if constexpr (K == 2)
+        asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2" : "=v"(r) : "v"(w));
+    else
+        asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3" : "=v"(r) : "v"(w));
+    return r;
+}
+__device__ __forceinline__ float4 s8f4(uint32_t w) { return make_float4(s8f<0>(w), s8f<1>(w), s8f<2>(w), s8f<3>(w)); }
 
 // RoPE of one pair (rope.hpp:90-96), each product rounded separately.
 __device__ __forceinline__ void rope2(float x0, float x1, float c, float s, float* y0, float* y1) {
@@ -330,6 +348,127 @@ __device__ __forceinline__ void chunk(Smem<NW>& sm, const Round<KVT>& R, float q
             }
         }
         out(tid, ot, mt, lt);
+    }
+}
+
+
+// ---- one chunk without the token's row (the fused QKV + attention launch) ----------
+// The attention of query head h over the cache rows [c0, min(c0 + 64*NW, pos))
+// for the wave's loaded round R: every row before the token, none of it (the
+// token's key is merged as its own partial).  q0/q1 (wave 0, lanes j < 32):
+// the head's q[j], q[j + 32] before RoPE (rc, rs: the table entries of pair j).
+//
+// Arranged for latency: the chunk's maximum score is formed first (one more
+// barrier), so every wave exponentiates against it and the waves' P.V sums
+// merge by plain addition, with no rescaling and no exponentials in the merge.
+// Q8_0 codes are converted with one sign-extending byte-select conversion
+// each, to the same values as the signed extraction.  (Converting them as
+// unsigned bytes and taking the bias out afterwards, as the M = 1 GEMV does,
+// loses bits to cancellation here: measured 4e-5 to 8e-5 against 1e-6 on the
+// logits.)  out(tid, acc, m, l) for tid < 64: the unnormalised partial.
+template <int NW>
+struct SmemQ {
+    __align__(16) float qs[D];
+    float wmax[NW], wl[NW];
+    __align__(16) float pbuf[NW][64];
+    __align__(16) float wacc[NW][D];
+};
+
+template <int KVT, int NW, class Out>
+__device__ __forceinline__ void chunk_q(SmemQ<NW>& sm, const Round<KVT>& R, float q0, float q1, float rc, float rs,
+                                        bool rot, int c0, int pos, float scale, Out&& out) {
+    static_assert(KVT == VLRF_KV_Q8_0 || KVT == VLRF_KV_F16, "Q8_0 / F16 caches");
+    constexpr bool Q8 = KVT == VLRF_KV_Q8_0;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int tg = lane >> 2, dg = lane & 3;
+    if (w == 0) {
+        float y0 = q0, y1 = q1;
+        if (rot) rope2(q0, q1, rc, rs, &y0, &y1);
+        if (lane < HALF) { sm.qs[lane] = y0; sm.qs[lane + HALF] = y1; }
+    }
+    __syncthreads();
+
+    // scores: lane = row c0 + 64w + lane (rows from pos on are masked)
+    const int t = c0 + w * 64 + lane;
+    const bool live = t < pos;
+    float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+#pragma unroll
+    for (int i = 0; i < D / 4; ++i) {
+        const float4 qv = *reinterpret_cast<const float4*>(&sm.qs[4 * i]);
+        float4 kf;
+        if constexpr (Q8) {
+            const uint4 kw = R.k[i >> 2];
+            kf = s8f4((i & 3) == 0 ? kw.x : (i & 3) == 1 ? kw.y : (i & 3) == 2 ? kw.z : kw.w);
+        } else {
+            kf = row4<KVT>(R.k, i);
+        }
+        s0 += qv.x * kf.x;
+        s1 += qv.y * kf.y;
+        s2 += qv.z * kf.z;
+        s3 += qv.w * kf.w;
+    }
+    const float sc = live ? ((s0 + s1) + (s2 + s3)) * R.ks * scale : kNegInf;
+    const float wm = wave_max(sc);
+    if (lane == 0) sm.wmax[w] = wm;
+    __syncthreads();
+    float M = sm.wmax[0];
+#pragma unroll
+    for (int k = 1; k < NW; ++k) M = fmaxf(M, sm.wmax[k]);
+    const float pe = live ? expf(sc - M) : 0.f;
+    const float lw = wave_sum(pe);
+    sm.pbuf[w][lane] = pe * R.vs;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // P.V: lane (tg, dg) over rows tg + 16j of the wave, dims 16dg..16dg+15
+    float acc[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float pp = sm.pbuf[w][tg + 16 * j];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float4 v4;
+            if constexpr (Q8) {
+                const uint4 vw = R.v[j][0];
+                v4 = s8f4(i == 0 ? vw.x : i == 1 ? vw.y : i == 2 ? vw.z : vw.w);
+            } else {
+                v4 = row4<KVT>(R.v[j], i);
+            }
+            acc[4 * i] += pp * v4.x;
+            acc[4 * i + 1] += pp * v4.y;
+            acc[4 * i + 2] += pp * v4.z;
+            acc[4 * i + 3] += pp * v4.w;
+        }
+    }
+    // sum over the 16 lanes tg of dim group dg: rotations by 4 and 8 within a
+    // 16-lane row (DPP row_ror), then the row and half exchanges
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        float v = acc[e];
+        v += dpp_f<0x124>(v);
+        v += dpp_f<0x128>(v);
+        float2 x = swap_rows16(v, v);
+        v = x.x + x.y;
+        x = swap_halves32(v, v);
+        acc[e] = x.x + x.y;
+    }
+    if (tg == 0) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) sm.wacc[w][16 * dg + e] = acc[e];
+    }
+    if (lane == 0) sm.wl[w] = lw;
+    __syncthreads();
+    if (tid < D) {
+        float ot = 0.f, lt = 0.f;
+#pragma unroll
+        for (int k = 0; k < NW; ++k) {
+            ot += sm.wacc[k][tid];
+            lt += sm.wl[k];
+        }
+        out(tid, ot, M, lt);
     }
 }
 

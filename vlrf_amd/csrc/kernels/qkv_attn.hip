@@ -202,7 +202,7 @@ __global__ __launch_bounds__(gemv::kGemvThreads) __attribute__((amdgpu_waves_per
     // once and then from that L2; placement only affects speed.  The token's
     // own row is left out (the new-row workgroup writes it meanwhile) and
     // enters the O projection's merge as one more partial.
-    __shared__ attn::Smem<8> sm;
+    __shared__ attn::SmemQ<8> sm;
     __shared__ int oks[gemv::kGemvWaves];
     const DecodeFuse& fz = P.fz;
     const int ab = b - P.nq, rep = P.rep, nch = fz.nch, nparts = nch + 1;
@@ -216,7 +216,6 @@ __global__ __launch_bounds__(gemv::kGemvThreads) __attribute__((amdgpu_waves_per
     attn::Round<KVT> R;
     attn::load_round<KVT>(R, fz.kq_w, fz.vq_w, fz.ks_w, fz.vs_w, hb, c0 + w * 64, cap, lane);
     const int pos = min(P.state[1], cap - 1);   // the host checks capacity before queuing
-    const int ctx = pos + 1;
     attn::NewRow nr;
     attn::rope_row(nr, fz, pos);
     issue_before_wait();
@@ -237,12 +236,11 @@ __global__ __launch_bounds__(gemv::kGemvThreads) __attribute__((amdgpu_waves_per
     if (w == 0) ok = poll_direct<2, u32x2>(c, off, use, v);
     if (!block_ok(ok, oks)) return;
     const bool rot = pos < fz.max_seq;   // rope.hpp:84: positions >= max_seq stay unrotated
-    attn::chunk<KVT, true, 8>(sm, R, __uint_as_float(v[0].x), __uint_as_float(v[1].x), nr, false, false, g, c0,
-                              cap, hb, ctx, pos, rot, false, P.scale, fz,
-                              [&](int t, float ot, float mt, float lt) {   // the chunk's partial, unnormalised
-                                  pp[t] = ot;
-                                  if (t == 0) { pp[attn::D] = mt; pp[attn::D + 1] = lt; }
-                              });
+    attn::chunk_q<KVT, 8>(sm, R, __uint_as_float(v[0].x), __uint_as_float(v[1].x), nr.rc, nr.rs, rot, c0, pos,
+                          P.scale, [&](int t, float ot, float mt, float lt) {   // the chunk's partial, unnormalised
+                              pp[t] = ot;
+                              if (t == 0) { pp[attn::D] = mt; pp[attn::D + 1] = lt; }
+                          });
 }
 
 int qkv_chunks(int w_dtype, int K) {
