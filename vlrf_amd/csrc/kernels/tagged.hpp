@@ -97,18 +97,19 @@ __device__ inline bool poll(const Ctl& c, const int (&off)[N], const bool (&use)
 }
 
 // Polls until every used piece of the wave is valid, re-reading all of them
-// (for waves that read few words: no gate).  False when the wait ran out
+// (for waves that read few words: no gate).  The clock is read after every
+// failed pass, the failure flag (a memory round trip of its own) after every
+// 8th, so a pass costs one round trip.  False when the wait ran out
 // (recorded) or another workgroup failed.
 template <int N, class VT>
 __device__ inline bool poll_direct(const Ctl& c, const int (&off)[N], const bool (&use)[N], VT (&v)[N]) {
-    for (;;) {
+    for (int it = 1;; ++it) {
         if (poll_pass<N, VT>(c, off, use, v)) return true;
-        if (__hip_atomic_load(c.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return false;
         if (wall_clock64() - c.t0 > c.limit) {
             fail(c);
             return false;
         }
-        __builtin_amdgcn_s_sleep(1);
+        if ((it & 7) == 0 && __hip_atomic_load(c.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return false;
     }
 }
 
