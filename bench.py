@@ -17,14 +17,26 @@ WRITE_SIZE passes over `bench.py --roofline-only`, each scaled by the same
 counter on a plain 256 MiB device copy), read from the committed summary
 profiles/gemv_swiglu_q8_1b_pmc.txt; null when that file is absent.
 
+step_kernels: the step's time per kernel (the fused QKV + attention launch,
+O, gate/up, down, LM head, argmax) at the timed contexts, read from the
+committed rocprofv3 trace of the same workload
+(profiles/decode_step_llama1b_{q8,q4}_kernel_stats.md, the last 128 steps'
+dispatches; made with `--summarize-trace`), with each kernel's algorithmic
+bytes at context 2112 and the GB/s and fraction of peak they imply: the
+metric's attention + GEMV breakdown.  (HIP events cannot separate a step's
+launches: an event between two launches adds more than some kernels take.)
+
 cpu_baseline: the oracle's restatement of the reference decode step
 (oracle/vlrf_oracle.c: f32 decoded weights, AVX2 streaming GEMV, full-cache
-dequant, per-head flash attention) on the host's cores at context 2048.
+dequant, per-head flash attention) at context 2048 on every hardware thread
+of the process's CPU set (nproc and the CPU model in the line), up to 32
+steps within about 20 s.
 
     python bench.py [--gpus 1] [--steps 128] [--warmup 8] [--dtype q8_0|q4_0]
     python bench.py --roofline-only     # copy calibration + roofline launches only
     python bench.py --prefill           # config 5: one Llama-8B-shape layer, T=2048 prefill
     python bench.py --configs           # configs 1-3: kernel-level GB/s, one JSON line each
+    python bench.py --summarize-trace run_kernel_trace.csv --steps 128 --launches-per-step 90
 
 --prefill prints its own line: one Llama-8B-shape
 layer (hidden 4096, 32/8 heads, head_dim 128, FFN 14336 SwiGLU, Q8_0 weights)
@@ -263,14 +275,100 @@ def configs_bench(V, F):
         print(json.dumps(line), flush=True)
 
 
-def cpu_baseline(cfg, f32w, ctx_len, budget_s=12.0, max_steps=8):
-    """Oracle decode steps at context ctx_len on the host cores."""
+def weight_bytes(dtype, rows, cols):
+    """Device bytes of a quantized weight: codes plus one f16 scale per 32."""
+    codes = rows * cols if dtype == 8 else rows * cols // 2
+    return codes + rows * (cols // 32) * 2
+
+
+# Launch kinds of a decode step, in launch order (vlrf_hip_model_step_profile).
+STEP_KINDS = ("qkv_attn", "o_proj", "gate_up", "down")
+
+
+def kernel_bytes(cfg, dtype, ctx_len, nparts):
+    """Algorithmic HBM bytes per launch of each kind at context ctx_len: the
+    weights once, the cache rows attention reads, activations in and out."""
+    D, Fd, H, G = cfg["d_model"], cfg["d_ff"], cfg["n_heads"], cfg["n_kv_heads"]
+    dh = D // H
+    dkv, V_ = G * dh, cfg["vocab_size"]
+    part = H * nparts * 68 * 4
+    kv_read = ctx_len * dkv * 2 + ctx_len * 4 * 2          # K and V codes + row scales
+    return {
+        "qkv_attn": weight_bytes(dtype, D + 2 * dkv, D) + kv_read + D * 8 + 2 * dkv + 8 + part,
+        "o_proj": weight_bytes(dtype, D, D) + part + D * 8,
+        "gate_up": 2 * weight_bytes(dtype, Fd, D) + D * 8 + Fd * 4,
+        "down": weight_bytes(dtype, D, Fd) + Fd * 4 + D * 8,
+        "lm_head": weight_bytes(dtype, V_, D) + D * 8 + V_ * 4,
+        "argmax": V_ * 4,
+    }
+
+
+KERNEL_KINDS = (  # (kind, pattern in the profile's kernel name)
+    ("qkv_attn", "qkv_attn_kernel<"),
+    ("o_proj", ", false, 28>"),
+    ("gate_up", ", true, 17>"),
+    ("down", ", false, 20>"),
+    ("lm_head", ", false, 1>"),
+    ("argmax", "argmax_step_kernel"),
+)
+
+
+def step_kernels(cfg, dtype, wname):
+    """Per-kernel time and algorithmic GB/s of the timed steps, from the
+    committed rocprofv3 kernel trace of the same workload
+    (profiles/decode_step_llama1b_{q8,q4}_kernel_stats.md: the last 128 steps'
+    dispatches, the steps queued without the graph so the tracer sees each
+    launch).  Event timing cannot separate the launches of a step: an event
+    between two launches adds more than some of the kernels take."""
+    path = os.path.join(ROOT, "profiles", f"decode_step_llama1b_{wname[:2]}_kernel_stats.md")
+    if not os.path.exists(path):
+        return None
+    calls, avg = {}, {}
+    for line in open(path):
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) < 7 or not cells[1].replace(".", "").isdigit():
+            continue
+        for kind, pat in KERNEL_KINDS:
+            if pat in cells[0]:
+                n, us = float(cells[1]), float(cells[2])
+                calls[kind] = calls.get(kind, 0.0) + n
+                avg[kind] = avg.get(kind, 0.0) + n * us
+    if not calls:
+        return None
+    ctx_mid = 2048 + 64
+    nparts = (cfg["max_seq_len"] + 511) // 512 + 1
+    nb = kernel_bytes(cfg, dtype, ctx_mid, nparts)
+    out = {}
+    for kind, _ in KERNEL_KINDS:
+        if kind not in calls:
+            continue
+        us = avg[kind] / calls[kind]
+        gbs = nb[kind] / (us * 1e-6) / 1e9
+        out[kind] = {"us": round(us, 3), "bytes": int(nb[kind]), "GB/s": round(gbs, 1),
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "calls_per_step": round(calls[kind], 2)}
+    return {"kernels": out, "source": os.path.relpath(path, ROOT),
+            "bytes_at_ctx": ctx_mid}
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(cfg, f32w, ctx_len, budget_s=20.0, max_steps=32):
+    """Oracle decode steps at context ctx_len on every hardware thread the
+    process may use."""
     import oracle
     try:
         ncpu = len(os.sched_getaffinity(0))
     except AttributeError:
         ncpu = os.cpu_count() or 1
-    threads = max(1, min(16, ncpu))
+    threads = max(1, ncpu)
     om = oracle.Model(cfg, f32w, n_threads=threads)
     om.reset()
     om.fill_kv(ctx_len - 1, seed=7)
@@ -285,9 +383,38 @@ def cpu_baseline(cfg, f32w, ctx_len, budget_s=12.0, max_steps=8):
     dt = time.perf_counter() - t0
     del om
     return {"value": round(n / dt, 3), "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"{n} decode steps of the 1.1B f32-decoded model at context {ctx_len}-"
-                      f"{ctx_len + n} (oracle restatement, {threads} threads, KV cache filled "
-                      f"with seeded codes instead of a CPU prefill)"}
+            "nproc": os.cpu_count(), "cpu": cpu_model(),
+            "sample": f"{n} decode steps (of the 128 timed on the GPU) of the 1.1B f32-decoded model at "
+                      f"context {ctx_len}-{ctx_len + n} (oracle restatement, {threads} threads = every "
+                      f"hardware thread of the process's CPU set, KV cache filled with seeded codes "
+                      f"instead of a CPU prefill)"}
+
+
+def summarize_trace(path, steps, per_step):
+    """The last `steps` decode steps of a rocprofv3 kernel trace (CSV): the
+    runtime's own copy and fill kernels left out, the remaining dispatches
+    taken from the end, steps x per_step of them; per-kernel average
+    duration and time per step, as markdown."""
+    import csv
+    rows = [r for r in csv.DictReader(open(path)) if not r["Kernel_Name"].startswith("__amd_rocclr")]
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    tail = rows[-steps * per_step:]
+    agg = {}
+    for r in tail:
+        d = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        name = r["Kernel_Name"]
+        agg.setdefault(name, []).append(d)
+    span = (int(tail[-1]["End_Timestamp"]) - int(tail[0]["Start_Timestamp"])) / 1e3
+    total = sum(sum(v) for v in agg.values())
+    print(f"{len(tail)} dispatches = {steps} steps x {per_step}; span {span / steps:.1f} us/step, "
+          f"kernel time {total / steps:.1f} us/step\n")
+    print("| kernel | calls/step | avg us | min us | max us | us/step | % |")
+    print("|---|---:|---:|---:|---:|---:|---:|")
+    for name, v in sorted(agg.items(), key=lambda kv: -sum(kv[1])):
+        short = name.replace("void ", "").replace("vlrf_hip::(anonymous namespace)::", "")
+        short = short.split("(")[0]
+        print(f"| {short} | {len(v) / steps:.2f} | {np.mean(v):.2f} | {np.min(v):.2f} | {np.max(v):.2f} | "
+              f"{sum(v) / steps:.1f} | {100 * sum(v) / total:.1f} |")
 
 
 def main():
@@ -300,6 +427,9 @@ def main():
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-roofline", action="store_true")
+    ap.add_argument("--summarize-trace", metavar="CSV",
+                    help="print a markdown table of a rocprofv3 kernel trace's last --steps steps")
+    ap.add_argument("--launches-per-step", type=int, default=90)
     ap.add_argument("--roofline-only", action="store_true",
                     help="run the copy calibration and the roofline launches only (PMC passes)")
     ap.add_argument("--prefill", action="store_true",
@@ -308,6 +438,10 @@ def main():
     ap.add_argument("--configs", action="store_true",
                     help="configs 1-3: kernel-level GB/s of attention and quantized linear")
     a = ap.parse_args()
+
+    if a.summarize_trace:
+        summarize_trace(a.summarize_trace, a.steps, a.launches_per_step)
+        return
 
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path; "
@@ -386,6 +520,9 @@ def main():
                           "peak": HBM_PEAK_GBS, "unit": "GB/s",
                           "frac": round(step_gbs / HBM_PEAK_GBS, 4)},
     }
+    kernels = step_kernels(cfg, dtype, a.dtype)
+    if kernels:
+        out["step_kernels"] = kernels
     del model
     if not a.no_roofline:
         out["roofline"] = gemv_roofline(ctx, V, F, cfg, dtype)

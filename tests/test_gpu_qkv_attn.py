@@ -132,3 +132,4 @@ def test_fused_wait_timeout_is_reported(ctx, orc):
         last = om.forward([last])
         ref.append(last)
     assert list(gpu) == ref
+
