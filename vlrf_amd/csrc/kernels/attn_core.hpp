@@ -443,21 +443,45 @@ __device__ __forceinline__ void chunk_q(SmemQ<NW>& sm, const Round<KVT>& R, floa
             acc[4 * i + 3] += pp * v4.w;
         }
     }
-    // sum over the 16 lanes tg of dim group dg: rotations by 4 and 8 within a
-    // 16-lane row (DPP row_ror), then the row and half exchanges
+    // Sum over the 16 lanes tg of dim group dg as a reduce-scatter: each
+    // exchange halves the values a lane holds, so 15 exchanges replace 64.
+    // Lane bits (t3 t2 | t1 t0 d1 d0), tg = t3t2t1t0: rows of 16 lanes differ
+    // in t3t2.  (1) rows t2=0/1 swap halves of acc (permlane16): lanes keep
+    // dims 8*t2 + [0,8); (2) halves t3=0/1 (permlane32): 4*t3 + [0,4); (3)
+    // lanes t1=0/1, 8 apart in a row (DPP rotate by 8): 2*t1 + [0,2); (4)
+    // lanes t0=0/1, 4 apart (rotate by 4 one way, 12 the other): t0.  The lane
+    // then holds dim 16*dg + 8*t2 + 4*t3 + 2*t1 + t0, summed over tg.
+    {
+        const int t0 = tg & 1, t1 = (tg >> 1) & 1, t2 = (tg >> 2) & 1, t3 = tg >> 3;
+        float v1[8];
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-        float v = acc[e];
-        v += dpp_f<0x124>(v);
-        v += dpp_f<0x128>(v);
-        float2 x = swap_rows16(v, v);
-        v = x.x + x.y;
-        x = swap_halves32(v, v);
-        acc[e] = x.x + x.y;
-    }
-    if (tg == 0) {
+        for (int e = 0; e < 8; ++e) {
+            const float2 x = swap_rows16(acc[e], acc[e + 8]);
+            v1[e] = x.x + x.y;
+        }
+        float v2[4];
 #pragma unroll
-        for (int e = 0; e < 16; ++e) sm.wacc[w][16 * dg + e] = acc[e];
+        for (int e = 0; e < 4; ++e) {
+            const float2 x = swap_halves32(v1[e], v1[e + 4]);
+            v2[e] = x.x + x.y;
+        }
+        float v3[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const float own = t1 ? v2[e + 2] : v2[e];
+            const float send = t1 ? v2[e] : v2[e + 2];
+            v3[e] = own + dpp_f<0x128>(send);
+        }
+        const float own = t0 ? v3[1] : v3[0];
+        const float send = t0 ? v3[0] : v3[1];
+        // row_ror:N reads lane (p - N) mod 16: rotate by 12 reaches p + 4, by 4
+        // p - 4.  Both rotations run on every lane and a bit mask picks one: a
+        // rotation left to a branch would run with its source lanes switched
+        // off and read zeros.
+        const float g4 = dpp_f<0x124>(send), g12 = dpp_f<0x12C>(send);
+        const int pick = -t0;
+        const float got = __int_as_float((__float_as_int(g4) & pick) | (__float_as_int(g12) & ~pick));
+        sm.wacc[w][16 * dg + 8 * t2 + 4 * t3 + 2 * t1 + t0] = own + got;
     }
     if (lane == 0) sm.wl[w] = lw;
     __syncthreads();
