@@ -50,3 +50,47 @@ def test_adapter_on_device_matches_reference_engine():
               "F32-derived weights uploaded as F32 / LM head F32", "forcing Q8_0 on f32 weights is refused"):
         assert "PASS decode: " + w in p.stdout, (w, p.stdout)
     assert "FAIL" not in p.stdout
+
+
+ENGINE = os.path.join(ROOT, "oracle", "_ref", "engine_hip")
+
+
+def _engine_model(tmp_path):
+    """A tiny Llama-style checkpoint as the engine loads it: an NFW v2 file
+    (the engine's WeightMap reads versions 1-2: f32 tensors, the projections
+    the decoded values of Q8_0 blocks, as the converter leaves them; zero
+    attention biases as converted checkpoints carry) with config.json beside
+    it."""
+    import json
+    import numpy as np
+    from vlrf_amd import formats as F
+    from vlrf_amd import nfw
+    cfg = F.tiny(F.DT_Q8_0, n_layers=2, max_seq_len=160)
+    tensors = {}
+    for name, rows, cols, kind in F.tensor_specs(cfg):
+        payload, dec = F.make_tensor(71, name, rows, cols, kind, F.DT_Q8_0, 0.1)
+        tensors[name] = dec.reshape(rows, cols) if rows > 1 else dec
+    tensors["layers.0.attn.q_proj.bias"] = np.zeros(cfg["d_model"], np.float32)
+    path = tmp_path / "model.nfw"
+    nfw.write_nfw(path, tensors, version=2)
+    conf = {k: cfg[k] for k in ("vocab_size", "d_model", "d_ff", "n_heads", "n_kv_heads", "n_layers", "max_seq_len")}
+    conf.update(layer_norm_eps=cfg["norm_eps"], rope_theta=cfg["rope_theta"], pre_norm=True, use_rms_norm=True,
+                tie_embeddings=False, pos_embedding="rotary", activation="silu", bos_token_id=1, eos_token_id=2)
+    (tmp_path / "config.json").write_text(json.dumps(conf))
+    return path
+
+
+@pytest.mark.gpu
+def test_engine_c_api_selects_the_hip_backend(tmp_path):
+    """The engine's own C API with the integration patch applied
+    (oracle/_ref/engine_hip, built by oracle/Makefile `engine` from the
+    reference's src/api/vlrf_api.cpp): vlrf_set_backend(VLRF_BACKEND_HIP) +
+    vlrf_generate_ids return the CPU backend's ids (F32 and Q8_0 KV caches,
+    and a request past max_seq_len)."""
+    if not os.path.exists(ENGINE):
+        pytest.skip("oracle/_ref/engine_hip not built (needs the reference tree)")
+    print("[case] engine C API with the HIP backend", flush=True)
+    p = subprocess.run([ENGINE, str(_engine_model(tmp_path))], capture_output=True, text=True, timeout=300)
+    print(p.stdout, p.stderr, flush=True)
+    assert p.returncode == 0, p.stdout + p.stderr
+    assert p.stdout.count("PASS engine vlrf_generate_ids, HIP backend == CPU backend") == 3, p.stdout

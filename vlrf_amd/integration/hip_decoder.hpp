@@ -10,7 +10,8 @@
 // eos_token_id (hit_eos) or when on_token returns false, with only token ids
 // crossing PCIe.  Supported: pre-norm Llama-style models (use_rms_norm, SiLU
 // with `ffn.gate.weight`, ROTARY, untied LM head or tied embeddings), no
-// biases, default MuP multipliers, F32/F16/Q8_0 KV cache.
+// biases (all-zero ones, as converted checkpoints carry, are accepted),
+// default MuP multipliers, F32/F16/Q8_0 KV cache.
 //
 // Weights: the device runs exactly the engine's weights.  A projection is
 // uploaded as Q4_0 or Q8_0 blocks only when encoding and decoding the tensor
@@ -41,7 +42,8 @@ public:
 
     HipDecoder(vlrf_hip_ctx_t ctx, ModelConfig const& c, WeightMap& wm, int weight_dtype = kAuto,
                bool allow_lossy = false)
-        : ctx_(ctx), vocab_(c.vocab_size), max_seq_(c.max_seq_len), eos_(c.eos_token_id), bos_(c.bos_token_id) {
+        : ctx_(ctx), vocab_(c.vocab_size), max_seq_(c.max_seq_len), eos_(c.eos_token_id), bos_(c.bos_token_id),
+          kv_dtype_(c.kv_cache_dtype) {
         if (!c.use_rms_norm || c.activation != Activation::SILU ||
             c.pos_embedding != PosEmbedding::ROTARY || !c.pre_norm || c.embedding_multiplier != 1.f ||
             c.attention_multiplier != 0.f || c.residual_multiplier != 1.f || c.logits_scaling != 1.f ||
@@ -57,9 +59,12 @@ public:
             const std::string p = "layers." + std::to_string(l) + ".";
             if (!wm.has(p + "ffn.gate.weight"))
                 throw std::runtime_error("HipDecoder: SwiGLU gate weight missing in layer " + std::to_string(l));
+            // Converted checkpoints carry zero biases (convert_gguf.py); those add
+            // nothing, any other bias is refused.
             for (const char* b : {"attn.q_proj.bias", "attn.k_proj.bias", "attn.v_proj.bias", "attn.o_proj.bias",
                                   "ffn.fc1.bias", "ffn.fc2.bias", "ffn.gate.bias"})
-                if (wm.has(p + b)) throw std::runtime_error(std::string("HipDecoder: biases unsupported: ") + p + b);
+                if (wm.has(p + b) && !all_zero(wm.get(p + b)))
+                    throw std::runtime_error(std::string("HipDecoder: non-zero bias unsupported: ") + p + b);
             for (const char* k : {"attn.q_proj.weight", "attn.k_proj.weight", "attn.v_proj.weight",
                                   "attn.o_proj.weight", "ffn.gate.weight", "ffn.fc1.weight", "ffn.fc2.weight"})
                 proj.push_back(p + k);
@@ -154,6 +159,14 @@ public:
         return r;
     }
 
+    // Whether this decoder still fits the engine's config: the KV cache dtype
+    // and length (vlrf_set_kv_cache_type / vlrf_set_ctx change them in place)
+    // and the token ids generate() stops or starts at.
+    bool matches(ModelConfig const& c) const {
+        return c.kv_cache_dtype == kv_dtype_ && c.max_seq_len == max_seq_ && c.eos_token_id == eos_ &&
+               c.bos_token_id == bos_ && c.vocab_size == vocab_;
+    }
+
     // The dtypes chosen for the layer projections and the LM head.
     int layer_dtype() const { return layer_dtype_; }
     int lm_head_dtype() const { return lm_dtype_; }
@@ -168,6 +181,12 @@ public:
 private:
     static void check(int rc) {
         if (rc != VLRF_HIP_OK) throw std::runtime_error(std::string("vlrf_hip: ") + vlrf_hip_last_error());
+    }
+    static bool all_zero(Tensor& t) {
+        const float* v = t.data_ptr();
+        for (int64_t i = 0; i < t.numel(); ++i)
+            if (v[i] != 0.f) return false;
+        return true;
     }
     static size_t block_bytes(int dt) { return dt == VLRF_DT_Q8_0 ? 34 : 18; }
     static void encode(Tensor& t, int dt, std::vector<unsigned char>& blocks) {
@@ -208,7 +227,7 @@ private:
     vlrf_hip_ctx_t ctx_;
     vlrf_hip_model_t m_ = nullptr;
     int vocab_;
-    int max_seq_, eos_, bos_;
+    int max_seq_, eos_, bos_, kv_dtype_;
     int layer_dtype_ = VLRF_DT_F32, lm_dtype_ = VLRF_DT_F32;
 };
 
