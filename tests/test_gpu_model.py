@@ -114,3 +114,32 @@ def test_argmax_ties_take_the_lowest_index(ctx):
         k = int(np.argmax(gl))
         assert k < P and gl[k + P] == gl[k] and gl[nv - P + (k - nv % P) % P] == gl[k]
         assert g_next == k
+
+
+@pytest.mark.parametrize("dtype", [V.DT_Q8_0, V.DT_Q4_0])
+def test_llama8b_layer_decode(ctx, orc, dtype):
+    """The decode step at the 8B shape (hidden 4096, 32/8 heads, d_head 128,
+    FFN 14336: the down projection's 14336-wide rows take the wide M = 1
+    GEMV), one layer, vocabulary 256: greedy stream identical to the
+    oracle's and teacher-forced logits within 1e-3."""
+    cfg = F.llama8b_layer(dtype, max_seq_len=96, n_layers=1, vocab_size=256)
+    print(f"[case] 8B-shape layer decode dtype={dtype}", flush=True)
+    m, om, _ = _models(ctx, orc, cfg, 23)
+    prompt = F.tokens(23, "prompt", 24, cfg["vocab_size"])
+    gpu = m.generate(prompt, 16)
+    om.reset()
+    om.forward(prompt)
+    last, ref = int(prompt[-1]), []
+    for _ in range(16):
+        last = om.forward([last])
+        ref.append(last)
+    assert list(gpu) == ref
+    m.reset()
+    om.reset()
+    worst = 0.0
+    for t in F.tokens(23, "feed", 12, cfg["vocab_size"]):
+        _, gl = m.step(int(t), want_logits=True)
+        _, ol = om.forward([int(t)], want_logits=True)
+        worst = max(worst, rel_err(gl, ol))
+    print(f"  teacher-forced logits: worst rel err {worst:.2e}", flush=True)
+    assert worst <= 1e-3, worst

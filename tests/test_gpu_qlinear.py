@@ -35,6 +35,24 @@ def test_config3_qlinear(ctx, orc, dtype, N, K, M):
     np.testing.assert_allclose(y, ref, rtol=1e-3, atol=1e-5 * np.abs(ref).max())
 
 
+@pytest.mark.parametrize("dtype", [V.DT_Q8_0, V.DT_Q4_0])
+@pytest.mark.parametrize("N,K", [(4096, 14336), (300, 14336), (37, 6176)])
+def test_m1_wide_rows(ctx, orc, dtype, N, K):
+    """M = 1 over rows wider than the general staging (K > 6144, up to the
+    8B shape's d_ff 14336): plain and with the residual added."""
+    print(f"[case] wide M=1 dtype={dtype} N={N} K={K}", flush=True)
+    w, dec = _weight(ctx, 11, f"W{N}x{K}", N, K, dtype)
+    x = F.normal(11, "xw", K).reshape(1, K)
+    res = F.normal(11, "rw", N).reshape(1, N)
+    dx, dy = ctx.to_device(x), ctx.alloc(N * 4)
+    ctx.qlinear(w, dx, dy, 1)
+    ref = orc.linear(x, dec)
+    assert rel_err(dy.download((1, N)), ref) <= 1e-3
+    dr = ctx.to_device(res)
+    ctx.qlinear(w, dx, dr, 1, residual=dr)
+    assert rel_err(dr.download((1, N)), ref + res) <= 1e-3
+
+
 @pytest.mark.parametrize("M", [1, 3, 9])
 @pytest.mark.parametrize("N,K", [(37, 64), (300, 96), (8, 1056)])
 def test_qlinear_ragged_shapes(ctx, orc, M, N, K):

@@ -36,6 +36,9 @@ struct Gemv<VLRF_DT_Q4_0> { static constexpr int EPL = 32; static constexpr floa
 
 constexpr float kNegInfF = -INFINITY;
 constexpr int kGemvMaxK = 6144;          // staged activations: 24 KiB of LDS
+// Plain and residual forms with one row per wave also take the d_ff-wide
+// rows of an 8B-shape down projection (56 KiB of LDS, two workgroups a CU).
+constexpr int kGemvWideMaxK = 14336;
 constexpr int kGemvMaxGroups = 512;      // workgroups of the row loop (2 per CU)
 constexpr int kGemvMaxOneGroups = 768;   // one row per wave up to 3 workgroups per CU
 constexpr int kGemvWaves = 8;            // waves per workgroup (one staged copy of x)

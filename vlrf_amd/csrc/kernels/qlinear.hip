@@ -199,6 +199,20 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(
                                               });
 }
 
+// The wide-row form (K up to kGemvWideMaxK, one row per wave) held to 128
+// VGPRs, so that two workgroups share a CU: an 8B-shape down projection's
+// 512 workgroups then run in one pass over the 256 CUs.
+template <int WT, int NC, int XM>
+__global__ __launch_bounds__(64 * kGemvWaves) __attribute__((amdgpu_waves_per_eu(4))) void gemv_wide_kernel(
+    const uint8_t* __restrict__ qa, const __half* __restrict__ da, int N, int K, const float* __restrict__ x,
+    const float* residual, float* y) {
+    gemv::gemv_body<WT, NC, 1, false, XM>(qa, da, nullptr, nullptr, N, K, x, nullptr, nullptr, nullptr, 0.f, 0,
+                                          blockIdx.x, gridDim.x, [&](int row, float out) {
+                                              if constexpr ((XM & 4) != 0) out = out + residual[row];
+                                              y[row] = out;
+                                          });
+}
+
 template <int WT, bool SWIGLU>
 int launch_gemv(hipStream_t s, const DevWeight& a, const DevWeight* b, const float* x, float* y,
                 const float* norm_w, float eps, const float* residual, const int* x_row = nullptr,
@@ -246,10 +260,24 @@ int launch_gemv(hipStream_t s, const DevWeight& a, const DevWeight* b, const flo
         VH_GEMV(2, 1);
     } else if (nc <= 3) {
         VH_GEMV(3, 1);
-    } else {
+    } else if (WT == VLRF_DT_Q8_0 && nc <= 6) {
         // Q4_0 chunks are 2048 wide, so K <= kGemvMaxK needs at most 3 of them.
-        VH_ARG(WT == VLRF_DT_Q8_0 && nc <= 6, "gemv: K %d too large for the M=1 path", a.K);
         if constexpr (WT == VLRF_DT_Q8_0) VH_GEMV(6, 1);
+    } else {
+        // Wide rows (K <= kGemvWideMaxK): one row per wave, plain or with the
+        // residual, one register set (14 / 7 chunks of 16 bytes per lane).
+        constexpr int NCW = WT == VLRF_DT_Q8_0 ? 14 : 7;
+        VH_ARG(!SWIGLU && nc <= NCW && (xm == 16 || xm == 20), "gemv: K %d too large for the M=1 path (form %d)",
+               a.K, xm);
+        if constexpr (!SWIGLU) {
+            const dim3 grid((a.N + kGemvWaves - 1) / kGemvWaves);
+            if (xm == 16)
+                hipLaunchKernelGGL((gemv_wide_kernel<WT, NCW, 16>), grid, dim3(64 * kGemvWaves), 0, s, a.q, a.d, a.N,
+                                   a.K, x, residual, y);
+            else
+                hipLaunchKernelGGL((gemv_wide_kernel<WT, NCW, 20>), grid, dim3(64 * kGemvWaves), 0, s, a.q, a.d, a.N,
+                                   a.K, x, residual, y);
+        }
     }
 #undef VH_GEMV
 #undef VH_GEMV_XM
@@ -257,9 +285,16 @@ int launch_gemv(hipStream_t s, const DevWeight& a, const DevWeight* b, const flo
     return VLRF_HIP_OK;
 }
 
-// The LDS-staged GEMV covers K up to kGemvMaxK columns.
+// The LDS-staged GEMV covers K up to kGemvMaxK columns in every form.
 bool gemv_fits(const DevWeight& w) {
     return (w.dtype == VLRF_DT_Q8_0 || w.dtype == VLRF_DT_Q4_0) && w.K <= kGemvMaxK;
+}
+
+// ... and up to kGemvWideMaxK in the plain / residual forms with one row per
+// wave (N <= 8 * kGemvMaxOneGroups).
+bool gemv_wide_fits(const DevWeight& w) {
+    return (w.dtype == VLRF_DT_Q8_0 || w.dtype == VLRF_DT_Q4_0) && w.K <= gemv::kGemvWideMaxK &&
+           (w.N + kGemvWaves - 1) / kGemvWaves <= kGemvMaxOneGroups;
 }
 
 int check_weight(const DevWeight& w) {
@@ -280,7 +315,7 @@ int launch_qlinear(hipStream_t s, const DevWeight& w, const float* x, float* y, 
     if (rc) return rc;
     VH_ARG(M >= 1 && M <= 16, "qlinear: M=%d outside [1,16]", M);
     VH_ARG(x && y, "qlinear: null activation pointer");
-    if (M == 1 && gemv_fits(w)) {
+    if (M == 1 && (gemv_fits(w) || (!norm_w && gemv_wide_fits(w)))) {
         if (w.dtype == VLRF_DT_Q8_0) return launch_gemv<VLRF_DT_Q8_0, false>(s, w, nullptr, x, y, norm_w, eps, residual);
         return launch_gemv<VLRF_DT_Q4_0, false>(s, w, nullptr, x, y, norm_w, eps, residual);
     }
