@@ -35,6 +35,7 @@ steps within about 20 s.
     python bench.py [--gpus 1] [--steps 128] [--warmup 8] [--dtype q8_0|q4_0]
     python bench.py --roofline-only     # copy calibration + roofline launches only
     python bench.py --prefill           # config 5: one Llama-8B-shape layer, T=2048 prefill
+    python bench.py --decode-8b [--layers 4]   # decode at the 8B layer shape (d_head 128)
     python bench.py --configs           # configs 1-3: kernel-level GB/s, one JSON line each
     python bench.py --summarize-trace run_kernel_trace.csv --steps 128 --launches-per-step 90
 
@@ -417,6 +418,46 @@ def summarize_trace(path, steps, per_step):
               f"{sum(v) / steps:.1f} | {100 * sum(v) / total:.1f} |")
 
 
+def decode8b_bench(a, V, F):
+    """Decode at the Llama-8B layer shape (the d_head 128 path): `layers` layers
+    (hidden 4096, 32/8 heads, FFN 14336) + a 32000-row LM head, cache filled to
+    ctx by the MFMA prefill, then `steps` timed greedy steps; us per layer
+    includes the LM head's share."""
+    dtype = V.DT_Q8_0 if a.dtype == "q8_0" else V.DT_Q4_0
+    ctx = V.Context(0)
+    cfg = F.llama8b_layer(dtype, max_seq_len=a.ctx + a.warmup + a.steps + 8, n_layers=a.layers,
+                          vocab_size=32000)
+    m = V.Model(ctx, cfg)
+    F.load_model(m, a.seed)
+    prompt = F.tokens(a.seed, "bench8b.prompt", a.ctx, cfg["vocab_size"])
+    nxt = m.prefill_mfma(prompt)
+    if a.warmup:
+        nxt = int(m.generate_ids(nxt, a.warmup)[-1])
+    used = m.used
+    ctx.sync()
+    ctx.timer_start()
+    m.generate_async(nxt, a.steps)
+    ms = ctx.timer_stop()
+    step_bytes = [sum(m.step_bytes(used + i)) for i in range(a.steps)]
+    gbs = sum(step_bytes) / (ms / 1e3) / 1e9
+    return {
+        "metric": "decode us per layer at the Llama-8B shape",
+        "value": round(ms / a.steps / a.layers * 1e3, 2),
+        "unit": "us/layer",
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms / a.steps, 4),
+        "higher_is_better": False,
+        "dtype": f"f32 compute, {a.dtype} weights, q8_0 KV",
+        "data": "synthetic: seeded N(0,0.02) weights, random token ids",
+        "config": {"workload": "llama-8B-shape greedy decode, ctx %d->%d, batch 1" % (used, used + a.steps),
+                   "layers": a.layers, "hidden": 4096, "ffn": 14336, "heads": "32/8", "head_dim": 128,
+                   "vocab": 32000},
+        "step_roofline": {"bytes_per_step": int(np.mean(step_bytes)), "achieved": round(gbs, 1),
+                          "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4)},
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -435,6 +476,9 @@ def main():
     ap.add_argument("--prefill", action="store_true",
                     help="config 5: one Llama-8B-shape layer prefill on the matrix cores")
     ap.add_argument("--prefill-tokens", type=int, default=2048)
+    ap.add_argument("--decode-8b", action="store_true",
+                    help="decode at the Llama-8B layer shape (d_head 128), us per layer")
+    ap.add_argument("--layers", type=int, default=4, help="--decode-8b: layers of the model")
     ap.add_argument("--configs", action="store_true",
                     help="configs 1-3: kernel-level GB/s of attention and quantized linear")
     a = ap.parse_args()
@@ -453,6 +497,12 @@ def main():
 
     if a.configs:
         configs_bench(V, F)
+        return
+
+    if a.decode_8b:
+        if a.steps == 128:           # the 1.1B default; 32 steps of an 8B-shape model suffice
+            a.steps = 32
+        print(json.dumps(decode8b_bench(a, V, F)), flush=True)
         return
 
     if a.prefill:

@@ -143,3 +143,32 @@ def test_llama8b_layer_decode(ctx, orc, dtype):
         worst = max(worst, rel_err(gl, ol))
     print(f"  teacher-forced logits: worst rel err {worst:.2e}", flush=True)
     assert worst <= 1e-3, worst
+
+
+@pytest.mark.parametrize("n_heads,n_kv,dtype", [(8, 2, V.DT_Q8_0), (8, 8, V.DT_Q8_0), (8, 2, V.DT_Q4_0)])
+def test_head_dim_128_chunked_cache(ctx, orc, n_heads, n_kv, dtype):
+    """d_head 128 over a cache of three 512-row chunks (the chunked decode
+    attention with the token's key as its own partial, merged by the O
+    projection): a 1100-token prompt fed through the decode step, then a
+    greedy stream identical to the oracle's and teacher-forced logits within
+    1e-3 at contexts past the second chunk boundary."""
+    cfg = dict(vocab_size=256, d_model=128 * n_heads, d_ff=2048, n_heads=n_heads, n_kv_heads=n_kv, n_layers=2,
+               max_seq_len=1400, norm_eps=1e-5, rope_theta=10000.0, weight_dtype=dtype)
+    print(f"[case] d_head 128 chunked cache heads={n_heads}/{n_kv} dtype={dtype}", flush=True)
+    m, om, _ = _models(ctx, orc, cfg, 29)
+    prompt = F.tokens(29, "prompt", 1100, cfg["vocab_size"])
+    gpu = m.generate(prompt, 24)
+    om.reset()
+    om.forward(prompt)
+    last, ref = int(prompt[-1]), []
+    for _ in range(24):
+        last = om.forward([last])
+        ref.append(last)
+    assert list(gpu) == ref
+    worst = 0.0
+    for t in F.tokens(29, "feed", 8, cfg["vocab_size"]):
+        _, gl = m.step(int(t), want_logits=True)
+        _, ol = om.forward([int(t)], want_logits=True)
+        worst = max(worst, rel_err(gl, ol))
+    print(f"  teacher-forced logits at ctx {m.used}: worst rel err {worst:.2e}", flush=True)
+    assert worst <= 1e-3, worst

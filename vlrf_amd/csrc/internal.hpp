@@ -122,7 +122,7 @@ int launch_qlinear(hipStream_t s, const DevWeight& w, const float* x, float* y, 
 // chunked form (DecodeFuse::chunks, nch chunks per head), merged in the GEMV's
 // prologue.
 int launch_qlinear_merge(hipStream_t s, const DevWeight& w, const float* chunks, int nch, const float* residual,
-                         float* y);
+                         float* y, int head_dim = 64);
 // Most chunks launch_qlinear_merge takes for w (0: not on that path).
 int qlinear_merge_max_chunks(const DevWeight& w);
 int launch_qlinear_gather(hipStream_t s, const DevWeight& w, const float* table, const int* row,
@@ -213,6 +213,10 @@ constexpr int kAttnChunkRows = 512;   // cache rows per chunk of the chunked for
 // where it does not apply (d_head != 64, more than 8 KV heads, caches the
 // single-pass kernel covers, or more than kAttnMaxChunks chunks).
 int attn_decode_chunks(int cap, int d_head, int n_kv);
+// The d_head 128 chunked form (Q8_0 cache): nch chunks of 512 rows, whose
+// partials (acc[0..127], m, l; d_head + 4 floats) are followed by the new
+// key's, nch + 1 per head.  0 where it does not apply.
+int attn_decode_chunks128(int cap, int n_heads, int n_kv, int kv_dtype);
 
 // Split-K decode attention over K/V elements of kv_dtype (VLRF_KV_Q8_0 codes
 // with row scales ks/vs, VLRF_KV_F16 bits, VLRF_KV_F32) laid out

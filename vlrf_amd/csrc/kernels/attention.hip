@@ -882,6 +882,147 @@ __global__ __launch_bounds__(64) void attn_f32_tiled_kernel(const float* __restr
     }
 }
 
+// ---- chunked form at d_head 128 (Q8_0 cache) ---------------------------------------
+// The decode step's attention for 8B-shape heads: one workgroup per query
+// head and 512-row chunk of the cache (REP heads of a chunk on one XCD, as
+// above), each writing the unnormalised partial (acc[0..127], m, l) of the
+// rows before the token; one more workgroup (the last) rotates the token's K
+// row, quantizes the K and V rows into the cache (kv_cache.hpp:102-117) and
+// writes every head's partial of the new key (m = q.k_stored * scale, l = 1,
+// acc = v_stored) as partial nch, so the O projection's prologue merges the
+// chunks and then the new key: the order of the reference's online softmax
+// (attention.hpp:207-309), where the token's key comes last.
+constexpr int kChunkStride128 = attn::D128 + 4;
+
+struct NewRow128Smem {
+    __align__(16) float nk[8 * attn::D128];   // the stored K / V rows read back
+    __align__(16) float nv[8 * attn::D128];
+    float amax[2 * (kCH / 64)];
+};
+
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_f<0xB1>(v);    // quad_perm [1,0,3,2]
+    v += dpp_f<0x4E>(v);    // quad_perm [2,3,0,1]
+    v += dpp_f<0x141>(v);   // row_half_mirror
+    v += dpp_f<0x140>(v);   // row_mirror
+    return v;
+}
+
+__device__ void new_row128(const float* __restrict__ q, long head_stride, int pos, int n_heads, float scale,
+                           const DecodeFuse& fz, int nch) {
+    __shared__ NewRow128Smem sm;
+    constexpr int NT = kCH, W = kCH / 64, D = attn::D128, HALF = attn::HALF128;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int G = fz.n_kv, npairs = G * HALF, nrow = G * D, rep = n_heads / G, nparts = nch + 1;
+    const int trow = min(pos, fz.max_seq - 1);
+    const bool rot = pos < fz.max_seq;   // rope.hpp:84: positions >= max_seq stay unrotated
+    // thread t: K pair t (head t / 64, dims j and j + 64), V elements t and t + 512
+    const int kp = min(tid, npairs - 1), kh = kp / HALF, kj = kp - kh * HALF;
+    float k0 = fz.k_new[kh * D + kj], k1 = fz.k_new[kh * D + kj + HALF];
+    const float v0 = fz.v_new[min(tid, nrow - 1)], v1 = fz.v_new[min(tid + NT, nrow - 1)];
+    if (tid < npairs && rot)
+        attn::rope2(k0, k1, fz.cos_t[(size_t)trow * HALF + kj], fz.sin_t[(size_t)trow * HALF + kj], &k0, &k1);
+    const float ak_w = wave_max(tid < npairs ? fmaxf(fabsf(k0), fabsf(k1)) : 0.f);
+    float av_l = tid < nrow ? fabsf(v0) : 0.f;
+    if (tid + NT < nrow) av_l = fmaxf(av_l, fabsf(v1));
+    const float av_w = wave_max(av_l);
+    if (lane == 0) { sm.amax[w] = ak_w; sm.amax[W + w] = av_w; }
+    __syncthreads();
+    float ak = 0.f, av = 0.f;
+#pragma unroll
+    for (int k = 0; k < W; ++k) {
+        ak = fmaxf(ak, sm.amax[k]);
+        av = fmaxf(av, sm.amax[W + k]);
+    }
+    const float sk = ak != 0.f ? ak / 127.f : 0.f, sv = av != 0.f ? av / 127.f : 0.f;
+    const float ik = ak != 0.f ? 1.f / sk : 0.f, iv = av != 0.f ? 1.f / sv : 0.f;
+    if (tid < npairs) {
+        int8_t* krow = fz.kq_w + (size_t)kh * head_stride + (size_t)pos * D;
+        sm.nk[kh * D + kj] = attn::store_elem<VLRF_KV_Q8_0>(krow, kj, k0, sk, ik, ak != 0.f, true);
+        sm.nk[kh * D + kj + HALF] = attn::store_elem<VLRF_KV_Q8_0>(krow, kj + HALF, k1, sk, ik, ak != 0.f, true);
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int e = tid + u * NT;
+        if (e < nrow) {
+            const int vh = e / D, vj = e - vh * D;
+            int8_t* vrow = fz.vq_w + (size_t)vh * head_stride + (size_t)pos * D;
+            sm.nv[e] = attn::store_elem<VLRF_KV_Q8_0>(vrow, vj, u ? v1 : v0, sv, iv, av != 0.f, true);
+        }
+    }
+    if (tid == 0) { fz.ks_w[pos] = sk; fz.vs_w[pos] = sv; }
+    __syncthreads();
+    // Head hh's new-key score: 16 threads a head, 4 RoPE pairs each, summed
+    // over the 16-lane row.
+    for (int hh0 = 0; hh0 < n_heads; hh0 += NT / 16) {
+        const int hh = hh0 + tid / 16, sub = tid & 15;
+        const int hq = min(hh, n_heads - 1), g = hq / rep;
+        float a = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int j = 4 * sub + i;
+            float y0 = q[(size_t)hq * D + j], y1 = q[(size_t)hq * D + j + HALF];
+            if (rot)
+                attn::rope2(y0, y1, fz.cos_t[(size_t)trow * HALF + j], fz.sin_t[(size_t)trow * HALF + j], &y0, &y1);
+            a += y0 * sm.nk[g * D + j] + y1 * sm.nk[g * D + j + HALF];
+        }
+        a = row16_sum(a);
+        if (hh < n_heads && sub == 0) {
+            float* pp = fz.chunks + ((size_t)hh * nparts + nch) * kChunkStride128;
+            pp[D] = a * scale;
+            pp[D + 1] = 1.f;
+        }
+    }
+    for (int e = tid; e < n_heads * D; e += NT) {
+        const int hh = e / D, d = e - hh * D;
+        fz.chunks[((size_t)hh * nparts + nch) * kChunkStride128 + d] = sm.nv[(hh / rep) * D + d];
+    }
+}
+
+template <int REP>
+__global__ __launch_bounds__(kCH) void attn_chunk128_kernel(const float* __restrict__ q, const int8_t* kc,
+                                                            const int8_t* vc, const float* ks, const float* vs,
+                                                            long head_stride, const int* __restrict__ pos_dev,
+                                                            float scale, DecodeFuse fz, int nch, int na) {
+    constexpr int D = attn::D128, HALF = attn::HALF128, NW = kCH / 64;
+    const int b = blockIdx.x;
+    const int cap = (int)(head_stride / D);
+    if (b == na) {
+        new_row128(q, head_stride, min(*pos_dev, cap - 1), REP * fz.n_kv, scale, fz, nch);
+        return;
+    }
+    __shared__ attn::SmemQ128<NW> sm;
+    const int k = b >> 3, r = k % REP, pc = (b & 7) + 8 * (k / REP);
+    if (pc >= fz.n_kv * nch) return;
+    const int g = pc / nch, chunk = pc - g * nch, h = g * REP + r, c0 = chunk * kCH;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const size_t hb = (size_t)g * head_stride;
+    attn::Round128 R;
+    attn::load_round128(R, kc, vc, ks, vs, hb, c0 + w * 64, cap, lane);
+    float q0 = 0.f, q1 = 0.f;
+    if (w == 0) {
+        q0 = q[(size_t)h * D + lane];
+        q1 = q[(size_t)h * D + lane + HALF];
+    }
+    // The K/V loads stay above the device position's load and the exit below.
+    __builtin_amdgcn_sched_barrier(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    const int pos = min(*pos_dev, cap - 1);   // the host checks capacity before queuing
+    float* pp = fz.chunks + ((size_t)h * (nch + 1) + chunk) * kChunkStride128;
+    if (c0 >= pos) {   // no cache row before the token: the empty partial (acc 0, m -inf, l 0)
+        if (tid < D) pp[tid] = 0.f;
+        if (tid == 0) { pp[D] = attn::kNegInf; pp[D + 1] = 0.f; }
+        return;
+    }
+    const int trow = min(pos, fz.max_seq - 1);
+    const float rc = fz.cos_t[(size_t)trow * HALF + lane], rs = fz.sin_t[(size_t)trow * HALF + lane];
+    attn::chunk_q128<NW>(sm, R, q0, q1, rc, rs, pos < fz.max_seq, c0, pos, scale,
+                         [&](int t, float ot, float mt, float lt) {
+                             pp[t] = ot;
+                             if (t == 0) { pp[D] = mt; pp[D + 1] = lt; }
+                         });
+}
+
 }  // namespace
 
 int attn_decode_splits(int max_ctx) { return (max_ctx + kChunk - 1) / kChunk; }
@@ -889,6 +1030,14 @@ int attn_decode_splits(int max_ctx) { return (max_ctx + kChunk - 1) / kChunk; }
 int attn_decode_chunks(int cap, int d_head, int n_kv) {
     const int n = (cap + kCH - 1) / kCH;
     return d_head == 64 && n_kv <= 8 && cap > kSPMaxCtx && n <= kAttnMaxChunks ? n : 0;
+}
+
+int attn_decode_chunks128(int cap, int n_heads, int n_kv, int kv_dtype) {
+    const int n = (cap + kCH - 1) / kCH;
+    const int rep = n_kv > 0 ? n_heads / n_kv : 0;
+    return kv_dtype == VLRF_KV_Q8_0 && n_kv >= 1 && n_kv <= 8 && n_heads % n_kv == 0 &&
+                   (rep == 1 || rep == 2 || rep == 4 || rep == 8) && n + 1 <= kAttnMaxChunks
+               ? n : 0;
 }
 
 int launch_attn_decode(hipStream_t s, const float* q, const void* kc, const void* vc, const float* ks,
@@ -916,6 +1065,26 @@ int launch_attn_decode(hipStream_t s, const float* q, const void* kc, const void
     }
     const int8_t* k8 = static_cast<const int8_t*>(kc);
     const int8_t* v8 = static_cast<const int8_t*>(vc);
+    if (fuse && fz.nch > 0 && d_head == 128) {
+        // d_head 128 chunked form: nch chunk partials and the new key's (nch + 1 per head).
+        VH_ARG(fz.chunks && fz.nch == attn_decode_chunks128((int)(head_stride / d_head), n_heads, n_kv, kv_dtype),
+               "attn_decode: d_head 128 chunked form for %d chunks does not apply", fz.nch);
+        VH_ARG(fz.k_new && fz.v_new && fz.cos_t && fz.sin_t, "attn_decode: d_head 128 chunked form needs the row");
+        const int na = 8 * rep * ((n_kv * fz.nch + 7) / 8);
+        const dim3 cgrid(na + 1);
+#define VH_C128(R)                                                                                              \
+    hipLaunchKernelGGL((attn_chunk128_kernel<R>), cgrid, dim3(kCH), 0, s, q, k8, v8, ks, vs, head_stride, ctx_dev, \
+                       scale, fz, fz.nch, na)
+        switch (rep) {
+            case 1: VH_C128(1); break;
+            case 2: VH_C128(2); break;
+            case 4: VH_C128(4); break;
+            default: VH_C128(8); break;
+        }
+#undef VH_C128
+        VH_LAUNCHED();
+        return VLRF_HIP_OK;
+    }
     if (fuse && fz.nch > 0) {
         // Chunked form: REP workgroups per (KV head, chunk), grouped by XCD
         // (8 slots per group of 8 chunk indices); partials for the next GEMV.

@@ -496,5 +496,142 @@ __device__ __forceinline__ void chunk_q(SmemQ<NW>& sm, const Round<KVT>& R, floa
     }
 }
 
+// ---- d_head 128: one chunk without the token's row --------------------------------
+// The 8B-shape heads (d_head 128, Q8_0 cache) in the arrangement of chunk_q:
+// wave w scores rows c0 + 64w + lane (lane = token, its 128 codes in eight
+// 16-byte words), every wave exponentiates against the chunk's common
+// maximum, and P.V runs with lane (tg, dg) = (lane / 8, lane % 8) owning dims
+// 16dg..16dg+15 over rows tg + 8j (j < 8).  The 8 lanes tg of a dim group are
+// summed by a reduce-scatter (lane bits: dg = bits 0-2, tg = bits 3-5):
+// permlane16 pairs bit 4, permlane32 bit 5, a DPP rotation by 8 bit 3, so each
+// lane ends with two dims, 16*dg + 8*t1 + 4*t2 + 2*t0 + {0, 1}.
+constexpr int D128 = 128, HALF128 = 64;
+
+struct Round128 {
+    uint4 k[8];        // token base + lane: codes 16i..16i+15
+    uint4 v[8];        // token base + tg + 8j: codes 16dg..16dg+15
+    float ks, vs;      // row scales of token base + lane
+};
+
+__device__ __forceinline__ void load_round128(Round128& R, const int8_t* kc, const int8_t* vc, const float* ks,
+                                              const float* vs, size_t hb, int base, int cap, int lane) {
+    const int tg = lane >> 3, dg = lane & 7;
+    const int t = min(base + lane, cap - 1);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) R.k[i] = gload16(kc + hb + (size_t)t * D128 + 16 * i);
+    R.ks = *(gfloat*)(ks + t);
+    R.vs = *(gfloat*)(vs + t);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int tv = min(base + tg + 8 * j, cap - 1);
+        R.v[j] = gload16(vc + hb + (size_t)tv * D128 + 16 * dg);
+    }
+}
+
+template <int NW>
+struct SmemQ128 {
+    __align__(16) float qs[D128];
+    float wmax[NW], wl[NW];
+    __align__(16) float pbuf[NW][64];
+    __align__(16) float wacc[NW][D128];
+};
+
+// q0/q1 (wave 0, lane j): q[j], q[j + 64] before RoPE (rc, rs: the table
+// entries of pair j).  out(tid, acc, m, l) for tid < 128: the unnormalised
+// partial over rows [c0, min(c0 + 64*NW, pos)).
+template <int NW, class Out>
+__device__ __forceinline__ void chunk_q128(SmemQ128<NW>& sm, const Round128& R, float q0, float q1, float rc,
+                                           float rs, bool rot, int c0, int pos, float scale, Out&& out) {
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int tg = lane >> 3, dg = lane & 7;
+    if (w == 0) {
+        float y0 = q0, y1 = q1;
+        if (rot) rope2(q0, q1, rc, rs, &y0, &y1);
+        sm.qs[lane] = y0;
+        sm.qs[lane + HALF128] = y1;
+    }
+    __syncthreads();
+
+    const int t = c0 + w * 64 + lane;
+    const bool live = t < pos;
+    float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+#pragma unroll
+    for (int i = 0; i < D128 / 4; ++i) {
+        const float4 qv = *reinterpret_cast<const float4*>(&sm.qs[4 * i]);
+        const uint4 kw = R.k[i >> 2];
+        const float4 kf = s8f4((i & 3) == 0 ? kw.x : (i & 3) == 1 ? kw.y : (i & 3) == 2 ? kw.z : kw.w);
+        s0 += qv.x * kf.x;
+        s1 += qv.y * kf.y;
+        s2 += qv.z * kf.z;
+        s3 += qv.w * kf.w;
+    }
+    const float sc = live ? ((s0 + s1) + (s2 + s3)) * R.ks * scale : kNegInf;
+    const float wm = wave_max(sc);
+    if (lane == 0) sm.wmax[w] = wm;
+    __syncthreads();
+    float M = sm.wmax[0];
+#pragma unroll
+    for (int k = 1; k < NW; ++k) M = fmaxf(M, sm.wmax[k]);
+    const float pe = live ? expf(sc - M) : 0.f;
+    const float lw = wave_sum(pe);
+    sm.pbuf[w][lane] = pe * R.vs;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    float acc[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const float pp = sm.pbuf[w][tg + 8 * j];
+        const uint4 vw = R.v[j];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float4 v4 = s8f4(i == 0 ? vw.x : i == 1 ? vw.y : i == 2 ? vw.z : vw.w);
+            acc[4 * i] += pp * v4.x;
+            acc[4 * i + 1] += pp * v4.y;
+            acc[4 * i + 2] += pp * v4.z;
+            acc[4 * i + 3] += pp * v4.w;
+        }
+    }
+    {
+        const int t0 = tg & 1, t1 = (tg >> 1) & 1, t2 = tg >> 2;
+        float v1[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {   // rows differing in bit 4 (t1): dims 8*t1 + [0, 8)
+            const float2 x = swap_rows16(acc[e], acc[e + 8]);
+            v1[e] = x.x + x.y;
+        }
+        float v2[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {   // halves (bit 5, t2): 4*t2 + [0, 4)
+            const float2 x = swap_halves32(v1[e], v1[e + 4]);
+            v2[e] = x.x + x.y;
+        }
+        float v3[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {   // lanes 8 apart in a row (bit 3, t0): 2*t0 + [0, 2)
+            const float own = t0 ? v2[e + 2] : v2[e];
+            const float send = t0 ? v2[e] : v2[e + 2];
+            v3[e] = own + dpp_f<0x128>(send);
+        }
+        const int d = 16 * dg + 8 * t1 + 4 * t2 + 2 * t0;
+        sm.wacc[w][d] = v3[0];
+        sm.wacc[w][d + 1] = v3[1];
+    }
+    if (lane == 0) sm.wl[w] = lw;
+    __syncthreads();
+    if (tid < D128) {
+        float ot = 0.f, lt = 0.f;
+#pragma unroll
+        for (int k = 0; k < NW; ++k) {
+            ot += sm.wacc[k][tid];
+            lt += sm.wl[k];
+        }
+        out(tid, ot, M, lt);
+    }
+}
+
 }  // namespace attn
 }  // namespace vlrf_hip

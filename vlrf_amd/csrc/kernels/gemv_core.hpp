@@ -274,10 +274,13 @@ __device__ __forceinline__ void gemv_body(const uint8_t* __restrict__ qa, const 
     using S = Shape<WT, NC>;
     constexpr int NM = SWIGLU ? 2 : 1;
     constexpr int NT = kGemvThreads;
-    // XM & 8: x is decode attention output in its chunked form (head dim 64):
-    // element e is dim e % 64 of head e / 64, merged here from the nparts
-    // chunk partials of that head (log-sum-exp, attention.hpp:207-309's rule).
+    // XM & 8: x is decode attention output in its chunked form (head dim HD:
+    // 64, or 128 with XM & 32): element e is dim e % HD of head e / HD, merged
+    // here from the nparts chunk partials of that head (HD + 4 floats each:
+    // acc, m, l; log-sum-exp, attention.hpp:207-309's rule).
     constexpr bool MERGE = XM & 8;
+    constexpr int HD = (XM & 32) ? 128 : 64, CS = HD + 4;
+    static_assert(HD != 64 || CS == kAttnChunkStride, "partial layout");
     // XM & 16: every wave has at most one row (N <= the grid's row step), so
     // the second register set of the pipeline is neither loaded nor held.
     constexpr bool ONE = XM & 16;
@@ -316,12 +319,12 @@ __device__ __forceinline__ void gemv_body(const uint8_t* __restrict__ qa, const 
             if constexpr (MERGE) {                 // the head's chunk words, before any use (the 16
                                                    // threads of a head share the (m, l) loads in L1)
                 const int e = in ? 4 * f : 0;
-                const float* ph = x + (size_t)(e >> 6) * nparts * kAttnChunkStride + (e & 63);
+                const float* ph = x + (size_t)(e / HD) * nparts * CS + (e % HD);
 #pragma unroll
                 for (int c = 0; c < NP; ++c)
                     if (c < nparts) {
-                        pa[p][c] = *reinterpret_cast<const float4*>(ph + (size_t)c * kAttnChunkStride);
-                        pml[p][c] = *reinterpret_cast<const float2*>(ph - (e & 63) + (size_t)c * kAttnChunkStride + 64);
+                        pa[p][c] = *reinterpret_cast<const float4*>(ph + (size_t)c * CS);
+                        pml[p][c] = *reinterpret_cast<const float2*>(ph - (e % HD) + (size_t)c * CS + HD);
                     }
             } else {
                 const float4 t = reinterpret_cast<const float4*>(xs)[in ? f : 0];

@@ -216,7 +216,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) __attribute__((amdgpu_waves_per_eu
 template <int WT, bool SWIGLU>
 int launch_gemv(hipStream_t s, const DevWeight& a, const DevWeight* b, const float* x, float* y,
                 const float* norm_w, float eps, const float* residual, const int* x_row = nullptr,
-                float* x_copy = nullptr, int nparts = 0) {
+                float* x_copy = nullptr, int nparts = 0, int head_dim = 64) {
     constexpr int CW = 64 * Gemv<WT>::EPL;
     const int nc = (a.K + CW - 1) / CW;
     const uint8_t* qb = b ? b->q : nullptr;
@@ -227,7 +227,10 @@ int launch_gemv(hipStream_t s, const DevWeight& a, const DevWeight* b, const flo
            "gemv: chunk merge takes a plain x of whole 64-wide heads and at most %d chunks", kAttnMaxChunks);
     const int groups1 = (a.N + kGemvWaves - 1) / kGemvWaves;
     const bool one = groups1 <= kGemvMaxOneGroups;       // RPW 1: one row per wave
-    const int xm = (x_row ? 2 : 0) | (norm_w ? 1 : 0) | (residual ? 4 : 0) | (nparts ? 8 : 0) | (one ? 16 : 0);
+    const int xm = (x_row ? 2 : 0) | (norm_w ? 1 : 0) | (residual ? 4 : 0) | (nparts ? 8 : 0) | (one ? 16 : 0) |
+                   (nparts && head_dim == 128 ? 32 : 0);
+    VH_ARG(!nparts || head_dim == 64 || (head_dim == 128 && xm == 60 && a.K % 128 == 0),
+           "gemv: chunk merge of head dim %d (form %d)", head_dim, xm);
 #define VH_GEMV_XM(NC, RPW, XM)                                                                            \
     do {                                                                                                  \
         const int groups = (a.N + kGemvWaves * (RPW)-1) / (kGemvWaves * (RPW));                            \
@@ -252,6 +255,7 @@ int launch_gemv(hipStream_t s, const DevWeight& a, const DevWeight* b, const flo
             else if (xm == 21) VH_GEMV_XM(NC, RPW, 21);                   \
             else if (xm == 23) VH_GEMV_XM(NC, RPW, 23);                   \
             else if (xm == 28) VH_GEMV_XM(NC, RPW, 28);                   \
+            else if (xm == 60) VH_GEMV_XM(NC, RPW, 60);                   \
         }                                                                 \
     } while (0)
     if (nc <= 1) {
@@ -260,6 +264,9 @@ int launch_gemv(hipStream_t s, const DevWeight& a, const DevWeight* b, const flo
         VH_GEMV(2, 1);
     } else if (nc <= 3) {
         VH_GEMV(3, 1);
+    } else if (WT == VLRF_DT_Q8_0 && nc == 4) {
+        // K = 4096 (the 8B shape's d_model): 2 activation slots per thread.
+        if constexpr (WT == VLRF_DT_Q8_0) VH_GEMV(4, 1);
     } else if (WT == VLRF_DT_Q8_0 && nc <= 6) {
         // Q4_0 chunks are 2048 wide, so K <= kGemvMaxK needs at most 3 of them.
         if constexpr (WT == VLRF_DT_Q8_0) VH_GEMV(6, 1);
@@ -332,22 +339,25 @@ int qlinear_merge_max_chunks(const DevWeight& w) {
     if (!gemv_fits(w) || w.K % 64) return 0;
     const int cw = w.dtype == VLRF_DT_Q8_0 ? 64 * Gemv<VLRF_DT_Q8_0>::EPL : 64 * Gemv<VLRF_DT_Q4_0>::EPL;
     int nc = (w.K + cw - 1) / cw;
-    if (nc > 3) nc = 6;                                  // the instantiated chunk counts: 1, 2, 3, 6
+    if (nc > 4 || (nc == 4 && w.dtype != VLRF_DT_Q8_0)) nc = 6;   // instantiated: 1, 2, 3, 4 (Q8_0), 6
     const int per = (nc * cw / 4 + 64 * kGemvWaves - 1) / (64 * kGemvWaves);
     return kAttnMaxChunks / per;
 }
 
 int launch_qlinear_merge(hipStream_t s, const DevWeight& w, const float* chunks, int nch, const float* residual,
-                         float* y) {
+                         float* y, int head_dim) {
     int rc = check_weight(w);
     if (rc) return rc;
     VH_ARG(chunks && y && residual && nch >= 1, "qlinear_merge: bad arguments");
     VH_ARG(gemv_fits(w), "qlinear_merge: weight does not take the M=1 GEMV path");
     VH_ARG(nch <= qlinear_merge_max_chunks(w), "qlinear_merge: %d chunks, at most %d for K %d", nch,
            qlinear_merge_max_chunks(w), w.K);
+    VH_ARG(head_dim == 64 || head_dim == 128, "qlinear_merge: head dim %d", head_dim);
     if (w.dtype == VLRF_DT_Q8_0)
-        return launch_gemv<VLRF_DT_Q8_0, false>(s, w, nullptr, chunks, y, nullptr, 0.f, residual, nullptr, nullptr, nch);
-    return launch_gemv<VLRF_DT_Q4_0, false>(s, w, nullptr, chunks, y, nullptr, 0.f, residual, nullptr, nullptr, nch);
+        return launch_gemv<VLRF_DT_Q8_0, false>(s, w, nullptr, chunks, y, nullptr, 0.f, residual, nullptr, nullptr, nch,
+                                                head_dim);
+    return launch_gemv<VLRF_DT_Q4_0, false>(s, w, nullptr, chunks, y, nullptr, 0.f, residual, nullptr, nullptr, nch,
+                                            head_dim);
 }
 
 int launch_qlinear_gather(hipStream_t s, const DevWeight& w, const float* table, const int* row,

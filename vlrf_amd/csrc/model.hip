@@ -89,6 +89,7 @@ struct vlrf_hip_model {
     // Fused QKV + attention launch (kernels/qkv_attn.hip) where it applies
     // (VLRF_HIP_QKV_ATTN=0 queues the two kernels instead).
     bool qkv_attn = false;
+    bool chunk_new = false;         // d_head 128 chunked attention: the new key is partial nch
     uint64_t* qkv_tags = nullptr;   // [L][D + 2*dkv] tagged projection outputs
     int* step_status = nullptr;     // [4] failure flag, workgroup, phase, layer
     long long wait_limit = 0;       // wall-clock ticks a wait may last
@@ -169,7 +170,7 @@ int enqueue_step(vlrf_hip_model* m, hipStream_t s) {
                                              (long)m->S * m->dh, m->H, m->G, m->dh, 1, m->state + 1,
                                              m->n_splits, scale, m->part, m->att, &fz);
         }
-        if (!rc) rc = m->nch ? launch_qlinear_merge(s, Ly.wo, m->chunks, m->nparts, m->x, m->x)
+        if (!rc) rc = m->nch ? launch_qlinear_merge(s, Ly.wo, m->chunks, m->nparts, m->x, m->x, m->dh)
                              : launch_qlinear(s, Ly.wo, m->att, m->x, 1, nullptr, 0.f, m->x);
         if (!rc) rc = launch_qlinear_swiglu(s, Ly.wg, Ly.wu, m->x, m->h, 1, Ly.ln2, eps);
         if (!rc) rc = launch_qlinear(s, Ly.wd, m->h, m->x, 1, nullptr, 0.f, m->x);
@@ -406,8 +407,17 @@ int vlrf_hip_model_create(vlrf_hip_ctx_t ctx, const vlrf_hip_model_config* cfg, 
             m->qkv_attn = true;
         }
     }
-    m->nparts = m->nch + (m->qkv_attn ? 1 : 0);
-    if (m->nch) dalloc((void**)&m->chunks, (size_t)m->H * m->nparts * kAttnChunkStride * 4);
+    // d_head 128 (the 8B shape): the chunked form with the new key as its own
+    // partial, where the O projection's GEMV can merge nch + 1 partials.
+    if (dh == 128 && (c.weight_dtype == VLRF_DT_Q8_0 || c.weight_dtype == VLRF_DT_Q4_0) && wo_shape.K == m->D) {
+        const int n = attn_decode_chunks128(m->S, m->H, m->G, c.kv_dtype);
+        if (n && n + 1 <= qlinear_merge_max_chunks(wo_shape)) {
+            m->nch = n;
+            m->chunk_new = true;
+        }
+    }
+    m->nparts = m->nch + (m->qkv_attn || m->chunk_new ? 1 : 0);
+    if (m->nch) dalloc((void**)&m->chunks, (size_t)m->H * m->nparts * (dh + 4) * 4);
     // Zero words carry no epoch (the epoch starts at 1).
     auto tagged = [&](uint64_t** p, size_t words) {
         dalloc((void**)p, words * 8);
