@@ -272,10 +272,15 @@ void launch_cfg(hipStream_t s, int wt, const uint16_t* a, const DevWeight& w0, c
 // before use.
 namespace lds_gemm {
 
-constexpr int BM = 256, BN = 128, NT = 512, WM = 128, WN = 32, MI = WM / 32;
-constexpr int A_B = BM * 128;                 // one K step of A: 256 rows x 64 bf16
-constexpr int A_IT = A_B / (NT * 16);         // 16-byte loads per thread
-template <int WT, int NM> struct Stage {
+// BM: 256 rows of A (waves 2 x 4 over 128 x 32 blocks) or 128 (64 x 32 blocks).
+constexpr int BN = 128, NT = 512, WN = 32;
+template <int BM> struct ATile {
+    static constexpr int WM = BM / 2, MI = WM / 32;
+    static constexpr int A_B = BM * 128;                 // one K step of A: BM rows x 64 bf16
+    static constexpr int A_IT = A_B / (NT * 16);         // 16-byte loads per thread
+};
+template <int WT, int NM, int BM> struct Stage {
+    static constexpr int A_IT = ATile<BM>::A_IT;
     static constexpr int CB = WT == VLRF_DT_Q8_0 ? 64 : 32;   // code bytes of a row per K step
     static constexpr int W_B = NM * BN * CB;  // codes: NM*BN rows
     static constexpr int S_B = NM * BN * 4;   // two f16 block scales per row
@@ -314,13 +319,16 @@ template <int WT> __device__ __forceinline__ int swz_w(int n) {
 
 }  // namespace lds_gemm
 
-template <int WT, int NM, int EPI>
+// ldo: the row stride of out and residual (N, or the whole width when this
+// launch covers a column range of a wider output).
+template <int WT, int NM, int EPI, int BM>
 __global__ __launch_bounds__(lds_gemm::NT) void mfma_qgemm_lds_kernel(
     const uint16_t* __restrict__ A, const uint8_t* __restrict__ qa, const __half* __restrict__ da,
-    const uint8_t* __restrict__ qb, const __half* __restrict__ db, int M, int N, int K,
+    const uint8_t* __restrict__ qb, const __half* __restrict__ db, int M, int N, int K, int ldo,
     const float* __restrict__ residual, void* __restrict__ out) {
     using namespace lds_gemm;
-    using S = Stage<WT, NM>;
+    using S = Stage<WT, NM, BM>;
+    constexpr int WM = ATile<BM>::WM, MI = ATile<BM>::MI, A_B = ATile<BM>::A_B, A_IT = ATile<BM>::A_IT;
     constexpr int CB = S::CB, RPI = 1024 / CB, CPR = CB / 16;   // rows / chunks per 1 KB load
     __shared__ __align__(16) uint8_t A0[A_B], A1[A_B], A2[A_B];
     __shared__ __align__(16) uint8_t W0[S::W_B], W1[S::W_B], W2[S::W_B];
@@ -460,13 +468,13 @@ __global__ __launch_bounds__(lds_gemm::NT) void mfma_qgemm_lds_kernel(
 #pragma unroll
                 for (int m = 0; m < 2; ++m) {
                     if (row < M && col + m * BN < N) {
-                        const size_t o = (size_t)row * N + col + m * BN;
+                        const size_t o = (size_t)row * ldo + col + m * BN;
                         if constexpr (EPI == 5) reinterpret_cast<float*>(out)[o] = acc[m][i][v] + residual[o];
                         else reinterpret_cast<float*>(out)[o] = acc[m][i][v];
                     }
                 }
             } else if (row < M && col < N) {
-                const size_t o = (size_t)row * N + col;
+                const size_t o = (size_t)row * ldo + col;
                 if constexpr (EPI >= 2) {
                     const float g = acc[0][i][v], u = acc[NM - 1][i][v];
                     const float hv = u * (g / (1.f + expf(-g)));   // silu(g) * u, ops.hpp:409-441
@@ -481,27 +489,76 @@ __global__ __launch_bounds__(lds_gemm::NT) void mfma_qgemm_lds_kernel(
         }
 }
 
-template <int WT, int EPI>
-void launch_lds_wt(hipStream_t s, const uint16_t* a, const DevWeight& w0, const DevWeight* w1, int M,
-                   const float* residual, void* out) {
+// Rows [n0, n0 + nn) of the weights (columns of the output), BM-row tiles of A.
+template <int WT, int EPI, int BM>
+void launch_lds_wt(hipStream_t s, const uint16_t* a, const DevWeight& w0, const DevWeight* w1, int M, int n0,
+                   int nn, const float* residual, void* out) {
     constexpr int TN = lds_gemm::BN * (EPI >= 4 ? 2 : 1);
-    const dim3 grid((w0.N + TN - 1) / TN, (M + lds_gemm::BM - 1) / lds_gemm::BM);
+    const dim3 grid((nn + TN - 1) / TN, (M + BM - 1) / BM);
+    const size_t rowb = WT == VLRF_DT_Q8_0 ? (size_t)w0.K : (size_t)w0.K / 2;
+    const uint8_t* qa = w0.q + (size_t)n0 * rowb;
+    const __half* da = w0.d + (size_t)n0 * (w0.K / 32);
+    const float* res = residual ? residual + n0 : nullptr;
+    void* o = EPI == 2 ? (void*)(static_cast<uint16_t*>(out) + n0) : (void*)(static_cast<float*>(out) + n0);
     if constexpr (EPI >= 4)   // wide: both halves from the one matrix
-        hipLaunchKernelGGL((mfma_qgemm_lds_kernel<WT, 2, EPI>), grid, dim3(lds_gemm::NT), 0, s, a, w0.q, w0.d,
-                           w0.q, w0.d, M, w0.N, w0.K, residual, out);
+        hipLaunchKernelGGL((mfma_qgemm_lds_kernel<WT, 2, EPI, BM>), grid, dim3(lds_gemm::NT), 0, s, a, qa, da, qa, da,
+                           M, nn, w0.K, w0.N, res, o);
     else if constexpr (EPI >= 2)   // SwiGLU: gate and up tiles together
-        hipLaunchKernelGGL((mfma_qgemm_lds_kernel<WT, 2, EPI>), grid, dim3(lds_gemm::NT), 0, s, a, w0.q, w0.d,
-                           w1->q, w1->d, M, w0.N, w0.K, residual, out);
+        hipLaunchKernelGGL((mfma_qgemm_lds_kernel<WT, 2, EPI, BM>), grid, dim3(lds_gemm::NT), 0, s, a, qa, da,
+                           w1->q + (size_t)n0 * rowb, w1->d + (size_t)n0 * (w0.K / 32), M, nn, w0.K, w0.N, res, o);
     else
-        hipLaunchKernelGGL((mfma_qgemm_lds_kernel<WT, 1, EPI>), grid, dim3(lds_gemm::NT), 0, s, a, w0.q, w0.d,
-                           w0.q, w0.d, M, w0.N, w0.K, residual, out);
+        hipLaunchKernelGGL((mfma_qgemm_lds_kernel<WT, 1, EPI, BM>), grid, dim3(lds_gemm::NT), 0, s, a, qa, da, qa, da,
+                           M, nn, w0.K, w0.N, res, o);
 }
 
-template <int EPI>
-void launch_lds(hipStream_t s, const uint16_t* a, const DevWeight& w0, const DevWeight* w1, int M,
+template <int EPI, int BM>
+void launch_lds(hipStream_t s, const uint16_t* a, const DevWeight& w0, const DevWeight* w1, int M, int n0, int nn,
                 const float* residual, void* out) {
-    if (w0.dtype == VLRF_DT_Q8_0) launch_lds_wt<VLRF_DT_Q8_0, EPI>(s, a, w0, w1, M, residual, out);
-    else launch_lds_wt<VLRF_DT_Q4_0, EPI>(s, a, w0, w1, M, residual, out);
+    if (w0.dtype == VLRF_DT_Q8_0) launch_lds_wt<VLRF_DT_Q8_0, EPI, BM>(s, a, w0, w1, M, n0, nn, residual, out);
+    else launch_lds_wt<VLRF_DT_Q4_0, EPI, BM>(s, a, w0, w1, M, n0, nn, residual, out);
+}
+
+// Tile plan of an M > 128 GEMM on the lds ring (one workgroup per CU: the
+// ring takes 99-147 KiB of LDS).  Plain and residual GEMMs take 256 x 256
+// tiles (two 128-row halves of the weight: twice the MFMA work per staged
+// byte) where they still give at least 3/4 of a round of workgroups, else
+// 256 x 128 (O and down of the 8B layer at T = 2048 ran 1.335 against 1.166 ms
+// per layer wide, and slower again as 128 x 256 tiles, whose waves decode
+// twice the codes per MFMA).  A last round of 256-row tiles at most half full
+// (SwiGLU's 896 tiles at T = 2048) is run instead as 128-row tiles over its
+// columns: twice as many, each with half the MFMA work but the same decode
+// work per wave, so the round takes more than half as long (8B layer at
+// T = 2048: 1.1667 -> 1.1555 ms, same-box A/B).
+struct LdsPlan {
+    bool wide = false;   // 2 x BN weight rows per tile (plain / residual GEMMs)
+    int n_split = 0;     // > 0: columns [n_split, N) in a second launch of 128-row tiles
+};
+
+LdsPlan lds_plan(int M, int N, bool swiglu, int cus) {
+    LdsPlan p;
+    const int mt = (M + 255) / 256;
+    const long wide_groups = (long)((N + 2 * lds_gemm::BN - 1) / (2 * lds_gemm::BN)) * mt;
+    p.wide = !swiglu && 4 * wide_groups >= 3L * cus;
+    const int tn = p.wide ? 2 * lds_gemm::BN : lds_gemm::BN;   // weight rows per tile (of each matrix)
+    const int nt = (N + tn - 1) / tn;
+    const long full = (long)nt * mt, rem = full % cus;
+    if (N % tn == 0 && full >= cus && rem > 0 && 2 * rem <= cus && rem % mt == 0)
+        p.n_split = (int)((nt - rem / mt) * tn);
+    return p;
+}
+
+// Runs a plan: EPI of the narrow form (the wide form is EPI + 4 for 0 / 1).
+template <int EPI>
+void launch_lds_plan(hipStream_t s, const LdsPlan& p, const uint16_t* a, const DevWeight& w0, const DevWeight* w1,
+                     int M, const float* residual, void* out) {
+    constexpr int EW = EPI <= 1 ? EPI + 4 : EPI;
+    const int n1 = p.n_split ? p.n_split : w0.N;
+    if (p.wide) launch_lds<EW, 256>(s, a, w0, w1, M, 0, n1, residual, out);
+    else launch_lds<EPI, 256>(s, a, w0, w1, M, 0, n1, residual, out);
+    if (p.n_split) {
+        if (p.wide) launch_lds<EW, 128>(s, a, w0, w1, M, p.n_split, w0.N - p.n_split, residual, out);
+        else launch_lds<EPI, 128>(s, a, w0, w1, M, p.n_split, w0.N - p.n_split, residual, out);
+    }
 }
 
 // out[r][:] = bf16(w ? rmsnorm(x[r]) * w : x[r]), one 256-lane workgroup per row
@@ -782,8 +839,19 @@ int small_grid_y(int N, int K) {
     return want < ns ? want : ns;
 }
 
-constexpr long kWideGroups = 192;   // 3/4 of the CUs (at 128, O and down of the 8B layer at
-                                    // T = 2048 go wide and the layer runs 1.335 against 1.166 ms)
+// Compute units of the current device (the tile plan's round size).
+int lds_cus() {
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+            cus = n;
+        else
+            cus = 256;
+    }
+    return cus;
+}
 
 int check_qgemm(const DevWeight& w, int M) {
     VH_ARG(w.dtype == VLRF_DT_Q8_0 || w.dtype == VLRF_DT_Q4_0,
@@ -813,15 +881,9 @@ int launch_qgemm(hipStream_t s, const DevWeight& w, const uint16_t* a, int M, co
     if (rc) return rc;
     VH_ARG(a && y, "qgemm: null operand");
     if (M > 128) {
-        // 2*BN-wide tiles (twice the MFMA work per byte staged) where they still
-        // give at least kWideGroups workgroups
-        const long groups = (long)((w.N + 2 * lds_gemm::BN - 1) / (2 * lds_gemm::BN)) *
-                            ((M + lds_gemm::BM - 1) / lds_gemm::BM);
-        if (groups >= kWideGroups) {
-            if (residual) launch_lds<5>(s, a, w, nullptr, M, residual, y);
-            else launch_lds<4>(s, a, w, nullptr, M, nullptr, y);
-        } else if (residual) launch_lds<1>(s, a, w, nullptr, M, residual, y);
-        else launch_lds<0>(s, a, w, nullptr, M, nullptr, y);
+        const LdsPlan p = lds_plan(M, w.N, false, lds_cus());
+        if (residual) launch_lds_plan<1>(s, p, a, w, nullptr, M, residual, y);
+        else launch_lds_plan<0>(s, p, a, w, nullptr, M, nullptr, y);
     } else {
         if (residual) launch_cfg<CfgSmall, 1>(s, w.dtype, a, w, nullptr, M, residual, y);
         else launch_cfg<CfgSmall, 0>(s, w.dtype, a, w, nullptr, M, nullptr, y);
@@ -839,8 +901,9 @@ int launch_qgemm_swiglu(hipStream_t s, const DevWeight& wg, const DevWeight& wu,
     VH_ARG(wg.N == wu.N && wg.K == wu.K && wg.dtype == wu.dtype, "qgemm_swiglu: gate/up differ");
     VH_ARG(a && h, "qgemm_swiglu: null operand");
     if (M > 128) {
-        if (h_bf16) launch_lds<2>(s, a, wg, &wu, M, nullptr, h);
-        else launch_lds<3>(s, a, wg, &wu, M, nullptr, h);
+        const LdsPlan p = lds_plan(M, wg.N, true, lds_cus());
+        if (h_bf16) launch_lds_plan<2>(s, p, a, wg, &wu, M, nullptr, h);
+        else launch_lds_plan<3>(s, p, a, wg, &wu, M, nullptr, h);
     } else {
         if (h_bf16) launch_cfg<CfgSmall, 2>(s, wg.dtype, a, wg, &wu, M, nullptr, h);
         else launch_cfg<CfgSmall, 3>(s, wg.dtype, a, wg, &wu, M, nullptr, h);
