@@ -299,8 +299,10 @@ def kernel_bytes(cfg, dtype, ctx_len, nparts):
         "o_proj": weight_bytes(dtype, D, D) + part + D * 8,
         "gate_up": 2 * weight_bytes(dtype, Fd, D) + D * 8 + Fd * 4,
         "down": weight_bytes(dtype, D, Fd) + Fd * 4 + D * 8,
-        "lm_head": weight_bytes(dtype, V_, D) + D * 8 + V_ * 4,
-        "argmax": V_ * 4,
+        # The LM head's workgroups (at most 512) also leave one (max, index)
+        # pair each, and the argmax step reduces only those.
+        "lm_head": weight_bytes(dtype, V_, D) + D * 8 + V_ * 4 + 512 * 8,
+        "argmax": 512 * 8,
     }
 
 
@@ -309,8 +311,8 @@ KERNEL_KINDS = (  # (kind, pattern in the profile's kernel name)
     ("o_proj", ", false, 28>"),
     ("gate_up", ", true, 17>"),
     ("down", ", false, 20>"),
-    ("lm_head", ", false, 1>"),
-    ("argmax", "argmax_step_kernel"),
+    ("lm_head", ", false, 65>"),
+    ("argmax", "argmax_pairs_step_kernel"),
 )
 
 

@@ -94,19 +94,21 @@ def test_unset_weights_rejected(ctx):
         m.step(0)
 
 
-def test_argmax_ties_take_the_lowest_index(ctx):
+@pytest.mark.parametrize("dtype", [V.DT_Q8_0, V.DT_Q4_0])
+def test_argmax_ties_take_the_lowest_index(ctx, dtype):
     """sampler::argmax (transformer.hpp:43-47) returns the first index of the
     maximum.  An LM head whose rows repeat with period 37 over a 32000-token
     vocabulary gives every logit 864-865 bit-identical copies spread over all
-    the argmax threads and waves; each step's token must be the lowest index
-    of the maximum."""
-    cfg = dict(F.tiny(V.DT_Q8_0, n_layers=1, max_seq_len=64), vocab_size=32000)
+    the LM head's workgroups and waves (whose per-workgroup maxima the step's
+    argmax reduces); each step's token must be the lowest index of the
+    maximum."""
+    cfg = dict(F.tiny(dtype, n_layers=1, max_seq_len=64), vocab_size=32000)
     m = V.Model(ctx, cfg)
     F.load_model(m, 31, norm_std=0.1)
     D, nv, P = cfg["d_model"], cfg["vocab_size"], 37
     rows = np.random.default_rng(31).normal(0.0, 0.5, (P, D)).astype(np.float32)
     w = np.tile(rows, (nv // P + 1, 1))[:nv]
-    m.set_weight("lm_head.weight", F.quantize(w.reshape(-1), V.DT_Q8_0), V.DT_Q8_0, nv, D)
+    m.set_weight("lm_head.weight", F.quantize(w.reshape(-1), dtype), dtype, nv, D)
     m.reset()
     for t in F.tokens(31, "tie", 12, nv):
         print(f"[case] argmax ties, token {int(t)}", flush=True)

@@ -204,3 +204,24 @@ def test_config5_attention_t2048_vs_oracle(ctx):
     tail = slice(T - 64, T)
     check(got[tail] - x[tail], ref[tail] - x[tail], "layer update, rows 1984-2047")
     check(got[:64] - x[:64], ref[:64] - x[:64], "layer update, rows 0-63")
+
+
+@pytest.mark.parametrize("dtype", [V.DT_Q8_0, V.DT_Q4_0])
+def test_new_weights_after_a_prefill_replace_the_bf16_expansion(ctx, dtype):
+    """A prefill of more than 128 rows leaves each projection's bf16 expansion
+    on the device; setting the weights again must drop it, so a model given
+    new weights after a prefill computes what a fresh model with those
+    weights computes, bit for bit."""
+    cfg = F.tiny(dtype, n_layers=2, max_seq_len=256)
+    D, T = cfg["d_model"], 150
+    x = F.normal(41, "bfx", T * D).reshape(T, D)
+    m = V.Model(ctx, cfg)
+    F.load_model(m, 41, norm_std=0.1)
+    m.forward_hidden(ctx.to_device(x))
+    F.load_model(m, 42, norm_std=0.1)
+    m.reset()
+    got = m.forward_hidden(ctx.to_device(x)).download((T, D))
+    fresh = V.Model(ctx, cfg)
+    F.load_model(fresh, 42, norm_std=0.1)
+    ref = fresh.forward_hidden(ctx.to_device(x)).download((T, D))
+    assert np.array_equal(got, ref)

@@ -88,3 +88,57 @@ def test_prefill_swiglu_ragged(ctx, orc, dtype, M, Fd, K):
     xn = orc.rms_norm(x, g, 1e-5)
     ref = orc.silu_mul(orc.linear(xn, udec), orc.linear(xn, gdec))
     assert rel_err(dh.download((M, Fd)), ref) <= TOL
+
+
+def _both_forms(monkeypatch, run):
+    """run() with the weights' bf16 expansion (the default for M > 128) and with
+    VLRF_HIP_PREFILL_BF16=0 (codes decoded in registers)."""
+    monkeypatch.delenv("VLRF_HIP_PREFILL_BF16", raising=False)
+    a = run()
+    monkeypatch.setenv("VLRF_HIP_PREFILL_BF16", "0")
+    b = run()
+    monkeypatch.delenv("VLRF_HIP_PREFILL_BF16", raising=False)
+    return a, b
+
+
+@pytest.mark.parametrize("dtype", [V.DT_Q8_0, V.DT_Q4_0])
+# 256x128 tiles (1000 x 1024), wide 256x256 tiles (2048 x 6144), a ragged
+# wide edge (520 x 16600), the residual form (300 x 4096 x 2048)
+@pytest.mark.parametrize("M,N,K,res", [(1000, 1024, 512, False), (2048, 6144, 256, False),
+                                       (520, 16600, 64, False), (300, 4096, 2048, True)])
+def test_bf16_expansion_equals_in_register_decode(ctx, monkeypatch, dtype, M, N, K, res):
+    """The GEMM over the weights' bf16 expansion multiplies the operands the
+    in-register decode forms, in the same MFMA order: bit-identical outputs."""
+    print(f"[case] bf16 expansion dtype={dtype} M={M} N={N} K={K} res={res}", flush=True)
+    x = F.normal(24, f"bx{M}x{K}", M * K).reshape(M, K)
+    r = F.normal(24, f"br{M}x{N}", M * N).reshape(M, N)
+    dx = ctx.to_device(x)
+
+    def run():
+        w, _ = _weight(ctx, 24, f"B{N}x{K}", N, K, dtype)   # a fresh weight: no expansion yet
+        dy = ctx.to_device(r) if res else ctx.alloc(M * N * 4)
+        ctx.qlinear(w, dx, dy, M, residual=dy if res else None)
+        return dy.download((M, N))
+
+    a, b = _both_forms(monkeypatch, run)
+    assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("dtype", [V.DT_Q8_0, V.DT_Q4_0])
+# 2048 x 14336: 112 x 8 tiles of 256 x 128, the last round (128 columns x 8)
+# as 128-row tiles over columns 12288..14335 (two launches)
+@pytest.mark.parametrize("M,Fd,K", [(2048, 14336, 128), (257, 1000, 192)])
+def test_bf16_expansion_swiglu_equals_in_register_decode(ctx, monkeypatch, dtype, M, Fd, K):
+    print(f"[case] bf16 expansion swiglu dtype={dtype} M={M} F={Fd} K={K}", flush=True)
+    x = F.normal(25, f"sx{M}x{K}", M * K).reshape(M, K)
+    dx = ctx.to_device(x)
+
+    def run():
+        wg, _ = _weight(ctx, 25, f"SG{Fd}x{K}", Fd, K, dtype)
+        wu, _ = _weight(ctx, 25, f"SU{Fd}x{K}", Fd, K, dtype)
+        dh = ctx.alloc(M * Fd * 4)
+        ctx.qlinear_swiglu(wg, wu, dx, dh, M)
+        return dh.download((M, Fd))
+
+    a, b = _both_forms(monkeypatch, run)
+    assert np.array_equal(a, b)

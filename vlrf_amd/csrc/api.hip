@@ -64,14 +64,21 @@ void weight_release(DevWeight& w) {
     if (w.q) (void)hipFree(w.q);
     if (w.d) (void)hipFree(w.d);
     if (w.f) (void)hipFree(w.f);
+    if (w.bf) (void)hipFree(w.bf);
     w.q = nullptr;
     w.d = nullptr;
     w.f = nullptr;
+    w.bf = nullptr;
 }
 
 int weight_upload_rows(hipStream_t s, DevWeight& w, const void* host, int row0, int nrows) {
     VH_ARG(host != nullptr, "weight upload: null host pointer");
     VH_ARG(row0 >= 0 && nrows >= 0 && row0 + nrows <= w.N, "weight upload: rows out of range");
+    if (w.bf) {   // the expansion no longer matches the codes: made again when next needed
+        VH_CHECK(hipStreamSynchronize(s));
+        (void)hipFree(w.bf);
+        w.bf = nullptr;
+    }
     const int K = w.K;
     const size_t nel = (size_t)nrows * K;
     if (w.dtype == VLRF_DT_F32) {

@@ -60,6 +60,10 @@ struct DevWeight {
     uint8_t* q = nullptr;
     __half* d = nullptr;
     float* f = nullptr;
+    // bf16(code * scale) of every element, [N][K]: made by the first GEMM with
+    // more than 128 rows of A (weight_expand_bf16), dropped when rows are
+    // uploaded or the weight is released.  A cache of q / d, hence mutable.
+    mutable uint16_t* bf = nullptr;
 };
 
 size_t weight_device_bytes(int dtype, int N, int K);
@@ -67,6 +71,9 @@ size_t weight_device_bytes(int dtype, int N, int K);
 int weight_upload_rows(hipStream_t s, DevWeight& w, const void* host, int row0, int nrows);
 int weight_alloc(DevWeight& w, int dtype, int N, int K);
 void weight_release(DevWeight& w);
+// Makes w.bf on stream s unless it exists or VLRF_HIP_PREFILL_BF16=0; false
+// (the GEMM then decodes codes in registers) when disabled or out of memory.
+bool weight_expand_bf16(hipStream_t s, const DevWeight& w);
 
 // ---- KV cache ------------------------------------------------------------------
 // k and v address [n_kv][max_seq][d_head] elements of the layer's dtype: int8
@@ -328,6 +335,14 @@ struct QkvAttnParams {
 bool qkv_attn_supported(int w_dtype, int N, int K, int nch, int n_kv);
 int qkv_attn_blocks(int rep, int n_kv, int nch);
 int launch_qkv_attn(hipStream_t s, const QkvAttnParams& p, int w_dtype, int kv_dtype, bool gather);
+
+// The LM head's GEMV (RMSNorm fused, the row loop: N > 8 * 768 rows) writing
+// besides the logits one (max, first row) pair per workgroup to pairs[*npairs]
+// (*npairs <= 512), reduced by launch_argmax_pairs_step.
+bool qlinear_argmax_supported(const DevWeight& w);
+int launch_qlinear_argmax(hipStream_t s, const DevWeight& w, const float* x, float* y, const float* norm_w,
+                          float eps, float2* pairs, int* npairs);
+int launch_argmax_pairs_step(hipStream_t s, const float2* pairs, int np, int* state, int* gen_ids, int gen_cap);
 
 int launch_embed(hipStream_t s, const float* table, const int* tok_dev, float* x, int D);
 // argmax over logits[n] (first maximum) -> state[0] (token), appends to

@@ -289,6 +289,19 @@ __global__ __launch_bounds__(256) void embed_kernel(const float* __restrict__ ta
 // sampler::argmax (transformer.hpp:43-47): first index of the maximum.  Each
 // thread issues all of its float4 loads before comparing (one memory round
 // trip); ties keep the lower index at every level.
+// The step's state after its token: state[0] = token, appended to
+// gen_ids[state[2]++], state[1] (position) += 1, state[3] (the epoch of the
+// next step's tagged words: every launch of this step has finished reading
+// them) += 1.
+__device__ __forceinline__ void step_state_advance(int tok, int* state, int* gen_ids, int gen_cap) {
+    state[0] = tok;
+    const int g = state[2];
+    if (g < gen_cap) gen_ids[g] = tok;
+    state[2] = g + 1;
+    state[1] = state[1] + 1;
+    state[3] = state[3] + 1;
+}
+
 constexpr int kArgmaxPer = 16;   // float4 per thread: n <= 1024*4*16 = 65536
 __global__ __launch_bounds__(1024) void argmax_step_kernel(const float* __restrict__ logits, int n,
                                                            int* state, int* gen_ids, int gen_cap) {
@@ -342,17 +355,46 @@ __global__ __launch_bounds__(1024) void argmax_step_kernel(const float* __restri
             take(ov, oi);
         }
     }
-    if (tid == 0) {
-        const int tok = idx < 0 ? 0 : idx;
-        state[0] = tok;
-        const int g = state[2];
-        if (g < gen_cap) gen_ids[g] = tok;
-        state[2] = g + 1;
-        state[1] = state[1] + 1;
-        // The next step's epoch: the tag of the words the fused QKV + attention
-        // launch exchanges (every launch of this step has finished reading it).
-        state[3] = state[3] + 1;
+    if (tid == 0) step_state_advance(idx < 0 ? 0 : idx, state, gen_ids, gen_cap);
+}
+
+// The same step over the LM head's per-workgroup (max, first index) pairs
+// (gemv_kernel's argmax form): one pair per thread, the rule of
+// argmax_step_kernel (larger value; the lower index on equal values).
+__global__ __launch_bounds__(512) void argmax_pairs_step_kernel(const float2* __restrict__ pairs, int np, int* state,
+                                                                int* gen_ids, int gen_cap) {
+    __shared__ float bv[8];
+    __shared__ int bi[8];
+    const int tid = threadIdx.x;
+    float best = -INFINITY;
+    int idx = -1;
+    if (tid < np) {
+        const float2 p = pairs[tid];
+        best = p.x;
+        idx = __float_as_int(p.y);
     }
+    auto take = [&](float ov, int oi) {
+        if (oi >= 0 && (idx < 0 || best < ov || (best == ov && oi < idx))) { best = ov; idx = oi; }
+    };
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(best, o);
+        const int oi = __shfl_xor(idx, o);
+        take(ov, oi);
+    }
+    if ((tid & 63) == 0) { bv[tid >> 6] = best; bi[tid >> 6] = idx; }
+    __syncthreads();
+    if (tid < 64) {
+        best = tid < 8 ? bv[tid] : -INFINITY;
+        idx = tid < 8 ? bi[tid] : -1;
+#pragma unroll
+        for (int o = 4; o > 0; o >>= 1) {
+            const float ov = __shfl_xor(best, o);
+            const int oi = __shfl_xor(idx, o);
+            take(ov, oi);
+        }
+    }
+    if (tid == 0) step_state_advance(idx < 0 ? 0 : idx, state, gen_ids, gen_cap);
 }
 
 }  // namespace
@@ -429,6 +471,13 @@ int launch_rope(hipStream_t s, float* x, int T, int n_heads, int d_head, int pos
 
 int launch_embed(hipStream_t s, const float* table, const int* tok_dev, float* x, int D) {
     hipLaunchKernelGGL(embed_kernel, dim3(1), dim3(256), 0, s, table, tok_dev, x, D);
+    VH_LAUNCHED();
+    return VLRF_HIP_OK;
+}
+
+int launch_argmax_pairs_step(hipStream_t s, const float2* pairs, int np, int* state, int* gen_ids, int gen_cap) {
+    VH_ARG(np >= 1 && np <= 512, "argmax_pairs: %d pairs outside [1,512]", np);
+    hipLaunchKernelGGL(argmax_pairs_step_kernel, dim3(1), dim3(512), 0, s, pairs, np, state, gen_ids, gen_cap);
     VH_LAUNCHED();
     return VLRF_HIP_OK;
 }

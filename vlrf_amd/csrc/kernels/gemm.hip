@@ -317,6 +317,47 @@ template <int WT> __device__ __forceinline__ int swz_w(int n) {
     return WT == VLRF_DT_Q8_0 ? (n >> 2) & 3 : (n >> 3) & 1;
 }
 
+// The tile's results: accumulator v of MFMA tile i holds row 32i + 8(v/4) +
+// 4h + v%4, column l32 of the wave's block.  EPI 0 plain, 1 + residual,
+// 2 / 3 silu(gate) * up as bf16 / f32 (NM 2: gate, up), 4 / 5 wide (NM 2: the
+// two BN-column halves of one weight) plain / + residual.
+template <int NM, int EPI, int BM>
+__device__ __forceinline__ void store_tile(const f32x16 (&acc)[NM][ATile<BM>::MI], int m0, int n0, int wm, int wn,
+                                           int h, int l32, int M, int N, int ldo, const float* __restrict__ residual,
+                                           void* __restrict__ out) {
+    constexpr int WM = ATile<BM>::WM, MI = ATile<BM>::MI;
+    constexpr bool WIDE = EPI >= 4;
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int row = m0 + wm * WM + 32 * i + 8 * (v >> 2) + 4 * h + (v & 3);
+            const int col = n0 + wn * WN + l32;
+            if constexpr (WIDE) {
+#pragma unroll
+                for (int m = 0; m < 2; ++m) {
+                    if (row < M && col + m * BN < N) {
+                        const size_t o = (size_t)row * ldo + col + m * BN;
+                        if constexpr (EPI == 5) reinterpret_cast<float*>(out)[o] = acc[m][i][v] + residual[o];
+                        else reinterpret_cast<float*>(out)[o] = acc[m][i][v];
+                    }
+                }
+            } else if (row < M && col < N) {
+                const size_t o = (size_t)row * ldo + col;
+                if constexpr (EPI >= 2) {
+                    const float g = acc[0][i][v], u = acc[NM - 1][i][v];
+                    const float hv = u * (g / (1.f + expf(-g)));   // silu(g) * u, ops.hpp:409-441
+                    if constexpr (EPI == 2) reinterpret_cast<uint16_t*>(out)[o] = (uint16_t)bf16_bits(hv);
+                    else reinterpret_cast<float*>(out)[o] = hv;
+                } else if constexpr (EPI == 1) {
+                    reinterpret_cast<float*>(out)[o] = acc[0][i][v] + residual[o];
+                } else {
+                    reinterpret_cast<float*>(out)[o] = acc[0][i][v];
+                }
+            }
+        }
+}
+
 }  // namespace lds_gemm
 
 // ldo: the row stride of out and residual (N, or the whole width when this
@@ -457,36 +498,236 @@ __global__ __launch_bounds__(lds_gemm::NT) void mfma_qgemm_lds_kernel(
 #undef VH_LDS_STEP
     }
 
-    // Accumulator v of tile i holds row 32i + 8(v/4) + 4h + v%4, column l32 of the wave block.
+    lds_gemm::store_tile<NM, EPI, BM>(acc, m0, n0, wm, wn, h, l32, M, N, ldo, residual, out);
+}
+
+// ---- GEMM over bf16 weights ---------------------------------------------------
+// out = A . W^T with W the weight's bf16 expansion (rows [N][K]): A tiles of BM
+// rows and weight tiles of BN rows are staged in LDS by direct-to-LDS loads
+// (64 elements = 128 B of a row per K step, the A tile's swizzle for both) and
+// read straight into the MFMA operands, so no wave decodes codes.  WR x WC
+// waves; a wave owns WM = BM / WR rows of A (MI MFMA tiles of 32) and
+// WNR = BN / WC weight rows (NB blocks of 32).  SwiGLU tiles hold BN / 2 gate
+// rows, then the same BN / 2 up rows; a wave's first NB / 2 blocks are gate
+// rows and the others the matching up rows, so its outputs are
+// WM x WNR / 2.  The ring is three stages deep where they fit in the 160 KiB
+// of LDS and two otherwise.
+template <int BM_, int BN_, int WR_, int WC_> struct BTile {
+    static constexpr int BM = BM_, BN = BN_, WR = WR_, WC = WC_;
+    static constexpr int NW = WR * WC, NT = 64 * NW;
+    static constexpr int WM = BM / WR, MI = WM / 32;
+    static constexpr int WNR = BN / WC, NB = WNR / 32;
+    static constexpr int A_B = BM * 128, W_B = BN * 128, ST = A_B + W_B;
+    static constexpr int A_IT = BM / (8 * NW), W_IT = BN / (8 * NW);   // 1 KiB loads per wave and step
+    static constexpr int NS = 3 * ST <= 160 * 1024 ? 3 : 2;
+    static constexpr int LPS = A_IT + W_IT;
+    static_assert(A_IT * 8 * NW == BM && W_IT * 8 * NW == BN && MI >= 1 && NB >= 2 && NB % 2 == 0, "tile shape");
+    // Every row a lane reads is l32 mod 16, so all share one swizzle.
+    static_assert(WM % 16 == 0 && WNR % 32 == 0, "row swizzle");
+};
+
+// EPI: 0 plain, 1 + residual, 2 / 3 silu(gate) * up as bf16 / f32.
+template <class T, int EPI>
+__global__ __launch_bounds__(T::NT) void mfma_bgemm_kernel(
+    const uint16_t* __restrict__ A, const uint16_t* __restrict__ ba, const uint16_t* __restrict__ bb, int M, int N,
+    int K, int ldo, const float* __restrict__ residual, void* __restrict__ out) {
+    using lds_gemm::dma16;
+    using lds_gemm::lds_addr;
+    using lds_gemm::swz_a;
+    constexpr int MI = T::MI, NB = T::NB, WM = T::WM, WNR = T::WNR, BN = T::BN;
+    constexpr int A_B = T::A_B, ST = T::ST, NS = T::NS, LPS = T::LPS, NW = T::NW;
+    constexpr bool SWIGLU = EPI >= 2;
+    __shared__ __align__(16) uint8_t lds[NS * ST];
+    const int lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave / T::WC, wn = wave % T::WC;
+    const int m0 = blockIdx.y * T::BM;
+    const int n0 = blockIdx.x * (SWIGLU ? BN / 2 : BN);   // first output column
+
+    // Sources of K step 0 (step k adds 128 B) and destinations: wave w's load
+    // `it` fills rows 8 (NW it + w) .. + 7 of the tile, lane l row + l / 8,
+    // its 16-byte chunk (l % 8) ^ swizzle.  Rows past M or N load the last row
+    // (in bounds; never stored).
+    const char* ga[T::A_IT];
+    const char* gb[T::W_IT];
+#pragma unroll
+    for (int it = 0; it < T::A_IT; ++it) {
+        const int r = (it * NW + wave) * 8 + (lane >> 3), c = (lane & 7) ^ swz_a(r);
+        ga[it] = reinterpret_cast<const char*>(A + (size_t)min(m0 + r, M - 1) * K + c * 8);
+    }
+#pragma unroll
+    for (int it = 0; it < T::W_IT; ++it) {
+        const int t = (it * NW + wave) * 8 + (lane >> 3), c = (lane & 7) ^ swz_a(t);
+        const bool up = SWIGLU && t >= BN / 2;
+        const int gn = min(n0 + (up ? t - BN / 2 : t), N - 1);
+        gb[it] = reinterpret_cast<const char*>((up ? bb : ba) + (size_t)gn * K + c * 8);
+    }
+    const uint32_t base = lds_addr(lds);
+    auto load = [&](int kt, int buf) {
+        const uint32_t sa = base + buf * ST, sb = sa + A_B;
+#pragma unroll
+        for (int it = 0; it < T::A_IT; ++it) dma16(ga[it] + (size_t)kt * 128, sa + (it * NW + wave) * 8 * 128);
+#pragma unroll
+        for (int it = 0; it < T::W_IT; ++it) dma16(gb[it] + (size_t)kt * 128, sb + (it * NW + wave) * 8 * 128);
+    };
+
+    f32x16 acc[NB][MI];
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int i = 0; i < MI; ++i) acc[b][i] = f32x16{};
+
+    // A K step is 4 groups g = 2p + q of 16 elements (lane half h holds the
+    // 16-byte chunk 2(2p + h) + q).  A wave's weight block b starts at tile
+    // row wb + boff(b): wb = wn * WNR (plain) or wn * WNR / 2 (SwiGLU: gate
+    // blocks, then the up blocks BN / 2 rows further).
+    const int sw = (l32 >> 1) & 7;
+    const int a_off = (wm * WM + l32) * 128;
+    const int b_off = A_B + ((SWIGLU ? wn * (WNR / 2) : wn * WNR) + l32) * 128;
+    auto boff = [](int b) {
+        return SWIGLU ? ((b < NB / 2 ? 0 : BN / 2) + 32 * (b % (NB / 2))) * 128 : 32 * b * 128;
+    };
+    bf16x8 fa[2][MI], fb[2][NB];
+    auto rd = [&](const uint8_t* St, int g, bf16x8 (&a)[MI], bf16x8 (&b)[NB]) {
+        const int x = 16 * ((2 * (2 * (g >> 1) + h) + (g & 1)) ^ sw);
+        const uint8_t* pa = St + a_off + x;
+        const uint8_t* pb = St + b_off + x;
+#pragma unroll
+        for (int i = 0; i < MI; ++i) a[i] = *reinterpret_cast<const bf16x8*>(pa + i * 32 * 128);
+#pragma unroll
+        for (int j = 0; j < NB; ++j) b[j] = *reinterpret_cast<const bf16x8*>(pb + boff(j));
+    };
+    auto mm = [&](const bf16x8 (&a)[MI], const bf16x8 (&b)[NB]) {
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+#pragma unroll
+            for (int i = 0; i < MI; ++i)
+                acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[j][i], 0, 0, 0);
+    };
+    // One phase: group g's MFMAs (operands in a / b) interleaved one for one
+    // with the LDS reads of the next group into the other register set
+    // (scheduling-group barriers pin the order; left alone, the compiler sinks
+    // each read next to its use and reuses one register set, so every group's
+    // read latency sits in series with its MFMAs).
+    constexpr int NR = MI + NB, NMF = MI * NB;
+    auto phase = [&](const bf16x8 (&a)[MI], const bf16x8 (&b)[NB], const uint8_t* St, int g, bf16x8 (&na)[MI],
+                     bf16x8 (&nb)[NB]) {
+        mm(a, b);
+        rd(St, g, na, nb);
+#pragma unroll
+        for (int i = 0; i < NMF; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);              // one MFMA
+            if (i < NR) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // one LDS read
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    // The ring: NS stages, stage k % NS holds step k.  A step's barrier sits
+    // before its last group's MFMAs, whose operands are already in registers:
+    // past it every wave has read the whole stage, so the stage is refilled
+    // with step k + NS at once, and the next step's first group is read from
+    // LDS under the last group's MFMAs.  Each load is issued NS - 1 steps
+    // before the barrier that waits for it.  No MFMA sits under a branch (the
+    // accumulators would be copied at the join): after the last step the
+    // first group of the next stage is read all the same (in bounds, unused).
+    constexpr int W_ALL = 0x70;                                                     // vmcnt(0) lgkmcnt(0)
+    constexpr int W_ONE = (LPS & 15) | (7 << 4) | ((LPS >> 4) << 14);                // vmcnt(LPS) lgkmcnt(0)
+    constexpr int W_PRO = ((NS - 1) * LPS & 15) | (7 << 4) | (15 << 8) | (((NS - 1) * LPS >> 4) << 14);
+    const int nk = K / 64;
+#pragma unroll
+    for (int j = 0; j < NS; ++j)
+        if (j < nk) load(j, j);
+    if (nk >= NS) __builtin_amdgcn_s_waitcnt(W_PRO);   // step 0's loads: the oldest NS - 1 ... 0 pending
+    else __builtin_amdgcn_s_waitcnt(W_ALL);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    rd(lds, 0, fa[0], fb[0]);
+    __builtin_amdgcn_sched_barrier(0);
+    int st = 0;   // stage of step k
+    for (int k = 0; k < nk; ++k) {
+        const uint8_t* St = lds + st * ST;
+        const int sn = st + 1 == NS ? 0 : st + 1;
+        phase(fa[0], fb[0], St, 1, fa[1], fb[1]);
+        phase(fa[1], fb[1], St, 2, fa[0], fb[0]);
+        phase(fa[0], fb[0], St, 3, fa[1], fb[1]);
+        if (k + 1 < nk) {
+            // step k + 1's loads are in (with NS 3, step k + 2's may be pending)
+            if (NS == 3 && k + 2 < nk) __builtin_amdgcn_s_waitcnt(W_ONE);
+            else __builtin_amdgcn_s_waitcnt(W_ALL);
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            if (k + NS < nk) load(k + NS, st);
+        }
+        phase(fa[1], fb[1], lds + sn * ST, 0, fa[0], fb[0]);
+        st = sn;
+    }
+
+    // Accumulator v of tile (j, i) holds row 32i + 8(v/4) + 4h + v%4 of the
+    // wave's rows, weight row l32 of block j.
 #pragma unroll
     for (int i = 0; i < MI; ++i)
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
             const int row = m0 + wm * WM + 32 * i + 8 * (v >> 2) + 4 * h + (v & 3);
-            const int col = n0 + wn * WN + l32;
-            if constexpr (WIDE) {
+            if (row >= M) continue;
+            if constexpr (SWIGLU) {
 #pragma unroll
-                for (int m = 0; m < 2; ++m) {
-                    if (row < M && col + m * BN < N) {
-                        const size_t o = (size_t)row * ldo + col + m * BN;
-                        if constexpr (EPI == 5) reinterpret_cast<float*>(out)[o] = acc[m][i][v] + residual[o];
-                        else reinterpret_cast<float*>(out)[o] = acc[m][i][v];
+                for (int j = 0; j < NB / 2; ++j) {
+                    const int col = n0 + wn * (WNR / 2) + 32 * j + l32;
+                    if (col < N) {
+                        const size_t o = (size_t)row * ldo + col;
+                        const float g = acc[j][i][v], u = acc[j + NB / 2][i][v];
+                        const float hv = u * (g / (1.f + expf(-g)));   // silu(g) * u, ops.hpp:409-441
+                        if constexpr (EPI == 2) reinterpret_cast<uint16_t*>(out)[o] = (uint16_t)bf16_bits(hv);
+                        else reinterpret_cast<float*>(out)[o] = hv;
                     }
                 }
-            } else if (row < M && col < N) {
-                const size_t o = (size_t)row * ldo + col;
-                if constexpr (EPI >= 2) {
-                    const float g = acc[0][i][v], u = acc[NM - 1][i][v];
-                    const float hv = u * (g / (1.f + expf(-g)));   // silu(g) * u, ops.hpp:409-441
-                    if constexpr (EPI == 2) reinterpret_cast<uint16_t*>(out)[o] = (uint16_t)bf16_bits(hv);
-                    else reinterpret_cast<float*>(out)[o] = hv;
-                } else if constexpr (EPI == 1) {
-                    reinterpret_cast<float*>(out)[o] = acc[0][i][v] + residual[o];
-                } else {
-                    reinterpret_cast<float*>(out)[o] = acc[0][i][v];
+            } else {
+#pragma unroll
+                for (int j = 0; j < NB; ++j) {
+                    const int col = n0 + wn * WNR + 32 * j + l32;
+                    if (col < N) {
+                        const size_t o = (size_t)row * ldo + col;
+                        if constexpr (EPI == 1) reinterpret_cast<float*>(out)[o] = acc[j][i][v] + residual[o];
+                        else reinterpret_cast<float*>(out)[o] = acc[j][i][v];
+                    }
                 }
             }
         }
+}
+
+// bf16 expansion of Q8_0 / Q4_0 rows, one 32-element block per thread:
+// element = bf16(code * scale) with the conversion the GEMM's in-register
+// decode uses, so both GEMM forms multiply identical operands.  Q8_0 code e
+// is element e; Q4_0 byte j holds elements 2j (low nibble) and 2j + 1 (high),
+// both minus 8 (the oracle's orc_dequant_q4_0).
+template <int WT>
+__global__ __launch_bounds__(256) void expand_bf16_kernel(const uint8_t* __restrict__ q, const __half* __restrict__ d,
+                                                          uint16_t* __restrict__ out, size_t nblocks) {
+    const size_t b = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (b >= nblocks) return;
+    const float sc = __half2float(d[b]);
+    int e[32];
+    if constexpr (WT == VLRF_DT_Q8_0) {
+        const uint4 u0 = reinterpret_cast<const uint4*>(q + b * 32)[0], u1 = reinterpret_cast<const uint4*>(q + b * 32)[1];
+        const uint32_t w[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+        for (int i = 0; i < 32; ++i) e[i] = (int8_t)(w[i >> 2] >> (8 * (i & 3)));
+    } else {
+        const uint4 u = *reinterpret_cast<const uint4*>(q + b * 16);
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int i = 0; i < 32; ++i) e[i] = (int)((w[i >> 3] >> (4 * (i & 7))) & 0xFu) - 8;
+    }
+    uint32_t o[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const __bf16 lo = (__bf16)((float)e[2 * i] * sc), hi = (__bf16)((float)e[2 * i + 1] * sc);
+        o[i] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+    }
+    uint4* dst = reinterpret_cast<uint4*>(out + b * 32);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dst[i] = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
 }
 
 // Rows [n0, n0 + nn) of the weights (columns of the output), BM-row tiles of A.
@@ -509,6 +750,19 @@ void launch_lds_wt(hipStream_t s, const uint16_t* a, const DevWeight& w0, const 
     else
         hipLaunchKernelGGL((mfma_qgemm_lds_kernel<WT, 1, EPI, BM>), grid, dim3(lds_gemm::NT), 0, s, a, qa, da, qa, da,
                            M, nn, w0.K, w0.N, res, o);
+}
+
+// Over the weights' bf16 expansions: columns [n0, n0 + nn) of the output.
+template <class T, int EPI>
+void launch_bgemm(hipStream_t s, const uint16_t* a, const DevWeight& w0, const DevWeight* w1, int M, int n0, int nn,
+                  const float* residual, void* out) {
+    constexpr int TN = EPI >= 2 ? T::BN / 2 : T::BN;   // output columns per tile
+    const dim3 grid((nn + TN - 1) / TN, (M + T::BM - 1) / T::BM);
+    const uint16_t* ba = w0.bf + (size_t)n0 * w0.K;
+    const uint16_t* bb = EPI >= 2 ? w1->bf + (size_t)n0 * w0.K : ba;
+    const float* res = residual ? residual + n0 : nullptr;
+    void* o = EPI == 2 ? (void*)(static_cast<uint16_t*>(out) + n0) : (void*)(static_cast<float*>(out) + n0);
+    hipLaunchKernelGGL((mfma_bgemm_kernel<T, EPI>), grid, dim3(T::NT), 0, s, a, ba, bb, M, nn, w0.K, w0.N, res, o);
 }
 
 template <int EPI, int BM>
@@ -559,6 +813,35 @@ void launch_lds_plan(hipStream_t s, const LdsPlan& p, const uint16_t* a, const D
         if (p.wide) launch_lds<EW, 128>(s, a, w0, w1, M, p.n_split, w0.N - p.n_split, residual, out);
         else launch_lds<EPI, 128>(s, a, w0, w1, M, p.n_split, w0.N - p.n_split, residual, out);
     }
+}
+
+int lds_cus();
+
+// Tile plan of the GEMM over bf16 expansions, on the rule of lds_plan: 256 x 256
+// tiles (8 waves of 128 x 64) where they give at least 3/4 of a round of
+// workgroups, else 128 x 256 tiles (8 waves of 64 x 64; no decode, so 128-row
+// tiles cost no extra work per MFMA); a last round of 256-row tiles at most
+// half full runs as 128-row tiles over its columns.  Measured at the 8B layer
+// (T = 2048): four waves per workgroup with larger wave tiles (64 x 128,
+// 128 x 64, 128 x 128; one wave per SIMD) ran 12-29% slower.
+using BBig = BTile<256, 256, 2, 4>;
+using BHalf = BTile<128, 256, 2, 4>;
+
+template <int EPI>
+void launch_bgemm_plan(hipStream_t s, const uint16_t* a, const DevWeight& w0, const DevWeight* w1, int M,
+                       const float* residual, void* out) {
+    const int cus = lds_cus(), N = w0.N;
+    const int tn = EPI >= 2 ? BBig::BN / 2 : BBig::BN;   // output columns per tile
+    const int mt = (M + BBig::BM - 1) / BBig::BM, nt = (N + tn - 1) / tn;
+    const long full = (long)mt * nt, rem = full % cus;
+    if (EPI < 2 && 4 * full < 3L * cus) {
+        launch_bgemm<BHalf, EPI>(s, a, w0, w1, M, 0, N, residual, out);
+        return;
+    }
+    int n_split = N;
+    if (N % tn == 0 && full >= cus && rem > 0 && 2 * rem <= cus && rem % mt == 0) n_split = (int)((nt - rem / mt) * tn);
+    launch_bgemm<BBig, EPI>(s, a, w0, w1, M, 0, n_split, residual, out);
+    if (n_split < N) launch_bgemm<BHalf, EPI>(s, a, w0, w1, M, n_split, N - n_split, residual, out);
 }
 
 // out[r][:] = bf16(w ? rmsnorm(x[r]) * w : x[r]), one 256-lane workgroup per row
@@ -875,15 +1158,42 @@ int launch_rows_to_bf16(hipStream_t s, const float* x, const float* w, uint16_t*
     return VLRF_HIP_OK;
 }
 
+bool weight_expand_bf16(hipStream_t s, const DevWeight& w) {
+    if (w.bf) return true;
+    const char* e = getenv("VLRF_HIP_PREFILL_BF16");
+    if ((e && e[0] == '0') || !w.q || !w.d || (w.dtype != VLRF_DT_Q8_0 && w.dtype != VLRF_DT_Q4_0)) return false;
+    const size_t n = (size_t)w.N * w.K, nb = n / 32;
+    uint16_t* bf = nullptr;
+    if (hipMalloc(&bf, n * sizeof(uint16_t)) != hipSuccess) {
+        (void)hipGetLastError();   // not an error: the GEMM decodes the codes instead
+        return false;
+    }
+    const dim3 grid((unsigned)((nb + 255) / 256));
+    if (w.dtype == VLRF_DT_Q8_0) hipLaunchKernelGGL(expand_bf16_kernel<VLRF_DT_Q8_0>, grid, dim3(256), 0, s, w.q, w.d, bf, nb);
+    else hipLaunchKernelGGL(expand_bf16_kernel<VLRF_DT_Q4_0>, grid, dim3(256), 0, s, w.q, w.d, bf, nb);
+    if (hipGetLastError() != hipSuccess) {
+        (void)hipFree(bf);
+        return false;
+    }
+    w.bf = bf;
+    return true;
+}
+
 int launch_qgemm(hipStream_t s, const DevWeight& w, const uint16_t* a, int M, const float* residual,
                  float* y) {
     int rc = check_qgemm(w, M);
     if (rc) return rc;
     VH_ARG(a && y, "qgemm: null operand");
     if (M > 128) {
-        const LdsPlan p = lds_plan(M, w.N, false, lds_cus());
-        if (residual) launch_lds_plan<1>(s, p, a, w, nullptr, M, residual, y);
-        else launch_lds_plan<0>(s, p, a, w, nullptr, M, nullptr, y);
+        weight_expand_bf16(s, w);
+        if (w.bf) {
+            if (residual) launch_bgemm_plan<1>(s, a, w, nullptr, M, residual, y);
+            else launch_bgemm_plan<0>(s, a, w, nullptr, M, nullptr, y);
+        } else {
+            const LdsPlan p = lds_plan(M, w.N, false, lds_cus());
+            if (residual) launch_lds_plan<1>(s, p, a, w, nullptr, M, residual, y);
+            else launch_lds_plan<0>(s, p, a, w, nullptr, M, nullptr, y);
+        }
     } else {
         if (residual) launch_cfg<CfgSmall, 1>(s, w.dtype, a, w, nullptr, M, residual, y);
         else launch_cfg<CfgSmall, 0>(s, w.dtype, a, w, nullptr, M, nullptr, y);
@@ -901,9 +1211,18 @@ int launch_qgemm_swiglu(hipStream_t s, const DevWeight& wg, const DevWeight& wu,
     VH_ARG(wg.N == wu.N && wg.K == wu.K && wg.dtype == wu.dtype, "qgemm_swiglu: gate/up differ");
     VH_ARG(a && h, "qgemm_swiglu: null operand");
     if (M > 128) {
-        const LdsPlan p = lds_plan(M, wg.N, true, lds_cus());
-        if (h_bf16) launch_lds_plan<2>(s, p, a, wg, &wu, M, nullptr, h);
-        else launch_lds_plan<3>(s, p, a, wg, &wu, M, nullptr, h);
+        if (weight_expand_bf16(s, wg) && !weight_expand_bf16(s, wu)) {
+            (void)hipFree(wg.bf);   // both or neither
+            wg.bf = nullptr;
+        }
+        if (wg.bf) {
+            if (h_bf16) launch_bgemm_plan<2>(s, a, wg, &wu, M, nullptr, h);
+            else launch_bgemm_plan<3>(s, a, wg, &wu, M, nullptr, h);
+        } else {
+            const LdsPlan p = lds_plan(M, wg.N, true, lds_cus());
+            if (h_bf16) launch_lds_plan<2>(s, p, a, wg, &wu, M, nullptr, h);
+            else launch_lds_plan<3>(s, p, a, wg, &wu, M, nullptr, h);
+        }
     } else {
         if (h_bf16) launch_cfg<CfgSmall, 2>(s, wg.dtype, a, wg, &wu, M, nullptr, h);
         else launch_cfg<CfgSmall, 3>(s, wg.dtype, a, wg, &wu, M, nullptr, h);

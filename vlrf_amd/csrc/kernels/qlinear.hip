@@ -186,17 +186,42 @@ using gemv::kGemvMaxK;
 using gemv::kGemvMaxOneGroups;
 using gemv::kGemvWaves;
 
+// XM & 64 (argmax form): besides y, the workgroup's largest output and its
+// first row go to argp[blockIdx.x] (value, row bits) -- the first level of the
+// greedy step's argmax (transformer.hpp:43-47), so the step kernel reduces one
+// pair per workgroup instead of every logit.  A wave meets its rows in
+// increasing order, so keeping strictly larger values keeps the first maximum.
 template <int WT, int NC, int RPW, bool SWIGLU, int XM>
 __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(
     const uint8_t* __restrict__ qa, const __half* __restrict__ da, const uint8_t* __restrict__ qb,
     const __half* __restrict__ db, int N, int K, const float* __restrict__ x,
     const int* __restrict__ x_row, float* x_copy, const float* __restrict__ norm_w, float eps,
-    const float* residual, float* y, int nparts) {
-    gemv::gemv_body<WT, NC, RPW, SWIGLU, XM>(qa, da, qb, db, N, K, x, x_row, x_copy, norm_w, eps, nparts, blockIdx.x,
+    const float* residual, float* y, int nparts, float2* argp) {
+    constexpr int GM = XM & ~64;   // the GEMV's own form
+    float best = -INFINITY;
+    int bidx = -1;                 // lane 0 of each wave
+    gemv::gemv_body<WT, NC, RPW, SWIGLU, GM>(qa, da, qb, db, N, K, x, x_row, x_copy, norm_w, eps, nparts, blockIdx.x,
                                               gridDim.x, [&](int row, float out) {
                                                   if constexpr ((XM & 4) != 0) out = out + residual[row];
                                                   y[row] = out;
+                                                  if constexpr ((XM & 64) != 0)
+                                                      if (bidx < 0 || out > best) { best = out; bidx = row; }
                                               });
+    if constexpr ((XM & 64) != 0) {
+        __shared__ float sb[kGemvWaves];
+        __shared__ int si[kGemvWaves];
+        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+        if (lane == 0) { sb[wave] = best; si[wave] = bidx; }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            for (int w = 0; w < kGemvWaves; ++w)
+                if (si[w] >= 0 && (bidx < 0 || sb[w] > best || (sb[w] == best && si[w] < bidx))) {
+                    best = sb[w];
+                    bidx = si[w];
+                }
+            argp[blockIdx.x] = make_float2(best, __int_as_float(bidx));
+        }
+    }
 }
 
 // The wide-row form (K up to kGemvWideMaxK, one row per wave) held to 128
@@ -216,7 +241,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) __attribute__((amdgpu_waves_per_eu
 template <int WT, bool SWIGLU>
 int launch_gemv(hipStream_t s, const DevWeight& a, const DevWeight* b, const float* x, float* y,
                 const float* norm_w, float eps, const float* residual, const int* x_row = nullptr,
-                float* x_copy = nullptr, int nparts = 0, int head_dim = 64) {
+                float* x_copy = nullptr, int nparts = 0, int head_dim = 64, float2* argp = nullptr) {
     constexpr int CW = 64 * Gemv<WT>::EPL;
     const int nc = (a.K + CW - 1) / CW;
     const uint8_t* qb = b ? b->q : nullptr;
@@ -227,8 +252,10 @@ int launch_gemv(hipStream_t s, const DevWeight& a, const DevWeight* b, const flo
            "gemv: chunk merge takes a plain x of whole 64-wide heads and at most %d chunks", kAttnMaxChunks);
     const int groups1 = (a.N + kGemvWaves - 1) / kGemvWaves;
     const bool one = groups1 <= kGemvMaxOneGroups;       // RPW 1: one row per wave
+    VH_ARG(!argp || (norm_w && !x_row && !residual && !nparts && !one && !SWIGLU),
+           "gemv: the argmax form is the normalised LM head's row loop");
     const int xm = (x_row ? 2 : 0) | (norm_w ? 1 : 0) | (residual ? 4 : 0) | (nparts ? 8 : 0) | (one ? 16 : 0) |
-                   (nparts && head_dim == 128 ? 32 : 0);
+                   (nparts && head_dim == 128 ? 32 : 0) | (argp ? 64 : 0);
     VH_ARG(!nparts || head_dim == 64 || (head_dim == 128 && xm == 60 && a.K % 128 == 0),
            "gemv: chunk merge of head dim %d (form %d)", head_dim, xm);
 #define VH_GEMV_XM(NC, RPW, XM)                                                                            \
@@ -236,12 +263,13 @@ int launch_gemv(hipStream_t s, const DevWeight& a, const DevWeight* b, const flo
         const int groups = (a.N + kGemvWaves * (RPW)-1) / (kGemvWaves * (RPW));                            \
         dim3 grid(((XM)&16) || groups < kGemvMaxGroups ? groups : kGemvMaxGroups);                         \
         hipLaunchKernelGGL((gemv_kernel<WT, NC, RPW, SWIGLU, XM>), grid, dim3(64 * kGemvWaves), 0, s, a.q, \
-                           a.d, qb, db, a.N, a.K, x, x_row, x_copy, norm_w, eps, residual, y, nparts);      \
+                           a.d, qb, db, a.N, a.K, x, x_row, x_copy, norm_w, eps, residual, y, nparts, argp); \
     } while (0)
 #define VH_GEMV(NC, RPW)                                                   \
     do {                                                                  \
         if (xm == 0) VH_GEMV_XM(NC, RPW, 0);                              \
         else if (xm == 1) VH_GEMV_XM(NC, RPW, 1);                         \
+        else if (xm == 65) VH_GEMV_XM(NC, RPW, 65);                       \
         else if (xm == 16) VH_GEMV_XM(NC, RPW, 16);                       \
         else if (xm == 17) VH_GEMV_XM(NC, RPW, 17);                       \
         else if constexpr (!SWIGLU) {                                     \
@@ -331,6 +359,22 @@ int launch_qlinear(hipStream_t s, const DevWeight& w, const float* x, float* y, 
         case VLRF_DT_Q4_0: return dispatch_m<VLRF_DT_Q4_0, false>(s, w, nullptr, x, y, M, norm_w, eps, residual);
         default:           return dispatch_m<VLRF_DT_F32, false>(s, w, nullptr, x, y, M, norm_w, eps, residual);
     }
+}
+
+bool qlinear_argmax_supported(const DevWeight& w) {
+    return gemv_fits(w) && (w.N + kGemvWaves - 1) / kGemvWaves > kGemvMaxOneGroups;
+}
+
+int launch_qlinear_argmax(hipStream_t s, const DevWeight& w, const float* x, float* y, const float* norm_w,
+                          float eps, float2* pairs, int* npairs) {
+    int rc = check_weight(w);
+    if (rc) return rc;
+    VH_ARG(qlinear_argmax_supported(w) && norm_w && x && y && pairs, "qlinear_argmax: not supported");
+    const int groups = (w.N + kGemvWaves - 1) / kGemvWaves;
+    *npairs = groups < kGemvMaxGroups ? groups : kGemvMaxGroups;
+    if (w.dtype == VLRF_DT_Q8_0)
+        return launch_gemv<VLRF_DT_Q8_0, false>(s, w, nullptr, x, y, norm_w, eps, nullptr, nullptr, nullptr, 0, 64, pairs);
+    return launch_gemv<VLRF_DT_Q4_0, false>(s, w, nullptr, x, y, norm_w, eps, nullptr, nullptr, nullptr, 0, 64, pairs);
 }
 
 bool qlinear_gather_supported(const DevWeight& w) { return gemv_fits(w); }

@@ -68,6 +68,7 @@ struct vlrf_hip_model {
     const float* cos_t = nullptr;
     const float* sin_t = nullptr;
     float *x = nullptr, *qkv = nullptr, *att = nullptr, *h = nullptr, *logits = nullptr, *part = nullptr;
+    float2* argpairs = nullptr;   // [512] the LM head's per-workgroup (max, first index)
     int nch = 0;               // decode attention in chunked form (merged by the O GEMV) when > 0
     int nparts = 0;            // partials per head: nch, plus the token's own key when fused
     float* chunks = nullptr;   // its partials [H][nparts][kAttnChunkStride]
@@ -179,8 +180,16 @@ int enqueue_step(vlrf_hip_model* m, hipStream_t s) {
         if (!rc) rc = launch_qlinear_swiglu(s, Ly.wg, Ly.wu, m->x, m->h, 1, Ly.ln2, eps);
         if (!rc) rc = launch_qlinear(s, Ly.wd, m->h, m->x, 1, nullptr, 0.f, m->x);
     }
-    if (!rc) rc = launch_qlinear(s, m->lm_head, m->x, m->logits, 1, m->ln_final, eps, nullptr);
-    if (!rc) rc = launch_argmax_step(s, m->logits, m->V, m->state, m->gen_ids, m->S);
+    if (qlinear_argmax_supported(m->lm_head)) {
+        // The LM head's workgroups leave (max, first index) pairs: the argmax
+        // step reduces those instead of the 32000 logits.
+        int np = 0;
+        if (!rc) rc = launch_qlinear_argmax(s, m->lm_head, m->x, m->logits, m->ln_final, eps, m->argpairs, &np);
+        if (!rc) rc = launch_argmax_pairs_step(s, m->argpairs, np, m->state, m->gen_ids, m->S);
+    } else {
+        if (!rc) rc = launch_qlinear(s, m->lm_head, m->x, m->logits, 1, m->ln_final, eps, nullptr);
+        if (!rc) rc = launch_argmax_step(s, m->logits, m->V, m->state, m->gen_ids, m->S);
+    }
     return rc;
 }
 
@@ -410,6 +419,7 @@ int vlrf_hip_model_create(vlrf_hip_ctx_t ctx, const vlrf_hip_model_config* cfg, 
     dalloc((void**)&m->att, (size_t)m->D * 4);
     dalloc((void**)&m->h, (size_t)m->F * 4);
     dalloc((void**)&m->logits, (size_t)m->V * 4);
+    dalloc((void**)&m->argpairs, 512 * sizeof(float2));
     dalloc((void**)&m->part, (size_t)m->H * m->n_splits * (dh + 2) * 4);
     // Chunked decode attention when the O projection's GEMV can merge it.
     m->nch = c.weight_dtype == VLRF_DT_Q8_0 || c.weight_dtype == VLRF_DT_Q4_0
@@ -532,7 +542,7 @@ void vlrf_hip_model_destroy(vlrf_hip_model_t m) {
     }
     weight_release(m->lm_head);
     for (void* p : {(void*)m->embed, (void*)m->ln_final, (void*)m->x, (void*)m->qkv, (void*)m->att,
-                    (void*)m->h, (void*)m->logits, (void*)m->part, (void*)m->chunks, (void*)m->state,
+                    (void*)m->h, (void*)m->logits, (void*)m->argpairs, (void*)m->part, (void*)m->chunks, (void*)m->state,
                     (void*)m->gen_ids, (void*)m->prompt})
         if (p) (void)hipFree(p);
     for (void* p : {(void*)m->pf_x, (void*)m->pf_qkv, (void*)m->pf_a, (void*)m->pf_att, (void*)m->pf_h,
