@@ -504,26 +504,32 @@ __global__ __launch_bounds__(lds_gemm::NT) void mfma_qgemm_lds_kernel(
 // ---- GEMM over bf16 weights ---------------------------------------------------
 // out = A . W^T with W the weight's bf16 expansion (rows [N][K]): A tiles of BM
 // rows and weight tiles of BN rows are staged in LDS by direct-to-LDS loads
-// (64 elements = 128 B of a row per K step, the A tile's swizzle for both) and
-// read straight into the MFMA operands, so no wave decodes codes.  WR x WC
+// (BK elements = 2 BK bytes of a row per K step, the 16-byte chunks of row r
+// swizzled by (r / 2) mod chunks, for both) and read straight into the MFMA
+// operands, so no wave decodes codes.  WR x WC
 // waves; a wave owns WM = BM / WR rows of A (MI MFMA tiles of 32) and
 // WNR = BN / WC weight rows (NB blocks of 32).  SwiGLU tiles hold BN / 2 gate
 // rows, then the same BN / 2 up rows; a wave's first NB / 2 blocks are gate
 // rows and the others the matching up rows, so its outputs are
-// WM x WNR / 2.  The ring is three stages deep where they fit in the 160 KiB
-// of LDS and two otherwise.
-template <int BM_, int BN_, int WR_, int WC_> struct BTile {
-    static constexpr int BM = BM_, BN = BN_, WR = WR_, WC = WC_;
+// WM x WNR / 2.  The ring holds as many stages as fit in the 160 KiB of LDS,
+// at most four.
+template <int BM_, int BN_, int WR_, int WC_, int BK_ = 64> struct BTile {
+    static constexpr int BM = BM_, BN = BN_, WR = WR_, WC = WC_, BK = BK_;
     static constexpr int NW = WR * WC, NT = 64 * NW;
     static constexpr int WM = BM / WR, MI = WM / 32;
     static constexpr int WNR = BN / WC, NB = WNR / 32;
-    static constexpr int A_B = BM * 128, W_B = BN * 128, ST = A_B + W_B;
-    static constexpr int A_IT = BM / (8 * NW), W_IT = BN / (8 * NW);   // 1 KiB loads per wave and step
-    static constexpr int NS = 3 * ST <= 160 * 1024 ? 3 : 2;
+    static constexpr int RB = 2 * BK, CPR = RB / 16, RPL = 1024 / RB;   // row bytes, chunks, rows per 1 KiB
+    static constexpr int NG = BK / 16;                                   // MFMA k groups per step
+    static constexpr int A_B = BM * RB, W_B = BN * RB, ST = A_B + W_B;
+    static constexpr int A_IT = BM / (RPL * NW), W_IT = BN / (RPL * NW);   // 1 KiB loads per wave and step
+    static constexpr int NS = 160 * 1024 / ST < 4 ? 160 * 1024 / ST : 4;
     static constexpr int LPS = A_IT + W_IT;
-    static_assert(A_IT * 8 * NW == BM && W_IT * 8 * NW == BN && MI >= 1 && NB >= 2 && NB % 2 == 0, "tile shape");
+    static_assert(BK == 32 || BK == 64, "K step");
+    static_assert(NS >= 2 && (NS - 1) * LPS < 64, "ring");
+    static_assert(A_IT * RPL * NW == BM && W_IT * RPL * NW == BN && MI >= 1 && NB >= 2 && NB % 2 == 0, "tile shape");
     // Every row a lane reads is l32 mod 16, so all share one swizzle.
     static_assert(WM % 16 == 0 && WNR % 32 == 0, "row swizzle");
+    __device__ static int swz(int r) { return (r >> 1) & (CPR - 1); }
 };
 
 // EPI: 0 plain, 1 + residual, 2 / 3 silu(gate) * up as bf16 / f32.
@@ -533,9 +539,9 @@ __global__ __launch_bounds__(T::NT) void mfma_bgemm_kernel(
     int K, int ldo, const float* __restrict__ residual, void* __restrict__ out) {
     using lds_gemm::dma16;
     using lds_gemm::lds_addr;
-    using lds_gemm::swz_a;
     constexpr int MI = T::MI, NB = T::NB, WM = T::WM, WNR = T::WNR, BN = T::BN;
     constexpr int A_B = T::A_B, ST = T::ST, NS = T::NS, LPS = T::LPS, NW = T::NW;
+    constexpr int RB = T::RB, CPR = T::CPR, RPL = T::RPL, NG = T::NG;
     constexpr bool SWIGLU = EPI >= 2;
     __shared__ __align__(16) uint8_t lds[NS * ST];
     const int lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
@@ -544,20 +550,20 @@ __global__ __launch_bounds__(T::NT) void mfma_bgemm_kernel(
     const int m0 = blockIdx.y * T::BM;
     const int n0 = blockIdx.x * (SWIGLU ? BN / 2 : BN);   // first output column
 
-    // Sources of K step 0 (step k adds 128 B) and destinations: wave w's load
-    // `it` fills rows 8 (NW it + w) .. + 7 of the tile, lane l row + l / 8,
-    // its 16-byte chunk (l % 8) ^ swizzle.  Rows past M or N load the last row
-    // (in bounds; never stored).
+    // Sources of K step 0 (step k adds RB bytes) and destinations: wave w's
+    // load `it` fills rows RPL (NW it + w) .. + RPL - 1 of the tile, lane l row
+    // + l / CPR, its 16-byte chunk (l % CPR) ^ swizzle.  Rows past M or N load
+    // the last row (in bounds; never stored).
     const char* ga[T::A_IT];
     const char* gb[T::W_IT];
 #pragma unroll
     for (int it = 0; it < T::A_IT; ++it) {
-        const int r = (it * NW + wave) * 8 + (lane >> 3), c = (lane & 7) ^ swz_a(r);
+        const int r = (it * NW + wave) * RPL + lane / CPR, c = (lane % CPR) ^ T::swz(r);
         ga[it] = reinterpret_cast<const char*>(A + (size_t)min(m0 + r, M - 1) * K + c * 8);
     }
 #pragma unroll
     for (int it = 0; it < T::W_IT; ++it) {
-        const int t = (it * NW + wave) * 8 + (lane >> 3), c = (lane & 7) ^ swz_a(t);
+        const int t = (it * NW + wave) * RPL + lane / CPR, c = (lane % CPR) ^ T::swz(t);
         const bool up = SWIGLU && t >= BN / 2;
         const int gn = min(n0 + (up ? t - BN / 2 : t), N - 1);
         gb[it] = reinterpret_cast<const char*>((up ? bb : ba) + (size_t)gn * K + c * 8);
@@ -566,9 +572,9 @@ __global__ __launch_bounds__(T::NT) void mfma_bgemm_kernel(
     auto load = [&](int kt, int buf) {
         const uint32_t sa = base + buf * ST, sb = sa + A_B;
 #pragma unroll
-        for (int it = 0; it < T::A_IT; ++it) dma16(ga[it] + (size_t)kt * 128, sa + (it * NW + wave) * 8 * 128);
+        for (int it = 0; it < T::A_IT; ++it) dma16(ga[it] + (size_t)kt * RB, sa + (it * NW + wave) * 1024);
 #pragma unroll
-        for (int it = 0; it < T::W_IT; ++it) dma16(gb[it] + (size_t)kt * 128, sb + (it * NW + wave) * 8 * 128);
+        for (int it = 0; it < T::W_IT; ++it) dma16(gb[it] + (size_t)kt * RB, sb + (it * NW + wave) * 1024);
     };
 
     f32x16 acc[NB][MI];
@@ -577,15 +583,15 @@ __global__ __launch_bounds__(T::NT) void mfma_bgemm_kernel(
 #pragma unroll
         for (int i = 0; i < MI; ++i) acc[b][i] = f32x16{};
 
-    // A K step is 4 groups g = 2p + q of 16 elements (lane half h holds the
+    // A K step is NG groups g = 2p + q of 16 elements (lane half h holds the
     // 16-byte chunk 2(2p + h) + q).  A wave's weight block b starts at tile
     // row wb + boff(b): wb = wn * WNR (plain) or wn * WNR / 2 (SwiGLU: gate
     // blocks, then the up blocks BN / 2 rows further).
-    const int sw = (l32 >> 1) & 7;
-    const int a_off = (wm * WM + l32) * 128;
-    const int b_off = A_B + ((SWIGLU ? wn * (WNR / 2) : wn * WNR) + l32) * 128;
+    const int sw = T::swz(l32);
+    const int a_off = (wm * WM + l32) * RB;
+    const int b_off = A_B + ((SWIGLU ? wn * (WNR / 2) : wn * WNR) + l32) * RB;
     auto boff = [](int b) {
-        return SWIGLU ? ((b < NB / 2 ? 0 : BN / 2) + 32 * (b % (NB / 2))) * 128 : 32 * b * 128;
+        return SWIGLU ? ((b < NB / 2 ? 0 : BN / 2) + 32 * (b % (NB / 2))) * RB : 32 * b * RB;
     };
     bf16x8 fa[2][MI], fb[2][NB];
     auto rd = [&](const uint8_t* St, int g, bf16x8 (&a)[MI], bf16x8 (&b)[NB]) {
@@ -593,7 +599,7 @@ __global__ __launch_bounds__(T::NT) void mfma_bgemm_kernel(
         const uint8_t* pa = St + a_off + x;
         const uint8_t* pb = St + b_off + x;
 #pragma unroll
-        for (int i = 0; i < MI; ++i) a[i] = *reinterpret_cast<const bf16x8*>(pa + i * 32 * 128);
+        for (int i = 0; i < MI; ++i) a[i] = *reinterpret_cast<const bf16x8*>(pa + i * 32 * RB);
 #pragma unroll
         for (int j = 0; j < NB; ++j) b[j] = *reinterpret_cast<const bf16x8*>(pb + boff(j));
     };
@@ -630,10 +636,10 @@ __global__ __launch_bounds__(T::NT) void mfma_bgemm_kernel(
     // before the barrier that waits for it.  No MFMA sits under a branch (the
     // accumulators would be copied at the join): after the last step the
     // first group of the next stage is read all the same (in bounds, unused).
-    constexpr int W_ALL = 0x70;                                                     // vmcnt(0) lgkmcnt(0)
-    constexpr int W_ONE = (LPS & 15) | (7 << 4) | ((LPS >> 4) << 14);                // vmcnt(LPS) lgkmcnt(0)
+    constexpr int W_ALL = 0x70;                                                           // vmcnt(0) lgkmcnt(0)
+    constexpr int W_IN = ((NS - 2) * LPS & 15) | (7 << 4) | (((NS - 2) * LPS >> 4) << 14);   // vmcnt((NS-2) LPS) lgkmcnt(0)
     constexpr int W_PRO = ((NS - 1) * LPS & 15) | (7 << 4) | (15 << 8) | (((NS - 1) * LPS >> 4) << 14);
-    const int nk = K / 64;
+    const int nk = K / T::BK;
 #pragma unroll
     for (int j = 0; j < NS; ++j)
         if (j < nk) load(j, j);
@@ -648,11 +654,13 @@ __global__ __launch_bounds__(T::NT) void mfma_bgemm_kernel(
         const uint8_t* St = lds + st * ST;
         const int sn = st + 1 == NS ? 0 : st + 1;
         phase(fa[0], fb[0], St, 1, fa[1], fb[1]);
-        phase(fa[1], fb[1], St, 2, fa[0], fb[0]);
-        phase(fa[0], fb[0], St, 3, fa[1], fb[1]);
+        if constexpr (NG == 4) {
+            phase(fa[1], fb[1], St, 2, fa[0], fb[0]);
+            phase(fa[0], fb[0], St, 3, fa[1], fb[1]);
+        }
         if (k + 1 < nk) {
-            // step k + 1's loads are in (with NS 3, step k + 2's may be pending)
-            if (NS == 3 && k + 2 < nk) __builtin_amdgcn_s_waitcnt(W_ONE);
+            // step k + 1's loads are in (steps k + 2 .. k + NS - 1 may be pending)
+            if (k + NS - 1 < nk) __builtin_amdgcn_s_waitcnt(W_IN);
             else __builtin_amdgcn_s_waitcnt(W_ALL);
             __builtin_amdgcn_s_barrier();
             asm volatile("" ::: "memory");
@@ -823,13 +831,11 @@ int lds_cus();
 // tiles cost no extra work per MFMA); a last round of 256-row tiles at most
 // half full runs as 128-row tiles over its columns.  Measured at the 8B layer
 // (T = 2048): four waves per workgroup with larger wave tiles (64 x 128,
-// 128 x 64, 128 x 128; one wave per SIMD) ran 12-29% slower.
-using BBig = BTile<256, 256, 2, 4>;
-using BHalf = BTile<128, 256, 2, 4>;
-
-template <int EPI>
-void launch_bgemm_plan(hipStream_t s, const uint16_t* a, const DevWeight& w0, const DevWeight* w1, int M,
-                       const float* residual, void* out) {
+// 128 x 64, 128 x 128; one wave per SIMD) ran 12-29% slower, and 32-element K
+// steps (a ring four stages deep, twice the barriers) 4-11% slower.
+template <class BBig, class BHalf, int EPI>
+void launch_bgemm_plan_t(hipStream_t s, const uint16_t* a, const DevWeight& w0, const DevWeight* w1, int M,
+                         const float* residual, void* out) {
     const int cus = lds_cus(), N = w0.N;
     const int tn = EPI >= 2 ? BBig::BN / 2 : BBig::BN;   // output columns per tile
     const int mt = (M + BBig::BM - 1) / BBig::BM, nt = (N + tn - 1) / tn;
@@ -842,6 +848,12 @@ void launch_bgemm_plan(hipStream_t s, const uint16_t* a, const DevWeight& w0, co
     if (N % tn == 0 && full >= cus && rem > 0 && 2 * rem <= cus && rem % mt == 0) n_split = (int)((nt - rem / mt) * tn);
     launch_bgemm<BBig, EPI>(s, a, w0, w1, M, 0, n_split, residual, out);
     if (n_split < N) launch_bgemm<BHalf, EPI>(s, a, w0, w1, M, n_split, N - n_split, residual, out);
+}
+
+template <int EPI>
+void launch_bgemm_plan(hipStream_t s, const uint16_t* a, const DevWeight& w0, const DevWeight* w1, int M,
+                       const float* residual, void* out) {
+    launch_bgemm_plan_t<BTile<256, 256, 2, 4>, BTile<128, 256, 2, 4>, EPI>(s, a, w0, w1, M, residual, out);
 }
 
 // out[r][:] = bf16(w ? rmsnorm(x[r]) * w : x[r]), one 256-lane workgroup per row
