@@ -513,7 +513,7 @@ __global__ __launch_bounds__(lds_gemm::NT) void mfma_qgemm_lds_kernel(
 // rows and the others the matching up rows, so its outputs are
 // WM x WNR / 2.  The ring holds as many stages as fit in the 160 KiB of LDS,
 // at most four.
-template <int BM_, int BN_, int WR_, int WC_, int BK_ = 64> struct BTile {
+template <int BM_, int BN_, int WR_, int WC_, int BK_ = 64, int NSMAX = 4> struct BTile {
     static constexpr int BM = BM_, BN = BN_, WR = WR_, WC = WC_, BK = BK_;
     static constexpr int NW = WR * WC, NT = 64 * NW;
     static constexpr int WM = BM / WR, MI = WM / 32;
@@ -522,7 +522,7 @@ template <int BM_, int BN_, int WR_, int WC_, int BK_ = 64> struct BTile {
     static constexpr int NG = BK / 16;                                   // MFMA k groups per step
     static constexpr int A_B = BM * RB, W_B = BN * RB, ST = A_B + W_B;
     static constexpr int A_IT = BM / (RPL * NW), W_IT = BN / (RPL * NW);   // 1 KiB loads per wave and step
-    static constexpr int NS = 160 * 1024 / ST < 4 ? 160 * 1024 / ST : 4;
+    static constexpr int NS = 160 * 1024 / ST < NSMAX ? 160 * 1024 / ST : NSMAX;
     static constexpr int LPS = A_IT + W_IT;
     static_assert(BK == 32 || BK == 64, "K step");
     static_assert(NS >= 2 && (NS - 1) * LPS < 64, "ring");
@@ -830,9 +830,12 @@ int lds_cus();
 // workgroups, else 128 x 256 tiles (8 waves of 64 x 64; no decode, so 128-row
 // tiles cost no extra work per MFMA); a last round of 256-row tiles at most
 // half full runs as 128-row tiles over its columns.  Measured at the 8B layer
-// (T = 2048): four waves per workgroup with larger wave tiles (64 x 128,
-// 128 x 64, 128 x 128; one wave per SIMD) ran 12-29% slower, and 32-element K
-// steps (a ring four stages deep, twice the barriers) 4-11% slower.
+// (T = 2048), slower than this plan: four waves per workgroup with larger
+// wave tiles (64 x 128, 128 x 64, 128 x 128; one wave per SIMD) by 12-29%;
+// 32-element K steps (a ring four stages deep, twice the barriers) by 4-11%;
+// two workgroups per CU (128 x 128 or 64 x 256 tiles of 4 waves, two-stage
+// rings of 64-80 KiB, so one workgroup's barrier leaves the other computing)
+// by 8-25%.
 template <class BBig, class BHalf, int EPI>
 void launch_bgemm_plan_t(hipStream_t s, const uint16_t* a, const DevWeight& w0, const DevWeight* w1, int M,
                          const float* residual, void* out) {
