@@ -29,21 +29,7 @@ namespace attn {
 constexpr int D = 64, HALF = 32;
 constexpr float kNegInf = -INFINITY;
 
-// Signed byte K of a word as f32 in one instruction (SDWA source select with
-// sign extension; the compiler otherwise extracts the byte first).
-template <int K>
-__device__ __forceinline__ float s8f(uint32_t w) {
-    float r;
-    if constexpr (K == 0)
-        asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0" : "=v"(r) : "v"(w));
-    else if constexpr (K == 1)
-        asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1" : "=v"(r) : "v"(w));
-    else if constexpr (K == 2)
-        asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2" : "=v"(r) : "v"(w));
-    else
-        asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3" : "=v"(r) : "v"(w));
-    return r;
-}
+using gemv::s8f;
 __device__ __forceinline__ float4 s8f4(uint32_t w) { return make_float4(s8f<0>(w), s8f<1>(w), s8f<2>(w), s8f<3>(w)); }
 
 // RoPE of one pair (rope.hpp:90-96), each product rounded separately.

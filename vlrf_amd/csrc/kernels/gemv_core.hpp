@@ -29,8 +29,11 @@ namespace gemv {
 
 template <int WT>
 struct Gemv;
+// EPL: codes per lane and chunk.  BIAS: Q4_0 nibbles n are converted unsigned
+// and the dots corrected by 8 times the lane's sum of x (the codes are n - 8);
+// Q8_0 codes are converted signed in one instruction (s8f), with no bias.
 template <>
-struct Gemv<VLRF_DT_Q8_0> { static constexpr int EPL = 16; static constexpr float BIAS = 128.f; };
+struct Gemv<VLRF_DT_Q8_0> { static constexpr int EPL = 16; static constexpr float BIAS = 0.f; };
 template <>
 struct Gemv<VLRF_DT_Q4_0> { static constexpr int EPL = 32; static constexpr float BIAS = 8.f; };
 
@@ -45,6 +48,22 @@ constexpr int kGemvWaves = 8;            // waves per workgroup (one staged copy
 constexpr int kGemvThreads = 64 * kGemvWaves;
 
 __device__ __forceinline__ float ub(uint32_t v, int k) { return (float)((v >> (8 * k)) & 0xFFu); }
+
+// Signed byte K of a word as f32 in one instruction (SDWA source select with
+// sign extension; the compiler otherwise extracts the byte first).
+template <int K>
+__device__ __forceinline__ float s8f(uint32_t w) {
+    float r;
+    if constexpr (K == 0)
+        asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0" : "=v"(r) : "v"(w));
+    else if constexpr (K == 1)
+        asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1" : "=v"(r) : "v"(w));
+    else if constexpr (K == 2)
+        asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2" : "=v"(r) : "v"(w));
+    else
+        asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3" : "=v"(r) : "v"(w));
+    return r;
+}
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 // Global-memory views: a pointer read from a table in memory is otherwise a
@@ -135,9 +154,10 @@ __device__ __forceinline__ void gemv_compute(const GemvRegs<NM, RPW, NC>& R, con
                 if constexpr (WT == VLRF_DT_Q8_0) {
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
-                        const uint32_t b = u[j] ^ 0x80808080u;
-#pragma unroll
-                        for (int k = 0; k < 4; ++k) p += ub(b, k) * xv[4 * j + k];
+                        p += s8f<0>(u[j]) * xv[4 * j];
+                        p += s8f<1>(u[j]) * xv[4 * j + 1];
+                        p += s8f<2>(u[j]) * xv[4 * j + 2];
+                        p += s8f<3>(u[j]) * xv[4 * j + 3];
                     }
                 } else {
 #pragma unroll
@@ -209,7 +229,8 @@ __device__ __forceinline__ void gemv_merge(PA&& pa, PML&& pml, int nparts, int X
 // Stages the thread's x slots v (times the norm weight gw when NORM) in the
 // lane-interleaved layout with one barrier: RMSNorm (ops.hpp:488-498) is per
 // row, so W.((x*inv)*w) = inv * W.(x*w) and 1/rms (inv) is applied to the
-// dots.  xsum[c] = BIAS times the lane's sum of staged x in chunk c.
+// dots.  xsum[c] = BIAS times the lane's sum of staged x in chunk c (0 for
+// Q8_0).
 template <int WT, int NC, bool NORM>
 __device__ __forceinline__ void gemv_stage(const float4 (&v)[Shape<WT, NC>::PER], const float4 (&gw)[Shape<WT, NC>::PER],
                                            float4* xs4, float* red, int K, float eps, float& inv,
@@ -250,10 +271,12 @@ __device__ __forceinline__ void gemv_stage(const float4 (&v)[Shape<WT, NC>::PER]
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
         float sacc = 0.f;
+        if constexpr (Gemv<WT>::BIAS != 0.f) {
 #pragma unroll
-        for (int i = 0; i < EPL / 4; ++i) {
-            const float4 o = xs4[(c * (EPL / 4) + i) * 64 + lane];
-            sacc += (o.x + o.y) + (o.z + o.w);
+            for (int i = 0; i < EPL / 4; ++i) {
+                const float4 o = xs4[(c * (EPL / 4) + i) * 64 + lane];
+                sacc += (o.x + o.y) + (o.z + o.w);
+            }
         }
         xsum[c] = sacc * Gemv<WT>::BIAS;
     }
