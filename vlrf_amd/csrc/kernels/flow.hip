@@ -112,11 +112,11 @@ struct Step {
         }
         if (RPW == 1 && res_w >= 0 && ok) ok = poll_word(c, (int)((res_w + min(row0, N - 1)) * 8), lane == 0, &res);
         if (!block_ok(ok, sm.ok)) return;
-        float inv, xsum[NC];
-        gemv::gemv_stage<WT, NC, NORM>(v, gw, xs4, sm.red, K, P.eps, inv, xsum);
+        float inv;
+        gemv::gemv_stage<WT, NC, NORM>(v, gw, xs4, sm.red, K, P.eps, inv);
         const bool with_res = RPW == 1 && (res_plain || res_w >= 0);
         if (row0 < N)
-            gemv::gemv_compute<WT, NM, RPW, NC, NM == 2>(A, xs4, xsum, inv, row0, N, K, lane, [&](int row, float o) {
+            gemv::gemv_compute<WT, NM, RPW, NC, NM == 2>(A, xs4, inv, row0, N, K, lane, [&](int row, float o) {
                 if (lane == 0 && row < N) {
                     if (with_res) o = o + res;
                     put_word(P.arena + out_w + row, __float_as_uint(o), c.tag);
@@ -245,8 +245,8 @@ struct Step {
         issue_before_wait();
         const bool ok = poll_x<WT, NCD>(c, P.a.x2 + (long long)(P.L - 1) * P.a.ld_x, K, v);
         if (!block_ok(ok, sm.ok)) return;
-        float inv, xsum[NCD];
-        gemv::gemv_stage<WT, NCD, true>(v, gw, xs4, sm.red, K, P.eps, inv, xsum);
+        float inv;
+        gemv::gemv_stage<WT, NCD, true>(v, gw, xs4, sm.red, K, P.eps, inv);
         // First maximum of the rows the wave visits (rows ascend; ties keep the
         // lower index), as std::max_element over the logits.
         float best = -INFINITY;
@@ -259,11 +259,11 @@ struct Step {
         };
         for (; row0 < N; row0 += 2 * rstep) {
             const int r1 = row0 + rstep;
-            gemv::gemv_compute<WT, 1, 1, NCD, false>(A, xs4, xsum, inv, row0, N, K, lane, store);
+            gemv::gemv_compute<WT, 1, 1, NCD, false>(A, xs4, inv, row0, N, K, lane, store);
             if (r1 >= N) break;
             const int r2 = r1 + rstep;
             gemv::gemv_load<WT, 1, 1, NCD>(A, P.lm_q, P.lm_d, nullptr, nullptr, r2, N, K, lane);
-            gemv::gemv_compute<WT, 1, 1, NCD, false>(B, xs4, xsum, inv, r1, N, K, lane, store);
+            gemv::gemv_compute<WT, 1, 1, NCD, false>(B, xs4, inv, r1, N, K, lane, store);
             if (r2 >= N) break;
             gemv::gemv_load<WT, 1, 1, NCD>(B, P.lm_q, P.lm_d, nullptr, nullptr, r2 + rstep, N, K, lane);
         }

@@ -29,13 +29,13 @@ namespace gemv {
 
 template <int WT>
 struct Gemv;
-// EPL: codes per lane and chunk.  BIAS: Q4_0 nibbles n are converted unsigned
-// and the dots corrected by 8 times the lane's sum of x (the codes are n - 8);
-// Q8_0 codes are converted signed in one instruction (s8f), with no bias.
+// EPL: codes per lane and chunk.  Each code becomes an f32 in one instruction:
+// Q8_0 codes as signed bytes (s8f); Q4_0 codes n - 8 as (n - 8) / 16 (s4f), so
+// their block scales are taken times SCALE = 16 (exact).
 template <>
-struct Gemv<VLRF_DT_Q8_0> { static constexpr int EPL = 16; static constexpr float BIAS = 0.f; };
+struct Gemv<VLRF_DT_Q8_0> { static constexpr int EPL = 16; static constexpr float SCALE = 1.f; };
 template <>
-struct Gemv<VLRF_DT_Q4_0> { static constexpr int EPL = 32; static constexpr float BIAS = 8.f; };
+struct Gemv<VLRF_DT_Q4_0> { static constexpr int EPL = 32; static constexpr float SCALE = 16.f; };
 
 constexpr float kNegInfF = -INFINITY;
 constexpr int kGemvMaxK = 6144;          // staged activations: 24 KiB of LDS
@@ -46,8 +46,6 @@ constexpr int kGemvMaxGroups = 512;      // workgroups of the row loop (2 per CU
 constexpr int kGemvMaxOneGroups = 768;   // one row per wave up to 3 workgroups per CU
 constexpr int kGemvWaves = 8;            // waves per workgroup (one staged copy of x)
 constexpr int kGemvThreads = 64 * kGemvWaves;
-
-__device__ __forceinline__ float ub(uint32_t v, int k) { return (float)((v >> (8 * k)) & 0xFFu); }
 
 // Signed byte K of a word as f32 in one instruction (SDWA source select with
 // sign extension; the compiler otherwise extracts the byte first).
@@ -62,6 +60,24 @@ __device__ __forceinline__ float s8f(uint32_t w) {
         asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2" : "=v"(r) : "v"(w));
     else
         asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3" : "=v"(r) : "v"(w));
+    return r;
+}
+
+// (n - 8) / 16 for the nibble n in bits 0-3 of byte K of w ^ 0x88888888: the
+// flipped top bit makes the sign-extended 4-bit value n - 8, and the
+// conversion (v_cvt_off_f32_i4, the byte chosen by an SDWA source select)
+// divides it by 16.
+template <int K>
+__device__ __forceinline__ float s4f(uint32_t w) {
+    float r;
+    if constexpr (K == 0)
+        asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0" : "=v"(r) : "v"(w));
+    else if constexpr (K == 1)
+        asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1" : "=v"(r) : "v"(w));
+    else if constexpr (K == 2)
+        asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2" : "=v"(r) : "v"(w));
+    else
+        asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3" : "=v"(r) : "v"(w));
     return r;
 }
 
@@ -129,7 +145,7 @@ __device__ __forceinline__ void gemv_load(GemvRegs<NM, RPW, NC>& R, const uint8_
 // for SwiGLU), 1/rms applied.
 template <int WT, int NM, int RPW, int NC, bool SWIGLU, class Out>
 __device__ __forceinline__ void gemv_compute(const GemvRegs<NM, RPW, NC>& R, const float4* xs4,
-                                             const float (&xsum)[NC], float inv, int row0, int N, int K,
+                                             float inv, int row0, int N, int K,
                                              int lane, Out&& out) {
     constexpr int EPL = Gemv<WT>::EPL;
     float acc[NM][RPW];
@@ -162,18 +178,21 @@ __device__ __forceinline__ void gemv_compute(const GemvRegs<NM, RPW, NC>& R, con
                 } else {
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
-                        const uint32_t lo = u[j] & 0x0F0F0F0Fu, hi = (u[j] >> 4) & 0x0F0F0F0Fu;
-#pragma unroll
-                        for (int k = 0; k < 4; ++k) {
-                            // byte 4j+k holds elements 2(4j+k) (low) and 2(4j+k)+1 (high)
-                            p += ub(lo, k) * xv[8 * j + 2 * k];
-                            p += ub(hi, k) * xv[8 * j + 2 * k + 1];
-                        }
+                        // byte 4j+k holds elements 2(4j+k) (low nibble) and 2(4j+k)+1 (high)
+                        const uint32_t w = u[j] ^ 0x88888888u, w4 = w >> 4;
+                        p += s4f<0>(w) * xv[8 * j];
+                        p += s4f<0>(w4) * xv[8 * j + 1];
+                        p += s4f<1>(w) * xv[8 * j + 2];
+                        p += s4f<1>(w4) * xv[8 * j + 3];
+                        p += s4f<2>(w) * xv[8 * j + 4];
+                        p += s4f<2>(w4) * xv[8 * j + 5];
+                        p += s4f<3>(w) * xv[8 * j + 6];
+                        p += s4f<3>(w4) * xv[8 * j + 7];
                     }
                 }
                 const bool in = row0 + r < N && c * (64 * EPL) + lane * EPL < K;
-                const float sc = in ? __half2float(__ushort_as_half((unsigned short)R.s[m][r][c])) : 0.f;
-                acc[m][r] = fmaf(sc, p - xsum[c], acc[m][r]);
+                const float sc = in ? __half2float(__ushort_as_half((unsigned short)R.s[m][r][c])) * Gemv<WT>::SCALE : 0.f;
+                acc[m][r] = fmaf(sc, p, acc[m][r]);
             }
     }
 #pragma unroll
@@ -229,12 +248,10 @@ __device__ __forceinline__ void gemv_merge(PA&& pa, PML&& pml, int nparts, int X
 // Stages the thread's x slots v (times the norm weight gw when NORM) in the
 // lane-interleaved layout with one barrier: RMSNorm (ops.hpp:488-498) is per
 // row, so W.((x*inv)*w) = inv * W.(x*w) and 1/rms (inv) is applied to the
-// dots.  xsum[c] = BIAS times the lane's sum of staged x in chunk c (0 for
-// Q8_0).
+// dots.
 template <int WT, int NC, bool NORM>
 __device__ __forceinline__ void gemv_stage(const float4 (&v)[Shape<WT, NC>::PER], const float4 (&gw)[Shape<WT, NC>::PER],
-                                           float4* xs4, float* red, int K, float eps, float& inv,
-                                           float (&xsum)[NC]) {
+                                           float4* xs4, float* red, int K, float eps, float& inv) {
     constexpr int EPL = Gemv<WT>::EPL, CW = Shape<WT, NC>::CW;
     constexpr int XF4 = Shape<WT, NC>::XF4, PER = Shape<WT, NC>::PER;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -267,18 +284,6 @@ __device__ __forceinline__ void gemv_stage(const float4 (&v)[Shape<WT, NC>::PER]
 #pragma unroll
         for (int w = 0; w < kGemvWaves; ++w) ss += red[w];
         inv = 1.f / sqrtf(ss / (float)K + eps);
-    }
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-        float sacc = 0.f;
-        if constexpr (Gemv<WT>::BIAS != 0.f) {
-#pragma unroll
-            for (int i = 0; i < EPL / 4; ++i) {
-                const float4 o = xs4[(c * (EPL / 4) + i) * 64 + lane];
-                sacc += (o.x + o.y) + (o.z + o.w);
-            }
-        }
-        xsum[c] = sacc * Gemv<WT>::BIAS;
     }
 }
 
@@ -326,7 +331,6 @@ __device__ __forceinline__ void gemv_body(const uint8_t* __restrict__ qa, const 
     // into registers instead of staging it once per workgroup was measured
     // slower: 16 waves per CU re-reading x and the norm weight cost more L1
     // bandwidth than the two barriers.)
-    float xsum[NC];
     float inv = 1.f;                                  // 1/rms, applied to the finished dots
     GemvRegs<NM, RPW, NC> A, B;
     {
@@ -377,24 +381,24 @@ __device__ __forceinline__ void gemv_body(const uint8_t* __restrict__ qa, const 
                 if (f < XF4 && 4 * f < K) reinterpret_cast<float4*>(x_copy)[f] = v[p];
             }
         }
-        gemv_stage<WT, NC, NORM>(v, gw, xs4, red, K, eps, inv, xsum);
+        gemv_stage<WT, NC, NORM>(v, gw, xs4, red, K, eps, inv);
     }
 
     auto store = [&](int row, float out) {
         if (lane == 0 && row < N) st(row, out);
     };
     if constexpr (ONE) {
-        if (row0 < N) gemv_compute<WT, NM, RPW, NC, SWIGLU>(A, xs4, xsum, inv, row0, N, K, lane, store);
+        if (row0 < N) gemv_compute<WT, NM, RPW, NC, SWIGLU>(A, xs4, inv, row0, N, K, lane, store);
         return;
     }
     // Loads stay unconditional inside the loop as well (see gemv_load).
     for (; row0 < N; row0 += 2 * rstep) {
         const int r1 = row0 + rstep;
-        gemv_compute<WT, NM, RPW, NC, SWIGLU>(A, xs4, xsum, inv, row0, N, K, lane, store);
+        gemv_compute<WT, NM, RPW, NC, SWIGLU>(A, xs4, inv, row0, N, K, lane, store);
         if (r1 >= N) break;
         const int r2 = r1 + rstep;
         gemv_load<WT, NM, RPW, NC>(A, qa, da, qb, db, r2, N, K, lane);
-        gemv_compute<WT, NM, RPW, NC, SWIGLU>(B, xs4, xsum, inv, r1, N, K, lane, store);
+        gemv_compute<WT, NM, RPW, NC, SWIGLU>(B, xs4, inv, r1, N, K, lane, store);
         if (r2 >= N) break;
         gemv_load<WT, NM, RPW, NC>(B, qa, da, qb, db, r2 + rstep, N, K, lane);
     }
