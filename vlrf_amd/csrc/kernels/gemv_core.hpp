@@ -200,7 +200,11 @@ __device__ __forceinline__ void gemv_compute(const GemvRegs<NM, RPW, NC>& R, con
         float o = wave_sum(acc[0][r]) * inv;
         if constexpr (SWIGLU) {
             const float u = wave_sum(acc[1][r]) * inv;
-            o = u * (o / (1.f + expf(-o)));   // silu(g) * u, ops.hpp:409-441
+            // silu(g) * u (ops.hpp:409-441) with the hardware exp and
+            // reciprocal (about 1 ulp each): once per row and wave, on the
+            // finished dots, where the correctly rounded forms cost ~20
+            // instructions
+            o = u * (o * __builtin_amdgcn_rcpf(1.f + __expf(-o)));
         }
         out(row0 + r, o);
     }
@@ -231,7 +235,7 @@ __device__ __forceinline__ void gemv_merge(PA&& pa, PML&& pml, int nparts, int X
                 const float2 ml = pml(p, c);
                 if (ml.x != kNegInfF) {
                     const float4 a = pa(p, c);
-                    const float wgt = expf(ml.x - mt);
+                    const float wgt = __expf(ml.x - mt);   // hardware exp (~1 ulp)
                     lt += wgt * ml.y;
                     o.x += wgt * a.x;
                     o.y += wgt * a.y;
@@ -283,7 +287,9 @@ __device__ __forceinline__ void gemv_stage(const float4 (&v)[Shape<WT, NC>::PER]
         ss = 0.f;
 #pragma unroll
         for (int w = 0; w < kGemvWaves; ++w) ss += red[w];
-        inv = 1.f / sqrtf(ss / (float)K + eps);
+        // 1/rms with the hardware reciprocal square root and reciprocal
+        // (~1 ulp each; the scale is applied to the finished dots)
+        inv = __builtin_amdgcn_rsqf(ss * __builtin_amdgcn_rcpf((float)K) + eps);
     }
 }
 
