@@ -400,7 +400,7 @@ __device__ __forceinline__ void chunk_q(SmemQ<NW>& sm, const Round<KVT>& R, floa
     float M = sm.wmax[0];
 #pragma unroll
     for (int k = 1; k < NW; ++k) M = fmaxf(M, sm.wmax[k]);
-    const float pe = live ? expf(sc - M) : 0.f;
+    const float pe = live ? __expf(sc - M) : 0.f;   // hardware exp (~1 ulp), on the chunk's serial path
     const float lw = wave_sum(pe);
     sm.pbuf[w][lane] = pe * R.vs;
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -558,7 +558,7 @@ __device__ __forceinline__ void chunk_q128(SmemQ128<NW>& sm, const Round128& R, 
     float M = sm.wmax[0];
 #pragma unroll
     for (int k = 1; k < NW; ++k) M = fmaxf(M, sm.wmax[k]);
-    const float pe = live ? expf(sc - M) : 0.f;
+    const float pe = live ? __expf(sc - M) : 0.f;   // hardware exp (~1 ulp), on the chunk's serial path
     const float lw = wave_sum(pe);
     sm.pbuf[w][lane] = pe * R.vs;
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");

@@ -244,7 +244,7 @@ __device__ __forceinline__ void gemv_merge(PA&& pa, PML&& pml, int nparts, int X
                 }
             }
         }
-        const float il = lt > 0.f ? 1.f / lt : 0.f;
+        const float il = lt > 0.f ? __builtin_amdgcn_rcpf(lt) : 0.f;   // hardware reciprocal (~1 ulp)
         v[p] = in ? make_float4(o.x * il, o.y * il, o.z * il, o.w * il) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
 }
