@@ -149,23 +149,25 @@ __device__ void new_row(const QkvAttnParams& P, uint32_t tag) {
         if (tid == 0) { fz.ks_w[pos] = sk; fz.vs_w[pos] = sv; }
     }
     __syncthreads();
-    // The new key's partial of head h: score q.k_stored (four interleaved sums,
-    // as the chunk's merge forms it), weight 1, value the stored V row.
-    for (int hh = tid; hh < H; hh += NT) {
-        const int g = hh / P.rep;
-        float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-#pragma unroll
-        for (int i = 0; i < attn::D / 4; ++i) {
-            const float4 qv = *reinterpret_cast<const float4*>(&sm.qs[hh * attn::D + 4 * i]);
-            const float4 kv = *reinterpret_cast<const float4*>(&sm.nk[g * attn::D + 4 * i]);
-            a0 += qv.x * kv.x;
-            a1 += qv.y * kv.y;
-            a2 += qv.z * kv.z;
-            a3 += qv.w * kv.w;
+    // The new key's partial of head h: score q.k_stored, weight 1, value the
+    // stored V row.  Each head's dot runs on one 16-lane row, 4 dims a lane,
+    // summed by row rotations (one thread per head reading its head's q row
+    // had every lane of a read on one LDS bank).
+    static_assert(attn::D == 16 * 4, "16 lanes x 4 dims per head");
+    for (int h0 = 0; h0 < H; h0 += NT / 16) {
+        const int hh = h0 + (tid >> 4), i = tid & 15, hc = min(hh, H - 1);
+        const float4 qv = *reinterpret_cast<const float4*>(&sm.qs[hc * attn::D + 4 * i]);
+        const float4 kv = *reinterpret_cast<const float4*>(&sm.nk[(hc / P.rep) * attn::D + 4 * i]);
+        float a = (qv.x * kv.x + qv.y * kv.y) + (qv.z * kv.z + qv.w * kv.w);
+        a += dpp_f<0x128>(a);   // row_ror:8
+        a += dpp_f<0x124>(a);   // row_ror:4
+        a += dpp_f<0x122>(a);   // row_ror:2
+        a += dpp_f<0x121>(a);   // row_ror:1: every lane of the row holds the sum
+        if (i == 0 && hh < H) {
+            float* pp = fz.chunks + ((size_t)hh * nparts + fz.nch) * kAttnChunkStride;
+            pp[attn::D] = a * P.scale;
+            pp[attn::D + 1] = 1.f;
         }
-        float* pp = fz.chunks + ((size_t)hh * nparts + fz.nch) * kAttnChunkStride;
-        pp[attn::D] = ((a0 + a1) + (a2 + a3)) * P.scale;
-        pp[attn::D + 1] = 1.f;
     }
     for (int e = tid; e < H * attn::D; e += NT) {
         const int hh = e / attn::D, d = e - hh * attn::D;
