@@ -147,7 +147,8 @@ int vlrf_hip_attn_decode_noalloc(vlrf_hip_kv_t kv, int layer, const float* q, fl
 int vlrf_hip_weight_upload(vlrf_hip_ctx_t ctx, const void* host, int dtype, int N, int K,
                            vlrf_hip_weight_t* out);
 void vlrf_hip_weight_free(vlrf_hip_weight_t w);
-size_t vlrf_hip_weight_bytes(vlrf_hip_weight_t w);   /* device bytes of the packed weight */
+size_t vlrf_hip_weight_bytes(vlrf_hip_weight_t w);   /* device bytes of the packed weight, plus its bf16
+                                                       expansion once a GEMM of > 128 rows made it */
 /* x, y device f32, M >= 1.  norm_w (nullable, device f32 [K]): x rows
  * are first RMS-normalised with weight norm_w and `eps` (ops.hpp:478-499).
  * residual (nullable, device f32 [M,N], may alias y): added after the product

@@ -142,3 +142,19 @@ def test_bf16_expansion_swiglu_equals_in_register_decode(ctx, monkeypatch, dtype
 
     a, b = _both_forms(monkeypatch, run)
     assert np.array_equal(a, b)
+
+
+def test_bf16_expansion_is_counted_in_the_weight_bytes(ctx):
+    """vlrf_hip_weight_bytes: the packed codes and scales, plus 2 bytes per
+    weight once a GEMM of more than 128 rows has made the bf16 expansion."""
+    N, K, M = 384, 512, 200
+    w, _ = _weight(ctx, 26, "WB", N, K, V.DT_Q8_0)
+    packed = N * K + N * (K // 32) * 2
+    assert w.device_bytes == packed
+    x = ctx.to_device(F.normal(26, "wbx", M * K).reshape(M, K))
+    y = ctx.alloc(M * N * 4)
+    ctx.qlinear(w, x, y, 8)                      # M <= 128: no expansion
+    assert w.device_bytes == packed
+    ctx.qlinear(w, x, y, M)
+    ctx.sync()
+    assert w.device_bytes == packed + 2 * N * K

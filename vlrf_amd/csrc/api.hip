@@ -564,7 +564,8 @@ void vlrf_hip_weight_free(vlrf_hip_weight_t w) {
 }
 
 size_t vlrf_hip_weight_bytes(vlrf_hip_weight_t w) {
-    return w ? weight_device_bytes(w->w.dtype, w->w.N, w->w.K) : 0;
+    if (!w) return 0;
+    return weight_device_bytes(w->w.dtype, w->w.N, w->w.K) + (w->w.bf ? (size_t)w->w.N * w->w.K * 2 : 0);
 }
 
 // M <= 16 runs the f32 GEMV / small-M kernels; larger M (prefill) runs the
