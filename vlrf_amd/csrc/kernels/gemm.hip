@@ -835,7 +835,9 @@ int lds_cus();
 // 32-element K steps (a ring four stages deep, twice the barriers) by 4-11%;
 // two workgroups per CU (128 x 128 or 64 x 256 tiles of 4 waves, two-stage
 // rings of 64-80 KiB, so one workgroup's barrier leaves the other computing)
-// by 8-25%.
+// by 8-25%; a third weight-tile stage for the 256 x 256 tiles (rings of two A
+// and three weight stages, all 160 KiB, weight loads leading by two steps) by
+// 0-2%.
 template <class BBig, class BHalf, int EPI>
 void launch_bgemm_plan_t(hipStream_t s, const uint16_t* a, const DevWeight& w0, const DevWeight* w1, int M,
                          const float* residual, void* out) {
