@@ -629,8 +629,10 @@ __global__ __launch_bounds__(512) void attn_prefill_kernel(
     constexpr int KS = D + 8, VS = kPK + 8;          // padded LDS row strides (bf16)
     constexpr int ITEMS = kPK * (D / 16);            // staging items of 16 elements per tile
     static_assert(ITEMS <= NT, "one staging item per thread");
-    __shared__ __align__(16) __bf16 Ks[kPK * KS];    // K tile [key][d]
-    __shared__ __align__(16) __bf16 Vt[D * VS];      // V tile transposed [d][vt_col(d, key)]
+    // Double-buffered: tile kt + 1 is staged into the other buffer as soon as
+    // a thread has finished computing tile kt, so one barrier per tile.
+    __shared__ __align__(16) __bf16 Ks2[2][kPK * KS];   // K tile [key][d]
+    __shared__ __align__(16) __bf16 Vt2[2][D * VS];     // V tile transposed [d][vt_col(d, key)]
 
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, hh = lane >> 5, lq = lane & 31;
     const int g = blockIdx.y, h = g * REP + w % REP;
@@ -679,10 +681,12 @@ __global__ __launch_bounds__(512) void attn_prefill_kernel(
         const int kp = kt * kPK + skey, kr = kp < kv_end ? kp : 0;
         load_raw<KVT>(raw, kq, vq, ks, vs, hb + (size_t)kr * D + 16 * spart, kr);
     };
-    if (stager) fetch(0);
-    for (int kt = 0; kt < ntile; ++kt) {
+    // Registers (tile kt) -> LDS buffer buf as bf16 (rows past kv_end zero).
+    auto stage = [&](int kt, int buf) {
+        __bf16* Ks = Ks2[buf];
+        __bf16* Vt = Vt2[buf];
         const int kv0 = kt * kPK;
-        if (stager) {                                // registers -> LDS as bf16 (rows past kv_end zero)
+        if (stager) {
             const bool live = kv0 + skey < kv_end;
             float kf[16], vf[16];                    // dequantize_row_q8_0 / f16_to_f32
             raw_f32<KVT>(raw.k, KVT == VLRF_KV_Q8_0 ? raw.sk : 1.f, live, kf);
@@ -701,10 +705,15 @@ __global__ __launch_bounds__(512) void attn_prefill_kernel(
                 Vt[d * VS + vt_col(d, skey)] = (__bf16)vf[e];
             }
         }
-        __syncthreads();
-        // The next tile's loads go out now and land while this tile is computed.
-        if (stager && kt + 1 < ntile) fetch(kt + 1);
-
+    };
+    if (stager) fetch(0);
+    stage(0, 0);
+    if (stager && ntile > 1) fetch(1);
+    __syncthreads();
+    for (int kt = 0; kt < ntile; ++kt) {
+        const int kv0 = kt * kPK;
+        const __bf16* Ks = Ks2[kt & 1];
+        const __bf16* Vt = Vt2[kt & 1];
         if (q0 < T && kv0 <= wave_last) {            // tiles wholly past this wave's queries: nothing to do
             // S^T = K . Q^T for the two 32-key blocks of the tile.
             f32x16 sc[2] = {f32x16{}, f32x16{}};
@@ -782,7 +791,12 @@ __global__ __launch_bounds__(512) void attn_prefill_kernel(
                 }
             }
         }
-        __syncthreads();                             // before the next tile overwrites Ks / Vt
+        if (kt + 1 < ntile) {   // the buffer tile kt - 1 used: every thread passed the last barrier
+            stage(kt + 1, (kt + 1) & 1);
+            // The tile after next: its loads land while tile kt + 1 is computed.
+            if (stager && kt + 2 < ntile) fetch(kt + 2);
+        }
+        __syncthreads();
     }
 
     // out[q][h*D + d] = O / l (output acc * (1/l), attention.hpp:300-307), d = 32c + 8(v/4) + 4hh + v%4.
