@@ -837,7 +837,13 @@ int lds_cus();
 // rings of 64-80 KiB, so one workgroup's barrier leaves the other computing)
 // by 8-25%; a third weight-tile stage for the 256 x 256 tiles (rings of two A
 // and three weight stages, all 160 KiB, weight loads leading by two steps) by
-// 0-2%.
+// 0-2%; for the residual GEMMs at M = 2048, N = 4096 (O and down, one round of
+// 128 x 256 tiles), 256 x 256 tiles split two ways over K (256 workgroups, the
+// second of a tile's halves to finish adding the first's partial sums, read
+// back through agent-coherent loads) by 3-4% for the layer: O 134 against
+// 94 us, down 316 against 281 us (with agent-scope fences in the join
+// instead, which write back and invalidate the XCD's L2 under the workgroups
+// still computing: 207 and 382 us).
 template <class BBig, class BHalf, int EPI>
 void launch_bgemm_plan_t(hipStream_t s, const uint16_t* a, const DevWeight& w0, const DevWeight* w1, int M,
                          const float* residual, void* out) {
