@@ -704,38 +704,36 @@ __global__ __launch_bounds__(T::NT) void mfma_bgemm_kernel(
         }
 }
 
-// bf16 expansion of Q8_0 / Q4_0 rows, one 32-element block per thread:
-// element = bf16(code * scale) with the conversion the GEMM's in-register
+// bf16 expansion of Q8_0 / Q4_0 rows, a quarter block (8 elements) per
+// thread, so a wave's code loads and 16-byte stores are each one contiguous
+// run: element = bf16(code * scale) with the conversion the GEMM's in-register
 // decode uses, so both GEMM forms multiply identical operands.  Q8_0 code e
 // is element e; Q4_0 byte j holds elements 2j (low nibble) and 2j + 1 (high),
 // both minus 8 (the oracle's orc_dequant_q4_0).
 template <int WT>
 __global__ __launch_bounds__(256) void expand_bf16_kernel(const uint8_t* __restrict__ q, const __half* __restrict__ d,
-                                                          uint16_t* __restrict__ out, size_t nblocks) {
-    const size_t b = (size_t)blockIdx.x * 256 + threadIdx.x;
-    if (b >= nblocks) return;
-    const float sc = __half2float(d[b]);
-    int e[32];
+                                                          uint16_t* __restrict__ out, size_t nparts) {
+    const size_t t = (size_t)blockIdx.x * 256 + threadIdx.x;   // elements 8t .. 8t + 7, of block t / 4
+    if (t >= nparts) return;
+    const float sc = __half2float(d[t >> 2]);
+    int e[8];
     if constexpr (WT == VLRF_DT_Q8_0) {
-        const uint4 u0 = reinterpret_cast<const uint4*>(q + b * 32)[0], u1 = reinterpret_cast<const uint4*>(q + b * 32)[1];
-        const uint32_t w[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+        const uint2 u = *reinterpret_cast<const uint2*>(q + t * 8);   // block t / 4, codes 8 (t % 4) ..
+        const uint32_t w[2] = {u.x, u.y};
 #pragma unroll
-        for (int i = 0; i < 32; ++i) e[i] = (int8_t)(w[i >> 2] >> (8 * (i & 3)));
+        for (int i = 0; i < 8; ++i) e[i] = (int8_t)(w[i >> 2] >> (8 * (i & 3)));
     } else {
-        const uint4 u = *reinterpret_cast<const uint4*>(q + b * 16);
-        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+        const uint32_t u = *reinterpret_cast<const uint32_t*>(q + t * 4);   // block t / 4, bytes 4 (t % 4) ..
 #pragma unroll
-        for (int i = 0; i < 32; ++i) e[i] = (int)((w[i >> 3] >> (4 * (i & 7))) & 0xFu) - 8;
+        for (int i = 0; i < 8; ++i) e[i] = (int)((u >> (4 * i)) & 0xFu) - 8;
     }
-    uint32_t o[16];
+    uint32_t o[4];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
+    for (int i = 0; i < 4; ++i) {
         const __bf16 lo = (__bf16)((float)e[2 * i] * sc), hi = (__bf16)((float)e[2 * i + 1] * sc);
         o[i] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
     }
-    uint4* dst = reinterpret_cast<uint4*>(out + b * 32);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) dst[i] = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
+    *reinterpret_cast<uint4*>(out + t * 8) = make_uint4(o[0], o[1], o[2], o[3]);
 }
 
 // Rows [n0, n0 + nn) of the weights (columns of the output), BM-row tiles of A.
@@ -1191,9 +1189,10 @@ bool weight_expand_bf16(hipStream_t s, const DevWeight& w) {
         (void)hipGetLastError();   // not an error: the GEMM decodes the codes instead
         return false;
     }
-    const dim3 grid((unsigned)((nb + 255) / 256));
-    if (w.dtype == VLRF_DT_Q8_0) hipLaunchKernelGGL(expand_bf16_kernel<VLRF_DT_Q8_0>, grid, dim3(256), 0, s, w.q, w.d, bf, nb);
-    else hipLaunchKernelGGL(expand_bf16_kernel<VLRF_DT_Q4_0>, grid, dim3(256), 0, s, w.q, w.d, bf, nb);
+    const size_t np = nb * 4;   // quarter blocks, one per thread
+    const dim3 grid((unsigned)((np + 255) / 256));
+    if (w.dtype == VLRF_DT_Q8_0) hipLaunchKernelGGL(expand_bf16_kernel<VLRF_DT_Q8_0>, grid, dim3(256), 0, s, w.q, w.d, bf, np);
+    else hipLaunchKernelGGL(expand_bf16_kernel<VLRF_DT_Q4_0>, grid, dim3(256), 0, s, w.q, w.d, bf, np);
     if (hipGetLastError() != hipSuccess) {
         (void)hipFree(bf);
         return false;
