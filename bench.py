@@ -367,23 +367,36 @@ def cpu_model():
     return "unknown"
 
 
-def cpu_baseline(cfg, f32w, ctx_len, budget_s=20.0, max_steps=32):
+def cpu_baseline_plan(cfg, ctx_len, max_steps):
+    """The oracle model's own configuration for the CPU leg: its cache holds
+    the ctx_len - 1 filled rows, the warm-up step and up to max_steps timed
+    steps, whatever cache the GPU model was sized for (the GPU run's --steps
+    does not bound the CPU sample)."""
+    ocfg = dict(cfg)
+    ocfg["max_seq_len"] = ctx_len + max_steps + 1
+    return ocfg
+
+
+def cpu_baseline(cfg, f32w, ctx_len, gpu_steps, budget_s=20.0, max_steps=32, threads=None):
     """Oracle decode steps at context ctx_len on every hardware thread the
     process may use."""
     import oracle
-    try:
-        ncpu = len(os.sched_getaffinity(0))
-    except AttributeError:
-        ncpu = os.cpu_count() or 1
-    threads = max(1, ncpu)
-    om = oracle.Model(cfg, f32w, n_threads=threads)
+    if threads is None:
+        try:
+            threads = len(os.sched_getaffinity(0))
+        except AttributeError:
+            threads = os.cpu_count() or 1
+    threads = max(1, threads)
+    ocfg = cpu_baseline_plan(cfg, ctx_len, max_steps)
+    om = oracle.Model(ocfg, f32w, n_threads=threads)
     om.reset()
     om.fill_kv(ctx_len - 1, seed=7)
     tok = 1
     t0 = time.perf_counter()
-    tok = om.forward([tok])                   # warm-up step
+    tok = om.forward([tok])                   # warm-up step: the cache now holds ctx_len rows
     warm = time.perf_counter() - t0
-    n = max(1, min(max_steps, int(budget_s / max(warm, 1e-3))))
+    room = ocfg["max_seq_len"] - om.used      # rows left for timed steps
+    n = max(1, min(max_steps, room, int(budget_s / max(warm, 1e-3))))
     t0 = time.perf_counter()
     for _ in range(n):
         tok = om.forward([tok])
@@ -391,7 +404,7 @@ def cpu_baseline(cfg, f32w, ctx_len, budget_s=20.0, max_steps=32):
     del om
     return {"value": round(n / dt, 3), "unit": "tok/s", "cores": threads, "kind": "port",
             "nproc": os.cpu_count(), "cpu": cpu_model(),
-            "sample": f"{n} decode steps (of the 128 timed on the GPU) of the 1.1B f32-decoded model at "
+            "sample": f"{n} decode steps (the GPU timed {gpu_steps}) of the 1.1B-shape f32-decoded model at "
                       f"context {ctx_len}-{ctx_len + n} (oracle restatement, {threads} threads = every "
                       f"hardware thread of the process's CPU set, KV cache filled with seeded codes "
                       f"instead of a CPU prefill)"}
@@ -583,8 +596,14 @@ def main():
     if not a.no_roofline:
         out["roofline"] = gemv_roofline(ctx, V, F, cfg, dtype)
     if not a.no_cpu_baseline:
+        # The GPU line is complete at this point: a failure of the CPU leg is
+        # reported in the line instead of discarding the GPU measurement.
         log("[bench] cpu baseline ...")
-        out["cpu_baseline"] = cpu_baseline(cfg, f32w, a.ctx)
+        try:
+            out["cpu_baseline"] = cpu_baseline(cfg, f32w, a.ctx, a.steps)
+        except Exception as e:       # noqa: BLE001 - reported, not hidden
+            log(f"[bench] cpu baseline failed: {e!r}")
+            out["cpu_baseline"] = {"value": None, "error": repr(e)}
     print(json.dumps(out), flush=True)
 
 

@@ -28,7 +28,7 @@ HIP_FLAGS = [
 CXX_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-pthread"]
 
 HIP_SOURCES = ["api.hip", "model.hip", "kernels/qlinear.hip", "kernels/attention.hip",
-               "kernels/elementwise.hip", "kernels/gemm.hip", "kernels/ops.hip", "kernels/flow.hip", "kernels/qkv_attn.hip"]
+               "kernels/elementwise.hip", "kernels/gemm.hip", "kernels/ops.hip", "kernels/qkv_attn.hip"]
 CXX_SOURCES = ["host/format.cpp", "host/nfw.cpp"]
 
 

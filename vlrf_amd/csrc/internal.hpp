@@ -239,73 +239,6 @@ int launch_attn_f32_tiled(hipStream_t s, const float* Q, const float* K, const f
                           float* O, int n_h, int T, int ctx_len, int d_h, float scale,
                           int causal);
 
-// ---- the decode step as one launch (kernels/flow.hip) ----------------------------
-// Per layer: the fused QKV weight, O, gate, up, down (codes and block scales),
-// the two norm weights and the layer's KV cache.
-struct FlowLayer {
-    const uint8_t* q[5] = {};
-    const __half* d[5] = {};
-    const float* ln1 = nullptr;
-    const float* ln2 = nullptr;
-    int8_t* kc = nullptr;
-    int8_t* vc = nullptr;
-    float* ks = nullptr;
-    float* vs = nullptr;
-};
-// Layers the one-launch step carries in its kernel arguments (4 KiB in all).
-constexpr int kFlowMaxLayers = 26;
-
-// Workgroups of each phase (multiples of 8, so every phase starts on XCD 0).
-struct FlowPlan {
-    int nq = 0, na = 0, no = 0, ngu = 0, nd = 0;   // per layer: QKV, attention, O, gate/up, down
-    int per_layer = 0, nlm = 0, total = 0;         // + LM head, + 8 for the argmax
-};
-
-// Word offsets into the tagged arena (64-bit words: value bits | epoch << 32)
-// and per-layer strides of its buffers.
-struct FlowArena {
-    long long words = 0;
-    long long qkv = 0, part = 0, att = 0, x1 = 0, h = 0, x2 = 0, lm = 0;
-    int ld_qkv = 0, ld_part = 0, ld_x = 0, ld_h = 0;
-};
-
-struct FlowParams {
-    int L = 0, D = 0, F = 0, H = 0, G = 0, V = 0, S = 0, nch = 0, rep = 0;
-    int w_dtype = 0, kv_dtype = 0;
-    const float* embed = nullptr;
-    const uint8_t* lm_q = nullptr;
-    const __half* lm_d = nullptr;
-    const float* ln_final = nullptr;
-    const float* cos_t = nullptr;
-    const float* sin_t = nullptr;
-    float scale = 0.f, eps = 0.f;
-    int* state = nullptr;                // [0] token, [1] position, [2] generated count, [3] epoch
-    int* gen_ids = nullptr;
-    int gen_cap = 0;
-    float* logits = nullptr;
-    uint64_t* arena = nullptr;
-    FlowArena a;
-    int gate_chunk = 0;                  // the attention chunk holding the token (per launch)
-    int* status = nullptr;               // [0] failure flag, [1] block, [2] phase, [3] layer
-    long long limit = 0;                 // wall-clock ticks one wait may last
-    FlowPlan plan;
-    FlowLayer layers[kFlowMaxLayers];
-};
-
-// The block plan and arena of the one-launch step for this shape, or ok =
-// false when the shape takes the per-kernel step (flow.hip lists why).
-struct FlowShape {
-    bool ok = false;
-    FlowPlan plan;
-    FlowArena a;
-    int nch = 0;
-};
-FlowShape flow_shape(int w_dtype, int lm_dtype, int kv_dtype, int L, int D, int F, int H, int G, int dh, int V,
-                     int S);
-// FlowParams::gate_chunk for a step at position pos.
-int flow_gate_chunk(const FlowShape& f, int pos);
-int launch_flow_step(hipStream_t s, const FlowParams& p);
-
 // A layer's QKV projection and its chunked decode attention in one launch
 // (kernels/qkv_attn.hip): the projection's rows are published as tagged words
 // (value | epoch << 32, epoch = state[3]) in `tags`, which the attention's

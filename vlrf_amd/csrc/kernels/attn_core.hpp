@@ -1,6 +1,6 @@
 // attn_core.hpp - the decode attention of one query head over one block of
 // cache rows, shared by the stand-alone decode kernel (attention.hip) and the
-// one-launch decode step (flow.hip).
+// fused QKV + attention launch (qkv_attn.hip).
 //
 // Reference semantics: AttentionBlock::flash_attn_head (attention.hpp:207-309)
 // for T = 1 (non-causal, attention.hpp:171), scale 1/sqrt(d_h)

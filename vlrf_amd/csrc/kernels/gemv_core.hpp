@@ -1,5 +1,6 @@
 // gemv_core.hpp - building blocks of the M = 1 dequant GEMV, shared by the
-// stand-alone kernel (qlinear.hip) and the one-launch decode step (flow.hip).
+// stand-alone kernel (qlinear.hip) and the fused QKV + attention launch
+// (qkv_attn.hip).
 //
 // Reference contract: compute::linear -> ops::gemm(x, W, y, 1, 0, false, true)
 // at M = 1 (include/model/compute.hpp:58-68, ops.hpp:212-252) on weights

@@ -1,6 +1,5 @@
 // tagged.hpp - exchange of values between the workgroups of one launch as
-// tagged 64-bit words, shared by the one-launch decode step (flow.hip) and the
-// fused QKV + attention launch of the per-kernel step (qkv_attn.hip).
+// tagged 64-bit words (the fused QKV + attention launch, qkv_attn.hip).
 //
 // A word holds the value's bits in its low half and the producer's epoch in
 // its high half, written with one device-scope store; it is valid when its tag

@@ -23,13 +23,6 @@
 // memory, so the whole step is captured once as a HIP graph and replayed with
 // no host round trip between steps.
 //
-// VLRF_HIP_FLOW=1 runs the same phases instead as ONE launch per step whose
-// workgroups wait for each other's tagged outputs (kernels/flow.hip), where
-// the shape allows.  It gives the same token streams but is slower on the
-// MI355X (1.1B shape, ctx 2048: 0.754 against 0.594 ms per step, same box): a
-// tagged exchange between workgroups costs 2.7-3 us, no less than a graph
-// kernel boundary plus its first-byte latency, so the per-kernel graph stays
-// the default.
 #include "internal.hpp"
 #include "runtime.hpp"
 
@@ -84,13 +77,6 @@ struct vlrf_hip_model {
     hipGraph_t graph_n = nullptr;
     hipGraphExec_t exec_n = nullptr;
     bool use_graph = true;     // VLRF_HIP_GRAPH=0: queue the step's kernels directly
-    // One-launch step (kernels/flow.hip), planned once every weight is set.
-    bool flow_allowed = false;  // VLRF_HIP_FLOW=1: the one-launch step
-    bool flow_planned = false;
-    FlowShape flow;
-    FlowParams fp;             // everything but the per-launch gate
-    uint64_t* flow_arena = nullptr;
-    int* flow_status = nullptr;         // [4] failure flag, block, phase, layer
     // Fused QKV + attention launch (kernels/qkv_attn.hip) where it applies
     // (VLRF_HIP_QKV_ATTN=0 queues the two kernels instead).
     bool qkv_attn = false;
@@ -235,97 +221,20 @@ void drop_graphs(vlrf_hip_model* m) {
     m->graph = m->graph_n = nullptr;
 }
 
-void drop_flow(vlrf_hip_model* m) {
-    for (void* p : {(void*)m->flow_arena, (void*)m->flow_status})
-        if (p) (void)hipFree(p);
-    m->flow_arena = nullptr;
-    m->flow_status = nullptr;
-    m->flow = FlowShape();
-    m->flow_planned = false;
-}
-
-// Plans the one-launch step once every weight is set (the LM head's format is
-// known only then): the layer pointers (carried in the kernel arguments), the
-// tagged arena (zero: no word carries an epoch, which starts at 1) and the
-// status words.
-int ensure_flow(vlrf_hip_model* m) {
-    if (m->flow_planned || !m->flow_allowed) return VLRF_HIP_OK;
-    m->flow_planned = true;
-    const FlowShape f = flow_shape(m->cfg.weight_dtype, m->lm_head.dtype, m->cfg.kv_dtype, m->L, m->D, m->F, m->H,
-                                   m->G, m->dh, m->V, m->S);
-    if (!f.ok) return VLRF_HIP_OK;   // the per-kernel step
-    hipStream_t s = m->ctx->stream;
-    FlowParams& p = m->fp;
-    p = FlowParams();
-    for (int l = 0; l < m->L; ++l) {
-        const Layer& Ly = m->layers[l];
-        const DevWeight* ws[5] = {&Ly.wqkv, &Ly.wo, &Ly.wg, &Ly.wu, &Ly.wd};
-        for (int i = 0; i < 5; ++i) {
-            p.layers[l].q[i] = ws[i]->q;
-            p.layers[l].d[i] = ws[i]->d;
-        }
-        p.layers[l].ln1 = Ly.ln1;
-        p.layers[l].ln2 = Ly.ln2;
-        p.layers[l].kc = Ly.kv.k;
-        p.layers[l].vc = Ly.kv.v;
-        p.layers[l].ks = Ly.kv.ks;
-        p.layers[l].vs = Ly.kv.vs;
-    }
-    if (hipMalloc((void**)&m->flow_arena, (size_t)f.a.words * 8) != hipSuccess ||
-        hipMalloc((void**)&m->flow_status, 4 * sizeof(int)) != hipSuccess) {
-        drop_flow(m);
-        set_error("model: hipMalloc of the one-launch step's buffers failed");
-        return VLRF_HIP_ERR_NOMEM;
-    }
-    VH_CHECK(hipMemsetAsync(m->flow_arena, 0, (size_t)f.a.words * 8, s));
-    VH_CHECK(hipMemsetAsync(m->flow_status, 0, 4 * sizeof(int), s));
-    VH_CHECK(hipStreamSynchronize(s));
-    p.L = m->L; p.D = m->D; p.F = m->F; p.H = m->H; p.G = m->G; p.V = m->V; p.S = m->S;
-    p.nch = f.nch;
-    p.rep = m->H / m->G;
-    p.w_dtype = m->cfg.weight_dtype;
-    p.kv_dtype = m->cfg.kv_dtype;
-    p.embed = m->embed;
-    p.lm_q = m->lm_head.q;
-    p.lm_d = m->lm_head.d;
-    p.ln_final = m->ln_final;
-    p.cos_t = m->cos_t;
-    p.sin_t = m->sin_t;
-    p.scale = 1.f / std::sqrt((float)m->dh);   // attention.hpp:373-374
-    p.eps = m->cfg.norm_eps;
-    p.state = m->state;
-    p.gen_ids = m->gen_ids;
-    p.gen_cap = m->S;
-    p.logits = m->logits;
-    p.arena = m->flow_arena;
-    p.a = f.a;
-    p.status = m->flow_status;
-    p.limit = m->wait_limit;
-    p.plan = f.plan;
-    m->flow = f;
-    return VLRF_HIP_OK;
-}
-
-// One decode step on the context stream at host position pos: the one-launch
-// step, the captured graph, or the same kernels queued one by one when graphs
-// are switched off.
-int launch_step(vlrf_hip_model* m, int pos) {
-    if (m->flow.ok) {
-        m->fp.gate_chunk = flow_gate_chunk(m->flow, pos);
-        return launch_flow_step(m->ctx->stream, m->fp);
-    }
+// One decode step on the context stream: the captured graph, or the same
+// kernels queued one by one when graphs are switched off.
+int launch_step(vlrf_hip_model* m) {
     if (!m->use_graph) return enqueue_step(m, m->ctx->stream);
     VH_CHECK(hipGraphLaunch(m->exec, m->ctx->stream));
     return VLRF_HIP_OK;
 }
 
 // After the queued steps have finished: a launch whose wait for another
-// workgroup's output ran out (the one-launch step, or the fused QKV +
-// attention launch) left its flag; report it, clear it and move to a fresh
+// workgroup's output ran out (the fused QKV + attention launch) left its flag; report it, clear it and move to a fresh
 // epoch (the failed step may have published words of the old one), and take
 // the device position as the host's.
 int check_waits(vlrf_hip_model* m) {
-    int* status = m->flow.ok ? m->flow_status : m->step_status;
+    int* status = m->step_status;
     if (!status) return VLRF_HIP_OK;
     hipStream_t s = m->ctx->stream;
     int* st = m->pinned + 4;
@@ -349,8 +258,6 @@ int check_ready(vlrf_hip_model* m) {
     VH_ARG(m != nullptr, "model: null handle");
     VH_CHECK(hipSetDevice(m->ctx->device));
     VH_ARG(m->ready(), "model: not every weight has been set");
-    const int rc = ensure_flow(m);
-    if (rc || m->flow.ok) return rc;
     return ensure_graph(m);
 }
 
@@ -402,7 +309,6 @@ int vlrf_hip_model_create(vlrf_hip_ctx_t ctx, const vlrf_hip_model_config* cfg, 
     m->n_splits = attn_decode_splits(m->S);
     m->layers.resize(m->L);
     if (const char* g = std::getenv("VLRF_HIP_GRAPH")) m->use_graph = std::strcmp(g, "0") != 0;
-    if (const char* g = std::getenv("VLRF_HIP_FLOW")) m->flow_allowed = std::strcmp(g, "1") == 0;
 
     int rc = VLRF_HIP_OK;
     auto dalloc = [&](void** p, size_t bytes) {
@@ -507,7 +413,7 @@ int vlrf_hip_model_create(vlrf_hip_ctx_t ctx, const vlrf_hip_model_config* cfg, 
         set_error("model_create: hipHostMalloc failed");
         rc = VLRF_HIP_ERR_NOMEM;
     }
-    if (!rc) {   // the one-launch step's epoch starts at 1 (its arena starts as zero words)
+    if (!rc) {   // the epoch starts at 1: the zeroed tagged words carry none
         m->pinned[0] = m->pinned[1] = m->pinned[2] = 0;
         m->pinned[3] = 1;
         if (hipMemcpy(m->state, m->pinned, 4 * sizeof(int), hipMemcpyHostToDevice) != hipSuccess) {
@@ -546,7 +452,7 @@ void vlrf_hip_model_destroy(vlrf_hip_model_t m) {
                     (void*)m->gen_ids, (void*)m->prompt})
         if (p) (void)hipFree(p);
     for (void* p : {(void*)m->pf_x, (void*)m->pf_qkv, (void*)m->pf_a, (void*)m->pf_att, (void*)m->pf_h,
-                    (void*)m->pf_ids, (void*)m->flow_arena, (void*)m->flow_status, (void*)m->qkv_tags,
+                    (void*)m->pf_ids, (void*)m->qkv_tags,
                     (void*)m->step_status})
         if (p) (void)hipFree(p);
     if (m->pinned) (void)hipHostFree(m->pinned);
@@ -585,7 +491,6 @@ int vlrf_hip_model_set_weight(vlrf_hip_model_t m, const char* name, const void* 
             VH_CHECK(hipStreamSynchronize(s));
             // The captured step graphs hold the old pointers: drop them.
             drop_graphs(m);
-            drop_flow(m);   // and the one-launch step's plan (it depends on the LM head's format)
             weight_release(m->lm_head);
             if ((rc = weight_alloc(m->lm_head, dtype, m->V, m->D))) return rc;
         }
@@ -662,7 +567,7 @@ int vlrf_hip_model_step(vlrf_hip_model_t m, int32_t token, int32_t* next, float*
     hipStream_t s = m->ctx->stream;
     m->pinned[0] = token;
     VH_CHECK(hipMemcpyAsync(m->state, m->pinned, sizeof(int), hipMemcpyHostToDevice, s));
-    if ((rc = launch_step(m, m->pos))) return rc;
+    if ((rc = launch_step(m))) return rc;
     VH_CHECK(hipMemcpyAsync(m->pinned, m->state, sizeof(int), hipMemcpyDeviceToHost, s));
     if (logits) VH_CHECK(hipMemcpyAsync(logits, m->logits, (size_t)m->V * 4, hipMemcpyDeviceToHost, s));
     VH_CHECK(hipStreamSynchronize(s));
@@ -687,7 +592,7 @@ int vlrf_hip_model_prefill(vlrf_hip_model_t m, const int32_t* ids, int n, int32_
     VH_CHECK(hipStreamSynchronize(s));
     for (int i = 0; i < n; ++i) {
         VH_CHECK(hipMemcpyAsync(m->state, m->prompt + i, sizeof(int), hipMemcpyDeviceToDevice, s));
-        if ((rc = launch_step(m, m->pos + i))) return rc;
+        if ((rc = launch_step(m))) return rc;
     }
     VH_CHECK(hipMemcpyAsync(m->pinned, m->state, sizeof(int), hipMemcpyDeviceToHost, s));
     VH_CHECK(hipStreamSynchronize(s));
@@ -839,10 +744,10 @@ int vlrf_hip_model_generate_async(vlrf_hip_model_t m, int32_t first, int n_steps
     m->pinned[2] = 0;
     VH_CHECK(hipMemcpyAsync(m->state, m->pinned, 3 * sizeof(int), hipMemcpyHostToDevice, s));
     int i = 0;
-    if (m->exec_n && !m->flow.ok)   // the steps need no host input: whole runs of kGraphSteps
+    if (m->exec_n)   // the steps need no host input: whole runs of kGraphSteps
         for (; i + kGraphSteps <= n_steps; i += kGraphSteps) VH_CHECK(hipGraphLaunch(m->exec_n, s));
     for (; i < n_steps; ++i)
-        if ((rc = launch_step(m, m->pos + i))) return rc;
+        if ((rc = launch_step(m))) return rc;
     m->pos += n_steps;
     return VLRF_HIP_OK;
 }
