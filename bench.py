@@ -8,23 +8,28 @@ through the decode step, then W warm-up decode steps), then exactly `steps`
 greedy decode steps are timed with HIP events on the library's stream
 (context 2048 -> 2048+steps).  value = steps / time (tok/s).
 
-roofline: the dominant kernel of the step, the fused RMSNorm + gate/up
-dequant-GEMV with the SwiGLU epilogue (52% of a step's bytes), timed live
-with HIP events over launches that rotate through 12 distinct weight pairs
-(295 MB, more than the 256 MB Infinity Cache), so the bytes come from HBM.
-`traffic` is the HBM bytes per launch that rocprofv3 counted (FETCH_SIZE and
-WRITE_SIZE passes over `bench.py --roofline-only`, each scaled by the same
-counter on a plain 256 MiB device copy), read from the committed summary
-profiles/gemv_swiglu_q8_1b_pmc.txt; null when that file is absent.
+step_kernels: after the timed steps, as many more greedy steps with the
+step's kernels queued one by one and every launch timed by its own start/stop
+events (vlrf_hip_model_time_launches: hipExtLaunchKernel stamps the kernel's
+own begin and end, so no marker sits between launches), on the library's
+stream.  Per kernel kind: average us per launch, launches and us per step,
+algorithmic bytes per launch at the middle context, and the GB/s and fraction
+of the 8 TB/s peak they imply (the metric's attention + GEMV breakdown), with
+the committed rocprofv3 trace's average beside it (rocprof_us, from
+profiles/decode_step_llama1b_{q8,q4}_kernel_stats.md).
 
-step_kernels: the step's time per kernel (the fused QKV + attention launch,
-O, gate/up, down, LM head, argmax) at the timed contexts, read from the
-committed rocprofv3 trace of the same workload
-(profiles/decode_step_llama1b_{q8,q4}_kernel_stats.md, the last 128 steps'
-dispatches; made with `--summarize-trace`), with each kernel's algorithmic
-bytes at context 2112 and the GB/s and fraction of peak they imply: the
-metric's attention + GEMV breakdown.  (HIP events cannot separate a step's
-launches: an event between two launches adds more than some kernels take.)
+roofline: the dominant kernel of the step by time per step, from step_kernels
+(the fused RMSNorm + QKV + RoPE + KV append + attention launch at this shape).
+`traffic` is null: a rocprofv3 counter pass over that launch has not been run
+(a profiler crash inside its dispatch interception).
+
+roofline_gemv: the fused RMSNorm + gate/up dequant-GEMV with the SwiGLU
+epilogue (52% of a step's bytes), timed with HIP events over launches that
+rotate through 12 distinct weight pairs (295 MB, more than the 256 MB
+Infinity Cache), so the bytes come from HBM; its `traffic` is the HBM bytes
+per launch that rocprofv3 counted (FETCH_SIZE and WRITE_SIZE passes over
+`bench.py --roofline-only`, each scaled by the same counter on a plain 256 MiB
+device copy), read from profiles/gemv_swiglu_q8_1b_pmc.txt.
 
 cpu_baseline: the oracle's restatement of the reference decode step
 (oracle/vlrf_oracle.c: f32 decoded weights, AVX2 streaming GEMV, full-cache
@@ -286,8 +291,6 @@ def weight_bytes(dtype, rows, cols):
     return codes + rows * (cols // 32) * 2
 
 
-# Launch kinds of a decode step, in launch order (vlrf_hip_model_step_profile).
-STEP_KINDS = ("qkv_attn", "o_proj", "gate_up", "down")
 
 
 def kernel_bytes(cfg, dtype, ctx_len, nparts):
@@ -320,17 +323,14 @@ KERNEL_KINDS = (  # (kind, pattern in the profile's kernel name)
 )
 
 
-def step_kernels(cfg, dtype, wname):
-    """Per-kernel time and algorithmic GB/s of the timed steps, from the
-    committed rocprofv3 kernel trace of the same workload
-    (profiles/decode_step_llama1b_{q8,q4}_kernel_stats.md: the last 128 steps'
-    dispatches, the steps queued without the graph so the tracer sees each
-    launch).  Event timing cannot separate the launches of a step: an event
-    between two launches adds more than some of the kernels take."""
+def profile_kernel_us(wname):
+    """Average us per launch of each kind in the committed rocprofv3 kernel
+    trace of the same workload (profiles/decode_step_llama1b_{q8,q4}_kernel_stats.md),
+    for comparison with the live event timing."""
     path = os.path.join(ROOT, "profiles", f"decode_step_llama1b_{wname[:2]}_kernel_stats.md")
     if not os.path.exists(path):
-        return None
-    calls, avg = {}, {}
+        return None, None
+    calls, tot = {}, {}
     for line in open(path):
         cells = [c.strip() for c in line.strip().strip("|").split("|")]
         if len(cells) < 7 or not cells[1].replace(".", "").isdigit():
@@ -339,22 +339,49 @@ def step_kernels(cfg, dtype, wname):
             if pat in cells[0]:
                 n, us = float(cells[1]), float(cells[2])
                 calls[kind] = calls.get(kind, 0.0) + n
-                avg[kind] = avg.get(kind, 0.0) + n * us
-    if not calls:
-        return None
-    ctx_mid = 2048 + 64
+                tot[kind] = tot.get(kind, 0.0) + n * us
+    return {k: round(tot[k] / calls[k], 3) for k in calls}, os.path.relpath(path, ROOT)
+
+
+def step_kernels(model, cfg, dtype, wname, first, steps, ctx_first):
+    """Live per-kernel breakdown of the decode step: `steps` greedy steps with
+    every launch timed by its own start/stop events (vlrf_hip_model_time_launches,
+    the kernels queued one by one), at contexts ctx_first..ctx_first+steps-1.
+    Per kind: average us per launch, launches per step, algorithmic bytes per
+    launch at the middle context and the GB/s and fraction of peak they imply."""
+    live = model.time_launches(first, steps)
+    ctx_mid = ctx_first + steps // 2
     nparts = (cfg["max_seq_len"] + 511) // 512 + 1
     nb = kernel_bytes(cfg, dtype, ctx_mid, nparts)
+    prof, src = profile_kernel_us(wname)
     out = {}
-    for kind, _ in KERNEL_KINDS:
-        if kind not in calls:
-            continue
-        us = avg[kind] / calls[kind]
-        gbs = nb[kind] / (us * 1e-6) / 1e9
-        out[kind] = {"us": round(us, 3), "bytes": int(nb[kind]), "GB/s": round(gbs, 1),
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "calls_per_step": round(calls[kind], 2)}
-    return {"kernels": out, "source": os.path.relpath(path, ROOT),
-            "bytes_at_ctx": ctx_mid}
+    for kind, (us_sum, n) in live.items():
+        us = us_sum / n
+        row = {"us": round(us, 3), "calls_per_step": round(n / steps, 2), "us_per_step": round(us_sum / steps, 2)}
+        if kind in nb:
+            gbs = nb[kind] / (us * 1e-6) / 1e9
+            row.update({"bytes": int(nb[kind]), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)})
+        if prof and kind in prof:
+            row["rocprof_us"] = prof[kind]
+        out[kind] = row
+    res = {"kernels": out, "timing": "hipExtLaunchKernel start/stop events per launch, %d steps" % steps,
+           "contexts": [ctx_first, ctx_first + steps - 1], "bytes_at_ctx": ctx_mid}
+    if src:
+        res["rocprof_source"] = src
+    return res
+
+
+def dominant_roofline(sk):
+    """The roofline object for the step's dominant kernel by time per step."""
+    kind, row = max(((k, r) for k, r in sk["kernels"].items() if "bytes" in r), key=lambda kv: kv[1]["us_per_step"])
+    names = {"qkv_attn": "qkv_attn_kernel (RMSNorm + QKV projection + RoPE + KV append + chunked attention)",
+             "gate_up": "gemv_kernel (RMSNorm + gate/up + SwiGLU)", "down": "gemv_kernel (down + residual)",
+             "o_proj": "gemv_kernel (partials merge + O projection + residual)",
+             "lm_head": "gemv_kernel (final RMSNorm + LM head + argmax pairs)"}
+    return {"kernel": names.get(kind, kind), "kind": kind, "bound": "hbm", "achieved": row["GB/s"],
+            "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": row["frac"], "traffic": None,
+            "bytes_per_launch": row["bytes"], "us_per_launch": row["us"], "us_per_step": row["us_per_step"],
+            "timing": sk["timing"]}
 
 
 def cpu_model():
@@ -531,7 +558,8 @@ def main():
         return
 
     dtype = V.DT_Q8_0 if a.dtype == "q8_0" else V.DT_Q4_0
-    cfg = F.llama_1b(max_seq_len=a.ctx + a.steps, weight_dtype=dtype)
+    # Room for the timed steps and, after them, as many steps timed launch by launch.
+    cfg = F.llama_1b(max_seq_len=a.ctx + 2 * a.steps, weight_dtype=dtype)
     ctx = V.Context(0)
     log("[bench]", ctx.device_info())
     if a.roofline_only:
@@ -589,12 +617,18 @@ def main():
                           "peak": HBM_PEAK_GBS, "unit": "GB/s",
                           "frac": round(step_gbs / HBM_PEAK_GBS, 4)},
     }
-    kernels = step_kernels(cfg, dtype, a.dtype)
-    if kernels:
-        out["step_kernels"] = kernels
+    if not a.no_roofline:
+        # The step's kernels timed one by one over the next `steps` steps: the
+        # dominant one by time per step is the roofline; gate/up with weights
+        # rotating through more than the memory-side cache is reported beside it.
+        sk = step_kernels(model, cfg, dtype, a.dtype, int(ids[-1]), a.steps, a.ctx + a.steps)
+        out["step_kernels"] = sk
+        out["roofline"] = dominant_roofline(sk)
+        log(f"[bench] dominant kernel {out['roofline']['kind']}: {out['roofline']['us_per_launch']} us, "
+            f"frac {out['roofline']['frac']}")
     del model
     if not a.no_roofline:
-        out["roofline"] = gemv_roofline(ctx, V, F, cfg, dtype)
+        out["roofline_gemv"] = gemv_roofline(ctx, V, F, cfg, dtype)
     if not a.no_cpu_baseline:
         # The GPU line is complete at this point: a failure of the CPU leg is
         # reported in the line instead of discarding the GPU measurement.

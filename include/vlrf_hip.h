@@ -287,6 +287,25 @@ int  vlrf_hip_model_read_generated(vlrf_hip_model_t m, int32_t* out_ids, int n);
  * vlrf_hip_kv_read (token-major elements of the cache dtype, Q8_0 row scales).  Synchronous. */
 int  vlrf_hip_model_kv_read(vlrf_hip_model_t m, int layer, int row0, int n, int8_t* k_q,
                             int8_t* v_q, float* k_s, float* v_s);
+/* Measurement, no reference counterpart (the reference times whole calls,
+ * vlrf_cli's tok/s): n_steps greedy decode steps from token `first`, as
+ * vlrf_hip_model_generate_async, with the step's kernels queued one by one and
+ * every launch timed by its own start/stop events (hipExtLaunchKernel stamps
+ * them with the kernel's begin and end).  Per launch kind: us[k] = summed
+ * kernel time in microseconds, calls[k] = launches.  Advances the position
+ * by n_steps (1..256); synchronous. */
+enum {
+    VLRF_HIP_LK_QKV = 0,      /* RMSNorm + QKV projection (fused with RoPE, the KV append and attention) */
+    VLRF_HIP_LK_ATTN = 1,     /* stand-alone decode attention (when not fused) */
+    VLRF_HIP_LK_O = 2,        /* O projection (+ merge of the attention partials) + residual */
+    VLRF_HIP_LK_GATE_UP = 3,  /* RMSNorm + gate/up + SwiGLU */
+    VLRF_HIP_LK_DOWN = 4,     /* down projection + residual */
+    VLRF_HIP_LK_LM_HEAD = 5,  /* final RMSNorm + LM head */
+    VLRF_HIP_LK_ARGMAX = 6,   /* greedy argmax + step state */
+    VLRF_HIP_LK_OTHER = 7,    /* embedding gather, attention combine */
+    VLRF_HIP_LK_KINDS = 8
+};
+int  vlrf_hip_model_time_launches(vlrf_hip_model_t m, int32_t first, int n_steps, double us[8], int calls[8]);
 /* Device bytes read per decode step at context length ctx_len, by stream:
  * [0] projection + LM-head weights, [1] KV cache, [2] everything else
  * (norm weights, embedding row, activations).  For roofline accounting. */

@@ -174,3 +174,29 @@ def test_head_dim_128_chunked_cache(ctx, orc, n_heads, n_kv, dtype):
         worst = max(worst, rel_err(gl, ol))
     print(f"  teacher-forced logits at ctx {m.used}: worst rel err {worst:.2e}", flush=True)
     assert worst <= 1e-3, worst
+
+
+def test_time_launches_runs_the_same_steps(ctx, orc):
+    """vlrf_hip_model_time_launches (each launch timed by its own events)
+    decodes the same greedy stream as generate and labels every launch: one
+    QKV (+ attention) launch, O, gate/up and down per layer, one LM head and
+    one argmax per step, all with positive durations."""
+    cfg = F.tiny(V.DT_Q8_0, n_layers=3, max_seq_len=96)
+    m, _, _ = _models(ctx, orc, cfg, 25)
+    prompt = F.tokens(25, "p", 12, cfg["vocab_size"])
+    ref = m.generate(prompt, 20)
+    m.reset()
+    m.prefill(prompt)
+    steps = 20
+    kinds = m.time_launches(int(prompt[-1]), steps)
+    got = m.read_generated(steps)
+    assert list(got) == list(ref)
+    assert m.used == 12 + steps
+    L = cfg["n_layers"]
+    for k in ("o_proj", "gate_up", "down"):
+        assert kinds[k][1] == L * steps, (k, kinds[k])
+    assert kinds["qkv_attn"][1] == L * steps
+    assert kinds["lm_head"][1] == steps and kinds["argmax"][1] == steps
+    assert all(us > 0 for us, _ in kinds.values())
+    with pytest.raises(V.HipError):
+        m.time_launches(int(prompt[-1]), 96)      # past the cache

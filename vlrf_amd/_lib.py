@@ -95,6 +95,7 @@ _SIGS = {
     "vlrf_hip_model_generate_async": (i32, [vp, i32, i32]),
     "vlrf_hip_model_read_generated": (i32, [vp, vp, i32]),
     "vlrf_hip_model_step_bytes": (i32, [vp, i32, C.POINTER(C.c_double)]),
+    "vlrf_hip_model_time_launches": (i32, [vp, i32, i32, C.POINTER(C.c_double), C.POINTER(C.c_int)]),
 }
 
 _LIB = None

@@ -15,6 +15,7 @@ namespace vlrf_hip {
 
 namespace {
 thread_local std::string g_error;
+thread_local LaunchTimer* g_launch_timer = nullptr;
 }
 
 void set_error(const char* fmt, ...) {
@@ -25,6 +26,8 @@ void set_error(const char* fmt, ...) {
     va_end(ap);
     g_error = buf;
 }
+
+LaunchTimer*& launch_timer() { return g_launch_timer; }
 
 size_t weight_device_bytes(int dtype, int N, int K) {
     const size_t n = (size_t)N * K;

@@ -5,6 +5,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <hip/hip_fp16.h>
 
 #include <cstdint>
@@ -45,6 +46,33 @@ void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
                                   hipGetErrorString(e_), __FILE__, __LINE__);     \
             return VLRF_HIP_ERR_RUNTIME;                                          \
         }                                                                         \
+    } while (0)
+
+// ---- per-launch kernel timing ------------------------------------------------
+// While a LaunchTimer is installed on the calling thread, launches made with
+// VH_LAUNCH take its next start/stop event pair: hipExtLaunchKernel stamps them
+// with the kernel's own begin and end, so each launch's duration is measured
+// without a marker between launches.  `cur_kind` labels the launches that
+// follow (the decode step sets it per phase).  With no timer, a plain launch.
+struct LaunchTimer {
+    hipEvent_t* start = nullptr;
+    hipEvent_t* stop = nullptr;
+    int* kind = nullptr;
+    int n = 0, cap = 0, cur_kind = 0;
+};
+LaunchTimer*& launch_timer();   // the calling thread's timer (null: none)
+
+#define VH_LAUNCH(K, GRID, BLOCK, SHM, S, ...)                                                   \
+    do {                                                                                           \
+        ::vlrf_hip::LaunchTimer* lt_ = ::vlrf_hip::launch_timer();                                \
+        if (lt_ && lt_->n < lt_->cap) {                                                            \
+            lt_->kind[lt_->n] = lt_->cur_kind;                                                     \
+            hipExtLaunchKernelGGL(K, GRID, BLOCK, SHM, S, lt_->start[lt_->n], lt_->stop[lt_->n], 0, \
+                                  __VA_ARGS__);                                                    \
+            ++lt_->n;                                                                              \
+        } else {                                                                                   \
+            hipLaunchKernelGGL(K, GRID, BLOCK, SHM, S, __VA_ARGS__);                               \
+        }                                                                                          \
     } while (0)
 
 // ---- device-resident quantized weight ---------------------------------------

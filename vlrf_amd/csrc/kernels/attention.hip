@@ -1087,7 +1087,7 @@ int launch_attn_decode(hipStream_t s, const float* q, const void* kc, const void
         const int na = 8 * rep * ((n_kv * fz.nch + 7) / 8);
         const dim3 cgrid(na + 1);
 #define VH_C128(R)                                                                                              \
-    hipLaunchKernelGGL((attn_chunk128_kernel<R>), cgrid, dim3(kCH), 0, s, q, k8, v8, ks, vs, head_stride, ctx_dev, \
+    VH_LAUNCH((attn_chunk128_kernel<R>), cgrid, dim3(kCH), 0, s, q, k8, v8, ks, vs, head_stride, ctx_dev, \
                        scale, fz, fz.nch, na)
         switch (rep) {
             case 1: VH_C128(1); break;
@@ -1106,7 +1106,7 @@ int launch_attn_decode(hipStream_t s, const float* q, const void* kc, const void
                "attn_decode: chunked form for %d chunks does not apply", fz.nch);
         const dim3 cgrid(8 * rep * ((n_kv * fz.nch + 7) / 8));
 #define VH_CHK(KT, R)                                                                                         \
-    hipLaunchKernelGGL((attn_decode_single_kernel<KT, R, true, kCH>), cgrid, dim3(kCH), 0, s, q, k8, v8, ks, vs, \
+    VH_LAUNCH((attn_decode_single_kernel<KT, R, true, kCH>), cgrid, dim3(kCH), 0, s, q, k8, v8, ks, vs, \
                        head_stride, ctx_len, ctx_dev, scale, fz.chunks, fz, fz.nch)
 #define VH_CHK_R(KT)                     \
     switch (rep) {                       \
@@ -1127,7 +1127,7 @@ int launch_attn_decode(hipStream_t s, const float* q, const void* kc, const void
     }
     if (d_head == 64 && head_stride / d_head <= kSPMaxCtx && (!fuse || n_kv <= 8)) {
 #define VH_SP(KT, R, FU)                                                                                     \
-    hipLaunchKernelGGL((attn_decode_single_kernel<KT, R, FU>), dim3(n_heads), dim3(64 * kSPWaves), 0, s, q, k8, \
+    VH_LAUNCH((attn_decode_single_kernel<KT, R, FU>), dim3(n_heads), dim3(64 * kSPWaves), 0, s, q, k8, \
                        v8, ks, vs, head_stride, ctx_len, ctx_dev, scale, out, fz, 0)
 #define VH_SP_R(KT, FU)                       \
     switch (rep) {                            \
@@ -1152,7 +1152,7 @@ int launch_attn_decode(hipStream_t s, const float* q, const void* kc, const void
     }
     dim3 grid(n_splits, n_kv), block(kAttnThreads);
 #define VH_AD(D, R, T, FU)                                                                          \
-    hipLaunchKernelGGL((attn_decode_partial_kernel<D, R, T, FU>), grid, block, 0, s, q, k8, v8, ks,  \
+    VH_LAUNCH((attn_decode_partial_kernel<D, R, T, FU>), grid, block, 0, s, q, k8, v8, ks,  \
                        vs, head_stride, ctx_len, ctx_dev, n_splits, scale, part, fz)
 #define VH_AD_R(D, T, FU)                       \
     switch (rep) {                              \
@@ -1179,9 +1179,9 @@ int launch_attn_decode(hipStream_t s, const float* q, const void* kc, const void
 #undef VH_AD
     VH_LAUNCHED();
     if (d_head == 64)
-        hipLaunchKernelGGL((attn_combine_kernel<64>), dim3(n_heads), dim3(256), 0, s, part, n_splits, out);
+        VH_LAUNCH((attn_combine_kernel<64>), dim3(n_heads), dim3(256), 0, s, part, n_splits, out);
     else
-        hipLaunchKernelGGL((attn_combine_kernel<128>), dim3(n_heads), dim3(256), 0, s, part, n_splits, out);
+        VH_LAUNCH((attn_combine_kernel<128>), dim3(n_heads), dim3(256), 0, s, part, n_splits, out);
     VH_LAUNCHED();
     return VLRF_HIP_OK;
 }

@@ -470,14 +470,14 @@ int launch_rope(hipStream_t s, float* x, int T, int n_heads, int d_head, int pos
 }
 
 int launch_embed(hipStream_t s, const float* table, const int* tok_dev, float* x, int D) {
-    hipLaunchKernelGGL(embed_kernel, dim3(1), dim3(256), 0, s, table, tok_dev, x, D);
+    VH_LAUNCH(embed_kernel, dim3(1), dim3(256), 0, s, table, tok_dev, x, D);
     VH_LAUNCHED();
     return VLRF_HIP_OK;
 }
 
 int launch_argmax_pairs_step(hipStream_t s, const float2* pairs, int np, int* state, int* gen_ids, int gen_cap) {
     VH_ARG(np >= 1 && np <= 512, "argmax_pairs: %d pairs outside [1,512]", np);
-    hipLaunchKernelGGL(argmax_pairs_step_kernel, dim3(1), dim3(512), 0, s, pairs, np, state, gen_ids, gen_cap);
+    VH_LAUNCH(argmax_pairs_step_kernel, dim3(1), dim3(512), 0, s, pairs, np, state, gen_ids, gen_cap);
     VH_LAUNCHED();
     return VLRF_HIP_OK;
 }
@@ -485,7 +485,7 @@ int launch_argmax_pairs_step(hipStream_t s, const float2* pairs, int np, int* st
 int launch_argmax_step(hipStream_t s, const float* logits, int n, int* state, int* gen_ids,
                        int gen_cap) {
     VH_ARG(n >= 1 && n <= 1024 * 4 * kArgmaxPer, "argmax: %d logits outside [1,%d]", n, 1024 * 4 * kArgmaxPer);
-    hipLaunchKernelGGL(argmax_step_kernel, dim3(1), dim3(1024), 0, s, logits, n, state, gen_ids, gen_cap);
+    VH_LAUNCH(argmax_step_kernel, dim3(1), dim3(1024), 0, s, logits, n, state, gen_ids, gen_cap);
     VH_LAUNCHED();
     return VLRF_HIP_OK;
 }

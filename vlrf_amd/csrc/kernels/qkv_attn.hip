@@ -279,8 +279,8 @@ int launch_qkv_attn(hipStream_t s, const QkvAttnParams& p, int w_dtype, int kv_d
     const int nc = qkv_chunks(w_dtype, p.K);
 #define VH_QA(WT, KT, NC)                                                                                  \
     do {                                                                                                   \
-        if (gather) hipLaunchKernelGGL((qkv_attn_kernel<WT, KT, NC, true>), grid, block, 0, s, p);         \
-        else hipLaunchKernelGGL((qkv_attn_kernel<WT, KT, NC, false>), grid, block, 0, s, p);               \
+        if (gather) VH_LAUNCH((qkv_attn_kernel<WT, KT, NC, true>), grid, block, 0, s, p);                  \
+        else VH_LAUNCH((qkv_attn_kernel<WT, KT, NC, false>), grid, block, 0, s, p);                        \
     } while (0)
 #define VH_QA_KV(WT, NC)                                       \
     if (kv_dtype == VLRF_KV_Q8_0) VH_QA(WT, VLRF_KV_Q8_0, NC);  \

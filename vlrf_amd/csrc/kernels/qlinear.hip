@@ -262,8 +262,8 @@ int launch_gemv(hipStream_t s, const DevWeight& a, const DevWeight* b, const flo
     do {                                                                                                  \
         const int groups = (a.N + kGemvWaves * (RPW)-1) / (kGemvWaves * (RPW));                            \
         dim3 grid(((XM)&16) || groups < kGemvMaxGroups ? groups : kGemvMaxGroups);                         \
-        hipLaunchKernelGGL((gemv_kernel<WT, NC, RPW, SWIGLU, XM>), grid, dim3(64 * kGemvWaves), 0, s, a.q, \
-                           a.d, qb, db, a.N, a.K, x, x_row, x_copy, norm_w, eps, residual, y, nparts, argp); \
+        VH_LAUNCH((gemv_kernel<WT, NC, RPW, SWIGLU, XM>), grid, dim3(64 * kGemvWaves), 0, s, a.q, a.d, qb, \
+                  db, a.N, a.K, x, x_row, x_copy, norm_w, eps, residual, y, nparts, argp);             \
     } while (0)
 #define VH_GEMV(NC, RPW)                                                   \
     do {                                                                  \
@@ -307,11 +307,11 @@ int launch_gemv(hipStream_t s, const DevWeight& a, const DevWeight* b, const flo
         if constexpr (!SWIGLU) {
             const dim3 grid((a.N + kGemvWaves - 1) / kGemvWaves);
             if (xm == 16)
-                hipLaunchKernelGGL((gemv_wide_kernel<WT, NCW, 16>), grid, dim3(64 * kGemvWaves), 0, s, a.q, a.d, a.N,
-                                   a.K, x, residual, y);
+                VH_LAUNCH((gemv_wide_kernel<WT, NCW, 16>), grid, dim3(64 * kGemvWaves), 0, s, a.q, a.d, a.N, a.K,
+                          x, residual, y);
             else
-                hipLaunchKernelGGL((gemv_wide_kernel<WT, NCW, 20>), grid, dim3(64 * kGemvWaves), 0, s, a.q, a.d, a.N,
-                                   a.K, x, residual, y);
+                VH_LAUNCH((gemv_wide_kernel<WT, NCW, 20>), grid, dim3(64 * kGemvWaves), 0, s, a.q, a.d, a.N, a.K,
+                          x, residual, y);
         }
     }
 #undef VH_GEMV

@@ -104,9 +104,15 @@ struct vlrf_hip_model {
 
 namespace {
 
+// Labels the launches that follow for an installed LaunchTimer.
+void lk(int kind) {
+    if (LaunchTimer* t = launch_timer()) t->cur_kind = kind;
+}
+
 int enqueue_step(vlrf_hip_model* m, hipStream_t s) {
     // Layer 0's QKV projection gathers the embedding row itself when it can.
     const bool gather = qlinear_gather_supported(m->layers[0].wqkv);
+    lk(VLRF_HIP_LK_OTHER);
     int rc = gather ? VLRF_HIP_OK : launch_embed(s, m->embed, m->state, m->x, m->D);
     const float eps = m->cfg.norm_eps;
     const float scale = 1.f / std::sqrt((float)m->dh);   // attention.hpp:373-374
@@ -149,31 +155,41 @@ int enqueue_step(vlrf_hip_model* m, hipStream_t s) {
             p.status = m->step_status;
             p.limit = m->wait_limit;
             p.layer = l;
+            lk(VLRF_HIP_LK_QKV);
             if (!rc) rc = launch_qkv_attn(s, p, m->cfg.weight_dtype, m->cfg.kv_dtype, l == 0 && gather);
         } else {
+            lk(VLRF_HIP_LK_QKV);
             if (!rc) {
                 if (l == 0 && gather)   // embedding_lookup (ops.hpp:615-626) fused: x = embed[token]
                     rc = launch_qlinear_gather(s, Ly.wqkv, m->embed, m->state, m->x, m->qkv, Ly.ln1, eps);
                 else
                     rc = launch_qlinear(s, Ly.wqkv, m->x, m->qkv, 1, Ly.ln1, eps, nullptr);
             }
+            lk(VLRF_HIP_LK_ATTN);
             if (!rc) rc = launch_attn_decode(s, q, Ly.kv.k, Ly.kv.v, Ly.kv.ks, Ly.kv.vs, Ly.kv.dtype,
                                              (long)m->S * m->dh, m->H, m->G, m->dh, 1, m->state + 1,
                                              m->n_splits, scale, m->part, m->att, &fz);
         }
+        lk(VLRF_HIP_LK_O);
         if (!rc) rc = m->nch ? launch_qlinear_merge(s, Ly.wo, m->chunks, m->nparts, m->x, m->x, m->dh)
                              : launch_qlinear(s, Ly.wo, m->att, m->x, 1, nullptr, 0.f, m->x);
+        lk(VLRF_HIP_LK_GATE_UP);
         if (!rc) rc = launch_qlinear_swiglu(s, Ly.wg, Ly.wu, m->x, m->h, 1, Ly.ln2, eps);
+        lk(VLRF_HIP_LK_DOWN);
         if (!rc) rc = launch_qlinear(s, Ly.wd, m->h, m->x, 1, nullptr, 0.f, m->x);
     }
     if (qlinear_argmax_supported(m->lm_head)) {
         // The LM head's workgroups leave (max, first index) pairs: the argmax
         // step reduces those instead of the 32000 logits.
         int np = 0;
+        lk(VLRF_HIP_LK_LM_HEAD);
         if (!rc) rc = launch_qlinear_argmax(s, m->lm_head, m->x, m->logits, m->ln_final, eps, m->argpairs, &np);
+        lk(VLRF_HIP_LK_ARGMAX);
         if (!rc) rc = launch_argmax_pairs_step(s, m->argpairs, np, m->state, m->gen_ids, m->S);
     } else {
+        lk(VLRF_HIP_LK_LM_HEAD);
         if (!rc) rc = launch_qlinear(s, m->lm_head, m->x, m->logits, 1, m->ln_final, eps, nullptr);
+        lk(VLRF_HIP_LK_ARGMAX);
         if (!rc) rc = launch_argmax_step(s, m->logits, m->V, m->state, m->gen_ids, m->S);
     }
     return rc;
@@ -758,6 +774,78 @@ int vlrf_hip_model_read_generated(vlrf_hip_model_t m, int32_t* out_ids, int n) {
     hipStream_t s = m->ctx->stream;
     VH_CHECK(hipMemcpyAsync(out_ids, m->gen_ids, (size_t)n * sizeof(int), hipMemcpyDeviceToHost, s));
     VH_CHECK(hipStreamSynchronize(s));
+    return check_waits(m);
+}
+
+int vlrf_hip_model_time_launches(vlrf_hip_model_t m, int32_t first, int n_steps, double us[VLRF_HIP_LK_KINDS],
+                                 int calls[VLRF_HIP_LK_KINDS]) {
+    int rc = check_ready(m);
+    if (rc) return rc;
+    VH_ARG(us && calls, "time_launches: null output");
+    VH_ARG(first >= 0 && first < m->V, "time_launches: token %d outside [0,%d)", first, m->V);
+    VH_ARG(n_steps >= 1 && n_steps <= 256, "time_launches: n_steps %d outside [1,256]", n_steps);
+    if (m->pos + n_steps > m->S) {
+        set_error("KVCache::append: exceeds max_seq_len (%d + %d > %d)", m->pos, n_steps, m->S);
+        return VLRF_HIP_ERR_OVERFLOW;
+    }
+    for (int k = 0; k < VLRF_HIP_LK_KINDS; ++k) {
+        us[k] = 0.0;
+        calls[k] = 0;
+    }
+    hipStream_t s = m->ctx->stream;
+    // At most 6 launches per layer plus 3 per step (stand-alone attention with
+    // its combine, the embedding, the LM head and the argmax).
+    const int cap = n_steps * (6 * m->L + 3);
+    std::vector<hipEvent_t> ev(2 * (size_t)cap, nullptr);
+    std::vector<int> kind(cap, 0);
+    LaunchTimer t;
+    t.start = ev.data();
+    t.stop = ev.data() + cap;
+    t.kind = kind.data();
+    t.cap = cap;
+    auto destroy = [&]() {
+        for (hipEvent_t e : ev)
+            if (e) (void)hipEventDestroy(e);
+    };
+    for (auto& e : ev)
+        if (hipEventCreate(&e) != hipSuccess) {
+            destroy();
+            set_error("time_launches: hipEventCreate failed");
+            return VLRF_HIP_ERR_RUNTIME;
+        }
+    if (hipStreamSynchronize(s) != hipSuccess) {
+        destroy();
+        set_error("time_launches: stream synchronisation failed");
+        return VLRF_HIP_ERR_RUNTIME;
+    }
+    m->pinned[0] = first;
+    m->pinned[1] = m->pos;
+    m->pinned[2] = 0;
+    if (hipMemcpyAsync(m->state, m->pinned, 3 * sizeof(int), hipMemcpyHostToDevice, s) != hipSuccess) {
+        destroy();
+        set_error("time_launches: state upload failed");
+        return VLRF_HIP_ERR_RUNTIME;
+    }
+    launch_timer() = &t;
+    for (int i = 0; i < n_steps && !rc; ++i) rc = enqueue_step(m, s);
+    launch_timer() = nullptr;
+    if (!rc) m->pos += n_steps;
+    if (!rc && hipStreamSynchronize(s) != hipSuccess) {
+        set_error("time_launches: the timed steps failed");
+        rc = VLRF_HIP_ERR_RUNTIME;
+    }
+    for (int j = 0; j < t.n && !rc; ++j) {
+        float ms = 0.f;
+        if (hipEventElapsedTime(&ms, t.start[j], t.stop[j]) != hipSuccess) {
+            set_error("time_launches: no timing for launch %d", j);
+            rc = VLRF_HIP_ERR_RUNTIME;
+            break;
+        }
+        us[t.kind[j]] += ms * 1e3;
+        calls[t.kind[j]] += 1;
+    }
+    destroy();
+    if (rc) return rc;
     return check_waits(m);
 }
 

@@ -319,6 +319,16 @@ class Model:
         self.prefill(prompt_ids)
         return self.generate_ids(int(prompt_ids[-1]), max_new_tokens)
 
+    LAUNCH_KINDS = ("qkv_attn", "attn", "o_proj", "gate_up", "down", "lm_head", "argmax", "other")
+
+    def time_launches(self, first, n_steps):
+        """n_steps greedy steps from `first` with every launch timed by its own
+        events: {kind: (summed kernel us, launches)} for the kinds launched."""
+        us = (C.c_double * 8)()
+        calls = (C.c_int * 8)()
+        check(lib().vlrf_hip_model_time_launches(self.h, int(first), n_steps, us, calls))
+        return {k: (us[i], calls[i]) for i, k in enumerate(self.LAUNCH_KINDS) if calls[i]}
+
     def step_bytes(self, ctx_len):
         out = (C.c_double * 3)()
         check(lib().vlrf_hip_model_step_bytes(self.h, ctx_len, out))
