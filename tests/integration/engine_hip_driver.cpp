@@ -9,8 +9,10 @@
 // file with config.json beside it) and runs it.
 //   engine_hip <weights.nfw>
 // Cases: greedy with the engine's default F32 KV cache and with a Q8_0 cache
-// (vlrf_set_kv_cache_type), and a request past max_seq_len.  Each prints
-// PASS/FAIL; exit status 0 = all pass.
+// (vlrf_set_kv_cache_type), and a request past max_seq_len; after each run
+// vlrf_context_length must report what the CPU backend reports (the prompt
+// plus one row per generated token, transformer.hpp:324-326,444-482).  Each
+// prints PASS/FAIL; exit status 0 = all pass.
 #include "vlrf.h"
 
 #include <cstdio>
@@ -44,9 +46,11 @@ std::vector<int32_t> run(VlrfModel m, std::vector<int32_t> const& prompt, int ma
 void compare(VlrfModel m, std::vector<int32_t> const& prompt, int max_new, const std::string& what) {
     if (vlrf_set_backend(VLRF_BACKEND_CPU) != VLRF_OK) { report(false, what + ": CPU backend"); return; }
     const std::vector<int32_t> cpu = run(m, prompt, max_new);
+    const int32_t cpu_ctx = vlrf_context_length(m);
     if (vlrf_set_backend(VLRF_BACKEND_HIP) != VLRF_OK) { report(false, what + ": HIP backend unavailable"); return; }
     const std::string info = vlrf_backend_info();
     const std::vector<int32_t> hip = run(m, prompt, max_new);
+    const int32_t hip_ctx = vlrf_context_length(m);
     int first = -1;
     for (size_t i = 0; i < cpu.size() && i < hip.size(); ++i)
         if (cpu[i] != hip[i]) { first = (int)i; break; }
@@ -54,6 +58,8 @@ void compare(VlrfModel m, std::vector<int32_t> const& prompt, int max_new, const
                 cpu.size(), hip.size(), first);
     report(!cpu.empty() && cpu.size() == hip.size() && first < 0 && info.find("HIP") != std::string::npos,
            "engine vlrf_generate_ids, HIP backend == CPU backend: " + what);
+    std::printf("  %s: vlrf_context_length cpu %d, hip %d\n", what.c_str(), cpu_ctx, hip_ctx);
+    report(cpu_ctx == hip_ctx && cpu_ctx > 0, "engine vlrf_context_length after generate, HIP == CPU: " + what);
 }
 
 }  // namespace

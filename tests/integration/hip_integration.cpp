@@ -19,7 +19,13 @@
 //              Q4_0-derived and with plain f32 weights (the device dtype
 //              follows the weights, a lossy one is refused); stops at EOS, at
 //              max_seq_len, on an on_token veto, and an empty prompt.  Token
-//              ids, tokens_generated and hit_eos must be identical.
+//              ids, tokens_generated and hit_eos must be identical;
+//   prefill    the opt-in matrix-core prompt pass (HipDecoder::set_prefill_mfma):
+//              logits after a 100-token prompt within 1e-2 of the reference's
+//              forward(prompt) + forward(last id), then generation from it;
+//   cache      HipDecoder::read_cache after a device generate: the reference's
+//              KVCache storage filled with the device rows, a CPU forward with
+//              that cache within 1e-3 of the reference's own continuation.
 // Without a usable device (or with --cpu) the first two run through
 // HipBackend's CPU fallback and `decode` is skipped.  Exit status 0 = all pass.
 
@@ -31,6 +37,7 @@
 #include "hip_backend.hpp"
 #include "hip_decoder.hpp"
 
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -371,6 +378,87 @@ void check_decode_stops(HipBackend const& be) {
     compare("on_token stops after 7", ref, dec2.generate(prompt, gc.max_new_tokens, gc.on_token));
 }
 
+double rel_err_f(const float* a, const float* b, int64_t n) {
+    double num = 0.0, den = 0.0;
+    for (int64_t i = 0; i < n; ++i) {
+        num = std::max(num, std::fabs((double)a[i] - (double)b[i]));
+        den = std::max(den, std::fabs((double)b[i]));
+    }
+    return den > 0 ? num / den : num;
+}
+
+int argmax_f(const float* v, int n) {
+    int best = 0;
+    for (int i = 1; i < n; ++i)
+        if (v[i] > v[best]) best = i;
+    return best;
+}
+
+// The opt-in matrix-core prompt pass: bf16 parity class.
+void check_prefill_mfma(HipBackend const& be) {
+    const vlrf::ModelConfig c = tiny_config(vlrf::KVCacheDType::Q8_0);
+    vlrf::TransformerModel m;
+    m.init(c);
+    fill_weights(m, c, VLRF_DT_Q8_0);
+    const std::vector<int> prompt = prompt_ids(100, c.vocab_size);
+    m.reset_kv_cache();
+    m.forward(prompt, true);
+    Tensor ref = m.forward({prompt.back()}, true);   // generate's first decode step (transformer.hpp:448-482)
+    vlrf::HipDecoder dec(be.context(), c, m.wm);
+    dec.set_prefill_mfma(64);
+    report(dec.prefill_uses_mfma(prompt.size()) && !dec.prefill_uses_mfma(63),
+           "prefill: the matrix-core pass applies from 64 prompt tokens", 0.0);
+    dec.prefill(prompt);
+    std::vector<float> logits(c.vocab_size);
+    const int next = dec.step(prompt.back(), logits.data());
+    const double e = rel_err_f(logits.data(), ref.data_ptr(), c.vocab_size);
+    report(e <= 1e-2 && dec.used() == (int)prompt.size() + 1,
+           "prefill: logits after a 100-token prompt on the matrix cores within 1e-2 of the reference", e);
+    report(next == argmax_f(ref.data_ptr(), c.vocab_size), "prefill: first generated id == the reference's", 0.0);
+    vlrf::GenerationConfig gc;
+    gc.max_new_tokens = 40;
+    gc.do_sample = false;
+    const auto want = m.generate(prompt, gc);
+    const auto got = dec.generate(prompt, gc.max_new_tokens);
+    int same = 0;
+    while (same < got.tokens_generated && same < want.tokens_generated &&
+           got.token_ids[prompt.size() + same] == want.token_ids[prompt.size() + same])
+        ++same;
+    std::printf("  prefill: %d of %d generated ids equal to the reference's before the first difference\n", same,
+                want.tokens_generated);
+    report(got.tokens_generated == 40 && same >= 1, "prefill: generation continues after the matrix-core pass",
+           (double)same);
+}
+
+// Device cache rows brought into the reference's KVCache storage.
+void check_read_cache(HipBackend const& be, vlrf::KVCacheDType kv_dtype) {
+    const vlrf::ModelConfig c = tiny_config(kv_dtype);
+    vlrf::TransformerModel m;
+    m.init(c);
+    fill_weights(m, c, VLRF_DT_Q8_0);
+    const std::vector<int> prompt = prompt_ids(40, c.vocab_size);
+    vlrf::GenerationConfig gc;
+    gc.max_new_tokens = 20;
+    gc.do_sample = false;
+    const auto ref = m.generate(prompt, gc);
+    const int last = ref.token_ids.back();
+    Tensor want = m.forward({last}, true);            // the reference continuing from its own cache
+    vlrf::TransformerModel m2;
+    m2.init(c);
+    fill_weights(m2, c, VLRF_DT_Q8_0);
+    vlrf::HipDecoder dec(be.context(), c, m2.wm);
+    const auto got = dec.generate(prompt, gc.max_new_tokens);
+    m2.reset_kv_cache();
+    dec.read_cache(m2.kv_caches, (int)prompt.size() + got.tokens_generated);
+    const bool rows = m2.context_used() == m.context_used() - 1;
+    Tensor cont = m2.forward({last}, true);           // the CPU continuing from the device's cache
+    const double e = rel_err_f(cont.data_ptr(), want.data_ptr(), c.vocab_size);
+    report(rows && e <= 1e-3 && argmax_f(cont.data_ptr(), c.vocab_size) == argmax_f(want.data_ptr(), c.vocab_size),
+           std::string("cache: CPU forward over the device's cache rows == the reference's, KV ") +
+               vlrf::kv_cache_dtype_name(kv_dtype),
+           e);
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
@@ -387,6 +475,9 @@ int main(int argc, char** argv) {
             check_decode(be, dt);
         for (int wdt : {VLRF_DT_Q4_0, VLRF_DT_F32}) check_decode_weights(be, wdt);
         check_decode_stops(be);
+        check_prefill_mfma(be);
+        for (auto dt : {vlrf::KVCacheDType::F32, vlrf::KVCacheDType::F16, vlrf::KVCacheDType::Q8_0})
+            check_read_cache(be, dt);
     } else
         std::printf("SKIP decode (no HIP device)\n");
     std::printf("%s: %d failure(s)\n", g_fail ? "FAILED" : "OK", g_fail);

@@ -49,6 +49,15 @@ def test_adapter_on_device_matches_reference_engine():
     for w in ("Q8_0-derived weights kept as Q8_0 blocks", "Q4_0-derived weights uploaded as Q4_0 / LM head Q4_0",
               "F32-derived weights uploaded as F32 / LM head F32", "forcing Q8_0 on f32 weights is refused"):
         assert "PASS decode: " + w in p.stdout, (w, p.stdout)
+    # The opt-in matrix-core prompt pass (bf16 parity class) and the device
+    # cache brought back into the engine's KVCache storage.
+    for w in ("prefill: the matrix-core pass applies from 64 prompt tokens",
+              "prefill: logits after a 100-token prompt on the matrix cores within 1e-2 of the reference",
+              "prefill: first generated id == the reference's", "prefill: generation continues",
+              "cache: CPU forward over the device's cache rows == the reference's, KV f32",
+              "cache: CPU forward over the device's cache rows == the reference's, KV f16",
+              "cache: CPU forward over the device's cache rows == the reference's, KV q8_0"):
+        assert "PASS " + w in p.stdout, (w, p.stdout)
     assert "FAIL" not in p.stdout
 
 
@@ -94,3 +103,4 @@ def test_engine_c_api_selects_the_hip_backend(tmp_path):
     print(p.stdout, p.stderr, flush=True)
     assert p.returncode == 0, p.stdout + p.stderr
     assert p.stdout.count("PASS engine vlrf_generate_ids, HIP backend == CPU backend") == 3, p.stdout
+    assert p.stdout.count("PASS engine vlrf_context_length after generate, HIP == CPU") == 3, p.stdout

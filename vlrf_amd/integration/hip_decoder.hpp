@@ -17,12 +17,25 @@
 // uploaded as Q4_0 or Q8_0 blocks only when encoding and decoding the tensor
 // reproduces it bit for bit (weights that came from GGUF blocks,
 // convert_gguf.py:233-263); otherwise the layers run on f32 weights.
+//
+// Prompt ingestion.  By default the prompt runs through the decode step one
+// token at a time: f32 activations and the f32 GEMV, so the KV rows and the
+// greedy stream match the reference bit for bit where its arithmetic allows
+// (the parity class of the decode tests).  Opt-in (set_prefill_mfma, or the
+// environment variable VLRF_HIP_PREFILL_MFMA=<min prompt tokens>): prompts of
+// at least that many tokens run as one batched pass on the matrix cores
+// (vlrf_hip_model_prefill_mfma: bf16 operands, f32 accumulation, the
+// reference's batched forward(prompt), transformer.hpp:444-448), block-dtype
+// weights only.  Its parity class is the bf16 one: logits after the prompt
+// within 1e-2 of the reference's; the greedy stream may part from the
+// reference's where two logits lie closer than that.
 #pragma once
 
 #include "transformer.hpp"
 #include "vlrf_hip.h"
 
 #include <algorithm>
+#include <cstdlib>
 #include <cstring>
 #include <functional>
 #include <stdexcept>
@@ -86,6 +99,9 @@ public:
         mc.weight_dtype = layer_dtype_;
         mc.kv_dtype = c.kv_cache_dtype;          // KVCacheDType values are the ABI's VLRF_KV_*
         check(vlrf_hip_model_create(ctx_, &mc, &m_));
+        mfma_ok_ = (layer_dtype_ == VLRF_DT_Q8_0 || layer_dtype_ == VLRF_DT_Q4_0) && c.d_model % 64 == 0 &&
+                   c.d_ff % 64 == 0;
+        if (const char* e = std::getenv("VLRF_HIP_PREFILL_MFMA")) set_prefill_mfma(std::atoi(e));
         try {
             auto put_f32 = [&](const std::string& name, const std::string& key) {
                 Tensor& t = wm.get(key);
@@ -129,13 +145,8 @@ public:
     TransformerModel::GenerationResult generate(std::vector<int> const& prompt, int max_new_tokens,
                                                 std::function<bool(int)> const& on_token = nullptr) {
         TransformerModel::GenerationResult r;
-        check(vlrf_hip_model_reset(m_));
         r.token_ids = prompt;
-        if (!prompt.empty()) {
-            int32_t next = 0;
-            std::vector<int32_t> ids(prompt.begin(), prompt.end());
-            check(vlrf_hip_model_prefill(m_, ids.data(), (int)ids.size(), &next));
-        }
+        prefill(prompt);
         int32_t last = prompt.empty() ? bos_ : prompt.back();
         int left = std::min(max_new_tokens, max_seq_ - (int)prompt.size());
         std::vector<int32_t> buf;
@@ -170,6 +181,54 @@ public:
     // The dtypes chosen for the layer projections and the LM head.
     int layer_dtype() const { return layer_dtype_; }
     int lm_head_dtype() const { return lm_dtype_; }
+
+    // Prompts of at least min_tokens (> 0) run as one matrix-core pass (see
+    // the file comment); 0 switches it off.  No effect where the layers run
+    // on f32 weights.
+    void set_prefill_mfma(int min_tokens) { prefill_mfma_min_ = min_tokens > 0 ? min_tokens : 0; }
+    bool prefill_uses_mfma(size_t n) const { return mfma_ok_ && prefill_mfma_min_ > 0 && (int)n >= prefill_mfma_min_; }
+
+    // Resets the device cache and runs the prompt (the reference's
+    // forward(prompt) with the cache, transformer.hpp:444-448).
+    void prefill(std::vector<int> const& prompt) {
+        check(vlrf_hip_model_reset(m_));
+        if (prompt.empty()) return;
+        int32_t next = 0;
+        std::vector<int32_t> ids(prompt.begin(), prompt.end());
+        if (prefill_uses_mfma(ids.size()))
+            check(vlrf_hip_model_prefill_mfma(m_, ids.data(), (int)ids.size(), &next));
+        else
+            check(vlrf_hip_model_prefill(m_, ids.data(), (int)ids.size(), &next));
+    }
+
+    // Tokens in the device cache.
+    int used() const { return vlrf_hip_model_used(m_); }
+
+    // Copies the device cache's first `used` rows of every layer into the
+    // engine's caches (the reference's token-major KVCache storage,
+    // kv_cache.hpp:132-148) and sets their `used`, so that a CPU forward
+    // with the cache continues where the device stopped.
+    void read_cache(std::vector<KVCache>& caches, int used) {
+        if (used < 0 || used > max_seq_) throw std::runtime_error("HipDecoder::read_cache: bad row count");
+        for (size_t l = 0; l < caches.size(); ++l) {
+            KVCache& c = caches[l];
+            int8_t *k = nullptr, *v = nullptr;
+            float *ks = nullptr, *vs = nullptr;
+            switch (c.dtype) {
+                case KVCacheDType::Q8_0:
+                    k = c.K_q8.data(); v = c.V_q8.data(); ks = c.K_scale.data(); vs = c.V_scale.data();
+                    break;
+                case KVCacheDType::F16:
+                    k = reinterpret_cast<int8_t*>(c.K_f16.data()); v = reinterpret_cast<int8_t*>(c.V_f16.data());
+                    break;
+                default:
+                    k = reinterpret_cast<int8_t*>(c.K.data_ptr()); v = reinterpret_cast<int8_t*>(c.V.data_ptr());
+                    break;
+            }
+            if (used) check(vlrf_hip_model_kv_read(m_, (int)l, 0, used, k, v, ks, vs));
+            c.used = used;
+        }
+    }
 
     // One decode step of `token` with the logits copied to host (vocab floats).
     int step(int token, float* logits) {
@@ -229,6 +288,8 @@ private:
     int vocab_;
     int max_seq_, eos_, bos_, kv_dtype_;
     int layer_dtype_ = VLRF_DT_F32, lm_dtype_ = VLRF_DT_F32;
+    bool mfma_ok_ = false;
+    int prefill_mfma_min_ = 0;
 };
 
 }  // namespace vlrf
