@@ -156,7 +156,11 @@ size_t vlrf_hip_weight_bytes(vlrf_hip_weight_t w);   /* device bytes of the pack
  * M <= 16 (decode, ops.hpp:238-310 for M = 1..16) computes in f32.  M > 16
  * (prefill, ops.hpp:254-305) runs on the matrix cores: x (normalised) and the
  * decoded weights are rounded to bf16, accumulation is f32; it takes Q8_0 or
- * Q4_0 weights with K % 64 == 0 and uses the context's scratch buffer. */
+ * Q4_0 weights with K % 64 == 0 and uses the context's scratch buffer.
+ * Graph capture of the stream: the scratch buffer cannot grow while the
+ * stream is captured (VLRF_HIP_ERR_ARG: make the same call once first), and a
+ * weight's bf16 expansion is not made then (the GEMM decodes the blocks in its
+ * tiles instead, same 1e-2 class). */
 int vlrf_hip_qlinear(vlrf_hip_ctx_t ctx, vlrf_hip_weight_t w, const float* x, float* y, int M,
                      const float* norm_w, float eps, const float* residual);
 

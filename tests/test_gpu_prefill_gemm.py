@@ -8,6 +8,7 @@ import pytest
 
 import vlrf_amd as V
 from conftest import rel_err
+from vlrf_amd import _lib
 from vlrf_amd import formats as F
 
 pytestmark = pytest.mark.gpu
@@ -158,3 +159,70 @@ def test_bf16_expansion_is_counted_in_the_weight_bytes(ctx):
     ctx.qlinear(w, x, y, M)
     ctx.sync()
     assert w.device_bytes == packed + 2 * N * K
+
+
+def _hip():
+    import ctypes as C
+    h = C.CDLL("libamdhip64.so")
+    h.hipStreamBeginCapture.argtypes = [C.c_void_p, C.c_int]
+    h.hipStreamEndCapture.argtypes = [C.c_void_p, C.POINTER(C.c_void_p)]
+    h.hipGraphInstantiate.argtypes = [C.POINTER(C.c_void_p), C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t]
+    h.hipGraphLaunch.argtypes = [C.c_void_p, C.c_void_p]
+    h.hipGraphExecDestroy.argtypes = [C.c_void_p]
+    h.hipGraphDestroy.argtypes = [C.c_void_p]
+    return h
+
+
+def test_prefill_gemm_under_graph_capture(orc):
+    """A stream under graph capture: the M > 128 GEMM records no allocation
+    (the weight's bf16 expansion is not made, the tiles decode the blocks),
+    the captured graph replays to the eager result, replay after replay with
+    eager work between; a call that would grow the context scratch while
+    capturing is refused with an error instead of being recorded."""
+    import ctypes as C
+    hip = _hip()
+    ctx = V.Context(0)                  # its own scratch buffer, empty until the first call
+    M, N, K = 160, 512, 1024
+    print(f"[case] qgemm under capture M={M} N={N} K={K}", flush=True)
+    w1, dec = _weight(ctx, 31, "cap", N, K, V.DT_Q8_0)
+    w2, _ = _weight(ctx, 31, "cap", N, K, V.DT_Q8_0)          # the same blocks, never expanded
+    packed = w2.device_bytes
+    x = F.normal(31, "capx", M * K).reshape(M, K)
+    dx, y1, y2 = ctx.to_device(x), ctx.alloc(M * N * 4), ctx.alloc(M * N * 4)
+    ctx.qlinear(w1, dx, y1, M)                                 # eager: grows the scratch, expands w1
+    ctx.sync()
+    eager = y1.download((M, N))
+    ref = x.astype(np.float64) @ dec.astype(np.float64).T
+    assert rel_err(eager, ref) <= TOL
+    s = C.c_void_p(ctx.stream())
+    assert hip.hipStreamBeginCapture(s, 2) == 0               # hipStreamCaptureModeRelaxed
+    rc = V.lib().vlrf_hip_qlinear(ctx.h, w2.h, dx.ptr, y2.ptr, M, None, C.c_float(0.0), None)
+    g = C.c_void_p()
+    assert hip.hipStreamEndCapture(s, C.byref(g)) == 0
+    assert rc == 0, V.lib().vlrf_hip_last_error()
+    assert V.lib().vlrf_hip_weight_bytes(w2.h) == packed       # no expansion recorded
+    ge = C.c_void_p()
+    assert hip.hipGraphInstantiate(C.byref(ge), g, None, None, 0) == 0
+    for i in range(3):
+        y2.zero()
+        ctx.qlinear(w1, dx, y1, M)                             # eager work between replays
+        assert hip.hipGraphLaunch(ge, s) == 0
+        ctx.sync()
+        got = y2.download((M, N))
+        assert rel_err(got, ref) <= TOL, i
+        assert rel_err(got, eager) <= 1e-3, i
+    hip.hipGraphExecDestroy(ge)
+    hip.hipGraphDestroy(g)
+    # Scratch growth while capturing: refused, the capture ends cleanly.
+    M2 = 4 * M
+    dx2, y3 = ctx.to_device(np.tile(x, (4, 1))), ctx.alloc(M2 * N * 4)
+    assert hip.hipStreamBeginCapture(s, 2) == 0
+    rc = V.lib().vlrf_hip_qlinear(ctx.h, w1.h, dx2.ptr, y3.ptr, M2, None, C.c_float(0.0), None)
+    g = C.c_void_p()
+    hip.hipStreamEndCapture(s, C.byref(g))
+    if g.value:
+        hip.hipGraphDestroy(g)
+    assert rc == _lib.ERR_ARG and b"captured" in V.lib().vlrf_hip_last_error()
+    ctx.qlinear(w1, dx2, y3, M2)                               # eagerly it runs
+    ctx.sync()
+    assert rel_err(y3.download((M2, N))[:M], ref) <= TOL

@@ -148,6 +148,15 @@ int vlrf_hip_ctx::rope_tables(int max_seq, int d_head, float theta, const float*
 
 int vlrf_hip_ctx::scratch(size_t bytes, float** out) {
     if (bytes > scratch_bytes) {
+        // Growing synchronises and allocates, which a stream under graph
+        // capture must not record.
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
+            (void)hipGetLastError();
+            set_error("scratch: the call needs %zu bytes of context scratch (%zu held) while the stream is being "
+                      "captured; make the same call once before capturing", bytes, scratch_bytes);
+            return VLRF_HIP_ERR_ARG;
+        }
         if (scratch_buf) {
             VH_CHECK(hipStreamSynchronize(stream));
             (void)hipFree(scratch_buf);

@@ -1179,10 +1179,19 @@ int launch_rows_to_bf16(hipStream_t s, const float* x, const float* w, uint16_t*
     return VLRF_HIP_OK;
 }
 
+// Makes the weight's bf16 expansion on first use (an allocation and one
+// kernel).  Never while `s` is being captured into a graph: the allocation
+// would be recorded mid-capture, so the GEMM then decodes the codes in its
+// tiles instead (the same results to the 1e-2 class, a little slower).
 bool weight_expand_bf16(hipStream_t s, const DevWeight& w) {
     if (w.bf) return true;
     const char* e = getenv("VLRF_HIP_PREFILL_BF16");
     if ((e && e[0] == '0') || !w.q || !w.d || (w.dtype != VLRF_DT_Q8_0 && w.dtype != VLRF_DT_Q4_0)) return false;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
+        (void)hipGetLastError();
+        return false;
+    }
     const size_t n = (size_t)w.N * w.K, nb = n / 32;
     uint16_t* bf = nullptr;
     if (hipMalloc(&bf, n * sizeof(uint16_t)) != hipSuccess) {
@@ -1233,11 +1242,14 @@ int launch_qgemm_swiglu(hipStream_t s, const DevWeight& wg, const DevWeight& wu,
     VH_ARG(wg.N == wu.N && wg.K == wu.K && wg.dtype == wu.dtype, "qgemm_swiglu: gate/up differ");
     VH_ARG(a && h, "qgemm_swiglu: null operand");
     if (M > 128) {
-        if (weight_expand_bf16(s, wg) && !weight_expand_bf16(s, wu)) {
-            (void)hipFree(wg.bf);   // both or neither
+        const bool both = weight_expand_bf16(s, wg) && weight_expand_bf16(s, wu);
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (!both && wg.bf && !wu.bf && hipStreamIsCapturing(s, &cs) == hipSuccess &&
+            cs == hipStreamCaptureStatusNone) {
+            (void)hipFree(wg.bf);   // both or neither (no free while capturing)
             wg.bf = nullptr;
         }
-        if (wg.bf) {
+        if (both) {
             if (h_bf16) launch_bgemm_plan<2>(s, a, wg, &wu, M, nullptr, h);
             else launch_bgemm_plan<3>(s, a, wg, &wu, M, nullptr, h);
         } else {
