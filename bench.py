@@ -43,11 +43,14 @@ steps within about 20 s.
     python bench.py --decode-8b [--layers 4]   # decode at the 8B layer shape (d_head 128)
     python bench.py --configs           # configs 1-3: kernel-level GB/s, one JSON line each
     python bench.py --summarize-trace run_kernel_trace.csv --steps 128 --launches-per-step 90
+    python bench.py --summarize-runs run_kernel_trace.csv --skip 2 --runs 5   # prefill runs
 
 --prefill prints its own line: one Llama-8B-shape
-layer (hidden 4096, 32/8 heads, head_dim 128, FFN 14336 SwiGLU, Q8_0 weights)
-over a causal 2048-token prompt of N(0,1) embedded rows, on the matrix cores
-(bf16 operands, f32 accumulation), each run from an empty cache.  FLOPs per
+layer (hidden 4096, 32/8 heads, head_dim 128, FFN 14336 SwiGLU, Q8_0 weights
+dequantized into the GEMM tiles) over a causal 2048-token prompt of N(0,1)
+embedded rows, on the matrix cores (bf16 operands, f32 accumulation), each run
+from an empty cache; the variant over bf16 copies of the weights is reported
+beside it as `bf16_expansion`.  FLOPs per
 layer = 2*T*(D*(D+2*dkv) + D*D + 3*D*F) + 4*H*d*T*T/2 = 927.7 GFLOP; the
 roofline is the dense bf16 MFMA peak (2.5 PFLOP/s).
 
@@ -152,8 +155,31 @@ def prefill_flops(cfg, T):
     return gemm + attn
 
 
+def prefill_runs(ctx, model, x, out, warmup, steps):
+    """warmup + steps layer prefills from an empty cache: (mean ms of the
+    timed runs, ms of the first run)."""
+    times, first_ms = [], None
+    for i in range(warmup + steps):
+        model.reset()
+        ctx.timer_start()
+        model.forward_hidden(x, out)
+        ms = ctx.timer_stop()
+        if first_ms is None:
+            first_ms = ms
+        if i >= warmup:
+            times.append(ms)
+    return float(np.mean(times)), first_ms
+
+
 def prefill_bench(a, V, F):
-    """One Llama-8B-shape layer, T-token causal prefill (MFMA path)."""
+    """One Llama-8B-shape layer, T-token causal prefill (MFMA path).
+
+    value: the stated workload of the configuration, quantized weights
+    dequantized into the GEMM's LDS tiles (VLRF_HIP_PREFILL_BF16=0: no bf16
+    copy of any weight exists).  Beside it, `bf16_expansion`: the same layer
+    once each weight has a bf16 expansion (2 bytes per weight, made by the
+    first GEMM of more than 128 rows on it), timed after its first run, with
+    the first run (which makes the expansions) reported as well."""
     dtype = V.DT_Q8_0 if a.dtype == "q8_0" else V.DT_Q4_0
     T = a.prefill_tokens
     cfg = F.llama8b_layer(dtype, max_seq_len=T)
@@ -165,32 +191,31 @@ def prefill_bench(a, V, F):
     log(f"[prefill] weights generated and uploaded in {time.time() - t0:.1f}s")
     x = ctx.to_device(F.normal(a.seed, "prefill.x", T * cfg["d_model"]))
     out = ctx.alloc(T * cfg["d_model"] * 4)
-    times, first_ms = [], None
-    for i in range(a.warmup + a.steps):
-        model.reset()
-        ctx.timer_start()
-        model.forward_hidden(x, out)
-        ms = ctx.timer_stop()
-        if first_ms is None:
-            first_ms = ms
-        if i >= a.warmup:
-            times.append(ms)
-    ms = float(np.mean(times))
     fl = prefill_flops(cfg, T)
+    os.environ["VLRF_HIP_PREFILL_BF16"] = "0"
+    ms, _ = prefill_runs(ctx, model, x, out, a.warmup, a.steps)
+    os.environ["VLRF_HIP_PREFILL_BF16"] = "1"
+    bms, bfirst = prefill_runs(ctx, model, x, out, 1, a.steps)
     tflops = fl / (ms / 1e3) / 1e12
+    btflops = fl / (bms / 1e3) / 1e12
+    log(f"[prefill] in-tile dequant {ms:.4f} ms ({tflops:.1f} TFLOP/s); bf16 expansions {bms:.4f} ms "
+        f"({btflops:.1f} TFLOP/s), first run with the expansion {bfirst:.4f} ms")
     return {
         "metric": "prefill TFLOP/s of one Llama-8B-shape layer, T=%d" % T,
         "value": round(tflops, 1), "unit": "TFLOP/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
         "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "bf16 operands, f32 accumulate, %s weights, q8_0 KV" % a.dtype,
+        "dtype": "bf16 operands, f32 accumulate, %s weights dequantized in the GEMM tiles, q8_0 KV" % a.dtype,
         "data": "synthetic: seeded N(0,0.02) weights, N(0,1) embedded rows",
         "config": {"workload": "llama-8B-shape layer prefill, causal T=%d from an empty cache" % T,
                    "weights": a.dtype, "hidden": 4096, "ffn": 14336, "heads": "32/8", "head_dim": 128},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
                      "flops_per_step": fl},
-        # the first (warm-up) run also makes the weights' bf16 expansions, once
-        "first_run_ms": round(first_ms, 4),
+        # The weights' bf16 expansions (2 bytes per weight beside the blocks),
+        # made once by the first run: not the configuration's workload.
+        "bf16_expansion": {"tflops": round(btflops, 1), "ms_per_step": round(bms, 4),
+                           "frac": round(btflops / MFMA_BF16_PEAK_TFLOPS, 4),
+                           "first_run_ms_with_expansion": round(bfirst, 4)},
     }
 
 
@@ -464,6 +489,59 @@ def summarize_trace(path, steps, per_step):
               f"{sum(v) / steps:.1f} | {100 * sum(v) / total:.1f} |")
 
 
+def summarize_runs(path, skip, nruns, clock_ghz=2.4, simds=1024):
+    """Per-kernel averages over runs [skip, skip + nruns) of a rocprofv3 CSV
+    (kernel trace or counter collection), a run being the dispatches between
+    two groups of the runtime's own copy/fill kernels (model.reset() before
+    each layer prefill).  With SQ_VALU_MFMA_BUSY_CYCLES in the file: the MFMA
+    busy fraction of each kernel, busy cycles / (duration x clock x SIMDs)."""
+    import csv
+    import collections
+    disp = collections.OrderedDict()
+    for r in csv.DictReader(open(path)):
+        k = r.get("Dispatch_Id") or r.get("Correlation_Id")
+        e = disp.setdefault(k, {"name": r["Kernel_Name"], "t0": int(r["Start_Timestamp"]),
+                                "us": (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3})
+        if "Counter_Name" in r:
+            e[r["Counter_Name"]] = float(r["Counter_Value"])
+    runs, cur = [], []
+    for e in sorted(disp.values(), key=lambda e: e["t0"]):
+        if e["name"].startswith("__amd_rocclr"):
+            if cur:
+                runs.append(cur)
+                cur = []
+            continue
+        cur.append(e)
+    if cur:
+        runs.append(cur)
+    sel = runs[skip:skip + nruns]
+    agg = collections.OrderedDict()
+    for run in sel:
+        for e in run:
+            n = e["name"].replace("void ", "").replace("vlrf_hip::(anonymous namespace)::", "")
+            agg.setdefault(n.replace("vlrf_hip::", "").split("(")[0], []).append(e)
+    mfma = any("SQ_VALU_MFMA_BUSY_CYCLES" in e for run in sel for e in run)
+    tot_us = sum(e["us"] for run in sel for e in run) / max(1, len(sel))
+    print(f"runs {skip}..{skip + len(sel) - 1} of {len(runs)} (dispatches per run {[len(r) for r in sel]}); "
+          f"kernel time per run {tot_us:.1f} us\n")
+    head = "| kernel | calls/run | avg us | min us | max us | us/run |" + (" MFMA busy |" if mfma else "")
+    print(head)
+    print("|---|---:|---:|---:|---:|---:|" + ("---:|" if mfma else ""))
+    busy_tot = 0.0
+    for n, es in agg.items():
+        us = [e["us"] for e in es]
+        line = (f"| {n} | {len(es) / len(sel):.2f} | {np.mean(us):.2f} | {np.min(us):.2f} | {np.max(us):.2f} | "
+                f"{sum(us) / len(sel):.1f} |")
+        if mfma:
+            mb = np.mean([e.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) for e in es])
+            busy_tot += mb * len(es) / len(sel)
+            line += f" {mb / (np.mean(us) * 1e-6 * clock_ghz * 1e9 * simds):.3f} |"
+        print(line)
+    if mfma:
+        print(f"\nwhole run: MFMA busy {busy_tot / (tot_us * 1e-6 * clock_ghz * 1e9 * simds):.3f} "
+              f"of the run's kernel time ({clock_ghz} GHz x {simds} SIMDs)")
+
+
 def decode8b_bench(a, V, F):
     """Decode at the Llama-8B layer shape (the d_head 128 path): `layers` layers
     (hidden 4096, 32/8 heads, FFN 14336) + a 32000-row LM head, cache filled to
@@ -517,6 +595,10 @@ def main():
     ap.add_argument("--summarize-trace", metavar="CSV",
                     help="print a markdown table of a rocprofv3 kernel trace's last --steps steps")
     ap.add_argument("--launches-per-step", type=int, default=90)
+    ap.add_argument("--summarize-runs", metavar="CSV",
+                    help="per-kernel table of runs [--skip, --skip + --runs) of a rocprofv3 CSV (prefill runs)")
+    ap.add_argument("--skip", type=int, default=0)
+    ap.add_argument("--runs", type=int, default=1)
     ap.add_argument("--roofline-only", action="store_true",
                     help="run the copy calibration and the roofline launches only (PMC passes)")
     ap.add_argument("--prefill", action="store_true",
@@ -531,6 +613,9 @@ def main():
 
     if a.summarize_trace:
         summarize_trace(a.summarize_trace, a.steps, a.launches_per_step)
+        return
+    if a.summarize_runs:
+        summarize_runs(a.summarize_runs, a.skip, a.runs)
         return
 
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
