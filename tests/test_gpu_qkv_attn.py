@@ -51,6 +51,8 @@ CASES = [  # (weights, cache, max_seq_len, heads, kv heads, d_model)
     (V.DT_Q8_0, V.KV_Q8_0, 600, 8, 1, 512),    # GQA 8
     (V.DT_Q8_0, V.KV_Q8_0, 600, 8, 4, 512),    # GQA 2
     (V.DT_Q4_0, V.KV_F16, 300, 8, 8, 512),     # no grouping, 8 KV heads
+    (V.DT_Q4_0, V.KV_Q8_0, 1100, 16, 2, 1024),  # 16 heads, three chunks
+    (V.DT_Q8_0, V.KV_Q8_0, 600, 32, 4, 2048),   # the 1.1B attention shape
 ]
 
 
@@ -132,4 +134,5 @@ def test_fused_wait_timeout_is_reported(ctx, orc):
         last = om.forward([last])
         ref.append(last)
     assert list(gpu) == ref
+
 
