@@ -135,6 +135,23 @@ def test_small_m_swiglu_ragged(ctx, orc, dtype):
     assert rel_err(dh.download((M, Fd)), ref) <= 1e-4
 
 
+def test_small_m_one_launch_calls_in_a_row(ctx, orc):
+    """The small-M path reduces each row tile's slice partials in the tile's
+    last workgroup, found by a per-tile counter that the reduction resets:
+    calls in a row on one context with different tile and slice counts (a
+    grid of fewer columns than slices, so workgroups take two slices, then
+    one slice, then 22 slices) each match the oracle, twice over."""
+    cases = [(4, 20000, 2048), (2, 300, 256), (16, 2048, 5632), (9, 5632, 2048)]
+    for rep in range(2):
+        for i, (M, N, K) in enumerate(cases):
+            print(f"[case] small-M calls in a row: M={M} N={N} K={K} (pass {rep})", flush=True)
+            w, dec = _weight(ctx, 40 + i, f"R{N}x{K}", N, K, V.DT_Q8_0)
+            x = F.normal(40 + i, f"rx{M}x{K}", M * K).reshape(M, K)
+            dx, dy = ctx.to_device(x), ctx.alloc(M * N * 4)
+            ctx.qlinear(w, dx, dy, M)
+            assert rel_err(dy.download((M, N)), orc.linear(x, dec)) <= 1e-4, (M, N, K)
+
+
 def test_qlinear_rejects_bad_shapes(ctx):
     w, _ = _weight(ctx, 11, "Wbad", 64, 96, V.DT_Q8_0)
     x = ctx.alloc(96 * 4 * 17)

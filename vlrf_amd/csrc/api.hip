@@ -181,6 +181,7 @@ vlrf_hip_ctx::~vlrf_hip_ctx() {
         (void)hipFree(t.sin_t);
     }
     if (scratch_buf) (void)hipFree(scratch_buf);
+    if (small_tile_ctr) (void)hipFree(small_tile_ctr);
     if (ev0) (void)hipEventDestroy(ev0);
     if (ev1) (void)hipEventDestroy(ev1);
     if (stream) (void)hipStreamDestroy(stream);
@@ -291,6 +292,13 @@ int vlrf_hip_init(int device, vlrf_hip_ctx_t* out) {
         return VLRF_HIP_ERR_RUNTIME;
     }
     c->noalloc_scratch = static_cast<float*>(fixed);
+    const size_t ctr_bytes = (size_t)kSmallMaxTiles * kSmallTileCtrStride * sizeof(int);
+    if (hipMalloc((void**)&c->small_tile_ctr, ctr_bytes) != hipSuccess ||
+        hipMemset(c->small_tile_ctr, 0, ctr_bytes) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
+        set_error("init: the small-M tile counters could not be allocated");
+        delete c;
+        return VLRF_HIP_ERR_NOMEM;
+    }
     *out = c;
     return VLRF_HIP_OK;
 }
@@ -592,7 +600,8 @@ int vlrf_hip_qlinear(vlrf_hip_ctx_t ctx, vlrf_hip_weight_t w, const float* x, fl
         float* scratch = nullptr;
         int rc = ctx->scratch(qlinear_small_scratch(w->w.N, w->w.K, false), &scratch);
         if (rc) return rc;
-        return launch_qlinear_small(ctx->stream, w->w, nullptr, x, M, norm_w, eps, residual, scratch, y);
+        return launch_qlinear_small(ctx->stream, w->w, nullptr, x, M, norm_w, eps, residual, scratch,
+                                    ctx->small_tile_ctr, kSmallMaxTiles, y);
     }
     if (M <= 16) return launch_qlinear(ctx->stream, w->w, x, y, M, norm_w, eps, residual);
     VH_ARG(x && y, "qlinear: null activation pointer");
@@ -614,7 +623,8 @@ int vlrf_hip_qlinear_swiglu(vlrf_hip_ctx_t ctx, vlrf_hip_weight_t wg, vlrf_hip_w
         float* scratch = nullptr;
         int rc = ctx->scratch(qlinear_small_scratch(wg->w.N, wg->w.K, true), &scratch);
         if (rc) return rc;
-        return launch_qlinear_small(ctx->stream, wg->w, &wu->w, x, M, norm_w, eps, nullptr, scratch, h);
+        return launch_qlinear_small(ctx->stream, wg->w, &wu->w, x, M, norm_w, eps, nullptr, scratch,
+                                    ctx->small_tile_ctr, kSmallMaxTiles, h);
     }
     if (M <= 16) return launch_qlinear_swiglu(ctx->stream, wg->w, wu->w, x, h, M, norm_w, eps);
     VH_ARG(x && h, "swiglu: null activation pointer");

@@ -191,12 +191,17 @@ int launch_qgemm_swiglu(hipStream_t s, const DevWeight& wg, const DevWeight& wu,
                         int M, void* h, bool h_bf16);
 // Small M (2..16) on the matrix cores with f32-class accuracy (x split into
 // bf16 hi + lo): y = x.W0^T (+ residual), or silu(x.W0^T) * (x.W1^T) when w1
-// is given.  Per-slice partial sums go to scratch (qlinear_small_scratch bytes).
+// is given, in one launch.  Per-slice partial sums go to scratch
+// (qlinear_small_scratch bytes); tile_ctr holds kSmallTileCtrStride ints per
+// row tile for at least qlinear_small_tiles(N) tiles, zero between calls.
+constexpr int kSmallTileCtrStride = 32;   // ints per row-tile counter (its own 128-byte line)
+constexpr int kSmallMaxTiles = 4096;      // row tiles a context's counters cover (N <= 262144 at 64 rows a tile)
 bool qlinear_small_supported(const DevWeight& w);
 size_t qlinear_small_scratch(int N, int K, bool two);
+int qlinear_small_tiles(int N);
 int launch_qlinear_small(hipStream_t s, const DevWeight& w0, const DevWeight* w1, const float* x,
                          int M, const float* norm_w, float eps, const float* residual, float* scratch,
-                         float* y);
+                         int* tile_ctr, int tile_ctr_tiles, float* y);
 int launch_rope(hipStream_t s, float* x, int T, int n_heads, int d_head, int pos_offset,
                 int max_seq, const float* cos_t, const float* sin_t);
 

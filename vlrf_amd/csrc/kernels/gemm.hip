@@ -921,26 +921,34 @@ __global__ __launch_bounds__(256) void rows_to_bf16_kernel(const float* __restri
 }
 
 // ---- small M on the matrix cores ------------------------------------------------
-// y[M,N] = x[M,K] . W^T for 2 <= M <= 16, W Q8_0/Q4_0 with K % 256 == 0, in two
-// kernels.  qlinear_small_partial_kernel: workgroup (gx, gy) owns weight rows
-// 128gx .. +127 and the 256-column slices gy, gy + gridDim.y, ...  Per slice it
+// y[M,N] = x[M,K] . W^T for 2 <= M <= 16, W Q8_0/Q4_0 with K % 256 == 0, in one
+// kernel.  qlinear_small_kernel<.., NW>: workgroup (gx, gy) owns the 16*NW
+// weight rows of tile gx and the 256-column slices gy, gy + gridDim.y, ...
+// (NW = 4 waves by default: 64-row tiles, about three workgroups per CU at
+// the configuration's shapes).  Per slice it
 // stages the 16 x 256 activations (rows >= M zero, times the norm weight when
 // given) in LDS as bf16 hi and lo planes, laid out [block][row][32] so that
 // lane (c, g) of a wave reads its MFMA operand, row c, columns 8g..8g+7 of a
 // block, as 16 contiguous bytes and the wave's 64 reads cover one KiB.  Wave w
-// owns rows 16w..16w+15 of the 128.  It loads their codes and scales with
+// owns rows 16w..16w+15 of the tile.  It loads their codes and scales with
 // 16-byte (codes) and 4-byte (scales) lane loads over contiguous runs of each
 // row, as the M = 1 GEMV does, and transposes them through LDS: lane (c, g)
 // then reads the codes of row c, columns 8g..8g+7 of each block (A operand),
 // one MFMA per plane multiplies them with the block's activations, and the
 // f32 result D (lane (m, g) holds rows 4g+v, v = 0..3, column m) takes the
-// block scales of those rows.  The workgroup's partial [128][16]
-// tile goes to P[gy][mat][n][16], and with a norm the slice's sum of x^2 per
-// row to SS[gy][16].  qlinear_small_reduce_kernel adds the partials in slice
-// order (deterministic) and applies the epilogue.  With a norm, x is scaled by
-// w before the product and by inv_rms after it: rms_norm is per row, so
-// W.((x*inv)*w) = inv * W.(x*w) (ops.hpp:488-498, rounded differently).
-constexpr int kSmallRows = 128;          // weight rows per workgroup (8 waves x 16)
+// block scales of those rows.  The workgroup's partial [128][M] tile goes to
+// P[gy][mat][n][16], and with a norm the slice's sum of x^2 per row to
+// SS[gx][gy][16], as device-coherent stores; once they are acknowledged one
+// thread adds 1 to the row tile's counter (its own 128-byte line).  The
+// workgroup that brings it to the slice count (the last of the tile's
+// slices) resets it and reduces the tile: the partials of every slice added
+// in slice order (deterministic, whichever workgroup comes last), then the
+// epilogue.  With a norm, x is scaled by w before the product and by inv_rms
+// after it: rms_norm is per row, so W.((x*inv)*w) = inv * W.(x*w)
+// (ops.hpp:488-498, rounded differently).  The counters belong to the
+// context (kSmallTileCtrStride ints per row tile, zero at creation, zero
+// again after every call), so calls need no clearing and none is recorded
+// under graph capture; calls on one context are serialised by its stream.
 constexpr int kSmallSlice = 256;         // K columns per slice (8 blocks)
 
 __device__ __forceinline__ float wave32_sum(float v) {     // sum over each half-wave
@@ -950,6 +958,14 @@ __device__ __forceinline__ float wave32_sum(float v) {     // sum over each half
     v += dpp_f<0x140>(v);
     const float2 t = swap_rows16(v, v);
     return t.x + t.y;
+}
+
+// Four floats at byte offset off of the buffer rs, written device-coherent by
+// another workgroup (sc1 load; rs is uniform, the offset per lane).
+__device__ __forceinline__ float4 ld_agent4(__amdgpu_buffer_rsrc_t rs, uint32_t off) {
+    typedef float f4v __attribute__((ext_vector_type(4)));
+    const f4v v = __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 16));
+    return make_float4(v.x, v.y, v.z, v.w);
 }
 
 // Codes of one lane's 8 columns of a block -> bf16 (exact).
@@ -969,27 +985,31 @@ __device__ __forceinline__ bf16x8 codes_bf16(uint2 c) {
     return r;
 }
 
-template <int WT, int NM>
-__global__ __launch_bounds__(512) void qlinear_small_partial_kernel(
+template <int WT, int NM, int EPI, int NW>
+__global__ __launch_bounds__(64 * NW) void qlinear_small_kernel(
     const uint8_t* __restrict__ qa, const __half* __restrict__ da, const uint8_t* __restrict__ qb,
     const __half* __restrict__ db, int N, int K, int M, const float* __restrict__ x,
-    const float* __restrict__ norm_w, float* __restrict__ P, float* __restrict__ SS) {
+    const float* __restrict__ norm_w, float eps, const float* __restrict__ residual, float* __restrict__ y,
+    float* __restrict__ P, float* __restrict__ SS, int* __restrict__ tile_ctr) {
     constexpr int CB = WT == VLRF_DT_Q8_0 ? 256 : 128;   // code bytes of a row per slice
     constexpr int CS = CB + 16;                          // padded LDS row stride
     constexpr int LPR = CB / 16;                         // lanes per row in a coalesced load
     constexpr int CL = 16 * LPR / 64;                    // 16-byte code loads per lane and matrix
     __shared__ __align__(16) uint16_t xh[8 * 16 * 32];
     __shared__ __align__(16) uint16_t xl[8 * 16 * 32];
-    __shared__ __align__(16) uint8_t cs[NM][8][16 * CS];  // per wave: its 16 rows' codes
-    __shared__ __align__(16) uint32_t ssc[NM][8][16 * 4]; // per wave: 16 rows x 8 f16 scales
+    __shared__ __align__(16) uint8_t cs[NM][NW][16 * CS];  // per wave: its 16 rows' codes
+    __shared__ __align__(16) uint32_t ssc[NM][NW][16 * 4]; // per wave: 16 rows x 8 f16 scales
+    constexpr int ROWS = 16 * NW, NI = 512 / (64 * NW);   // rows per workgroup; staging items per thread
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, c = lane & 15;
-    const int rbase = blockIdx.x * kSmallRows + 16 * wave;
+    const int rbase = blockIdx.x * ROWS + 16 * wave;
     const int ns = K / kSmallSlice;
     const size_t rowb = WT == VLRF_DT_Q8_0 ? (size_t)K : (size_t)K / 2;
-    // staging: thread t converts row t/32, columns 8(t%32) .. +7 of the slice
-    const int sm = tid >> 5, sk = 8 * (tid & 31);
-    float ss = 0.f;
+    // staging: item e = tid + 64 NW i converts row e/32, columns 8(e%32) .. +7 of the slice
+    const int sk = 8 * (tid & 31);
+    float ss[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) ss[i] = 0.f;
     f32x4 acc[NM];
 #pragma unroll
     for (int m = 0; m < NM; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -998,11 +1018,16 @@ __global__ __launch_bounds__(512) void qlinear_small_partial_kernel(
         const int k0 = sl * kSmallSlice;
         // Activations first (L2, needed first), then the codes and scales (HBM):
         // loads complete in order, so the staging below waits for x only.
-        float4 a0 = make_float4(0.f, 0.f, 0.f, 0.f), a1 = a0;
-        if (sm < M) {
-            const float4* xp = reinterpret_cast<const float4*>(x + (size_t)sm * K + k0 + sk);
-            a0 = xp[0];
-            a1 = xp[1];
+        float4 a0[NI], a1[NI];
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int sm = (tid >> 5) + 2 * NW * i;
+            a0[i] = a1[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (sm < M) {
+                const float4* xp = reinterpret_cast<const float4*>(x + (size_t)sm * K + k0 + sk);
+                a0[i] = xp[0];
+                a1[i] = xp[1];
+            }
         }
         // Codes: load i of lane l covers row LPR-group i*64/LPR + l/LPR, bytes
         // 16(l % LPR) .. +15 of the row's slice: runs of CB contiguous bytes.
@@ -1021,18 +1046,21 @@ __global__ __launch_bounds__(512) void qlinear_small_partial_kernel(
             const int r = min(rbase + (lane >> 2), N - 1);      // 16 rows x 4 dwords of scales
             sv[m] = *reinterpret_cast<const uint32_t*>(d + (size_t)r * (K / 32) + k0 / 32 + 2 * (lane & 3));
         }
-        {
+#pragma unroll
+        for (int it = 0; it < NI; ++it) {
+            const int sm = (tid >> 5) + 2 * NW * it;
+            float4 b0 = a0[it], b1 = a1[it];
             if (sm < M) {
-                ss += a0.x * a0.x + a0.y * a0.y + a0.z * a0.z + a0.w * a0.w +
-                      a1.x * a1.x + a1.y * a1.y + a1.z * a1.z + a1.w * a1.w;
+                ss[it] += b0.x * b0.x + b0.y * b0.y + b0.z * b0.z + b0.w * b0.w +
+                          b1.x * b1.x + b1.y * b1.y + b1.z * b1.z + b1.w * b1.w;
                 if (norm_w) {
                     const float4* wp = reinterpret_cast<const float4*>(norm_w + k0 + sk);
                     const float4 w0 = wp[0], w1 = wp[1];
-                    a0 = make_float4(a0.x * w0.x, a0.y * w0.y, a0.z * w0.z, a0.w * w0.w);
-                    a1 = make_float4(a1.x * w1.x, a1.y * w1.y, a1.z * w1.z, a1.w * w1.w);
+                    b0 = make_float4(b0.x * w0.x, b0.y * w0.y, b0.z * w0.z, b0.w * w0.w);
+                    b1 = make_float4(b1.x * w1.x, b1.y * w1.y, b1.z * w1.z, b1.w * w1.w);
                 }
             }
-            const float v[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+            const float v[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
             uint32_t h[4], l[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -1079,68 +1107,117 @@ __global__ __launch_bounds__(512) void qlinear_small_partial_kernel(
         __syncthreads();                      // before the next slice overwrites the staging
     }
 
+    // This slice's partials, device-coherent (the tile's last workgroup may
+    // run on another XCD): columns m < M only.
+    const int S = gridDim.y;
     float* Pw = P + (size_t)blockIdx.y * NM * N * 16;
 #pragma unroll
     for (int m = 0; m < NM; ++m)
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
             const int n = rbase + 4 * g + v;
-            if (n < N) Pw[((size_t)m * N + n) * 16 + c] = acc[m][v];
+            if (n < N && c < M)
+                __hip_atomic_store(&Pw[((size_t)m * N + n) * 16 + c], acc[m][v], __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
         }
     if (SS) {
-        ss = wave32_sum(ss);                  // threads 32r .. 32r+31 hold row r
-        if ((tid & 31) == 0 && blockIdx.x == 0) SS[blockIdx.y * 16 + sm] = ss;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int sm = (tid >> 5) + 2 * NW * i;
+            const float t = wave32_sum(ss[i]);   // threads 32r .. 32r+31 hold row r
+            if ((tid & 31) == 0 && sm < M)
+                __hip_atomic_store(&SS[((size_t)blockIdx.x * S + blockIdx.y) * 16 + sm], t, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
-}
+    __builtin_amdgcn_s_waitcnt(0x0F70);       // this wave's stores acknowledged (vmcnt 0)
+    __shared__ int last;
+    __syncthreads();
+    if (tid == 0) {
+        int* ctr = tile_ctr + (size_t)blockIdx.x * kSmallTileCtrStride;
+        last = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == S - 1;
+        if (last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!last) return;
 
-// y[m][n] = epilogue(sum over slices of P[s][.][n][m]): EPI 0 store, 1 add the
-// residual, 3 SwiGLU silu(g) * u; with SS, times inv_rms of row m first.
-template <int NM, int EPI>
-__global__ __launch_bounds__(256) void qlinear_small_reduce_kernel(const float* __restrict__ P,
-                                                                   const float* __restrict__ SS, int S,
-                                                                   int N, int K, int M, float eps,
-                                                                   const float* residual, float* y) {
-    const int n = blockIdx.x * 16 + (threadIdx.x >> 4), m = threadIdx.x & 15;
-    if (n >= N || m >= M) return;
-    // Four independent chains, combined in a fixed order: the loads of a
-    // chain do not wait for each other's L2 round trips.
-    const size_t st = (size_t)NM * N * 16;
-    float o[NM];
+    // The tile's reduction: thread (row r = tid / 4, columns 4q..4q+3).
+    const int r = tid >> 2, q4 = tid & 3, n = blockIdx.x * ROWS + r;
+    if (n >= N || 4 * q4 >= M) return;
+    // Byte offsets stay below 2^32: the partials are S * NM * N * 64 bytes and
+    // the host bounds that (qlinear_small_scratch).
+    const uint32_t st = (uint32_t)NM * N * 64;                      // bytes per slice
+    const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(P, 0, 0x7fffffff, 0x00020000);
+    float4 o[NM];
 #pragma unroll
     for (int j = 0; j < NM; ++j) {
-        const float* p = P + ((size_t)j * N + n) * 16 + m;
-        float t0 = 0.f, t1 = 0.f, t2 = 0.f, t3 = 0.f;
-        int s = 0;
-        for (; s + 4 <= S; s += 4) {
-            t0 += p[s * st];
-            t1 += p[(s + 1) * st];
-            t2 += p[(s + 2) * st];
-            t3 += p[(s + 3) * st];
-        }
-        for (; s < S; ++s) t0 += p[s * st];
-        o[j] = (t0 + t1) + (t2 + t3);
-    }
-    if (SS) {
-        float ss = 0.f;
-        for (int s = 0; s < S; ++s) ss += SS[s * 16 + m];
-        const float inv = 1.f / sqrtf(ss / (float)K + eps);
+        const uint32_t base = (uint32_t)(((size_t)j * N + n) * 64 + 16 * q4);
+        float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
+        int sl = 0;
+        for (; sl + 4 <= S; sl += 4) {        // four independent loads in flight, added in slice order
+            float4 v4[4];
 #pragma unroll
-        for (int j = 0; j < NM; ++j) o[j] *= inv;
+            for (int u = 0; u < 4; ++u) v4[u] = ld_agent4(prs, base + (uint32_t)(sl + u) * st);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                t.x += v4[u].x; t.y += v4[u].y; t.z += v4[u].z; t.w += v4[u].w;
+            }
+        }
+        for (; sl < S; ++sl) {
+            const float4 v4 = ld_agent4(prs, base + (uint32_t)sl * st);
+            t.x += v4.x; t.y += v4.y; t.z += v4.z; t.w += v4.w;
+        }
+        o[j] = t;
     }
-    const size_t off = (size_t)m * N + n;
-    float out = o[0];
-    if constexpr (EPI >= 2) out = o[1] * (o[0] / (1.f + expf(-o[0])));   // silu(g) * u, ops.hpp:409-441
-    if constexpr (EPI == 1) out += residual[off];
-    y[off] = out;
+    float inv[4] = {1.f, 1.f, 1.f, 1.f};
+    if (SS) {
+        const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(SS, 0, 0x7fffffff, 0x00020000);
+        float4 ssum = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int sl = 0; sl < S; ++sl) {
+            const float4 v4 = ld_agent4(srs, (uint32_t)((((size_t)blockIdx.x * S + sl) * 16 + 4 * q4) * 4));
+            ssum.x += v4.x; ssum.y += v4.y; ssum.z += v4.z; ssum.w += v4.w;
+        }
+        const float sv[4] = {ssum.x, ssum.y, ssum.z, ssum.w};
+#pragma unroll
+        for (int u = 0; u < 4; ++u) inv[u] = 1.f / sqrtf(sv[u] / (float)K + eps);
+    }
+    const float o0[4] = {o[0].x, o[0].y, o[0].z, o[0].w};
+    float o1[4] = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (NM == 2) {
+        o1[0] = o[1].x; o1[1] = o[1].y; o1[2] = o[1].z; o1[3] = o[1].w;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int m = 4 * q4 + u;
+        if (m >= M) break;
+        const size_t off = (size_t)m * N + n;
+        float out = o0[u] * inv[u];
+        if constexpr (EPI >= 2) {
+            const float gv = out, uv = o1[u] * inv[u];
+            out = uv * (gv / (1.f + expf(-gv)));   // silu(g) * u, ops.hpp:409-441
+        }
+        if constexpr (EPI == 1) out += residual[off];
+        y[off] = out;
+    }
 }
 
 // Workgroup columns: one per slice (every workgroup loads once and computes
 // once) up to about 1024 workgroups (4 per CU); beyond that columns take
 // several slices, which bounds the partial-sum scratch.
-int small_grid_y(int N, int K) {
-    const int groups = (N + kSmallRows - 1) / kSmallRows, ns = K / kSmallSlice;
+int small_grid_y(int N, int K, int rows) {
+    const int groups = (N + rows - 1) / rows, ns = K / kSmallSlice;
     const int want = (1024 + groups - 1) / groups;
     return want < ns ? want : ns;
+}
+
+// Waves per workgroup of the small-M kernel (16 rows each): 4 (VLRF_HIP_SMALL_WAVES=8: 8).
+int small_waves() {
+    static int nw = 0;
+    if (!nw) {
+        const char* e = getenv("VLRF_HIP_SMALL_WAVES");
+        nw = e && std::atoi(e) == 8 ? 8 : 4;
+    }
+    return nw;
 }
 
 // Compute units of the current device (the tile plan's round size).
@@ -1269,44 +1346,51 @@ bool qlinear_small_supported(const DevWeight& w) {
     return (w.dtype == VLRF_DT_Q8_0 || w.dtype == VLRF_DT_Q4_0) && w.q && w.d && w.K % kSmallSlice == 0;
 }
 
+int qlinear_small_tiles(int N) { const int rows = 16 * small_waves(); return (N + rows - 1) / rows; }
+
 size_t qlinear_small_scratch(int N, int K, bool two) {
-    const size_t S = (size_t)small_grid_y(N, K);
-    return S * (two ? 2 : 1) * (size_t)N * 16 * sizeof(float) + S * 16 * sizeof(float);
+    const size_t S = (size_t)small_grid_y(N, K, 16 * small_waves()), tiles = (size_t)qlinear_small_tiles(N);
+    return S * (two ? 2 : 1) * (size_t)N * 16 * sizeof(float) + tiles * S * 16 * sizeof(float);
 }
 
 int launch_qlinear_small(hipStream_t s, const DevWeight& w0, const DevWeight* w1, const float* x,
                          int M, const float* norm_w, float eps, const float* residual, float* scratch,
-                         float* y) {
+                         int* tile_ctr, int tile_ctr_tiles, float* y) {
     VH_ARG(M >= 2 && M <= 16, "qlinear_small: M=%d outside [2,16]", M);
     VH_ARG(qlinear_small_supported(w0), "qlinear_small: dtype %d / K %d not supported", w0.dtype, w0.K);
     if (w1) VH_ARG(w1->N == w0.N && w1->K == w0.K && w1->dtype == w0.dtype && w1->q && w1->d,
                    "qlinear_small: gate/up differ");
-    VH_ARG(x && y && scratch, "qlinear_small: null pointer");
-    const int N = w0.N, K = w0.K, S = small_grid_y(N, K), NM = w1 ? 2 : 1;
+    VH_ARG(x && y && scratch && tile_ctr, "qlinear_small: null pointer");
+    VH_ARG(!(w1 && residual), "qlinear_small: no residual on the SwiGLU form");
+    const int NW = small_waves();
+    const int N = w0.N, K = w0.K, S = small_grid_y(N, K, 16 * NW), NM = w1 ? 2 : 1;
+    VH_ARG(qlinear_small_tiles(N) <= tile_ctr_tiles, "qlinear_small: %d row tiles, the context counts %d",
+           qlinear_small_tiles(N), tile_ctr_tiles);
+    VH_ARG(qlinear_small_scratch(N, K, w1 != nullptr) < 0x7fffffffu, "qlinear_small: partials exceed 2 GiB");
     float* P = scratch;
     float* SS = norm_w ? scratch + (size_t)S * NM * N * 16 : nullptr;
-    const dim3 grid((N + kSmallRows - 1) / kSmallRows, S), rgrid((N + 15) / 16);
+    const dim3 grid(qlinear_small_tiles(N), S);
     const uint8_t* qb = w1 ? w1->q : nullptr;
     const __half* db = w1 ? w1->d : nullptr;
-#define VH_PART(WT, NMV)                                                                            \
-    hipLaunchKernelGGL((qlinear_small_partial_kernel<WT, NMV>), grid, dim3(512), 0, s, w0.q, w0.d, qb, \
-                       db, N, K, M, x, norm_w, P, SS)
-    if (w0.dtype == VLRF_DT_Q8_0) {
-        if (w1) VH_PART(VLRF_DT_Q8_0, 2); else VH_PART(VLRF_DT_Q8_0, 1);
-    } else {
-        if (w1) VH_PART(VLRF_DT_Q4_0, 2); else VH_PART(VLRF_DT_Q4_0, 1);
-    }
-#undef VH_PART
-    VH_LAUNCHED();
-    if (w1)
-        hipLaunchKernelGGL((qlinear_small_reduce_kernel<2, 3>), rgrid, dim3(256), 0, s, P, SS, S, N, K, M, eps,
-                           nullptr, y);
-    else if (residual)
-        hipLaunchKernelGGL((qlinear_small_reduce_kernel<1, 1>), rgrid, dim3(256), 0, s, P, SS, S, N, K, M, eps,
-                           residual, y);
-    else
-        hipLaunchKernelGGL((qlinear_small_reduce_kernel<1, 0>), rgrid, dim3(256), 0, s, P, SS, S, N, K, M, eps,
-                           nullptr, y);
+#define VH_SMALL(WT, NMV, EPIV)                                                                             \
+    do {                                                                                                    \
+        if (NW == 8)                                                                                        \
+            hipLaunchKernelGGL((qlinear_small_kernel<WT, NMV, EPIV, 8>), grid, dim3(512), 0, s, w0.q, w0.d, qb, \
+                               db, N, K, M, x, norm_w, eps, residual, y, P, SS, tile_ctr);                  \
+        else                                                                                                \
+            hipLaunchKernelGGL((qlinear_small_kernel<WT, NMV, EPIV, 4>), grid, dim3(256), 0, s, w0.q, w0.d, qb, \
+                               db, N, K, M, x, norm_w, eps, residual, y, P, SS, tile_ctr);                  \
+    } while (0)
+#define VH_SMALL_T(WT)                                         \
+    do {                                                       \
+        if (w1) VH_SMALL(WT, 2, 3);                            \
+        else if (residual) VH_SMALL(WT, 1, 1);                 \
+        else VH_SMALL(WT, 1, 0);                               \
+    } while (0)
+    if (w0.dtype == VLRF_DT_Q8_0) VH_SMALL_T(VLRF_DT_Q8_0);
+    else VH_SMALL_T(VLRF_DT_Q4_0);
+#undef VH_SMALL_T
+#undef VH_SMALL
     VH_LAUNCHED();
     return VLRF_HIP_OK;
 }

@@ -22,6 +22,7 @@ struct vlrf_hip_ctx {
     void* scratch_buf = nullptr;     // split-K partials of the standalone ops
     size_t scratch_bytes = 0;
     float* noalloc_scratch = nullptr;   // this device's fixed array for vlrf_hip_attn_decode_noalloc
+    int* small_tile_ctr = nullptr;      // small-M linear: row-tile counters (zero between calls)
 
     // Device cos/sin tables built on the host as RopeCache::init does.
     int rope_tables(int max_seq, int d_head, float theta, const float** c, const float** s);
