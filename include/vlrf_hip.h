@@ -116,9 +116,11 @@ int vlrf_hip_kv_read(vlrf_hip_kv_t kv, int layer, int row0, int n, int8_t* k_q, 
 /* Replaces: KVCache::dequant_into (kv_cache.hpp:259-286): device f32
  * K_out/V_out [ctx_len, n_kv_heads*d_head], token-major like the reference. */
 int vlrf_hip_kv_dequant(vlrf_hip_kv_t kv, int layer, int ctx_len, float* K_out, float* V_out);
-/* Decode attention of one token over the cache (any dtype), GQA-aware split-K:
+/* Decode attention of one token over the cache (any dtype), GQA-aware:
  * q [n_heads*d_head] (already rotated), out [n_heads*d_head]; query head h
- * reads kv head h/(n_heads/n_kv_heads); non-causal over [0, ctx_len).
+ * reads kv head h/(n_heads/n_kv_heads); non-causal over [0, ctx_len).  At
+ * d_head 64 and ctx_len <= 8192 one launch (each head's context in at most 16
+ * chunks, merged by the head's last workgroup), else split-K + a combine.
  * Replaces the decode branch of AttentionBlock::forward: dequant_into +
  * reshape/expand_kv_heads + sdp_heads (attention.hpp:127-176). */
 int vlrf_hip_attn_decode(vlrf_hip_kv_t kv, int layer, const float* q, float* out,
@@ -126,10 +128,11 @@ int vlrf_hip_attn_decode(vlrf_hip_kv_t kv, int layer, const float* q, float* out
 /* vlrf_hip_attn_decode that allocates nothing: no counterpart in the
  * reference; for callers that cannot allocate device memory (HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
- * arguments, kernels and results; the split-K partials go to one fixed 2 MiB
- * device array per GPU (resolved at vlrf_hip_init), so n_heads * splits *
- * (d_head + 2) floats must fit in 2^19 (splits = ceil(ctx_len / 64)),
- * otherwise VLRF_HIP_ERR_ARG.  Calls that overlap on one GPU race. */
+ * arguments, kernels and results; the chunk / split-K partials go to one
+ * fixed 2 MiB device array per GPU (resolved at vlrf_hip_init), so n_heads *
+ * splits * (d_head + 2) floats must fit in 2^19 (splits = ceil(ctx_len / 64)),
+ * otherwise VLRF_HIP_ERR_ARG; the per-head merge counters are the context's
+ * (allocated at vlrf_hip_init).  Calls that overlap on one GPU race. */
 int vlrf_hip_attn_decode_noalloc(vlrf_hip_kv_t kv, int layer, const float* q, float* out,
                                  int n_heads, int ctx_len, float scale);
 

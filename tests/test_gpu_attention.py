@@ -91,9 +91,9 @@ def _gqa_reference(orc, q, kq, vq, ks, vs, n_heads, n_kv, d, ctx_len, scale):
                                                     (8, 2, 64, 4600)])
 def test_q8_decode_attention(ctx, orc, n_heads, n_kv, d, ctx_len):
     """Benchmark config 2 (32q/4kv, d 64, ctx 4096) and other GQA groupings.
-    Caches of up to 512 rows at d_head 64 take the single-pass kernel (one
-    workgroup per query head; 509 + 3 rows fill every wave's round), larger
-    ones and d_head 128 the split-K kernel and its combine."""
+    d_head 64 takes the one-launch chunked kernel (64-row chunks up to 1024
+    tokens; 509 + 3 rows fill a chunk's round), d_head 128 the split-K
+    kernel and its combine."""
     import vlrf_amd as V_
     print(f"[case] q8 decode heads={n_heads}/{n_kv} d={d} ctx={ctx_len}", flush=True)
     row = n_kv * d
@@ -111,3 +111,46 @@ def test_q8_decode_attention(ctx, orc, n_heads, n_kv, d, ctx_len):
     ref = _gqa_reference(orc, q, kq, vq, ks, vs, n_heads, n_kv, d, ctx_len, scale)
     assert rel_err(out, ref) <= 1e-3
     assert np.max(np.abs(out - ref)) <= 1e-4
+
+
+def _dequant_rows(kv, ctx_len):
+    import vlrf_amd as V_
+    kq, vq, ks, vs = kv.read(0, 0, ctx_len)
+    if kv.dtype == V_.KV_Q8_0:
+        return kq.astype(np.float32) * ks[:, None], vq.astype(np.float32) * vs[:, None]
+    if kv.dtype == V_.KV_F16:
+        return kq.view(np.float16).astype(np.float32), vq.view(np.float16).astype(np.float32)
+    return kq, vq
+
+
+@pytest.mark.parametrize("kv_name", ["Q8_0", "F16", "F32"])
+@pytest.mark.parametrize("n_heads,n_kv,ctx_len", [(32, 4, 1024), (32, 4, 1025), (8, 2, 2049),
+                                                  (16, 16, 4097), (32, 4, 8192), (8, 8, 8193)])
+def test_decode_attention_chunk_sizes(ctx, orc, kv_name, n_heads, n_kv, ctx_len):
+    """d_head 64 decode attention in one launch: contexts at the chunk-size
+    steps (64 rows up to 1024 tokens, then 128/256/512 so that at most 16
+    chunks cover the context) and past 8192 (the split-K pair of launches).
+    Two calls in a row, the second over a shorter context: the per-head
+    counters left by the first must read zero again."""
+    import vlrf_amd as V_
+    dt = {"Q8_0": V_.KV_Q8_0, "F16": V_.KV_F16, "F32": V_.KV_F32}[kv_name]
+    print(f"[case] decode chunks kv={kv_name} heads={n_heads}/{n_kv} ctx={ctx_len}", flush=True)
+    d, row = 64, n_kv * 64
+    kv = V_.KVCache(ctx, 1, ctx_len + 5, n_kv, d, dt)
+    K = F.normal(9, "Kc", ctx_len * row)
+    Vv = F.normal(9, "Vc", ctx_len * row)
+    kv.append(0, ctx.to_device(K), ctx.to_device(Vv), ctx_len)
+    Kd, Vd = _dequant_rows(kv, ctx_len)
+    scale = np.float32(0.125)
+    rep = n_heads // n_kv
+    for call, n in enumerate((ctx_len, max(1, ctx_len // 3))):
+        q = F.normal(call, "q", n_heads * d)
+        dout = ctx.alloc(q.nbytes)
+        kv.attention_decode(0, ctx.to_device(q), dout, n_heads, n, scale)
+        out = dout.download(q.shape)
+        ref = np.concatenate([orc.flash_attn_head(q[h * d:(h + 1) * d][None, :],
+                                                  Kd[:n, (h // rep) * d:(h // rep + 1) * d],
+                                                  Vd[:n, (h // rep) * d:(h // rep + 1) * d], scale, False)[0]
+                              for h in range(n_heads)])
+        assert rel_err(out, ref) <= 1e-3, (call, n)
+        assert np.max(np.abs(out - ref)) <= 1e-4, (call, n)

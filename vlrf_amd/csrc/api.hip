@@ -402,7 +402,7 @@ int vlrf_hip_attn_f32(vlrf_hip_ctx_t ctx, const float* Q, const float* K, const 
         int rc = ctx->scratch((size_t)n_h * splits * (d_h + 2) * sizeof(float), &part);
         if (rc) return rc;
         return launch_attn_decode(ctx->stream, Q, K, V, nullptr, nullptr, VLRF_KV_F32, (long)ctx_len * d_h, n_h,
-                                  n_h, d_h, ctx_len, nullptr, splits, scale, part, O);
+                                  n_h, d_h, ctx_len, nullptr, splits, scale, part, O, nullptr, ctx->small_tile_ctr);
     }
     return launch_attn_f32_tiled(ctx->stream, Q, K, V, O, n_h, T, ctx_len, d_h, scale, causal);
 }
@@ -531,7 +531,8 @@ int vlrf_hip_attn_decode(vlrf_hip_kv_t kv, int layer, const float* q, float* out
     if (rc) return rc;
     const KVLayer& L = kv->layers[layer];
     return launch_attn_decode(kv->ctx->stream, q, L.k, L.v, L.ks, L.vs, L.dtype, (long)kv->max_seq * kv->d_head,
-                              n_heads, kv->n_kv, kv->d_head, ctx_len, nullptr, splits, scale, part, out);
+                              n_heads, kv->n_kv, kv->d_head, ctx_len, nullptr, splits, scale, part, out, nullptr,
+                              kv->ctx->small_tile_ctr);
 }
 
 int vlrf_hip_attn_decode_noalloc(vlrf_hip_kv_t kv, int layer, const float* q, float* out, int n_heads,
@@ -552,7 +553,7 @@ int vlrf_hip_attn_decode_noalloc(vlrf_hip_kv_t kv, int layer, const float* q, fl
     const KVLayer& L = kv->layers[layer];
     return launch_attn_decode(kv->ctx->stream, q, L.k, L.v, L.ks, L.vs, L.dtype, (long)kv->max_seq * kv->d_head,
                               n_heads, kv->n_kv, kv->d_head, ctx_len, nullptr, splits, scale,
-                              kv->ctx->noalloc_scratch, out);
+                              kv->ctx->noalloc_scratch, out, nullptr, kv->ctx->small_tile_ctr);
 }
 
 // ---- quantized linear ----------------------------------------------------------

@@ -262,12 +262,14 @@ int attn_decode_chunks128(int cap, int n_heads, int n_kv, int kv_dtype);
 // with row scales ks/vs, VLRF_KV_F16 bits, VLRF_KV_F32) laid out
 // [n_kv][head_stride/d][d]: a cache layer (head_stride = max_seq*d) or plain
 // f32 K/V.  ctx from *ctx_dev (+1 when fused) when non-null.  part must hold
-// n_heads*n_splits*(d+2) floats.
+// n_heads*n_splits*(d+2) floats.  ctr (unfused, host context length, d 64): a
+// context's counter array (kSmallTileCtrStride ints per query head, zero
+// between calls); with it the attention and the chunk merge run in one launch.
 int attn_decode_splits(int max_ctx);
 int launch_attn_decode(hipStream_t s, const float* q, const void* kc, const void* vc, const float* ks,
                        const float* vs, int kv_dtype, long head_stride, int n_heads, int n_kv, int d_head,
                        int ctx_len, const int* ctx_dev, int n_splits, float scale, float* part, float* out,
-                       const DecodeFuse* fuse = nullptr);
+                       const DecodeFuse* fuse = nullptr, int* ctr = nullptr);
 int launch_attn_f32_tiled(hipStream_t s, const float* Q, const float* K, const float* V,
                           float* O, int n_h, int T, int ctx_len, int d_h, float scale,
                           int causal);

@@ -31,6 +31,7 @@
 #include "attn_core.hpp"
 
 #include <cmath>
+#include <cstdlib>
 
 namespace vlrf_hip {
 namespace {
@@ -394,6 +395,7 @@ constexpr int kSPMaxCtx = kSPWaves * 64 * kSPRounds;   // cache rows the single 
 // Chunked form (CH tokens per workgroup, one query head each): partials of
 // kChunkStride floats -- acc[0..63] (unnormalised), m at 64, l at 65 --
 // merged by the next GEMV's prologue.
+constexpr int kChunksMaxCtx = 8192;   // the one-launch chunked form: at most 16 chunks of 512 rows
 constexpr int kCH = 512, kChunkStride = kAttnChunkStride;   // 256 / 1024: 0.645 / 0.673 ms per step against 0.620
 
 // CH > 0 (fused decode only): the same algorithm on one CH-token chunk of the
@@ -1037,6 +1039,93 @@ __global__ __launch_bounds__(kCH) void attn_chunk128_kernel(const float* __restr
                          });
 }
 
+
+// ---- stand-alone decode attention in one launch ----------------------------------
+// vlrf_hip_attn_decode / attn_f32 at T = 1 (AttentionBlock::flash_attn_head for
+// one query row over the cache, attention.hpp:207-309, non-causal): workgroup
+// (query head h, chunk c) runs attn::chunk over cache rows [c*CH, c*CH + CH)
+// and stores its unnormalised partial (acc[64], m, l; stride D + 2) device-
+// coherent; once those stores are acknowledged one thread adds 1 to the head's
+// counter (its own 128-byte line in the context's counter array, zero between
+// calls).  The workgroup that brings it to nch resets it and merges the head's
+// partials in chunk order with the log-sum-exp rule (the same result whichever
+// workgroup comes last): out = sum_c e^(m_c - M) acc_c / sum_c e^(m_c - M) l_c.
+// nch = ceil(ctx_len / CH) <= kAttnMaxChunks; rows at or past the context are
+// masked.  The REP query heads of a chunk run on one XCD (workgroup b on XCD
+// b % 8), as in the fused step, so a chunk's K/V rows come from HBM once.
+template <int KVT, int REP, int CH>
+__global__ __launch_bounds__(CH) void attn_decode_chunks_kernel(
+    const float* __restrict__ q, const int8_t* kc, const int8_t* vc, const float* ks, const float* vs,
+    long head_stride, int ctx_len, float scale, float* __restrict__ out, float* __restrict__ part,
+    int* __restrict__ ctr, int n_kv, int nch) {
+    constexpr int D = attn::D, HALF = attn::HALF, NW = CH / 64, PS = D + 2;
+    __shared__ attn::Smem<NW> sm;
+    __shared__ int last;
+    const int b = blockIdx.x, k = b >> 3, r = k % REP, pc = (b & 7) + 8 * (k / REP);
+    if (pc >= n_kv * nch) return;   // padding of the grid: no counter, no partial
+    const int g = pc / nch, chunk = pc - g * nch, h = g * REP + r, c0 = chunk * CH;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int cap = (int)(head_stride / D);
+    const size_t hb = (size_t)g * head_stride;
+    float q0 = 0.f, q1 = 0.f;
+    if (w == 0) {
+        const int j = lane & (HALF - 1);
+        q0 = q[(size_t)h * D + j];
+        q1 = q[(size_t)h * D + j + HALF];
+    }
+    attn::Round<KVT> R;
+    attn::load_round<KVT>(R, kc, vc, ks, vs, hb, c0 + w * 64, cap, lane);
+    const int ctx = min(ctx_len, cap);
+    const DecodeFuse fz{};
+    const attn::NewRow nr;
+    float* pp = part + ((size_t)h * nch + chunk) * PS;
+    attn::chunk<KVT, false, NW>(sm, R, q0, q1, nr, false, false, g, c0, cap, hb, ctx, -1, false, false, scale, fz,
+                                [&](int t, float ot, float mt, float lt) {
+                                    __hip_atomic_store(&pp[t], ot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                                    if (t == 0) {
+                                        __hip_atomic_store(&pp[D], mt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                                        __hip_atomic_store(&pp[D + 1], lt, __ATOMIC_RELAXED,
+                                                           __HIP_MEMORY_SCOPE_AGENT);
+                                    }
+                                });
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // this wave's stores acknowledged (vmcnt 0)
+    __syncthreads();
+    if (tid == 0) {
+        int* c = ctr + (size_t)h * kSmallTileCtrStride;
+        last = __hip_atomic_fetch_add(c, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nch - 1;
+        if (last) __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!last || tid >= D) return;
+    // The merge: lane d of wave 0, every chunk's loads issued before any use.
+    const float* ph = part + (size_t)h * nch * PS;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(ph), 0, nch * PS * 4,
+                                                                        0x00020000);
+    float pm[kAttnMaxChunks], pl[kAttnMaxChunks], pa[kAttnMaxChunks];
+#pragma unroll
+    for (int c = 0; c < kAttnMaxChunks; ++c) {
+        const int o = (c < nch ? c : nch - 1) * PS;
+        pm[c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, (o + D) * 4, 0, 16));
+        pl[c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, (o + D + 1) * 4, 0, 16));
+        pa[c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, (o + tid) * 4, 0, 16));
+    }
+    float M = kNegInf;
+#pragma unroll
+    for (int c = 0; c < kAttnMaxChunks; ++c)
+        if (c < nch) M = fmaxf(M, pm[c]);
+    float L = 0.f, O = 0.f;
+    if (M != kNegInf) {
+#pragma unroll
+        for (int c = 0; c < kAttnMaxChunks; ++c)
+            if (c < nch && pm[c] != kNegInf) {
+                const float wgt = expf(pm[c] - M);
+                L += wgt * pl[c];
+                O += wgt * pa[c];
+            }
+    }
+    out[(size_t)h * D + tid] = L > 0.f ? O * (1.f / L) : 0.f;
+}
+
 }  // namespace
 
 int attn_decode_splits(int max_ctx) { return (max_ctx + kChunk - 1) / kChunk; }
@@ -1057,7 +1146,7 @@ int attn_decode_chunks128(int cap, int n_heads, int n_kv, int kv_dtype) {
 int launch_attn_decode(hipStream_t s, const float* q, const void* kc, const void* vc, const float* ks,
                        const float* vs, int kv_dtype, long head_stride, int n_heads, int n_kv, int d_head,
                        int ctx_len, const int* ctx_dev, int n_splits, float scale, float* part, float* out,
-                       const DecodeFuse* fuse) {
+                       const DecodeFuse* fuse, int* ctr) {
     VH_ARG(n_kv > 0 && n_heads % n_kv == 0, "attn_decode: n_heads %d not a multiple of n_kv %d",
            n_heads, n_kv);
     const int rep = n_heads / n_kv;
@@ -1122,6 +1211,47 @@ int launch_attn_decode(hipStream_t s, const float* q, const void* kc, const void
         }
 #undef VH_CHK_R
 #undef VH_CHK
+        VH_LAUNCHED();
+        return VLRF_HIP_OK;
+    }
+    static const bool chunks_on = [] {
+        const char* e = std::getenv("VLRF_HIP_ATTN_CHUNKS");   // "0": the split-K pair of launches instead
+        return !(e && e[0] == '0');
+    }();
+    if (chunks_on && !fuse && ctr && !ctx_dev && d_head == 64 && ctx_len <= kChunksMaxCtx &&
+        n_heads <= kSmallMaxTiles) {
+        // One launch: the smallest chunk (64..512 rows) that splits the context
+        // into at most kAttnMaxChunks chunks; nch <= ceil(ctx_len / 64) = n_splits,
+        // so the partials fit the split-K buffer.
+        int CHR = 64;
+        while ((ctx_len + CHR - 1) / CHR > kAttnMaxChunks) CHR *= 2;
+        const int nch = (ctx_len + CHR - 1) / CHR;
+        const dim3 cgrid(8 * rep * ((n_kv * nch + 7) / 8));
+#define VH_CC(KT, R, C)                                                                                        \
+    VH_LAUNCH((attn_decode_chunks_kernel<KT, R, C>), cgrid, dim3(C), 0, s, q, k8, v8, ks, vs, head_stride, \
+              ctx_len, scale, out, part, ctr, n_kv, nch)
+#define VH_CC_R(KT, C)                      \
+    switch (rep) {                          \
+        case 1: VH_CC(KT, 1, C); break;     \
+        case 2: VH_CC(KT, 2, C); break;     \
+        case 4: VH_CC(KT, 4, C); break;     \
+        default: VH_CC(KT, 8, C); break;    \
+    }
+#define VH_CC_T(C)                                             \
+    switch (kv_dtype) {                                        \
+        case VLRF_KV_Q8_0: VH_CC_R(VLRF_KV_Q8_0, C) break;     \
+        case VLRF_KV_F16: VH_CC_R(VLRF_KV_F16, C) break;       \
+        default: VH_CC_R(VLRF_KV_F32, C) break;                \
+    }
+        switch (CHR) {
+            case 64: VH_CC_T(64) break;
+            case 128: VH_CC_T(128) break;
+            case 256: VH_CC_T(256) break;
+            default: VH_CC_T(512) break;
+        }
+#undef VH_CC_T
+#undef VH_CC_R
+#undef VH_CC
         VH_LAUNCHED();
         return VLRF_HIP_OK;
     }
