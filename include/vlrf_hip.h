@@ -35,14 +35,14 @@ extern "C" {
 
 /* ---- data types: GGML type ids, as the reference's GGUF reader uses them
  * (tools/converter/convert_gguf.py GGMLType) -------------------------------- */
-#define VLRF_DT_F32   0
-#define VLRF_DT_Q4_0  2
-#define VLRF_DT_Q8_0  8
+#define VLRF_HIP_DT_F32   0
+#define VLRF_HIP_DT_Q4_0  2
+#define VLRF_HIP_DT_Q8_0  8
 
 /* KV cache dtypes: reference include/model/kv_cache.hpp:36-40 (KVCacheDType). */
-#define VLRF_KV_F32   0
-#define VLRF_KV_F16   1   /* the reference's f32_to_f16 (kv_cache.hpp:68-97), bit-exact */
-#define VLRF_KV_Q8_0  2
+#define VLRF_HIP_KV_F32   0
+#define VLRF_HIP_KV_F16   1   /* the reference's f32_to_f16 (kv_cache.hpp:68-97), bit-exact */
+#define VLRF_HIP_KV_Q8_0  2
 
 typedef struct vlrf_hip_ctx*    vlrf_hip_ctx_t;
 typedef struct vlrf_hip_weight* vlrf_hip_weight_t;
@@ -87,7 +87,7 @@ int vlrf_hip_attn_f32(vlrf_hip_ctx_t ctx, const float* Q, const float* K, const 
                       float* O, int n_h, int T, int ctx_len, int d_h, float scale, int causal);
 
 /* ============================================================================
- * KV cache (reference kv_cache.hpp:14-17,132-293), dtype VLRF_KV_F32, _F16 or
+ * KV cache (reference kv_cache.hpp:14-17,132-293), dtype VLRF_HIP_KV_F32, _F16 or
  * _Q8_0 (per token row).  Device layout: per layer, K and V elements
  * [n_kv_heads][max_seq][d_head] (head-major, so one head's history is one
  * contiguous stream): f32, f16 bits, or int8 codes with one f32 scale per
@@ -239,8 +239,8 @@ int vlrf_synth_tokens(uint64_t seed, uint64_t stream, int vocab, int32_t* out, i
 typedef struct vlrf_hip_model_config {
     int32_t vocab_size, d_model, d_ff, n_heads, n_kv_heads, n_layers, max_seq_len;
     float   norm_eps, rope_theta;
-    int32_t weight_dtype;   /* VLRF_DT_Q8_0 / VLRF_DT_Q4_0 / VLRF_DT_F32 for the projections */
-    int32_t kv_dtype;       /* VLRF_KV_F32 / _F16 / _Q8_0: ModelConfig::kv_cache_dtype (config.hpp),
+    int32_t weight_dtype;   /* VLRF_HIP_DT_Q8_0 / VLRF_HIP_DT_Q4_0 / VLRF_HIP_DT_F32 for the projections */
+    int32_t kv_dtype;       /* VLRF_HIP_KV_F32 / _F16 / _Q8_0: ModelConfig::kv_cache_dtype (config.hpp),
                                the reference's KVCacheDType numbering, whose default F32 is 0 */
 } vlrf_hip_model_config;
 
@@ -251,7 +251,7 @@ void vlrf_hip_model_destroy(vlrf_hip_model_t m);
  * "layers.{l}.ffn.gate.weight"): embed.weight / lm_head.weight /
  * ln_final.weight, layers.{l}.{ln1,ln2}.weight,
  * layers.{l}.attn.{q,k,v,o}_proj.weight, layers.{l}.ffn.{gate,fc1,fc2}.weight.
- * Norm weights and the embedding are f32 (dtype VLRF_DT_F32); projection and
+ * Norm weights and the embedding are f32 (dtype VLRF_HIP_DT_F32); projection and
  * LM-head weights are in `dtype` host blocks.  Synchronous. */
 int  vlrf_hip_model_set_weight(vlrf_hip_model_t m, const char* name, const void* host,
                                int dtype, int rows, int cols);

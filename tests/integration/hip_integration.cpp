@@ -206,18 +206,18 @@ void check_ops(HipBackend const& be) {
 
 // Block round trip so the reference runs on exactly what the blocks hold.
 void roundtrip(Tensor& t, int dtype) {
-    std::vector<unsigned char> blocks((size_t)t.numel() / 32 * (dtype == VLRF_DT_Q8_0 ? 34 : 18));
-    if (dtype == VLRF_DT_Q8_0)
+    std::vector<unsigned char> blocks((size_t)t.numel() / 32 * (dtype == VLRF_HIP_DT_Q8_0 ? 34 : 18));
+    if (dtype == VLRF_HIP_DT_Q8_0)
         vlrf_quantize_q8_0(t.data_ptr(), blocks.data(), t.numel());
     else
         vlrf_quantize_q4_0(t.data_ptr(), blocks.data(), t.numel());
     vlrf_dequantize(blocks.data(), dtype, t.data_ptr(), t.numel());
 }
 
-const char* dtype_name(int dt) { return dt == VLRF_DT_Q8_0 ? "Q8_0" : dt == VLRF_DT_Q4_0 ? "Q4_0" : "F32"; }
+const char* dtype_name(int dt) { return dt == VLRF_HIP_DT_Q8_0 ? "Q8_0" : dt == VLRF_HIP_DT_Q4_0 ? "Q4_0" : "F32"; }
 
 // A tiny Llama-style model; `wdt` is the block dtype its projection weights
-// come from (VLRF_DT_F32: plain normal f32 weights that no block holds).
+// come from (VLRF_HIP_DT_F32: plain normal f32 weights that no block holds).
 vlrf::ModelConfig tiny_config(vlrf::KVCacheDType kv_dtype) {
     vlrf::ModelConfig c;
     c.vocab_size = 512;
@@ -247,7 +247,7 @@ void fill_weights(vlrf::TransformerModel& m, vlrf::ModelConfig const& c, int wdt
         Tensor t = normal_tensor(dims, stream++, sd);
         if (offset != 0.f)
             for (int64_t i = 0; i < t.numel(); ++i) t.data_ptr()[i] += offset;
-        if (proj && wdt != VLRF_DT_F32) roundtrip(t, wdt);
+        if (proj && wdt != VLRF_HIP_DT_F32) roundtrip(t, wdt);
         m.wm.tensors[name] = t;
     };
     put("embed.weight", {c.vocab_size, c.d_model}, 1.f, false, 0.f);
@@ -294,14 +294,14 @@ void check_decode(HipBackend const& be, vlrf::KVCacheDType kv_dtype) {
     const vlrf::ModelConfig c = tiny_config(kv_dtype);
     vlrf::TransformerModel m;
     m.init(c);
-    fill_weights(m, c, VLRF_DT_Q8_0);
+    fill_weights(m, c, VLRF_HIP_DT_Q8_0);
     const std::vector<int> prompt = prompt_ids(40, c.vocab_size);
     vlrf::GenerationConfig gc;
     gc.max_new_tokens = 64;
     gc.do_sample = false;
     const auto ref = m.generate(prompt, gc);
     vlrf::HipDecoder dec(be.context(), c, m.wm);
-    report(dec.layer_dtype() == VLRF_DT_Q8_0 && dec.lm_head_dtype() == VLRF_DT_Q8_0,
+    report(dec.layer_dtype() == VLRF_HIP_DT_Q8_0 && dec.lm_head_dtype() == VLRF_HIP_DT_Q8_0,
            "decode: Q8_0-derived weights kept as Q8_0 blocks", 0.0);
     compare(std::string("64 greedy steps, KV ") + vlrf::kv_cache_dtype_name(kv_dtype), ref,
             dec.generate(prompt, gc.max_new_tokens));
@@ -327,10 +327,10 @@ void check_decode_weights(HipBackend const& be, int wdt) {
            0.0);
     compare(std::string("48 greedy steps, ") + dtype_name(wdt) + " weights", ref,
             dec.generate(prompt, gc.max_new_tokens));
-    if (wdt == VLRF_DT_F32) {
+    if (wdt == VLRF_HIP_DT_F32) {
         bool refused = false;
         try {
-            vlrf::HipDecoder forced(be.context(), c, m.wm, VLRF_DT_Q8_0);
+            vlrf::HipDecoder forced(be.context(), c, m.wm, VLRF_HIP_DT_Q8_0);
         } catch (std::runtime_error const& e) {
             refused = std::strstr(e.what(), "not exactly representable") != nullptr;
         }
@@ -349,14 +349,14 @@ void check_decode_stops(HipBackend const& be) {
     {
         vlrf::TransformerModel m;
         m.init(c);
-        fill_weights(m, c, VLRF_DT_Q8_0);
+        fill_weights(m, c, VLRF_HIP_DT_Q8_0);
         gc.max_new_tokens = 64;
         eos = m.generate(prompt, gc).token_ids[prompt.size() + 20];
     }
     c.eos_token_id = eos;
     vlrf::TransformerModel m;
     m.init(c);
-    fill_weights(m, c, VLRF_DT_Q8_0);
+    fill_weights(m, c, VLRF_HIP_DT_Q8_0);
     vlrf::HipDecoder dec(be.context(), c, m.wm);
     gc.max_new_tokens = 64;
     compare("eos_token_id " + std::to_string(eos) + " reached", m.generate(prompt, gc),
@@ -365,7 +365,7 @@ void check_decode_stops(HipBackend const& be) {
     c.eos_token_id = -1;
     vlrf::TransformerModel m2;
     m2.init(c);
-    fill_weights(m2, c, VLRF_DT_Q8_0);
+    fill_weights(m2, c, VLRF_HIP_DT_Q8_0);
     vlrf::HipDecoder dec2(be.context(), c, m2.wm);
     compare("max_new_tokens 500 > max_seq_len 160 - 40", m2.generate(prompt, gc),
             dec2.generate(prompt, gc.max_new_tokens));
@@ -399,7 +399,7 @@ void check_prefill_mfma(HipBackend const& be) {
     const vlrf::ModelConfig c = tiny_config(vlrf::KVCacheDType::Q8_0);
     vlrf::TransformerModel m;
     m.init(c);
-    fill_weights(m, c, VLRF_DT_Q8_0);
+    fill_weights(m, c, VLRF_HIP_DT_Q8_0);
     const std::vector<int> prompt = prompt_ids(100, c.vocab_size);
     m.reset_kv_cache();
     m.forward(prompt, true);
@@ -435,7 +435,7 @@ void check_read_cache(HipBackend const& be, vlrf::KVCacheDType kv_dtype) {
     const vlrf::ModelConfig c = tiny_config(kv_dtype);
     vlrf::TransformerModel m;
     m.init(c);
-    fill_weights(m, c, VLRF_DT_Q8_0);
+    fill_weights(m, c, VLRF_HIP_DT_Q8_0);
     const std::vector<int> prompt = prompt_ids(40, c.vocab_size);
     vlrf::GenerationConfig gc;
     gc.max_new_tokens = 20;
@@ -445,7 +445,7 @@ void check_read_cache(HipBackend const& be, vlrf::KVCacheDType kv_dtype) {
     Tensor want = m.forward({last}, true);            // the reference continuing from its own cache
     vlrf::TransformerModel m2;
     m2.init(c);
-    fill_weights(m2, c, VLRF_DT_Q8_0);
+    fill_weights(m2, c, VLRF_HIP_DT_Q8_0);
     vlrf::HipDecoder dec(be.context(), c, m2.wm);
     const auto got = dec.generate(prompt, gc.max_new_tokens);
     m2.reset_kv_cache();
@@ -473,7 +473,7 @@ int main(int argc, char** argv) {
     if (dev) {
         for (auto dt : {vlrf::KVCacheDType::F32, vlrf::KVCacheDType::F16, vlrf::KVCacheDType::Q8_0})
             check_decode(be, dt);
-        for (int wdt : {VLRF_DT_Q4_0, VLRF_DT_F32}) check_decode_weights(be, wdt);
+        for (int wdt : {VLRF_HIP_DT_Q4_0, VLRF_HIP_DT_F32}) check_decode_weights(be, wdt);
         check_decode_stops(be);
         check_prefill_mfma(be);
         for (auto dt : {vlrf::KVCacheDType::F32, vlrf::KVCacheDType::F16, vlrf::KVCacheDType::Q8_0})

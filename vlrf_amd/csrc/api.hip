@@ -32,29 +32,29 @@ LaunchTimer*& launch_timer() { return g_launch_timer; }
 size_t weight_device_bytes(int dtype, int N, int K) {
     const size_t n = (size_t)N * K;
     switch (dtype) {
-        case VLRF_DT_Q8_0: return n + (n / 32) * 2;
-        case VLRF_DT_Q4_0: return n / 2 + (n / 32) * 2;
+        case VLRF_HIP_DT_Q8_0: return n + (n / 32) * 2;
+        case VLRF_HIP_DT_Q4_0: return n / 2 + (n / 32) * 2;
         default: return n * 4;
     }
 }
 
 int weight_alloc(DevWeight& w, int dtype, int N, int K) {
     VH_ARG(N > 0 && K > 0, "weight: empty shape %dx%d", N, K);
-    VH_ARG(dtype == VLRF_DT_F32 || dtype == VLRF_DT_Q8_0 || dtype == VLRF_DT_Q4_0,
+    VH_ARG(dtype == VLRF_HIP_DT_F32 || dtype == VLRF_HIP_DT_Q8_0 || dtype == VLRF_HIP_DT_Q4_0,
            "weight: unsupported dtype %d", dtype);
-    VH_ARG(dtype == VLRF_DT_F32 || K % 32 == 0, "weight: K=%d not a multiple of 32", K);
+    VH_ARG(dtype == VLRF_HIP_DT_F32 || K % 32 == 0, "weight: K=%d not a multiple of 32", K);
     w.dtype = dtype;
     w.N = N;
     w.K = K;
     const size_t n = (size_t)N * K;
-    if (dtype == VLRF_DT_F32) {
+    if (dtype == VLRF_HIP_DT_F32) {
         if (hipMalloc(&w.f, n * 4) != hipSuccess) {
             set_error("weight: hipMalloc(%zu) failed", n * 4);
             return VLRF_HIP_ERR_NOMEM;
         }
         return VLRF_HIP_OK;
     }
-    const size_t qbytes = dtype == VLRF_DT_Q8_0 ? n : n / 2;
+    const size_t qbytes = dtype == VLRF_HIP_DT_Q8_0 ? n : n / 2;
     if (hipMalloc(&w.q, qbytes) != hipSuccess || hipMalloc(&w.d, (n / 32) * 2) != hipSuccess) {
         weight_release(w);
         set_error("weight: hipMalloc failed for %dx%d", N, K);
@@ -84,7 +84,7 @@ int weight_upload_rows(hipStream_t s, DevWeight& w, const void* host, int row0, 
     }
     const int K = w.K;
     const size_t nel = (size_t)nrows * K;
-    if (w.dtype == VLRF_DT_F32) {
+    if (w.dtype == VLRF_HIP_DT_F32) {
         VH_CHECK(hipMemcpyAsync(w.f + (size_t)row0 * K, host, nel * 4, hipMemcpyHostToDevice, s));
         VH_CHECK(hipStreamSynchronize(s));
         return VLRF_HIP_OK;
@@ -92,7 +92,7 @@ int weight_upload_rows(hipStream_t s, DevWeight& w, const void* host, int row0, 
     const int bpr = K / 32;                       // blocks per row
     const size_t nb = (size_t)nrows * bpr;
     const uint8_t* in = static_cast<const uint8_t*>(host);
-    const bool q8 = w.dtype == VLRF_DT_Q8_0;
+    const bool q8 = w.dtype == VLRF_HIP_DT_Q8_0;
     const size_t bsz = q8 ? 34 : 18, qpb = q8 ? 32 : 16;
     std::vector<uint8_t> q(nb * qpb);
     std::vector<uint16_t> d(nb);
@@ -221,7 +221,7 @@ int kv_rows_to_host(hipStream_t s, const KVLayer& L, int G, int D, int max_seq, 
         VH_CHECK(hipMemcpyAsync(hk.data() + (size_t)g * n * hd, L.k + off, n * hd, hipMemcpyDeviceToHost, s));
         VH_CHECK(hipMemcpyAsync(hv.data() + (size_t)g * n * hd, L.v + off, n * hd, hipMemcpyDeviceToHost, s));
     }
-    const bool q8 = L.dtype == VLRF_KV_Q8_0;
+    const bool q8 = L.dtype == VLRF_HIP_KV_Q8_0;
     if (k_s && q8) VH_CHECK(hipMemcpyAsync(k_s, L.ks + row0, n * sizeof(float), hipMemcpyDeviceToHost, s));
     if (v_s && q8) VH_CHECK(hipMemcpyAsync(v_s, L.vs + row0, n * sizeof(float), hipMemcpyDeviceToHost, s));
     VH_CHECK(hipStreamSynchronize(s));
@@ -401,7 +401,7 @@ int vlrf_hip_attn_f32(vlrf_hip_ctx_t ctx, const float* Q, const float* K, const 
         float* part = nullptr;
         int rc = ctx->scratch((size_t)n_h * splits * (d_h + 2) * sizeof(float), &part);
         if (rc) return rc;
-        return launch_attn_decode(ctx->stream, Q, K, V, nullptr, nullptr, VLRF_KV_F32, (long)ctx_len * d_h, n_h,
+        return launch_attn_decode(ctx->stream, Q, K, V, nullptr, nullptr, VLRF_HIP_KV_F32, (long)ctx_len * d_h, n_h,
                                   n_h, d_h, ctx_len, nullptr, splits, scale, part, O, nullptr, ctx->small_tile_ctr);
     }
     return launch_attn_f32_tiled(ctx->stream, Q, K, V, O, n_h, T, ctx_len, d_h, scale, causal);
@@ -413,7 +413,7 @@ int vlrf_hip_kv_create(vlrf_hip_ctx_t ctx, int n_layers, int max_seq, int n_kv_h
     VH_CTX(ctx);
     VH_ARG(out != nullptr, "kv_create: null output");
     *out = nullptr;
-    VH_ARG(dtype == VLRF_KV_Q8_0 || dtype == VLRF_KV_F16 || dtype == VLRF_KV_F32,
+    VH_ARG(dtype == VLRF_HIP_KV_Q8_0 || dtype == VLRF_HIP_KV_F16 || dtype == VLRF_HIP_KV_F32,
            "kv_create: cache dtype %d is not F32, F16 or Q8_0", dtype);
     VH_ARG(n_layers >= 1 && max_seq >= 1 && n_kv_heads >= 1 && d_head >= 2 && d_head % 16 == 0,
            "kv_create: bad shape layers=%d max_seq=%d n_kv=%d d_head=%d", n_layers, max_seq,
@@ -430,7 +430,7 @@ int vlrf_hip_kv_create(vlrf_hip_ctx_t ctx, int n_layers, int max_seq, int n_kv_h
     const size_t data = (size_t)n_kv_heads * max_seq * d_head * kv_elem_bytes(dtype);
     for (auto& L : kv->layers) {
         L.dtype = dtype;
-        const bool q8 = dtype == VLRF_KV_Q8_0;
+        const bool q8 = dtype == VLRF_HIP_KV_Q8_0;
         if (hipMalloc(&L.k, data) != hipSuccess || hipMalloc(&L.v, data) != hipSuccess ||
             (q8 && hipMalloc(&L.ks, max_seq * sizeof(float)) != hipSuccess) ||
             (q8 && hipMalloc(&L.vs, max_seq * sizeof(float)) != hipSuccess)) {

@@ -136,12 +136,12 @@ int vlrf_quantize_q4_0(const float* src, void* dst, int64_t n) {
 int vlrf_dequantize(const void* src, int dtype, float* dst, int64_t n) {
     if (!src || !dst || n < 0) return VLRF_HIP_ERR_ARG;
     const uint8_t* in = static_cast<const uint8_t*>(src);
-    if (dtype == VLRF_DT_F32) {
+    if (dtype == VLRF_HIP_DT_F32) {
         std::memcpy(dst, src, sizeof(float) * (size_t)n);
         return VLRF_HIP_OK;
     }
     if (n % 32) return VLRF_HIP_ERR_ARG;
-    if (dtype == VLRF_DT_Q8_0) {
+    if (dtype == VLRF_HIP_DT_Q8_0) {
         parallel_blocks(n / 32, [&](int64_t b0, int64_t b1) {
             for (int64_t b = b0; b < b1; ++b) {
                 uint16_t d16;
@@ -152,7 +152,7 @@ int vlrf_dequantize(const void* src, int dtype, float* dst, int64_t n) {
         });
         return VLRF_HIP_OK;
     }
-    if (dtype == VLRF_DT_Q4_0) {
+    if (dtype == VLRF_HIP_DT_Q4_0) {
         parallel_blocks(n / 32, [&](int64_t b0, int64_t b1) {
             for (int64_t b = b0; b < b1; ++b) {
                 uint16_t d16;

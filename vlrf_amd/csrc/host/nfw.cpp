@@ -265,7 +265,7 @@ static int nfw_read_f32(vlrf_nfw_t f, int i, float* dst, int64_t n) {
         for (int64_t k = 0; k < e.numel; ++k) dst[k] = half_to_float(h[k]);
         return VLRF_HIP_OK;
     }
-    return vlrf_dequantize(raw.data(), e.dtype == VLRF_NFW_Q8_0 ? VLRF_DT_Q8_0 : VLRF_DT_Q4_0, dst, e.numel);
+    return vlrf_dequantize(raw.data(), e.dtype == VLRF_NFW_Q8_0 ? VLRF_HIP_DT_Q8_0 : VLRF_HIP_DT_Q4_0, dst, e.numel);
 }
 
 int vlrf_nfw_read_f32(vlrf_nfw_t f, int i, float* dst, int64_t n) {
@@ -300,7 +300,7 @@ static int model_load_nfw(vlrf_hip_model_t m, const char* path, int* n_loaded) {
         const int rows = e.ndim >= 2 ? e.dims[0] : 1;
         const int cols = e.ndim >= 1 ? e.dims[e.ndim - 1] : 1;
         if (f32_slot || e.dtype == VLRF_NFW_F32 || e.dtype == VLRF_NFW_F16) {
-            if (!f32_slot && cfg.weight_dtype != VLRF_DT_F32 && n != "lm_head.weight") {
+            if (!f32_slot && cfg.weight_dtype != VLRF_HIP_DT_F32 && n != "lm_head.weight") {
                 set_error("load_nfw: '%s' is %s but the model's projections are block type %d "
                           "(create the model with weight_dtype F32, or store the tensor as Q8_0/Q4_0)",
                           n.c_str(), e.dtype == VLRF_NFW_F16 ? "F16" : "F32", cfg.weight_dtype);
@@ -308,7 +308,7 @@ static int model_load_nfw(vlrf_hip_model_t m, const char* path, int* n_loaded) {
             }
             std::vector<float> v((size_t)e.numel);
             if ((rc = vlrf_nfw_read_f32(f, i, v.data(), e.numel))) return rc;
-            rc = vlrf_hip_model_set_weight(m, n.c_str(), v.data(), VLRF_DT_F32, rows, cols);
+            rc = vlrf_hip_model_set_weight(m, n.c_str(), v.data(), VLRF_HIP_DT_F32, rows, cols);
         } else {
             std::vector<uint8_t> raw((size_t)e.bytes);
             if ((rc = vlrf_nfw_read(f, i, raw.data(), e.bytes))) return rc;

@@ -83,7 +83,7 @@ LaunchTimer*& launch_timer();   // the calling thread's timer (null: none)
 //       d = f16 [N][K/32].
 // F32:  f = float [N][K].
 struct DevWeight {
-    int dtype = VLRF_DT_F32;
+    int dtype = VLRF_HIP_DT_F32;
     int N = 0, K = 0;
     uint8_t* q = nullptr;
     __half* d = nullptr;
@@ -111,11 +111,11 @@ struct KVLayer {
     int8_t* v = nullptr;
     float* ks = nullptr;   // [max_seq], Q8_0 only
     float* vs = nullptr;
-    int dtype = VLRF_KV_Q8_0;
+    int dtype = VLRF_HIP_KV_Q8_0;
 };
 
 __host__ __device__ inline int kv_elem_bytes(int dtype) {
-    return dtype == VLRF_KV_F32 ? 4 : dtype == VLRF_KV_F16 ? 2 : 1;
+    return dtype == VLRF_HIP_KV_F32 ? 4 : dtype == VLRF_HIP_KV_F16 ? 2 : 1;
 }
 
 // KVCache's f32 -> f16 element conversion (kv_cache.hpp:68-97): the mantissa is
@@ -258,8 +258,8 @@ int attn_decode_chunks(int cap, int d_head, int n_kv);
 // key's, nch + 1 per head.  0 where it does not apply.
 int attn_decode_chunks128(int cap, int n_heads, int n_kv, int kv_dtype);
 
-// Split-K decode attention over K/V elements of kv_dtype (VLRF_KV_Q8_0 codes
-// with row scales ks/vs, VLRF_KV_F16 bits, VLRF_KV_F32) laid out
+// Split-K decode attention over K/V elements of kv_dtype (VLRF_HIP_KV_Q8_0 codes
+// with row scales ks/vs, VLRF_HIP_KV_F16 bits, VLRF_HIP_KV_F32) laid out
 // [n_kv][head_stride/d][d]: a cache layer (head_stride = max_seq*d) or plain
 // f32 K/V.  ctx from *ctx_dev (+1 when fused) when non-null.  part must hold
 // n_heads*n_splits*(d+2) floats.  ctr (unfused, host context length, d 64): a

@@ -43,15 +43,15 @@ constexpr float kNegInf = -INFINITY;
 
 using attn::rope2;
 
-// KVT: cache element type VLRF_KV_Q8_0 (int8 codes, f32 scale per token row),
-// VLRF_KV_F16 (the reference's f16 bits) or VLRF_KV_F32; kc/vc address the
+// KVT: cache element type VLRF_HIP_KV_Q8_0 (int8 codes, f32 scale per token row),
+// VLRF_HIP_KV_F16 (the reference's f16 bits) or VLRF_HIP_KV_F32; kc/vc address the
 // elements ([n_kv][head_stride/D][D]) as bytes.
 template <int D, int REP, int KVT, bool FUSED>
 __global__ __launch_bounds__(kAttnThreads) void attn_decode_partial_kernel(
     const float* __restrict__ q, const int8_t* kc, const int8_t* vc, const float* ks, const float* vs,
     long head_stride, int ctx_len, const int* __restrict__ ctx_dev, int n_splits, float scale,
     float* __restrict__ part, DecodeFuse fz) {
-    constexpr bool Q8 = KVT == VLRF_KV_Q8_0, H16 = KVT == VLRF_KV_F16;
+    constexpr bool Q8 = KVT == VLRF_HIP_KV_Q8_0, H16 = KVT == VLRF_HIP_KV_F16;
     constexpr int EB = Q8 ? 1 : H16 ? 2 : 4;             // bytes per cache element
     constexpr int HALF = D / 2;
     static_assert(HALF == 32 || HALF == 64, "a RoPE pair index is tid % HALF only for HALF | 64");
@@ -384,7 +384,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_partial_kernel(
 // results; the group's first head writes it), leaves the token at `pos` out
 // of the rounds (its cache row may not be written yet) and adds it to the
 // final merge as one more entry: score q.k_stored, weight 1, value the stored
-// V row.  KVT: VLRF_KV_Q8_0 codes + row scales, VLRF_KV_F16 bits, VLRF_KV_F32.
+// V row.  KVT: VLRF_HIP_KV_Q8_0 codes + row scales, VLRF_HIP_KV_F16 bits, VLRF_HIP_KV_F32.
 // Measured on the MI355X (32q/4kv Q8_0, d 64, stream launches): single pass
 // 5.8 / 7.0 / 8.6 / 11.9 us at ctx 64 / 512 / 1024 / 2048 against 6.9 / 7.7 /
 // 7.8 / 8.1 us for split-K + combine.  One workgroup's memory parallelism caps
@@ -571,7 +571,7 @@ constexpr int kPQ = 32, kPK = 64;         // queries per wave, keys per tile
 // row, K and V) held in registers between their load and the LDS store.
 template <int KVT>
 struct RawKV {
-    static constexpr int W = KVT == VLRF_KV_Q8_0 ? 1 : KVT == VLRF_KV_F16 ? 2 : 4;   // uint4 per 16 elements
+    static constexpr int W = KVT == VLRF_HIP_KV_Q8_0 ? 1 : KVT == VLRF_HIP_KV_F16 ? 2 : 4;   // uint4 per 16 elements
     uint4 k[W], v[W];
     float sk, sv;
 };
@@ -585,7 +585,7 @@ __device__ __forceinline__ void load_raw(RawKV<KVT>& r, const int8_t* kq, const 
         r.k[i] = *reinterpret_cast<const uint4*>(kq + e0 * EB + 16 * i);
         r.v[i] = *reinterpret_cast<const uint4*>(vq + e0 * EB + 16 * i);
     }
-    if constexpr (KVT == VLRF_KV_Q8_0) {
+    if constexpr (KVT == VLRF_HIP_KV_Q8_0) {
         r.sk = ks[row];
         r.sv = vs[row];
     }
@@ -594,11 +594,11 @@ __device__ __forceinline__ void load_raw(RawKV<KVT>& r, const int8_t* kq, const 
 // The 16 elements -> f32 (Q8_0 codes times the row scale, f16 widened); zero where !live.
 template <int KVT>
 __device__ __forceinline__ void raw_f32(const uint4 (&w)[RawKV<KVT>::W], float scale, bool live, float (&o)[16]) {
-    if constexpr (KVT == VLRF_KV_Q8_0) {
+    if constexpr (KVT == VLRF_HIP_KV_Q8_0) {
         const uint32_t u[4] = {w[0].x, w[0].y, w[0].z, w[0].w};
 #pragma unroll
         for (int e = 0; e < 16; ++e) o[e] = (float)(int8_t)(u[e >> 2] >> (8 * (e & 3))) * (live ? scale : 0.f);
-    } else if constexpr (KVT == VLRF_KV_F16) {
+    } else if constexpr (KVT == VLRF_HIP_KV_F16) {
         const uint32_t u[8] = {w[0].x, w[0].y, w[0].z, w[0].w, w[1].x, w[1].y, w[1].z, w[1].w};
 #pragma unroll
         for (int e = 0; e < 16; ++e) o[e] = live ? f16_bits_to_f32((u[e >> 1] >> (16 * (e & 1))) & 0xFFFFu) : 0.f;
@@ -691,8 +691,8 @@ __global__ __launch_bounds__(512) void attn_prefill_kernel(
         if (stager) {
             const bool live = kv0 + skey < kv_end;
             float kf[16], vf[16];                    // dequantize_row_q8_0 / f16_to_f32
-            raw_f32<KVT>(raw.k, KVT == VLRF_KV_Q8_0 ? raw.sk : 1.f, live, kf);
-            raw_f32<KVT>(raw.v, KVT == VLRF_KV_Q8_0 ? raw.sv : 1.f, live, vf);
+            raw_f32<KVT>(raw.k, KVT == VLRF_HIP_KV_Q8_0 ? raw.sk : 1.f, live, kf);
+            raw_f32<KVT>(raw.v, KVT == VLRF_HIP_KV_Q8_0 ? raw.sv : 1.f, live, vf);
             bf16x8 k0, k1;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
@@ -954,8 +954,8 @@ __device__ void new_row128(const float* __restrict__ q, long head_stride, int po
     const float ik = ak != 0.f ? 1.f / sk : 0.f, iv = av != 0.f ? 1.f / sv : 0.f;
     if (tid < npairs) {
         int8_t* krow = fz.kq_w + (size_t)kh * head_stride + (size_t)pos * D;
-        sm.nk[kh * D + kj] = attn::store_elem<VLRF_KV_Q8_0>(krow, kj, k0, sk, ik, ak != 0.f, true);
-        sm.nk[kh * D + kj + HALF] = attn::store_elem<VLRF_KV_Q8_0>(krow, kj + HALF, k1, sk, ik, ak != 0.f, true);
+        sm.nk[kh * D + kj] = attn::store_elem<VLRF_HIP_KV_Q8_0>(krow, kj, k0, sk, ik, ak != 0.f, true);
+        sm.nk[kh * D + kj + HALF] = attn::store_elem<VLRF_HIP_KV_Q8_0>(krow, kj + HALF, k1, sk, ik, ak != 0.f, true);
     }
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
@@ -963,7 +963,7 @@ __device__ void new_row128(const float* __restrict__ q, long head_stride, int po
         if (e < nrow) {
             const int vh = e / D, vj = e - vh * D;
             int8_t* vrow = fz.vq_w + (size_t)vh * head_stride + (size_t)pos * D;
-            sm.nv[e] = attn::store_elem<VLRF_KV_Q8_0>(vrow, vj, u ? v1 : v0, sv, iv, av != 0.f, true);
+            sm.nv[e] = attn::store_elem<VLRF_HIP_KV_Q8_0>(vrow, vj, u ? v1 : v0, sv, iv, av != 0.f, true);
         }
     }
     if (tid == 0) { fz.ks_w[pos] = sk; fz.vs_w[pos] = sv; }
@@ -1138,7 +1138,7 @@ int attn_decode_chunks(int cap, int d_head, int n_kv) {
 int attn_decode_chunks128(int cap, int n_heads, int n_kv, int kv_dtype) {
     const int n = (cap + kCH - 1) / kCH;
     const int rep = n_kv > 0 ? n_heads / n_kv : 0;
-    return kv_dtype == VLRF_KV_Q8_0 && n_kv >= 1 && n_kv <= 8 && n_heads % n_kv == 0 &&
+    return kv_dtype == VLRF_HIP_KV_Q8_0 && n_kv >= 1 && n_kv <= 8 && n_heads % n_kv == 0 &&
                    (rep == 1 || rep == 2 || rep == 4 || rep == 8) && n + 1 <= kAttnMaxChunks
                ? n : 0;
 }
@@ -1154,12 +1154,12 @@ int launch_attn_decode(hipStream_t s, const float* q, const void* kc, const void
     VH_ARG(rep == 1 || rep == 2 || rep == 4 || rep == 8, "attn_decode: GQA group %d not in {1,2,4,8}", rep);
     VH_ARG(n_splits >= 1 && n_splits <= kMaxSplits, "attn_decode: %d splits outside [1,%d]", n_splits,
            kMaxSplits);
-    VH_ARG(kv_dtype == VLRF_KV_F32 || kv_dtype == VLRF_KV_F16 || kv_dtype == VLRF_KV_Q8_0,
+    VH_ARG(kv_dtype == VLRF_HIP_KV_F32 || kv_dtype == VLRF_HIP_KV_F16 || kv_dtype == VLRF_HIP_KV_Q8_0,
            "attn_decode: cache dtype %d", kv_dtype);
     if (!ctx_dev)
         VH_ARG(ctx_len >= 1 && ctx_len <= n_splits * kChunk, "attn_decode: ctx_len %d outside [1,%d]",
                ctx_len, n_splits * kChunk);
-    VH_ARG(kc && vc && (kv_dtype != VLRF_KV_Q8_0 || (ks && vs)), "attn_decode: missing K/V operands");
+    VH_ARG(kc && vc && (kv_dtype != VLRF_HIP_KV_Q8_0 || (ks && vs)), "attn_decode: missing K/V operands");
     DecodeFuse fz{};
     if (fuse) {
         VH_ARG(ctx_dev, "attn_decode: fusion needs a device position");
@@ -1205,9 +1205,9 @@ int launch_attn_decode(hipStream_t s, const float* q, const void* kc, const void
         default: VH_CHK(KT, 8); break;   \
     }
         switch (kv_dtype) {
-            case VLRF_KV_Q8_0: VH_CHK_R(VLRF_KV_Q8_0) break;
-            case VLRF_KV_F16: VH_CHK_R(VLRF_KV_F16) break;
-            default: VH_CHK_R(VLRF_KV_F32) break;
+            case VLRF_HIP_KV_Q8_0: VH_CHK_R(VLRF_HIP_KV_Q8_0) break;
+            case VLRF_HIP_KV_F16: VH_CHK_R(VLRF_HIP_KV_F16) break;
+            default: VH_CHK_R(VLRF_HIP_KV_F32) break;
         }
 #undef VH_CHK_R
 #undef VH_CHK
@@ -1239,9 +1239,9 @@ int launch_attn_decode(hipStream_t s, const float* q, const void* kc, const void
     }
 #define VH_CC_T(C)                                             \
     switch (kv_dtype) {                                        \
-        case VLRF_KV_Q8_0: VH_CC_R(VLRF_KV_Q8_0, C) break;     \
-        case VLRF_KV_F16: VH_CC_R(VLRF_KV_F16, C) break;       \
-        default: VH_CC_R(VLRF_KV_F32, C) break;                \
+        case VLRF_HIP_KV_Q8_0: VH_CC_R(VLRF_HIP_KV_Q8_0, C) break;     \
+        case VLRF_HIP_KV_F16: VH_CC_R(VLRF_HIP_KV_F16, C) break;       \
+        default: VH_CC_R(VLRF_HIP_KV_F32, C) break;                \
     }
         switch (CHR) {
             case 64: VH_CC_T(64) break;
@@ -1268,9 +1268,9 @@ int launch_attn_decode(hipStream_t s, const float* q, const void* kc, const void
     }
 #define VH_SP_T(FU)                                                 \
     switch (kv_dtype) {                                             \
-        case VLRF_KV_Q8_0: VH_SP_R(VLRF_KV_Q8_0, FU) break;         \
-        case VLRF_KV_F16: VH_SP_R(VLRF_KV_F16, FU) break;           \
-        default: VH_SP_R(VLRF_KV_F32, FU) break;                    \
+        case VLRF_HIP_KV_Q8_0: VH_SP_R(VLRF_HIP_KV_Q8_0, FU) break;         \
+        case VLRF_HIP_KV_F16: VH_SP_R(VLRF_HIP_KV_F16, FU) break;           \
+        default: VH_SP_R(VLRF_HIP_KV_F32, FU) break;                    \
     }
         if (fuse) { VH_SP_T(true) }
         else { VH_SP_T(false) }
@@ -1293,9 +1293,9 @@ int launch_attn_decode(hipStream_t s, const float* q, const void* kc, const void
     }
 #define VH_AD_T(D, FU)                                                   \
     switch (kv_dtype) {                                                  \
-        case VLRF_KV_Q8_0: VH_AD_R(D, VLRF_KV_Q8_0, FU) break;           \
-        case VLRF_KV_F16: VH_AD_R(D, VLRF_KV_F16, FU) break;             \
-        default: VH_AD_R(D, VLRF_KV_F32, FU) break;                      \
+        case VLRF_HIP_KV_Q8_0: VH_AD_R(D, VLRF_HIP_KV_Q8_0, FU) break;           \
+        case VLRF_HIP_KV_F16: VH_AD_R(D, VLRF_HIP_KV_F16, FU) break;             \
+        default: VH_AD_R(D, VLRF_HIP_KV_F32, FU) break;                      \
     }
     if (d_head == 64) {
         if (fuse) { VH_AD_T(64, true) }
@@ -1357,9 +1357,9 @@ int launch_attn_prefill(hipStream_t s, const float* qkv, int ld, const KVLayer& 
     }
 #define VH_AP_T(D)                                                  \
     switch (L.dtype) {                                              \
-        case VLRF_KV_Q8_0: VH_AP_R(D, VLRF_KV_Q8_0) break;          \
-        case VLRF_KV_F16: VH_AP_R(D, VLRF_KV_F16) break;            \
-        default: VH_AP_R(D, VLRF_KV_F32) break;                     \
+        case VLRF_HIP_KV_Q8_0: VH_AP_R(D, VLRF_HIP_KV_Q8_0) break;          \
+        case VLRF_HIP_KV_F16: VH_AP_R(D, VLRF_HIP_KV_F16) break;            \
+        default: VH_AP_R(D, VLRF_HIP_KV_F32) break;                     \
     }
     if (d_head == 64) { VH_AP_T(64) } else { VH_AP_T(128) }
 #undef VH_AP_T

@@ -43,12 +43,12 @@ __device__ __forceinline__ void rope2(float x0, float x1, float c, float s, floa
 // Elements 4i..4i+3 of a 64-element row held as 16-byte words, as f32.
 template <int KVT>
 __device__ __forceinline__ float4 row4(const uint4* wds, int i) {
-    if constexpr (KVT == VLRF_KV_Q8_0) {
+    if constexpr (KVT == VLRF_HIP_KV_Q8_0) {
         const uint4 k = wds[i >> 2];
         const uint32_t u = (i & 3) == 0 ? k.x : (i & 3) == 1 ? k.y : (i & 3) == 2 ? k.z : k.w;
         return make_float4((float)(int8_t)u, (float)(int8_t)(u >> 8), (float)(int8_t)(u >> 16),
                            (float)(int8_t)(u >> 24));
-    } else if constexpr (KVT == VLRF_KV_F16) {
+    } else if constexpr (KVT == VLRF_HIP_KV_F16) {
         const uint4 k = wds[i >> 1];
         const uint32_t a = (i & 1) ? k.z : k.x, b = (i & 1) ? k.w : k.y;
         return make_float4(f16_bits_to_f32(a & 0xFFFFu), f16_bits_to_f32(a >> 16), f16_bits_to_f32(b & 0xFFFFu),
@@ -61,7 +61,7 @@ __device__ __forceinline__ float4 row4(const uint4* wds, int i) {
 
 template <int KVT>
 struct KV {
-    static constexpr int EB = KVT == VLRF_KV_Q8_0 ? 1 : KVT == VLRF_KV_F16 ? 2 : 4;   // bytes per element
+    static constexpr int EB = KVT == VLRF_HIP_KV_Q8_0 ? 1 : KVT == VLRF_HIP_KV_F16 ? 2 : 4;   // bytes per element
     static constexpr int KW = D * EB / 16;   // 16-byte words of a K row
     static constexpr int VW = EB;            // 16-byte words of a 16-element V piece
 };
@@ -96,8 +96,8 @@ __device__ __forceinline__ void load_round(Round<KVT>& R, const int8_t* kc, cons
 #pragma unroll
     for (int i = 0; i < KV<KVT>::KW; ++i)
         R.k[i] = gload16(kc + (hb + (size_t)t * D) * EB + 16 * i);
-    R.ks = KVT == VLRF_KV_Q8_0 ? *(gfloat*)(ks + t) : 1.f;
-    R.vs = KVT == VLRF_KV_Q8_0 ? *(gfloat*)(vs + t) : 1.f;
+    R.ks = KVT == VLRF_HIP_KV_Q8_0 ? *(gfloat*)(ks + t) : 1.f;
+    R.vs = KVT == VLRF_HIP_KV_Q8_0 ? *(gfloat*)(vs + t) : 1.f;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int tv = min(base + tg + 16 * j, cap - 1);
@@ -113,11 +113,11 @@ __device__ __forceinline__ void load_round(Round<KVT>& R, const int8_t* kc, cons
 // the value attention reads back returned.
 template <int KVT>
 __device__ __forceinline__ float store_elem(int8_t* row, int j, float x, float sc, float inv, bool nz, bool wr) {
-    if constexpr (KVT == VLRF_KV_Q8_0) {
+    if constexpr (KVT == VLRF_HIP_KV_Q8_0) {
         const int c = nz ? min(127, max(-127, (int)roundf(x * inv))) : 0;
         if (wr) row[j] = (int8_t)c;
         return (float)c * sc;
-    } else if constexpr (KVT == VLRF_KV_F16) {
+    } else if constexpr (KVT == VLRF_HIP_KV_F16) {
         const uint16_t hb16 = f32_to_f16_kv(x);
         if (wr) reinterpret_cast<uint16_t*>(row)[j] = hb16;
         return f16_bits_to_f32(hb16);
@@ -167,7 +167,7 @@ template <int KVT, bool FUSED, int NW, class Out>
 __device__ __forceinline__ void chunk(Smem<NW>& sm, const Round<KVT>& R, float q0, float q1, const NewRow& nr, bool writer,
                                       bool scale_writer, int g, int c0, int cap, size_t hb, int ctx, int pos, bool rot,
                                       bool has_new, float scale, const DecodeFuse& fz, Out&& out) {
-    constexpr bool Q8 = KVT == VLRF_KV_Q8_0;
+    constexpr bool Q8 = KVT == VLRF_HIP_KV_Q8_0;
     constexpr int EB = KV<KVT>::EB, NT = 64 * NW;
     constexpr bool V2 = NT < 512;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -363,8 +363,8 @@ struct SmemQ {
 template <int KVT, int NW, class Out>
 __device__ __forceinline__ void chunk_q(SmemQ<NW>& sm, const Round<KVT>& R, float q0, float q1, float rc, float rs,
                                         bool rot, int c0, int pos, float scale, Out&& out) {
-    static_assert(KVT == VLRF_KV_Q8_0 || KVT == VLRF_KV_F16, "Q8_0 / F16 caches");
-    constexpr bool Q8 = KVT == VLRF_KV_Q8_0;
+    static_assert(KVT == VLRF_HIP_KV_Q8_0 || KVT == VLRF_HIP_KV_F16, "Q8_0 / F16 caches");
+    constexpr bool Q8 = KVT == VLRF_HIP_KV_Q8_0;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int tg = lane >> 2, dg = lane & 3;
     if (w == 0) {

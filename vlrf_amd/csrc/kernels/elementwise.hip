@@ -88,14 +88,14 @@ __device__ void quantize_row_to_cache(const float* __restrict__ src, int8_t* __r
 // Q8_0 quantize_row_q8_0, F16 the reference's f32_to_f16 per element, F32 copy.
 __device__ void store_row_to_cache(const float* __restrict__ src, int8_t* dst, float* sc, int dtype,
                                    int p, int n_kv, int D, int max_seq, float* red) {
-    if (dtype == VLRF_KV_Q8_0) {
+    if (dtype == VLRF_HIP_KV_Q8_0) {
         quantize_row_to_cache(src, dst, sc, p, n_kv, D, max_seq, red);
         return;
     }
     for (int i = threadIdx.x; i < n_kv * D; i += 256) {
         const int h = i / D, d = i - h * D;
         const size_t o = ((size_t)h * max_seq + p) * D + d;
-        if (dtype == VLRF_KV_F16) reinterpret_cast<uint16_t*>(dst)[o] = f32_to_f16_kv(src[i]);
+        if (dtype == VLRF_HIP_KV_F16) reinterpret_cast<uint16_t*>(dst)[o] = f32_to_f16_kv(src[i]);
         else reinterpret_cast<float*>(dst)[o] = src[i];
     }
 }
@@ -236,10 +236,10 @@ __global__ __launch_bounds__(256) void kv_dequant_kernel(const int8_t* __restric
         const int h = i / D, d = i - h * D;
         const size_t src = ((size_t)h * max_seq + t) * D + d;
         float kv, vv;
-        if (dtype == VLRF_KV_Q8_0) {
+        if (dtype == VLRF_HIP_KV_Q8_0) {
             kv = (float)kq[src] * ks[t];
             vv = (float)vq[src] * vs[t];
-        } else if (dtype == VLRF_KV_F16) {
+        } else if (dtype == VLRF_HIP_KV_F16) {
             kv = f16_bits_to_f32(reinterpret_cast<const uint16_t*>(kq)[src]);
             vv = f16_bits_to_f32(reinterpret_cast<const uint16_t*>(vq)[src]);
         } else {

@@ -55,7 +55,7 @@ struct TileCfg {
 
 // Raw weight bytes of EB elements: Q8_0 one byte each, Q4_0 a nibble each.
 template <int WT, int EB>
-struct WBytes { static constexpr int DW = WT == VLRF_DT_Q8_0 ? EB / 4 : EB / 8; };
+struct WBytes { static constexpr int DW = WT == VLRF_HIP_DT_Q8_0 ? EB / 4 : EB / 8; };
 
 template <int DW>
 __device__ __forceinline__ void load_dwords(uint32_t (&o)[DW], const uint8_t* p) {
@@ -100,7 +100,7 @@ __device__ __forceinline__ void gemm_load(GemmStage<C, WT, NM>& st, const uint16
     for (int m = 0; m < NM; ++m) {
         const uint8_t* q = m ? qb : qa;
         const uint16_t* d = reinterpret_cast<const uint16_t*>(m ? db : da);
-        if constexpr (WT == VLRF_DT_Q8_0) load_dwords(st.w[m], q + (size_t)wn * K + kb);
+        if constexpr (WT == VLRF_HIP_DT_Q8_0) load_dwords(st.w[m], q + (size_t)wn * K + kb);
         else load_dwords(st.w[m], q + (size_t)wn * (K / 2) + kb / 2);
         st.s[m] = d[(size_t)wn * (K / 32) + kb / 32];
     }
@@ -120,7 +120,7 @@ __device__ __forceinline__ void gemm_store(const GemmStage<C, WT, NM>& st, uint1
     for (int m = 0; m < NM; ++m) {
         const float sc = __half2float(__ushort_as_half((unsigned short)st.s[m]));
         float v[C::EB];
-        if constexpr (WT == VLRF_DT_Q8_0) {
+        if constexpr (WT == VLRF_HIP_DT_Q8_0) {
 #pragma unroll
             for (int j = 0; j < C::EB; ++j) v[j] = (float)(int8_t)(st.w[m][j >> 2] >> (8 * (j & 3))) * sc;
         } else {
@@ -240,11 +240,11 @@ void launch_cfg(hipStream_t s, int wt, const uint16_t* a, const DevWeight& w0, c
     const dim3 grid((w0.N + C::BN - 1) / C::BN, (M + C::BM - 1) / C::BM), block(C::NT);
     const uint8_t* qb = w1 ? w1->q : nullptr;
     const __half* db = w1 ? w1->d : nullptr;
-    if (wt == VLRF_DT_Q8_0)
-        hipLaunchKernelGGL((mfma_qgemm_kernel<C, VLRF_DT_Q8_0, EPI>), grid, block, 0, s, a, w0.q, w0.d, qb, db,
+    if (wt == VLRF_HIP_DT_Q8_0)
+        hipLaunchKernelGGL((mfma_qgemm_kernel<C, VLRF_HIP_DT_Q8_0, EPI>), grid, block, 0, s, a, w0.q, w0.d, qb, db,
                            M, w0.N, w0.K, residual, out);
     else
-        hipLaunchKernelGGL((mfma_qgemm_kernel<C, VLRF_DT_Q4_0, EPI>), grid, block, 0, s, a, w0.q, w0.d, qb, db,
+        hipLaunchKernelGGL((mfma_qgemm_kernel<C, VLRF_HIP_DT_Q4_0, EPI>), grid, block, 0, s, a, w0.q, w0.d, qb, db,
                            M, w0.N, w0.K, residual, out);
 }
 
@@ -281,7 +281,7 @@ template <int BM> struct ATile {
 };
 template <int WT, int NM, int BM> struct Stage {
     static constexpr int A_IT = ATile<BM>::A_IT;
-    static constexpr int CB = WT == VLRF_DT_Q8_0 ? 64 : 32;   // code bytes of a row per K step
+    static constexpr int CB = WT == VLRF_HIP_DT_Q8_0 ? 64 : 32;   // code bytes of a row per K step
     static constexpr int W_B = NM * BN * CB;  // codes: NM*BN rows
     static constexpr int S_B = NM * BN * 4;   // two f16 block scales per row
     static constexpr int W_TI = W_B / 1024;   // 1 KB code loads per step (wave w issues w, w+8, ...)
@@ -314,7 +314,7 @@ __device__ __forceinline__ void dma4(const void* g, uint32_t base) {
 __device__ __forceinline__ int swz_a(int r) { return (r >> 1) & 7; }
 // code chunk swizzle within a row: Q8_0 rows of 4 chunks, Q4_0 rows of 2
 template <int WT> __device__ __forceinline__ int swz_w(int n) {
-    return WT == VLRF_DT_Q8_0 ? (n >> 2) & 3 : (n >> 3) & 1;
+    return WT == VLRF_HIP_DT_Q8_0 ? (n >> 2) & 3 : (n >> 3) & 1;
 }
 
 // The tile's results: accumulator v of MFMA tile i holds row 32i + 8(v/4) +
@@ -396,7 +396,7 @@ __global__ __launch_bounds__(lds_gemm::NT) void mfma_qgemm_lds_kernel(
     }
     const char* gw[S::W_IT];
     uint32_t lw[S::W_IT];
-    const size_t rowb = WT == VLRF_DT_Q8_0 ? (size_t)K : (size_t)K / 2;   // code bytes of a weight row
+    const size_t rowb = WT == VLRF_HIP_DT_Q8_0 ? (size_t)K : (size_t)K / 2;   // code bytes of a weight row
 #pragma unroll
     for (int it = 0; it < S::W_IT; ++it) {
         const int li = min(it * 8 + wave, S::W_TI - 1);   // waves past the last load: never issued
@@ -438,7 +438,7 @@ __global__ __launch_bounds__(lds_gemm::NT) void mfma_qgemm_lds_kernel(
                 const int n = m * BN + wn * WN + l32;
                 const uint32_t s2 = *reinterpret_cast<const uint32_t*>(Ss + n * 4);
                 const float sc = __half2float(__ushort_as_half((unsigned short)(p ? s2 >> 16 : s2 & 0xFFFFu)));
-                if constexpr (WT == VLRF_DT_Q8_0) {
+                if constexpr (WT == VLRF_HIP_DT_Q8_0) {
                     // Q8_0: lane half h takes code chunk 2p + h (16 codes), slice q its half q
                     const int c = 2 * p + h;
                     const uint4 u = *reinterpret_cast<const uint4*>(Ws + n * CB + 16 * (c ^ swz_w<WT>(n)));
@@ -717,7 +717,7 @@ __global__ __launch_bounds__(256) void expand_bf16_kernel(const uint8_t* __restr
     if (t >= nparts) return;
     const float sc = __half2float(d[t >> 2]);
     int e[8];
-    if constexpr (WT == VLRF_DT_Q8_0) {
+    if constexpr (WT == VLRF_HIP_DT_Q8_0) {
         const uint2 u = *reinterpret_cast<const uint2*>(q + t * 8);   // block t / 4, codes 8 (t % 4) ..
         const uint32_t w[2] = {u.x, u.y};
 #pragma unroll
@@ -742,7 +742,7 @@ void launch_lds_wt(hipStream_t s, const uint16_t* a, const DevWeight& w0, const 
                    int nn, const float* residual, void* out) {
     constexpr int TN = lds_gemm::BN * (EPI >= 4 ? 2 : 1);
     const dim3 grid((nn + TN - 1) / TN, (M + BM - 1) / BM);
-    const size_t rowb = WT == VLRF_DT_Q8_0 ? (size_t)w0.K : (size_t)w0.K / 2;
+    const size_t rowb = WT == VLRF_HIP_DT_Q8_0 ? (size_t)w0.K : (size_t)w0.K / 2;
     const uint8_t* qa = w0.q + (size_t)n0 * rowb;
     const __half* da = w0.d + (size_t)n0 * (w0.K / 32);
     const float* res = residual ? residual + n0 : nullptr;
@@ -774,8 +774,8 @@ void launch_bgemm(hipStream_t s, const uint16_t* a, const DevWeight& w0, const D
 template <int EPI, int BM>
 void launch_lds(hipStream_t s, const uint16_t* a, const DevWeight& w0, const DevWeight* w1, int M, int n0, int nn,
                 const float* residual, void* out) {
-    if (w0.dtype == VLRF_DT_Q8_0) launch_lds_wt<VLRF_DT_Q8_0, EPI, BM>(s, a, w0, w1, M, n0, nn, residual, out);
-    else launch_lds_wt<VLRF_DT_Q4_0, EPI, BM>(s, a, w0, w1, M, n0, nn, residual, out);
+    if (w0.dtype == VLRF_HIP_DT_Q8_0) launch_lds_wt<VLRF_HIP_DT_Q8_0, EPI, BM>(s, a, w0, w1, M, n0, nn, residual, out);
+    else launch_lds_wt<VLRF_HIP_DT_Q4_0, EPI, BM>(s, a, w0, w1, M, n0, nn, residual, out);
 }
 
 // Tile plan of an M > 128 GEMM on the lds ring (one workgroup per CU: the
@@ -972,7 +972,7 @@ __device__ __forceinline__ float4 ld_agent4(__amdgpu_buffer_rsrc_t rs, uint32_t 
 template <int WT>
 __device__ __forceinline__ bf16x8 codes_bf16(uint2 c) {
     bf16x8 r;
-    if constexpr (WT == VLRF_DT_Q8_0) {
+    if constexpr (WT == VLRF_HIP_DT_Q8_0) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             r[e] = (__bf16)(float)(int8_t)(c.x >> (8 * e));
@@ -991,7 +991,7 @@ __global__ __launch_bounds__(64 * NW) void qlinear_small_kernel(
     const __half* __restrict__ db, int N, int K, int M, const float* __restrict__ x,
     const float* __restrict__ norm_w, float eps, const float* __restrict__ residual, float* __restrict__ y,
     float* __restrict__ P, float* __restrict__ SS, int* __restrict__ tile_ctr) {
-    constexpr int CB = WT == VLRF_DT_Q8_0 ? 256 : 128;   // code bytes of a row per slice
+    constexpr int CB = WT == VLRF_HIP_DT_Q8_0 ? 256 : 128;   // code bytes of a row per slice
     constexpr int CS = CB + 16;                          // padded LDS row stride
     constexpr int LPR = CB / 16;                         // lanes per row in a coalesced load
     constexpr int CL = 16 * LPR / 64;                    // 16-byte code loads per lane and matrix
@@ -1004,7 +1004,7 @@ __global__ __launch_bounds__(64 * NW) void qlinear_small_kernel(
     const int g = lane >> 4, c = lane & 15;
     const int rbase = blockIdx.x * ROWS + 16 * wave;
     const int ns = K / kSmallSlice;
-    const size_t rowb = WT == VLRF_DT_Q8_0 ? (size_t)K : (size_t)K / 2;
+    const size_t rowb = WT == VLRF_HIP_DT_Q8_0 ? (size_t)K : (size_t)K / 2;
     // staging: item e = tid + 64 NW i converts row e/32, columns 8(e%32) .. +7 of the slice
     const int sk = 8 * (tid & 31);
     float ss[NI];
@@ -1089,7 +1089,7 @@ __global__ __launch_bounds__(64 * NW) void qlinear_small_kernel(
 #pragma unroll
             for (int m = 0; m < NM; ++m) {
                 uint2 code;
-                if constexpr (WT == VLRF_DT_Q8_0)
+                if constexpr (WT == VLRF_HIP_DT_Q8_0)
                     code = *reinterpret_cast<const uint2*>(&cs[m][wave][c * CS + 32 * j + 8 * g]);
                 else
                     code = make_uint2(*reinterpret_cast<const uint32_t*>(&cs[m][wave][c * CS + 16 * j + 4 * g]), 0u);
@@ -1235,7 +1235,7 @@ int lds_cus() {
 }
 
 int check_qgemm(const DevWeight& w, int M) {
-    VH_ARG(w.dtype == VLRF_DT_Q8_0 || w.dtype == VLRF_DT_Q4_0,
+    VH_ARG(w.dtype == VLRF_HIP_DT_Q8_0 || w.dtype == VLRF_HIP_DT_Q4_0,
            "qgemm: the MFMA path takes Q8_0/Q4_0 weights (dtype %d)", w.dtype);
     VH_ARG(w.q != nullptr && w.d != nullptr, "qgemm: weight not allocated");
     VH_ARG(w.K % kBK == 0, "qgemm: K=%d must be a multiple of %d", w.K, kBK);
@@ -1263,7 +1263,7 @@ int launch_rows_to_bf16(hipStream_t s, const float* x, const float* w, uint16_t*
 bool weight_expand_bf16(hipStream_t s, const DevWeight& w) {
     if (w.bf) return true;
     const char* e = getenv("VLRF_HIP_PREFILL_BF16");
-    if ((e && e[0] == '0') || !w.q || !w.d || (w.dtype != VLRF_DT_Q8_0 && w.dtype != VLRF_DT_Q4_0)) return false;
+    if ((e && e[0] == '0') || !w.q || !w.d || (w.dtype != VLRF_HIP_DT_Q8_0 && w.dtype != VLRF_HIP_DT_Q4_0)) return false;
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(s, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
         (void)hipGetLastError();
@@ -1277,8 +1277,8 @@ bool weight_expand_bf16(hipStream_t s, const DevWeight& w) {
     }
     const size_t np = nb * 4;   // quarter blocks, one per thread
     const dim3 grid((unsigned)((np + 255) / 256));
-    if (w.dtype == VLRF_DT_Q8_0) hipLaunchKernelGGL(expand_bf16_kernel<VLRF_DT_Q8_0>, grid, dim3(256), 0, s, w.q, w.d, bf, np);
-    else hipLaunchKernelGGL(expand_bf16_kernel<VLRF_DT_Q4_0>, grid, dim3(256), 0, s, w.q, w.d, bf, np);
+    if (w.dtype == VLRF_HIP_DT_Q8_0) hipLaunchKernelGGL(expand_bf16_kernel<VLRF_HIP_DT_Q8_0>, grid, dim3(256), 0, s, w.q, w.d, bf, np);
+    else hipLaunchKernelGGL(expand_bf16_kernel<VLRF_HIP_DT_Q4_0>, grid, dim3(256), 0, s, w.q, w.d, bf, np);
     if (hipGetLastError() != hipSuccess) {
         (void)hipFree(bf);
         return false;
@@ -1343,7 +1343,7 @@ int launch_qgemm_swiglu(hipStream_t s, const DevWeight& wg, const DevWeight& wu,
 }
 
 bool qlinear_small_supported(const DevWeight& w) {
-    return (w.dtype == VLRF_DT_Q8_0 || w.dtype == VLRF_DT_Q4_0) && w.q && w.d && w.K % kSmallSlice == 0;
+    return (w.dtype == VLRF_HIP_DT_Q8_0 || w.dtype == VLRF_HIP_DT_Q4_0) && w.q && w.d && w.K % kSmallSlice == 0;
 }
 
 int qlinear_small_tiles(int N) { const int rows = 16 * small_waves(); return (N + rows - 1) / rows; }
@@ -1387,8 +1387,8 @@ int launch_qlinear_small(hipStream_t s, const DevWeight& w0, const DevWeight* w1
         else if (residual) VH_SMALL(WT, 1, 1);                 \
         else VH_SMALL(WT, 1, 0);                               \
     } while (0)
-    if (w0.dtype == VLRF_DT_Q8_0) VH_SMALL_T(VLRF_DT_Q8_0);
-    else VH_SMALL_T(VLRF_DT_Q4_0);
+    if (w0.dtype == VLRF_HIP_DT_Q8_0) VH_SMALL_T(VLRF_HIP_DT_Q8_0);
+    else VH_SMALL_T(VLRF_HIP_DT_Q4_0);
 #undef VH_SMALL_T
 #undef VH_SMALL
     VH_LAUNCHED();

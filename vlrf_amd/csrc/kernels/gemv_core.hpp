@@ -34,9 +34,9 @@ struct Gemv;
 // Q8_0 codes as signed bytes (s8f); Q4_0 codes n - 8 as (n - 8) / 16 (s4f), so
 // their block scales are taken times SCALE = 16 (exact).
 template <>
-struct Gemv<VLRF_DT_Q8_0> { static constexpr int EPL = 16; static constexpr float SCALE = 1.f; };
+struct Gemv<VLRF_HIP_DT_Q8_0> { static constexpr int EPL = 16; static constexpr float SCALE = 1.f; };
 template <>
-struct Gemv<VLRF_DT_Q4_0> { static constexpr int EPL = 32; static constexpr float SCALE = 16.f; };
+struct Gemv<VLRF_HIP_DT_Q4_0> { static constexpr int EPL = 32; static constexpr float SCALE = 16.f; };
 
 constexpr float kNegInfF = -INFINITY;
 constexpr int kGemvMaxK = 6144;          // staged activations: 24 KiB of LDS
@@ -116,7 +116,7 @@ __device__ __forceinline__ void gemv_load(GemvRegs<NM, RPW, NC>& R, const uint8_
                                           int lane) {
     constexpr int EPL = Gemv<WT>::EPL;
     constexpr int CW = 64 * EPL;
-    const size_t qrow = WT == VLRF_DT_Q8_0 ? (size_t)K : (size_t)K / 2;
+    const size_t qrow = WT == VLRF_HIP_DT_Q8_0 ? (size_t)K : (size_t)K / 2;
     const int kb = K / 32;
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
@@ -168,7 +168,7 @@ __device__ __forceinline__ void gemv_compute(const GemvRegs<NM, RPW, NC>& R, con
             for (int r = 0; r < RPW; ++r) {
                 const uint32_t u[4] = {R.w[m][r][c].x, R.w[m][r][c].y, R.w[m][r][c].z, R.w[m][r][c].w};
                 float p = 0.f;
-                if constexpr (WT == VLRF_DT_Q8_0) {
+                if constexpr (WT == VLRF_HIP_DT_Q8_0) {
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
                         p += s8f<0>(u[j]) * xv[4 * j];

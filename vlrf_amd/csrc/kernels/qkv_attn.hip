@@ -71,7 +71,7 @@ template <int KVT>
 __device__ void new_row(const QkvAttnParams& P, uint32_t tag) {
     __shared__ NewRowSmem sm;
     constexpr int NT = gemv::kGemvThreads, W = gemv::kGemvWaves;
-    constexpr bool Q8 = KVT == VLRF_KV_Q8_0;
+    constexpr bool Q8 = KVT == VLRF_HIP_KV_Q8_0;
     const DecodeFuse& fz = P.fz;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int G = fz.n_kv, D = P.K, H = G * P.rep, npairs = G * attn::HALF, nrow = G * attn::D;
@@ -246,7 +246,7 @@ __global__ __launch_bounds__(gemv::kGemvThreads) __attribute__((amdgpu_waves_per
 }
 
 int qkv_chunks(int w_dtype, int K) {
-    const int cw = 64 * (w_dtype == VLRF_DT_Q8_0 ? gemv::Gemv<VLRF_DT_Q8_0>::EPL : gemv::Gemv<VLRF_DT_Q4_0>::EPL);
+    const int cw = 64 * (w_dtype == VLRF_HIP_DT_Q8_0 ? gemv::Gemv<VLRF_HIP_DT_Q8_0>::EPL : gemv::Gemv<VLRF_HIP_DT_Q4_0>::EPL);
     return (K + cw - 1) / cw;
 }
 
@@ -256,9 +256,9 @@ int qkv_chunks(int w_dtype, int K) {
 // wave for the projection (d_model <= 2048) and the chunked decode attention
 // (d_head 64, at most 8 KV heads, at most 15 chunks: 16 partials per head).
 bool qkv_attn_supported(int w_dtype, int N, int K, int nch, int n_kv) {
-    if (w_dtype != VLRF_DT_Q8_0 && w_dtype != VLRF_DT_Q4_0) return false;
+    if (w_dtype != VLRF_HIP_DT_Q8_0 && w_dtype != VLRF_HIP_DT_Q4_0) return false;
     const int nc = qkv_chunks(w_dtype, K);
-    if (nc > (w_dtype == VLRF_DT_Q8_0 ? 2 : 1) || K > kQkvAttnMaxD) return false;
+    if (nc > (w_dtype == VLRF_HIP_DT_Q8_0 ? 2 : 1) || K > kQkvAttnMaxD) return false;
     return nch > 0 && nch + 1 <= kAttnMaxChunks && n_kv >= 1 && n_kv <= 8 &&
            (N + gemv::kGemvWaves - 1) / gemv::kGemvWaves <= gemv::kGemvMaxOneGroups && N == K + 2 * n_kv * attn::D;
 }
@@ -273,7 +273,7 @@ int launch_qkv_attn(hipStream_t s, const QkvAttnParams& p, int w_dtype, int kv_d
            p.N);
     VH_ARG(!gather || p.x_copy, "qkv_attn: the gather needs the residual stream");
     // An F32 cache's rounds need more registers than this kernel keeps (it would spill).
-    VH_ARG(kv_dtype == VLRF_KV_Q8_0 || kv_dtype == VLRF_KV_F16, "qkv_attn: cache dtype %d not fused", kv_dtype);
+    VH_ARG(kv_dtype == VLRF_HIP_KV_Q8_0 || kv_dtype == VLRF_HIP_KV_F16, "qkv_attn: cache dtype %d not fused", kv_dtype);
     VH_ARG(p.na == qkv_attn_blocks(p.rep, p.fz.n_kv, p.fz.nch), "qkv_attn: %d attention workgroups", p.na);
     const dim3 grid(p.nq + p.na + 1), block(gemv::kGemvThreads);
     const int nc = qkv_chunks(w_dtype, p.K);
@@ -283,13 +283,13 @@ int launch_qkv_attn(hipStream_t s, const QkvAttnParams& p, int w_dtype, int kv_d
         else VH_LAUNCH((qkv_attn_kernel<WT, KT, NC, false>), grid, block, 0, s, p);                        \
     } while (0)
 #define VH_QA_KV(WT, NC)                                       \
-    if (kv_dtype == VLRF_KV_Q8_0) VH_QA(WT, VLRF_KV_Q8_0, NC);  \
-    else VH_QA(WT, VLRF_KV_F16, NC);
-    if (w_dtype == VLRF_DT_Q8_0) {
-        if (nc == 1) { VH_QA_KV(VLRF_DT_Q8_0, 1) }
-        else { VH_QA_KV(VLRF_DT_Q8_0, 2) }
+    if (kv_dtype == VLRF_HIP_KV_Q8_0) VH_QA(WT, VLRF_HIP_KV_Q8_0, NC);  \
+    else VH_QA(WT, VLRF_HIP_KV_F16, NC);
+    if (w_dtype == VLRF_HIP_DT_Q8_0) {
+        if (nc == 1) { VH_QA_KV(VLRF_HIP_DT_Q8_0, 1) }
+        else { VH_QA_KV(VLRF_HIP_DT_Q8_0, 2) }
     } else {
-        VH_QA_KV(VLRF_DT_Q4_0, 1)
+        VH_QA_KV(VLRF_HIP_DT_Q4_0, 1)
     }
 #undef VH_QA_KV
 #undef VH_QA

@@ -25,9 +25,9 @@ constexpr int kTile = 1024;
 constexpr int kRPW = 2;
 
 template <int WT> struct WT_;
-template <> struct WT_<VLRF_DT_Q8_0> { static constexpr int EPL = 4; };
-template <> struct WT_<VLRF_DT_Q4_0> { static constexpr int EPL = 8; };
-template <> struct WT_<VLRF_DT_F32>  { static constexpr int EPL = 4; };
+template <> struct WT_<VLRF_HIP_DT_Q8_0> { static constexpr int EPL = 4; };
+template <> struct WT_<VLRF_HIP_DT_Q4_0> { static constexpr int EPL = 8; };
+template <> struct WT_<VLRF_HIP_DT_F32>  { static constexpr int EPL = 4; };
 
 // Partial dot of the lane's EPL weights of row n starting at column c with the
 // staged activations xr (EPL floats per activation row, stride kTile).
@@ -38,12 +38,12 @@ __device__ __forceinline__ void lane_dot(const uint8_t* __restrict__ q, const __
     constexpr int EPL = WT_<WT>::EPL;
     float w[EPL];
     float scale = 1.f;
-    if constexpr (WT == VLRF_DT_Q8_0) {
+    if constexpr (WT == VLRF_HIP_DT_Q8_0) {
         const uint32_t u = *reinterpret_cast<const uint32_t*>(q + (size_t)n * K + c);
 #pragma unroll
         for (int i = 0; i < 4; ++i) w[i] = (float)(int8_t)(u >> (8 * i));
         scale = __half2float(d[(size_t)n * (K / 32) + c / 32]);
-    } else if constexpr (WT == VLRF_DT_Q4_0) {
+    } else if constexpr (WT == VLRF_HIP_DT_Q4_0) {
         const uint32_t u = *reinterpret_cast<const uint32_t*>(q + (size_t)n * (K / 2) + c / 2);
 #pragma unroll
         for (int i = 0; i < 8; ++i) w[i] = (float)((int)((u >> (4 * i)) & 0xFu) - 8);
@@ -62,7 +62,7 @@ __device__ __forceinline__ void lane_dot(const uint8_t* __restrict__ q, const __
                 const float4 xv = *reinterpret_cast<const float4*>(xm + i);
                 p += w[i] * xv.x + w[i + 1] * xv.y + w[i + 2] * xv.z + w[i + 3] * xv.w;
             }
-            if constexpr (WT == VLRF_DT_F32) acc[m] += p;
+            if constexpr (WT == VLRF_HIP_DT_F32) acc[m] += p;
             else acc[m] += scale * p;
         }
     }
@@ -292,16 +292,16 @@ int launch_gemv(hipStream_t s, const DevWeight& a, const DevWeight* b, const flo
         VH_GEMV(2, 1);
     } else if (nc <= 3) {
         VH_GEMV(3, 1);
-    } else if (WT == VLRF_DT_Q8_0 && nc == 4) {
+    } else if (WT == VLRF_HIP_DT_Q8_0 && nc == 4) {
         // K = 4096 (the 8B shape's d_model): 2 activation slots per thread.
-        if constexpr (WT == VLRF_DT_Q8_0) VH_GEMV(4, 1);
-    } else if (WT == VLRF_DT_Q8_0 && nc <= 6) {
+        if constexpr (WT == VLRF_HIP_DT_Q8_0) VH_GEMV(4, 1);
+    } else if (WT == VLRF_HIP_DT_Q8_0 && nc <= 6) {
         // Q4_0 chunks are 2048 wide, so K <= kGemvMaxK needs at most 3 of them.
-        if constexpr (WT == VLRF_DT_Q8_0) VH_GEMV(6, 1);
+        if constexpr (WT == VLRF_HIP_DT_Q8_0) VH_GEMV(6, 1);
     } else {
         // Wide rows (K <= kGemvWideMaxK): one row per wave, plain or with the
         // residual, one register set (14 / 7 chunks of 16 bytes per lane).
-        constexpr int NCW = WT == VLRF_DT_Q8_0 ? 14 : 7;
+        constexpr int NCW = WT == VLRF_HIP_DT_Q8_0 ? 14 : 7;
         VH_ARG(!SWIGLU && nc <= NCW && (xm == 16 || xm == 20), "gemv: K %d too large for the M=1 path (form %d)",
                a.K, xm);
         if constexpr (!SWIGLU) {
@@ -322,22 +322,22 @@ int launch_gemv(hipStream_t s, const DevWeight& a, const DevWeight* b, const flo
 
 // The LDS-staged GEMV covers K up to kGemvMaxK columns in every form.
 bool gemv_fits(const DevWeight& w) {
-    return (w.dtype == VLRF_DT_Q8_0 || w.dtype == VLRF_DT_Q4_0) && w.K <= kGemvMaxK;
+    return (w.dtype == VLRF_HIP_DT_Q8_0 || w.dtype == VLRF_HIP_DT_Q4_0) && w.K <= kGemvMaxK;
 }
 
 // ... and up to kGemvWideMaxK in the plain / residual forms with one row per
 // wave (N <= 8 * kGemvMaxOneGroups).
 bool gemv_wide_fits(const DevWeight& w) {
-    return (w.dtype == VLRF_DT_Q8_0 || w.dtype == VLRF_DT_Q4_0) && w.K <= gemv::kGemvWideMaxK &&
+    return (w.dtype == VLRF_HIP_DT_Q8_0 || w.dtype == VLRF_HIP_DT_Q4_0) && w.K <= gemv::kGemvWideMaxK &&
            (w.N + kGemvWaves - 1) / kGemvWaves <= kGemvMaxOneGroups;
 }
 
 int check_weight(const DevWeight& w) {
     VH_ARG(w.N > 0 && w.K > 0, "qlinear: empty weight");
-    VH_ARG(w.dtype == VLRF_DT_F32 || w.dtype == VLRF_DT_Q8_0 || w.dtype == VLRF_DT_Q4_0,
+    VH_ARG(w.dtype == VLRF_HIP_DT_F32 || w.dtype == VLRF_HIP_DT_Q8_0 || w.dtype == VLRF_HIP_DT_Q4_0,
            "qlinear: unsupported weight dtype %d", w.dtype);
     VH_ARG(w.K % 32 == 0, "qlinear: K=%d must be a multiple of 32", w.K);
-    if (w.dtype == VLRF_DT_F32) VH_ARG(w.f != nullptr, "qlinear: f32 weight not allocated");
+    if (w.dtype == VLRF_HIP_DT_F32) VH_ARG(w.f != nullptr, "qlinear: f32 weight not allocated");
     else VH_ARG(w.q != nullptr && w.d != nullptr, "qlinear: quantized weight not allocated");
     return VLRF_HIP_OK;
 }
@@ -351,13 +351,13 @@ int launch_qlinear(hipStream_t s, const DevWeight& w, const float* x, float* y, 
     VH_ARG(M >= 1 && M <= 16, "qlinear: M=%d outside [1,16]", M);
     VH_ARG(x && y, "qlinear: null activation pointer");
     if (M == 1 && (gemv_fits(w) || (!norm_w && gemv_wide_fits(w)))) {
-        if (w.dtype == VLRF_DT_Q8_0) return launch_gemv<VLRF_DT_Q8_0, false>(s, w, nullptr, x, y, norm_w, eps, residual);
-        return launch_gemv<VLRF_DT_Q4_0, false>(s, w, nullptr, x, y, norm_w, eps, residual);
+        if (w.dtype == VLRF_HIP_DT_Q8_0) return launch_gemv<VLRF_HIP_DT_Q8_0, false>(s, w, nullptr, x, y, norm_w, eps, residual);
+        return launch_gemv<VLRF_HIP_DT_Q4_0, false>(s, w, nullptr, x, y, norm_w, eps, residual);
     }
     switch (w.dtype) {
-        case VLRF_DT_Q8_0: return dispatch_m<VLRF_DT_Q8_0, false>(s, w, nullptr, x, y, M, norm_w, eps, residual);
-        case VLRF_DT_Q4_0: return dispatch_m<VLRF_DT_Q4_0, false>(s, w, nullptr, x, y, M, norm_w, eps, residual);
-        default:           return dispatch_m<VLRF_DT_F32, false>(s, w, nullptr, x, y, M, norm_w, eps, residual);
+        case VLRF_HIP_DT_Q8_0: return dispatch_m<VLRF_HIP_DT_Q8_0, false>(s, w, nullptr, x, y, M, norm_w, eps, residual);
+        case VLRF_HIP_DT_Q4_0: return dispatch_m<VLRF_HIP_DT_Q4_0, false>(s, w, nullptr, x, y, M, norm_w, eps, residual);
+        default:           return dispatch_m<VLRF_HIP_DT_F32, false>(s, w, nullptr, x, y, M, norm_w, eps, residual);
     }
 }
 
@@ -372,18 +372,18 @@ int launch_qlinear_argmax(hipStream_t s, const DevWeight& w, const float* x, flo
     VH_ARG(qlinear_argmax_supported(w) && norm_w && x && y && pairs, "qlinear_argmax: not supported");
     const int groups = (w.N + kGemvWaves - 1) / kGemvWaves;
     *npairs = groups < kGemvMaxGroups ? groups : kGemvMaxGroups;
-    if (w.dtype == VLRF_DT_Q8_0)
-        return launch_gemv<VLRF_DT_Q8_0, false>(s, w, nullptr, x, y, norm_w, eps, nullptr, nullptr, nullptr, 0, 64, pairs);
-    return launch_gemv<VLRF_DT_Q4_0, false>(s, w, nullptr, x, y, norm_w, eps, nullptr, nullptr, nullptr, 0, 64, pairs);
+    if (w.dtype == VLRF_HIP_DT_Q8_0)
+        return launch_gemv<VLRF_HIP_DT_Q8_0, false>(s, w, nullptr, x, y, norm_w, eps, nullptr, nullptr, nullptr, 0, 64, pairs);
+    return launch_gemv<VLRF_HIP_DT_Q4_0, false>(s, w, nullptr, x, y, norm_w, eps, nullptr, nullptr, nullptr, 0, 64, pairs);
 }
 
 bool qlinear_gather_supported(const DevWeight& w) { return gemv_fits(w); }
 
 int qlinear_merge_max_chunks(const DevWeight& w) {
     if (!gemv_fits(w) || w.K % 64) return 0;
-    const int cw = w.dtype == VLRF_DT_Q8_0 ? 64 * Gemv<VLRF_DT_Q8_0>::EPL : 64 * Gemv<VLRF_DT_Q4_0>::EPL;
+    const int cw = w.dtype == VLRF_HIP_DT_Q8_0 ? 64 * Gemv<VLRF_HIP_DT_Q8_0>::EPL : 64 * Gemv<VLRF_HIP_DT_Q4_0>::EPL;
     int nc = (w.K + cw - 1) / cw;
-    if (nc > 4 || (nc == 4 && w.dtype != VLRF_DT_Q8_0)) nc = 6;   // instantiated: 1, 2, 3, 4 (Q8_0), 6
+    if (nc > 4 || (nc == 4 && w.dtype != VLRF_HIP_DT_Q8_0)) nc = 6;   // instantiated: 1, 2, 3, 4 (Q8_0), 6
     const int per = (nc * cw / 4 + 64 * kGemvWaves - 1) / (64 * kGemvWaves);
     return kAttnMaxChunks / per;
 }
@@ -397,10 +397,10 @@ int launch_qlinear_merge(hipStream_t s, const DevWeight& w, const float* chunks,
     VH_ARG(nch <= qlinear_merge_max_chunks(w), "qlinear_merge: %d chunks, at most %d for K %d", nch,
            qlinear_merge_max_chunks(w), w.K);
     VH_ARG(head_dim == 64 || head_dim == 128, "qlinear_merge: head dim %d", head_dim);
-    if (w.dtype == VLRF_DT_Q8_0)
-        return launch_gemv<VLRF_DT_Q8_0, false>(s, w, nullptr, chunks, y, nullptr, 0.f, residual, nullptr, nullptr, nch,
+    if (w.dtype == VLRF_HIP_DT_Q8_0)
+        return launch_gemv<VLRF_HIP_DT_Q8_0, false>(s, w, nullptr, chunks, y, nullptr, 0.f, residual, nullptr, nullptr, nch,
                                                 head_dim);
-    return launch_gemv<VLRF_DT_Q4_0, false>(s, w, nullptr, chunks, y, nullptr, 0.f, residual, nullptr, nullptr, nch,
+    return launch_gemv<VLRF_HIP_DT_Q4_0, false>(s, w, nullptr, chunks, y, nullptr, 0.f, residual, nullptr, nullptr, nch,
                                             head_dim);
 }
 
@@ -409,9 +409,9 @@ int launch_qlinear_gather(hipStream_t s, const DevWeight& w, const float* table,
     int rc = check_weight(w);
     if (rc) return rc;
     VH_ARG(gemv_fits(w), "qlinear_gather: weight dtype %d / K %d not supported", w.dtype, w.K);
-    if (w.dtype == VLRF_DT_Q8_0)
-        return launch_gemv<VLRF_DT_Q8_0, false>(s, w, nullptr, table, y, norm_w, eps, nullptr, row, x_copy);
-    return launch_gemv<VLRF_DT_Q4_0, false>(s, w, nullptr, table, y, norm_w, eps, nullptr, row, x_copy);
+    if (w.dtype == VLRF_HIP_DT_Q8_0)
+        return launch_gemv<VLRF_HIP_DT_Q8_0, false>(s, w, nullptr, table, y, norm_w, eps, nullptr, row, x_copy);
+    return launch_gemv<VLRF_HIP_DT_Q4_0, false>(s, w, nullptr, table, y, norm_w, eps, nullptr, row, x_copy);
 }
 
 int launch_qlinear_swiglu(hipStream_t s, const DevWeight& wg, const DevWeight& wu,
@@ -424,13 +424,13 @@ int launch_qlinear_swiglu(hipStream_t s, const DevWeight& wg, const DevWeight& w
            "swiglu: gate/up shapes or dtypes differ");
     VH_ARG(M >= 1 && M <= 16, "swiglu: M=%d outside [1,16]", M);
     if (M == 1 && gemv_fits(wg)) {
-        if (wg.dtype == VLRF_DT_Q8_0) return launch_gemv<VLRF_DT_Q8_0, true>(s, wg, &wu, x, h, norm_w, eps, nullptr);
-        return launch_gemv<VLRF_DT_Q4_0, true>(s, wg, &wu, x, h, norm_w, eps, nullptr);
+        if (wg.dtype == VLRF_HIP_DT_Q8_0) return launch_gemv<VLRF_HIP_DT_Q8_0, true>(s, wg, &wu, x, h, norm_w, eps, nullptr);
+        return launch_gemv<VLRF_HIP_DT_Q4_0, true>(s, wg, &wu, x, h, norm_w, eps, nullptr);
     }
     switch (wg.dtype) {
-        case VLRF_DT_Q8_0: return dispatch_m<VLRF_DT_Q8_0, true>(s, wg, &wu, x, h, M, norm_w, eps, nullptr);
-        case VLRF_DT_Q4_0: return dispatch_m<VLRF_DT_Q4_0, true>(s, wg, &wu, x, h, M, norm_w, eps, nullptr);
-        default:           return dispatch_m<VLRF_DT_F32, true>(s, wg, &wu, x, h, M, norm_w, eps, nullptr);
+        case VLRF_HIP_DT_Q8_0: return dispatch_m<VLRF_HIP_DT_Q8_0, true>(s, wg, &wu, x, h, M, norm_w, eps, nullptr);
+        case VLRF_HIP_DT_Q4_0: return dispatch_m<VLRF_HIP_DT_Q4_0, true>(s, wg, &wu, x, h, M, norm_w, eps, nullptr);
+        default:           return dispatch_m<VLRF_HIP_DT_F32, true>(s, wg, &wu, x, h, M, norm_w, eps, nullptr);
     }
 }
 

@@ -311,9 +311,9 @@ int vlrf_hip_model_create(vlrf_hip_ctx_t ctx, const vlrf_hip_model_config* cfg, 
     VH_ARG(rep == 1 || rep == 2 || rep == 4 || rep == 8, "model: GQA group %d not in {1,2,4,8}", rep);
     VH_ARG(c.n_kv_heads * dh <= 1024, "model: kv row %d exceeds 1024", c.n_kv_heads * dh);
     VH_ARG(c.d_model % 32 == 0 && c.d_ff % 32 == 0, "model: d_model and d_ff must be multiples of 32");
-    VH_ARG(c.weight_dtype == VLRF_DT_Q8_0 || c.weight_dtype == VLRF_DT_Q4_0 || c.weight_dtype == VLRF_DT_F32,
+    VH_ARG(c.weight_dtype == VLRF_HIP_DT_Q8_0 || c.weight_dtype == VLRF_HIP_DT_Q4_0 || c.weight_dtype == VLRF_HIP_DT_F32,
            "model: unsupported weight dtype %d", c.weight_dtype);
-    VH_ARG(c.kv_dtype == VLRF_KV_F32 || c.kv_dtype == VLRF_KV_F16 || c.kv_dtype == VLRF_KV_Q8_0,
+    VH_ARG(c.kv_dtype == VLRF_HIP_KV_F32 || c.kv_dtype == VLRF_HIP_KV_F16 || c.kv_dtype == VLRF_HIP_KV_Q8_0,
            "model: unsupported KV cache dtype %d", c.kv_dtype);
 
     auto* m = new (std::nothrow) vlrf_hip_model();
@@ -344,7 +344,7 @@ int vlrf_hip_model_create(vlrf_hip_ctx_t ctx, const vlrf_hip_model_config* cfg, 
     dalloc((void**)&m->argpairs, 512 * sizeof(float2));
     dalloc((void**)&m->part, (size_t)m->H * m->n_splits * (dh + 2) * 4);
     // Chunked decode attention when the O projection's GEMV can merge it.
-    m->nch = c.weight_dtype == VLRF_DT_Q8_0 || c.weight_dtype == VLRF_DT_Q4_0
+    m->nch = c.weight_dtype == VLRF_HIP_DT_Q8_0 || c.weight_dtype == VLRF_HIP_DT_Q4_0
                  ? attn_decode_chunks(m->S, dh, m->G) : 0;
     DevWeight wo_shape;
     wo_shape.dtype = c.weight_dtype;
@@ -356,7 +356,7 @@ int vlrf_hip_model_create(vlrf_hip_ctx_t ctx, const vlrf_hip_model_config* cfg, 
     // Q8_0/F16 caches (an F32 cache's rounds need more registers than the
     // fused kernel keeps: it would spill).
     const char* qa_env = std::getenv("VLRF_HIP_QKV_ATTN");
-    if (!(qa_env && std::strcmp(qa_env, "0") == 0) && c.kv_dtype != VLRF_KV_F32 && dh == 64 && m->G <= 8 &&
+    if (!(qa_env && std::strcmp(qa_env, "0") == 0) && c.kv_dtype != VLRF_HIP_KV_F32 && dh == 64 && m->G <= 8 &&
         wo_shape.K == m->D) {
         const int n = (m->S + kAttnChunkRows - 1) / kAttnChunkRows;
         if (n + 1 <= qlinear_merge_max_chunks(wo_shape) &&
@@ -367,7 +367,7 @@ int vlrf_hip_model_create(vlrf_hip_ctx_t ctx, const vlrf_hip_model_config* cfg, 
     }
     // d_head 128 (the 8B shape): the chunked form with the new key as its own
     // partial, where the O projection's GEMV can merge nch + 1 partials.
-    if (dh == 128 && (c.weight_dtype == VLRF_DT_Q8_0 || c.weight_dtype == VLRF_DT_Q4_0) && wo_shape.K == m->D) {
+    if (dh == 128 && (c.weight_dtype == VLRF_HIP_DT_Q8_0 || c.weight_dtype == VLRF_HIP_DT_Q4_0) && wo_shape.K == m->D) {
         const int n = attn_decode_chunks128(m->S, m->H, m->G, c.kv_dtype);
         if (n && n + 1 <= qlinear_merge_max_chunks(wo_shape)) {
             m->nch = n;
@@ -415,7 +415,7 @@ int vlrf_hip_model_create(vlrf_hip_ctx_t ctx, const vlrf_hip_model_config* cfg, 
         Ly.kv.dtype = c.kv_dtype;
         dalloc((void**)&Ly.kv.k, kvdata);
         dalloc((void**)&Ly.kv.v, kvdata);
-        if (c.kv_dtype == VLRF_KV_Q8_0) {
+        if (c.kv_dtype == VLRF_HIP_KV_Q8_0) {
             dalloc((void**)&Ly.kv.ks, (size_t)m->S * 4);
             dalloc((void**)&Ly.kv.vs, (size_t)m->S * 4);
         }
@@ -489,13 +489,13 @@ int vlrf_hip_model_set_weight(vlrf_hip_model_t m, const char* name, const void* 
     };
     int rc;
     if (n == "embed.weight") {
-        if ((rc = need(VLRF_DT_F32, m->V, m->D))) return rc;
+        if ((rc = need(VLRF_HIP_DT_F32, m->V, m->D))) return rc;
         if ((rc = upload_f32(s, m->embed, host, (size_t)m->V * m->D))) return rc;
         m->embed_set = true;
         return VLRF_HIP_OK;
     }
     if (n == "ln_final.weight") {
-        if ((rc = need(VLRF_DT_F32, 1, m->D))) return rc;
+        if ((rc = need(VLRF_HIP_DT_F32, 1, m->D))) return rc;
         if ((rc = upload_f32(s, m->ln_final, host, m->D))) return rc;
         m->ln_final_set = true;
         return VLRF_HIP_OK;
@@ -520,7 +520,7 @@ int vlrf_hip_model_set_weight(vlrf_hip_model_t m, const char* name, const void* 
     Layer& Ly = m->layers[l];
     const int wdt = m->cfg.weight_dtype;
     if (rest == "ln1.weight" || rest == "ln2.weight") {
-        if ((rc = need(VLRF_DT_F32, 1, m->D))) return rc;
+        if ((rc = need(VLRF_HIP_DT_F32, 1, m->D))) return rc;
         const bool one = rest == "ln1.weight";
         if ((rc = upload_f32(s, one ? Ly.ln1 : Ly.ln2, host, m->D))) return rc;
         Ly.set |= 1u << (one ? kLn1 : kLn2);
@@ -681,7 +681,7 @@ int check_prefill(vlrf_hip_model* m, int T) {
     int rc = check_ready(m);
     if (rc) return rc;
     VH_ARG(T >= 1, "prefill: no rows");
-    VH_ARG(m->cfg.weight_dtype == VLRF_DT_Q8_0 || m->cfg.weight_dtype == VLRF_DT_Q4_0,
+    VH_ARG(m->cfg.weight_dtype == VLRF_HIP_DT_Q8_0 || m->cfg.weight_dtype == VLRF_HIP_DT_Q4_0,
            "prefill_mfma: needs Q8_0/Q4_0 weights (dtype %d)", m->cfg.weight_dtype);
     VH_ARG(m->D % 64 == 0 && m->F % 64 == 0, "prefill_mfma: d_model %d / d_ff %d not multiples of 64",
            m->D, m->F);
@@ -863,7 +863,7 @@ int vlrf_hip_model_step_bytes(vlrf_hip_model_t m, int ctx_len, double out[3]) {
             w += (double)weight_device_bytes(dw->dtype, dw->N, dw->K);
     w += (double)weight_device_bytes(m->lm_head.dtype, m->V, m->D);
     // K and V elements of the context (plus one f32 scale per row for Q8_0), per layer.
-    const bool q8 = m->cfg.kv_dtype == VLRF_KV_Q8_0;
+    const bool q8 = m->cfg.kv_dtype == VLRF_HIP_KV_Q8_0;
     const double kv = (double)m->L * (2.0 * ctx_len * m->dkv * kv_elem_bytes(m->cfg.kv_dtype) +
                                       (q8 ? 2.0 * ctx_len * 4.0 : 0.0));
     // Norm weights (2 per layer + final) and the embedding row.

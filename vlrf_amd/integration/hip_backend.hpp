@@ -166,7 +166,7 @@ private:
         if (it != wcache_.end()) {
             w = it->second.w;
         } else {
-            if (vlrf_hip_weight_upload(ctx_, B.data_ptr(), VLRF_DT_F32, N, K, &w) != VLRF_HIP_OK)
+            if (vlrf_hip_weight_upload(ctx_, B.data_ptr(), VLRF_HIP_DT_F32, N, K, &w) != VLRF_HIP_OK)
                 return false;
             wcache_.emplace(key, Cached{w, B.storage, N, K});
         }

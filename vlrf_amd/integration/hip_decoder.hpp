@@ -48,7 +48,7 @@ class HipDecoder {
 public:
     // weight_dtype kAuto: per the weights (the smallest of Q4_0, Q8_0 whose
     // blocks hold every layer projection exactly, else F32; the LM head is
-    // chosen on its own).  VLRF_DT_Q8_0 / VLRF_DT_Q4_0 / VLRF_DT_F32 force a
+    // chosen on its own).  VLRF_HIP_DT_Q8_0 / VLRF_HIP_DT_Q4_0 / VLRF_HIP_DT_F32 force a
     // dtype; a block dtype that would change a tensor is refused (naming it)
     // unless allow_lossy.
     static constexpr int kAuto = -1;
@@ -64,8 +64,8 @@ public:
              c.kv_cache_dtype != static_cast<int>(KVCacheDType::F16) &&
              c.kv_cache_dtype != static_cast<int>(KVCacheDType::Q8_0)))
             throw std::runtime_error("HipDecoder: unsupported model family");
-        if (weight_dtype != kAuto && weight_dtype != VLRF_DT_F32 && weight_dtype != VLRF_DT_Q8_0 &&
-            weight_dtype != VLRF_DT_Q4_0)
+        if (weight_dtype != kAuto && weight_dtype != VLRF_HIP_DT_F32 && weight_dtype != VLRF_HIP_DT_Q8_0 &&
+            weight_dtype != VLRF_HIP_DT_Q4_0)
             throw std::runtime_error("HipDecoder: weight dtype " + std::to_string(weight_dtype) + " unsupported");
         std::vector<std::string> proj;
         for (int l = 0; l < c.n_layers; ++l) {
@@ -97,9 +97,9 @@ public:
         mc.norm_eps = c.layer_norm_eps;
         mc.rope_theta = c.rope_theta;
         mc.weight_dtype = layer_dtype_;
-        mc.kv_dtype = c.kv_cache_dtype;          // KVCacheDType values are the ABI's VLRF_KV_*
+        mc.kv_dtype = c.kv_cache_dtype;          // KVCacheDType values are the ABI's VLRF_HIP_KV_*
         check(vlrf_hip_model_create(ctx_, &mc, &m_));
-        mfma_ok_ = (layer_dtype_ == VLRF_DT_Q8_0 || layer_dtype_ == VLRF_DT_Q4_0) && c.d_model % 64 == 0 &&
+        mfma_ok_ = (layer_dtype_ == VLRF_HIP_DT_Q8_0 || layer_dtype_ == VLRF_HIP_DT_Q4_0) && c.d_model % 64 == 0 &&
                    c.d_ff % 64 == 0;
         if (const char* e = std::getenv("VLRF_HIP_PREFILL_MFMA")) set_prefill_mfma(std::atoi(e));
         try {
@@ -107,13 +107,13 @@ public:
                 Tensor& t = wm.get(key);
                 const int rows = t.ndim() == 2 ? t.dim(0) : 1;
                 const int cols = t.ndim() == 2 ? t.dim(1) : t.dim(0);
-                check(vlrf_hip_model_set_weight(m_, name.c_str(), t.data_ptr(), VLRF_DT_F32, rows, cols));
+                check(vlrf_hip_model_set_weight(m_, name.c_str(), t.data_ptr(), VLRF_HIP_DT_F32, rows, cols));
             };
             auto put_proj = [&](const std::string& name, const std::string& key, int dt) {
                 Tensor& t = wm.get(key);
                 const int rows = t.dim(0), cols = t.dim(1);
-                if (dt == VLRF_DT_F32) {
-                    check(vlrf_hip_model_set_weight(m_, name.c_str(), t.data_ptr(), VLRF_DT_F32, rows, cols));
+                if (dt == VLRF_HIP_DT_F32) {
+                    check(vlrf_hip_model_set_weight(m_, name.c_str(), t.data_ptr(), VLRF_HIP_DT_F32, rows, cols));
                     return;
                 }
                 std::vector<unsigned char> blocks;
@@ -247,12 +247,12 @@ private:
             if (v[i] != 0.f) return false;
         return true;
     }
-    static size_t block_bytes(int dt) { return dt == VLRF_DT_Q8_0 ? 34 : 18; }
+    static size_t block_bytes(int dt) { return dt == VLRF_HIP_DT_Q8_0 ? 34 : 18; }
     static void encode(Tensor& t, int dt, std::vector<unsigned char>& blocks) {
         if (t.numel() % 32 != 0)
             throw std::runtime_error("HipDecoder: a block dtype needs 32 | numel");
         blocks.resize((size_t)t.numel() / 32 * block_bytes(dt));
-        check(dt == VLRF_DT_Q8_0 ? vlrf_quantize_q8_0(t.data_ptr(), blocks.data(), t.numel())
+        check(dt == VLRF_HIP_DT_Q8_0 ? vlrf_quantize_q8_0(t.data_ptr(), blocks.data(), t.numel())
                                  : vlrf_quantize_q4_0(t.data_ptr(), blocks.data(), t.numel()));
     }
     // Whether dtype dt's blocks reproduce the tensor bit for bit.
@@ -265,29 +265,29 @@ private:
         return std::memcmp(back.data(), t.data_ptr(), sizeof(float) * back.size()) == 0;
     }
     static int pick_dtype(WeightMap& wm, std::vector<std::string> const& keys, int want, bool allow_lossy) {
-        if (want == VLRF_DT_F32) return VLRF_DT_F32;
+        if (want == VLRF_HIP_DT_F32) return VLRF_HIP_DT_F32;
         if (want != kAuto) {
             if (!allow_lossy)
                 for (auto const& k : keys)
                     if (!exact(wm.get(k), want))
                         throw std::runtime_error("HipDecoder: " + k + " is not exactly representable in " +
-                                                 (want == VLRF_DT_Q8_0 ? "Q8_0" : "Q4_0") +
-                                                 " blocks; pass VLRF_DT_F32 or kAuto, or allow_lossy");
+                                                 (want == VLRF_HIP_DT_Q8_0 ? "Q8_0" : "Q4_0") +
+                                                 " blocks; pass VLRF_HIP_DT_F32 or kAuto, or allow_lossy");
             return want;
         }
-        for (int dt : {VLRF_DT_Q4_0, VLRF_DT_Q8_0}) {
+        for (int dt : {VLRF_HIP_DT_Q4_0, VLRF_HIP_DT_Q8_0}) {
             bool all = true;
             for (auto const& k : keys)
                 if (!(all = exact(wm.get(k), dt))) break;
             if (all) return dt;
         }
-        return VLRF_DT_F32;
+        return VLRF_HIP_DT_F32;
     }
     vlrf_hip_ctx_t ctx_;
     vlrf_hip_model_t m_ = nullptr;
     int vocab_;
     int max_seq_, eos_, bos_, kv_dtype_;
-    int layer_dtype_ = VLRF_DT_F32, lm_dtype_ = VLRF_DT_F32;
+    int layer_dtype_ = VLRF_HIP_DT_F32, lm_dtype_ = VLRF_HIP_DT_F32;
     bool mfma_ok_ = false;
     int prefill_mfma_min_ = 0;
 };
