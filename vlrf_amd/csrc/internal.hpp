@@ -23,7 +23,7 @@ void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
     do {                                                                          \
         hipError_t e_ = (expr);                                                   \
         if (e_ != hipSuccess) {                                                   \
-            ::vlrf_hip::set_error("%s failed: %s (%s:%d)", #expr,                \
+            ::vlrf_hip::set_error("%s failed: %s (%s:%d)", #expr,                 \
                                   hipGetErrorString(e_), __FILE__, __LINE__);     \
             return VLRF_HIP_ERR_RUNTIME;                                          \
         }                                                                         \
@@ -42,7 +42,7 @@ void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
     do {                                                                          \
         hipError_t e_ = hipGetLastError();                                        \
         if (e_ != hipSuccess) {                                                   \
-            ::vlrf_hip::set_error("kernel launch failed: %s (%s:%d)",            \
+            ::vlrf_hip::set_error("kernel launch failed: %s (%s:%d)",             \
                                   hipGetErrorString(e_), __FILE__, __LINE__);     \
             return VLRF_HIP_ERR_RUNTIME;                                          \
         }                                                                         \
@@ -62,17 +62,17 @@ struct LaunchTimer {
 };
 LaunchTimer*& launch_timer();   // the calling thread's timer (null: none)
 
-#define VH_LAUNCH(K, GRID, BLOCK, SHM, S, ...)                                                   \
-    do {                                                                                           \
-        ::vlrf_hip::LaunchTimer* lt_ = ::vlrf_hip::launch_timer();                                \
-        if (lt_ && lt_->n < lt_->cap) {                                                            \
-            lt_->kind[lt_->n] = lt_->cur_kind;                                                     \
+#define VH_LAUNCH(K, GRID, BLOCK, SHM, S, ...)                                                      \
+    do {                                                                                            \
+        ::vlrf_hip::LaunchTimer* lt_ = ::vlrf_hip::launch_timer();                                  \
+        if (lt_ && lt_->n < lt_->cap) {                                                             \
+            lt_->kind[lt_->n] = lt_->cur_kind;                                                      \
             hipExtLaunchKernelGGL(K, GRID, BLOCK, SHM, S, lt_->start[lt_->n], lt_->stop[lt_->n], 0, \
-                                  __VA_ARGS__);                                                    \
-            ++lt_->n;                                                                              \
-        } else {                                                                                   \
-            hipLaunchKernelGGL(K, GRID, BLOCK, SHM, S, __VA_ARGS__);                               \
-        }                                                                                          \
+                                  __VA_ARGS__);                                                     \
+            ++lt_->n;                                                                               \
+        } else {                                                                                    \
+            hipLaunchKernelGGL(K, GRID, BLOCK, SHM, S, __VA_ARGS__);                                \
+        }                                                                                           \
     } while (0)
 
 // ---- device-resident quantized weight ---------------------------------------

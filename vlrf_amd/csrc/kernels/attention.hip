@@ -1176,7 +1176,7 @@ int launch_attn_decode(hipStream_t s, const float* q, const void* kc, const void
         const int na = 8 * rep * ((n_kv * fz.nch + 7) / 8);
         const dim3 cgrid(na + 1);
 #define VH_C128(R)                                                                                              \
-    VH_LAUNCH((attn_chunk128_kernel<R>), cgrid, dim3(kCH), 0, s, q, k8, v8, ks, vs, head_stride, ctx_dev, \
+    VH_LAUNCH((attn_chunk128_kernel<R>), cgrid, dim3(kCH), 0, s, q, k8, v8, ks, vs, head_stride, ctx_dev,       \
                        scale, fz, fz.nch, na)
         switch (rep) {
             case 1: VH_C128(1); break;
@@ -1195,7 +1195,7 @@ int launch_attn_decode(hipStream_t s, const float* q, const void* kc, const void
                "attn_decode: chunked form for %d chunks does not apply", fz.nch);
         const dim3 cgrid(8 * rep * ((n_kv * fz.nch + 7) / 8));
 #define VH_CHK(KT, R)                                                                                         \
-    VH_LAUNCH((attn_decode_single_kernel<KT, R, true, kCH>), cgrid, dim3(kCH), 0, s, q, k8, v8, ks, vs, \
+    VH_LAUNCH((attn_decode_single_kernel<KT, R, true, kCH>), cgrid, dim3(kCH), 0, s, q, k8, v8, ks, vs,       \
                        head_stride, ctx_len, ctx_dev, scale, fz.chunks, fz, fz.nch)
 #define VH_CHK_R(KT)                     \
     switch (rep) {                       \
@@ -1228,7 +1228,7 @@ int launch_attn_decode(hipStream_t s, const float* q, const void* kc, const void
         const int nch = (ctx_len + CHR - 1) / CHR;
         const dim3 cgrid(8 * rep * ((n_kv * nch + 7) / 8));
 #define VH_CC(KT, R, C)                                                                                        \
-    VH_LAUNCH((attn_decode_chunks_kernel<KT, R, C>), cgrid, dim3(C), 0, s, q, k8, v8, ks, vs, head_stride, \
+    VH_LAUNCH((attn_decode_chunks_kernel<KT, R, C>), cgrid, dim3(C), 0, s, q, k8, v8, ks, vs, head_stride,     \
               ctx_len, scale, out, part, ctr, n_kv, nch)
 #define VH_CC_R(KT, C)                      \
     switch (rep) {                          \
@@ -1237,10 +1237,10 @@ int launch_attn_decode(hipStream_t s, const float* q, const void* kc, const void
         case 4: VH_CC(KT, 4, C); break;     \
         default: VH_CC(KT, 8, C); break;    \
     }
-#define VH_CC_T(C)                                             \
-    switch (kv_dtype) {                                        \
-        case VLRF_HIP_KV_Q8_0: VH_CC_R(VLRF_HIP_KV_Q8_0, C) break;     \
-        case VLRF_HIP_KV_F16: VH_CC_R(VLRF_HIP_KV_F16, C) break;       \
+#define VH_CC_T(C)                                                 \
+    switch (kv_dtype) {                                            \
+        case VLRF_HIP_KV_Q8_0: VH_CC_R(VLRF_HIP_KV_Q8_0, C) break; \
+        case VLRF_HIP_KV_F16: VH_CC_R(VLRF_HIP_KV_F16, C) break;   \
         default: VH_CC_R(VLRF_HIP_KV_F32, C) break;                \
     }
         switch (CHR) {
@@ -1257,7 +1257,7 @@ int launch_attn_decode(hipStream_t s, const float* q, const void* kc, const void
     }
     if (d_head == 64 && head_stride / d_head <= kSPMaxCtx && (!fuse || n_kv <= 8)) {
 #define VH_SP(KT, R, FU)                                                                                     \
-    VH_LAUNCH((attn_decode_single_kernel<KT, R, FU>), dim3(n_heads), dim3(64 * kSPWaves), 0, s, q, k8, \
+    VH_LAUNCH((attn_decode_single_kernel<KT, R, FU>), dim3(n_heads), dim3(64 * kSPWaves), 0, s, q, k8,       \
                        v8, ks, vs, head_stride, ctx_len, ctx_dev, scale, out, fz, 0)
 #define VH_SP_R(KT, FU)                       \
     switch (rep) {                            \
@@ -1268,9 +1268,9 @@ int launch_attn_decode(hipStream_t s, const float* q, const void* kc, const void
     }
 #define VH_SP_T(FU)                                                 \
     switch (kv_dtype) {                                             \
-        case VLRF_HIP_KV_Q8_0: VH_SP_R(VLRF_HIP_KV_Q8_0, FU) break;         \
-        case VLRF_HIP_KV_F16: VH_SP_R(VLRF_HIP_KV_F16, FU) break;           \
-        default: VH_SP_R(VLRF_HIP_KV_F32, FU) break;                    \
+        case VLRF_HIP_KV_Q8_0: VH_SP_R(VLRF_HIP_KV_Q8_0, FU) break; \
+        case VLRF_HIP_KV_F16: VH_SP_R(VLRF_HIP_KV_F16, FU) break;   \
+        default: VH_SP_R(VLRF_HIP_KV_F32, FU) break;                \
     }
         if (fuse) { VH_SP_T(true) }
         else { VH_SP_T(false) }
@@ -1282,7 +1282,7 @@ int launch_attn_decode(hipStream_t s, const float* q, const void* kc, const void
     }
     dim3 grid(n_splits, n_kv), block(kAttnThreads);
 #define VH_AD(D, R, T, FU)                                                                          \
-    VH_LAUNCH((attn_decode_partial_kernel<D, R, T, FU>), grid, block, 0, s, q, k8, v8, ks,  \
+    VH_LAUNCH((attn_decode_partial_kernel<D, R, T, FU>), grid, block, 0, s, q, k8, v8, ks,          \
                        vs, head_stride, ctx_len, ctx_dev, n_splits, scale, part, fz)
 #define VH_AD_R(D, T, FU)                       \
     switch (rep) {                              \
@@ -1293,9 +1293,9 @@ int launch_attn_decode(hipStream_t s, const float* q, const void* kc, const void
     }
 #define VH_AD_T(D, FU)                                                   \
     switch (kv_dtype) {                                                  \
-        case VLRF_HIP_KV_Q8_0: VH_AD_R(D, VLRF_HIP_KV_Q8_0, FU) break;           \
-        case VLRF_HIP_KV_F16: VH_AD_R(D, VLRF_HIP_KV_F16, FU) break;             \
-        default: VH_AD_R(D, VLRF_HIP_KV_F32, FU) break;                      \
+        case VLRF_HIP_KV_Q8_0: VH_AD_R(D, VLRF_HIP_KV_Q8_0, FU) break;   \
+        case VLRF_HIP_KV_F16: VH_AD_R(D, VLRF_HIP_KV_F16, FU) break;     \
+        default: VH_AD_R(D, VLRF_HIP_KV_F32, FU) break;                  \
     }
     if (d_head == 64) {
         if (fuse) { VH_AD_T(64, true) }
@@ -1345,7 +1345,7 @@ int launch_attn_prefill(hipStream_t s, const float* qkv, int ld, const KVLayer& 
     VH_ARG(ld % 4 == 0, "attn_prefill: row stride %d not a multiple of 4", ld);
     const int nqb = 8 / rep;                        // query blocks of 32 per workgroup (8 waves)
     dim3 grid(((T + kPQ - 1) / kPQ + nqb - 1) / nqb, n_kv);
-#define VH_AP(D, R, KT)                                                                               \
+#define VH_AP(D, R, KT)                                                                                 \
     hipLaunchKernelGGL((attn_prefill_kernel<D, R, KT>), grid, dim3(512), 0, s, qkv, ld, L.k, L.v, L.ks, \
                        L.vs, (long)max_seq * d_head, T, pos0, scale, n_heads, out)
 #define VH_AP_R(D, KT)                      \
@@ -1357,9 +1357,9 @@ int launch_attn_prefill(hipStream_t s, const float* qkv, int ld, const KVLayer& 
     }
 #define VH_AP_T(D)                                                  \
     switch (L.dtype) {                                              \
-        case VLRF_HIP_KV_Q8_0: VH_AP_R(D, VLRF_HIP_KV_Q8_0) break;          \
-        case VLRF_HIP_KV_F16: VH_AP_R(D, VLRF_HIP_KV_F16) break;            \
-        default: VH_AP_R(D, VLRF_HIP_KV_F32) break;                     \
+        case VLRF_HIP_KV_Q8_0: VH_AP_R(D, VLRF_HIP_KV_Q8_0) break;  \
+        case VLRF_HIP_KV_F16: VH_AP_R(D, VLRF_HIP_KV_F16) break;    \
+        default: VH_AP_R(D, VLRF_HIP_KV_F32) break;                 \
     }
     if (d_head == 64) { VH_AP_T(64) } else { VH_AP_T(128) }
 #undef VH_AP_T

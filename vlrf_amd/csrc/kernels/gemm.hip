@@ -483,7 +483,7 @@ __global__ __launch_bounds__(lds_gemm::NT) void mfma_qgemm_lds_kernel(
     if (nk > 1) load(1, 1);
     // Unrolled by the ring size so each step names its buffers statically.
     for (int kt = 0; kt < nk; kt += 3) {
-#define VH_LDS_STEP(KT, AS, WS, SS, NEXT)                                                     \
+#define VH_LDS_STEP(KT, AS, WS, SS, NEXT)                                                  \
         if (KT < nk) {                                                                     \
             if (KT + 1 < nk) __builtin_amdgcn_s_waitcnt(S::WAIT);                          \
             else __builtin_amdgcn_s_waitcnt(0);                                            \
@@ -1372,14 +1372,14 @@ int launch_qlinear_small(hipStream_t s, const DevWeight& w0, const DevWeight* w1
     const dim3 grid(qlinear_small_tiles(N), S);
     const uint8_t* qb = w1 ? w1->q : nullptr;
     const __half* db = w1 ? w1->d : nullptr;
-#define VH_SMALL(WT, NMV, EPIV)                                                                             \
-    do {                                                                                                    \
-        if (NW == 8)                                                                                        \
+#define VH_SMALL(WT, NMV, EPIV)                                                                                 \
+    do {                                                                                                        \
+        if (NW == 8)                                                                                            \
             hipLaunchKernelGGL((qlinear_small_kernel<WT, NMV, EPIV, 8>), grid, dim3(512), 0, s, w0.q, w0.d, qb, \
-                               db, N, K, M, x, norm_w, eps, residual, y, P, SS, tile_ctr);                  \
-        else                                                                                                \
+                               db, N, K, M, x, norm_w, eps, residual, y, P, SS, tile_ctr);                      \
+        else                                                                                                    \
             hipLaunchKernelGGL((qlinear_small_kernel<WT, NMV, EPIV, 4>), grid, dim3(256), 0, s, w0.q, w0.d, qb, \
-                               db, N, K, M, x, norm_w, eps, residual, y, P, SS, tile_ctr);                  \
+                               db, N, K, M, x, norm_w, eps, residual, y, P, SS, tile_ctr);                      \
     } while (0)
 #define VH_SMALL_T(WT)                                         \
     do {                                                       \

@@ -282,8 +282,8 @@ int launch_qkv_attn(hipStream_t s, const QkvAttnParams& p, int w_dtype, int kv_d
         if (gather) VH_LAUNCH((qkv_attn_kernel<WT, KT, NC, true>), grid, block, 0, s, p);                  \
         else VH_LAUNCH((qkv_attn_kernel<WT, KT, NC, false>), grid, block, 0, s, p);                        \
     } while (0)
-#define VH_QA_KV(WT, NC)                                       \
-    if (kv_dtype == VLRF_HIP_KV_Q8_0) VH_QA(WT, VLRF_HIP_KV_Q8_0, NC);  \
+#define VH_QA_KV(WT, NC)                                               \
+    if (kv_dtype == VLRF_HIP_KV_Q8_0) VH_QA(WT, VLRF_HIP_KV_Q8_0, NC); \
     else VH_QA(WT, VLRF_HIP_KV_F16, NC);
     if (w_dtype == VLRF_HIP_DT_Q8_0) {
         if (nc == 1) { VH_QA_KV(VLRF_HIP_DT_Q8_0, 1) }

@@ -259,13 +259,13 @@ int launch_gemv(hipStream_t s, const DevWeight& a, const DevWeight* b, const flo
     VH_ARG(!nparts || head_dim == 64 || (head_dim == 128 && xm == 60 && a.K % 128 == 0),
            "gemv: chunk merge of head dim %d (form %d)", head_dim, xm);
 #define VH_GEMV_XM(NC, RPW, XM)                                                                            \
-    do {                                                                                                  \
+    do {                                                                                                   \
         const int groups = (a.N + kGemvWaves * (RPW)-1) / (kGemvWaves * (RPW));                            \
         dim3 grid(((XM)&16) || groups < kGemvMaxGroups ? groups : kGemvMaxGroups);                         \
         VH_LAUNCH((gemv_kernel<WT, NC, RPW, SWIGLU, XM>), grid, dim3(64 * kGemvWaves), 0, s, a.q, a.d, qb, \
-                  db, a.N, a.K, x, x_row, x_copy, norm_w, eps, residual, y, nparts, argp);             \
+                  db, a.N, a.K, x, x_row, x_copy, norm_w, eps, residual, y, nparts, argp);                 \
     } while (0)
-#define VH_GEMV(NC, RPW)                                                   \
+#define VH_GEMV(NC, RPW)                                                  \
     do {                                                                  \
         if (xm == 0) VH_GEMV_XM(NC, RPW, 0);                              \
         else if (xm == 1) VH_GEMV_XM(NC, RPW, 1);                         \
