@@ -215,18 +215,20 @@ int launch_rope_append(hipStream_t s, const KVLayer& L, float* q, const float* k
                        const int* pos_dev, const float* cos_t, const float* sin_t);
 int launch_kv_dequant(hipStream_t s, const KVLayer& L, int n_kv, int d_head, int max_seq,
                       int ctx_len, float* K_out, float* V_out);
-// Prefill: RoPE on q (in place) and k of T tokens of a [T][ld] QKV buffer at
-// positions pos0.., then the Q8_0 append of their K/V rows.
+// Prefill: RoPE on k (and, rope_q, on q in place) of T tokens of a [T][ld]
+// QKV buffer at positions pos0.., then the cache append of their K/V rows.
 int launch_prefill_rope_append(hipStream_t s, const KVLayer& L, float* qkv, int ld, int T, int n_heads,
                                int n_kv, int d_head, int max_seq, int pos0, const float* cos_t,
-                               const float* sin_t);
+                               const float* sin_t, bool rope_q = true);
 // x[t] = table[ids[t]] for T device ids
 int launch_embed_rows(hipStream_t s, const float* table, const int* ids, float* x, int T, int D);
-// Causal attention of T new tokens (positions pos0..) over the Q8_0 cache on
-// the matrix cores: q (rotated, f32) read from the [T][ld] QKV buffer, the
-// cache rows [0, pos0+T) dequantized to bf16, out bf16 [T][n_heads*d_head].
+// Causal attention of T new tokens (positions pos0..) over the cache on the
+// matrix cores: q (f32) read from the [T][ld] QKV buffer and, with the RoPE
+// tables (null: q already rotated), rotated on load; the cache rows
+// [0, pos0+T) dequantized to bf16, out bf16 [T][n_heads*d_head].
 int launch_attn_prefill(hipStream_t s, const float* qkv, int ld, const KVLayer& L, int T, int pos0,
-                        int n_heads, int n_kv, int d_head, int max_seq, float scale, uint16_t* out);
+                        int n_heads, int n_kv, int d_head, int max_seq, float scale, const float* cos_t,
+                        const float* sin_t, uint16_t* out);
 
 // Decode fusion of the attention kernel (model step): RoPE of q and of the
 // token's k at the device position, and the append of its K/V row.

@@ -624,7 +624,8 @@ template <int D, int REP, int KVT>
 __global__ __launch_bounds__(512) void attn_prefill_kernel(
     const float* __restrict__ qkv, int ld, const int8_t* __restrict__ kq, const int8_t* __restrict__ vq,
     const float* __restrict__ ks, const float* __restrict__ vs, long head_stride, int T, int pos0,
-    float scale, int n_heads, uint16_t* __restrict__ out) {
+    float scale, int n_heads, const float* __restrict__ cos_t, const float* __restrict__ sin_t,
+    uint16_t* __restrict__ out) {
     typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
     typedef float f32x16 __attribute__((ext_vector_type(16)));
     constexpr int NT = 512, NQB = 8 / REP;           // waves: REP heads x NQB query blocks
@@ -658,14 +659,39 @@ __global__ __launch_bounds__(512) void attn_prefill_kernel(
 
     bf16x8 qf[D / 16];                               // B operand: query lq, dims 16kk + 8hh + e
     {
+        // The lane's dims j and j + D/2 (groups kk and kk + D/32) are a RoPE
+        // pair (rope.hpp:90-96): with tables the query is rotated here, on
+        // load, at its position pos0 + qi, by the same separately rounded
+        // products as the per-row RoPE.
         const float* qr = qkv + (size_t)qi * ld + (size_t)h * D;
+        float xv[D / 16][8];
 #pragma unroll
         for (int kk = 0; kk < D / 16; ++kk) {
             const float4 a = *reinterpret_cast<const float4*>(qr + 16 * kk + 8 * hh);
             const float4 b = *reinterpret_cast<const float4*>(qr + 16 * kk + 8 * hh + 4);
-            qf[kk] = bf16x8{(__bf16)a.x, (__bf16)a.y, (__bf16)a.z, (__bf16)a.w,
-                            (__bf16)b.x, (__bf16)b.y, (__bf16)b.z, (__bf16)b.w};
+            xv[kk][0] = a.x; xv[kk][1] = a.y; xv[kk][2] = a.z; xv[kk][3] = a.w;
+            xv[kk][4] = b.x; xv[kk][5] = b.y; xv[kk][6] = b.z; xv[kk][7] = b.w;
         }
+        if (cos_t) {
+            const float* ct = cos_t + (size_t)(pos0 + qi) * (D / 2);
+            const float* st = sin_t + (size_t)(pos0 + qi) * (D / 2);
+#pragma unroll
+            for (int kk = 0; kk < D / 32; ++kk) {
+                const float4 c0 = *reinterpret_cast<const float4*>(ct + 16 * kk + 8 * hh);
+                const float4 c1 = *reinterpret_cast<const float4*>(ct + 16 * kk + 8 * hh + 4);
+                const float4 s0 = *reinterpret_cast<const float4*>(st + 16 * kk + 8 * hh);
+                const float4 s1 = *reinterpret_cast<const float4*>(st + 16 * kk + 8 * hh + 4);
+                const float cv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+                const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    attn::rope2(xv[kk][e], xv[kk + D / 32][e], cv[e], sv[e], &xv[kk][e], &xv[kk + D / 32][e]);
+            }
+        }
+#pragma unroll
+        for (int kk = 0; kk < D / 16; ++kk)
+            qf[kk] = bf16x8{(__bf16)xv[kk][0], (__bf16)xv[kk][1], (__bf16)xv[kk][2], (__bf16)xv[kk][3],
+                            (__bf16)xv[kk][4], (__bf16)xv[kk][5], (__bf16)xv[kk][6], (__bf16)xv[kk][7]};
     }
     f32x16 o[D / 32];
 #pragma unroll
@@ -1335,7 +1361,8 @@ int launch_attn_f32_tiled(hipStream_t s, const float* Q, const float* K, const f
 }
 
 int launch_attn_prefill(hipStream_t s, const float* qkv, int ld, const KVLayer& L, int T, int pos0,
-                        int n_heads, int n_kv, int d_head, int max_seq, float scale, uint16_t* out) {
+                        int n_heads, int n_kv, int d_head, int max_seq, float scale, const float* cos_t,
+                        const float* sin_t, uint16_t* out) {
     VH_ARG(n_kv > 0 && n_heads % n_kv == 0, "attn_prefill: n_heads %d not a multiple of n_kv %d", n_heads, n_kv);
     const int rep = n_heads / n_kv;
     VH_ARG(d_head == 64 || d_head == 128, "attn_prefill: d_head %d not in {64,128}", d_head);
@@ -1343,11 +1370,12 @@ int launch_attn_prefill(hipStream_t s, const float* qkv, int ld, const KVLayer& 
     VH_ARG(T >= 1 && pos0 >= 0 && pos0 + T <= max_seq, "attn_prefill: positions [%d,%d) outside the cache",
            pos0, pos0 + T);
     VH_ARG(ld % 4 == 0, "attn_prefill: row stride %d not a multiple of 4", ld);
+    VH_ARG(!cos_t == !sin_t, "attn_prefill: RoPE takes both tables");
     const int nqb = 8 / rep;                        // query blocks of 32 per workgroup (8 waves)
     dim3 grid(((T + kPQ - 1) / kPQ + nqb - 1) / nqb, n_kv);
 #define VH_AP(D, R, KT)                                                                                 \
     hipLaunchKernelGGL((attn_prefill_kernel<D, R, KT>), grid, dim3(512), 0, s, qkv, ld, L.k, L.v, L.ks, \
-                       L.vs, (long)max_seq * d_head, T, pos0, scale, n_heads, out)
+                       L.vs, (long)max_seq * d_head, T, pos0, scale, n_heads, cos_t, sin_t, out)
 #define VH_AP_R(D, KT)                      \
     switch (rep) {                          \
         case 1: VH_AP(D, 1, KT); break;     \

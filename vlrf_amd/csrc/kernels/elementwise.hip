@@ -169,7 +169,7 @@ __global__ __launch_bounds__(256) void rope_append_kernel(int8_t* kq, int8_t* vq
 // then the K and V rows appended to the cache (attention.hpp:109-128 order).
 __global__ __launch_bounds__(256) void prefill_rope_append_kernel(
     int8_t* kq, int8_t* vq, float* ks, float* vs, int dtype, float* qkv, int ld, int n_heads, int n_kv, int D,
-    int max_seq, int pos0, const float* __restrict__ cos_t, const float* __restrict__ sin_t) {
+    int max_seq, int pos0, const float* __restrict__ cos_t, const float* __restrict__ sin_t, int rope_q) {
     __shared__ float red[4];
     __shared__ float kr[1024];
     const int t = blockIdx.x, p = pos0 + t;
@@ -182,7 +182,9 @@ __global__ __launch_bounds__(256) void prefill_rope_append_kernel(
     const float* s = sin_t + (size_t)p * half;
     for (int i = threadIdx.x; i < row; i += 256) kr[i] = k[i];
     __syncthreads();
-    if (half % 4 == 0) {
+    if (!rope_q) {
+        // q is rotated by its consumer (the prefill attention, on load)
+    } else if (half % 4 == 0) {
         // four pairs per thread: float4 loads and stores of x0 and x1, the same
         // separately rounded products per element as rope_pair
         for (int i4 = threadIdx.x; i4 < n_heads * half / 4; i4 += 256) {
@@ -423,13 +425,13 @@ int launch_rope_append(hipStream_t s, const KVLayer& L, float* q, const float* k
 
 int launch_prefill_rope_append(hipStream_t s, const KVLayer& L, float* qkv, int ld, int T, int n_heads,
                                int n_kv, int d_head, int max_seq, int pos0, const float* cos_t,
-                               const float* sin_t) {
+                               const float* sin_t, bool rope_q) {
     VH_ARG(n_kv * d_head <= 1024, "prefill_rope_append: kv row %d exceeds 1024", n_kv * d_head);
     VH_ARG(d_head % 2 == 0 && T >= 1, "prefill_rope_append: bad shape");
     VH_ARG(pos0 >= 0 && pos0 + T <= max_seq, "prefill_rope_append: positions [%d,%d) outside the cache",
            pos0, pos0 + T);
     hipLaunchKernelGGL(prefill_rope_append_kernel, dim3(T), dim3(256), 0, s, L.k, L.v, L.ks, L.vs, L.dtype, qkv, ld,
-                       n_heads, n_kv, d_head, max_seq, pos0, cos_t, sin_t);
+                       n_heads, n_kv, d_head, max_seq, pos0, cos_t, sin_t, rope_q ? 1 : 0);
     VH_LAUNCHED();
     return VLRF_HIP_OK;
 }

@@ -665,10 +665,11 @@ int enqueue_prefill_layers(vlrf_hip_model* m, const float* x_in, float* x_out, i
         float* dst = l == m->L - 1 ? x_out : x;                  // and leaving it
         rc = launch_rows_to_bf16(s, src, Ly.ln1, m->pf_a, T, m->D, eps);
         if (!rc) rc = launch_qgemm(s, Ly.wqkv, m->pf_a, T, nullptr, m->pf_qkv);
+        // k rotated and appended here; q rotated by the attention as it loads it
         if (!rc) rc = launch_prefill_rope_append(s, Ly.kv, m->pf_qkv, ld, T, m->H, m->G, m->dh, m->S, m->pos,
-                                                 m->cos_t, m->sin_t);
+                                                 m->cos_t, m->sin_t, false);
         if (!rc) rc = launch_attn_prefill(s, m->pf_qkv, ld, Ly.kv, T, m->pos, m->H, m->G, m->dh, m->S, scale,
-                                          m->pf_att);
+                                          m->cos_t, m->sin_t, m->pf_att);
         if (!rc) rc = launch_qgemm(s, Ly.wo, m->pf_att, T, src, x);            // x = src + att . Wo^T
         if (!rc) rc = launch_rows_to_bf16(s, x, Ly.ln2, m->pf_a, T, m->D, eps);
         if (!rc) rc = launch_qgemm_swiglu(s, Ly.wg, Ly.wu, m->pf_a, T, m->pf_h, true);
