@@ -215,17 +215,18 @@ int launch_rope_append(hipStream_t s, const KVLayer& L, float* q, const float* k
                        const int* pos_dev, const float* cos_t, const float* sin_t);
 int launch_kv_dequant(hipStream_t s, const KVLayer& L, int n_kv, int d_head, int max_seq,
                       int ctx_len, float* K_out, float* V_out);
-// Prefill: RoPE on k (and, rope_q, on q in place) of T tokens of a [T][ld]
-// QKV buffer at positions pos0.., then the cache append of their K/V rows.
-int launch_prefill_rope_append(hipStream_t s, const KVLayer& L, float* qkv, int ld, int T, int n_heads,
+// Prefill: RoPE on k of T tokens of a [T][ld] QKV buffer at positions
+// pos0.., then the cache append of their K/V rows (q is left as it is: the
+// prefill attention rotates it as it loads it).
+int launch_prefill_rope_append(hipStream_t s, const KVLayer& L, const float* qkv, int ld, int T, int n_heads,
                                int n_kv, int d_head, int max_seq, int pos0, const float* cos_t,
-                               const float* sin_t, bool rope_q = true);
+                               const float* sin_t);
 // x[t] = table[ids[t]] for T device ids
 int launch_embed_rows(hipStream_t s, const float* table, const int* ids, float* x, int T, int D);
 // Causal attention of T new tokens (positions pos0..) over the cache on the
-// matrix cores: q (f32) read from the [T][ld] QKV buffer and, with the RoPE
-// tables (null: q already rotated), rotated on load; the cache rows
-// [0, pos0+T) dequantized to bf16, out bf16 [T][n_heads*d_head].
+// matrix cores: q (f32, not yet rotated) read from the [T][ld] QKV buffer and
+// rotated by the RoPE tables on load; the cache rows [0, pos0+T) dequantized
+// to bf16, out bf16 [T][n_heads*d_head].
 int launch_attn_prefill(hipStream_t s, const float* qkv, int ld, const KVLayer& L, int T, int pos0,
                         int n_heads, int n_kv, int d_head, int max_seq, float scale, const float* cos_t,
                         const float* sin_t, uint16_t* out);

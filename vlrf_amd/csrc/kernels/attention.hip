@@ -660,9 +660,9 @@ __global__ __launch_bounds__(512) void attn_prefill_kernel(
     bf16x8 qf[D / 16];                               // B operand: query lq, dims 16kk + 8hh + e
     {
         // The lane's dims j and j + D/2 (groups kk and kk + D/32) are a RoPE
-        // pair (rope.hpp:90-96): with tables the query is rotated here, on
-        // load, at its position pos0 + qi, by the same separately rounded
-        // products as the per-row RoPE.
+        // pair (rope.hpp:90-96): the query is rotated here, on load, at its
+        // position pos0 + qi, by the same separately rounded products as the
+        // per-row RoPE.
         const float* qr = qkv + (size_t)qi * ld + (size_t)h * D;
         float xv[D / 16][8];
 #pragma unroll
@@ -672,7 +672,7 @@ __global__ __launch_bounds__(512) void attn_prefill_kernel(
             xv[kk][0] = a.x; xv[kk][1] = a.y; xv[kk][2] = a.z; xv[kk][3] = a.w;
             xv[kk][4] = b.x; xv[kk][5] = b.y; xv[kk][6] = b.z; xv[kk][7] = b.w;
         }
-        if (cos_t) {
+        {
             const float* ct = cos_t + (size_t)(pos0 + qi) * (D / 2);
             const float* st = sin_t + (size_t)(pos0 + qi) * (D / 2);
 #pragma unroll
@@ -1370,7 +1370,7 @@ int launch_attn_prefill(hipStream_t s, const float* qkv, int ld, const KVLayer& 
     VH_ARG(T >= 1 && pos0 >= 0 && pos0 + T <= max_seq, "attn_prefill: positions [%d,%d) outside the cache",
            pos0, pos0 + T);
     VH_ARG(ld % 4 == 0, "attn_prefill: row stride %d not a multiple of 4", ld);
-    VH_ARG(!cos_t == !sin_t, "attn_prefill: RoPE takes both tables");
+    VH_ARG(cos_t && sin_t, "attn_prefill: missing RoPE tables");
     const int nqb = 8 / rep;                        // query blocks of 32 per workgroup (8 waves)
     dim3 grid(((T + kPQ - 1) / kPQ + nqb - 1) / nqb, n_kv);
 #define VH_AP(D, R, KT)                                                                                 \

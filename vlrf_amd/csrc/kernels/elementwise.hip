@@ -165,48 +165,24 @@ __global__ __launch_bounds__(256) void rope_append_kernel(int8_t* kq, int8_t* vq
 }
 
 // Prefill: token t of a [T][ld] QKV buffer (q: n_heads*D at column 0, k and v:
-// n_kv*D each after it) at position pos0 + t: q rotated in place, k rotated,
-// then the K and V rows appended to the cache (attention.hpp:109-128 order).
+// n_kv*D each after it) at position pos0 + t: k rotated, then the K and V rows
+// appended to the cache (attention.hpp:109-128 order; q is rotated by the
+// prefill attention as it loads it).  One workgroup a token, for the rows
+// prefill_kv_rows_kernel's lane layout does not fit.
 __global__ __launch_bounds__(256) void prefill_rope_append_kernel(
-    int8_t* kq, int8_t* vq, float* ks, float* vs, int dtype, float* qkv, int ld, int n_heads, int n_kv, int D,
-    int max_seq, int pos0, const float* __restrict__ cos_t, const float* __restrict__ sin_t, int rope_q) {
+    int8_t* kq, int8_t* vq, float* ks, float* vs, int dtype, const float* qkv, int ld, int n_heads, int n_kv,
+    int D, int max_seq, int pos0, const float* __restrict__ cos_t, const float* __restrict__ sin_t) {
     __shared__ float red[4];
     __shared__ float kr[1024];
     const int t = blockIdx.x, p = pos0 + t;
     if (p < 0 || p >= max_seq) return;   // host checks capacity; never write past the cache
     const int half = D / 2, row = n_kv * D;
-    float* q = qkv + (size_t)t * ld;
-    const float* k = q + (size_t)n_heads * D;
+    const float* k = qkv + (size_t)t * ld + (size_t)n_heads * D;
     const float* v = k + row;
     const float* c = cos_t + (size_t)p * half;
     const float* s = sin_t + (size_t)p * half;
     for (int i = threadIdx.x; i < row; i += 256) kr[i] = k[i];
     __syncthreads();
-    if (!rope_q) {
-        // q is rotated by its consumer (the prefill attention, on load)
-    } else if (half % 4 == 0) {
-        // four pairs per thread: float4 loads and stores of x0 and x1, the same
-        // separately rounded products per element as rope_pair
-        for (int i4 = threadIdx.x; i4 < n_heads * half / 4; i4 += 256) {
-            const int h = 4 * i4 / half, j = 4 * i4 - h * half;
-            float4* x0p = reinterpret_cast<float4*>(q + (size_t)h * D + j);
-            float4* x1p = reinterpret_cast<float4*>(q + (size_t)h * D + half + j);
-            const float4 x0 = *x0p, x1 = *x1p;
-            const float4 c4 = *reinterpret_cast<const float4*>(c + j), s4 = *reinterpret_cast<const float4*>(s + j);
-            float4 y0, y1;
-            rope2v(x0.x, x1.x, c4.x, s4.x, &y0.x, &y1.x);
-            rope2v(x0.y, x1.y, c4.y, s4.y, &y0.y, &y1.y);
-            rope2v(x0.z, x1.z, c4.z, s4.z, &y0.z, &y1.z);
-            rope2v(x0.w, x1.w, c4.w, s4.w, &y0.w, &y1.w);
-            *x0p = y0;
-            *x1p = y1;
-        }
-    } else {
-        for (int i = threadIdx.x; i < n_heads * half; i += 256) {
-            const int h = i / half, j = i - h * half;
-            rope_pair(q + (size_t)h * D, j, half, c[j], s[j]);
-        }
-    }
     for (int i = threadIdx.x; i < n_kv * half; i += 256) {
         const int h = i / half, j = i - h * half;
         rope_pair(kr + h * D, j, half, c[j], s[j]);
@@ -214,6 +190,86 @@ __global__ __launch_bounds__(256) void prefill_rope_append_kernel(
     __syncthreads();
     store_row_to_cache(kr, kq, ks, dtype, p, n_kv, D, max_seq, red);
     store_row_to_cache(v, vq, vs, dtype, p, n_kv, D, max_seq, red);
+}
+
+// The prefill's K/V rows with q left to its consumer: one wave per token (four
+// a workgroup), no LDS and no barrier.  Lane l holds PPL consecutive RoPE pairs
+// of one head (elements j and j + D/2, j = j0 .. j0 + PPL - 1) of the K row
+// and 2 PPL consecutive elements of the V row, read straight from the QKV
+// buffer; RoPE as rope_pair, then per row the cache dtype's store as
+// store_row_to_cache (Q8_0: the row's amax by a wave max, the same scale,
+// reciprocal and rounding), as contiguous runs of PPL (K) and 2 PPL (V)
+// elements.  n_kv * D / 2 == 64 * PPL and (D / 2) % PPL == 0.
+template <int PPL>
+__global__ __launch_bounds__(256) void prefill_kv_rows_kernel(
+    int8_t* kq, int8_t* vq, float* ks, float* vs, int dtype, const float* __restrict__ qkv, int ld, int n_heads,
+    int D, int max_seq, int pos0, int T, const float* __restrict__ cos_t, const float* __restrict__ sin_t) {
+    const int lane = threadIdx.x & 63, t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int p = pos0 + t;
+    if (t >= T || p < 0 || p >= max_seq) return;   // host checks capacity; never write past the cache
+    const int half = D / 2, pr = lane * PPL, h = pr / half, j0 = pr - h * half;
+    const float* k = qkv + (size_t)t * ld + (size_t)n_heads * D;
+    const float* v = k + (size_t)(64 * PPL * 2);          // the V row follows the K row (n_kv * D = 128 PPL)
+    float y0[PPL], y1[PPL], vv[2 * PPL];
+#pragma unroll
+    for (int i = 0; i < PPL; ++i) {
+        const float x0 = k[h * D + j0 + i], x1 = k[h * D + half + j0 + i];
+        rope2v(x0, x1, cos_t[(size_t)p * half + j0 + i], sin_t[(size_t)p * half + j0 + i], &y0[i], &y1[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < 2 * PPL; ++i) vv[i] = v[2 * PPL * lane + i];
+    const int vh = (2 * PPL * lane) / D, vd = 2 * PPL * lane - vh * D;
+    int8_t* krow = kq;
+    int8_t* vrow = vq;
+    if (dtype == VLRF_HIP_KV_Q8_0) {
+        auto quant = [](float x, float amax, float inv) -> int8_t {
+            int q = 0;
+            if (amax != 0.f) {
+                q = (int)roundf(x * inv);
+                q = min(127, max(-127, q));
+            }
+            return (int8_t)q;
+        };
+        float ak = 0.f, av = 0.f;
+#pragma unroll
+        for (int i = 0; i < PPL; ++i) ak = fmaxf(ak, fmaxf(fabsf(y0[i]), fabsf(y1[i])));
+#pragma unroll
+        for (int i = 0; i < 2 * PPL; ++i) av = fmaxf(av, fabsf(vv[i]));
+        ak = wave_max(ak);
+        av = wave_max(av);
+        const float sk = ak != 0.f ? ak / 127.f : 0.f, sv = av != 0.f ? av / 127.f : 0.f;
+        const float ik = ak != 0.f ? 1.f / sk : 0.f, iv = av != 0.f ? 1.f / sv : 0.f;
+        int8_t* kr = krow + ((size_t)h * max_seq + p) * D;
+        int8_t* vr = vrow + ((size_t)vh * max_seq + p) * D;
+#pragma unroll
+        for (int i = 0; i < PPL; ++i) {
+            kr[j0 + i] = quant(y0[i], ak, ik);
+            kr[half + j0 + i] = quant(y1[i], ak, ik);
+        }
+#pragma unroll
+        for (int i = 0; i < 2 * PPL; ++i) vr[vd + i] = quant(vv[i], av, iv);
+        if (lane == 0) { ks[p] = sk; vs[p] = sv; }
+    } else if (dtype == VLRF_HIP_KV_F16) {
+        uint16_t* kr = reinterpret_cast<uint16_t*>(krow) + ((size_t)h * max_seq + p) * D;
+        uint16_t* vr = reinterpret_cast<uint16_t*>(vrow) + ((size_t)vh * max_seq + p) * D;
+#pragma unroll
+        for (int i = 0; i < PPL; ++i) {
+            kr[j0 + i] = f32_to_f16_kv(y0[i]);
+            kr[half + j0 + i] = f32_to_f16_kv(y1[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < 2 * PPL; ++i) vr[vd + i] = f32_to_f16_kv(vv[i]);
+    } else {
+        float* kr = reinterpret_cast<float*>(krow) + ((size_t)h * max_seq + p) * D;
+        float* vr = reinterpret_cast<float*>(vrow) + ((size_t)vh * max_seq + p) * D;
+#pragma unroll
+        for (int i = 0; i < PPL; ++i) {
+            kr[j0 + i] = y0[i];
+            kr[half + j0 + i] = y1[i];
+        }
+#pragma unroll
+        for (int i = 0; i < 2 * PPL; ++i) vr[vd + i] = vv[i];
+    }
 }
 
 // x[t] = table[ids[t]] (ops.hpp:615-626), one workgroup per token.
@@ -423,15 +479,31 @@ int launch_rope_append(hipStream_t s, const KVLayer& L, float* q, const float* k
     return VLRF_HIP_OK;
 }
 
-int launch_prefill_rope_append(hipStream_t s, const KVLayer& L, float* qkv, int ld, int T, int n_heads,
+int launch_prefill_rope_append(hipStream_t s, const KVLayer& L, const float* qkv, int ld, int T, int n_heads,
                                int n_kv, int d_head, int max_seq, int pos0, const float* cos_t,
-                               const float* sin_t, bool rope_q) {
+                               const float* sin_t) {
     VH_ARG(n_kv * d_head <= 1024, "prefill_rope_append: kv row %d exceeds 1024", n_kv * d_head);
     VH_ARG(d_head % 2 == 0 && T >= 1, "prefill_rope_append: bad shape");
     VH_ARG(pos0 >= 0 && pos0 + T <= max_seq, "prefill_rope_append: positions [%d,%d) outside the cache",
            pos0, pos0 + T);
+    const int pairs = n_kv * d_head / 2, ppl = pairs / 64;
+    if (pairs % 64 == 0 && (ppl == 1 || ppl == 2 || ppl == 4 || ppl == 8) && (d_head / 2) % ppl == 0) {
+        const dim3 grid((T + 3) / 4);
+#define VH_KVR(P)                                                                                              \
+    hipLaunchKernelGGL(prefill_kv_rows_kernel<P>, grid, dim3(256), 0, s, L.k, L.v, L.ks, L.vs, L.dtype, qkv, ld, \
+                       n_heads, d_head, max_seq, pos0, T, cos_t, sin_t)
+        switch (ppl) {
+            case 1: VH_KVR(1); break;
+            case 2: VH_KVR(2); break;
+            case 4: VH_KVR(4); break;
+            default: VH_KVR(8); break;
+        }
+#undef VH_KVR
+        VH_LAUNCHED();
+        return VLRF_HIP_OK;
+    }
     hipLaunchKernelGGL(prefill_rope_append_kernel, dim3(T), dim3(256), 0, s, L.k, L.v, L.ks, L.vs, L.dtype, qkv, ld,
-                       n_heads, n_kv, d_head, max_seq, pos0, cos_t, sin_t, rope_q ? 1 : 0);
+                       n_heads, n_kv, d_head, max_seq, pos0, cos_t, sin_t);
     VH_LAUNCHED();
     return VLRF_HIP_OK;
 }

@@ -667,7 +667,7 @@ int enqueue_prefill_layers(vlrf_hip_model* m, const float* x_in, float* x_out, i
         if (!rc) rc = launch_qgemm(s, Ly.wqkv, m->pf_a, T, nullptr, m->pf_qkv);
         // k rotated and appended here; q rotated by the attention as it loads it
         if (!rc) rc = launch_prefill_rope_append(s, Ly.kv, m->pf_qkv, ld, T, m->H, m->G, m->dh, m->S, m->pos,
-                                                 m->cos_t, m->sin_t, false);
+                                                 m->cos_t, m->sin_t);
         if (!rc) rc = launch_attn_prefill(s, m->pf_qkv, ld, Ly.kv, T, m->pos, m->H, m->G, m->dh, m->S, scale,
                                           m->cos_t, m->sin_t, m->pf_att);
         if (!rc) rc = launch_qgemm(s, Ly.wo, m->pf_att, T, src, x);            // x = src + att . Wo^T
