@@ -26,7 +26,11 @@
 // single-pass kernel below in chunked form instead: one query head and one
 // 512-row chunk per workgroup, a (m, l, acc) partial per chunk, merged by the
 // O projection's GEMV prologue, so the step has no combine launch; caches of
-// at most 512 rows take the single pass over the whole context.
+// at most 512 rows take the single pass over the whole context.  The
+// stand-alone calls (vlrf_hip_attn_decode, vlrf_hip_attn_f32 at T = 1) at
+// d_head 64 run attn_decode_chunks_kernel: the same chunk code on 64..512-row
+// chunks, merged in the same launch by each head's last workgroup; the
+// split-K kernel and its combine serve d_head 128 and longer contexts.
 #include "../internal.hpp"
 #include "attn_core.hpp"
 
