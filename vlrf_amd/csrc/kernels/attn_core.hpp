@@ -341,8 +341,8 @@ __device__ __forceinline__ void chunk(Smem<NW>& sm, const Round<KVT>& R, float q
 // ---- one chunk without the token's row (the fused QKV + attention launch) ----------
 // The attention of query head h over the cache rows [c0, min(c0 + 64*NW, pos))
 // for the wave's loaded round R: every row before the token, none of it (the
-// token's key is merged as its own partial).  q0/q1 (wave 0, lanes j < 32):
-// the head's q[j], q[j + 32] before RoPE (rc, rs: the table entries of pair j).
+// token's key is merged as its own partial).  The head's rotated q is in
+// sm.qs (stage_q, before a workgroup barrier).
 //
 // Arranged for latency: the chunk's maximum score is formed first (one more
 // barrier), so every wave exponentiates against it and the waves' P.V sums
@@ -360,19 +360,23 @@ struct SmemQ {
     __align__(16) float wacc[NW][D];
 };
 
+// q of the head into sm.qs, rotated (lanes j < 32 of one wave: q[j], q[j + 32]
+// before RoPE; rc, rs the table entries of pair j).  The caller's next
+// workgroup barrier publishes it to chunk_q.
+template <int NW>
+__device__ __forceinline__ void stage_q(SmemQ<NW>& sm, float q0, float q1, float rc, float rs, bool rot) {
+    const int lane = threadIdx.x & 63;
+    float y0 = q0, y1 = q1;
+    if (rot) rope2(q0, q1, rc, rs, &y0, &y1);
+    if (lane < HALF) { sm.qs[lane] = y0; sm.qs[lane + HALF] = y1; }
+}
+
 template <int KVT, int NW, class Out>
-__device__ __forceinline__ void chunk_q(SmemQ<NW>& sm, const Round<KVT>& R, float q0, float q1, float rc, float rs,
-                                        bool rot, int c0, int pos, float scale, Out&& out) {
+__device__ __forceinline__ void chunk_q(SmemQ<NW>& sm, const Round<KVT>& R, int c0, int pos, float scale, Out&& out) {
     static_assert(KVT == VLRF_HIP_KV_Q8_0 || KVT == VLRF_HIP_KV_F16, "Q8_0 / F16 caches");
     constexpr bool Q8 = KVT == VLRF_HIP_KV_Q8_0;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int tg = lane >> 2, dg = lane & 3;
-    if (w == 0) {
-        float y0 = q0, y1 = q1;
-        if (rot) rope2(q0, q1, rc, rs, &y0, &y1);
-        if (lane < HALF) { sm.qs[lane] = y0; sm.qs[lane + HALF] = y1; }
-    }
-    __syncthreads();
 
     // scores: lane = row c0 + 64w + lane (rows from pos on are masked)
     const int t = c0 + w * 64 + lane;

@@ -235,14 +235,19 @@ __global__ __launch_bounds__(gemv::kGemvThreads) __attribute__((amdgpu_waves_per
     bool use[2] = {true, true};
     u32x2 v[2];
     bool ok = true;
-    if (w == 0) ok = poll_direct<2, u32x2>(c, off, use, v);
+    if (w == 0) {
+        ok = poll_direct<2, u32x2>(c, off, use, v);
+        // rope.hpp:84: positions >= max_seq stay unrotated.  Staged before the
+        // barrier that also publishes the workgroup's wait results.
+        if (ok)
+            attn::stage_q<8>(sm, __uint_as_float(v[0].x), __uint_as_float(v[1].x), nr.rc, nr.rs, pos < fz.max_seq);
+    }
     if (!block_ok(ok, oks)) return;
-    const bool rot = pos < fz.max_seq;   // rope.hpp:84: positions >= max_seq stay unrotated
-    attn::chunk_q<KVT, 8>(sm, R, __uint_as_float(v[0].x), __uint_as_float(v[1].x), nr.rc, nr.rs, rot, c0, pos,
-                          P.scale, [&](int t, float ot, float mt, float lt) {   // the chunk's partial, unnormalised
-                              pp[t] = ot;
-                              if (t == 0) { pp[attn::D] = mt; pp[attn::D + 1] = lt; }
-                          });
+    // the chunk's partial, unnormalised
+    attn::chunk_q<KVT, 8>(sm, R, c0, pos, P.scale, [&](int t, float ot, float mt, float lt) {
+        pp[t] = ot;
+        if (t == 0) { pp[attn::D] = mt; pp[attn::D + 1] = lt; }
+    });
 }
 
 int qkv_chunks(int w_dtype, int K) {
