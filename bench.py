@@ -429,18 +429,8 @@ def cpu_baseline_plan(cfg, ctx_len, max_steps):
     return ocfg
 
 
-def cpu_baseline(cfg, f32w, ctx_len, gpu_steps, budget_s=20.0, max_steps=32, threads=None):
-    """Oracle decode steps at context ctx_len on every hardware thread the
-    process may use."""
-    import oracle
-    if threads is None:
-        try:
-            threads = len(os.sched_getaffinity(0))
-        except AttributeError:
-            threads = os.cpu_count() or 1
-    threads = max(1, threads)
-    ocfg = cpu_baseline_plan(cfg, ctx_len, max_steps)
-    om = oracle.Model(ocfg, f32w, n_threads=threads)
+def _cpu_decode_rate(om, ocfg, ctx_len, budget_s, max_steps):
+    """(steps, tok/s) of decode steps from a cache of ctx_len - 1 seeded rows."""
     om.reset()
     om.fill_kv(ctx_len - 1, seed=7)
     tok = 1
@@ -452,14 +442,52 @@ def cpu_baseline(cfg, f32w, ctx_len, gpu_steps, budget_s=20.0, max_steps=32, thr
     t0 = time.perf_counter()
     for _ in range(n):
         tok = om.forward([tok])
-    dt = time.perf_counter() - t0
-    del om
-    return {"value": round(n / dt, 3), "unit": "tok/s", "cores": threads, "kind": "port",
-            "nproc": os.cpu_count(), "cpu": cpu_model(),
-            "sample": f"{n} decode steps (the GPU timed {gpu_steps}) of the 1.1B-shape f32-decoded model at "
-                      f"context {ctx_len}-{ctx_len + n} (oracle restatement, {threads} threads = every "
-                      f"hardware thread of the process's CPU set, KV cache filled with seeded codes "
-                      f"instead of a CPU prefill)"}
+    return n, n / (time.perf_counter() - t0)
+
+
+def _port_threads(threads):
+    if threads is None:
+        try:
+            threads = len(os.sched_getaffinity(0))
+        except AttributeError:
+            threads = os.cpu_count() or 1
+    return max(1, threads)
+
+
+def cpu_baseline(cfg, f32w, ctx_len, gpu_steps, budget_s=20.0, max_steps=32, threads=None,
+                 prefer_ref=True, port_budget_s=8.0):
+    """Decode steps at context ctx_len on the CPU: the reference's own
+    TransformerModel (oracle/_ref, built from its sources with its default
+    flags; its thread pool takes every hardware thread) when that library is
+    present, with the C restatement (every hardware thread of the process's
+    CPU set) timed beside it as `port`; else the restatement alone.  Both
+    start from the same seeded Q8_0 cache rows instead of a CPU prefill."""
+    import oracle
+    ocfg = cpu_baseline_plan(cfg, ctx_len, max_steps)
+    pt = _port_threads(threads)
+    port_what = f"oracle restatement, {pt} threads = every hardware thread of the process's CPU set"
+    out = {"unit": "tok/s", "nproc": os.cpu_count(), "cpu": cpu_model()}
+    if prefer_ref and oracle.ref() is not None:
+        om = oracle.RefModel(ocfg, f32w)
+        n, rate = _cpu_decode_rate(om, ocfg, ctx_len, budget_s, max_steps)
+        del om
+        rt = oracle.RefModel.threads()
+        what = f"reference TransformerModel built from its sources, its own pool of {rt} threads"
+        om = oracle.Model(ocfg, f32w, n_threads=pt)
+        pn, prate = _cpu_decode_rate(om, ocfg, ctx_len, port_budget_s, max_steps)
+        del om
+        out.update(value=round(rate, 3), cores=rt, kind="reference",
+                   port={"value": round(prate, 3), "cores": pt, "steps": pn})
+    else:
+        om = oracle.Model(ocfg, f32w, n_threads=pt)
+        n, rate = _cpu_decode_rate(om, ocfg, ctx_len, budget_s, max_steps)
+        del om
+        what = port_what
+        out.update(value=round(rate, 3), cores=pt, kind="port")
+    out["sample"] = (f"{n} decode steps (the GPU timed {gpu_steps}) of the 1.1B-shape f32-decoded model at "
+                     f"context {ctx_len}-{ctx_len + n} ({what}, Q8_0 KV cache filled with seeded codes "
+                     f"instead of a CPU prefill)")
+    return {k: out[k] for k in ("value", "unit", "cores", "kind", "port", "nproc", "cpu", "sample") if k in out}
 
 
 def summarize_trace(path, steps, per_step):

@@ -127,6 +127,7 @@ def ref():
     R.ref_model_forward.argtypes = [C.c_void_p, i32p, C.c_int, C.c_void_p]
     R.ref_model_forward.restype = C.c_int
     R.ref_model_kv.argtypes = [C.c_void_p, C.c_int] + [C.c_void_p] * 4
+    R.ref_model_fill_kv.argtypes = [C.c_void_p, C.c_int, C.c_uint64]
     R.ref_model_destroy.argtypes = [C.c_void_p]
     _REF = R
     return R
@@ -338,5 +339,53 @@ class Model:
     def __del__(self):
         try:
             lib().orc_model_destroy(self.h)
+        except Exception:
+            pass
+
+
+class RefModel:
+    """The reference TransformerModel itself (oracle/_ref, built from its own
+    sources) behind the same calls as Model: Q8_0 KV cache, the reference's
+    own thread pool (every hardware thread, ops.hpp:34-37).  Weights are
+    borrowed, so this object keeps `weights` alive."""
+
+    def __init__(self, cfg, weights):
+        R = ref()
+        if R is None:
+            raise RuntimeError("oracle/_ref/libvlrf_ref.so was not built")
+        self.cfg = cfg
+        self.w = weights
+        self.h = R.ref_model_create(cfg["vocab_size"], cfg["d_model"], cfg["d_ff"], cfg["n_heads"],
+                                    cfg["n_kv_heads"], cfg["n_layers"], cfg["max_seq_len"],
+                                    cfg["norm_eps"], cfg["rope_theta"])
+        for k, v in weights.items():
+            R.ref_model_set_tensor(self.h, k.encode(), v, v.shape[0] if v.ndim == 2 else 0, v.shape[-1])
+        R.ref_model_bind(self.h)
+
+    @staticmethod
+    def threads():
+        return ref().ref_hw_threads()
+
+    def reset(self):
+        ref().ref_model_reset(self.h)
+
+    @property
+    def used(self):
+        return ref().ref_model_used(self.h)
+
+    def fill_kv(self, used, seed=1):
+        """Same seeded codes and scales as Model.fill_kv."""
+        ref().ref_model_fill_kv(self.h, int(used), int(seed))
+
+    def forward(self, ids, want_logits=False):
+        ids = np.ascontiguousarray(ids, np.int32)
+        logits = np.zeros(self.cfg["vocab_size"], np.float32) if want_logits else None
+        tok = ref().ref_model_forward(self.h, ids, ids.size,
+                                      logits.ctypes.data if want_logits else None)
+        return (tok, logits) if want_logits else tok
+
+    def __del__(self):
+        try:
+            ref().ref_model_destroy(self.h)
         except Exception:
             pass

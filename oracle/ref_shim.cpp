@@ -167,6 +167,30 @@ void ref_model_kv_raw(void* h, int l, void** k, void** v) {
     }
 }
 
+// Fills rows [0, used) of every layer's Q8_0 cache with the same seeded codes
+// and scales as the C restatement's orc_model_fill_kv, and sets the caches'
+// fill length (kv_cache.hpp:138 `used`), so a decode step can be timed at a
+// long context without a CPU prefill.  No-op for other cache types.
+void ref_model_fill_kv(void* h, int used, uint64_t seed) {
+    auto& m = static_cast<RefModel*>(h)->m;
+    uint64_t z = seed * 0x9E3779B97F4A7C15ull + 1;
+    for (auto& c : m.kv_caches) {
+        if (c.dtype != vlrf::KVCacheDType::Q8_0) return;
+        int n = used < c.max_seq_len ? used : c.max_seq_len;
+        size_t row = (size_t)c.row_dim;
+        for (int r = 0; r < n; ++r) {
+            for (size_t i = 0; i < row; ++i) {
+                z ^= z << 13; z ^= z >> 7; z ^= z << 17;
+                c.K_q8[(size_t)r * row + i] = (int8_t)((int)(z & 0xFF) % 255 - 127);
+                c.V_q8[(size_t)r * row + i] = (int8_t)((int)((z >> 8) & 0xFF) % 255 - 127);
+            }
+            c.K_scale[r] = 0.02f;
+            c.V_scale[r] = 0.02f;
+        }
+        c.used = n;
+    }
+}
+
 void ref_model_destroy(void* h) { delete static_cast<RefModel*>(h); }
 
 }  // extern "C"

@@ -265,6 +265,30 @@ def test_model_bit_exact_vs_reference():
         R.ref_model_destroy(h)
 
 
+@needs_ref
+def test_filled_cache_decode_bit_exact_vs_reference():
+    """The CPU baseline's set-up: both models' caches filled with the same
+    seeded Q8_0 rows (no prefill), then decode steps from there give the same
+    logits bit for bit, and the fill length is what was asked."""
+    cfg, w = _tiny(33)
+    om = oracle.Model(cfg, w, n_threads=R.ref_hw_threads())
+    rm = oracle.RefModel(cfg, w)
+    om.fill_kv(40, seed=7)
+    rm.fill_kv(40, seed=7)
+    assert om.used == rm.used == 40
+    t1 = t2 = 5
+    for _ in range(6):
+        t1, l1 = om.forward([t1], True)
+        t2, l2 = rm.forward([t2], True)
+        assert t1 == t2 and np.array_equal(l1, l2)
+    assert om.used == rm.used == 46
+    rm.fill_kv(40, seed=8)                    # another seed: other codes, other logits
+    _, l3 = rm.forward([5], True)
+    om.fill_kv(40, seed=7)
+    _, l4 = om.forward([5], True)
+    assert not np.array_equal(l3, l4)
+
+
 def test_model_prefill_matches_incremental():
     """The invariant of test_flash_attention.cpp:131-182 at model level: a
     one-shot prefill and token-by-token decode give the same next-token logits."""
