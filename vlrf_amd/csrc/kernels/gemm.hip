@@ -627,24 +627,53 @@ __global__ __launch_bounds__(T::NT) void mfma_bgemm_kernel(
         }
         __builtin_amdgcn_sched_barrier(0);
     };
+    // The phase after a step's barrier: the same MFMAs and next-group reads,
+    // with the refill of stage `buf` (step kt) spread over the MFMAs (PER
+    // direct-to-LDS loads after each), so the loads leave under the MFMAs
+    // instead of holding them up.
+    constexpr int PER = (LPS + NMF - 1) / NMF;
+    static_assert(NR <= NMF, "one read per MFMA");
+    auto phase_refill = [&](const bf16x8 (&a)[MI], const bf16x8 (&b)[NB], const uint8_t* St, int g,
+                            bf16x8 (&na)[MI], bf16x8 (&nb)[NB], int kt, int buf) {
+        const int x = 16 * ((2 * (2 * (g >> 1) + h) + (g & 1)) ^ sw);
+        const uint8_t* pa = St + a_off + x;
+        const uint8_t* pb = St + b_off + x;
+        const uint32_t sa = base + buf * ST, sb = sa + A_B;
+#pragma unroll
+        for (int j = 0, n = 0; j < NB; ++j)
+#pragma unroll
+            for (int i = 0; i < MI; ++i, ++n) {
+                acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[j][i], 0, 0, 0);
+                if (n < MI) na[n] = *reinterpret_cast<const bf16x8*>(pa + n * 32 * RB);
+                else if (n < NR) nb[n - MI] = *reinterpret_cast<const bf16x8*>(pb + boff(n - MI));
+#pragma unroll
+                for (int l = n * PER; l < (n + 1) * PER && l < LPS; ++l) {
+                    if (l < T::A_IT) dma16(ga[l] + (size_t)kt * RB, sa + (l * NW + wave) * 1024);
+                    else dma16(gb[l - T::A_IT] + (size_t)kt * RB, sb + ((l - T::A_IT) * NW + wave) * 1024);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+    };
 
     // The ring: NS stages, stage k % NS holds step k.  A step's barrier sits
     // before its last group's MFMAs, whose operands are already in registers:
     // past it every wave has read the whole stage, so the stage is refilled
-    // with step k + NS at once, and the next step's first group is read from
-    // LDS under the last group's MFMAs.  Each load is issued NS - 1 steps
-    // before the barrier that waits for it.  No MFMA sits under a branch (the
-    // accumulators would be copied at the join): after the last step the
-    // first group of the next stage is read all the same (in bounds, unused).
+    // with step k + NS under those MFMAs, and the next step's first group is
+    // read from LDS under them too.  Each load is issued NS - 1 steps before
+    // the barrier that waits for it.  Every step issues its refill, with the
+    // step index clamped to the last one (past the end a stage gets a copy of
+    // the last step, which is never read, or, in the last step, of its own
+    // bytes), so the count of loads in flight is the same at every wait.  No
+    // MFMA sits under a branch (the accumulators would be copied at the
+    // join): after the last step the first group of the next stage is read
+    // all the same (in bounds, unused).
     constexpr int W_ALL = 0x70;                                                           // vmcnt(0) lgkmcnt(0)
     constexpr int W_IN = ((NS - 2) * LPS & 15) | (7 << 4) | (((NS - 2) * LPS >> 4) << 14);   // vmcnt((NS-2) LPS) lgkmcnt(0)
     constexpr int W_PRO = ((NS - 1) * LPS & 15) | (7 << 4) | (15 << 8) | (((NS - 1) * LPS >> 4) << 14);
     const int nk = K / T::BK;
 #pragma unroll
-    for (int j = 0; j < NS; ++j)
-        if (j < nk) load(j, j);
-    if (nk >= NS) __builtin_amdgcn_s_waitcnt(W_PRO);   // step 0's loads: the oldest NS - 1 ... 0 pending
-    else __builtin_amdgcn_s_waitcnt(W_ALL);
+    for (int j = 0; j < NS; ++j) load(min(j, nk - 1), j);
+    __builtin_amdgcn_s_waitcnt(W_PRO);   // step 0's loads in: the newer NS - 1 stages pending
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     rd(lds, 0, fa[0], fb[0]);
@@ -660,15 +689,14 @@ __global__ __launch_bounds__(T::NT) void mfma_bgemm_kernel(
         }
         if (k + 1 < nk) {
             // step k + 1's loads are in (steps k + 2 .. k + NS - 1 may be pending)
-            if (k + NS - 1 < nk) __builtin_amdgcn_s_waitcnt(W_IN);
-            else __builtin_amdgcn_s_waitcnt(W_ALL);
+            __builtin_amdgcn_s_waitcnt(W_IN);
             __builtin_amdgcn_s_barrier();
             asm volatile("" ::: "memory");
-            if (k + NS < nk) load(k + NS, st);
         }
-        phase(fa[1], fb[1], lds + sn * ST, 0, fa[0], fb[0]);
+        phase_refill(fa[1], fb[1], lds + sn * ST, 0, fa[0], fb[0], min(k + NS, nk - 1), st);
         st = sn;
     }
+    __builtin_amdgcn_s_waitcnt(W_ALL);   // no load into LDS outlives the workgroup
 
     // Accumulator v of tile (j, i) holds row 32i + 8(v/4) + 4h + v%4 of the
     // wave's rows, weight row l32 of block j.
