@@ -869,7 +869,9 @@ int lds_cus();
 // back through agent-coherent loads) by 3-4% for the layer: O 134 against
 // 94 us, down 316 against 281 us (with agent-scope fences in the join
 // instead, which write back and invalidate the XCD's L2 under the workgroups
-// still computing: 207 and 382 us).
+// still computing: 207 and 382 us); an XCD-aware tile order (each XCD a run
+// of tiles, M fastest) and a ring of five 32-element half-steps (half the
+// loads leading by two steps) by 2-6% (stand-alone SwiGLU GEMM, cycle counts).
 template <class BBig, class BHalf, int EPI>
 void launch_bgemm_plan_t(hipStream_t s, const uint16_t* a, const DevWeight& w0, const DevWeight* w1, int M,
                          const float* residual, void* out) {
