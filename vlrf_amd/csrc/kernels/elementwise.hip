@@ -192,6 +192,47 @@ __global__ __launch_bounds__(256) void prefill_rope_append_kernel(
     store_row_to_cache(v, vq, vs, dtype, p, n_kv, D, max_seq, red);
 }
 
+// N consecutive floats (16-byte aligned when VEC).
+template <int N, bool VEC>
+__device__ __forceinline__ void load_run(const float* __restrict__ p, float (&o)[N]) {
+    if constexpr (VEC) {
+        static_assert(N % 4 == 0, "whole float4s");
+#pragma unroll
+        for (int i = 0; i < N / 4; ++i) {
+            const float4 a = reinterpret_cast<const float4*>(p)[i];
+            o[4 * i] = a.x; o[4 * i + 1] = a.y; o[4 * i + 2] = a.z; o[4 * i + 3] = a.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < N; ++i) o[i] = p[i];
+    }
+}
+
+// N consecutive elements of type E stored from e (as whole 4-, 8- or 16-byte
+// words when VEC: the run starts at a multiple of its own size, at most 16).
+template <int N, bool VEC, typename E>
+__device__ __forceinline__ void store_run(E* __restrict__ p, const E (&e)[N]) {
+    constexpr int B = N * (int)sizeof(E);
+    if constexpr (VEC && B % 4 == 0) {
+        uint32_t w[B / 4];
+        __builtin_memcpy(w, e, B);
+        if constexpr (B % 16 == 0) {
+#pragma unroll
+            for (int i = 0; i < B / 16; ++i)
+                reinterpret_cast<uint4*>(p)[i] = make_uint4(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]);
+        } else if constexpr (B % 8 == 0) {
+#pragma unroll
+            for (int i = 0; i < B / 8; ++i) reinterpret_cast<uint2*>(p)[i] = make_uint2(w[2 * i], w[2 * i + 1]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < B / 4; ++i) reinterpret_cast<uint32_t*>(p)[i] = w[i];
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < N; ++i) p[i] = e[i];
+    }
+}
+
 // The prefill's K/V rows with q left to its consumer: one wave per token (four
 // a workgroup), no LDS and no barrier.  Lane l holds PPL consecutive RoPE pairs
 // of one head (elements j and j + D/2, j = j0 .. j0 + PPL - 1) of the K row
@@ -199,8 +240,10 @@ __global__ __launch_bounds__(256) void prefill_rope_append_kernel(
 // buffer; RoPE as rope_pair, then per row the cache dtype's store as
 // store_row_to_cache (Q8_0: the row's amax by a wave max, the same scale,
 // reciprocal and rounding), as contiguous runs of PPL (K) and 2 PPL (V)
-// elements.  n_kv * D / 2 == 64 * PPL and (D / 2) % PPL == 0.
-template <int PPL>
+// elements.  n_kv * D / 2 == 64 * PPL and (D / 2) % PPL == 0.  VEC (PPL a
+// multiple of 4, every row and table 16-byte aligned, D % 16 == 0): the runs
+// are read as float4 and written as whole words; the same values either way.
+template <int PPL, bool VEC>
 __global__ __launch_bounds__(256) void prefill_kv_rows_kernel(
     int8_t* kq, int8_t* vq, float* ks, float* vs, int dtype, const float* __restrict__ qkv, int ld, int n_heads,
     int D, int max_seq, int pos0, int T, const float* __restrict__ cos_t, const float* __restrict__ sin_t) {
@@ -210,17 +253,15 @@ __global__ __launch_bounds__(256) void prefill_kv_rows_kernel(
     const int half = D / 2, pr = lane * PPL, h = pr / half, j0 = pr - h * half;
     const float* k = qkv + (size_t)t * ld + (size_t)n_heads * D;
     const float* v = k + (size_t)(64 * PPL * 2);          // the V row follows the K row (n_kv * D = 128 PPL)
-    float y0[PPL], y1[PPL], vv[2 * PPL];
+    float x0[PPL], x1[PPL], cr[PPL], sr[PPL], y0[PPL], y1[PPL], vv[2 * PPL];
+    load_run<PPL, VEC>(k + h * D + j0, x0);
+    load_run<PPL, VEC>(k + h * D + half + j0, x1);
+    load_run<PPL, VEC>(cos_t + (size_t)p * half + j0, cr);
+    load_run<PPL, VEC>(sin_t + (size_t)p * half + j0, sr);
+    load_run<2 * PPL, VEC>(v + 2 * PPL * lane, vv);
 #pragma unroll
-    for (int i = 0; i < PPL; ++i) {
-        const float x0 = k[h * D + j0 + i], x1 = k[h * D + half + j0 + i];
-        rope2v(x0, x1, cos_t[(size_t)p * half + j0 + i], sin_t[(size_t)p * half + j0 + i], &y0[i], &y1[i]);
-    }
-#pragma unroll
-    for (int i = 0; i < 2 * PPL; ++i) vv[i] = v[2 * PPL * lane + i];
+    for (int i = 0; i < PPL; ++i) rope2v(x0[i], x1[i], cr[i], sr[i], &y0[i], &y1[i]);
     const int vh = (2 * PPL * lane) / D, vd = 2 * PPL * lane - vh * D;
-    int8_t* krow = kq;
-    int8_t* vrow = vq;
     if (dtype == VLRF_HIP_KV_Q8_0) {
         auto quant = [](float x, float amax, float inv) -> int8_t {
             int q = 0;
@@ -239,36 +280,40 @@ __global__ __launch_bounds__(256) void prefill_kv_rows_kernel(
         av = wave_max(av);
         const float sk = ak != 0.f ? ak / 127.f : 0.f, sv = av != 0.f ? av / 127.f : 0.f;
         const float ik = ak != 0.f ? 1.f / sk : 0.f, iv = av != 0.f ? 1.f / sv : 0.f;
-        int8_t* kr = krow + ((size_t)h * max_seq + p) * D;
-        int8_t* vr = vrow + ((size_t)vh * max_seq + p) * D;
+        int8_t* kr = kq + ((size_t)h * max_seq + p) * D;
+        int8_t* vr = vq + ((size_t)vh * max_seq + p) * D;
+        int8_t c0[PPL], c1[PPL], cv[2 * PPL];
 #pragma unroll
         for (int i = 0; i < PPL; ++i) {
-            kr[j0 + i] = quant(y0[i], ak, ik);
-            kr[half + j0 + i] = quant(y1[i], ak, ik);
+            c0[i] = quant(y0[i], ak, ik);
+            c1[i] = quant(y1[i], ak, ik);
         }
 #pragma unroll
-        for (int i = 0; i < 2 * PPL; ++i) vr[vd + i] = quant(vv[i], av, iv);
+        for (int i = 0; i < 2 * PPL; ++i) cv[i] = quant(vv[i], av, iv);
+        store_run<PPL, VEC>(kr + j0, c0);
+        store_run<PPL, VEC>(kr + half + j0, c1);
+        store_run<2 * PPL, VEC>(vr + vd, cv);
         if (lane == 0) { ks[p] = sk; vs[p] = sv; }
     } else if (dtype == VLRF_HIP_KV_F16) {
-        uint16_t* kr = reinterpret_cast<uint16_t*>(krow) + ((size_t)h * max_seq + p) * D;
-        uint16_t* vr = reinterpret_cast<uint16_t*>(vrow) + ((size_t)vh * max_seq + p) * D;
+        uint16_t* kr = reinterpret_cast<uint16_t*>(kq) + ((size_t)h * max_seq + p) * D;
+        uint16_t* vr = reinterpret_cast<uint16_t*>(vq) + ((size_t)vh * max_seq + p) * D;
+        uint16_t c0[PPL], c1[PPL], cv[2 * PPL];
 #pragma unroll
         for (int i = 0; i < PPL; ++i) {
-            kr[j0 + i] = f32_to_f16_kv(y0[i]);
-            kr[half + j0 + i] = f32_to_f16_kv(y1[i]);
+            c0[i] = f32_to_f16_kv(y0[i]);
+            c1[i] = f32_to_f16_kv(y1[i]);
         }
 #pragma unroll
-        for (int i = 0; i < 2 * PPL; ++i) vr[vd + i] = f32_to_f16_kv(vv[i]);
+        for (int i = 0; i < 2 * PPL; ++i) cv[i] = f32_to_f16_kv(vv[i]);
+        store_run<PPL, VEC>(kr + j0, c0);
+        store_run<PPL, VEC>(kr + half + j0, c1);
+        store_run<2 * PPL, VEC>(vr + vd, cv);
     } else {
-        float* kr = reinterpret_cast<float*>(krow) + ((size_t)h * max_seq + p) * D;
-        float* vr = reinterpret_cast<float*>(vrow) + ((size_t)vh * max_seq + p) * D;
-#pragma unroll
-        for (int i = 0; i < PPL; ++i) {
-            kr[j0 + i] = y0[i];
-            kr[half + j0 + i] = y1[i];
-        }
-#pragma unroll
-        for (int i = 0; i < 2 * PPL; ++i) vr[vd + i] = vv[i];
+        float* kr = reinterpret_cast<float*>(kq) + ((size_t)h * max_seq + p) * D;
+        float* vr = reinterpret_cast<float*>(vq) + ((size_t)vh * max_seq + p) * D;
+        store_run<PPL, VEC>(kr + j0, y0);
+        store_run<PPL, VEC>(kr + half + j0, y1);
+        store_run<2 * PPL, VEC>(vr + vd, vv);
     }
 }
 
@@ -489,14 +534,17 @@ int launch_prefill_rope_append(hipStream_t s, const KVLayer& L, const float* qkv
     const int pairs = n_kv * d_head / 2, ppl = pairs / 64;
     if (pairs % 64 == 0 && (ppl == 1 || ppl == 2 || ppl == 4 || ppl == 8) && (d_head / 2) % ppl == 0) {
         const dim3 grid((T + 3) / 4);
-#define VH_KVR(P)                                                                                              \
-    hipLaunchKernelGGL(prefill_kv_rows_kernel<P>, grid, dim3(256), 0, s, L.k, L.v, L.ks, L.vs, L.dtype, qkv, ld, \
-                       n_heads, d_head, max_seq, pos0, T, cos_t, sin_t)
+        auto a16 = [](const void* ptr) { return ((uintptr_t)ptr & 15) == 0; };
+        const bool vec = ppl % 4 == 0 && ld % 4 == 0 && (n_heads * d_head) % 4 == 0 && d_head % 16 == 0 &&
+                         a16(qkv) && a16(cos_t) && a16(sin_t) && a16(L.k) && a16(L.v);
+#define VH_KVR(P, VEC)                                                                                          \
+    hipLaunchKernelGGL((prefill_kv_rows_kernel<P, VEC>), grid, dim3(256), 0, s, L.k, L.v, L.ks, L.vs, L.dtype,   \
+                       qkv, ld, n_heads, d_head, max_seq, pos0, T, cos_t, sin_t)
         switch (ppl) {
-            case 1: VH_KVR(1); break;
-            case 2: VH_KVR(2); break;
-            case 4: VH_KVR(4); break;
-            default: VH_KVR(8); break;
+            case 1: VH_KVR(1, false); break;
+            case 2: VH_KVR(2, false); break;
+            case 4: if (vec) VH_KVR(4, true); else VH_KVR(4, false); break;
+            default: if (vec) VH_KVR(8, true); else VH_KVR(8, false); break;
         }
 #undef VH_KVR
         VH_LAUNCHED();
