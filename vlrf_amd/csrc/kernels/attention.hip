@@ -570,6 +570,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
 // the lane's own accumulators, and P re-enters the second product through the
 // same register exchange.
 constexpr int kPQ = 32, kPK = 64;         // queries per wave, keys per tile
+constexpr float kLazy = 8.f;              // log2 headroom of the prefill softmax's reference max
 
 // Raw cache elements of one staging item (16 consecutive elements of one key
 // row, K and V) held in registers between their load and the LDS store.
@@ -769,6 +770,10 @@ __global__ __launch_bounds__(512) void attn_prefill_kernel(
             }
             // Online softmax in base 2: exp(s*scale - m) = 2^(s*scale*log2(e) - m'),
             // the max taken on raw scores (scale > 0); masked scores give 2^-inf = 0.
+            // The reference point m_run moves only when a tile's max passes it by
+            // more than kLazy (so p <= 2^kLazy, exact in f32 and bf16 range): the
+            // rescale of l and O by 2^(m_old - m_new) is then rare, and skipped
+            // by the whole wave when no lane moved (the result is the same ratio).
             float mx = kNegInf;
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
@@ -778,8 +783,10 @@ __global__ __launch_bounds__(512) void attn_prefill_kernel(
                 const float2 t = half_swap(mx, mx);    // [lo, lo], [hi, hi]
                 mx = fmaxf(t.x, t.y);
             }
-            const float mn = fmaxf(m_run, mx * sl2); // finite: key 0 is in the first tile
-            const float corr = __builtin_amdgcn_exp2f(m_run - mn);   // 0 on the first tile
+            const float mt = mx * sl2;
+            const bool grow = mt > m_run + kLazy;    // always on the first tile (key 0 is in it)
+            const float mn = grow ? mt : m_run;
+            const float corr = grow ? __builtin_amdgcn_exp2f(m_run - mn) : 1.f;   // 0 on the first tile
             float sum = 0.f;
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
@@ -795,10 +802,12 @@ __global__ __launch_bounds__(512) void attn_prefill_kernel(
             }
             l_run = l_run * corr + sum;
             m_run = mn;
+            if (__builtin_amdgcn_ballot_w64(grow)) {
 #pragma unroll
-            for (int c = 0; c < D / 32; ++c)
+                for (int c = 0; c < D / 32; ++c)
 #pragma unroll
-                for (int v = 0; v < 16; ++v) o[c][v] *= corr;
+                    for (int v = 0; v < 16; ++v) o[c][v] *= corr;
+            }
 
             // O^T += V^T . P^T, 16 keys per step.  The B operand of lane (hh, q)
             // needs keys 16s + 8hh + e: v-group 2s+hh, elements 0..3 from lane
