@@ -34,6 +34,15 @@
 namespace vlrf_hip {
 namespace {
 
+// silu(g) * u (ops.hpp:409-441: g / (1 + exp(-g)) times u) for the bf16-class
+// GEMM epilogues: the hardware exp2 and reciprocal (about 1 ulp each) instead
+// of the library expf and the correctly rounded division, whose extra
+// instructions sat in every tile's epilogue.  g -> -inf gives -0 as the
+// division does; the f32-class paths keep the exact form.
+__device__ __forceinline__ float silu_mul_fast(float g, float u) {
+    return u * (g * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(g * -1.4426950408889634f)));
+}
+
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -216,7 +225,7 @@ __global__ __launch_bounds__(C::NT) void mfma_qgemm_kernel(
                     const size_t o = (size_t)row * N + col;
                     if constexpr (EPI >= 2) {
                         const float g = acc[0][i][j][v], u = acc[1][i][j][v];
-                        const float hv = u * (g / (1.f + expf(-g)));   // silu(g) * u, ops.hpp:409-441
+                        const float hv = silu_mul_fast(g, u);
                         if constexpr (EPI == 2) reinterpret_cast<uint16_t*>(out)[o] = (uint16_t)bf16_bits(hv);
                         else reinterpret_cast<float*>(out)[o] = hv;
                     } else if constexpr (EPI == 1) {
@@ -346,7 +355,7 @@ __device__ __forceinline__ void store_tile(const f32x16 (&acc)[NM][ATile<BM>::MI
                 const size_t o = (size_t)row * ldo + col;
                 if constexpr (EPI >= 2) {
                     const float g = acc[0][i][v], u = acc[NM - 1][i][v];
-                    const float hv = u * (g / (1.f + expf(-g)));   // silu(g) * u, ops.hpp:409-441
+                    const float hv = silu_mul_fast(g, u);
                     if constexpr (EPI == 2) reinterpret_cast<uint16_t*>(out)[o] = (uint16_t)bf16_bits(hv);
                     else reinterpret_cast<float*>(out)[o] = hv;
                 } else if constexpr (EPI == 1) {
@@ -713,7 +722,7 @@ __global__ __launch_bounds__(T::NT) void mfma_bgemm_kernel(
                     if (col < N) {
                         const size_t o = (size_t)row * ldo + col;
                         const float g = acc[j][i][v], u = acc[j + NB / 2][i][v];
-                        const float hv = u * (g / (1.f + expf(-g)));   // silu(g) * u, ops.hpp:409-441
+                        const float hv = silu_mul_fast(g, u);
                         if constexpr (EPI == 2) reinterpret_cast<uint16_t*>(out)[o] = (uint16_t)bf16_bits(hv);
                         else reinterpret_cast<float*>(out)[o] = hv;
                     }
