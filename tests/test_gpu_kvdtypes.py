@@ -149,3 +149,33 @@ def test_prefill_mfma_then_decode(ctx, orc, dtype):
         _, gl = m.step(tok, want_logits=True)
         tok, ol = om.forward([tok], want_logits=True)
         assert rel_err(gl, ol) <= 1e-2
+
+
+@pytest.mark.parametrize("kv_dtype", [V.KV_Q8_0, V.KV_F16, V.KV_F32])
+@pytest.mark.parametrize("n_heads,n_kv,d_model", [(8, 4, 1024), (8, 8, 1024), (4, 4, 256)])
+def test_prefill_append_vector_path_equals_element_path(ctx, monkeypatch, kv_dtype, n_heads, n_kv, d_model):
+    """The prefill's K/V append reads its runs as float4 and writes them as whole
+    words where rows and tables are aligned (4 and 8 RoPE pairs a lane: 512 and
+    1024 K elements a row); VLRF_HIP_KV_VEC=0 keeps the element-wise loads and
+    stores.  The same prefill either way leaves the same cache bit for bit, for
+    every cache type (the 2-pair shape takes the element path both times)."""
+    cfg = dict(F.tiny(V.DT_Q8_0, n_layers=1, max_seq_len=96), n_heads=n_heads, n_kv_heads=n_kv,
+               d_model=d_model, d_ff=2 * d_model, kv_dtype=kv_dtype)
+    print(f"[case] prefill append vec/element heads={n_heads}/{n_kv} d={d_model} kv={kv_dtype}", flush=True)
+    m = V.Model(ctx, cfg)
+    F.load_model(m, 53)
+    T = 70
+    x = ctx.to_device(F.normal(53, "kvvec", T * d_model))
+    caches = []
+    for flag in ("1", "0"):
+        monkeypatch.setenv("VLRF_HIP_KV_VEC", flag)
+        m.reset()
+        m.forward_hidden(x)
+        caches.append(m.kv_rows(0, 0, T))
+    for a, b in zip(*caches):
+        if a is None:
+            assert b is None
+        else:
+            assert np.array_equal(a, b)
+    kq = caches[0][0]
+    assert np.any(kq != 0)

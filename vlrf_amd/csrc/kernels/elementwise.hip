@@ -3,6 +3,8 @@
 // greedy argmax.
 #include "../internal.hpp"
 
+#include <cstdlib>
+
 #include <cmath>
 
 namespace vlrf_hip {
@@ -535,8 +537,9 @@ int launch_prefill_rope_append(hipStream_t s, const KVLayer& L, const float* qkv
     if (pairs % 64 == 0 && (ppl == 1 || ppl == 2 || ppl == 4 || ppl == 8) && (d_head / 2) % ppl == 0) {
         const dim3 grid((T + 3) / 4);
         auto a16 = [](const void* ptr) { return ((uintptr_t)ptr & 15) == 0; };
-        const bool vec = ppl % 4 == 0 && ld % 4 == 0 && (n_heads * d_head) % 4 == 0 && d_head % 16 == 0 &&
-                         a16(qkv) && a16(cos_t) && a16(sin_t) && a16(L.k) && a16(L.v);
+        const char* e = std::getenv("VLRF_HIP_KV_VEC");   // "0": element-wise loads and stores (same values)
+        const bool vec = !(e && e[0] == '0') && ppl % 4 == 0 && ld % 4 == 0 && (n_heads * d_head) % 4 == 0 &&
+                         d_head % 16 == 0 && a16(qkv) && a16(cos_t) && a16(sin_t) && a16(L.k) && a16(L.v);
 #define VH_KVR(P, VEC)                                                                                          \
     hipLaunchKernelGGL((prefill_kv_rows_kernel<P, VEC>), grid, dim3(256), 0, s, L.k, L.v, L.ks, L.vs, L.dtype,   \
                        qkv, ld, n_heads, d_head, max_seq, pos0, T, cos_t, sin_t)
