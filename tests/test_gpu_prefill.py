@@ -225,3 +225,45 @@ def test_new_weights_after_a_prefill_replace_the_bf16_expansion(ctx, dtype):
     F.load_model(fresh, 42, norm_std=0.1)
     ref = fresh.forward_hidden(ctx.to_device(x)).download((T, D))
     assert np.array_equal(got, ref)
+
+
+def test_prefill_attention_score_jumps_rescale(ctx):
+    """Scores that jump far past the running max at a later key tile: the
+    prefill softmax keeps a reference max and rescales O and l only when a
+    tile's max passes it by more than 2^8, so this case must take that path
+    (factor ~2^-23) and still compute the intended arithmetic.  Rows from
+    position 70 on carry a large component along input dim 0, which q_proj and
+    k_proj map onto the lowest-frequency RoPE pair of every head (dims 31 and
+    63: the rotation between positions < 150 apart is ~2e-2 rad), so the
+    scores of those rows against each other are ~16 above all others (~23 in
+    log2 units).  Scores that large also magnify the bf16 rounding of q and K
+    (about 2^-9 of a score of 20), so the reference is the float64 model of
+    the bf16 scheme, which rounds q and K the same way, at its 1e-3 bound; the
+    rows before the jump are also checked against the f32 oracle."""
+    import bf16_layer_ref as B
+    cfg = F.tiny(V.DT_Q8_0, n_layers=1, max_seq_len=192)
+    print("[case] prefill attention: score jump past the lazy rescale bound", flush=True)
+    m = V.Model(ctx, cfg)
+    w = F.load_model(m, 57, want_f32=True, norm_std=0.0)
+    D, H, G = cfg["d_model"], cfg["n_heads"], cfg["n_kv_heads"]
+    dh = D // H
+    for name, heads in (("attn.q_proj.weight", H), ("attn.k_proj.weight", G)):
+        full = "layers.0." + name
+        wt = w[full].copy()
+        for hd in range(heads):
+            wt[hd * dh + 31, 0] += 0.7           # dims 31 and 63 of the head: RoPE pair 31
+            wt[hd * dh + 63, 0] += 0.7
+        blocks = F.quantize(wt, V.DT_Q8_0)
+        m.set_weight(full, blocks, V.DT_Q8_0, wt.shape[0], wt.shape[1])
+        w[full] = F.dequantize(blocks, V.DT_Q8_0, wt.size).reshape(wt.shape)
+    om = oracle.Model(cfg, w, n_threads=8)
+    T = 150
+    x = F.normal(57, "jump", T * D).reshape(T, D)
+    x[70:, 0] += 24.0
+    got = m.forward_hidden(ctx.to_device(x)).download((T, D))
+    emu, _, _ = B.layer(x, w, cfg)
+    ne = norm_err(got[70:] - x[70:], emu[70:] - x[70:])
+    print(f"  rows 70-149 (after the jump) vs the bf16 model: normwise {ne:.2e}", flush=True)
+    assert ne <= TOL_EMU, ne
+    ref = om.forward_hidden(x)
+    check(got[:70] - x[:70], ref[:70] - x[:70], "layer update, rows 0-69")
