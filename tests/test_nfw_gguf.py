@@ -107,6 +107,8 @@ def test_nfw_rejects_bad_files(tmp_path):
         "negative_dim": one((-4, -8), 32, payload=bytes(128)),
         "dims_overflow": one((2**31 - 1,) * 3, 0),
         "numel_beyond_file": one((1 << 20,), 1 << 20, payload=bytes(64)),
+        "negative_numel": one((), -(1 << 61)),                        # numel * 4 would overflow int64
+        "negative_numel_f16": one((), -3, dtype=1, payload=bytes(8)),
     })
     for name, data in cases.items():
         p = tmp_path / f"{name}.nfw"

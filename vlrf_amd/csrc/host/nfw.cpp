@@ -161,6 +161,10 @@ static int nfw_open(const char* path, vlrf_nfw_t* out) {
             // first keeps the size products below in range.
             const int64_t left = size - std::ftell(f.f);
             if (e.numel > 2 * left) goto truncated;
+            if (e.numel < 0) {   // before any size product: a negative count must not reach one
+                set_error("nfw_open: tensor '%s' has a negative element count", e.name.c_str());
+                return VLRF_HIP_ERR_ARG;
+            }
             int64_t prod = 1;
             bool dims_ok = true;
             for (int d = 0; d < nd && dims_ok; ++d)
