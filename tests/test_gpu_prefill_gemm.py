@@ -91,25 +91,35 @@ def test_prefill_swiglu_ragged(ctx, orc, dtype, M, Fd, K):
     assert rel_err(dh.download((M, Fd)), ref) <= TOL
 
 
-def _both_forms(monkeypatch, run):
-    """run() with the weights' bf16 expansion (the default for M > 128) and with
-    VLRF_HIP_PREFILL_BF16=0 (codes decoded in registers)."""
+def _all_forms(monkeypatch, run):
+    """run() with the weights' bf16 expansion (the default for M > 128), with
+    VLRF_HIP_PREFILL_BF16=0 (Q8_0 with K % 128 == 0: codes decoded into LDS
+    tiles, once per workgroup; otherwise in registers) and with
+    VLRF_HIP_PREFILL_DQ=0 as well (codes decoded in registers)."""
     monkeypatch.delenv("VLRF_HIP_PREFILL_BF16", raising=False)
+    monkeypatch.delenv("VLRF_HIP_PREFILL_DQ", raising=False)
     a = run()
     monkeypatch.setenv("VLRF_HIP_PREFILL_BF16", "0")
     b = run()
+    monkeypatch.setenv("VLRF_HIP_PREFILL_DQ", "0")
+    c = run()
     monkeypatch.delenv("VLRF_HIP_PREFILL_BF16", raising=False)
-    return a, b
+    monkeypatch.delenv("VLRF_HIP_PREFILL_DQ", raising=False)
+    return a, b, c
 
 
 @pytest.mark.parametrize("dtype", [V.DT_Q8_0, V.DT_Q4_0])
 # 256x128 tiles (1000 x 1024), wide 256x256 tiles (2048 x 6144), a ragged
-# wide edge (520 x 16600), the residual form (300 x 4096 x 2048)
+# wide edge (520 x 16600), the residual form (300 x 4096 x 2048), ragged rows
+# and columns on the LDS-decode tiles (257 x 1000 x 256, 129 x 130 x 128, 300 x 100 x 384)
 @pytest.mark.parametrize("M,N,K,res", [(1000, 1024, 512, False), (2048, 6144, 256, False),
-                                       (520, 16600, 64, False), (300, 4096, 2048, True)])
+                                       (520, 16600, 64, False), (300, 4096, 2048, True),
+                                       (257, 1000, 256, False), (129, 130, 128, True),
+                                       (300, 100, 384, True)])
 def test_bf16_expansion_equals_in_register_decode(ctx, monkeypatch, dtype, M, N, K, res):
     """The GEMM over the weights' bf16 expansion multiplies the operands the
-    in-register decode forms, in the same MFMA order: bit-identical outputs."""
+    in-register and in-LDS decodes form, in the same MFMA order: bit-identical
+    outputs."""
     print(f"[case] bf16 expansion dtype={dtype} M={M} N={N} K={K} res={res}", flush=True)
     x = F.normal(24, f"bx{M}x{K}", M * K).reshape(M, K)
     r = F.normal(24, f"br{M}x{N}", M * N).reshape(M, N)
@@ -121,14 +131,14 @@ def test_bf16_expansion_equals_in_register_decode(ctx, monkeypatch, dtype, M, N,
         ctx.qlinear(w, dx, dy, M, residual=dy if res else None)
         return dy.download((M, N))
 
-    a, b = _both_forms(monkeypatch, run)
-    assert np.array_equal(a, b)
+    a, b, c = _all_forms(monkeypatch, run)
+    assert np.array_equal(a, b) and np.array_equal(a, c)
 
 
 @pytest.mark.parametrize("dtype", [V.DT_Q8_0, V.DT_Q4_0])
 # 2048 x 14336: 112 x 8 tiles of 256 x 128, the last round (128 columns x 8)
 # as 128-row tiles over columns 12288..14335 (two launches)
-@pytest.mark.parametrize("M,Fd,K", [(2048, 14336, 128), (257, 1000, 192)])
+@pytest.mark.parametrize("M,Fd,K", [(2048, 14336, 128), (257, 1000, 192), (257, 1000, 256), (600, 136, 512)])
 def test_bf16_expansion_swiglu_equals_in_register_decode(ctx, monkeypatch, dtype, M, Fd, K):
     print(f"[case] bf16 expansion swiglu dtype={dtype} M={M} F={Fd} K={K}", flush=True)
     x = F.normal(25, f"sx{M}x{K}", M * K).reshape(M, K)
@@ -141,8 +151,8 @@ def test_bf16_expansion_swiglu_equals_in_register_decode(ctx, monkeypatch, dtype
         ctx.qlinear_swiglu(wg, wu, dx, dh, M)
         return dh.download((M, Fd))
 
-    a, b = _both_forms(monkeypatch, run)
-    assert np.array_equal(a, b)
+    a, b, c = _all_forms(monkeypatch, run)
+    assert np.array_equal(a, b) and np.array_equal(a, c)
 
 
 def test_bf16_expansion_is_counted_in_the_weight_bytes(ctx):

@@ -741,6 +741,277 @@ __global__ __launch_bounds__(T::NT) void mfma_bgemm_kernel(
         }
 }
 
+// The same GEMM over Q8_0 codes, dequantized into LDS tiles: A is staged by
+// direct-to-LDS loads in a two-stage ring as above; the weight tile of each K
+// step is loaded as codes into registers (thread t: row t / TPR, the codes
+// of part t % TPR of the row's 64 and their f16 scale), decoded there to
+// bf16(code * scale) -- the conversion of the bf16 expansion -- and written
+// into one of two bf16 tile buffers laid out (and swizzled) as the ring's
+// weight stage, so the MFMA phases are the bf16 kernel's, on the same
+// operands in the same order: results equal the bf16-expansion GEMM's bit for
+// bit.  Each code is decoded once per workgroup.
+//
+// Step k decodes tile k + 1 into the buffer step k - 1 read, under its first
+// two groups' MFMAs (five to ten VALU instructions after each).  The codes of
+// tile k + 1 were loaded at the end of step k - 2, with A of step k, into the
+// register set (k + 1) % 2 (the loop is unrolled by two steps); the codes of
+// step k + 3 follow A of step k + 2 at the end of step k.  The code loads are
+// issued from inline assembly, so the compiler places no wait of its own for
+// them (its count would hold up the A loads issued after them too): step k
+// waits for its codes with A of step k + 1 and the codes of step k + 2 still
+// in flight (vmcnt(A_IT + LW)), its barrier for A of step k + 1 with the
+// codes of step k + 2 in flight (vmcnt(LW)).  With the decode under one
+// group's MFMAs and the codes loaded one step later (the compiler's waits)
+// the 8B layer ran 1.23 against 1.12 ms for the in-register decode; as here,
+// 1.05 ms.
+template <class T, int EPI, int NSA>
+__global__ __launch_bounds__(T::NT) void mfma_dqgemm_kernel(
+    const uint16_t* __restrict__ A, const uint8_t* __restrict__ qa, const __half* __restrict__ da,
+    const uint8_t* __restrict__ qb, const __half* __restrict__ db, int M, int N, int K, int ldo,
+    const float* __restrict__ residual, void* __restrict__ out) {
+    using lds_gemm::dma16;
+    using lds_gemm::lds_addr;
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    constexpr int MI = T::MI, NB = T::NB, WM = T::WM, WNR = T::WNR, BN = T::BN;
+    constexpr int A_B = T::A_B, NW = T::NW, RB = T::RB, CPR = T::CPR, RPL = T::RPL;
+    constexpr int W_B = BN * RB;
+    constexpr bool SWIGLU = EPI >= 2;
+    constexpr int TPR = T::NT / BN;              // threads per weight row
+    constexpr int CPT = 64 / TPR;                // codes per thread and K step
+    constexpr int NQ = CPT / 16, NC = CPT / 8;   // its 16-byte loads, 8-code chunks
+    constexpr int LW = NQ + 1;                   // loads per code set (the codes, the scale)
+    static_assert(T::BK == 64 && T::NG == 4 && T::NT % BN == 0 && (TPR == 2 || TPR == 4), "code split");
+    static_assert(NSA >= 2 && NSA * A_B + 2 * W_B <= 160 * 1024, "LDS");
+    // Loads in flight at each wait (step j ends with A of step j + NSA, then
+    // the codes of step j + 3): at step k's start the codes of step k + 1 are
+    // in with the last step's pair pending; at its barrier A of step k + 1,
+    // with the codes of step k + 1 (NSA > 2) and NSA - 2 later pairs pending;
+    // at the prologue's barrier A of step 0, with everything after it pending.
+    constexpr int VM_CODES = T::A_IT + LW;
+    constexpr int VM_BAR = LW + (NSA - 2) * (T::A_IT + LW);
+    constexpr int VM_PRO = (NSA - 1) * T::A_IT + 2 * LW;
+    static_assert(VM_PRO < 16 && VM_BAR < 16, "vmcnt immediates in four bits");
+    constexpr int W_BAR = VM_BAR | (7 << 4);                  // lgkmcnt(0) too: W writes and reads done
+    constexpr int W_PRO = VM_PRO | (7 << 4) | (15 << 8);
+    __shared__ __align__(16) uint8_t lds[NSA * A_B + 2 * W_B];
+    const int lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave / T::WC, wn = wave % T::WC;
+    const int m0 = blockIdx.y * T::BM;
+    const int n0 = blockIdx.x * (SWIGLU ? BN / 2 : BN);   // first output column
+
+    const char* ga[T::A_IT];
+#pragma unroll
+    for (int it = 0; it < T::A_IT; ++it) {
+        const int r = (it * NW + wave) * RPL + lane / CPR, c = (lane % CPR) ^ T::swz(r);
+        ga[it] = reinterpret_cast<const char*>(A + (size_t)min(m0 + r, M - 1) * K + c * 8);
+    }
+    const uint32_t base = lds_addr(lds);
+    auto load_a = [&](int kt, int buf) {
+        const uint32_t sa = base + buf * A_B;
+#pragma unroll
+        for (int it = 0; it < T::A_IT; ++it) dma16(ga[it] + (size_t)kt * RB, sa + (it * NW + wave) * 1024);
+    };
+    // This thread's codes: tile row wr, part pt of each K step's 64 (CPT
+    // codes from byte CPT pt; block 2 kt + CPT pt / 32 of the row).
+    const int wr = threadIdx.x / TPR, pt = threadIdx.x % TPR;
+    const bool wup = SWIGLU && wr >= BN / 2;
+    const int gnr = min(n0 + (wup ? wr - BN / 2 : wr), N - 1);
+    const uint8_t* qrow = (wup ? qb : qa) + (size_t)gnr * K + CPT * pt;
+    const __half* drow = (wup ? db : da) + (size_t)gnr * (K / 32) + CPT * pt / 32;
+    int woff[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) woff[c] = NSA * A_B + wr * RB + 16 * ((NC * pt + c) ^ T::swz(wr));
+    // Register sets: NQ 16-byte code loads and the scale (zero-extended).
+    u32x4 cq0[NQ], cq1[NQ];
+    uint32_t cs0, cs1;
+    auto load_w = [&](int kt, u32x4 (&q)[NQ], uint32_t& d) {
+        const uint8_t* p = qrow + (size_t)kt * 64;
+        const __half* ps = drow + 2 * kt;
+        asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(q[0]) : "v"(p));
+        if constexpr (NQ == 2) asm volatile("global_load_dwordx4 %0, %1, off offset:16" : "=v"(q[NQ - 1]) : "v"(p));
+        asm volatile("global_load_ushort %0, %1, off" : "=v"(d) : "v"(ps));
+    };
+    // Wait until at most N vector-memory operations are pending; the set's
+    // registers pass through the statement, so no use of them precedes it.
+    auto wait_w = [&](u32x4 (&q)[NQ], uint32_t& d, auto n) {
+        if constexpr (NQ == 2)
+            asm volatile("s_waitcnt vmcnt(%3)" : "+v"(q[0]), "+v"(q[NQ - 1]), "+v"(d) : "n"(decltype(n)::value));
+        else
+            asm volatile("s_waitcnt vmcnt(%2)" : "+v"(q[0]), "+v"(d) : "n"(decltype(n)::value));
+    };
+    // Chunks c0 .. c1 - 1 (8 codes each) of the thread's codes -> bf16 (the
+    // expansion's conversion), into W buffer wb.
+    auto store_w = [&](const u32x4 (&q)[NQ], uint32_t d, int wb, int c0, int c1) {
+        const float sc = __half2float(__ushort_as_half((unsigned short)d));
+#pragma unroll
+        for (int c = c0; c < c1; ++c) {
+            bf16x8 v;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = (__bf16)((float)(int8_t)(q[c >> 1][2 * (c & 1) + (e >> 2)] >> (8 * (e & 3))) * sc);
+            *reinterpret_cast<bf16x8*>(lds + woff[c] + wb * W_B) = v;
+        }
+    };
+
+    f32x16 acc[NB][MI];
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int i = 0; i < MI; ++i) acc[b][i] = f32x16{};
+
+    const int sw = T::swz(l32);
+    const int a_off = (wm * WM + l32) * RB;
+    const int b_off = NSA * A_B + ((SWIGLU ? wn * (WNR / 2) : wn * WNR) + l32) * RB;
+    auto boff = [](int b) {
+        return SWIGLU ? ((b < NB / 2 ? 0 : BN / 2) + 32 * (b % (NB / 2))) * RB : 32 * b * RB;
+    };
+    bf16x8 fa[2][MI], fb[2][NB];
+    // group g of the step in A stage sa, W buffer wb
+    auto rd = [&](int sa, int wb, int g, bf16x8 (&a)[MI], bf16x8 (&b)[NB]) {
+        const int x = 16 * ((2 * (2 * (g >> 1) + h) + (g & 1)) ^ sw);
+        const uint8_t* pa = lds + sa * A_B + a_off + x;
+        const uint8_t* pb = lds + wb * W_B + b_off + x;
+#pragma unroll
+        for (int i = 0; i < MI; ++i) a[i] = *reinterpret_cast<const bf16x8*>(pa + i * 32 * RB);
+#pragma unroll
+        for (int j = 0; j < NB; ++j) b[j] = *reinterpret_cast<const bf16x8*>(pb + boff(j));
+    };
+    auto mm = [&](const bf16x8 (&a)[MI], const bf16x8 (&b)[NB]) {
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+#pragma unroll
+            for (int i = 0; i < MI; ++i)
+                acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[j][i], 0, 0, 0);
+    };
+    constexpr int NR = MI + NB, NMF = MI * NB;
+    auto phase = [&](const bf16x8 (&a)[MI], const bf16x8 (&b)[NB], int sa, int wb, int g, bf16x8 (&na)[MI],
+                     bf16x8 (&nb)[NB]) {
+        mm(a, b);
+        rd(sa, wb, g, na, nb);
+#pragma unroll
+        for (int i = 0; i < NMF; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);              // one MFMA
+            if (i < NR) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // one LDS read
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // A phase with chunks c0 .. c1 - 1 of the next tile's decode spread over its MFMAs.
+    constexpr int DQ_V = (20 * (NC / 2) + NMF - 1) / NMF;   // decode VALU per MFMA (about 20 per chunk)
+    auto phase_dq = [&](const bf16x8 (&a)[MI], const bf16x8 (&b)[NB], int sa, int wb, int g, bf16x8 (&na)[MI],
+                        bf16x8 (&nb)[NB], const u32x4 (&q)[NQ], uint32_t d, int wnext, int c0, int c1) {
+        mm(a, b);
+        rd(sa, wb, g, na, nb);
+        store_w(q, d, wnext, c0, c1);
+#pragma unroll
+        for (int i = 0; i < NMF; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);              // one MFMA
+            if (i < NR) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // one LDS read
+            __builtin_amdgcn_sched_group_barrier(0x002, DQ_V, 0);           // decode VALU
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // After a step's barrier: the last group's MFMAs, the next step's first
+    // reads, and the refill (A of step kta into stage sa_fill, spread over the
+    // MFMAs, then the codes of step ktw into the register set given).
+    constexpr int PER = (T::A_IT + NMF - 1) / NMF;
+    auto phase_refill = [&](const bf16x8 (&a)[MI], const bf16x8 (&b)[NB], int sa, int wb, bf16x8 (&na)[MI],
+                            bf16x8 (&nb)[NB], int kta, int sa_fill, int ktw, u32x4 (&q)[NQ], uint32_t& d) {
+        const int x = 16 * ((2 * h) ^ sw);
+        const uint8_t* pa = lds + sa * A_B + a_off + x;
+        const uint8_t* pb = lds + wb * W_B + b_off + x;
+        const uint32_t sfa = base + sa_fill * A_B;
+#pragma unroll
+        for (int j = 0, n = 0; j < NB; ++j)
+#pragma unroll
+            for (int i = 0; i < MI; ++i, ++n) {
+                acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[j][i], 0, 0, 0);
+                if (n < MI) na[n] = *reinterpret_cast<const bf16x8*>(pa + n * 32 * RB);
+                else if (n < NR) nb[n - MI] = *reinterpret_cast<const bf16x8*>(pb + boff(n - MI));
+#pragma unroll
+                for (int l = n * PER; l < (n + 1) * PER && l < T::A_IT; ++l)
+                    dma16(ga[l] + (size_t)kta * RB, sfa + (l * NW + wave) * 1024);
+                if (n == NMF - 1) load_w(ktw, q, d);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+    };
+
+    // Prologue, so that every step finds the same loads in flight: codes 0
+    // (decoded into W buffer 0), then A 0 .. NSA - 3, and the pairs (A
+    // NSA - 2, codes 1), (A NSA - 1, codes 2).
+    const int nk = K / T::BK;
+    load_w(0, cq0, cs0);
+    wait_w(cq0, cs0, std::integral_constant<int, 0>{});
+    store_w(cq0, cs0, 0, 0, NC);
+#pragma unroll
+    for (int j = 0; j < NSA - 2; ++j) load_a(min(j, nk - 1), j);
+    load_a(min(NSA - 2, nk - 1), NSA - 2);
+    load_w(min(1, nk - 1), cq1, cs1);
+    load_a(min(NSA - 1, nk - 1), NSA - 1);
+    load_w(min(2, nk - 1), cq0, cs0);
+    __builtin_amdgcn_s_waitcnt(W_PRO);
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0) alone: the tile's LDS writes done
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    rd(0, 0, 0, fa[0], fb[0]);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // Step k: A stage k % NSA (st), W buffer k % 2; decodes the codes of step
+    // k + 1 (set qn) into W buffer (k + 1) % 2; set qn then takes the codes of
+    // step k + 3, A stage st A of step k + NSA.
+    int st = 0;
+    auto step = [&](int k, u32x4 (&qn)[NQ], uint32_t& dn) {
+        const int s = k & 1, s1 = s ^ 1, sn = st + 1 == NSA ? 0 : st + 1;
+        wait_w(qn, dn, std::integral_constant<int, VM_CODES>{});
+        phase_dq(fa[0], fb[0], st, s, 1, fa[1], fb[1], qn, dn, s1, 0, NC / 2);
+        phase_dq(fa[1], fb[1], st, s, 2, fa[0], fb[0], qn, dn, s1, NC / 2, NC);
+        phase(fa[0], fb[0], st, s, 3, fa[1], fb[1]);
+        __builtin_amdgcn_s_waitcnt(W_BAR);   // A of step k + 1 in; W writes and reads done
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        phase_refill(fa[1], fb[1], sn, s1, fa[0], fb[0], min(k + NSA, nk - 1), st, min(k + 3, nk - 1), qn, dn);
+        st = sn;
+    };
+    for (int k = 0; k < nk; k += 2) {
+        step(k, cq1, cs1);
+        step(k + 1, cq0, cs0);
+    }
+    wait_w(cq0, cs0, std::integral_constant<int, 0>{});   // nothing outlives the workgroup
+    wait_w(cq1, cs1, std::integral_constant<int, 0>{});
+
+    // Accumulator v of tile (j, i) holds row 32i + 8(v/4) + 4h + v%4 of the
+    // wave's rows, weight row l32 of block j.
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int row = m0 + wm * WM + 32 * i + 8 * (v >> 2) + 4 * h + (v & 3);
+            if (row >= M) continue;
+            if constexpr (SWIGLU) {
+#pragma unroll
+                for (int j = 0; j < NB / 2; ++j) {
+                    const int col = n0 + wn * (WNR / 2) + 32 * j + l32;
+                    if (col < N) {
+                        const size_t o = (size_t)row * ldo + col;
+                        const float g = acc[j][i][v], u = acc[j + NB / 2][i][v];
+                        const float hv = silu_mul_fast(g, u);
+                        if constexpr (EPI == 2) reinterpret_cast<uint16_t*>(out)[o] = (uint16_t)bf16_bits(hv);
+                        else reinterpret_cast<float*>(out)[o] = hv;
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < NB; ++j) {
+                    const int col = n0 + wn * WNR + 32 * j + l32;
+                    if (col < N) {
+                        const size_t o = (size_t)row * ldo + col;
+                        if constexpr (EPI == 1) reinterpret_cast<float*>(out)[o] = acc[j][i][v] + residual[o];
+                        else reinterpret_cast<float*>(out)[o] = acc[j][i][v];
+                    }
+                }
+            }
+        }
+}
+
 // bf16 expansion of Q8_0 / Q4_0 rows, a quarter block (8 elements) per
 // thread, so a wave's code loads and 16-byte stores are each one contiguous
 // run: element = bf16(code * scale) with the conversion the GEMM's in-register
@@ -902,6 +1173,56 @@ template <int EPI>
 void launch_bgemm_plan(hipStream_t s, const uint16_t* a, const DevWeight& w0, const DevWeight* w1, int M,
                        const float* residual, void* out) {
     launch_bgemm_plan_t<BTile<256, 256, 2, 4>, BTile<128, 256, 2, 4>, EPI>(s, a, w0, w1, M, residual, out);
+}
+
+// Over Q8_0 codes decoded into LDS tiles (mfma_dqgemm_kernel): columns [n0, n0 + nn).
+template <class T, int EPI>
+void launch_dqgemm(hipStream_t s, const uint16_t* a, const DevWeight& w0, const DevWeight* w1, int M, int n0,
+                   int nn, const float* residual, void* out) {
+    constexpr int TN = EPI >= 2 ? T::BN / 2 : T::BN;
+    const dim3 grid((nn + TN - 1) / TN, (M + T::BM - 1) / T::BM);
+    const size_t nd = (size_t)n0 * (w0.K / 32);
+    const uint8_t* qa = w0.q + (size_t)n0 * w0.K;
+    const __half* da = w0.d + nd;
+    const uint8_t* qb = EPI >= 2 ? w1->q + (size_t)n0 * w0.K : qa;
+    const __half* db = EPI >= 2 ? w1->d + nd : da;
+    const float* res = residual ? residual + n0 : nullptr;
+    void* o = EPI == 2 ? (void*)(static_cast<uint16_t*>(out) + n0) : (void*)(static_cast<float*>(out) + n0);
+    // Two A stages: three (the 128-row tiles in 112 KiB, the 256-row ones in
+    // 160 KiB) ran the 8B layer 0.5-1% slower.
+    constexpr int NSA = 2;
+    hipLaunchKernelGGL((mfma_dqgemm_kernel<T, EPI, NSA>), grid, dim3(T::NT), 0, s, a, qa, da, qb, db, M, nn, w0.K, w0.N,
+                       res, o);
+}
+
+// Q8_0 weights with K a multiple of 128 (whole 64-element K-step pairs).
+bool dqgemm_supported(const DevWeight& w) {
+    const char* e = getenv("VLRF_HIP_PREFILL_DQ");   // "0": the in-register decode instead
+    return !(e && e[0] == '0') && w.dtype == VLRF_HIP_DT_Q8_0 && w.K % 128 == 0;
+}
+
+// The tile plan of launch_bgemm_plan_t over codes, with half tiles of half
+// the columns rather than half the rows.
+template <int EPI>
+void launch_dqgemm_plan(hipStream_t s, const uint16_t* a, const DevWeight& w0, const DevWeight* w1, int M,
+                        const float* residual, void* out) {
+    using BBig = BTile<256, 256, 2, 4>;
+    // Half tiles of 256 x 128 (8 waves of 64 x 64): half the decode per
+    // workgroup and step of 128 x 256 tiles, the same MFMA work (8B layer at
+    // T = 2048: 1.081 against 1.053 ms with 128 x 256 half tiles).
+    using BHalf = BTile<256, 128, 4, 2>;
+    const int cus = lds_cus(), N = w0.N;
+    const int tn = EPI >= 2 ? BBig::BN / 2 : BBig::BN;
+    const int mt = (M + BBig::BM - 1) / BBig::BM, nt = (N + tn - 1) / tn;
+    const long full = (long)mt * nt, rem = full % cus;
+    if (EPI < 2 && 4 * full < 3L * cus) {
+        launch_dqgemm<BHalf, EPI>(s, a, w0, w1, M, 0, N, residual, out);
+        return;
+    }
+    int n_split = N;
+    if (N % tn == 0 && full >= cus && rem > 0 && 2 * rem <= cus && rem % mt == 0) n_split = (int)((nt - rem / mt) * tn);
+    launch_dqgemm<BBig, EPI>(s, a, w0, w1, M, 0, n_split, residual, out);
+    if (n_split < N) launch_dqgemm<BHalf, EPI>(s, a, w0, w1, M, n_split, N - n_split, residual, out);
 }
 
 // out[r][:] = bf16(w ? rmsnorm(x[r]) * w : x[r]), one 256-lane workgroup per row
@@ -1336,6 +1657,9 @@ int launch_qgemm(hipStream_t s, const DevWeight& w, const uint16_t* a, int M, co
         if (w.bf) {
             if (residual) launch_bgemm_plan<1>(s, a, w, nullptr, M, residual, y);
             else launch_bgemm_plan<0>(s, a, w, nullptr, M, nullptr, y);
+        } else if (dqgemm_supported(w)) {
+            if (residual) launch_dqgemm_plan<1>(s, a, w, nullptr, M, residual, y);
+            else launch_dqgemm_plan<0>(s, a, w, nullptr, M, nullptr, y);
         } else {
             const LdsPlan p = lds_plan(M, w.N, false, lds_cus());
             if (residual) launch_lds_plan<1>(s, p, a, w, nullptr, M, residual, y);
@@ -1368,6 +1692,9 @@ int launch_qgemm_swiglu(hipStream_t s, const DevWeight& wg, const DevWeight& wu,
         if (both) {
             if (h_bf16) launch_bgemm_plan<2>(s, a, wg, &wu, M, nullptr, h);
             else launch_bgemm_plan<3>(s, a, wg, &wu, M, nullptr, h);
+        } else if (dqgemm_supported(wg)) {
+            if (h_bf16) launch_dqgemm_plan<2>(s, a, wg, &wu, M, nullptr, h);
+            else launch_dqgemm_plan<3>(s, a, wg, &wu, M, nullptr, h);
         } else {
             const LdsPlan p = lds_plan(M, wg.N, true, lds_cus());
             if (h_bf16) launch_lds_plan<2>(s, p, a, wg, &wu, M, nullptr, h);
