@@ -813,8 +813,14 @@ __global__ __launch_bounds__(T::NT) void mfma_dqgemm_kernel(
         for (int it = 0; it < T::A_IT; ++it) dma16(ga[it] + (size_t)kt * RB, sa + (it * NW + wave) * 1024);
     };
     // This thread's codes: tile row wr, part pt of each K step's 64 (CPT
-    // codes from byte CPT pt; block 2 kt + CPT pt / 32 of the row).
-    const int wr = threadIdx.x / TPR, pt = threadIdx.x % TPR;
+    // codes from byte CPT pt; block 2 kt + CPT pt / 32 of the row).  A wave
+    // decodes 64 / TPR rows; lanes 8m .. 8m + 7, whose 16-byte LDS writes go
+    // out together, take rows (m & 1) + 2j + (16 / TPR)(m >> 1) of them, j <
+    // 8 / TPR: rows of distinct swizzles, so the eight writes of a chunk
+    // fill the eight 16-byte slots of a 128-byte row (rows t / TPR: two-way
+    // bank conflicts, rows 2i and 2i + 1 sharing a swizzle).
+    const int pt = lane % TPR, m8 = lane >> 3;
+    const int wr = wave * (64 / TPR) + (m8 & 1) + 2 * ((lane / TPR) % (8 / TPR)) + (16 / TPR) * (m8 >> 1);
     const bool wup = SWIGLU && wr >= BN / 2;
     const int gnr = min(n0 + (wup ? wr - BN / 2 : wr), N - 1);
     const uint8_t* qrow = (wup ? qb : qa) + (size_t)gnr * K + CPT * pt;
@@ -1206,6 +1212,8 @@ bool dqgemm_supported(const DevWeight& w) {
 template <int EPI>
 void launch_dqgemm_plan(hipStream_t s, const uint16_t* a, const DevWeight& w0, const DevWeight* w1, int M,
                         const float* residual, void* out) {
+    // 512 x 128 tiles (the A ring and two weight tiles in 160 KiB; half the
+    // decode per MFMA, twice the A bytes) ran the 8B layer 0.6% slower.
     using BBig = BTile<256, 256, 2, 4>;
     // Half tiles of 256 x 128 (8 waves of 64 x 64): half the decode per
     // workgroup and step of 128 x 256 tiles, the same MFMA work (8B layer at
