@@ -30,6 +30,7 @@
 // block, so the products carry ~16 significant bits of x and accumulate in
 // f32: results agree with the f32 reference to ~1e-5 relative.
 #include "../internal.hpp"
+#include "gemv_core.hpp"
 
 namespace vlrf_hip {
 namespace {
@@ -741,7 +742,40 @@ __global__ __launch_bounds__(T::NT) void mfma_bgemm_kernel(
         }
 }
 
-// The same GEMM over Q8_0 codes, dequantized into LDS tiles: A is staged by
+// One thread's codes of one K step (QB bytes: two or one 16-byte loads, or
+// one 8-byte load) and the f16 scale of their block (zero-extended), loaded
+// by inline assembly (see mfma_dqgemm_kernel).
+typedef uint32_t dq_u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t dq_u32x2 __attribute__((ext_vector_type(2)));
+template <int QB>
+struct DqCodes {
+    static constexpr int NQ = QB >= 16 ? QB / 16 : 1;   // loads of the codes
+    typedef typename std::conditional<(QB >= 16), dq_u32x4, dq_u32x2>::type V;
+    V q[NQ];
+    uint32_t d;
+    __device__ __forceinline__ uint32_t word(int j) const {
+        if constexpr (QB >= 16) return q[j >> 2][j & 3];
+        else return q[0][j];
+    }
+    __device__ __forceinline__ void load(const uint8_t* p, const __half* ps) {
+        if constexpr (QB >= 16) {
+            asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(q[0]) : "v"(p));
+            if constexpr (NQ == 2) asm volatile("global_load_dwordx4 %0, %1, off offset:16" : "=v"(q[NQ - 1]) : "v"(p));
+        } else {
+            asm volatile("global_load_dwordx2 %0, %1, off" : "=v"(q[0]) : "v"(p));
+        }
+        asm volatile("global_load_ushort %0, %1, off" : "=v"(d) : "v"(ps));
+    }
+    // Wait until at most N vector-memory operations are pending; the
+    // registers pass through the statement, so no use of them precedes it.
+    template <int N>
+    __device__ __forceinline__ void wait() {
+        if constexpr (NQ == 2) asm volatile("s_waitcnt vmcnt(%3)" : "+v"(q[0]), "+v"(q[NQ - 1]), "+v"(d) : "n"(N));
+        else asm volatile("s_waitcnt vmcnt(%2)" : "+v"(q[0]), "+v"(d) : "n"(N));
+    }
+};
+
+// The same GEMM over Q8_0 / Q4_0 codes, dequantized into LDS tiles: A is staged by
 // direct-to-LDS loads in a two-stage ring as above; the weight tile of each K
 // step is loaded as codes into registers (thread t: row t / TPR, the codes
 // of part t % TPR of the row's 64 and their f16 scale), decoded there to
@@ -764,22 +798,25 @@ __global__ __launch_bounds__(T::NT) void mfma_bgemm_kernel(
 // group's MFMAs and the codes loaded one step later (the compiler's waits)
 // the 8B layer ran 1.23 against 1.12 ms for the in-register decode; as here,
 // 1.05 ms.
-template <class T, int EPI, int NSA>
+template <class T, int WT, int EPI, int NSA>
 __global__ __launch_bounds__(T::NT) void mfma_dqgemm_kernel(
     const uint16_t* __restrict__ A, const uint8_t* __restrict__ qa, const __half* __restrict__ da,
     const uint8_t* __restrict__ qb, const __half* __restrict__ db, int M, int N, int K, int ldo,
     const float* __restrict__ residual, void* __restrict__ out) {
     using lds_gemm::dma16;
     using lds_gemm::lds_addr;
-    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
     constexpr int MI = T::MI, NB = T::NB, WM = T::WM, WNR = T::WNR, BN = T::BN;
     constexpr int A_B = T::A_B, NW = T::NW, RB = T::RB, CPR = T::CPR, RPL = T::RPL;
     constexpr int W_B = BN * RB;
     constexpr bool SWIGLU = EPI >= 2;
+    constexpr bool Q4 = WT == VLRF_HIP_DT_Q4_0;
     constexpr int TPR = T::NT / BN;              // threads per weight row
     constexpr int CPT = 64 / TPR;                // codes per thread and K step
-    constexpr int NQ = CPT / 16, NC = CPT / 8;   // its 16-byte loads, 8-code chunks
-    constexpr int LW = NQ + 1;                   // loads per code set (the codes, the scale)
+    constexpr int NC = CPT / 8;                  // its 8-code chunks
+    constexpr int RBQ = Q4 ? 32 : 64;            // code bytes of a row per K step
+    constexpr int QB = Q4 ? CPT / 2 : CPT;       // code bytes per thread and K step
+    using Codes = DqCodes<QB>;
+    constexpr int LW = Codes::NQ + 1;            // loads per code set (the codes, the scale)
     static_assert(T::BK == 64 && T::NG == 4 && T::NT % BN == 0 && (TPR == 2 || TPR == 4), "code split");
     static_assert(NSA >= 2 && NSA * A_B + 2 * W_B <= 160 * 1024, "LDS");
     // Loads in flight at each wait (step j ends with A of step j + NSA, then
@@ -823,38 +860,38 @@ __global__ __launch_bounds__(T::NT) void mfma_dqgemm_kernel(
     const int wr = wave * (64 / TPR) + (m8 & 1) + 2 * ((lane / TPR) % (8 / TPR)) + (16 / TPR) * (m8 >> 1);
     const bool wup = SWIGLU && wr >= BN / 2;
     const int gnr = min(n0 + (wup ? wr - BN / 2 : wr), N - 1);
-    const uint8_t* qrow = (wup ? qb : qa) + (size_t)gnr * K + CPT * pt;
+    const uint8_t* qrow = (wup ? qb : qa) + (size_t)gnr * (K / 64 * RBQ) + QB * pt;
     const __half* drow = (wup ? db : da) + (size_t)gnr * (K / 32) + CPT * pt / 32;
     int woff[NC];
 #pragma unroll
     for (int c = 0; c < NC; ++c) woff[c] = NSA * A_B + wr * RB + 16 * ((NC * pt + c) ^ T::swz(wr));
-    // Register sets: NQ 16-byte code loads and the scale (zero-extended).
-    u32x4 cq0[NQ], cq1[NQ];
-    uint32_t cs0, cs1;
-    auto load_w = [&](int kt, u32x4 (&q)[NQ], uint32_t& d) {
-        const uint8_t* p = qrow + (size_t)kt * 64;
-        const __half* ps = drow + 2 * kt;
-        asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(q[0]) : "v"(p));
-        if constexpr (NQ == 2) asm volatile("global_load_dwordx4 %0, %1, off offset:16" : "=v"(q[NQ - 1]) : "v"(p));
-        asm volatile("global_load_ushort %0, %1, off" : "=v"(d) : "v"(ps));
-    };
-    // Wait until at most N vector-memory operations are pending; the set's
-    // registers pass through the statement, so no use of them precedes it.
-    auto wait_w = [&](u32x4 (&q)[NQ], uint32_t& d, auto n) {
-        if constexpr (NQ == 2)
-            asm volatile("s_waitcnt vmcnt(%3)" : "+v"(q[0]), "+v"(q[NQ - 1]), "+v"(d) : "n"(decltype(n)::value));
-        else
-            asm volatile("s_waitcnt vmcnt(%2)" : "+v"(q[0]), "+v"(d) : "n"(decltype(n)::value));
-    };
+    // Register sets of the codes (two, alternating by step).
+    Codes cq0, cq1;
+    auto load_w = [&](int kt, Codes& q) { q.load(qrow + (size_t)kt * RBQ, drow + 2 * kt); };
     // Chunks c0 .. c1 - 1 (8 codes each) of the thread's codes -> bf16 (the
-    // expansion's conversion), into W buffer wb.
-    auto store_w = [&](const u32x4 (&q)[NQ], uint32_t d, int wb, int c0, int c1) {
-        const float sc = __half2float(__ushort_as_half((unsigned short)d));
+    // expansion's conversion), into W buffer wb.  Q8_0: signed bytes times
+    // the scale; Q4_0 (element 2b + i in nibble i of byte b): (n - 8) / 16
+    // (one conversion a code, gemv::s4f) times 16 x the scale, exact, so the
+    // same bf16 as (n - 8) x scale.
+    auto store_w = [&](const Codes& q, int wb, int c0, int c1) {
+        const float sc = __half2float(__ushort_as_half((unsigned short)q.d)) * (Q4 ? 16.f : 1.f);
 #pragma unroll
         for (int c = c0; c < c1; ++c) {
             bf16x8 v;
+            if constexpr (Q4) {
+                const uint32_t x = q.word(c) ^ 0x88888888u, x4 = x >> 4;
+                v[0] = (__bf16)(gemv::s4f<0>(x) * sc);
+                v[1] = (__bf16)(gemv::s4f<0>(x4) * sc);
+                v[2] = (__bf16)(gemv::s4f<1>(x) * sc);
+                v[3] = (__bf16)(gemv::s4f<1>(x4) * sc);
+                v[4] = (__bf16)(gemv::s4f<2>(x) * sc);
+                v[5] = (__bf16)(gemv::s4f<2>(x4) * sc);
+                v[6] = (__bf16)(gemv::s4f<3>(x) * sc);
+                v[7] = (__bf16)(gemv::s4f<3>(x4) * sc);
+            } else {
 #pragma unroll
-            for (int e = 0; e < 8; ++e) v[e] = (__bf16)((float)(int8_t)(q[c >> 1][2 * (c & 1) + (e >> 2)] >> (8 * (e & 3))) * sc);
+                for (int e = 0; e < 8; ++e) v[e] = (__bf16)((float)(int8_t)(q.word(2 * c + (e >> 2)) >> (8 * (e & 3))) * sc);
+            }
             *reinterpret_cast<bf16x8*>(lds + woff[c] + wb * W_B) = v;
         }
     };
@@ -904,10 +941,10 @@ __global__ __launch_bounds__(T::NT) void mfma_dqgemm_kernel(
     // A phase with chunks c0 .. c1 - 1 of the next tile's decode spread over its MFMAs.
     constexpr int DQ_V = (20 * (NC / 2) + NMF - 1) / NMF;   // decode VALU per MFMA (about 20 per chunk)
     auto phase_dq = [&](const bf16x8 (&a)[MI], const bf16x8 (&b)[NB], int sa, int wb, int g, bf16x8 (&na)[MI],
-                        bf16x8 (&nb)[NB], const u32x4 (&q)[NQ], uint32_t d, int wnext, int c0, int c1) {
+                        bf16x8 (&nb)[NB], const Codes& q, int wnext, int c0, int c1) {
         mm(a, b);
         rd(sa, wb, g, na, nb);
-        store_w(q, d, wnext, c0, c1);
+        store_w(q, wnext, c0, c1);
 #pragma unroll
         for (int i = 0; i < NMF; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);              // one MFMA
@@ -921,7 +958,7 @@ __global__ __launch_bounds__(T::NT) void mfma_dqgemm_kernel(
     // MFMAs, then the codes of step ktw into the register set given).
     constexpr int PER = (T::A_IT + NMF - 1) / NMF;
     auto phase_refill = [&](const bf16x8 (&a)[MI], const bf16x8 (&b)[NB], int sa, int wb, bf16x8 (&na)[MI],
-                            bf16x8 (&nb)[NB], int kta, int sa_fill, int ktw, u32x4 (&q)[NQ], uint32_t& d) {
+                            bf16x8 (&nb)[NB], int kta, int sa_fill, int ktw, Codes& q) {
         const int x = 16 * ((2 * h) ^ sw);
         const uint8_t* pa = lds + sa * A_B + a_off + x;
         const uint8_t* pb = lds + wb * W_B + b_off + x;
@@ -936,7 +973,7 @@ __global__ __launch_bounds__(T::NT) void mfma_dqgemm_kernel(
 #pragma unroll
                 for (int l = n * PER; l < (n + 1) * PER && l < T::A_IT; ++l)
                     dma16(ga[l] + (size_t)kta * RB, sfa + (l * NW + wave) * 1024);
-                if (n == NMF - 1) load_w(ktw, q, d);
+                if (n == NMF - 1) load_w(ktw, q);
                 __builtin_amdgcn_sched_barrier(0);
             }
     };
@@ -945,15 +982,15 @@ __global__ __launch_bounds__(T::NT) void mfma_dqgemm_kernel(
     // (decoded into W buffer 0), then A 0 .. NSA - 3, and the pairs (A
     // NSA - 2, codes 1), (A NSA - 1, codes 2).
     const int nk = K / T::BK;
-    load_w(0, cq0, cs0);
-    wait_w(cq0, cs0, std::integral_constant<int, 0>{});
-    store_w(cq0, cs0, 0, 0, NC);
+    load_w(0, cq0);
+    cq0.template wait<0>();
+    store_w(cq0, 0, 0, NC);
 #pragma unroll
     for (int j = 0; j < NSA - 2; ++j) load_a(min(j, nk - 1), j);
     load_a(min(NSA - 2, nk - 1), NSA - 2);
-    load_w(min(1, nk - 1), cq1, cs1);
+    load_w(min(1, nk - 1), cq1);
     load_a(min(NSA - 1, nk - 1), NSA - 1);
-    load_w(min(2, nk - 1), cq0, cs0);
+    load_w(min(2, nk - 1), cq0);
     __builtin_amdgcn_s_waitcnt(W_PRO);
     __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0) alone: the tile's LDS writes done
     __builtin_amdgcn_s_barrier();
@@ -965,24 +1002,24 @@ __global__ __launch_bounds__(T::NT) void mfma_dqgemm_kernel(
     // k + 1 (set qn) into W buffer (k + 1) % 2; set qn then takes the codes of
     // step k + 3, A stage st A of step k + NSA.
     int st = 0;
-    auto step = [&](int k, u32x4 (&qn)[NQ], uint32_t& dn) {
+    auto step = [&](int k, Codes& qn) {
         const int s = k & 1, s1 = s ^ 1, sn = st + 1 == NSA ? 0 : st + 1;
-        wait_w(qn, dn, std::integral_constant<int, VM_CODES>{});
-        phase_dq(fa[0], fb[0], st, s, 1, fa[1], fb[1], qn, dn, s1, 0, NC / 2);
-        phase_dq(fa[1], fb[1], st, s, 2, fa[0], fb[0], qn, dn, s1, NC / 2, NC);
+        qn.template wait<VM_CODES>();
+        phase_dq(fa[0], fb[0], st, s, 1, fa[1], fb[1], qn, s1, 0, NC / 2);
+        phase_dq(fa[1], fb[1], st, s, 2, fa[0], fb[0], qn, s1, NC / 2, NC);
         phase(fa[0], fb[0], st, s, 3, fa[1], fb[1]);
         __builtin_amdgcn_s_waitcnt(W_BAR);   // A of step k + 1 in; W writes and reads done
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
-        phase_refill(fa[1], fb[1], sn, s1, fa[0], fb[0], min(k + NSA, nk - 1), st, min(k + 3, nk - 1), qn, dn);
+        phase_refill(fa[1], fb[1], sn, s1, fa[0], fb[0], min(k + NSA, nk - 1), st, min(k + 3, nk - 1), qn);
         st = sn;
     };
     for (int k = 0; k < nk; k += 2) {
-        step(k, cq1, cs1);
-        step(k + 1, cq0, cs0);
+        step(k, cq1);
+        step(k + 1, cq0);
     }
-    wait_w(cq0, cs0, std::integral_constant<int, 0>{});   // nothing outlives the workgroup
-    wait_w(cq1, cs1, std::integral_constant<int, 0>{});
+    cq0.template wait<0>();   // nothing outlives the workgroup
+    cq1.template wait<0>();
 
     // Accumulator v of tile (j, i) holds row 32i + 8(v/4) + 4h + v%4 of the
     // wave's rows, weight row l32 of block j.
@@ -1188,23 +1225,28 @@ void launch_dqgemm(hipStream_t s, const uint16_t* a, const DevWeight& w0, const 
     constexpr int TN = EPI >= 2 ? T::BN / 2 : T::BN;
     const dim3 grid((nn + TN - 1) / TN, (M + T::BM - 1) / T::BM);
     const size_t nd = (size_t)n0 * (w0.K / 32);
-    const uint8_t* qa = w0.q + (size_t)n0 * w0.K;
+    const size_t rowb = w0.dtype == VLRF_HIP_DT_Q8_0 ? (size_t)w0.K : (size_t)w0.K / 2;
+    const uint8_t* qa = w0.q + (size_t)n0 * rowb;
     const __half* da = w0.d + nd;
-    const uint8_t* qb = EPI >= 2 ? w1->q + (size_t)n0 * w0.K : qa;
+    const uint8_t* qb = EPI >= 2 ? w1->q + (size_t)n0 * rowb : qa;
     const __half* db = EPI >= 2 ? w1->d + nd : da;
     const float* res = residual ? residual + n0 : nullptr;
     void* o = EPI == 2 ? (void*)(static_cast<uint16_t*>(out) + n0) : (void*)(static_cast<float*>(out) + n0);
     // Two A stages: three (the 128-row tiles in 112 KiB, the 256-row ones in
     // 160 KiB) ran the 8B layer 0.5-1% slower.
     constexpr int NSA = 2;
-    hipLaunchKernelGGL((mfma_dqgemm_kernel<T, EPI, NSA>), grid, dim3(T::NT), 0, s, a, qa, da, qb, db, M, nn, w0.K, w0.N,
-                       res, o);
+    if (w0.dtype == VLRF_HIP_DT_Q8_0)
+        hipLaunchKernelGGL((mfma_dqgemm_kernel<T, VLRF_HIP_DT_Q8_0, EPI, NSA>), grid, dim3(T::NT), 0, s, a, qa, da, qb, db,
+                           M, nn, w0.K, w0.N, res, o);
+    else
+        hipLaunchKernelGGL((mfma_dqgemm_kernel<T, VLRF_HIP_DT_Q4_0, EPI, NSA>), grid, dim3(T::NT), 0, s, a, qa, da, qb, db,
+                           M, nn, w0.K, w0.N, res, o);
 }
 
-// Q8_0 weights with K a multiple of 128 (whole 64-element K-step pairs).
+// Q8_0 / Q4_0 weights with K a multiple of 128 (whole 64-element K-step pairs).
 bool dqgemm_supported(const DevWeight& w) {
     const char* e = getenv("VLRF_HIP_PREFILL_DQ");   // "0": the in-register decode instead
-    return !(e && e[0] == '0') && w.dtype == VLRF_HIP_DT_Q8_0 && w.K % 128 == 0;
+    return !(e && e[0] == '0') && (w.dtype == VLRF_HIP_DT_Q8_0 || w.dtype == VLRF_HIP_DT_Q4_0) && w.K % 128 == 0;
 }
 
 // The tile plan of launch_bgemm_plan_t over codes, with half tiles of half
