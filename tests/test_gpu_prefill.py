@@ -133,6 +133,35 @@ def test_config5_llama8b_layer_t256(ctx, dtype):
     check(got, om.forward_hidden(x), "8B layer vs f32 oracle")
 
 
+@pytest.mark.parametrize("dtype", [V.DT_Q8_0, V.DT_Q4_0])
+def test_config5_layer_gemm_forms_identical(ctx, monkeypatch, dtype):
+    """The 8B-shape layer at T = 256 with each form of the M > 128 GEMM: over
+    the weights' bf16 expansions (the default), with the codes decoded into
+    the GEMM's LDS tiles (VLRF_HIP_PREFILL_BF16=0) and decoded in registers
+    (VLRF_HIP_PREFILL_DQ=0 too).  The forms multiply the same bf16 operands
+    in the same order, so the layer's outputs are identical bit for bit.  A
+    fresh model per form: an expansion, once made, stays with its weight."""
+    cfg = F.llama8b_layer(dtype, max_seq_len=512)
+    T, D = 256, cfg["d_model"]
+    x = F.normal(6, "cfg5.forms.x", T * D).reshape(T, D)
+    envs = ({}, {"VLRF_HIP_PREFILL_BF16": "0"}, {"VLRF_HIP_PREFILL_BF16": "0", "VLRF_HIP_PREFILL_DQ": "0"})
+    models = [V.Model(ctx, cfg) for _ in envs]
+    for name, rows, cols, kind in F.tensor_specs(cfg):        # each tensor made once, uploaded to all
+        payload, _ = F.make_tensor(6, name, rows, cols, kind, cfg["weight_dtype"], 0.0)
+        for m in models:
+            m.set_weight(name, payload, cfg["weight_dtype"] if kind == "proj" else F.DT_F32, rows, cols)
+    outs = []
+    for m, env in zip(models, envs):
+        print(f"[case] config5 8B layer T=256 dtype={dtype} env={env}", flush=True)
+        monkeypatch.delenv("VLRF_HIP_PREFILL_BF16", raising=False)
+        monkeypatch.delenv("VLRF_HIP_PREFILL_DQ", raising=False)
+        for k, v in env.items():
+            monkeypatch.setenv(k, v)
+        outs.append(m.forward_hidden(ctx.to_device(x)).download((T, D)))
+    assert np.isfinite(outs[0]).all()
+    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
+
+
 @pytest.mark.parametrize("chunks", [(96,), (64, 40)])
 def test_prefill_matches_bf16_model_tightly(ctx, chunks):
     """One layer against the float64 model of the bf16 scheme: the kernels
