@@ -183,19 +183,21 @@ def _hip():
     return h
 
 
-def test_prefill_gemm_under_graph_capture(orc):
+@pytest.mark.parametrize("dtype", [V.DT_Q8_0, V.DT_Q4_0])
+def test_prefill_gemm_under_graph_capture(orc, dtype):
     """A stream under graph capture: the M > 128 GEMM records no allocation
     (the weight's bf16 expansion is not made, the tiles decode the blocks),
-    the captured graph replays to the eager result, replay after replay with
-    eager work between; a call that would grow the context scratch while
-    capturing is refused with an error instead of being recorded."""
+    the captured graph replays to the eager result (over the expansion) bit
+    for bit, replay after replay with eager work between; a call that would
+    grow the context scratch while capturing is refused with an error
+    instead of being recorded."""
     import ctypes as C
     hip = _hip()
     ctx = V.Context(0)                  # its own scratch buffer, empty until the first call
     M, N, K = 160, 512, 1024
-    print(f"[case] qgemm under capture M={M} N={N} K={K}", flush=True)
-    w1, dec = _weight(ctx, 31, "cap", N, K, V.DT_Q8_0)
-    w2, _ = _weight(ctx, 31, "cap", N, K, V.DT_Q8_0)          # the same blocks, never expanded
+    print(f"[case] qgemm under capture dtype={dtype} M={M} N={N} K={K}", flush=True)
+    w1, dec = _weight(ctx, 31, "cap", N, K, dtype)
+    w2, _ = _weight(ctx, 31, "cap", N, K, dtype)              # the same blocks, never expanded
     packed = w2.device_bytes
     x = F.normal(31, "capx", M * K).reshape(M, K)
     dx, y1, y2 = ctx.to_device(x), ctx.alloc(M * N * 4), ctx.alloc(M * N * 4)
@@ -220,7 +222,7 @@ def test_prefill_gemm_under_graph_capture(orc):
         ctx.sync()
         got = y2.download((M, N))
         assert rel_err(got, ref) <= TOL, i
-        assert rel_err(got, eager) <= 1e-3, i
+        assert np.array_equal(got, eager), i
     hip.hipGraphExecDestroy(ge)
     hip.hipGraphDestroy(g)
     # Scratch growth while capturing: refused, the capture ends cleanly.
