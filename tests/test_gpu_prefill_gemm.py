@@ -91,6 +91,63 @@ def test_prefill_swiglu_ragged(ctx, orc, dtype, M, Fd, K):
     assert rel_err(dh.download((M, Fd)), ref) <= TOL
 
 
+@pytest.mark.parametrize("dtype", [V.DT_Q8_0, V.DT_Q4_0])
+# 17 <= M <= 128 over codes with K split into slices (64 x 256 tiles to M = 64,
+# 128 x 128 above): the 1.1B up and down shapes, the 8B down shape (16 col
+# tiles x 16 slices), ragged N, the residual form, and K = 128 (one slice).
+@pytest.mark.parametrize("M,N,K,res", [(17, 5632, 2048, False), (64, 2048, 5632, True), (65, 300, 1024, False),
+                                       (128, 4096, 14336, True), (100, 1000, 128, False), (33, 6144, 4096, False)])
+def test_split_k_gemm_mid_m(ctx, orc, monkeypatch, dtype, M, N, K, res):
+    """The K-split GEMM against the oracle, and against the unsplit
+    register-staged kernel (VLRF_HIP_PREFILL_DQ=0): the same bf16 products,
+    summed in another order (slices added last), so equal to f32 rounding."""
+    print(f"[case] split-K qgemm dtype={dtype} M={M} N={N} K={K} res={res}", flush=True)
+    w, dec = _weight(ctx, 26, f"S{N}x{K}", N, K, dtype)
+    x = F.normal(26, f"sx{M}x{K}", M * K).reshape(M, K)
+    r = F.normal(26, f"sr{M}x{N}", M * N).reshape(M, N)
+    dx = ctx.to_device(x)
+
+    def run():
+        dy = ctx.to_device(r) if res else ctx.alloc(M * N * 4)
+        ctx.qlinear(w, dx, dy, M, residual=dy if res else None)
+        return dy.download((M, N))
+
+    monkeypatch.delenv("VLRF_HIP_PREFILL_DQ", raising=False)
+    got = run()
+    monkeypatch.setenv("VLRF_HIP_PREFILL_DQ", "0")
+    unsplit = run()
+    monkeypatch.delenv("VLRF_HIP_PREFILL_DQ", raising=False)
+    ref = x.astype(np.float64) @ dec.astype(np.float64).T + (r if res else 0)
+    assert rel_err(got, ref) <= TOL
+    assert rel_err(got, unsplit) <= 2e-5, rel_err(got, unsplit)
+
+
+@pytest.mark.parametrize("dtype", [V.DT_Q8_0, V.DT_Q4_0])
+@pytest.mark.parametrize("M,Fd,K", [(17, 5632, 2048), (100, 1408, 1024), (128, 14336, 4096), (70, 200, 384)])
+def test_split_k_swiglu_mid_m(ctx, orc, monkeypatch, dtype, M, Fd, K):
+    """SwiGLU at 17 <= M <= 128 with K split: gate and up partial sums reduced
+    before silu(g) * u, against the oracle and the unsplit kernel."""
+    print(f"[case] split-K swiglu dtype={dtype} M={M} F={Fd} K={K}", flush=True)
+    wg, gdec = _weight(ctx, 27, f"SG{Fd}x{K}", Fd, K, dtype)
+    wu, udec = _weight(ctx, 27, f"SU{Fd}x{K}", Fd, K, dtype)
+    x = F.normal(27, f"ssx{M}x{K}", M * K).reshape(M, K)
+    dx = ctx.to_device(x)
+
+    def run():
+        dh = ctx.alloc(M * Fd * 4)
+        ctx.qlinear_swiglu(wg, wu, dx, dh, M)
+        return dh.download((M, Fd))
+
+    monkeypatch.delenv("VLRF_HIP_PREFILL_DQ", raising=False)
+    got = run()
+    monkeypatch.setenv("VLRF_HIP_PREFILL_DQ", "0")
+    unsplit = run()
+    monkeypatch.delenv("VLRF_HIP_PREFILL_DQ", raising=False)
+    ref = orc.silu_mul(orc.linear(x, udec), orc.linear(x, gdec))
+    assert rel_err(got, ref) <= TOL
+    assert rel_err(got, unsplit) <= 2e-5, rel_err(got, unsplit)
+
+
 def _all_forms(monkeypatch, run):
     """run() with the weights' bf16 expansion (the default for M > 128), with
     VLRF_HIP_PREFILL_BF16=0 (Q8_0 with K % 128 == 0: codes decoded into LDS

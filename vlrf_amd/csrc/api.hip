@@ -606,13 +606,17 @@ int vlrf_hip_qlinear(vlrf_hip_ctx_t ctx, vlrf_hip_weight_t w, const float* x, fl
     }
     if (M <= 16) return launch_qlinear(ctx->stream, w->w, x, y, M, norm_w, eps, residual);
     VH_ARG(x && y, "qlinear: null activation pointer");
+    // Scratch: the bf16 rows, then the K-split partial sums (17 <= M <= 128).
+    const size_t a_bytes = ((size_t)M * w->w.K * sizeof(uint16_t) + 255) & ~(size_t)255;
+    const size_t p_bytes = qgemm_part_bytes(w->w, M, false);
     float* scratch = nullptr;
-    int rc = ctx->scratch((size_t)M * w->w.K * sizeof(uint16_t), &scratch);
+    int rc = ctx->scratch(a_bytes + p_bytes, &scratch);
     if (rc) return rc;
     uint16_t* a = reinterpret_cast<uint16_t*>(scratch);
+    float* part = p_bytes ? reinterpret_cast<float*>(reinterpret_cast<char*>(scratch) + a_bytes) : nullptr;
     rc = launch_rows_to_bf16(ctx->stream, x, norm_w, a, M, w->w.K, eps);
     if (rc) return rc;
-    return launch_qgemm(ctx->stream, w->w, a, M, residual, y);
+    return launch_qgemm(ctx->stream, w->w, a, M, residual, y, part);
 }
 
 int vlrf_hip_qlinear_swiglu(vlrf_hip_ctx_t ctx, vlrf_hip_weight_t wg, vlrf_hip_weight_t wu,
@@ -629,13 +633,16 @@ int vlrf_hip_qlinear_swiglu(vlrf_hip_ctx_t ctx, vlrf_hip_weight_t wg, vlrf_hip_w
     }
     if (M <= 16) return launch_qlinear_swiglu(ctx->stream, wg->w, wu->w, x, h, M, norm_w, eps);
     VH_ARG(x && h, "swiglu: null activation pointer");
+    const size_t a_bytes = ((size_t)M * wg->w.K * sizeof(uint16_t) + 255) & ~(size_t)255;
+    const size_t p_bytes = qgemm_part_bytes(wg->w, M, true);
     float* scratch = nullptr;
-    int rc = ctx->scratch((size_t)M * wg->w.K * sizeof(uint16_t), &scratch);
+    int rc = ctx->scratch(a_bytes + p_bytes, &scratch);
     if (rc) return rc;
     uint16_t* a = reinterpret_cast<uint16_t*>(scratch);
+    float* part = p_bytes ? reinterpret_cast<float*>(reinterpret_cast<char*>(scratch) + a_bytes) : nullptr;
     rc = launch_rows_to_bf16(ctx->stream, x, norm_w, a, M, wg->w.K, eps);
     if (rc) return rc;
-    return launch_qgemm_swiglu(ctx->stream, wg->w, wu->w, a, M, h, false);
+    return launch_qgemm_swiglu(ctx->stream, wg->w, wu->w, a, M, h, false, part);
 }
 
 // ---- the engine's remaining per-op backend calls --------------------------------------

@@ -183,12 +183,16 @@ int launch_add(hipStream_t s, float* dst, const float* src, int64_t n);
 // out[r] = bf16(w ? rmsnorm(x[r]) * w : x[r]) for rows x D
 int launch_rows_to_bf16(hipStream_t s, const float* x, const float* w, uint16_t* out, int rows, int D,
                         float eps);
-// y[M,N] = a[M,K] . W^T (+ residual), a in bf16, W Q8_0/Q4_0 with K % 64 == 0
+// y[M,N] = a[M,K] . W^T (+ residual), a in bf16, W Q8_0/Q4_0 with K % 64 == 0.
+// `part`: device memory of qgemm_part_bytes(w, M, false) bytes for the K-split
+// partial sums of 17 <= M <= 128 (without it such a call takes the unsplit
+// register-staged kernel).
 int launch_qgemm(hipStream_t s, const DevWeight& w, const uint16_t* a, int M, const float* residual,
-                 float* y);
+                 float* y, float* part = nullptr);
 // h[M,N] = silu(a.Wg^T) * (a.Wu^T), stored as bf16 (h_bf16) or f32
 int launch_qgemm_swiglu(hipStream_t s, const DevWeight& wg, const DevWeight& wu, const uint16_t* a,
-                        int M, void* h, bool h_bf16);
+                        int M, void* h, bool h_bf16, float* part = nullptr);
+size_t qgemm_part_bytes(const DevWeight& w, int M, bool swiglu);
 // Small M (2..16) on the matrix cores with f32-class accuracy (x split into
 // bf16 hi + lo): y = x.W0^T (+ residual), or silu(x.W0^T) * (x.W1^T) when w1
 // is given, in one launch.  Per-slice partial sums go to scratch

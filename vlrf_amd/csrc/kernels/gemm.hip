@@ -801,14 +801,15 @@ struct DqCodes {
 template <class T, int WT, int EPI, int NSA>
 __global__ __launch_bounds__(T::NT) void mfma_dqgemm_kernel(
     const uint16_t* __restrict__ A, const uint8_t* __restrict__ qa, const __half* __restrict__ da,
-    const uint8_t* __restrict__ qb, const __half* __restrict__ db, int M, int N, int K, int ldo,
+    const uint8_t* __restrict__ qb, const __half* __restrict__ db, int M, int N, int K, int kl, int ldo,
     const float* __restrict__ residual, void* __restrict__ out) {
     using lds_gemm::dma16;
     using lds_gemm::lds_addr;
     constexpr int MI = T::MI, NB = T::NB, WM = T::WM, WNR = T::WNR, BN = T::BN;
     constexpr int A_B = T::A_B, NW = T::NW, RB = T::RB, CPR = T::CPR, RPL = T::RPL;
     constexpr int W_B = BN * RB;
-    constexpr bool SWIGLU = EPI >= 2;
+    // EPI 6 / 7: raw partial sums of K slice blockIdx.z (plain / gate and up).
+    constexpr bool SWIGLU = EPI == 2 || EPI == 3 || EPI == 7, PARTIAL = EPI >= 6;
     constexpr bool Q4 = WT == VLRF_HIP_DT_Q4_0;
     constexpr int TPR = T::NT / BN;              // threads per weight row
     constexpr int CPT = 64 / TPR;                // codes per thread and K step
@@ -836,12 +837,13 @@ __global__ __launch_bounds__(T::NT) void mfma_dqgemm_kernel(
     const int wm = wave / T::WC, wn = wave % T::WC;
     const int m0 = blockIdx.y * T::BM;
     const int n0 = blockIdx.x * (SWIGLU ? BN / 2 : BN);   // first output column
+    const int k0 = blockIdx.z * kl;                        // this launch's K range: k0 .. k0 + kl (rows K long)
 
     const char* ga[T::A_IT];
 #pragma unroll
     for (int it = 0; it < T::A_IT; ++it) {
         const int r = (it * NW + wave) * RPL + lane / CPR, c = (lane % CPR) ^ T::swz(r);
-        ga[it] = reinterpret_cast<const char*>(A + (size_t)min(m0 + r, M - 1) * K + c * 8);
+        ga[it] = reinterpret_cast<const char*>(A + (size_t)min(m0 + r, M - 1) * K + k0 + c * 8);
     }
     const uint32_t base = lds_addr(lds);
     auto load_a = [&](int kt, int buf) {
@@ -860,8 +862,8 @@ __global__ __launch_bounds__(T::NT) void mfma_dqgemm_kernel(
     const int wr = wave * (64 / TPR) + (m8 & 1) + 2 * ((lane / TPR) % (8 / TPR)) + (16 / TPR) * (m8 >> 1);
     const bool wup = SWIGLU && wr >= BN / 2;
     const int gnr = min(n0 + (wup ? wr - BN / 2 : wr), N - 1);
-    const uint8_t* qrow = (wup ? qb : qa) + (size_t)gnr * (K / 64 * RBQ) + QB * pt;
-    const __half* drow = (wup ? db : da) + (size_t)gnr * (K / 32) + CPT * pt / 32;
+    const uint8_t* qrow = (wup ? qb : qa) + (size_t)gnr * (K / 64 * RBQ) + k0 / 64 * RBQ + QB * pt;
+    const __half* drow = (wup ? db : da) + (size_t)gnr * (K / 32) + k0 / 32 + CPT * pt / 32;
     int woff[NC];
 #pragma unroll
     for (int c = 0; c < NC; ++c) woff[c] = NSA * A_B + wr * RB + 16 * ((NC * pt + c) ^ T::swz(wr));
@@ -976,12 +978,18 @@ __global__ __launch_bounds__(T::NT) void mfma_dqgemm_kernel(
                 if (n == NMF - 1) load_w(ktw, q);
                 __builtin_amdgcn_sched_barrier(0);
             }
+        // Reads beyond one per MFMA (one 32-row block per wave: MI + NB > MI NB).
+#pragma unroll
+        for (int n = NMF; n < NR; ++n) {
+            if (n < MI) na[n] = *reinterpret_cast<const bf16x8*>(pa + n * 32 * RB);
+            else nb[n - MI] = *reinterpret_cast<const bf16x8*>(pb + boff(n - MI));
+        }
     };
 
     // Prologue, so that every step finds the same loads in flight: codes 0
     // (decoded into W buffer 0), then A 0 .. NSA - 3, and the pairs (A
     // NSA - 2, codes 1), (A NSA - 1, codes 2).
-    const int nk = K / T::BK;
+    const int nk = kl / T::BK;
     load_w(0, cq0);
     cq0.template wait<0>();
     store_w(cq0, 0, 0, NC);
@@ -1023,6 +1031,27 @@ __global__ __launch_bounds__(T::NT) void mfma_dqgemm_kernel(
 
     // Accumulator v of tile (j, i) holds row 32i + 8(v/4) + 4h + v%4 of the
     // wave's rows, weight row l32 of block j.
+    if constexpr (PARTIAL) {
+        // Slice z's sums at out + z M ldo: plain column n at n, SwiGLU gate at
+        // n and up at N + n (ldo >= 2N).
+        float* P = static_cast<float*>(out) + (size_t)blockIdx.z * M * ldo;
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int row = m0 + wm * WM + 32 * i + 8 * (v >> 2) + 4 * h + (v & 3);
+                if (row >= M) continue;
+#pragma unroll
+                for (int j = 0; j < (SWIGLU ? NB / 2 : NB); ++j) {
+                    const int col = n0 + (SWIGLU ? wn * (WNR / 2) : wn * WNR) + 32 * j + l32;
+                    if (col < N) {
+                        P[(size_t)row * ldo + col] = acc[j][i][v];
+                        if constexpr (SWIGLU) P[(size_t)row * ldo + N + col] = acc[j + NB / 2][i][v];
+                    }
+                }
+            }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < MI; ++i)
 #pragma unroll
@@ -1237,10 +1266,10 @@ void launch_dqgemm(hipStream_t s, const uint16_t* a, const DevWeight& w0, const 
     constexpr int NSA = 2;
     if (w0.dtype == VLRF_HIP_DT_Q8_0)
         hipLaunchKernelGGL((mfma_dqgemm_kernel<T, VLRF_HIP_DT_Q8_0, EPI, NSA>), grid, dim3(T::NT), 0, s, a, qa, da, qb, db,
-                           M, nn, w0.K, w0.N, res, o);
+                           M, nn, w0.K, w0.K, w0.N, res, o);
     else
         hipLaunchKernelGGL((mfma_dqgemm_kernel<T, VLRF_HIP_DT_Q4_0, EPI, NSA>), grid, dim3(T::NT), 0, s, a, qa, da, qb, db,
-                           M, nn, w0.K, w0.N, res, o);
+                           M, nn, w0.K, w0.K, w0.N, res, o);
 }
 
 // Q8_0 / Q4_0 weights with K a multiple of 128 (whole 64-element K-step pairs).
@@ -1273,6 +1302,94 @@ void launch_dqgemm_plan(hipStream_t s, const uint16_t* a, const DevWeight& w0, c
     if (N % tn == 0 && full >= cus && rem > 0 && 2 * rem <= cus && rem % mt == 0) n_split = (int)((nt - rem / mt) * tn);
     launch_dqgemm<BBig, EPI>(s, a, w0, w1, M, 0, n_split, residual, out);
     if (n_split < N) launch_dqgemm<BHalf, EPI>(s, a, w0, w1, M, n_split, N - n_split, residual, out);
+}
+
+// ---- 17 <= M <= 128: mfma_dqgemm_kernel with K split over blockIdx.z ------------
+// One tile row (64 x 256 tiles for M <= 64, 128 x 128 above) leaves a GEMM of
+// these M with one workgroup per 128-256 weight rows: 16-48 of the 256 CUs at
+// the 1.1B and 8B shapes, each streaming its rows' whole K.  The K steps are
+// split into S contiguous slices instead, each slice's f32 sums written to a
+// partial buffer ([S][M][N], SwiGLU [S][M][2N]: gate, then up), and
+// splitk_reduce_kernel adds the slices in order (the same sum on every run)
+// and applies the epilogue.  S is the smallest divisor of K / 128 that gives
+// at least one workgroup per CU, at most one whose partials (written and read
+// back) move no more bytes than the weight: S <= K bpw / (8 M).
+
+// out[r][n] = sum over z of P[z][r][n] (EPI 0), + residual (1, in place
+// allowed), silu(sum of gate) * (sum of up) as bf16 (2) or f32 (3).
+template <int EPI>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ P, int S, int M, int N,
+                                                            int ldp, const float* residual, void* out) {
+    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (size_t)M * N) return;
+    const int row = (int)(idx / N), col = (int)(idx % N);
+    const size_t zs = (size_t)M * ldp;
+    const float* p = P + (size_t)row * ldp + col;
+    float g = 0.f;
+    for (int z = 0; z < S; ++z) g += p[z * zs];
+    if constexpr (EPI >= 2) {
+        float u = 0.f;
+        for (int z = 0; z < S; ++z) u += p[z * zs + N];
+        const float hv = silu_mul_fast(g, u);
+        if constexpr (EPI == 2) static_cast<uint16_t*>(out)[idx] = (uint16_t)bf16_bits(hv);
+        else static_cast<float*>(out)[idx] = hv;
+    } else if constexpr (EPI == 1) {
+        static_cast<float*>(out)[idx] = g + residual[idx];
+    } else {
+        static_cast<float*>(out)[idx] = g;
+    }
+}
+
+using SplitTile64 = BTile<64, 256, 2, 4>;     // M <= 64: 8 waves of 32 x 64
+using SplitTile128 = BTile<128, 128, 4, 2>;   // 65 <= M <= 128: 8 waves of 32 x 64
+
+int splitk_slices(const DevWeight& w, int M, bool swiglu, int cus) {
+    const int bn = M <= 64 ? SplitTile64::BN : SplitTile128::BN;
+    const long nt = (w.N + (swiglu ? bn / 2 : bn) - 1) / (swiglu ? bn / 2 : bn);
+    const double bpw = w.dtype == VLRF_HIP_DT_Q8_0 ? 34.0 / 32 : 18.0 / 32;   // weight bytes per element
+    const int cap = std::max(1, (int)(w.K * bpw / (8.0 * M)));
+    const int kb = w.K / 128;
+    int S = 1;
+    for (int d = 1; d <= kb && d <= cap; ++d) {
+        if (kb % d) continue;
+        S = d;
+        if (nt * d >= cus) break;
+    }
+    return S;
+}
+
+template <class T, int WT, int EPI>
+void launch_dq_split_t(hipStream_t s, const uint16_t* a, const DevWeight& w0, const DevWeight* w1, int M, int S,
+                       const float* residual, void* out, float* part) {
+    constexpr bool SW = EPI >= 2;
+    constexpr int TN = SW ? T::BN / 2 : T::BN;
+    const int N = w0.N, K = w0.K;
+    const dim3 grid((N + TN - 1) / TN, (M + T::BM - 1) / T::BM, S);
+    const uint8_t* qb = SW ? w1->q : w0.q;
+    const __half* db = SW ? w1->d : w0.d;
+    if (S == 1) {
+        hipLaunchKernelGGL((mfma_dqgemm_kernel<T, WT, EPI, 2>), grid, dim3(T::NT), 0, s, a, w0.q, w0.d, qb, db, M, N,
+                           K, K, N, residual, out);
+        return;
+    }
+    const int ldp = SW ? 2 * N : N;
+    hipLaunchKernelGGL((mfma_dqgemm_kernel<T, WT, SW ? 7 : 6, 2>), grid, dim3(T::NT), 0, s, a, w0.q, w0.d, qb, db, M,
+                       N, K, K / S, ldp, nullptr, part);
+    const size_t n = (size_t)M * N;
+    hipLaunchKernelGGL((splitk_reduce_kernel<EPI>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, part, S, M, N,
+                       ldp, residual, out);
+}
+
+template <int EPI>
+void launch_dq_split(hipStream_t s, const uint16_t* a, const DevWeight& w0, const DevWeight* w1, int M, int S,
+                     const float* residual, void* out, float* part) {
+    if (w0.dtype == VLRF_HIP_DT_Q8_0) {
+        if (M <= 64) launch_dq_split_t<SplitTile64, VLRF_HIP_DT_Q8_0, EPI>(s, a, w0, w1, M, S, residual, out, part);
+        else launch_dq_split_t<SplitTile128, VLRF_HIP_DT_Q8_0, EPI>(s, a, w0, w1, M, S, residual, out, part);
+    } else {
+        if (M <= 64) launch_dq_split_t<SplitTile64, VLRF_HIP_DT_Q4_0, EPI>(s, a, w0, w1, M, S, residual, out, part);
+        else launch_dq_split_t<SplitTile128, VLRF_HIP_DT_Q4_0, EPI>(s, a, w0, w1, M, S, residual, out, part);
+    }
 }
 
 // out[r][:] = bf16(w ? rmsnorm(x[r]) * w : x[r]), one 256-lane workgroup per row
@@ -1697,8 +1814,18 @@ bool weight_expand_bf16(hipStream_t s, const DevWeight& w) {
     return true;
 }
 
+// 17 <= M <= 128 over codes with K split: the partial-buffer bytes the call
+// needs (0 when it runs unsplit or on another kernel).
+static bool dq_split_path(const DevWeight& w, int M) { return M >= 17 && M <= 128 && dqgemm_supported(w); }
+
+size_t qgemm_part_bytes(const DevWeight& w, int M, bool swiglu) {
+    if (!dq_split_path(w, M)) return 0;
+    const int S = splitk_slices(w, M, swiglu, lds_cus());
+    return S > 1 ? (size_t)S * M * w.N * (swiglu ? 2 : 1) * sizeof(float) : 0;
+}
+
 int launch_qgemm(hipStream_t s, const DevWeight& w, const uint16_t* a, int M, const float* residual,
-                 float* y) {
+                 float* y, float* part) {
     int rc = check_qgemm(w, M);
     if (rc) return rc;
     VH_ARG(a && y, "qgemm: null operand");
@@ -1715,6 +1842,10 @@ int launch_qgemm(hipStream_t s, const DevWeight& w, const uint16_t* a, int M, co
             if (residual) launch_lds_plan<1>(s, p, a, w, nullptr, M, residual, y);
             else launch_lds_plan<0>(s, p, a, w, nullptr, M, nullptr, y);
         }
+    } else if (dq_split_path(w, M) && (part || qgemm_part_bytes(w, M, false) == 0)) {
+        const int S = splitk_slices(w, M, false, lds_cus());
+        if (residual) launch_dq_split<1>(s, a, w, nullptr, M, S, residual, y, part);
+        else launch_dq_split<0>(s, a, w, nullptr, M, S, nullptr, y, part);
     } else {
         if (residual) launch_cfg<CfgSmall, 1>(s, w.dtype, a, w, nullptr, M, residual, y);
         else launch_cfg<CfgSmall, 0>(s, w.dtype, a, w, nullptr, M, nullptr, y);
@@ -1724,7 +1855,7 @@ int launch_qgemm(hipStream_t s, const DevWeight& w, const uint16_t* a, int M, co
 }
 
 int launch_qgemm_swiglu(hipStream_t s, const DevWeight& wg, const DevWeight& wu, const uint16_t* a,
-                        int M, void* h, bool h_bf16) {
+                        int M, void* h, bool h_bf16, float* part) {
     int rc = check_qgemm(wg, M);
     if (rc) return rc;
     rc = check_qgemm(wu, M);
@@ -1750,6 +1881,10 @@ int launch_qgemm_swiglu(hipStream_t s, const DevWeight& wg, const DevWeight& wu,
             if (h_bf16) launch_lds_plan<2>(s, p, a, wg, &wu, M, nullptr, h);
             else launch_lds_plan<3>(s, p, a, wg, &wu, M, nullptr, h);
         }
+    } else if (dq_split_path(wg, M) && (part || qgemm_part_bytes(wg, M, true) == 0)) {
+        const int S = splitk_slices(wg, M, true, lds_cus());
+        if (h_bf16) launch_dq_split<2>(s, a, wg, &wu, M, S, nullptr, h, part);
+        else launch_dq_split<3>(s, a, wg, &wu, M, S, nullptr, h, part);
     } else {
         if (h_bf16) launch_cfg<CfgSmall, 2>(s, wg.dtype, a, wg, &wu, M, nullptr, h);
         else launch_cfg<CfgSmall, 3>(s, wg.dtype, a, wg, &wu, M, nullptr, h);

@@ -26,6 +26,7 @@
 #include "internal.hpp"
 #include "runtime.hpp"
 
+#include <algorithm>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
@@ -93,6 +94,8 @@ struct vlrf_hip_model {
     uint16_t* pf_att = nullptr;    // [T][D] bf16 attention output
     uint16_t* pf_h = nullptr;      // [T][F] bf16 SwiGLU output
     int* pf_ids = nullptr;         // [T]
+    float* pf_part = nullptr;      // K-split partial sums of the GEMMs of 17..128 rows
+    size_t pf_part_bytes = 0;
 
     bool ready() const {
         if (!embed_set || !ln_final_set || !lm_head_set) return false;
@@ -468,7 +471,7 @@ void vlrf_hip_model_destroy(vlrf_hip_model_t m) {
                     (void*)m->gen_ids, (void*)m->prompt})
         if (p) (void)hipFree(p);
     for (void* p : {(void*)m->pf_x, (void*)m->pf_qkv, (void*)m->pf_a, (void*)m->pf_att, (void*)m->pf_h,
-                    (void*)m->pf_ids, (void*)m->qkv_tags,
+                    (void*)m->pf_ids, (void*)m->pf_part, (void*)m->qkv_tags,
                     (void*)m->step_status})
         if (p) (void)hipFree(p);
     if (m->pinned) (void)hipHostFree(m->pinned);
@@ -622,6 +625,24 @@ namespace {
 
 // Grows the batched-prefill buffers to hold T rows (waits for queued work first).
 int prefill_reserve(vlrf_hip_model* m, int T) {
+    // The GEMMs' K-split partial sums at T rows (every layer has layer 0's shapes).
+    size_t need = 0;
+    if (!m->layers.empty()) {
+        const Layer& L0 = m->layers[0];
+        need = std::max({qgemm_part_bytes(L0.wqkv, T, false), qgemm_part_bytes(L0.wo, T, false),
+                         qgemm_part_bytes(L0.wg, T, true), qgemm_part_bytes(L0.wd, T, false)});
+    }
+    if (need > m->pf_part_bytes) {
+        VH_CHECK(hipStreamSynchronize(m->ctx->stream));
+        if (m->pf_part) (void)hipFree(m->pf_part);
+        m->pf_part = nullptr;
+        m->pf_part_bytes = 0;
+        if (hipMalloc(&m->pf_part, need) != hipSuccess) {
+            set_error("prefill: hipMalloc(%zu) failed", need);
+            return VLRF_HIP_ERR_NOMEM;
+        }
+        m->pf_part_bytes = need;
+    }
     if (T <= m->pf_cap) return VLRF_HIP_OK;
     VH_CHECK(hipStreamSynchronize(m->ctx->stream));
     for (void** p : {(void**)&m->pf_x, (void**)&m->pf_qkv, (void**)&m->pf_a, (void**)&m->pf_att,
@@ -664,16 +685,16 @@ int enqueue_prefill_layers(vlrf_hip_model* m, const float* x_in, float* x_out, i
         const float* src = l == 0 ? x_in : x;                    // the stream entering layer l
         float* dst = l == m->L - 1 ? x_out : x;                  // and leaving it
         rc = launch_rows_to_bf16(s, src, Ly.ln1, m->pf_a, T, m->D, eps);
-        if (!rc) rc = launch_qgemm(s, Ly.wqkv, m->pf_a, T, nullptr, m->pf_qkv);
+        if (!rc) rc = launch_qgemm(s, Ly.wqkv, m->pf_a, T, nullptr, m->pf_qkv, m->pf_part);
         // k rotated and appended here; q rotated by the attention as it loads it
         if (!rc) rc = launch_prefill_rope_append(s, Ly.kv, m->pf_qkv, ld, T, m->H, m->G, m->dh, m->S, m->pos,
                                                  m->cos_t, m->sin_t);
         if (!rc) rc = launch_attn_prefill(s, m->pf_qkv, ld, Ly.kv, T, m->pos, m->H, m->G, m->dh, m->S, scale,
                                           m->cos_t, m->sin_t, m->pf_att);
-        if (!rc) rc = launch_qgemm(s, Ly.wo, m->pf_att, T, src, x);            // x = src + att . Wo^T
+        if (!rc) rc = launch_qgemm(s, Ly.wo, m->pf_att, T, src, x, m->pf_part);   // x = src + att . Wo^T
         if (!rc) rc = launch_rows_to_bf16(s, x, Ly.ln2, m->pf_a, T, m->D, eps);
-        if (!rc) rc = launch_qgemm_swiglu(s, Ly.wg, Ly.wu, m->pf_a, T, m->pf_h, true);
-        if (!rc) rc = launch_qgemm(s, Ly.wd, m->pf_h, T, x, dst);              // dst = x + h . Wd^T
+        if (!rc) rc = launch_qgemm_swiglu(s, Ly.wg, Ly.wu, m->pf_a, T, m->pf_h, true, m->pf_part);
+        if (!rc) rc = launch_qgemm(s, Ly.wd, m->pf_h, T, x, dst, m->pf_part);   // dst = x + h . Wd^T
     }
     return rc;
 }
