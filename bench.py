@@ -293,7 +293,9 @@ def configs_bench(V, F):
             n3 = 24 if dtype == V.DT_Q8_0 else 48
             base = F.quantize(F.normal(7, f"cfg3.{wname}", N * Kd, 0.02), dtype)
             ws = [V.QuantWeight(ctx, base, dtype, N, Kd) for _ in range(n3)]
-            for M in (1, 4, 16):
+            # M = 64 and 128 beside the configuration's 1, 4, 16: the
+            # K-split matrix-core GEMM of 17..128 rows.
+            for M in (1, 4, 16, 64, 128):
                 x = ctx.to_device(F.normal(7, f"cfg3.x{M}", M * Kd))
                 y = ctx.alloc(M * N * 4)
 

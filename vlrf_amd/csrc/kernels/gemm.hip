@@ -1312,8 +1312,13 @@ void launch_dqgemm_plan(hipStream_t s, const uint16_t* a, const DevWeight& w0, c
 // partial buffer ([S][M][N], SwiGLU [S][M][2N]: gate, then up), and
 // splitk_reduce_kernel adds the slices in order (the same sum on every run)
 // and applies the epilogue.  S is the smallest divisor of K / 128 that gives
-// at least one workgroup per CU, at most one whose partials (written and read
-// back) move no more bytes than the weight: S <= K bpw / (8 M).
+// at least one workgroup per CU, at most one whose slices keep at least 8 K
+// steps (the pipeline's prologue and the partial stores are per slice):
+// summed over M = 17, 32, 64, 65, 100, 128 at four 1.1B / 8B shapes (Q8_0),
+// 689 us against 693 with 4 steps, 703 with 2, and 765 aiming at two
+// workgroups per CU; capping S further so that the partials (written and
+// read back, mostly from the caches) move no more bytes than the weight cost
+// 6% over M = 17, 64, 128 and both dtypes (706 against 663 us).
 
 // out[r][n] = sum over z of P[z][r][n] (EPI 0), + residual (1, in place
 // allowed), silu(sum of gate) * (sum of up) as bf16 (2) or f32 (3).
@@ -1346,12 +1351,12 @@ using SplitTile128 = BTile<128, 128, 4, 2>;   // 65 <= M <= 128: 8 waves of 32 x
 int splitk_slices(const DevWeight& w, int M, bool swiglu, int cus) {
     const int bn = M <= 64 ? SplitTile64::BN : SplitTile128::BN;
     const long nt = (w.N + (swiglu ? bn / 2 : bn) - 1) / (swiglu ? bn / 2 : bn);
-    const double bpw = w.dtype == VLRF_HIP_DT_Q8_0 ? 34.0 / 32 : 18.0 / 32;   // weight bytes per element
-    const int cap = std::max(1, (int)(w.K * bpw / (8.0 * M)));
     const int kb = w.K / 128;
+    constexpr int kMinSteps = 8;   // K steps per slice at least (2 and 4 measured slower in sum)
     int S = 1;
-    for (int d = 1; d <= kb && d <= cap; ++d) {
+    for (int d = 1; d <= kb; ++d) {
         if (kb % d) continue;
+        if (w.K / 64 / d < kMinSteps) break;
         S = d;
         if (nt * d >= cus) break;
     }
