@@ -1400,9 +1400,9 @@ void launch_dq_split(hipStream_t s, const uint16_t* a, const DevWeight& w0, cons
 // out[r][:] = bf16(w ? rmsnorm(x[r]) * w : x[r]), one 256-lane workgroup per row
 // (ops.hpp:488-498: sum of squares, 1/sqrt(mean + eps), (x * inv) * w).
 // Rows of D % 4 == 0 and D <= 4096 are read once, as float4 held in registers
-// (VEC = 4 per thread), and written as 4 packed bf16; others take the scalar loop.
-constexpr int kRowVec = 4;
-template <bool VEC>
+// (NV = 4 per thread; D <= 8192 / 16384 with NV = 8 / 16), and written as 4
+// packed bf16; others take the element loop (NV = 0).
+template <int NV>
 __global__ __launch_bounds__(256) void rows_to_bf16_kernel(const float* __restrict__ x,
                                                            const float* __restrict__ w,
                                                            uint16_t* __restrict__ out, int D, float eps) {
@@ -1416,11 +1416,11 @@ __global__ __launch_bounds__(256) void rows_to_bf16_kernel(const float* __restri
         __syncthreads();
         return 1.f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)D + eps);
     };
-    if constexpr (VEC) {
+    if constexpr (NV > 0) {
         const int n4 = D / 4;
-        float4 v[kRowVec], g[kRowVec];
+        float4 v[NV], g[NV];
 #pragma unroll
-        for (int p = 0; p < kRowVec; ++p) {
+        for (int p = 0; p < NV; ++p) {
             const int f = tid + 256 * p;
             v[p] = f < n4 ? reinterpret_cast<const float4*>(xr)[f] : make_float4(0.f, 0.f, 0.f, 0.f);
             if (w) g[p] = f < n4 ? reinterpret_cast<const float4*>(w)[f] : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -1429,11 +1429,11 @@ __global__ __launch_bounds__(256) void rows_to_bf16_kernel(const float* __restri
         if (w) {
             float ss = 0.f;
 #pragma unroll
-            for (int p = 0; p < kRowVec; ++p) ss += v[p].x * v[p].x + v[p].y * v[p].y + v[p].z * v[p].z + v[p].w * v[p].w;
+            for (int p = 0; p < NV; ++p) ss += v[p].x * v[p].x + v[p].y * v[p].y + v[p].z * v[p].z + v[p].w * v[p].w;
             inv = inv_rms(ss);
         }
 #pragma unroll
-        for (int p = 0; p < kRowVec; ++p) {
+        for (int p = 0; p < NV; ++p) {
             const int f = tid + 256 * p;
             if (f < n4) {
                 float4 t = v[p];
@@ -1780,10 +1780,14 @@ int check_qgemm(const DevWeight& w, int M) {
 int launch_rows_to_bf16(hipStream_t s, const float* x, const float* w, uint16_t* out, int rows, int D,
                         float eps) {
     VH_ARG(x && out && rows >= 1 && D >= 1, "rows_to_bf16: bad arguments");
-    if (D % 4 == 0 && D <= 4 * 256 * kRowVec)
-        hipLaunchKernelGGL(rows_to_bf16_kernel<true>, dim3(rows), dim3(256), 0, s, x, w, out, D, eps);
+    if (D % 4 == 0 && D <= 4096)
+        hipLaunchKernelGGL(rows_to_bf16_kernel<4>, dim3(rows), dim3(256), 0, s, x, w, out, D, eps);
+    else if (D % 4 == 0 && D <= 8192)
+        hipLaunchKernelGGL(rows_to_bf16_kernel<8>, dim3(rows), dim3(256), 0, s, x, w, out, D, eps);
+    else if (D % 4 == 0 && D <= 16384)
+        hipLaunchKernelGGL(rows_to_bf16_kernel<16>, dim3(rows), dim3(256), 0, s, x, w, out, D, eps);
     else
-        hipLaunchKernelGGL(rows_to_bf16_kernel<false>, dim3(rows), dim3(256), 0, s, x, w, out, D, eps);
+        hipLaunchKernelGGL(rows_to_bf16_kernel<0>, dim3(rows), dim3(256), 0, s, x, w, out, D, eps);
     VH_LAUNCHED();
     return VLRF_HIP_OK;
 }
