@@ -241,17 +241,19 @@ def _hip():
 
 
 @pytest.mark.parametrize("dtype", [V.DT_Q8_0, V.DT_Q4_0])
-def test_prefill_gemm_under_graph_capture(orc, dtype):
+@pytest.mark.parametrize("M", [160, 64])
+def test_prefill_gemm_under_graph_capture(orc, dtype, M):
     """A stream under graph capture: the M > 128 GEMM records no allocation
     (the weight's bf16 expansion is not made, the tiles decode the blocks),
     the captured graph replays to the eager result (over the expansion) bit
     for bit, replay after replay with eager work between; a call that would
     grow the context scratch while capturing is refused with an error
-    instead of being recorded."""
+    instead of being recorded.  M = 64 takes the K-split GEMM and its reduce
+    launch (partial sums in the context scratch after the bf16 rows)."""
     import ctypes as C
     hip = _hip()
     ctx = V.Context(0)                  # its own scratch buffer, empty until the first call
-    M, N, K = 160, 512, 1024
+    N, K = 512, 1024
     print(f"[case] qgemm under capture dtype={dtype} M={M} N={N} K={K}", flush=True)
     w1, dec = _weight(ctx, 31, "cap", N, K, dtype)
     w2, _ = _weight(ctx, 31, "cap", N, K, dtype)              # the same blocks, never expanded
