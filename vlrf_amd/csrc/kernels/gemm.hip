@@ -1358,7 +1358,7 @@ int splitk_slices(const DevWeight& w, int M, bool swiglu, int cus) {
         if (kb % d) continue;
         if (w.K / 64 / d < kMinSteps) break;
         S = d;
-        if (nt * d >= cus) break;
+        if (nt * d >= cus) break;   // (3/4 of the CUs measured the same in sum)
     }
     return S;
 }
