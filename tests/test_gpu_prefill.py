@@ -138,9 +138,10 @@ def test_config5_layer_gemm_forms_identical(ctx, monkeypatch, dtype):
     """The 8B-shape layer at T = 256 with each form of the M > 128 GEMM: over
     the weights' bf16 expansions (the default), with the codes decoded into
     the GEMM's LDS tiles (VLRF_HIP_PREFILL_BF16=0) and decoded in registers
-    (VLRF_HIP_PREFILL_DQ=0 too).  The forms multiply the same bf16 operands
-    in the same order, so the layer's outputs are identical bit for bit.  A
-    fresh model per form: an expansion, once made, stays with its weight."""
+    (VLRF_HIP_PREFILL_DQ=0 too).  The first two multiply the same bf16
+    operands and add them in the same order (K slices alike), so the layer's
+    outputs are identical bit for bit.  A fresh model per form: an
+    expansion, once made, stays with its weight."""
     cfg = F.llama8b_layer(dtype, max_seq_len=512)
     T, D = 256, cfg["d_model"]
     x = F.normal(6, "cfg5.forms.x", T * D).reshape(T, D)
@@ -159,7 +160,13 @@ def test_config5_layer_gemm_forms_identical(ctx, monkeypatch, dtype):
             monkeypatch.setenv(k, v)
         outs.append(m.forward_hidden(ctx.to_device(x)).download((T, D)))
     assert np.isfinite(outs[0]).all()
-    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
+    assert np.array_equal(outs[0], outs[1])
+    # At 256 rows the QKV, O and down GEMMs have few tiles, so the first two
+    # forms split K into slices and the in-register form does not: the f32
+    # summation order differs there, and a GEMM output one f32 ulp apart can
+    # round to another bf16 downstream (h, P), so the layers agree to the
+    # bf16 class (measured 1.9e-3 normwise).
+    assert norm_err(outs[2], outs[0]) <= TOL, norm_err(outs[2], outs[0])
 
 
 @pytest.mark.parametrize("chunks", [(96,), (64, 40)])
@@ -184,14 +191,16 @@ def test_prefill_matches_bf16_model_tightly(ctx, chunks):
         assert ne <= TOL_EMU, (i, ne)
 
 
-def test_config5_full_size_t2048(ctx):
+def test_config5_full_size_t2048(ctx, monkeypatch):
     """Config 5 at its full size (T = 2048), through properties that hold at
     any size and tie it to the oracle-checked T = 256 case: rows depend only
     on earlier rows (causal attention, per-row GEMMs), so the first 256 output
     rows equal a T = 256 run, and one 2048-row pass equals two 1024-row chunks
     (the second attending the cache the first left).  Per-row arithmetic does
     not depend on the row count (same kernels, same K order, key tiles at the
-    same absolute positions), so both hold bit for bit."""
+    same absolute positions), so both hold bit for bit -- with the T = 256
+    run's GEMMs unsplit (VLRF_HIP_PREFILL_SPLIT=0); split into K slices, as
+    its few tiles make them by default, it agrees to the bf16 class."""
     cfg = F.llama8b_layer(V.DT_Q8_0, max_seq_len=2048)
     print("[case] config5 8B layer T=2048 full size", flush=True)
     m = V.Model(ctx, cfg)
@@ -206,8 +215,13 @@ def test_config5_full_size_t2048(ctx):
     full = run(x)
     assert np.all(np.isfinite(full))
     m.reset()
+    head_split = run(x[:256])
+    monkeypatch.setenv("VLRF_HIP_PREFILL_SPLIT", "0")
+    m.reset()
     head = run(x[:256])
+    monkeypatch.delenv("VLRF_HIP_PREFILL_SPLIT")
     assert np.array_equal(head, full[:256])
+    assert norm_err(head_split, full[:256]) <= TOL, norm_err(head_split, full[:256])
     m.reset()
     first = run(x[:1024])
     second = run(x[1024:])

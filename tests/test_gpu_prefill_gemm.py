@@ -148,6 +148,15 @@ def test_split_k_swiglu_mid_m(ctx, orc, monkeypatch, dtype, M, Fd, K):
     assert rel_err(got, unsplit) <= 2e-5, rel_err(got, unsplit)
 
 
+def _check_forms(a, b, c):
+    """Expansion and in-LDS forms identical bit for bit; the in-register form
+    identical too, except where the GEMM's few tiles make the two others
+    split K into slices (300 x 4096 x 2048), which it does not: there it
+    differs by the f32 summation order only."""
+    assert np.array_equal(a, b)
+    assert np.array_equal(a, c) or rel_err(a, c) <= 2e-5, rel_err(a, c)
+
+
 def _all_forms(monkeypatch, run):
     """run() with the weights' bf16 expansion (the default for M > 128), with
     VLRF_HIP_PREFILL_BF16=0 (Q8_0 with K % 128 == 0: codes decoded into LDS
@@ -189,7 +198,7 @@ def test_bf16_expansion_equals_in_register_decode(ctx, monkeypatch, dtype, M, N,
         return dy.download((M, N))
 
     a, b, c = _all_forms(monkeypatch, run)
-    assert np.array_equal(a, b) and np.array_equal(a, c)
+    _check_forms(a, b, c)
 
 
 @pytest.mark.parametrize("dtype", [V.DT_Q8_0, V.DT_Q4_0])
@@ -209,7 +218,7 @@ def test_bf16_expansion_swiglu_equals_in_register_decode(ctx, monkeypatch, dtype
         return dh.download((M, Fd))
 
     a, b, c = _all_forms(monkeypatch, run)
-    assert np.array_equal(a, b) and np.array_equal(a, c)
+    _check_forms(a, b, c)
 
 
 def test_bf16_expansion_is_counted_in_the_weight_bytes(ctx):

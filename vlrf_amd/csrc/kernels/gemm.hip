@@ -546,19 +546,21 @@ template <int BM_, int BN_, int WR_, int WC_, int BK_ = 64, int NSMAX = 4> struc
 template <class T, int EPI>
 __global__ __launch_bounds__(T::NT) void mfma_bgemm_kernel(
     const uint16_t* __restrict__ A, const uint16_t* __restrict__ ba, const uint16_t* __restrict__ bb, int M, int N,
-    int K, int ldo, const float* __restrict__ residual, void* __restrict__ out) {
+    int K, int kl, int ldo, const float* __restrict__ residual, void* __restrict__ out) {
     using lds_gemm::dma16;
     using lds_gemm::lds_addr;
     constexpr int MI = T::MI, NB = T::NB, WM = T::WM, WNR = T::WNR, BN = T::BN;
     constexpr int A_B = T::A_B, ST = T::ST, NS = T::NS, LPS = T::LPS, NW = T::NW;
     constexpr int RB = T::RB, CPR = T::CPR, RPL = T::RPL, NG = T::NG;
-    constexpr bool SWIGLU = EPI >= 2;
+    // EPI 6 / 7: raw partial sums of K slice blockIdx.z (plain / gate and up).
+    constexpr bool SWIGLU = EPI == 2 || EPI == 3 || EPI == 7, PARTIAL = EPI >= 6;
     __shared__ __align__(16) uint8_t lds[NS * ST];
     const int lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wave / T::WC, wn = wave % T::WC;
     const int m0 = blockIdx.y * T::BM;
     const int n0 = blockIdx.x * (SWIGLU ? BN / 2 : BN);   // first output column
+    const int k0 = blockIdx.z * kl;                        // this launch's K range: k0 .. k0 + kl (rows K long)
 
     // Sources of K step 0 (step k adds RB bytes) and destinations: wave w's
     // load `it` fills rows RPL (NW it + w) .. + RPL - 1 of the tile, lane l row
@@ -569,14 +571,14 @@ __global__ __launch_bounds__(T::NT) void mfma_bgemm_kernel(
 #pragma unroll
     for (int it = 0; it < T::A_IT; ++it) {
         const int r = (it * NW + wave) * RPL + lane / CPR, c = (lane % CPR) ^ T::swz(r);
-        ga[it] = reinterpret_cast<const char*>(A + (size_t)min(m0 + r, M - 1) * K + c * 8);
+        ga[it] = reinterpret_cast<const char*>(A + (size_t)min(m0 + r, M - 1) * K + k0 + c * 8);
     }
 #pragma unroll
     for (int it = 0; it < T::W_IT; ++it) {
         const int t = (it * NW + wave) * RPL + lane / CPR, c = (lane % CPR) ^ T::swz(t);
         const bool up = SWIGLU && t >= BN / 2;
         const int gn = min(n0 + (up ? t - BN / 2 : t), N - 1);
-        gb[it] = reinterpret_cast<const char*>((up ? bb : ba) + (size_t)gn * K + c * 8);
+        gb[it] = reinterpret_cast<const char*>((up ? bb : ba) + (size_t)gn * K + k0 + c * 8);
     }
     const uint32_t base = lds_addr(lds);
     auto load = [&](int kt, int buf) {
@@ -680,7 +682,7 @@ __global__ __launch_bounds__(T::NT) void mfma_bgemm_kernel(
     constexpr int W_ALL = 0x70;                                                           // vmcnt(0) lgkmcnt(0)
     constexpr int W_IN = ((NS - 2) * LPS & 15) | (7 << 4) | (((NS - 2) * LPS >> 4) << 14);   // vmcnt((NS-2) LPS) lgkmcnt(0)
     constexpr int W_PRO = ((NS - 1) * LPS & 15) | (7 << 4) | (15 << 8) | (((NS - 1) * LPS >> 4) << 14);
-    const int nk = K / T::BK;
+    const int nk = kl / T::BK;
 #pragma unroll
     for (int j = 0; j < NS; ++j) load(min(j, nk - 1), j);
     __builtin_amdgcn_s_waitcnt(W_PRO);   // step 0's loads in: the newer NS - 1 stages pending
@@ -710,6 +712,27 @@ __global__ __launch_bounds__(T::NT) void mfma_bgemm_kernel(
 
     // Accumulator v of tile (j, i) holds row 32i + 8(v/4) + 4h + v%4 of the
     // wave's rows, weight row l32 of block j.
+    if constexpr (PARTIAL) {
+        // Slice z's sums at out + z M ldo: plain column n at n, SwiGLU gate at
+        // n and up at N + n (ldo >= 2N).
+        float* P = static_cast<float*>(out) + (size_t)blockIdx.z * M * ldo;
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int row = m0 + wm * WM + 32 * i + 8 * (v >> 2) + 4 * h + (v & 3);
+                if (row >= M) continue;
+#pragma unroll
+                for (int j = 0; j < (SWIGLU ? NB / 2 : NB); ++j) {
+                    const int col = n0 + (SWIGLU ? wn * (WNR / 2) : wn * WNR) + 32 * j + l32;
+                    if (col < N) {
+                        P[(size_t)row * ldo + col] = acc[j][i][v];
+                        if constexpr (SWIGLU) P[(size_t)row * ldo + N + col] = acc[j + NB / 2][i][v];
+                    }
+                }
+            }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < MI; ++i)
 #pragma unroll
@@ -1148,7 +1171,7 @@ void launch_bgemm(hipStream_t s, const uint16_t* a, const DevWeight& w0, const D
     const uint16_t* bb = EPI >= 2 ? w1->bf + (size_t)n0 * w0.K : ba;
     const float* res = residual ? residual + n0 : nullptr;
     void* o = EPI == 2 ? (void*)(static_cast<uint16_t*>(out) + n0) : (void*)(static_cast<float*>(out) + n0);
-    hipLaunchKernelGGL((mfma_bgemm_kernel<T, EPI>), grid, dim3(T::NT), 0, s, a, ba, bb, M, nn, w0.K, w0.N, res, o);
+    hipLaunchKernelGGL((mfma_bgemm_kernel<T, EPI>), grid, dim3(T::NT), 0, s, a, ba, bb, M, nn, w0.K, w0.K, w0.N, res, o);
 }
 
 template <int EPI, int BM>
@@ -1395,6 +1418,55 @@ void launch_dq_split(hipStream_t s, const uint16_t* a, const DevWeight& w0, cons
         if (M <= 64) launch_dq_split_t<SplitTile64, VLRF_HIP_DT_Q4_0, EPI>(s, a, w0, w1, M, S, residual, out, part);
         else launch_dq_split_t<SplitTile128, VLRF_HIP_DT_Q4_0, EPI>(s, a, w0, w1, M, S, residual, out, part);
     }
+}
+
+// ---- M > 128 with few tiles: the same K split --------------------------------
+// The plans above fill the GPU at the 8B shapes only from about T = 2048: at
+// M = 256 the O and down GEMMs have 32 tiles.  Below half a round of 256-row
+// x 128-column output tiles, both forms (over the bf16 expansions and over
+// the codes) split K into the same S slices (the smallest divisor of K / 128
+// giving a round, slices of at least 8 K steps) with the partial buffer and
+// splitk_reduce_kernel of the 17..128-row path, so the two forms still
+// multiply and add the same numbers in the same order.
+int big_split_slices(int M, int N, int K, int cus) {
+    const long g0 = (long)((M + 255) / 256) * ((N + 127) / 128);
+    const char* e = getenv("VLRF_HIP_PREFILL_SPLIT");   // "0": the unsplit plans at every M > 128
+    if ((e && e[0] == '0') || K % 128 || 2 * g0 >= cus) return 1;
+    const int kb = K / 128;
+    int S = 1;
+    for (int d = 1; d <= kb; ++d) {
+        if (kb % d) continue;
+        if (K / 64 / d < 8) break;
+        S = d;
+        if (g0 * d >= cus) break;
+    }
+    return S;
+}
+
+template <class T, int EPI>
+void launch_bgemm_split_t(hipStream_t s, const uint16_t* a, const DevWeight& w0, const DevWeight* w1, int M, int S,
+                          const float* residual, void* out, float* part) {
+    constexpr bool SW = EPI >= 2;
+    constexpr int TN = SW ? T::BN / 2 : T::BN;
+    const int N = w0.N, K = w0.K, ldp = SW ? 2 * N : N;
+    const dim3 grid((N + TN - 1) / TN, (M + T::BM - 1) / T::BM, S);
+    hipLaunchKernelGGL((mfma_bgemm_kernel<T, SW ? 7 : 6>), grid, dim3(T::NT), 0, s, a, w0.bf, SW ? w1->bf : w0.bf, M,
+                       N, K, K / S, ldp, nullptr, part);
+    const size_t n = (size_t)M * N;
+    hipLaunchKernelGGL((splitk_reduce_kernel<EPI>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, part, S, M, N,
+                       ldp, residual, out);
+}
+
+// bf16: over the expansions (of both matrices for SwiGLU); else over the codes.
+template <int EPI>
+void launch_big_split(hipStream_t s, bool bf16, const uint16_t* a, const DevWeight& w0, const DevWeight* w1, int M,
+                      int S, const float* residual, void* out, float* part) {
+    using TP = BTile<256, 128, 4, 2>;   // plain: 256 x 128 tiles
+    using TS = BTile<256, 256, 2, 4>;   // SwiGLU: 256 rows x 128 gate and 128 up rows
+    using T = typename std::conditional<(EPI >= 2), TS, TP>::type;
+    if (bf16) launch_bgemm_split_t<T, EPI>(s, a, w0, w1, M, S, residual, out, part);
+    else if (w0.dtype == VLRF_HIP_DT_Q8_0) launch_dq_split_t<T, VLRF_HIP_DT_Q8_0, EPI>(s, a, w0, w1, M, S, residual, out, part);
+    else launch_dq_split_t<T, VLRF_HIP_DT_Q4_0, EPI>(s, a, w0, w1, M, S, residual, out, part);
 }
 
 // out[r][:] = bf16(w ? rmsnorm(x[r]) * w : x[r]), one 256-lane workgroup per row
@@ -1828,8 +1900,9 @@ bool weight_expand_bf16(hipStream_t s, const DevWeight& w) {
 static bool dq_split_path(const DevWeight& w, int M) { return M >= 17 && M <= 128 && dqgemm_supported(w); }
 
 size_t qgemm_part_bytes(const DevWeight& w, int M, bool swiglu) {
-    if (!dq_split_path(w, M)) return 0;
-    const int S = splitk_slices(w, M, swiglu, lds_cus());
+    int S = 1;
+    if (M > 128) S = big_split_slices(M, w.N, w.K, lds_cus());
+    else if (dq_split_path(w, M)) S = splitk_slices(w, M, swiglu, lds_cus());
     return S > 1 ? (size_t)S * M * w.N * (swiglu ? 2 : 1) * sizeof(float) : 0;
 }
 
@@ -1840,7 +1913,11 @@ int launch_qgemm(hipStream_t s, const DevWeight& w, const uint16_t* a, int M, co
     VH_ARG(a && y, "qgemm: null operand");
     if (M > 128) {
         weight_expand_bf16(s, w);
-        if (w.bf) {
+        const int S = part ? big_split_slices(M, w.N, w.K, lds_cus()) : 1;
+        if (S > 1 && (w.bf || dqgemm_supported(w))) {
+            if (residual) launch_big_split<1>(s, w.bf != nullptr, a, w, nullptr, M, S, residual, y, part);
+            else launch_big_split<0>(s, w.bf != nullptr, a, w, nullptr, M, S, nullptr, y, part);
+        } else if (w.bf) {
             if (residual) launch_bgemm_plan<1>(s, a, w, nullptr, M, residual, y);
             else launch_bgemm_plan<0>(s, a, w, nullptr, M, nullptr, y);
         } else if (dqgemm_supported(w)) {
@@ -1879,7 +1956,11 @@ int launch_qgemm_swiglu(hipStream_t s, const DevWeight& wg, const DevWeight& wu,
             (void)hipFree(wg.bf);   // both or neither (no free while capturing)
             wg.bf = nullptr;
         }
-        if (both) {
+        const int S = part ? big_split_slices(M, wg.N, wg.K, lds_cus()) : 1;
+        if (S > 1 && (both || dqgemm_supported(wg))) {
+            if (h_bf16) launch_big_split<2>(s, both, a, wg, &wu, M, S, nullptr, h, part);
+            else launch_big_split<3>(s, both, a, wg, &wu, M, S, nullptr, h, part);
+        } else if (both) {
             if (h_bf16) launch_bgemm_plan<2>(s, a, wg, &wu, M, nullptr, h);
             else launch_bgemm_plan<3>(s, a, wg, &wu, M, nullptr, h);
         } else if (dqgemm_supported(wg)) {
