@@ -1425,7 +1425,9 @@ void launch_dq_split(hipStream_t s, const uint16_t* a, const DevWeight& w0, cons
 // M = 256 the O and down GEMMs have 32 tiles.  Below half a round of 256-row
 // x 128-column output tiles, both forms (over the bf16 expansions and over
 // the codes) split K into the same S slices (the smallest divisor of K / 128
-// giving a round, slices of at least 8 K steps) with the partial buffer and
+// giving 3/4 of a round, slices of at least 8 K steps: the partials here are
+// M rows wide, so fewer slices pay; 8B layer at T = 256 0.254 against 0.291
+// ms aiming at a full round, 0.262 at half a round) with the partial buffer and
 // splitk_reduce_kernel of the 17..128-row path, so the two forms still
 // multiply and add the same numbers in the same order.
 int big_split_slices(int M, int N, int K, int cus) {
@@ -1438,7 +1440,7 @@ int big_split_slices(int M, int N, int K, int cus) {
         if (kb % d) continue;
         if (K / 64 / d < 8) break;
         S = d;
-        if (g0 * d >= cus) break;
+        if (4 * g0 * d >= 3L * cus) break;
     }
     return S;
 }
