@@ -1345,6 +1345,42 @@ void launch_dqgemm_plan(hipStream_t s, const uint16_t* a, const DevWeight& w0, c
 
 // out[r][n] = sum over z of P[z][r][n] (EPI 0), + residual (1, in place
 // allowed), silu(sum of gate) * (sum of up) as bf16 (2) or f32 (3).
+// N % 4 == 0: four columns a thread (VEC), the same sums element by element.
+template <int EPI>
+__global__ __launch_bounds__(256) void splitk_reduce4_kernel(const float* __restrict__ P, int S, int M, int N,
+                                                             int ldp, const float* residual, void* out) {
+    const size_t idx = ((size_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (idx >= (size_t)M * N) return;
+    const int row = (int)(idx / N), col = (int)(idx % N);
+    const size_t zs = (size_t)M * ldp;
+    const float* p = P + (size_t)row * ldp + col;
+    float4 g = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int z = 0; z < S; ++z) {
+        const float4 t = *reinterpret_cast<const float4*>(p + z * zs);
+        g.x += t.x; g.y += t.y; g.z += t.z; g.w += t.w;
+    }
+    if constexpr (EPI >= 2) {
+        float4 u = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int z = 0; z < S; ++z) {
+            const float4 t = *reinterpret_cast<const float4*>(p + z * zs + N);
+            u.x += t.x; u.y += t.y; u.z += t.z; u.w += t.w;
+        }
+        const float h0 = silu_mul_fast(g.x, u.x), h1 = silu_mul_fast(g.y, u.y);
+        const float h2 = silu_mul_fast(g.z, u.z), h3 = silu_mul_fast(g.w, u.w);
+        if constexpr (EPI == 2)
+            *reinterpret_cast<uint2*>(static_cast<uint16_t*>(out) + idx) =
+                make_uint2(bf16_bits(h0) | (bf16_bits(h1) << 16), bf16_bits(h2) | (bf16_bits(h3) << 16));
+        else
+            *reinterpret_cast<float4*>(static_cast<float*>(out) + idx) = make_float4(h0, h1, h2, h3);
+    } else {
+        if constexpr (EPI == 1) {
+            const float4 r = *reinterpret_cast<const float4*>(residual + idx);
+            g.x += r.x; g.y += r.y; g.z += r.z; g.w += r.w;
+        }
+        *reinterpret_cast<float4*>(static_cast<float*>(out) + idx) = g;
+    }
+}
+
 template <int EPI>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ P, int S, int M, int N,
                                                             int ldp, const float* residual, void* out) {
@@ -1366,6 +1402,18 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
     } else {
         static_cast<float*>(out)[idx] = g;
     }
+}
+
+template <int EPI>
+void launch_splitk_reduce(hipStream_t s, const float* part, int S, int M, int N, int ldp, const float* residual,
+                          void* out) {
+    const size_t n = (size_t)M * N;
+    if (N % 4 == 0)
+        hipLaunchKernelGGL((splitk_reduce4_kernel<EPI>), dim3((unsigned)((n / 4 + 255) / 256)), dim3(256), 0, s, part, S,
+                           M, N, ldp, residual, out);
+    else
+        hipLaunchKernelGGL((splitk_reduce_kernel<EPI>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, part, S, M,
+                           N, ldp, residual, out);
 }
 
 using SplitTile64 = BTile<64, 256, 2, 4>;     // M <= 64: 8 waves of 32 x 64
@@ -1403,9 +1451,7 @@ void launch_dq_split_t(hipStream_t s, const uint16_t* a, const DevWeight& w0, co
     const int ldp = SW ? 2 * N : N;
     hipLaunchKernelGGL((mfma_dqgemm_kernel<T, WT, SW ? 7 : 6, 2>), grid, dim3(T::NT), 0, s, a, w0.q, w0.d, qb, db, M,
                        N, K, K / S, ldp, nullptr, part);
-    const size_t n = (size_t)M * N;
-    hipLaunchKernelGGL((splitk_reduce_kernel<EPI>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, part, S, M, N,
-                       ldp, residual, out);
+    launch_splitk_reduce<EPI>(s, part, S, M, N, ldp, residual, out);
 }
 
 template <int EPI>
@@ -1454,9 +1500,7 @@ void launch_bgemm_split_t(hipStream_t s, const uint16_t* a, const DevWeight& w0,
     const dim3 grid((N + TN - 1) / TN, (M + T::BM - 1) / T::BM, S);
     hipLaunchKernelGGL((mfma_bgemm_kernel<T, SW ? 7 : 6>), grid, dim3(T::NT), 0, s, a, w0.bf, SW ? w1->bf : w0.bf, M,
                        N, K, K / S, ldp, nullptr, part);
-    const size_t n = (size_t)M * N;
-    hipLaunchKernelGGL((splitk_reduce_kernel<EPI>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, part, S, M, N,
-                       ldp, residual, out);
+    launch_splitk_reduce<EPI>(s, part, S, M, N, ldp, residual, out);
 }
 
 // bf16: over the expansions (of both matrices for SwiGLU); else over the codes.
