@@ -134,6 +134,24 @@ def test_config5_llama8b_layer_t256(ctx, dtype):
 
 
 @pytest.mark.parametrize("dtype", [V.DT_Q8_0, V.DT_Q4_0])
+def test_config5_llama8b_layer_chunked(ctx, dtype):
+    """The 8B-shape layer over the same 256 rows as two chunks, 100 and 156:
+    the first chunk's GEMMs take the 17..128-row path with K split into
+    slices (QKV 8, O 8, gate/up 2, down 8 at this shape), the second the
+    split above 128 rows, and its attention reads the first chunk's cache
+    rows.  Against the oracle's single pass over all 256 rows."""
+    cfg = F.llama8b_layer(dtype, max_seq_len=512)
+    print(f"[case] config5 8B layer chunks 100 + 156 dtype={dtype}", flush=True)
+    m, om = _pair(ctx, cfg, 5, norm_std=0.0)
+    T, D = 256, cfg["d_model"]
+    x = F.normal(5, "cfg5.x", T * D).reshape(T, D)
+    a = m.forward_hidden(ctx.to_device(np.ascontiguousarray(x[:100]))).download((100, D))
+    b = m.forward_hidden(ctx.to_device(np.ascontiguousarray(x[100:]))).download((156, D))
+    assert m.used == T
+    check(np.concatenate([a, b]), om.forward_hidden(x), "8B layer in two chunks vs f32 oracle")
+
+
+@pytest.mark.parametrize("dtype", [V.DT_Q8_0, V.DT_Q4_0])
 def test_config5_layer_gemm_forms_identical(ctx, monkeypatch, dtype):
     """The 8B-shape layer at T = 256 with each form of the M > 128 GEMM: over
     the weights' bf16 expansions (the default), with the codes decoded into
