@@ -216,9 +216,9 @@ def test_config5_full_size_t2048(ctx, monkeypatch):
     rows equal a T = 256 run, and one 2048-row pass equals two 1024-row chunks
     (the second attending the cache the first left).  Per-row arithmetic does
     not depend on the row count (same kernels, same K order, key tiles at the
-    same absolute positions), so both hold bit for bit -- with the T = 256
-    run's GEMMs unsplit (VLRF_HIP_PREFILL_SPLIT=0); split into K slices, as
-    its few tiles make them by default, it agrees to the bf16 class."""
+    same absolute positions), so both hold bit for bit -- with the shorter
+    runs' GEMMs unsplit (VLRF_HIP_PREFILL_SPLIT=0); split into K slices, as
+    their few tiles make them by default, they agree to the bf16 class."""
     cfg = F.llama8b_layer(V.DT_Q8_0, max_seq_len=2048)
     print("[case] config5 8B layer T=2048 full size", flush=True)
     m = V.Model(ctx, cfg)
@@ -234,17 +234,20 @@ def test_config5_full_size_t2048(ctx, monkeypatch):
     assert np.all(np.isfinite(full))
     m.reset()
     head_split = run(x[:256])
+    m.reset()
+    chunks_split = np.concatenate([run(x[:1024]), run(x[1024:])])
     monkeypatch.setenv("VLRF_HIP_PREFILL_SPLIT", "0")
     m.reset()
     head = run(x[:256])
-    monkeypatch.delenv("VLRF_HIP_PREFILL_SPLIT")
-    assert np.array_equal(head, full[:256])
-    assert norm_err(head_split, full[:256]) <= TOL, norm_err(head_split, full[:256])
     m.reset()
     first = run(x[:1024])
     second = run(x[1024:])
+    monkeypatch.delenv("VLRF_HIP_PREFILL_SPLIT")
     assert m.used == T
+    assert np.array_equal(head, full[:256])
     assert np.array_equal(np.concatenate([first, second]), full)
+    assert norm_err(head_split, full[:256]) <= TOL, norm_err(head_split, full[:256])
+    assert norm_err(chunks_split, full) <= TOL, norm_err(chunks_split, full)
 
 
 def test_config5_attention_t2048_vs_oracle(ctx):

@@ -1468,25 +1468,25 @@ void launch_dq_split(hipStream_t s, const uint16_t* a, const DevWeight& w0, cons
 
 // ---- M > 128 with few tiles: the same K split --------------------------------
 // The plans above fill the GPU at the 8B shapes only from about T = 2048: at
-// M = 256 the O and down GEMMs have 32 tiles.  Below half a round of 256-row
+// M = 256 the O and down GEMMs have 32 tiles.  Below a round of 256-row
 // x 128-column output tiles, both forms (over the bf16 expansions and over
-// the codes) split K into the same S slices (the smallest divisor of K / 128
-// giving 3/4 of a round, slices of at least 8 K steps: the partials here are
-// M rows wide, so fewer slices pay; 8B layer at T = 256 0.254 against 0.291
-// ms aiming at a full round, 0.262 at half a round) with the partial buffer and
-// splitk_reduce_kernel of the 17..128-row path, so the two forms still
-// multiply and add the same numbers in the same order.
+// the codes) split K into the same S slices -- the largest divisor of K / 128
+// whose workgroups still fit one round, slices of at least 8 K steps -- with
+// the partial buffer and splitk_reduce_kernel of the 17..128-row path, so
+// the two forms still multiply and add the same numbers in the same order.
+// (8B layer, same box: against aiming at 3/4 of a round from below half a
+// round, T = 1024 0.677 -> 0.600 ms, its O and down now split in two; T =
+// 256 .. 768 within noise.  Aiming at a full round: T = 256 0.291 ms.)
 int big_split_slices(int M, int N, int K, int cus) {
     const long g0 = (long)((M + 255) / 256) * ((N + 127) / 128);
     const char* e = getenv("VLRF_HIP_PREFILL_SPLIT");   // "0": the unsplit plans at every M > 128
-    if ((e && e[0] == '0') || K % 128 || 2 * g0 >= cus) return 1;
+    if ((e && e[0] == '0') || K % 128 || g0 >= cus) return 1;
     const int kb = K / 128;
     int S = 1;
     for (int d = 1; d <= kb; ++d) {
         if (kb % d) continue;
-        if (K / 64 / d < 8) break;
+        if (K / 64 / d < 8 || g0 * d > cus) break;
         S = d;
-        if (4 * g0 * d >= 3L * cus) break;
     }
     return S;
 }
