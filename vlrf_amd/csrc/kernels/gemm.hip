@@ -1334,9 +1334,11 @@ void launch_dqgemm_plan(hipStream_t s, const uint16_t* a, const DevWeight& w0, c
 // split into S contiguous slices instead, each slice's f32 sums written to a
 // partial buffer ([S][M][N], SwiGLU [S][M][2N]: gate, then up), and
 // splitk_reduce_kernel adds the slices in order (the same sum on every run)
-// and applies the epilogue.  S is the smallest divisor of K / 128 that gives
-// at least one workgroup per CU, at most one whose slices keep at least 8 K
-// steps (the pipeline's prologue and the partial stores are per slice):
+// and applies the epilogue.  S is the largest divisor of K / 128 whose
+// workgroups fit one round of the CUs and whose slices keep at least 8 K
+// steps (the pipeline's prologue and the partial stores are per slice; 8B
+// QKV at M = 128, 48 column tiles: 4 slices 26.8 us, 8 slices 1.5 rounds
+// 30.2 us).  Measured while S was the smallest divisor reaching a round:
 // summed over M = 17, 32, 64, 65, 100, 128 at four 1.1B / 8B shapes (Q8_0),
 // 689 us against 693 with 4 steps, 703 with 2, and 765 aiming at two
 // workgroups per CU; capping S further so that the partials (written and
@@ -1427,9 +1429,8 @@ int splitk_slices(const DevWeight& w, int M, bool swiglu, int cus) {
     int S = 1;
     for (int d = 1; d <= kb; ++d) {
         if (kb % d) continue;
-        if (w.K / 64 / d < kMinSteps) break;
+        if (w.K / 64 / d < kMinSteps || (d > 1 && nt * d > cus)) break;
         S = d;
-        if (nt * d >= cus) break;   // (3/4 of the CUs measured the same in sum)
     }
     return S;
 }
